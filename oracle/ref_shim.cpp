@@ -1,0 +1,186 @@
+// ref_shim.cpp -- C entry points onto the reference's own CPU kernels.
+//
+// TEST INFRASTRUCTURE ONLY. Compiled (by oracle/Makefile, target `ref`) together
+// with the reference's sources where they lie under /root/reference into
+// oracle/_ref/libdynacore_ref.so. Nothing of the reference is copied: this file
+// only includes its headers at build time and forwards to its functions:
+//   dynacore/include/dynacore/tensor/fp16.h:18-62          fp16 conversion
+//   dynacore/src/quantization/quant_formats.cpp:12-222      dequantize_*, quantize_q8_0
+//   dynacore/cpu/generic/kernels_generic.cpp:187-310        quantize_act, dot_rows_* (generic)
+//   dynacore/cpu/avx2/kernels_avx2.cpp:610-1440             AVX2 quantizers and dots
+// Used to pin the C oracle (tests) and, on the GPU box, as the timed CPU
+// baseline ("reference" kind) of bench.py.
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cstdint>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#include "dynacore/cpu/cpu_kernels.h"
+#include "dynacore/hardware/cpu_info.h"
+#include "dynacore/quantization/quant_formats.h"
+#include "dynacore/tensor/dtype.h"
+#include "dynacore/tensor/fp16.h"
+
+using namespace dynacore;
+
+namespace {
+
+const CpuKernels& generic_table() {
+  static const CpuKernels k = [] {
+    CpuKernels t;
+    register_generic_kernels(t);
+    return t;
+  }();
+  return k;
+}
+
+const CpuKernels& avx2_table() {
+  static const CpuKernels k = [] {
+    CpuKernels t;
+    register_generic_kernels(t);
+    register_avx2_kernels(t);
+    return t;
+  }();
+  return k;
+}
+
+bool valid_type(int t) { return t == 6 || t == 10 || t == 14 || t == 16 || t == 17; }
+
+std::vector<const ActBlockQ8*> row_ptrs(const void* acts, int64_t row_bytes, int m) {
+  std::vector<const ActBlockQ8*> p(static_cast<size_t>(m));
+  for (int r = 0; r < m; ++r) p[static_cast<size_t>(r)] = reinterpret_cast<const ActBlockQ8*>(static_cast<const uint8_t*>(acts) + r * row_bytes);
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ref_has_avx2(void) { return cpu_info().features.avx2 ? 1 : 0; }
+int ref_physical_cores(void) { return static_cast<int>(cpu_info().physical_cores); }
+int ref_logical_cores(void) { return static_cast<int>(cpu_info().logical_cores); }
+
+float ref_fp16_to_fp32(uint16_t h) { return fp16_to_fp32(h); }
+uint16_t ref_fp32_to_fp16(float f) { return fp32_to_fp16(f); }
+
+int ref_dequantize(int dtype, const void* blocks, float* y, int64_t n) {
+  if (!valid_type(dtype)) return -1;
+  const auto t = static_cast<DType>(dtype);
+  const int64_t be = dtype_block_elems(t);
+  if (n % be != 0) return -1;
+  const int64_t nb = n / be;
+  switch (t) {
+    case DType::kQ4_0: quant::dequantize_q4_0(static_cast<const quant::BlockQ4_0*>(blocks), y, nb); break;
+    case DType::kQ8_0: quant::dequantize_q8_0(static_cast<const quant::BlockQ8_0*>(blocks), y, nb); break;
+    case DType::kQ4_K: quant::dequantize_q4_K(static_cast<const quant::BlockQ4_K*>(blocks), y, nb); break;
+    case DType::kQ6_K: quant::dequantize_q6_K(static_cast<const quant::BlockQ6_K*>(blocks), y, nb); break;
+    case DType::kQ8_K: quant::dequantize_q8_K(static_cast<const quant::BlockQ8_K*>(blocks), y, nb); break;
+    default: return -1;
+  }
+  return 0;
+}
+
+int ref_quantize_q8_0(const float* x, void* out, int64_t n) {
+  if (n % 32 != 0) return -1;
+  quant::quantize_q8_0(x, static_cast<quant::BlockQ8_0*>(out), n / 32);
+  return 0;
+}
+
+// tier: 0 = generic, 1 = AVX2.
+int ref_quantize_act(int tier, const float* x, void* out, int64_t n) {
+  if (n % 32 != 0) return -1;
+  const CpuKernels& k = tier ? avx2_table() : generic_table();
+  k.quantize_act(x, static_cast<ActBlockQ8*>(out), n);
+  return 0;
+}
+
+// Super-block (one scale per 256, ActBlockQ8 layout) and sub-scaled (ActSuperQ8): AVX2 only.
+int ref_quantize_act_sb(const float* x, void* out, int64_t n) {
+  const CpuKernels& k = avx2_table();
+  if (n % 256 != 0 || !k.quantize_act_sb) return -1;
+  k.quantize_act_sb(x, static_cast<ActBlockQ8*>(out), n);
+  return 0;
+}
+
+int ref_quantize_act_sx(const float* x, void* out, int64_t n) {
+  const CpuKernels& k = avx2_table();
+  if (n % 256 != 0 || !k.quantize_act_sx) return -1;
+  k.quantize_act_sx(x, static_cast<ActBlockQ8*>(out), n);
+  return 0;
+}
+
+// out[r] = dot(w row, act row r), r < m <= 4 (DotQ8RowsFn). kind: 0 = generic
+// per-32, 1 = AVX2 per-32, 2 = AVX2 super-block (acts from ref_quantize_act_sb),
+// 3 = AVX2 sub-scaled (acts from ref_quantize_act_sx).
+int ref_dot_rows(int kind, int dtype, const void* w, const void* acts, int64_t act_row_bytes, int m, int64_t k,
+                 float* out) {
+  if (!valid_type(dtype) || m < 1 || m > kDotRowsMax) return -1;
+  const CpuKernels& t = kind == 0 ? generic_table() : avx2_table();
+  const size_t i = static_cast<size_t>(dtype);
+  DotQ8RowsFn fn = kind <= 1 ? t.dot_q8_rows[i] : kind == 2 ? t.dot_q8_sb_rows[i] : t.dot_q8_sx_rows[i];
+  if (!fn) return -2;
+  const auto p = row_ptrs(acts, act_row_bytes, m);
+  fn(w, p.data(), m, k, out);
+  return 0;
+}
+
+// Multi-row AVX2 kernels over weight rows [n0, n1) (DotQ8RowsNFn):
+// kind 1 = per-32 (dot_q8_rows_n), 3 = sub-scaled (dot_q8_sx_rows_n).
+int ref_dot_rows_n(int kind, int dtype, const void* w, int64_t w_row_bytes, int64_t n0, int64_t n1, const void* acts,
+                   int64_t act_row_bytes, int m, int64_t k, float* y, int64_t y_stride, const float* bias) {
+  if (!valid_type(dtype) || m < 1 || m > kDotRowsNMax) return -1;
+  const CpuKernels& t = avx2_table();
+  const size_t i = static_cast<size_t>(dtype);
+  DotQ8RowsNFn fn = kind == 1 ? t.dot_q8_rows_n[i] : kind == 3 ? t.dot_q8_sx_rows_n[i] : nullptr;
+  if (!fn) return -2;
+  const auto p = row_ptrs(acts, act_row_bytes, m);
+  std::vector<float*> yp(static_cast<size_t>(m));
+  for (int r = 0; r < m; ++r) yp[static_cast<size_t>(r)] = y + r * y_stride;
+  fn(w, w_row_bytes, n0, n1, p.data(), m, k, yp.data(), bias);
+  return 0;
+}
+
+// Timed CPU baseline: `threads` std::threads split the N weight rows into
+// 16-row units (as CpuDevice's decode partition, dynacore/cpu/cpu_device.cpp:925-934),
+// each running the AVX2 multi-row kernel of `kind` over its rows; the weight
+// copies in `w_copies` are visited in rotation so successive calls read cold
+// memory (dynalm/benchmarks/bench_decode_matmul.cpp:11-14). Runs `iters` calls
+// after one warm-up call and returns the total nanoseconds of the timed calls.
+int64_t ref_bench_gemv(int kind, int dtype, const void* const* w_copies, int ncopies, int64_t w_row_bytes, int64_t n,
+                       const void* acts, int64_t act_row_bytes, int m, int64_t k, float* y, int threads, int iters) {
+  if (!valid_type(dtype) || m < 1 || m > kDotRowsNMax || ncopies < 1 || threads < 1 || iters < 1) return -1;
+  const CpuKernels& t = avx2_table();
+  const size_t ti = static_cast<size_t>(dtype);
+  DotQ8RowsNFn fn = kind == 1 ? t.dot_q8_rows_n[ti] : kind == 3 ? t.dot_q8_sx_rows_n[ti] : nullptr;
+  if (!fn) return -2;
+  const auto p = row_ptrs(acts, act_row_bytes, m);
+  const int64_t units = (n + 15) / 16;
+  auto run = [&](const void* w) {
+    std::atomic<int64_t> next{0};
+    auto worker = [&] {
+      std::vector<float*> yp(static_cast<size_t>(m));
+      for (;;) {
+        const int64_t u = next.fetch_add(4);
+        if (u >= units) break;
+        const int64_t n0 = u * 16, n1 = std::min(n, (u + 4) * 16);
+        for (int r = 0; r < m; ++r) yp[static_cast<size_t>(r)] = y + r * n + n0;
+        fn(w, w_row_bytes, n0, n1, p.data(), m, k, yp.data(), nullptr);
+      }
+    };
+    std::vector<std::thread> pool;
+    for (int i = 1; i < threads; ++i) pool.emplace_back(worker);
+    worker();
+    for (auto& th : pool) th.join();
+  };
+  run(w_copies[0]);
+  const auto t0 = std::chrono::steady_clock::now();
+  for (int it = 0; it < iters; ++it) run(w_copies[(it + 1) % ncopies]);
+  const auto t1 = std::chrono::steady_clock::now();
+  return std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
+}
+
+}  // extern "C"
