@@ -1,0 +1,238 @@
+"""Benchmark of the block-quantized matmul hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Headline (BASELINE.json metric "Q4_K GEMV HBM GB/s (% peak) at M=1; Q4_K GEMM int8
+TOPS (% peak) at M=512"): one step = quantize one activation row to Q8_K on the GPU
++ the Q4_K GEMV at config 3's gate/up shape (K=4096, N=14336, M=1), weights resident
+in HBM and rotated over copies totalling well over the 256 MB Infinity Cache (as
+dynalm/benchmarks/bench_decode_matmul.cpp:11-14 rotates layers). `value` is the
+step's algorithmic bytes (packed weights + quantized activations + fp32 output) per
+second. A second leg times the config 4 prefill GEMM (M=512) in int8 TOPS.
+
+Both `roofline` objects use per-kernel durations from HIP events on the launch
+stream over back-to-back launches of that kernel alone. `cpu_baseline` times the
+kernel dynacore selects on x86 for this call (Q4_K x sub-scaled int8,
+dot_rows_n_sx_q4_K, dynacore/src/kernel/matmul_registry.cpp:139-165) compiled from
+the reference sources (oracle/_ref) on the host cores, on a bounded sample.
+Inputs are synthetic: random valid Q4_K blocks (fp16 d, dmin in U(0.002, 0.02)) and
+N(0, 1) activations; timing does not depend on the values.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q4_K GEMV HBM GB/s (% peak) at M=1; Q4_K GEMM int8 TOPS (% peak) at M=512"
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E
+PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA
+K, N = 4096, 14336        # config 3 gate/up, config 4
+Q4K_ROW = K // 256 * 144
+Q8K_ROW = K // 256 * 292
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def random_q4k_rows(n: int, k: int, seed: int) -> np.ndarray:
+    """Random valid Q4_K blocks: random scales/codes, fp16 d and dmin in U(0.002, 0.02)."""
+    rng = np.random.default_rng(seed)
+    rows = rng.integers(0, 256, (n, k // 256, 144), dtype=np.uint8)
+    dd = rng.uniform(0.002, 0.02, (n, k // 256, 2)).astype(np.float16)
+    rows[:, :, 0:4] = dd.view(np.uint8).reshape(n, k // 256, 4)
+    return rows.reshape(n, -1)
+
+
+def time_launches(fn, iters: int, warmup: int) -> float:
+    """Average ms per call of fn(i) over `iters` back-to-back calls (HIP events on the current stream)."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(iters):
+        fn(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def cpu_baseline(w_host: np.ndarray, copies: int, budget_s: float) -> dict:
+    """dynacore's x86 decode kernel for this call, timed on the host cores."""
+    from oracle import oracle as O
+
+    x = O.normal(7, K)
+    nbytes = Q4K_ROW * N + K // 256 * 320 + 4 * N
+    cores = min(16, os.cpu_count() or 1)
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    r = O.ref()
+    if r is not None and r.ref_has_avx2():
+        import ctypes as C
+
+        acts = O.ref_quantize("sx", x)
+        ws = [w_host] + [w_host.copy() for _ in range(copies - 1)]
+        ptrs = (C.c_void_p * copies)(*[w.ctypes.data for w in ws])
+        y = np.empty(N, np.float32)
+        ns = r.ref_bench_gemv(3, O.Q4_K, ptrs, copies, Q4K_ROW, N, acts.ctypes.data, acts.size, 1, K, y.ctypes.data,
+                              cores, 2)
+        per = ns / 2 / 1e9
+        iters = max(4, int(budget_s / max(per, 1e-6)))
+        ns = r.ref_bench_gemv(3, O.Q4_K, ptrs, copies, Q4K_ROW, N, acts.ctypes.data, acts.size, 1, K, y.ctypes.data,
+                              cores, iters)
+        sec = ns / iters / 1e9
+        return {"value": round(nbytes / sec / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "reference",
+                "ms_per_call": round(sec * 1e3, 4), "tokens_per_s": round(1.0 / sec, 1),
+                "sample": f"{iters} calls of the full K=4096 N=14336 M=1 Q4_K GEMV, dynacore AVX2 "
+                          f"dot_rows_n_sx_q4_K (sub-scaled int8 activations, its x86 default), {cores} threads "
+                          f"over 16-row units, {copies} rotated weight copies",
+                "cpu": cpu, "isa": "avx2+fma+f16c"}
+    # scalar oracle restatement on a bounded sample of rows, scaled to N
+    a = O.quantize_act(O.ACT_SX, x[None])
+    rows = 256
+    t0 = time.perf_counter()
+    O.matmul(O.Q4_K, O.ACT_SX, w_host[:rows], a, K)
+    sec = (time.perf_counter() - t0) * N / rows
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "ms_per_call": round(sec * 1e3, 3), "tokens_per_s": round(1.0 / sec, 2),
+            "sample": f"{rows} of {N} rows of the Q4_K x sub-scaled GEMV (scalar oracle), scaled to N", "cpu": cpu}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--copies", type=int, default=16, help="rotated weight copies (x 33 MB)")
+    ap.add_argument("--gemm-m", type=int, default=512)
+    ap.add_argument("--gemm-iters", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=1.5)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path would shard the weight "
+              f"rows across GPUs, see DESIGN.md; no multi-GPU figure is produced)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import dynalm_amd as dq
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream().cuda_stream
+    log(f"device {torch.cuda.get_device_name(0)}; building inputs")
+
+    # ---- weights: `copies` device copies of one random Q4_K matrix
+    w_host = random_q4k_rows(N, K, 20261201)
+    w_src = torch.from_numpy(w_host).cuda()
+    weights = [dq.Weight.upload_device(dq.Q4_K, w_src, N, K, Q4K_ROW, stream) for _ in range(args.copies)]
+    del w_src
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1234)
+
+    # ---- decode step: quantize x (M=1) to Q8_K + GEMV
+    x = torch.randn((1, K), generator=gen, device="cuda", dtype=torch.float32)
+    acts = torch.empty((1, Q8K_ROW), dtype=torch.uint8, device="cuda")
+    y = torch.empty((1, N), dtype=torch.float32, device="cuda")
+    nc = args.copies
+
+    def step(i: int) -> None:
+        dq.act_quantize(dq.ACT_Q8_K, x, 1, K, K, acts, stream)
+        dq.gemv(weights[i % nc], dq.ACT_Q8_K, acts, 1, 0, N, y, N, None, stream)
+
+    def gemv_only(i: int) -> None:
+        dq.gemv(weights[i % nc], dq.ACT_Q8_K, acts, 1, 0, N, y, N, None, stream)
+
+    log(f"decode step x{args.steps} (warmup {args.warmup})")
+    ms_step = time_launches(step, args.steps, args.warmup)
+    log("GEMV kernel alone")
+    ms_gemv = time_launches(gemv_only, args.steps, args.warmup)
+    bytes_step = Q4K_ROW * N + Q8K_ROW + 4 * N
+    value = bytes_step / (ms_step * 1e-3) / 1e9
+    achieved = bytes_step / (ms_gemv * 1e-3) / 1e9
+
+    # ---- prefill GEMM, M = 512
+    m = args.gemm_m
+    xg = torch.randn((m, K), generator=gen, device="cuda", dtype=torch.float32)
+    ag = torch.empty((m, Q8K_ROW), dtype=torch.uint8, device="cuda")
+    dq.act_quantize(dq.ACT_Q8_K, xg, m, K, K, ag, stream)
+    yg = torch.empty((m, N), dtype=torch.float32, device="cuda")
+    ng = min(4, nc)
+
+    def gemm(i: int) -> None:
+        dq.gemm(weights[i % ng], dq.ACT_Q8_K, ag, m, 0, N, yg, N, None, stream)
+
+    log(f"GEMM M={m} x{args.gemm_iters}")
+    ms_gemm = time_launches(gemm, args.gemm_iters, 3)
+    ops = 2.0 * m * N * K
+    tops = ops / (ms_gemm * 1e-3) / 1e12
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: random valid Q4_K blocks (fp16 d/dmin in U(0.002,0.02)), x ~ N(0,1)",
+        "config": {
+            "workload": "config 3 gate/up decode step: quantize x to Q8_K + Q4_K GEMV, K=4096 N=14336 M=1",
+            "weight_copies": nc,
+            "weight_bytes": Q4K_ROW * N,
+            "algorithmic_bytes_per_step": bytes_step,
+        },
+        "pct_peak_hbm": round(100 * value / PEAK_HBM_GBS, 2),
+        "tokens_per_s": round(1e3 / ms_step, 1),
+        "roofline": {
+            "kernel": "k_gemv_q4k<Q8_K, M=1>",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "ms_per_launch": round(ms_gemv, 5),
+        },
+        "gemm": {
+            "workload": f"config 4 prefill: Q4_K x Q8_K GEMM, M={m} K=4096 N=14336",
+            "ms_per_launch": round(ms_gemm, 4),
+            "tops": round(tops, 2),
+            "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2),
+            "tokens_per_s": round(m / (ms_gemm * 1e-3), 1),
+            "roofline": {"kernel": "k_gemm_q4k", "bound": "mfma", "achieved": round(tops, 2),
+                         "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4),
+                         "traffic": None},
+        },
+    }
+    if not args.no_cpu:
+        log("CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(w_host, 4, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

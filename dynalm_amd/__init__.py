@@ -1,0 +1,202 @@
+"""dynalm_amd -- MI355X-native block-quantized matmul (Python mirror of the C ABI).
+
+The product is the C-ABI library ``dynalm_amd/lib/libdynaq.so`` (include/dynaq.h):
+hand-written gfx950 HIP kernels behind dynacore's quantized-matmul entry points.
+This module binds it with ctypes; device buffers are passed as integer device
+pointers and streams as integer hipStream_t handles, so any allocator (PyTorch
+included) can supply them. Loading fails loudly when the library is missing:
+there is no CPU fallback.
+
+Entry points mirror the reference's operator interface (names and argument
+meaning of dynacore/include/dynacore/cpu/qmm.h:116-137 and
+dynacore/include/dynacore/device/device.h:89-161):
+
+    Weight.upload(dtype, rows, k)      Device::upload + prepack_weight
+    act_quantize(fmt, x, m, k, ...)    qmm::Kernels::quantize_row / QuantizeActFn
+    gemv(w, fmt, acts, m, n0, n1, ...) qmm::Kernels::gemv / DotQ8RowsNFn
+    gemm(w, fmt, acts, m, n0, n1, ...) qmm::Kernels::gemm
+    matmul(w, x, m, ...)               Device::matmul
+
+Errors raise DqError carrying dynacore's StatusCode value
+(dynacore/include/dynacore/base/status.h:19-32).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+__all__ = [
+    "Q4_0", "Q8_0", "Q4_K", "Q6_K", "ACT_PER32", "ACT_Q8_0", "ACT_Q8_K", "GEMV_MAX_ROWS",
+    "DqError", "lib", "lib_path", "row_bytes", "act_row_bytes", "act_format_for", "Weight",
+    "act_quantize", "gemv", "gemm", "matmul", "partials_count", "debug_partials", "EXPORTS",
+]
+
+Q4_0, Q8_0, Q4_K, Q6_K = 6, 10, 14, 16
+ACT_PER32, ACT_Q8_0, ACT_Q8_K = 0, 1, 2
+GEMV_MAX_ROWS = 16
+
+STATUS_NAMES = {
+    0: "ok", 1: "invalid_argument", 2: "not_found", 3: "already_exists", 4: "out_of_memory",
+    5: "resource_exhausted", 6: "unsupported", 7: "io_error", 8: "corrupt", 9: "cancelled",
+    10: "deadline_exceeded", 11: "internal",
+}
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def lib_path() -> str:
+    return os.environ.get("DYNAQ_LIB", os.path.join(_HERE, "lib", "libdynaq.so"))
+
+
+_P = C.c_void_p
+_I64 = C.c_int64
+_I = C.c_int
+
+# Every symbol include/dynaq.h declares, with its ctypes signature.
+EXPORTS = {
+    "dq_version": (C.c_char_p, []),
+    "dq_last_error": (C.c_char_p, []),
+    "dq_row_bytes": (_I64, [_I, _I64]),
+    "dq_act_row_bytes": (_I64, [_I, _I64]),
+    "dq_act_format_for": (_I, [_I]),
+    "dq_weight_upload": (_I, [_I, _P, _I64, _I64, _I64, _P, C.POINTER(_P)]),
+    "dq_weight_upload_device": (_I, [_I, _P, _I64, _I64, _I64, _P, C.POINTER(_P)]),
+    "dq_weight_download": (_I, [_P, _P, _I64, _P]),
+    "dq_weight_free": (_I, [_P]),
+    "dq_weight_info": (_I, [_P, C.POINTER(_I), C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64)]),
+    "dq_act_quantize": (_I, [_I, _P, _I64, _I64, _I64, _P, _P]),
+    "dq_gemv": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
+    "dq_gemm": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
+    "dq_matmul": (_I, [_P, _P, _I64, _I64, _P, _I64, _P, _P]),
+    "dq_partials_count": (_I, [_I, _I, _I64, C.POINTER(_I64), C.POINTER(_I64)]),
+    "dq_debug_partials": (_I, [_P, _I, _P, _I64, _P, _P, _P]),
+}
+
+
+class DqError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{STATUS_NAMES.get(code, code)}: {message}")
+        self.code = code
+        self.status = STATUS_NAMES.get(code, str(code))
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded C-ABI library (raises if it is not built)."""
+    global _lib
+    if _lib is None:
+        path = lib_path()
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built: run `python -m dynalm_amd.build` (no CPU fallback exists)")
+        L = C.CDLL(path)
+        for name, (res, args) in EXPORTS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise DqError(rc, lib().dq_last_error().decode())
+
+
+def _ptr(x) -> int | None:
+    """Device pointer of a torch tensor / int / None."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if hasattr(x, "data_ptr"):
+        return x.data_ptr()
+    raise TypeError(f"expected a device pointer, got {type(x)!r}")
+
+
+def row_bytes(dtype: int, k: int) -> int:
+    return int(lib().dq_row_bytes(dtype, k))
+
+
+def act_row_bytes(fmt: int, k: int) -> int:
+    return int(lib().dq_act_row_bytes(fmt, k))
+
+
+def act_format_for(dtype: int) -> int:
+    return int(lib().dq_act_format_for(dtype))
+
+
+class Weight:
+    """A weight matrix in the device layout (owns its device memory)."""
+
+    def __init__(self, handle: int):
+        self._h = C.c_void_p(handle)
+        dt, n, k, nbytes = _I(), _I64(), _I64(), _I64()
+        _check(lib().dq_weight_info(self._h, C.byref(dt), C.byref(n), C.byref(k), C.byref(nbytes)))
+        self.dtype, self.n, self.k, self.device_bytes = dt.value, n.value, k.value, nbytes.value
+
+    @classmethod
+    def upload(cls, dtype: int, rows: np.ndarray, k: int, stream: int = 0) -> "Weight":
+        """Upload GGUF rows (uint8 [n, row_bytes]) from host memory."""
+        rows = np.ascontiguousarray(np.atleast_2d(rows), dtype=np.uint8)
+        h = C.c_void_p()
+        _check(lib().dq_weight_upload(dtype, rows.ctypes.data, rows.shape[0], k, rows.shape[1], stream, C.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def upload_device(cls, dtype: int, dev_rows, n: int, k: int, row_stride: int, stream: int = 0) -> "Weight":
+        h = C.c_void_p()
+        _check(lib().dq_weight_upload_device(dtype, _ptr(dev_rows), n, k, row_stride, stream, C.byref(h)))
+        return cls(h.value)
+
+    def download(self, stream: int = 0) -> np.ndarray:
+        rb = row_bytes(self.dtype, self.k)
+        out = np.zeros((self.n, rb), np.uint8)
+        _check(lib().dq_weight_download(self._h, out.ctypes.data, rb, stream))
+        return out
+
+    @property
+    def handle(self) -> C.c_void_p:
+        if self._h is None:
+            raise ValueError("weight was freed")
+        return self._h
+
+    def free(self) -> None:
+        if getattr(self, "_h", None) is not None and _lib is not None:
+            lib().dq_weight_free(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def act_quantize(fmt: int, x, m: int, k: int, x_stride: int, out, stream: int = 0) -> None:
+    _check(lib().dq_act_quantize(fmt, _ptr(x), m, k, x_stride, _ptr(out), stream))
+
+
+def gemv(w: Weight, fmt: int, acts, m: int, n0: int, n1: int, y, y_stride: int, bias=None, stream: int = 0) -> None:
+    _check(lib().dq_gemv(w.handle, fmt, _ptr(acts), m, n0, n1, _ptr(y), y_stride, _ptr(bias), stream))
+
+
+def gemm(w: Weight, fmt: int, acts, m: int, n0: int, n1: int, y, y_stride: int, bias=None, stream: int = 0) -> None:
+    _check(lib().dq_gemm(w.handle, fmt, _ptr(acts), m, n0, n1, _ptr(y), y_stride, _ptr(bias), stream))
+
+
+def matmul(w: Weight, x, m: int, x_stride: int, y, y_stride: int, bias=None, stream: int = 0) -> None:
+    _check(lib().dq_matmul(w.handle, _ptr(x), m, x_stride, _ptr(y), y_stride, _ptr(bias), stream))
+
+
+def partials_count(dtype: int, fmt: int, k: int) -> tuple[int, int]:
+    u, s = _I64(), _I64()
+    _check(lib().dq_partials_count(dtype, fmt, k, C.byref(u), C.byref(s)))
+    return int(u.value), int(s.value)
+
+
+def debug_partials(w: Weight, fmt: int, acts, m: int, units, sb=None, stream: int = 0) -> None:
+    _check(lib().dq_debug_partials(w.handle, fmt, _ptr(acts), m, _ptr(units), _ptr(sb), stream))

@@ -1,0 +1,342 @@
+// dq_api.cpp -- the C ABI of libdynaq.so (declared in include/dynaq.h).
+//
+// Host-side C++: argument validation with dynacore's status codes
+// (dynacore/include/dynacore/base/status.h:19-32; shape rules of
+// validate_matmul_shape, dynacore/src/kernel/matmul_registry.cpp:264-278),
+// weight handles, the per-device activation scratch of dq_matmul, and dispatch
+// by M (GEMV up to DQ_GEMV_MAX_ROWS rows, as KernelPlan's decode row limit
+// selects the decode kernels, dynacore/src/kernel/matmul_registry.cpp:287-429).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/dynaq.h"
+#include "dq_internal.h"
+
+struct dq_weight {
+  dq::WeightDev dev;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  const int code = e == hipErrorOutOfMemory ? DQ_OUT_OF_MEMORY : DQ_INTERNAL;
+  return fail(code, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define DQ_HIP(call, what)                        \
+  do {                                            \
+    const hipError_t e_ = (call);                 \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+bool weight_type_ok(int t) { return t == DQ_Q4_0 || t == DQ_Q8_0 || t == DQ_Q4_K || t == DQ_Q6_K; }
+bool act_fmt_ok(int f) { return f == DQ_ACT_PER32 || f == DQ_ACT_Q8_0 || f == DQ_ACT_Q8_K; }
+
+// The (weight, activation) pairs with kernels: the per-32 formats with Q8_0 / Q4_0
+// (dynacore's kInt8Per32 contract), Q8_K and per-32 with the K-quants.
+bool pair_ok(int t, int f) {
+  if (t == DQ_Q8_0 || t == DQ_Q4_0) return f == DQ_ACT_PER32 || f == DQ_ACT_Q8_0;
+  return f == DQ_ACT_Q8_K || f == DQ_ACT_PER32;
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// Per-device scratch for dq_matmul's quantized activations (grows, never shrinks).
+struct Scratch {
+  std::mutex mu;
+  std::vector<void*> ptr;
+  std::vector<size_t> bytes;
+};
+Scratch g_scratch;
+
+int scratch_get(int device, size_t need, hipStream_t s, void** out) {
+  std::lock_guard<std::mutex> lock(g_scratch.mu);
+  if ((int)g_scratch.ptr.size() <= device) {
+    g_scratch.ptr.resize(device + 1, nullptr);
+    g_scratch.bytes.resize(device + 1, 0);
+  }
+  if (g_scratch.bytes[device] < need) {
+    if (g_scratch.ptr[device] != nullptr) {
+      DQ_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
+      DQ_HIP(hipFree(g_scratch.ptr[device]), "hipFree");
+      g_scratch.ptr[device] = nullptr;
+      g_scratch.bytes[device] = 0;
+    }
+    size_t sz = need < (1u << 20) ? (1u << 20) : need;
+    DQ_HIP(hipMalloc(&g_scratch.ptr[device], sz), "hipMalloc(scratch)");
+    g_scratch.bytes[device] = sz;
+  }
+  *out = g_scratch.ptr[device];
+  return DQ_OK;
+}
+
+int validate_shape(int dtype, int64_t n, int64_t k) {
+  if (!weight_type_ok(dtype)) return fail(DQ_UNSUPPORTED, "weight type %d is not supported", dtype);
+  if (n <= 0 || k <= 0) return fail(DQ_INVALID_ARGUMENT, "weight dims must be positive (n %lld, k %lld)", (long long)n, (long long)k);
+  const int be = dq::block_elems(dtype);
+  if (k % be != 0) {
+    return fail(DQ_INVALID_ARGUMENT, "k %lld is not a multiple of the block (%d)", (long long)k, be);
+  }
+  // Buffer resources address a plane of one 8-row group with 32-bit offsets.
+  if ((k / be) * 8 * 128 >= (int64_t)1 << 31) return fail(DQ_UNSUPPORTED, "k %lld is too large", (long long)k);
+  return DQ_OK;
+}
+
+int upload_impl(int dtype, const void* rows, bool host, int64_t n, int64_t k, int64_t row_bytes, void* stream,
+                dq_weight** out) {
+  if (out == nullptr || rows == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
+  *out = nullptr;
+  if (int rc = validate_shape(dtype, n, k); rc != DQ_OK) return rc;
+  const int64_t rb = dq_row_bytes(dtype, k);
+  if (row_bytes < rb) return fail(DQ_INVALID_ARGUMENT, "row_bytes %lld < %lld", (long long)row_bytes, (long long)rb);
+  hipStream_t s = as_stream(stream);
+  auto* w = new (std::nothrow) dq_weight();
+  if (w == nullptr) return fail(DQ_OUT_OF_MEMORY, "host allocation failed");
+  dq::WeightDev& d = w->dev;
+  d.dtype = dtype;
+  d.n = n;
+  d.k = k;
+  d.n_pad = (n + dq::kRowGroup - 1) / dq::kRowGroup * dq::kRowGroup;
+  d.nblk = k / dq::block_elems(dtype);
+  hipError_t e = hipGetDevice(&d.device);
+  int rc = DQ_OK;
+  const uint8_t* src = static_cast<const uint8_t*>(rows);
+  void* staging = nullptr;
+  for (int p = 0; p < dq::num_planes(dtype) && e == hipSuccess; ++p) {
+    d.plane_bytes[p] = d.n_pad * d.nblk * dq::plane_unit(dtype, p);
+    e = hipMalloc(reinterpret_cast<void**>(&d.plane[p]), (size_t)d.plane_bytes[p]);
+    if (e == hipSuccess) e = hipMemsetAsync(d.plane[p], 0, (size_t)d.plane_bytes[p], s);
+  }
+  if (e == hipSuccess && host) {
+    e = hipMalloc(&staging, (size_t)(n * row_bytes));
+    if (e == hipSuccess) e = hipMemcpyAsync(staging, rows, (size_t)(n * row_bytes), hipMemcpyHostToDevice, s);
+    src = static_cast<const uint8_t*>(staging);
+  }
+  if (e == hipSuccess) e = dq::launch_repack(dtype, src, row_bytes, n, d.nblk, d.plane, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (staging != nullptr) hipFree(staging);
+  if (e != hipSuccess) {
+    rc = hip_fail(e, "weight upload");
+    for (int p = 0; p < dq::kMaxPlanes; ++p)
+      if (d.plane[p]) hipFree(d.plane[p]);
+    delete w;
+    return rc;
+  }
+  *out = w;
+  return DQ_OK;
+}
+
+int check_acts(const dq_weight* w, int fmt, const void* acts, int64_t m) {
+  if (w == nullptr || acts == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
+  if (!act_fmt_ok(fmt)) return fail(DQ_UNSUPPORTED, "activation format %d is not supported", fmt);
+  if (!pair_ok(w->dev.dtype, fmt)) {
+    return fail(DQ_UNSUPPORTED, "activation format %d is not supported with weight type %d", fmt, w->dev.dtype);
+  }
+  if (m < 0) return fail(DQ_INVALID_ARGUMENT, "m must be >= 0");
+  if (dq_act_row_bytes(fmt, w->dev.k) < 0) {
+    return fail(DQ_INVALID_ARGUMENT, "k %lld is not a multiple of the activation block", (long long)w->dev.k);
+  }
+  if (m * dq_act_row_bytes(fmt, w->dev.k) >= ((int64_t)1 << 32)) return fail(DQ_UNSUPPORTED, "activations exceed 4 GiB");
+  return DQ_OK;
+}
+
+int check_out(const dq_weight* w, int64_t m, int64_t n0, int64_t n1, float* y, int64_t y_stride) {
+  if (y == nullptr && m > 0) return fail(DQ_INVALID_ARGUMENT, "null output");
+  if (n0 < 0 || n1 > w->dev.n || n0 > n1) {
+    return fail(DQ_INVALID_ARGUMENT, "row range [%lld, %lld) outside [0, %lld)", (long long)n0, (long long)n1,
+                (long long)w->dev.n);
+  }
+  if (m > 1 && y_stride < n1) return fail(DQ_INVALID_ARGUMENT, "y_stride %lld < n1 %lld", (long long)y_stride, (long long)n1);
+  return DQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dq_version(void) { return "dynaq 0.1.0 (gfx950)"; }
+const char* dq_last_error(void) { return g_err.c_str(); }
+
+int64_t dq_row_bytes(int dtype, int64_t k) {
+  if (!weight_type_ok(dtype) || k < 0) return -1;
+  const int be = dq::block_elems(dtype);
+  if (k % be != 0) return -1;
+  return k / be * dq::block_bytes(dtype);
+}
+
+int64_t dq_act_row_bytes(int fmt, int64_t k) {
+  if (!act_fmt_ok(fmt) || k < 0) return -1;
+  const int be = dq::act_block_elems(fmt);
+  if (k % be != 0) return -1;
+  return k / be * dq::act_block_bytes(fmt);
+}
+
+int dq_act_format_for(int dtype) {
+  if (dtype == DQ_Q8_0 || dtype == DQ_Q4_0) return DQ_ACT_PER32;
+  if (dtype == DQ_Q4_K || dtype == DQ_Q6_K) return DQ_ACT_Q8_K;
+  return -1;
+}
+
+int dq_weight_upload(int dtype, const void* host_rows, int64_t n, int64_t k, int64_t row_bytes, void* stream,
+                     dq_weight** out) {
+  return upload_impl(dtype, host_rows, true, n, k, row_bytes, stream, out);
+}
+
+int dq_weight_upload_device(int dtype, const void* dev_rows, int64_t n, int64_t k, int64_t row_bytes, void* stream,
+                            dq_weight** out) {
+  return upload_impl(dtype, dev_rows, false, n, k, row_bytes, stream, out);
+}
+
+int dq_weight_download(const dq_weight* w, void* host_rows, int64_t row_bytes, void* stream) {
+  if (w == nullptr || host_rows == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
+  const dq::WeightDev& d = w->dev;
+  const int64_t rb = dq_row_bytes(d.dtype, d.k);
+  if (row_bytes < rb) return fail(DQ_INVALID_ARGUMENT, "row_bytes %lld < %lld", (long long)row_bytes, (long long)rb);
+  hipStream_t s = as_stream(stream);
+  void* staging = nullptr;
+  DQ_HIP(hipMalloc(&staging, (size_t)(d.n * row_bytes)), "hipMalloc(staging)");
+  hipError_t e = hipMemsetAsync(staging, 0, (size_t)(d.n * row_bytes), s);
+  if (e == hipSuccess) {
+    uint8_t* planes[dq::kMaxPlanes];
+    for (int p = 0; p < dq::kMaxPlanes; ++p) planes[p] = d.plane[p];
+    e = dq::launch_unpack(d.dtype, static_cast<uint8_t*>(staging), row_bytes, d.n, d.nblk, planes, s);
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(host_rows, staging, (size_t)(d.n * row_bytes), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  hipFree(staging);
+  if (e != hipSuccess) return hip_fail(e, "weight download");
+  return DQ_OK;
+}
+
+int dq_weight_free(dq_weight* w) {
+  if (w == nullptr) return DQ_OK;
+  for (int p = 0; p < dq::kMaxPlanes; ++p) {
+    if (w->dev.plane[p] != nullptr) hipFree(w->dev.plane[p]);
+  }
+  delete w;
+  return DQ_OK;
+}
+
+int dq_weight_info(const dq_weight* w, int* dtype, int64_t* n, int64_t* k, int64_t* device_bytes) {
+  if (w == nullptr) return fail(DQ_INVALID_ARGUMENT, "null weight");
+  if (dtype) *dtype = w->dev.dtype;
+  if (n) *n = w->dev.n;
+  if (k) *k = w->dev.k;
+  if (device_bytes) {
+    int64_t total = 0;
+    for (int p = 0; p < dq::kMaxPlanes; ++p) total += w->dev.plane_bytes[p];
+    *device_bytes = total;
+  }
+  return DQ_OK;
+}
+
+int dq_act_quantize(int fmt, const float* x, int64_t m, int64_t k, int64_t x_stride, void* out, void* stream) {
+  if (!act_fmt_ok(fmt)) return fail(DQ_UNSUPPORTED, "activation format %d is not supported", fmt);
+  const int64_t orb = dq_act_row_bytes(fmt, k);
+  if (orb < 0 || k <= 0) return fail(DQ_INVALID_ARGUMENT, "k %lld is not a multiple of the activation block", (long long)k);
+  if (m < 0) return fail(DQ_INVALID_ARGUMENT, "m must be >= 0");
+  if (m == 0) return DQ_OK;
+  if (x == nullptr || out == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
+  if (m > 1 && x_stride < k) return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)k);
+  if (k * 4 >= ((int64_t)1 << 32) || m > 65535) return fail(DQ_UNSUPPORTED, "activation shape too large");
+  if (reinterpret_cast<uintptr_t>(out) % 4 != 0) return fail(DQ_INVALID_ARGUMENT, "out must be 4-byte aligned");
+  DQ_HIP(dq::launch_quantize(fmt, x, m, k, x_stride, static_cast<uint8_t*>(out), orb, as_stream(stream)),
+         "quantize launch");
+  return DQ_OK;
+}
+
+int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0, int64_t n1, float* y,
+            int64_t y_stride, const float* bias, void* stream) {
+  if (int rc = check_acts(w, fmt, acts, m); rc != DQ_OK) return rc;
+  if (int rc = check_out(w, m, n0, n1, y, y_stride); rc != DQ_OK) return rc;
+  if (m == 0 || n0 == n1) return DQ_OK;
+  DQ_HIP(dq::launch_gemv(w->dev, fmt, static_cast<const uint8_t*>(acts), dq_act_row_bytes(fmt, w->dev.k), m, n0, n1, y,
+                         y_stride, bias, nullptr, as_stream(stream)),
+         "gemv launch");
+  return DQ_OK;
+}
+
+int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0, int64_t n1, float* y,
+            int64_t y_stride, const float* bias, void* stream) {
+  if (int rc = check_acts(w, fmt, acts, m); rc != DQ_OK) return rc;
+  if (int rc = check_out(w, m, n0, n1, y, y_stride); rc != DQ_OK) return rc;
+  if (!dq::gemm_supported(w->dev.dtype, fmt)) {
+    return fail(DQ_UNSUPPORTED, "no GEMM kernel for weight type %d with activation format %d", w->dev.dtype, fmt);
+  }
+  if (m == 0 || n0 == n1) return DQ_OK;
+  if ((m + 255) / 256 > 65535) return fail(DQ_UNSUPPORTED, "m too large");
+  DQ_HIP(dq::launch_gemm(w->dev, fmt, static_cast<const uint8_t*>(acts), dq_act_row_bytes(fmt, w->dev.k), m, n0, n1, y,
+                         y_stride, bias, as_stream(stream)),
+         "gemm launch");
+  return DQ_OK;
+}
+
+int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, float* y, int64_t y_stride,
+              const float* bias, void* stream) {
+  if (w == nullptr) return fail(DQ_INVALID_ARGUMENT, "null weight");
+  if (m < 0) return fail(DQ_INVALID_ARGUMENT, "m must be >= 0");
+  if (m == 0) return DQ_OK;
+  const int fmt = dq_act_format_for(w->dev.dtype);
+  const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
+  if (int rc = check_out(w, m, 0, w->dev.n, y, y_stride); rc != DQ_OK) return rc;
+  hipStream_t s = as_stream(stream);
+  void* acts = nullptr;
+  if (int rc = scratch_get(w->dev.device, (size_t)(m * arb), s, &acts); rc != DQ_OK) return rc;
+  if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, x_stride, acts, stream); rc != DQ_OK) return rc;
+  if (m > DQ_GEMV_MAX_ROWS && dq::gemm_supported(w->dev.dtype, fmt)) {
+    return dq_gemm(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
+  }
+  return dq_gemv(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
+}
+
+int dq_partials_count(int dtype, int fmt, int64_t k, int64_t* units, int64_t* sb_terms) {
+  if (!weight_type_ok(dtype) || !act_fmt_ok(fmt) || !pair_ok(dtype, fmt)) {
+    return fail(DQ_UNSUPPORTED, "unsupported pair (%d, %d)", dtype, fmt);
+  }
+  if (dq_row_bytes(dtype, k) < 0 || dq_act_row_bytes(fmt, k) < 0) return fail(DQ_INVALID_ARGUMENT, "bad k");
+  if (units) *units = dtype == DQ_Q6_K ? k / 16 : k / 32;
+  if (sb_terms) *sb_terms = (dtype == DQ_Q4_K || dtype == DQ_Q6_K) && fmt == DQ_ACT_Q8_K ? 2 * (k / 256) : 0;
+  return DQ_OK;
+}
+
+int dq_debug_partials(const dq_weight* w, int fmt, const void* acts, int64_t m, int32_t* units, int32_t* sb,
+                      void* stream) {
+  if (int rc = check_acts(w, fmt, acts, m); rc != DQ_OK) return rc;
+  int64_t nu = 0, ns = 0;
+  if (int rc = dq_partials_count(w->dev.dtype, fmt, w->dev.k, &nu, &ns); rc != DQ_OK) return rc;
+  if (units == nullptr || (ns > 0 && sb == nullptr)) return fail(DQ_INVALID_ARGUMENT, "null output");
+  if (m == 0) return DQ_OK;
+  const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
+  hipStream_t s = as_stream(stream);
+  DQ_HIP(dq::launch_units(w->dev, fmt, static_cast<const uint8_t*>(acts), arb, m, units, nu, s), "units launch");
+  if (ns > 0) {
+    // The GEMV kernel writes its exact super-block reductions; y goes to scratch.
+    void* yscratch = nullptr;
+    if (int rc = scratch_get(w->dev.device, (size_t)(m * w->dev.n * 4), s, &yscratch); rc != DQ_OK) return rc;
+    DQ_HIP(dq::launch_gemv(w->dev, fmt, static_cast<const uint8_t*>(acts), arb, m, 0, w->dev.n,
+                           static_cast<float*>(yscratch), w->dev.n, nullptr, sb, s),
+           "gemv launch");
+  }
+  return DQ_OK;
+}
+
+}  // extern "C"

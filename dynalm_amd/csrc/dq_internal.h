@@ -1,0 +1,40 @@
+// dq_internal.h -- host-side declarations shared by the C-ABI layer and the kernel launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dq_layout.h"
+
+namespace dq {
+
+// A weight on the device in the x8 layout of dq_layout.h.
+struct WeightDev {
+  int dtype = 0;
+  int device = 0;
+  int64_t n = 0, k = 0;    // logical rows and values per row
+  int64_t n_pad = 0;       // rows rounded up to a multiple of kRowGroup
+  int64_t nblk = 0;        // blocks (super-blocks for K-quants) per row
+  uint8_t* plane[kMaxPlanes] = {nullptr, nullptr, nullptr, nullptr};
+  int64_t plane_bytes[kMaxPlanes] = {0, 0, 0, 0};
+};
+
+hipError_t launch_quantize(int af, const float* x, int64_t m, int64_t k, int64_t x_stride, uint8_t* out, int64_t orb,
+                           hipStream_t s);
+hipError_t launch_repack(int t, const uint8_t* src, int64_t row_stride, int64_t n, int64_t nblk, uint8_t* const* planes,
+                         hipStream_t s);
+hipError_t launch_unpack(int t, uint8_t* dst, int64_t row_stride, int64_t n, int64_t nblk, uint8_t* const* planes,
+                         hipStream_t s);
+// dbg (nullable): per (row, weight row, super-block) the exact S and Mn of the
+// K-quant x Q8_K kernels.
+hipError_t launch_gemv(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
+                       float* y, int64_t ys, const float* bias, int32_t* dbg, hipStream_t s);
+hipError_t launch_units(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int32_t* units,
+                        int64_t nu, hipStream_t s);
+// int8 MFMA GEMM (Q4_K / Q6_K x Q8_K). Returns hipErrorInvalidValue for an
+// unsupported pair.
+hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
+                       float* y, int64_t ys, const float* bias, hipStream_t s);
+bool gemm_supported(int dtype, int af);
+
+}  // namespace dq

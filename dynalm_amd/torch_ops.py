@@ -1,0 +1,58 @@
+"""Torch-tensor conveniences over the C ABI (device memory and streams only).
+
+PyTorch supplies device buffers and the current HIP stream; every computation
+runs in libdynaq.so's kernels.
+"""
+from __future__ import annotations
+
+import torch
+
+import dynalm_amd as dq
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def quantize(fmt: int, x: torch.Tensor) -> torch.Tensor:
+    """x: [m, k] fp32 on the GPU -> [m, act_row_bytes] uint8."""
+    assert x.dtype == torch.float32 and x.is_cuda and x.dim() == 2 and x.stride(1) == 1
+    m, k = x.shape
+    out = torch.empty((m, dq.act_row_bytes(fmt, k)), dtype=torch.uint8, device=x.device)
+    dq.act_quantize(fmt, x, m, k, x.stride(0), out, stream())
+    return out
+
+
+def gemv(w: dq.Weight, fmt: int, acts: torch.Tensor, n0: int = 0, n1: int | None = None,
+         bias: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    m = acts.shape[0]
+    n1 = w.n if n1 is None else n1
+    y = torch.zeros((m, w.n), dtype=torch.float32, device=acts.device) if out is None else out
+    dq.gemv(w, fmt, acts, m, n0, n1, y, y.stride(0), bias, stream())
+    return y
+
+
+def gemm(w: dq.Weight, fmt: int, acts: torch.Tensor, n0: int = 0, n1: int | None = None,
+         bias: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    m = acts.shape[0]
+    n1 = w.n if n1 is None else n1
+    y = torch.zeros((m, w.n), dtype=torch.float32, device=acts.device) if out is None else out
+    dq.gemm(w, fmt, acts, m, n0, n1, y, y.stride(0), bias, stream())
+    return y
+
+
+def matmul(w: dq.Weight, x: torch.Tensor, bias: torch.Tensor | None = None,
+           out: torch.Tensor | None = None) -> torch.Tensor:
+    m = x.shape[0]
+    y = torch.empty((m, w.n), dtype=torch.float32, device=x.device) if out is None else out
+    dq.matmul(w, x, m, x.stride(0), y, y.stride(0), bias, stream())
+    return y
+
+
+def partials(w: dq.Weight, fmt: int, acts: torch.Tensor):
+    m = acts.shape[0]
+    nu, ns = dq.partials_count(w.dtype, fmt, w.k)
+    units = torch.zeros((m, w.n, nu), dtype=torch.int32, device=acts.device)
+    sb = torch.zeros((m, w.n, max(ns, 1)), dtype=torch.int32, device=acts.device)
+    dq.debug_partials(w, fmt, acts, m, units, sb if ns else None, stream())
+    return units, sb[:, :, :ns]

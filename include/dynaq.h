@@ -1,0 +1,156 @@
+/*
+ * dynaq.h -- C ABI of the MI355X block-quantized matmul library (libdynaq.so).
+ *
+ * y[m, n] = sum_k x[m, k] * w[n, k] (+ bias[n]) with w stored as GGUF blocks
+ * (Q8_0, Q4_0, Q4_K, Q6_K) and x quantized to int8 blocks on the GPU, behind
+ * the entry points dynacore's quantized matmul exposes:
+ *   dynacore/include/dynacore/device/device.h:89,103-106,161   Device::upload,
+ *       prepack_weight, matmul
+ *   dynacore/include/dynacore/cpu/qmm.h:116-137                qmm::Kernels
+ *       {quantize_row, gemv, gemm}
+ *   dynacore/include/dynacore/cpu/cpu_kernels.h:39,53-54       QuantizeActFn,
+ *       DotQ8RowsNFn
+ *
+ * Conventions (as the reference's, dynacore/include/dynacore/device/device.h:11-13
+ * and qmm.h:35-36):
+ *   - every pointer argument except host_rows of dq_weight_upload and
+ *     dq_weight_download is device memory owned by the caller;
+ *   - `stream` is a hipStream_t (NULL = the default stream); every call only
+ *     enqueues work on it, except upload/download/free, which synchronize it;
+ *   - calls return a dq_status (the values of dynacore's StatusCode,
+ *     dynacore/include/dynacore/base/status.h:19-32); no exception crosses the
+ *     ABI; dq_last_error() describes the last failure on the calling thread;
+ *   - weight handles are library-owned; calls on one stream are ordered, and
+ *     dq_matmul's activation scratch is per device (concurrent dq_matmul calls
+ *     on one device from different streams race, like CpuDevice's scratch,
+ *     dynacore/include/dynacore/cpu/cpu_device.h:106-118).
+ */
+#ifndef DYNAQ_H_
+#define DYNAQ_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DQ_API __attribute__((visibility("default")))
+
+/* dynacore::StatusCode (dynacore/include/dynacore/base/status.h:19-32). */
+typedef enum dq_status {
+  DQ_OK = 0,
+  DQ_INVALID_ARGUMENT = 1,
+  DQ_NOT_FOUND = 2,
+  DQ_ALREADY_EXISTS = 3,
+  DQ_OUT_OF_MEMORY = 4,
+  DQ_RESOURCE_EXHAUSTED = 5,
+  DQ_UNSUPPORTED = 6,
+  DQ_IO_ERROR = 7,
+  DQ_CORRUPT = 8,
+  DQ_CANCELLED = 9,
+  DQ_DEADLINE_EXCEEDED = 10,
+  DQ_INTERNAL = 11,
+} dq_status;
+
+/* Weight block types: dynacore::DType values (dynacore/include/dynacore/tensor/dtype.h:19-44),
+ * which are also GGUF's ggml_type ids' positions in dynacore's type table
+ * (dynalm/src/loader/gguf/gguf.cpp:38-48 maps GGUF ids 2/8/12/14 onto them). */
+typedef enum dq_dtype {
+  DQ_Q4_0 = 6,
+  DQ_Q8_0 = 10,
+  DQ_Q4_K = 14,
+  DQ_Q6_K = 16,
+} dq_dtype;
+
+/* Quantized activation formats (m rows of dq_act_row_bytes(fmt, k) bytes each):
+ *   DQ_ACT_PER32  dynacore ActBlockQ8 {float d; int32 sum; int8 q[32]}, 40 B per 32 values,
+ *                 d = amax/127, codes round half to even
+ *                 (dynacore/include/dynacore/cpu/cpu_kernels.h:31-37,
+ *                  dynacore/cpu/generic/kernels_generic.cpp:187-207);
+ *   DQ_ACT_Q8_0   GGUF block_q8_0 {fp16 d; int8 q[32]}, 34 B per 32 values, codes
+ *                 round half away from zero at the fp32 d
+ *                 (dynacore/src/quantization/quant_formats.cpp:60-74);
+ *   DQ_ACT_Q8_K   GGUF block_q8_K {float d; int8 q[256]; int16 bsums[16]}, 292 B per 256,
+ *                 d = amax256/127, codes round half to even
+ *                 (dynacore/include/dynacore/quantization/quant_formats.h:30,
+ *                  dynacore/cpu/avx2/kernels_avx2.cpp:638-644). */
+typedef enum dq_act_format {
+  DQ_ACT_PER32 = 0,
+  DQ_ACT_Q8_0 = 1,
+  DQ_ACT_Q8_K = 2,
+} dq_act_format;
+
+/* Activation rows at or below which dq_matmul runs the GEMV kernels. */
+#define DQ_GEMV_MAX_ROWS 16
+
+typedef struct dq_weight dq_weight;
+
+DQ_API const char* dq_version(void);
+/* Message of the last failing call on this thread ("" if none). */
+DQ_API const char* dq_last_error(void);
+
+/* Bytes of one GGUF row of k values of dtype (-1 if k is not a whole number of
+ * blocks); dynacore dtype_row_bytes (dynacore/src/tensor/dtype.cpp:50-54). */
+DQ_API int64_t dq_row_bytes(int dtype, int64_t k);
+/* Bytes of one quantized activation row (-1 if unsupported or misaligned). */
+DQ_API int64_t dq_act_row_bytes(int fmt, int64_t k);
+/* The activation format dq_matmul uses for weights of dtype: DQ_ACT_PER32 for
+ * Q8_0 / Q4_0, DQ_ACT_Q8_K for Q4_K / Q6_K. */
+DQ_API int dq_act_format_for(int dtype);
+
+/* Upload n GGUF rows of k values (row stride row_bytes >= dq_row_bytes(dtype, k))
+ * from host memory and repack them into the GPU layout of the current device.
+ * Replaces Device::upload + Device::prepack_weight
+ * (dynacore/include/dynacore/device/device.h:89,103-106) and qmm::pack_groups
+ * (dynacore/include/dynacore/cpu/qmm.h:109-114). Synchronizes `stream`. */
+DQ_API int dq_weight_upload(int dtype, const void* host_rows, int64_t n, int64_t k, int64_t row_bytes, void* stream,
+                            dq_weight** out);
+/* The same from rows already in device memory (not modified, not retained). */
+DQ_API int dq_weight_upload_device(int dtype, const void* dev_rows, int64_t n, int64_t k, int64_t row_bytes,
+                                   void* stream, dq_weight** out);
+/* Unpack the device copy back into GGUF rows in host memory (round-trip check). */
+DQ_API int dq_weight_download(const dq_weight* w, void* host_rows, int64_t row_bytes, void* stream);
+DQ_API int dq_weight_free(dq_weight* w);
+DQ_API int dq_weight_info(const dq_weight* w, int* dtype, int64_t* n, int64_t* k, int64_t* device_bytes);
+
+/* Quantize m rows of k fp32 values (row stride x_stride floats) into `out`
+ * (m rows of dq_act_row_bytes(fmt, k) bytes). Replaces QuantizeActFn
+ * (dynacore/include/dynacore/cpu/cpu_kernels.h:39) / qmm quantize_row
+ * (dynacore/include/dynacore/cpu/qmm.h:122-123); bit-identical results. */
+DQ_API int dq_act_quantize(int fmt, const float* x, int64_t m, int64_t k, int64_t x_stride, void* out, void* stream);
+
+/* y[r * y_stride + i] = dot(weight row i, activation row r) + (bias ? bias[i] : 0)
+ * for r < m and i in [n0, n1). `acts`: m rows in format fmt, as dq_act_quantize
+ * writes them. Replaces qmm::Kernels::gemv (dynacore/include/dynacore/cpu/qmm.h:125-126)
+ * and DotQ8RowsNFn (dynacore/include/dynacore/cpu/cpu_kernels.h:53-54).
+ * dq_gemv streams the weights once for up to DQ_GEMV_MAX_ROWS rows per pass; */
+DQ_API int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0, int64_t n1, float* y,
+                   int64_t y_stride, const float* bias, void* stream);
+/* dq_gemm runs the int8 MFMA GEMM (Q4_K / Q6_K with DQ_ACT_Q8_K); any m.
+ * Replaces qmm::Kernels::gemm (dynacore/include/dynacore/cpu/qmm.h:128-129). */
+DQ_API int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0, int64_t n1, float* y,
+                   int64_t y_stride, const float* bias, void* stream);
+
+/* y = x . w^T (+ bias): quantize x with dq_act_format_for(w), then GEMV for
+ * m <= DQ_GEMV_MAX_ROWS, else GEMM. Replaces Device::matmul
+ * (dynacore/include/dynacore/device/device.h:161; CpuDevice::matmul,
+ * dynacore/cpu/cpu_device.cpp:869-1177). Uses a per-device scratch buffer. */
+DQ_API int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, float* y, int64_t y_stride,
+                     const float* bias, void* stream);
+
+/* Exact integer partials of every (activation row r < m, weight row i < n):
+ * units[(r * n + i) * U + u] and sb[(r * n + i) * S + s], with U and S from
+ * dq_partials_count; the meaning of each is that of the CPU reference's integer
+ * sums (dynacore/cpu/generic/kernels_generic.cpp:210-310,
+ * dynacore/cpu/avx2/kernels_avx2.cpp:976-1058). The super-block terms come from
+ * the GEMV kernel's own exact reductions. sb may be NULL when S == 0. */
+DQ_API int dq_partials_count(int dtype, int fmt, int64_t k, int64_t* units, int64_t* sb_terms);
+DQ_API int dq_debug_partials(const dq_weight* w, int fmt, const void* acts, int64_t m, int32_t* units, int32_t* sb,
+                             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DYNAQ_H_ */

@@ -382,7 +382,6 @@ int dqo_quantize_act_rows(int fmt, const float* x, int64_t m, int64_t n, int64_t
  * consume the same bytes. */
 
 static int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
-static float round_fp16(float v) { return dqo_fp16_to_fp32(dqo_fp32_to_fp16(v)); }
 
 /* Q4_0: d = (value of largest magnitude) / -8 rounded to fp16, codes
  * clamp(floor(x / d + 8.5), 0, 15). */
@@ -669,11 +668,13 @@ float dqo_dot(int wtype, int fmt, const void* wrow, const void* arow, int64_t k)
           acc = acc + t6;
         }
       } else if (fmt == DQO_ACT_Q8_K) {
-        /* Q8_K order (super-block arithmetic of kernels_avx2.cpp:976-1014):
-         * acc = fma((float)S, d*da, acc); corr = fma(dmin*da, (float)Mn, corr). */
+        /* Q8_K: the exact super-block integers S and Mn of kernels_avx2.cpp:976-1014,
+         * combined in this library's canonical order
+         * u = d*(float)S; u = fma(-dmin, (float)Mn, u); acc = fma(da, u, acc). */
         const float da = rdf(a + b * 292);
-        acc = fmaf((float)sb[0], d * da, acc);
-        corr = fmaf(dmin * da, (float)sb[1], corr);
+        float u = d * (float)sb[0];
+        u = fmaf(-dmin, (float)sb[1], u);
+        acc = fmaf(da, u, acc);
       } else { /* sub-scaled, kernels_avx2.cpp:1221-1268 */
         const uint8_t* ab = a + b * 320;
         const float u = rdf(ab + 256);
@@ -697,8 +698,10 @@ float dqo_dot(int wtype, int fmt, const void* wrow, const void* arow, int64_t k)
           acc = acc + t3;
         }
       } else if (fmt == DQO_ACT_Q8_K) {
+        /* S of kernels_avx2.cpp:1019-1058; u = d*(float)S; acc = fma(da, u, acc). */
         const float da = rdf(a + b * 292);
-        acc = fmaf((float)sb[0], d * da, acc);
+        const float u = d * (float)sb[0];
+        acc = fmaf(da, u, acc);
       } else {
         const float u = rdf(a + b * 320 + 256);
         acc = fmaf((float)sb[0], d * u, acc);

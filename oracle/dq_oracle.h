@@ -32,7 +32,8 @@
  *                       dequantizers (d = 1, dmin = 0, unit scales).
  *   dots, per-32        reference generic dot_rows_* (kernels_generic.cpp:216-310),
  *                       bit-equal fp32; double-precision bound.
- *   dots, Q8_K / sx     the order defined here (no reference tier has it for Q8_K);
+ *   dots, Q8_K / sx     the order defined here (no reference tier has it for Q8_K:
+ *                       u = d*S; u = fma(-dmin, Mn, u); acc = fma(da, u, acc) per super-block);
  *                       reference AVX2 sb / sx kernels within fp32 tolerance and the
  *                       double-precision bound of test_int_kernels.cpp:131-147.
  *   weight encoders     our own (the reference has no Q4_0/Q4_K/Q6_K quantizer);

@@ -1,0 +1,84 @@
+"""The C-ABI library: loads, exports every symbol include/dynaq.h declares, and
+validates arguments before touching a GPU (CPU only; no compute calls)."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import pytest
+
+import dynalm_amd as dq
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dynaq.h")
+
+
+def declared_symbols() -> list[str]:
+    text = open(HEADER).read()
+    return re.findall(r"DQ_API\s+[\w\s\*]+?\b(dq_\w+)\s*\(", text)
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_symbols()
+    assert len(names) >= 15
+    lib = dq.lib()
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(dq.EXPORTS), set(names) ^ set(dq.EXPORTS)
+
+
+def test_exports_are_the_only_public_symbols():
+    import subprocess
+
+    out = subprocess.run(["nm", "-D", "--defined-only", dq.lib_path()], capture_output=True, text=True).stdout
+    public = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    assert {s for s in public if s.startswith("dq_")} == set(declared_symbols())
+
+
+def test_sizes():
+    # dtype_row_bytes (dynacore/src/tensor/dtype.cpp:24-54)
+    assert dq.row_bytes(dq.Q4_K, 4096) == 16 * 144
+    assert dq.row_bytes(dq.Q6_K, 14336) == 56 * 210
+    assert dq.row_bytes(dq.Q8_0, 4096) == 128 * 34
+    assert dq.row_bytes(dq.Q4_0, 4096) == 128 * 18
+    assert dq.row_bytes(dq.Q4_K, 100) == -1
+    assert dq.row_bytes(99, 256) == -1
+    assert dq.act_row_bytes(dq.ACT_Q8_K, 4096) == 16 * 292
+    assert dq.act_row_bytes(dq.ACT_PER32, 4096) == 128 * 40
+    assert dq.act_row_bytes(dq.ACT_Q8_0, 96) == 3 * 34
+    assert dq.act_row_bytes(dq.ACT_Q8_K, 96) == -1
+    assert dq.act_format_for(dq.Q4_K) == dq.ACT_Q8_K
+    assert dq.act_format_for(dq.Q6_K) == dq.ACT_Q8_K
+    assert dq.act_format_for(dq.Q8_0) == dq.ACT_PER32
+    assert dq.act_format_for(dq.Q4_0) == dq.ACT_PER32
+    assert dq.partials_count(dq.Q4_K, dq.ACT_Q8_K, 4096) == (128, 32)
+    assert dq.partials_count(dq.Q6_K, dq.ACT_Q8_K, 4096) == (256, 32)
+    assert dq.partials_count(dq.Q8_0, dq.ACT_PER32, 4096) == (128, 0)
+
+
+def _upload_status(dtype, n, k, row_bytes):
+    h = C.c_void_p()
+    buf = (C.c_uint8 * 64)()
+    return dq.lib().dq_weight_upload(dtype, C.addressof(buf), n, k, row_bytes, None, C.byref(h))
+
+
+def test_invalid_arguments_rejected_before_any_gpu_call():
+    """validate_matmul_shape's rules (dynacore/src/kernel/matmul_registry.cpp:264-278)
+    as status codes (dynacore StatusCode values)."""
+    assert _upload_status(3, 8, 256, 144) == 6            # kUnsupported weight type (i8)
+    assert _upload_status(dq.Q4_K, 8, 100, 144) == 1      # k not a multiple of the block
+    assert _upload_status(dq.Q4_K, 0, 256, 144) == 1      # n must be positive
+    assert _upload_status(dq.Q4_K, 8, 256, 100) == 1      # row stride < row bytes
+    assert b"row_bytes" in dq.lib().dq_last_error()
+    assert dq.lib().dq_act_quantize(7, None, 1, 256, 256, None, None) == 6
+    assert dq.lib().dq_act_quantize(dq.ACT_Q8_K, None, 1, 100, 100, None, None) == 1
+    assert dq.lib().dq_gemv(None, dq.ACT_Q8_K, None, 1, 0, 1, None, 1, None, None) == 1
+    assert dq.lib().dq_partials_count(dq.Q8_0, dq.ACT_Q8_K, 256, None, None) == 6
+    with pytest.raises(dq.DqError) as e:
+        dq.partials_count(dq.Q4_0, dq.ACT_Q8_K, 256)
+    assert e.value.status == "unsupported"
+
+
+def test_version():
+    assert b"gfx950" in dq.lib().dq_version()

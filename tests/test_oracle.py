@@ -1,0 +1,383 @@
+"""The CPU oracle, pinned (CPU only).
+
+Each oracle function is checked against something it does not share code with:
+the reference's own outputs (committed golden vectors from its compiled kernels,
+and the live build in oracle/_ref where present), numpy's IEEE conversions,
+independent bit-field decoders, brute-force integer sums and the reference
+tests' double-precision bounds. A planted mistake in the oracle (dropped term,
+wrong sign / index / rounding) fails at least one of these.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+from dqtest import BLOCK, TYPES, activations, weight_rows
+from oracle import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_vectors.npz")
+needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref (reference build) not present")
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(GOLDEN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+# ------------------------------------------------------------------ fp16
+
+
+def test_fp16_to_fp32_exhaustive_vs_numpy():
+    h = np.arange(65536, dtype=np.uint16)
+    mine = O.fp16_to_fp32(h)
+    ref = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(mine), nan)
+    assert np.array_equal(mine[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_fp32_to_fp16_vs_numpy():
+    rng = np.random.default_rng(3)
+    halves = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float32)
+    halves = halves[np.isfinite(halves)].astype(np.float64)
+    f = np.concatenate([
+        rng.integers(0, 2**32, 400000, dtype=np.uint64).astype(np.uint32).view(np.float32),
+        halves.astype(np.float32),
+        (halves * (1 + 2.0**-11)).astype(np.float32),   # exact midpoints (ties to even)
+        (halves * (1 + 2.0**-12)).astype(np.float32),
+        np.array([65504, 65519.996, 65520, 1e9, 2.0**-25, 2.0**-24 * 1.5, 2.0**-26, -0.0], np.float32),
+    ])
+    f = f[np.isfinite(f)]
+    with np.errstate(over="ignore"):
+        ref = f.astype(np.float16).view(np.uint16)
+    assert np.array_equal(O.fp32_to_fp16(f), ref)
+    nan = np.array([np.nan, -np.nan], np.float32)
+    assert list(O.fp32_to_fp16(nan)) == [0x7E00, 0xFE00]
+
+
+def test_fp16_golden(gold):
+    h = np.arange(65536, dtype=np.uint16)
+    mine, ref = O.fp16_to_fp32(h), gold["fp16_f"]
+    assert np.array_equal(np.isnan(mine), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(mine[ok].view(np.uint32), ref[ok].view(np.uint32))
+    assert np.array_equal(O.fp32_to_fp16(gold["f2h_f"]), gold["f2h_h"])
+
+
+# ---------------------------------------------------- Q4_K scale unpacking
+
+
+def _scale_min_bitfields(s: bytes, j: int) -> tuple[int, int]:
+    """Independent statement of the 12-byte layout as bit fields of a 96-bit integer:
+    scales 0-3 = bits 0-5 of bytes 0-3, mins 0-3 = bits 0-5 of bytes 4-7; scales 4-7 =
+    low nibble of bytes 8-11 + (bits 6-7 of bytes 0-3) << 4; mins 4-7 = high nibble
+    of bytes 8-11 + (bits 6-7 of bytes 4-7) << 4."""
+    v = int.from_bytes(s, "little")
+    byte = lambda i: (v >> (8 * i)) & 0xFF  # noqa: E731
+    if j < 4:
+        return byte(j) & 0x3F, byte(4 + j) & 0x3F
+    i = j - 4
+    return (byte(8 + i) & 0xF) | ((byte(i) >> 6) << 4), (byte(8 + i) >> 4) | ((byte(4 + i) >> 6) << 4)
+
+
+def test_scale_min_k4_brute_force():
+    import ctypes as C
+
+    lib = O.lib()
+    sc, mn = C.c_uint8(), C.c_uint8()
+    rng = np.random.default_rng(5)
+    for j in range(8):
+        # every value of each byte that j reads, other bytes random
+        for v in range(256):
+            for pos in {j % 4, 4 + j % 4, 8 + j % 4}:
+                s = bytearray(rng.integers(0, 256, 12, dtype=np.uint8).tobytes())
+                s[pos] = v
+                buf = (C.c_uint8 * 12).from_buffer_copy(bytes(s))
+                lib.dqo_scale_min_k4(j, C.addressof(buf), C.addressof(sc), C.addressof(mn))
+                assert (sc.value, mn.value) == _scale_min_bitfields(bytes(s), j)
+
+
+# ------------------------------------------------------------- quantizers
+
+
+@pytest.mark.parametrize("kind,fmt", [("q8_0", O.ACT_Q8_0), ("per32", O.ACT_PER32), ("sx", O.ACT_SX)])
+def test_act_quantizers_golden(gold, kind, fmt):
+    assert np.array_equal(O.quantize_act(fmt, gold["act_x"]), gold[f"act_{kind}"])
+
+
+def test_act_q8_K_golden(gold):
+    x = gold["act_x"]
+    mine = O.quantize_act(O.ACT_Q8_K, x).reshape(x.shape[0], -1, 292)
+    sb = gold["act_sb"].reshape(x.shape[0], -1, 40)  # ActBlockQ8 with one d per 8 blocks
+    assert np.array_equal(mine[:, :, 4:260].reshape(x.shape[0], -1), sb[:, :, 8:].reshape(x.shape[0], -1))
+    assert np.array_equal(mine[:, :, 0:4], sb[:, ::8, 0:4])
+    codes = mine[:, :, 4:260].view(np.int8).astype(np.int32).reshape(x.shape[0], -1, 16, 16)
+    bsums = mine[:, :, 260:292].copy().view(np.int16).reshape(x.shape[0], -1, 16)
+    assert np.array_equal(codes.sum(-1), bsums)
+
+
+def test_per32_invariants():
+    """test_int_kernels.cpp:119-128: |x - d q| <= d (0.5 + 3e-7 |q|), sum == sum(q), and
+    the amax element maps to +-127."""
+    x = activations(6, 1024, 11)
+    a = O.quantize_act(O.ACT_PER32, x).reshape(6, -1, 40)
+    d = a[:, :, 0:4].copy().view(np.float32)[..., 0].astype(np.float64)
+    s = a[:, :, 4:8].copy().view(np.int32)[..., 0]
+    q = a[:, :, 8:].view(np.int8).astype(np.int64)
+    xb = x.reshape(6, -1, 32).astype(np.float64)
+    assert np.all(np.abs(xb - d[..., None] * q) <= d[..., None] * (0.5 + 3e-7 * np.abs(q)) + 1e-12)
+    assert np.array_equal(q.sum(-1), s)
+    amax_at = np.abs(xb).argmax(-1)
+    qa = np.take_along_axis(q, amax_at[..., None], -1)[..., 0]
+    nz = d > 0
+    assert np.all(np.abs(qa[nz]) == 127)
+    assert np.all(q[~nz] == 0)
+
+
+def test_rounding_ties_separate_the_two_rules():
+    """amax = 127 gives d = 1 and id = 1, so x = k + 0.5 is an exact tie: per-32
+    rounds half to even, GGUF Q8_0 rounds half away from zero."""
+    x = np.zeros((1, 32), np.float32)
+    x[0, 0] = 127.0
+    x[0, 1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, -3.5]
+    per32 = O.quantize_act(O.ACT_PER32, x)[0, 8:].view(np.int8)
+    q80 = O.quantize_act(O.ACT_Q8_0, x)[0, 2:].view(np.int8)
+    assert list(per32[1:9]) == [0, 2, 2, 0, -2, -2, 4, -4]
+    assert list(q80[1:9]) == [1, 2, 3, -1, -2, -3, 4, -4]
+    assert per32[0] == 127 and q80[0] == 127
+
+
+def test_zero_block_and_nan():
+    x = np.zeros((1, 256), np.float32)
+    for fmt in (O.ACT_PER32, O.ACT_Q8_0, O.ACT_Q8_K):
+        assert not O.quantize_act(fmt, x).any()
+    x[0, 3] = np.nan
+    x[0, 4] = 2.0
+    a = O.quantize_act(O.ACT_PER32, x)[0]
+    assert a[:4].view(np.float32)[0] == np.float32(2.0) / np.float32(127.0)  # NaN never becomes amax
+    assert a[8 + 3].view(np.int8) == -127                                    # the clamp sends NaN to -127
+
+
+# ------------------------------------------------------------- dequantize
+
+
+@pytest.mark.parametrize("t", TYPES, ids=lambda t: O.TYPE_NAMES[t])
+def test_dequantize_golden(gold, t):
+    name = O.TYPE_NAMES[t]
+    mine = O.dequantize(t, gold[f"w_{name}"], 512)
+    assert np.array_equal(mine.view(np.uint32), gold[f"deq_{name}"].view(np.uint32))
+
+
+def test_dequantize_closed_forms():
+    """Hand-built blocks with known values."""
+    # Q8_0: d = 0.5 (fp16 0x3800), codes 0..31 -> 0.5 * i
+    b = np.zeros(34, np.uint8)
+    b[0:2] = np.array([0x3800], np.uint16).view(np.uint8)
+    b[2:] = np.arange(32, dtype=np.int8).view(np.uint8)
+    assert np.array_equal(O.dequantize(O.Q8_0, b, 32)[0], 0.5 * np.arange(32, dtype=np.float32))
+    # Q4_0: d = 1, nibbles lo = i % 16 -> value (i - 8), hi -> element 16 + i
+    b = np.zeros(18, np.uint8)
+    b[0:2] = np.array([0x3C00], np.uint16).view(np.uint8)
+    b[2:] = (np.arange(16) | ((15 - np.arange(16)) << 4)).astype(np.uint8)
+    want = np.concatenate([np.arange(16) - 8, (15 - np.arange(16)) - 8]).astype(np.float32)
+    assert np.array_equal(O.dequantize(O.Q4_0, b, 32)[0], want)
+    # Q4_K: d = 1, dmin = 1, sc_j = j + 1, m_j = 2j, all codes 3 -> (j+1)*3 - 2j
+    b = np.zeros(144, np.uint8)
+    b[0:4] = np.array([0x3C00, 0x3C00], np.uint16).view(np.uint8)
+    sc = [j + 1 for j in range(8)]
+    mn = [2 * j for j in range(8)]
+    for j in range(4):
+        b[4 + j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+        b[8 + j] = mn[j] | ((mn[j + 4] >> 4) << 6)
+        b[12 + j] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    b[16:] = 0x33
+    want = np.repeat([3 * sc[j] - mn[j] for j in range(8)], 32).astype(np.float32)
+    assert np.array_equal(O.dequantize(O.Q4_K, b, 256)[0], want)
+    # Q6_K: d = 1, scales = 1; value e has 6-bit code e % 64 -> e % 64 - 32
+    codes = np.arange(256) % 64
+    b = np.zeros(210, np.uint8)
+    for p in range(2):
+        v = codes[128 * p:128 * p + 128]
+        for l in range(32):
+            b[64 * p + l] = (v[l] & 15) | ((v[l + 64] & 15) << 4)
+            b[64 * p + l + 32] = (v[l + 32] & 15) | ((v[l + 96] & 15) << 4)
+            b[128 + 32 * p + l] = (v[l] >> 4) | ((v[l + 32] >> 4) << 2) | ((v[l + 64] >> 4) << 4) | ((v[l + 96] >> 4) << 6)
+    b[192:208] = 1
+    b[208:210] = np.array([0x3C00], np.uint16).view(np.uint8)
+    assert np.array_equal(O.dequantize(O.Q6_K, b, 256)[0], (codes - 32).astype(np.float32))
+
+
+# ---------------------------------------------------------------- partials
+
+
+def _int_codes(t: int, w: np.ndarray, k: int) -> np.ndarray:
+    """Integer weight codes recovered through the dequantizer with d = 1, dmin = 0
+    and unit scales (the reference's own dequantizer where oracle/_ref exists)."""
+    w = w.copy()
+    be, bb = BLOCK[t]
+    one = np.array([0x3C00], np.uint16).view(np.uint8)
+    for b in range(k // be):
+        o = b * bb
+        if t in (O.Q8_0, O.Q4_0):
+            w[:, o:o + 2] = one
+        elif t == O.Q4_K:
+            w[:, o:o + 2] = one
+            w[:, o + 2:o + 4] = 0
+            w[:, o + 4:o + 16] = np.array([1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1], np.uint8)
+        else:
+            w[:, o + 192:o + 208] = 1
+            w[:, o + 208:o + 210] = one
+    if O.ref_available():
+        deq = np.stack([O.ref_dequantize(t, w[i], k) for i in range(w.shape[0])])
+    else:
+        deq = O.dequantize(t, w, k)
+    codes = deq.astype(np.int64)
+    assert np.array_equal(codes.astype(np.float32), deq)
+    return codes
+
+
+def _act_codes(fmt: int, a: np.ndarray, k: int) -> np.ndarray:
+    if fmt == O.ACT_PER32:
+        return a.reshape(a.shape[0], -1, 40)[:, :, 8:].view(np.int8).reshape(a.shape[0], k).astype(np.int64)
+    if fmt == O.ACT_Q8_0:
+        return a.reshape(a.shape[0], -1, 34)[:, :, 2:].view(np.int8).reshape(a.shape[0], k).astype(np.int64)
+    if fmt == O.ACT_Q8_K:
+        return a.reshape(a.shape[0], -1, 292)[:, :, 4:260].view(np.int8).reshape(a.shape[0], k).astype(np.int64)
+    return a.reshape(a.shape[0], -1, 320)[:, :, :256].view(np.int8).reshape(a.shape[0], k).astype(np.int64)
+
+
+PAIRS_ALL = [(O.Q8_0, O.ACT_PER32), (O.Q8_0, O.ACT_Q8_0), (O.Q4_0, O.ACT_PER32), (O.Q4_0, O.ACT_Q8_0),
+             (O.Q4_K, O.ACT_PER32), (O.Q4_K, O.ACT_Q8_K), (O.Q4_K, O.ACT_SX),
+             (O.Q6_K, O.ACT_PER32), (O.Q6_K, O.ACT_Q8_K), (O.Q6_K, O.ACT_SX)]
+
+
+@pytest.mark.parametrize("t,fmt", PAIRS_ALL, ids=lambda p: str(p))
+def test_partials_brute_force(t, fmt):
+    k = 512
+    w = weight_rows(t, 3, k, 77 + t, edge=True)
+    x = activations(2, k, 78)
+    a = O.quantize_act(fmt, x)
+    units, sb = O.partials(t, fmt, w, a, k)
+    wc = _int_codes(t, w, k)
+    ac = _act_codes(fmt, a, k)
+    ul = 16 if t == O.Q6_K else 32
+    prod = (ac[:, None, :] * wc[None, :, :]).reshape(2, 3, k // ul, ul).sum(-1)
+    assert np.array_equal(units, prod)
+    if sb.shape[-1]:
+        nsb = k // 256
+        for n in range(3):
+            for b in range(nsb):
+                blk = w[n, b * BLOCK[t][1]:(b + 1) * BLOCK[t][1]]
+                if t == O.Q4_K:
+                    scm = [_scale_min_bitfields(bytes(blk[4:16]), j) for j in range(8)]
+                    scale = [s for s, _ in scm]
+                    mins = [mm for _, mm in scm]
+                else:
+                    scale = list(blk[192:208].view(np.int8).astype(int))
+                    mins = [0] * 16
+                for r in range(2):
+                    mult = [1] * 8
+                    if fmt == O.ACT_SX:
+                        mult = list(a[r, b * 320 + 260:b * 320 + 276].copy().view(np.int16))
+                    nunit = 256 // ul
+                    S = sum(int(scale[u]) * int(mult[u * ul // 32]) * int(prod[r, n, b * nunit + u]) for u in range(nunit))
+                    assert sb[r, n, 2 * b] == S
+                    if t == O.Q4_K:
+                        sums = ac[r, b * 256:(b + 1) * 256].reshape(8, 32).sum(-1)
+                        assert sb[r, n, 2 * b + 1] == sum(int(mins[j]) * int(sums[j]) for j in range(8))
+
+
+# -------------------------------------------------------------------- dots
+
+
+@pytest.mark.parametrize("t", TYPES, ids=lambda t: O.TYPE_NAMES[t])
+def test_generic_dots_golden_bit_exact(gold, t):
+    name = O.TYPE_NAMES[t]
+    y = O.matmul(t, O.ACT_PER32, gold[f"w_{name}"], gold["act_per32"], 512)
+    assert np.array_equal(y.view(np.uint32), gold[f"dot_{name}"].view(np.uint32))
+
+
+@pytest.mark.parametrize("t", (O.Q4_K, O.Q6_K), ids=lambda t: O.TYPE_NAMES[t])
+def test_q8K_and_sx_dots_vs_reference_avx2(gold, t):
+    """Q8_K (canonical order) vs the reference super-block kernel on the same codes,
+    and sub-scaled vs the reference sx kernel: fp32 reorderings only."""
+    name = O.TYPE_NAMES[t]
+    w = gold[f"w_{name}"]
+    yq = O.matmul(t, O.ACT_Q8_K, w, O.quantize_act(O.ACT_Q8_K, gold["act_x"]), 512)
+    mag = np.abs(gold[f"sbdot_{name}"]).max()
+    assert np.max(np.abs(yq - gold[f"sbdot_{name}"])) <= 1e-5 * mag
+    ys = O.matmul(t, O.ACT_SX, w, gold["act_sx"], 512)
+    assert np.max(np.abs(ys - gold[f"sxdot_{name}"])) <= 1e-5 * np.abs(gold[f"sxdot_{name}"]).max()
+
+
+@pytest.mark.parametrize("t,fmt", PAIRS_ALL, ids=lambda p: str(p))
+def test_dots_within_double_bound(t, fmt):
+    """|y - y_double| <= 1e-5 * sum|w_i x_i| against the double product of the
+    dequantized weights and activations (test_int_kernels.cpp:131-147)."""
+    k = 1024
+    w = weight_rows(t, 5, k, 300 + t, edge=True)
+    x = activations(3, k, 301)
+    a = O.quantize_act(fmt, x)
+    y = O.matmul(t, fmt, w, a, k)
+    wf = O.dequantize(t, w, k).astype(np.float64)
+    af = O.dequantize_act(fmt, a, k).astype(np.float64)
+    ref = af @ wf.T
+    mag = np.abs(af) @ np.abs(wf).T
+    assert np.all(np.abs(y - ref) <= 1e-5 * mag + 1e-30)
+
+
+# ---------------------------------------------------------------- encoders
+
+
+@pytest.mark.parametrize("t", TYPES, ids=lambda t: O.TYPE_NAMES[t])
+def test_encoders_error_bound(t):
+    k = 2048
+    x = O.normal(9, 4 * k, std=0.02, outlier_frac=0.01, outlier_sigma=8.0).reshape(4, k)
+    w = O.encode_weight(t, x)
+    xr = O.dequantize(t, w, k)
+    be = BLOCK[t][0]
+    err = np.abs(xr - x).reshape(4, -1, 32 if t != O.Q6_K else 16)
+    span = np.abs(x).reshape(err.shape).max(-1, keepdims=True)
+    # Q4_K: 15 steps over [min(0, lo), hi] (<= 2 span), half a step of error plus the
+    # rounding of the 6-bit scale and offset (ceil) to the super-block grid; Q6_K: step
+    # span/31; Q8_0: step span/127. Q4_0 maps the largest magnitude to code -8, so the
+    # other side clamps at +7 steps of span/8: up to one full step there.
+    # (Q8_0 codes use the fp32 d but decode with its fp16 rounding: + 127 * 2^-11 steps)
+    bound = {O.Q8_0: (0.5 + 127 * 2.0**-11) / 127.0, O.Q4_0: 1.0 / 8.0, O.Q4_K: 0.6 * 2.0 / 15.0, O.Q6_K: 0.5 / 31.0}[t]
+    if t == O.Q6_K:
+        # Q6_K codes never clamp (|x| / step <= 31): half of the unit's own step d * sc
+        blk = w.reshape(4, -1, 210)
+        d = O.fp16_to_fp32(blk[:, :, 208:210].copy().view(np.uint16)[..., 0]).astype(np.float64)
+        st = d[..., None] * blk[:, :, 192:208].view(np.int8).astype(np.float64)
+        assert np.all(err <= 0.5 * st.reshape(err.shape[:2])[..., None] * (1 + 1e-3) + 1e-9)
+    else:
+        assert np.all(err <= bound * span * (1 + 5e-3) + 1e-7), be
+    if O.ref_available():
+        ref = np.stack([O.ref_dequantize(t, w[i], k) for i in range(4)])
+        assert np.array_equal(ref.view(np.uint32), xr.view(np.uint32))
+
+
+# ------------------------------------------------------------ live reference
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_live_reference_quantizers(seed):
+    x = activations(3, 2048, seed)
+    for kind, fmt in (("q8_0", O.ACT_Q8_0), ("per32", O.ACT_PER32), ("per32_avx2", O.ACT_PER32), ("sx", O.ACT_SX)):
+        ref = np.stack([O.ref_quantize(kind, x[i]) for i in range(3)])
+        assert np.array_equal(O.quantize_act(fmt, x), ref), kind
+
+
+@needs_ref
+@pytest.mark.parametrize("t", TYPES, ids=lambda t: O.TYPE_NAMES[t])
+def test_live_reference_generic_dots(t):
+    k = 2048
+    w = weight_rows(t, 6, k, 500 + t, edge=True)
+    a = O.quantize_act(O.ACT_PER32, activations(4, k, 501))
+    y = O.matmul(t, O.ACT_PER32, w, a, k)
+    ref = np.stack([O.ref_dot_rows(0, t, w[i], a, k) for i in range(6)], 1)
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
