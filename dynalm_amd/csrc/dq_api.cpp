@@ -96,8 +96,8 @@ int validate_shape(int dtype, int64_t n, int64_t k) {
   if (k % be != 0) {
     return fail(DQ_INVALID_ARGUMENT, "k %lld is not a multiple of the block (%d)", (long long)k, be);
   }
-  // Buffer resources address a plane of one 8-row group with 32-bit offsets.
-  if ((k / be) * 8 * 128 >= (int64_t)1 << 31) return fail(DQ_UNSUPPORTED, "k %lld is too large", (long long)k);
+  // Buffer resources address a plane of one 64-row group with 32-bit offsets.
+  if ((k / be) * dq::kRowGroup * 128 >= (int64_t)1 << 31) return fail(DQ_UNSUPPORTED, "k %lld is too large", (long long)k);
   return DQ_OK;
 }
 
@@ -299,13 +299,19 @@ int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, f
   const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
   if (int rc = check_out(w, m, 0, w->dev.n, y, y_stride); rc != DQ_OK) return rc;
   hipStream_t s = as_stream(stream);
+  if (m <= DQ_GEMV_MAX_ROWS || !dq::gemm_supported(w->dev.dtype, fmt)) {
+    // decode: quantization fused into the GEMV (one launch per 4 rows)
+    if (x == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
+    if (m > 1 && x_stride < w->dev.k) {
+      return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)w->dev.k);
+    }
+    DQ_HIP(dq::launch_gemv_fused(w->dev, x, x_stride, m, y, y_stride, bias, s), "gemv launch");
+    return DQ_OK;
+  }
   void* acts = nullptr;
   if (int rc = scratch_get(w->dev.device, (size_t)(m * arb), s, &acts); rc != DQ_OK) return rc;
   if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, x_stride, acts, stream); rc != DQ_OK) return rc;
-  if (m > DQ_GEMV_MAX_ROWS && dq::gemm_supported(w->dev.dtype, fmt)) {
-    return dq_gemm(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
-  }
-  return dq_gemv(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
+  return dq_gemm(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
 }
 
 int dq_partials_count(int dtype, int fmt, int64_t k, int64_t* units, int64_t* sb_terms) {

@@ -16,8 +16,10 @@
 // whose MFMA sum is exactly Mn. Three int8 MFMA accumulations per output give
 // S = L + 32*H and Mn exactly in int32.
 //
-// Tiling: a workgroup of 4 waves computes 256 activation rows x 64 weight rows;
-// wave w owns activation rows 64w .. 64w+63 (4 x 4 MFMA tiles of 16 x 16). Per
+// Tiling: a workgroup of 8 waves (two per SIMD, so one wave's MFMAs overlap
+// another's dequantization and epilogue) computes 256 activation rows x 64
+// weight rows; wave w owns 64 activation rows x 32 weight rows (4 x 2 MFMA tiles
+// of 16 x 16). Per
 // super-block the 256 x 256 activation codes (64 KB) and the three 64 x 256
 // weight planes (48 KB) are staged in LDS; the next super-block's global loads
 // are issued before the MFMA phase so they overlap it.
@@ -40,7 +42,7 @@ namespace {
 
 constexpr int kBM = 256;       // activation rows per workgroup
 constexpr int kBN = 64;        // weight rows per workgroup
-constexpr int kThreads = 256;  // 4 waves
+constexpr int kThreads = 512;  // 8 waves: 4 along M (64 rows each) x 2 along N (32 rows each)
 constexpr int kPlanes = 3;     // H, L, M
 
 // LDS layout (bytes)
@@ -75,14 +77,13 @@ DQ_DEV v4u lds_ld16(const uint8_t* lds, int off) { return *reinterpret_cast<cons
 
 }  // namespace
 
-__global__ __launch_bounds__(kThreads) void k_gemm_q4k(const uint8_t* __restrict__ qs_plane,
-                                                       const uint8_t* __restrict__ hdr_plane, int nb, int64_t n_pad,
-                                                       int64_t nt0, int64_t n0, int64_t n1,
-                                                       const uint8_t* __restrict__ acts, int64_t arb, int64_t m,
-                                                       float* __restrict__ y, int64_t ys,
-                                                       const float* __restrict__ bias) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_q4k(
+    const uint8_t* __restrict__ qs_plane, const uint8_t* __restrict__ hdr_plane, int nb, int64_t n_pad, int64_t nt0,
+    int64_t n0, int64_t n1, const uint8_t* __restrict__ acts, int64_t arb, int64_t m, float* __restrict__ y, int64_t ys,
+    const float* __restrict__ bias) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave & 3, wn = wave >> 2;  // this wave's 64 activation rows and 32 weight rows
   const int li = lane & 15, lg = lane >> 4;
   const int64_t nbase = nt0 + (int64_t)blockIdx.x * kBN;  // first weight row of the tile (multiple of 8)
   const int64_t mbase = (int64_t)blockIdx.y * kBM;
@@ -90,36 +91,37 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q4k(const uint8_t* __restrict
 
   // ---- global sources
   const auto ra = rsrc(acts + mbase * arb, (u32)(mrows * arb));
-  const int bn = t >> 2, bs = t & 3;  // B staging: weight row nbase + bn, K-step bs
-  const int64_t wn = nbase + bn;
-  const bool wn_ok = wn < n_pad;
-  const int64_t G = wn_ok ? wn / kRowGroup : 0, r8 = wn % kRowGroup;
-  const auto rq = rsrc(qs_plane + G * nb * 1024, wn_ok ? (u32)(nb * 1024) : 0u);
-  const auto rh = rsrc(hdr_plane + G * nb * 128, wn_ok ? (u32)(nb * 128) : 0u);
+  // B staging: weight row nbase + bn, K-step bs, half hh (qs bytes 32bs + 16hh .. +16)
+  const int bn = t >> 3, bs = (t >> 1) & 3, hh = t & 1;
+  const int64_t wn_row = nbase + bn;
+  const bool wn_ok = wn_row < n_pad;
+  // 64-row layout (dq_layout.h): qs chunk c of row r, super-block b at ((b*8 + c)*64 + r)*16
+  // of its row group; the header at (b*64 + r)*16.
+  const int64_t G = wn_ok ? wn_row / kRowGroup : 0, rr = wn_row % kRowGroup;
+  const auto rq = rsrc(qs_plane + G * nb * 8192, wn_ok ? (u32)(nb * 8192) : 0u);
+  const auto rh = rsrc(hdr_plane + G * nb * 1024, wn_ok ? (u32)(nb * 1024) : 0u);
 
   // ---- prefetch registers for one super-block
-  v4u ga[16];
+  v4u ga[8];
   u32 gda;
-  v4u gq0, gq1, ghd;
+  v4u gq, ghd;
   auto prefetch = [&](int b) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int row = (t >> 4) + 16 * i, col = t & 15;
+    for (int i = 0; i < 8; ++i) {
+      const int row = (t >> 4) + 32 * i, col = t & 15;
       ga[i] = ld16(ra, (u32)(row * arb + (int64_t)b * 292 + 4 + 16 * col));
     }
-    gda = ld4(ra, (u32)(t * arb + (int64_t)b * 292));
-    const u32 o = (u32)((b * 8 + r8) * 128 + 32 * bs);
-    gq0 = ld16(rq, o);
-    gq1 = ld16(rq, o + 16);
-    ghd = ld16(rh, (u32)((b * 8 + r8) * 16));
+    gda = ld4(ra, (u32)((t & 255) * arb + (int64_t)b * 292));
+    gq = ld16(rq, (u32)(((b * 8 + 2 * bs + hh) * 64 + rr) * 16));
+    ghd = ld16(rh, (u32)((b * 64 + rr) * 16));
   };
 
-  v4i_t acc[kPlanes][4][4];
-  float accf[4][4][4];
+  v4i_t acc[kPlanes][4][2];
+  float accf[4][2][4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
+    for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
       for (int p = 0; p < kPlanes; ++p) acc[p][mt][nt] = v4i_t{0, 0, 0, 0};
 #pragma unroll
@@ -129,29 +131,29 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q4k(const uint8_t* __restrict
   prefetch(0);
   for (int b = 0; b < nb; ++b) {
     __syncthreads();  // the previous super-block's LDS reads are done
-    // ---- stage activations
+    // ---- stage activations (values 64s .. 64s+63 of row `row` at [s][row])
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int row = (t >> 4) + 16 * i, col = t & 15;
+    for (int i = 0; i < 8; ++i) {
+      const int row = (t >> 4) + 32 * i, col = t & 15;
       lds_st16(lds, kLdsA + (((col >> 2) * kBM + row) * 64 + 16 * (col & 3)), ga[i]);
     }
-    reinterpret_cast<float*>(lds + kLdsDA)[t] = as_f(gda);
-    // ---- dequantize the weight tile: row bn, K-step bs
+    if (t < kBM) reinterpret_cast<float*>(lds + kLdsDA)[t] = as_f(gda);
+    // ---- dequantize: low nibbles -> lane group hh (sub-block 2bs), high -> 2 + hh (2bs+1)
     {
       int sca, mna, scb, mnb;
       scale_min_k4(2 * bs, ghd.y, ghd.z, ghd.w, sca, mna);
       scale_min_k4(2 * bs + 1, ghd.y, ghd.z, ghd.w, scb, mnb);
-      if (bs == 0) {
+      if (bs == 0 && hh == 0) {
         float* dw = reinterpret_cast<float*>(lds + kLdsDW);
         dw[2 * bn] = h2f(ghd.x);
         dw[2 * bn + 1] = h2f(ghd.x >> 16);
       }
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const v4u raw = (g & 1) ? gq1 : gq0;
-        const v4u q = g < 2 ? (raw & 0x0F0F0F0Fu) : ((raw >> 4) & 0x0F0F0F0Fu);
-        const u32 sc = (u32)(g < 2 ? sca : scb);
-        const u32 mn = (u32)(g < 2 ? mna : mnb) * 0x01010101u;
+      for (int half = 0; half < 2; ++half) {
+        const v4u q = half == 0 ? (gq & 0x0F0F0F0Fu) : ((gq >> 4) & 0x0F0F0F0Fu);
+        const int g = 2 * half + hh;
+        const u32 sc = (u32)(half == 0 ? sca : scb);
+        const u32 mn = (u32)(half == 0 ? mna : mnb) * 0x01010101u;
         const v4u H = {split_hi(q.x, sc), split_hi(q.y, sc), split_hi(q.z, sc), split_hi(q.w, sc)};
         const v4u L = {split_lo(q.x, sc), split_lo(q.y, sc), split_lo(q.z, sc), split_lo(q.w, sc)};
         const v4u M = {mn, mn, mn, mn};
@@ -163,31 +165,32 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q4k(const uint8_t* __restrict
     __syncthreads();
     if (b + 1 < nb) prefetch(b + 1);
 
-    // ---- MFMA phase: 4 K-steps of 64
-#pragma unroll
+    // ---- MFMA phase: 4 K-steps of 64 (not unrolled: keeps one step's fragments live)
+#pragma unroll 1
     for (int s = 0; s < 4; ++s) {
       v4u a[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        a[mt] = lds_ld16(lds, kLdsA + ((s * kBM + 64 * wave + 16 * mt + li) * 64 + 16 * lg));
+        a[mt] = lds_ld16(lds, kLdsA + ((s * kBM + 64 * wm + 16 * mt + li) * 64 + 16 * lg));
       }
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
+      for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
         for (int p = 0; p < kPlanes; ++p) {
-          const v4u bf = lds_ld16(lds, kLdsB + (((s * kPlanes + p) * kBN + 16 * nt + li) * 64 + 16 * lg));
+          const v4u bf = lds_ld16(lds, kLdsB + (((s * kPlanes + p) * kBN + 32 * wn + 16 * nt + li) * 64 + 16 * lg));
 #pragma unroll
           for (int mt = 0; mt < 4; ++mt) acc[p][mt][nt] = mfma(a[mt], bf, acc[p][mt][nt]);
         }
       }
     }
 
-    // ---- epilogue of this super-block: exact S, Mn -> fp32
+    // ---- epilogue of this super-block: exact S, Mn -> fp32 (canonical order)
     const float* dw = reinterpret_cast<const float*>(lds + kLdsDW);
     const float* da = reinterpret_cast<const float*>(lds + kLdsDA);
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const float d = dw[2 * (16 * nt + li)], dmin = dw[2 * (16 * nt + li) + 1];
+    for (int nt = 0; nt < 2; ++nt) {
+      const int nl = 32 * wn + 16 * nt + li;
+      const float d = dw[2 * nl], dmin = dw[2 * nl + 1];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
@@ -196,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q4k(const uint8_t* __restrict
           const int Mn = acc[2][mt][nt][e];
           float u = d * (float)S;
           u = fmaf(-dmin, (float)Mn, u);
-          accf[mt][nt][e] = fmaf(da[64 * wave + 16 * mt + 4 * lg + e], u, accf[mt][nt][e]);
+          accf[mt][nt][e] = fmaf(da[64 * wm + 16 * mt + 4 * lg + e], u, accf[mt][nt][e]);
         }
 #pragma unroll
         for (int p = 0; p < kPlanes; ++p) acc[p][mt][nt] = v4i_t{0, 0, 0, 0};
@@ -206,15 +209,15 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q4k(const uint8_t* __restrict
 
   // ---- store
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int64_t n = nbase + 16 * nt + li;
+  for (int nt = 0; nt < 2; ++nt) {
+    const int64_t n = nbase + 32 * wn + 16 * nt + li;
     if (n < n0 || n >= n1) continue;
     const float bn_ = bias ? bias[n] : 0.0f;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int64_t mm = mbase + 64 * wave + 16 * mt + 4 * lg + e;
+        const int64_t mm = mbase + 64 * wm + 16 * mt + 4 * lg + e;
         if (mm < m) y[mm * ys + n] = bias ? accf[mt][nt][e] + bn_ : accf[mt][nt][e];
       }
     }

@@ -29,6 +29,10 @@ hipError_t launch_unpack(int t, uint8_t* dst, int64_t row_stride, int64_t n, int
 // K-quant x Q8_K kernels.
 hipError_t launch_gemv(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
                        float* y, int64_t ys, const float* bias, int32_t* dbg, hipStream_t s);
+// Decode matmul with the activation quantization fused into the GEMV (fp32 rows x,
+// row stride xs floats; the weight's activation format, dq_act_format_for).
+hipError_t launch_gemv_fused(const WeightDev& w, const float* x, int64_t xs, int64_t m, float* y, int64_t ys,
+                             const float* bias, hipStream_t s);
 hipError_t launch_units(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int32_t* units,
                         int64_t nu, hipStream_t s);
 // int8 MFMA GEMM (Q4_K / Q6_K x Q8_K). Returns hipErrorInvalidValue for an

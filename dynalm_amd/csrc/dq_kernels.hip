@@ -10,6 +10,7 @@
 //                dynacore/cpu/avx2/kernels_avx2.cpp:976-1058
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "dq_device.h"
 #include "dq_internal.h"
@@ -44,6 +45,39 @@ DQ_DEV u32 codes4_rne(const float v[4], float id, int& sum) {
   return packed;
 }
 
+// Q8_K quantization of one 256-value super-block held 4 values per lane (lane l:
+// values 4l .. 4l+3): d = amax/127, codes round half to even at 1/d
+// (kernels_avx2.cpp:638-644). Returns the lane's 4 packed codes, d, and in every
+// lane the sum of the 16 codes of its 4-lane group (bsums[l / 4]).
+DQ_DEV u32 q8k_quant(const float v[4], float& d, int& bsum) {
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = max8f(amax);
+#pragma unroll
+  for (int s = 8; s < 64; s <<= 1) amax = fmaxf(amax, __shfl_xor(amax, s, 64));
+  d = amax / 127.0f;
+  const float id = d > 0 ? 1.0f / d : 0.0f;
+  int sum = 0;
+  const u32 packed = codes4_rne(v, id, sum);
+  sum += dpp<kQuadXor1>(sum);
+  sum += dpp<kQuadXor2>(sum);
+  bsum = sum;
+  return packed;
+}
+
+// Per-32 ActBlockQ8 quantization (kernels_generic.cpp:187-207) of 8 blocks held 4
+// values per lane (lanes 8i .. 8i+7 hold block i): returns the lane's packed codes,
+// the block's d and (in every lane of the block) the block's code sum.
+DQ_DEV u32 per32_quant(const float v[4], float& d, int& sum) {
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = max8f(amax);
+  d = amax / 127.0f;
+  const float id = d > 0 ? 1.0f / d : 0.0f;
+  int s = 0;
+  const u32 packed = codes4_rne(v, id, s);
+  sum = red8(s);
+  return packed;
+}
+
 __global__ __launch_bounds__(64) void k_quant_q8k(const float* __restrict__ x, int64_t x_stride, int64_t k,
                                                   uint8_t* __restrict__ out, int64_t orb) {
   const int l = threadIdx.x;
@@ -51,20 +85,12 @@ __global__ __launch_bounds__(64) void k_quant_q8k(const float* __restrict__ x, i
   const auto rx = rsrc(x + row * x_stride, (u32)(k * 4));
   float v[4];
   load4f(rx, (u32)((sb * 256 + 4 * l) * 4), v);
-  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  amax = max8f(amax);
-#pragma unroll
-  for (int s = 8; s < 64; s <<= 1) amax = fmaxf(amax, __shfl_xor(amax, s, 64));
-  const float d = amax / 127.0f;
-  const float id = d > 0 ? 1.0f / d : 0.0f;
-  int sum = 0;
-  const u32 packed = codes4_rne(v, id, sum);
+  float d;
+  int bsum;
+  const u32 packed = q8k_quant(v, d, bsum);
   uint8_t* o = out + row * orb + sb * 292;
   *reinterpret_cast<u32*>(o + 4 + 4 * l) = packed;
-  // bsums: 16 values = 4 lanes
-  sum += dpp<kQuadXor1>(sum);
-  sum += dpp<kQuadXor2>(sum);
-  if ((l & 3) == 0) *reinterpret_cast<int16_t*>(o + 260 + 2 * (l >> 2)) = (int16_t)sum;
+  if ((l & 3) == 0) *reinterpret_cast<int16_t*>(o + 260 + 2 * (l >> 2)) = (int16_t)bsum;
   if (l == 0) *reinterpret_cast<float*>(o) = d;
 }
 
@@ -83,15 +109,14 @@ __global__ __launch_bounds__(64) void k_quant_b32(const float* __restrict__ x, i
   const float d = amax / 127.0f;
   const bool valid = blk * 32 < k;
   if (AF == kActPer32) {
-    const float id = d > 0 ? 1.0f / d : 0.0f;
-    int sum = 0;
-    const u32 packed = codes4_rne(v, id, sum);
-    sum = red8(sum);
+    float dd;
+    int sum;
+    const u32 packed = per32_quant(v, dd, sum);
     if (valid) {
       uint8_t* o = out + row * orb + blk * 40;
       *reinterpret_cast<u32*>(o + 8 + 4 * (l & 7)) = packed;
       if ((l & 7) == 0) {
-        *reinterpret_cast<float*>(o) = d;
+        *reinterpret_cast<float*>(o) = dd;
         *reinterpret_cast<int32_t*>(o + 4) = sum;
       }
     }
@@ -121,11 +146,6 @@ struct Planes {
   uint8_t* p[kMaxPlanes];
 };
 
-DQ_DEV int64_t plane_offset(int t, int64_t n, int64_t blk, int64_t nblk, int unit, int off) {
-  const int64_t G = n / kRowGroup, r = n % kRowGroup;
-  return ((G * nblk + blk) * kRowGroup + r) * unit + off;
-}
-
 template <bool kPack>
 __global__ __launch_bounds__(256) void k_repack(int t, const uint8_t* __restrict__ src, uint8_t* __restrict__ dst_rows,
                                                 int64_t row_stride, int64_t n, int64_t nblk, Planes planes) {
@@ -137,7 +157,7 @@ __global__ __launch_bounds__(256) void k_repack(int t, const uint8_t* __restrict
   const int64_t blk = o / bb;
   int p, off;
   plane_of_byte(t, (int)(o % bb), &p, &off);
-  const int64_t at = plane_offset(t, row, blk, nblk, plane_unit(t, p), off);
+  const int64_t at = plane_offset(t, p, row, blk, nblk, off);
   if (kPack) {
     planes.p[p][at] = src[row * row_stride + o];
   } else {
@@ -146,299 +166,339 @@ __global__ __launch_bounds__(256) void k_repack(int t, const uint8_t* __restrict
 }
 
 // ===================================================================== GEMV
-// One wave (64 lanes) per group of 8 weight rows: lane l -> row r = l / 8 of the
-// group, chunk c = l % 8. M activation rows share each weight load. Weights are
-// loaded in batches of U blocks (super-blocks) ahead of their use.
+// Lane r of every wave owns weight row 64*G + r of the workgroup's row group G
+// (the 64-row layout of dq_layout.h), so at each step all lanes multiply their
+// own weight bytes with the same activation values: those are wave-uniform and
+// come through scalar loads, the weights through 1 KB-contiguous vector loads,
+// and a row's sums need no cross-lane reduction. The W waves of a workgroup
+// split the row's blocks into W contiguous slices (W times more bytes in flight
+// per row group).
+//
+// fp32 order. K-quants x Q8_K: each lane computes its super-blocks' exact S, Mn
+// and t = fma(-dmin, (float)Mn, d*(float)S) and writes t to LDS; after a barrier
+// lane r of wave 0 runs acc = fma(da, t, acc) over all super-blocks in order --
+// the canonical order of the CPU oracle, so outputs are bit-identical to it.
+// Per-32 activations: each wave accumulates its slice in the reference's generic
+// per-block order; the W slice sums are then added in slice order.
 
-// ---- Q4_K: chunk c = bytes 16c .. 16c+15 of the 128 B of qs: low nibbles are
-// values 16h .. 16h+15 of sub-block ja = 2*(c/2), high nibbles the same values of
-// sub-block jb = ja + 1, with h = c % 2.
-template <int AF, int M, int U>
-__global__ __launch_bounds__(64) void k_gemv_q4k(const uint8_t* __restrict__ qs_plane,
-                                                 const uint8_t* __restrict__ hdr_plane, int nb, int64_t g0,
-                                                 int64_t n0, int64_t n1, const uint8_t* __restrict__ acts,
-                                                 int64_t arb, float* __restrict__ y, int64_t ys,
-                                                 const float* __restrict__ bias, int32_t* __restrict__ dbg,
-                                                 int64_t dbg_n) {
-  const int lane = threadIdx.x, r = lane >> 3, c = lane & 7, jp = c >> 1, h = c & 1;
-  const int ja = 2 * jp, jb = ja + 1;
-  const int64_t G = g0 + blockIdx.x;
-  const int64_t n = G * kRowGroup + r;
-  const auto rq = rsrc(qs_plane + G * nb * 1024, (u32)(nb * 1024));
-  const auto rh = rsrc(hdr_plane + G * nb * 128, (u32)(nb * 128));
-  const auto ra = rsrc(acts, (u32)(M * arb));
-  float acc[M];
-#pragma unroll
-  for (int mm = 0; mm < M; ++mm) acc[mm] = 0.0f;
+typedef u32 v4ua __attribute__((ext_vector_type(4), aligned(4)));
 
-  for (int b0 = 0; b0 < nb; b0 += U) {
-    v4u q[U], hd[U], alo[U][M], ahi[U][M];
-    v2u ma[U][M], mb[U][M];
-    u32 da[U][M];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int b = b0 + u;
-      q[u] = ld16(rq, (u32)((b * 8 + r) * 128 + c * 16));
-      hd[u] = ld16(rh, (u32)((b * 8 + r) * 16));
-#pragma unroll
-      for (int mm = 0; mm < M; ++mm) {
-        if (AF == kActQ8_K) {
-          const u32 base = (u32)(mm * arb + (int64_t)b * 292);
-          alo[u][mm] = ld16(ra, base + 4 + 32 * ja + 16 * h);
-          ahi[u][mm] = ld16(ra, base + 4 + 32 * jb + 16 * h);
-          ma[u][mm] = ld8(ra, base + 260 + 8 * jp);  // bsums[4jp .. 4jp+3]
-          da[u][mm] = ld4(ra, base);
-        } else {  // per-32 ActBlockQ8
-          const u32 base = (u32)(mm * arb + ((int64_t)b * 8 + ja) * 40);
-          alo[u][mm] = ld16(ra, base + 8 + 16 * h);
-          ahi[u][mm] = ld16(ra, base + 40 + 8 + 16 * h);
-          ma[u][mm] = ld8(ra, base);       // d, sum of block ja
-          mb[u][mm] = ld8(ra, base + 40);  // d, sum of block jb
-        }
-      }
+// Wave-uniform loads (scalar loads when base and offset are uniform).
+DQ_DEV u32 uld(const uint8_t* __restrict__ p, u32 off) { return *reinterpret_cast<const u32*>(p + off); }
+DQ_DEV v4u uld16(const uint8_t* __restrict__ p, u32 off) {
+  const v4ua v = *reinterpret_cast<const v4ua*>(p + off);
+  return v4u{v.x, v.y, v.z, v.w};
+}
+DQ_DEV u32 bfe(u32 v, int off, int w) { return __builtin_amdgcn_ubfe(v, off, w); }
+DQ_DEV int sbfe(u32 v, int off, int w) { return __builtin_amdgcn_sbfe((int)v, off, w); }
+DQ_DEV int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Activation codes 16c .. 16c+15 of a 32-value per-32 / GGUF-Q8_0 block at base (uniform).
+template <int AF>
+DQ_DEV void act_codes32(const uint8_t* __restrict__ a, u32 base, v4u& x0, v4u& x1) {
+  if (AF == kActPer32) {
+    x0 = uld16(a, base + 8);
+    x1 = uld16(a, base + 24);
+  } else {  // GGUF Q8_0: codes at byte 2 of the 34-byte block
+    const u32 off = base + 2, al = off & ~3u;
+    const v4u y0 = uld16(a, al), y1 = uld16(a, al + 16);
+    const u32 y2 = uld(a, al + 32);
+    if ((off & 3u) == 0) {
+      x0 = y0;
+      x1 = y1;
+    } else {
+      x0 = v4u{__builtin_amdgcn_alignbyte(y0.y, y0.x, 2), __builtin_amdgcn_alignbyte(y0.z, y0.y, 2),
+               __builtin_amdgcn_alignbyte(y0.w, y0.z, 2), __builtin_amdgcn_alignbyte(y1.x, y0.w, 2)};
+      x1 = v4u{__builtin_amdgcn_alignbyte(y1.y, y1.x, 2), __builtin_amdgcn_alignbyte(y1.z, y1.y, 2),
+               __builtin_amdgcn_alignbyte(y1.w, y1.z, 2), __builtin_amdgcn_alignbyte(y2, y1.w, 2)};
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int b = b0 + u;
-      if (b >= nb) break;
-      const float d = h2f(hd[u].x), dmin = h2f(hd[u].x >> 16);
-      int sca, mna, scb, mnb;
-      scale_min_k4(ja, hd[u].y, hd[u].z, hd[u].w, sca, mna);
-      scale_min_k4(jb, hd[u].y, hd[u].z, hd[u].w, scb, mnb);
-      const v4u lo = q[u] & 0x0F0F0F0Fu;
-      const v4u hi = (q[u] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-      for (int mm = 0; mm < M; ++mm) {
-        const int plo = sdot16(lo, alo[u][mm], 0);
-        const int phi = sdot16(hi, ahi[u][mm], 0);
-        if (AF == kActQ8_K) {
-          // bsums of values 16h.. of sub-blocks ja, jb: indices 4jp + h and 4jp + 2 + h.
-          const int bsa = (int)(int16_t)(ma[u][mm].x >> (16 * h));
-          const int bsb = (int)(int16_t)(ma[u][mm].y >> (16 * h));
-          const int S = red8(sca * plo + scb * phi);
-          const int Mn = red8(mna * bsa + mnb * bsb);
-          // canonical order: u = d*S; u = fma(-dmin, Mn, u); acc = fma(da, u, acc)
-          float t = d * (float)S;
-          t = fmaf(-dmin, (float)Mn, t);
-          acc[mm] = fmaf(as_f(da[u][mm]), t, acc[mm]);
-          if (dbg != nullptr && c == 0 && n < dbg_n) {
-            int32_t* o = dbg + ((mm * dbg_n + n) * nb + b) * 2;
-            o[0] = S;
-            o[1] = Mn;
-          }
-        } else {
-          // Whole sub-block partials (lanes h = 0, 1 hold the two halves); lane h
-          // then adds sub-block ja (h = 0) or jb (h = 1) in the generic form
-          // a.d * (d*sc*P - dmin*m*a.sum) (kernels_generic.cpp:274).
-          const int pa = red2(plo), pb = red2(phi);
-          const int P = h ? pb : pa, sc = h ? scb : sca, mn = h ? mnb : mna;
-          const v2u meta = h ? mb[u][mm] : ma[u][mm];
-          const float ad = as_f(meta.x);
-          const float t = (d * (float)sc) * (float)P - (dmin * (float)mn) * (float)(int)meta.y;
-          acc[mm] += ad * t;
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int mm = 0; mm < M; ++mm) {
-    const float v = AF == kActQ8_K ? acc[mm] : red8f(acc[mm]);
-    if (c == 0 && n >= n0 && n < n1) y[mm * ys + n] = bias ? v + bias[n] : v;
   }
 }
 
-// ---- Q6_K: chunk c = ql bytes 16c .. 16c+15 (half p = c/4, Lp0 = 16*(c%4)): low
-// nibbles are values 128p + Lp0 + i, high nibbles values 128p + Lp0 + 64 + i; their
-// 2 high bits come from qh bytes 32p + 16*(c%2) + i at bit pairs s and s + 2,
-// s = (c%4)/2 (quant_formats.cpp:192-216). Scale units u_lo = 8p + c%4, u_hi = u_lo + 4.
-template <int AF, int M, int U>
-__global__ __launch_bounds__(64) void k_gemv_q6k(const uint8_t* __restrict__ ql_plane,
-                                                 const uint8_t* __restrict__ qh_plane,
-                                                 const uint8_t* __restrict__ sc_plane,
-                                                 const uint8_t* __restrict__ d_plane, int nb, int64_t g0, int64_t n0,
-                                                 int64_t n1, const uint8_t* __restrict__ acts, int64_t arb,
+// kFuse: the activations arrive as fp32 rows (x, row stride xs floats) and each
+// wave quantizes its own slice into LDS with the standalone quantizers' device
+// functions (q8k_quant / per32_quant), so the codes are the same bytes.
+template <int WT, int AF, int M, int W, int U, bool kFuse>
+__global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
+                                                 const uint8_t* __restrict__ p2, const uint8_t* __restrict__ p3,
+                                                 int nblk, int64_t g0, int64_t n0, int64_t n1,
+                                                 const uint8_t* __restrict__ acts_g, int64_t arb_g,
+                                                 const float* __restrict__ x, int64_t xs,
                                                  float* __restrict__ y, int64_t ys, const float* __restrict__ bias,
                                                  int32_t* __restrict__ dbg, int64_t dbg_n) {
-  const int lane = threadIdx.x, r = lane >> 3, c = lane & 7, p = c >> 2, cc = c & 3, s = cc >> 1;
-  const int ulo = 8 * p + cc, uhi = ulo + 4;
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr bool kSb = AF == kActQ8_K;
+  // Q8_K: t-terms [M][nblk][64] then da [M][nblk]; per-32: slice sums [W][M][64];
+  // kFuse: then the quantized activation rows [M][row bytes]
+  float* rec = reinterpret_cast<float*>(smem);
+  float* dav = rec + M * nblk * 64;
+  const int r = threadIdx.x & 63, wave = wave_id();
   const int64_t G = g0 + blockIdx.x;
   const int64_t n = G * kRowGroup + r;
-  const auto rl = rsrc(ql_plane + G * nb * 1024, (u32)(nb * 1024));
-  const auto rhh = rsrc(qh_plane + G * nb * 512, (u32)(nb * 512));
-  const auto rs = rsrc(sc_plane + G * nb * 128, (u32)(nb * 128));
-  const auto rd = rsrc(d_plane + G * nb * 16, (u32)(nb * 16));
-  const auto ra = rsrc(acts, (u32)(M * arb));
-  float acc[M];
-#pragma unroll
-  for (int mm = 0; mm < M; ++mm) acc[mm] = 0.0f;
-
-  for (int b0 = 0; b0 < nb; b0 += U) {
-    v4u L[U], H[U], alo[U][M], ahi[U][M];
-    v2u sc8[U];
-    u32 dw[U], m0[U][M], m1[U][M], m2[U][M];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int b = b0 + u;
-      L[u] = ld16(rl, (u32)((b * 8 + r) * 128 + 16 * c));
-      H[u] = ld16(rhh, (u32)((b * 8 + r) * 64 + 32 * p + 16 * (cc & 1)));
-      sc8[u] = ld8(rs, (u32)((b * 8 + r) * 16 + 8 * p));
-      dw[u] = ld2(rd, (u32)((b * 8 + r) * 2));
-#pragma unroll
-      for (int mm = 0; mm < M; ++mm) {
-        if (AF == kActQ8_K) {
-          const u32 base = (u32)(mm * arb + (int64_t)b * 292);
-          alo[u][mm] = ld16(ra, base + 4 + 128 * p + 16 * cc);
-          ahi[u][mm] = ld16(ra, base + 4 + 128 * p + 64 + 16 * cc);
-          m0[u][mm] = ld2(ra, base + 260 + 2 * ulo);
-          m1[u][mm] = ld2(ra, base + 260 + 2 * uhi);
-          m2[u][mm] = ld4(ra, base);
-        } else {
-          const int64_t bl = (int64_t)b * 8 + 4 * p + (cc >> 1), bh = bl + 2;
-          alo[u][mm] = ld16(ra, (u32)(mm * arb + bl * 40 + 8 + 16 * (cc & 1)));
-          ahi[u][mm] = ld16(ra, (u32)(mm * arb + bh * 40 + 8 + 16 * (cc & 1)));
-          m0[u][mm] = ld4(ra, (u32)(mm * arb + bl * 40));
-          m1[u][mm] = ld4(ra, (u32)(mm * arb + bh * 40));
+  const int b0 = wave * nblk / W, b1 = (wave + 1) * nblk / W;  // this wave's blocks
+  uint8_t* lds_act = smem + (kSb ? (size_t)M * nblk * 65 * 4 : (size_t)W * M * 64 * 4);
+  const int64_t arb = kFuse ? (int64_t)nblk * (kSb ? 292 : 40) : arb_g;
+  const uint8_t* acts = kFuse ? lds_act : acts_g;
+  if (kFuse) {
+    // quantize this wave's blocks of every activation row into LDS
+    for (int mm = 0; mm < M; ++mm) {
+      const int64_t kk = (int64_t)nblk * (kSb ? 256 : 32);
+      const auto rx = rsrc(x + mm * xs, (u32)(kk * 4));
+      if (kSb) {
+        for (int b = b0; b < b1; ++b) {
+          float v[4];
+          load4f(rx, (u32)((b * 256 + 4 * r) * 4), v);
+          float d;
+          int bsum;
+          const u32 packed = q8k_quant(v, d, bsum);
+          uint8_t* o = lds_act + (mm * nblk + b) * 292;
+          *reinterpret_cast<u32*>(o + 4 + 4 * r) = packed;
+          if ((r & 3) == 0) *reinterpret_cast<int16_t*>(o + 260 + 2 * (r >> 2)) = (int16_t)bsum;
+          if (r == 0) *reinterpret_cast<float*>(o) = d;
         }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int b = b0 + u;
-      if (b >= nb) break;
-      const v4u qlo = (L[u] & 0x0F0F0F0Fu) | (((H[u] >> (2 * s)) & 0x03030303u) << 4);
-      const v4u qhi = ((L[u] >> 4) & 0x0F0F0F0Fu) | (((H[u] >> (2 * s + 4)) & 0x03030303u) << 4);
-      const int sclo = (int)(int8_t)(sc8[u].x >> (8 * cc));
-      const int schi = (int)(int8_t)(sc8[u].y >> (8 * cc));
-      const float d = h2f(dw[u]);
-#pragma unroll
-      for (int mm = 0; mm < M; ++mm) {
-        if (AF == kActQ8_K) {
-          // sum (q - 32) a = sum q a - 32 * (sum of the 16 codes) = ... - 32 * bsums[u]
-          const int plo = sdot16(qlo, alo[u][mm], 0) - 32 * (int)(int16_t)m0[u][mm];
-          const int phi = sdot16(qhi, ahi[u][mm], 0) - 32 * (int)(int16_t)m1[u][mm];
-          const int S = red8(sclo * plo + schi * phi);
-          acc[mm] = fmaf(as_f(m2[u][mm]), d * (float)S, acc[mm]);
-          if (dbg != nullptr && c == 0 && n < dbg_n) {
-            int32_t* o = dbg + ((mm * dbg_n + n) * nb + b) * 2;
-            o[0] = S;
-            o[1] = 0;
-          }
-        } else {
-          // signed codes q - 32 as int8 bytes: flip bit 5, then extend its sign.
-          v4u slo = qlo ^ 0x20202020u, shi = qhi ^ 0x20202020u;
-          slo |= (slo & 0x20202020u) * 6u;
-          shi |= (shi & 0x20202020u) * 6u;
-          const int plo = sdot16(slo, alo[u][mm], 0);
-          const int phi = sdot16(shi, ahi[u][mm], 0);
-          // generic order per 16 values: ((a.d * d) * sc) * P (kernels_generic.cpp:304)
-          acc[mm] += ((as_f(m0[u][mm]) * d) * (float)sclo) * (float)plo;
-          acc[mm] += ((as_f(m1[u][mm]) * d) * (float)schi) * (float)phi;
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int mm = 0; mm < M; ++mm) {
-    const float v = AF == kActQ8_K ? acc[mm] : red8f(acc[mm]);
-    if (c == 0 && n >= n0 && n < n1) y[mm * ys + n] = bias ? v + bias[n] : v;
-  }
-}
-
-// ---- Q8_0 / Q4_0 with per-32 or GGUF Q8_0 activations: lane c takes the whole
-// 32-value block 8*it + c of its row.
-
-// 32 activation codes of a GGUF Q8_0 block (34 B; codes at byte 2, so 2-byte aligned).
-DQ_DEV void ld_q80_codes(__amdgpu_buffer_rsrc_t ra, u32 base, v4u& a0, v4u& a1) {
-  const u32 off = base + 2, al = off & ~3u, sh = off & 3u;  // sh is 0 or 2
-  const v4u x0 = ld16(ra, al), x1 = ld16(ra, al + 16);
-  const u32 x2 = ld4(ra, al + 32);
-  if (sh == 0) {
-    a0 = x0;
-    a1 = x1;
-  } else {
-    a0.x = __builtin_amdgcn_alignbyte(x0.y, x0.x, 2);
-    a0.y = __builtin_amdgcn_alignbyte(x0.z, x0.y, 2);
-    a0.z = __builtin_amdgcn_alignbyte(x0.w, x0.z, 2);
-    a0.w = __builtin_amdgcn_alignbyte(x1.x, x0.w, 2);
-    a1.x = __builtin_amdgcn_alignbyte(x1.y, x1.x, 2);
-    a1.y = __builtin_amdgcn_alignbyte(x1.z, x1.y, 2);
-    a1.z = __builtin_amdgcn_alignbyte(x1.w, x1.z, 2);
-    a1.w = __builtin_amdgcn_alignbyte(x2, x1.w, 2);
-  }
-}
-
-template <int WT, int AF, int M, int U>
-__global__ __launch_bounds__(64) void k_gemv_b32(const uint8_t* __restrict__ qs_plane,
-                                                 const uint8_t* __restrict__ d_plane, int nblk, int64_t g0, int64_t n0,
-                                                 int64_t n1, const uint8_t* __restrict__ acts, int64_t arb,
-                                                 float* __restrict__ y, int64_t ys, const float* __restrict__ bias) {
-  constexpr int kUnit = WT == kQ8_0 ? 32 : 16;  // qs bytes per block
-  const int lane = threadIdx.x, r = lane >> 3, c = lane & 7;
-  const int64_t G = g0 + blockIdx.x;
-  const int64_t n = G * kRowGroup + r;
-  const auto rq = rsrc(qs_plane + G * nblk * 8 * kUnit, (u32)(nblk * 8 * kUnit));
-  const auto rd = rsrc(d_plane + G * nblk * 16, (u32)(nblk * 16));
-  const auto ra = rsrc(acts, (u32)(M * arb));
-  const int ab = AF == kActPer32 ? 40 : 34;
-  float acc[M];
-#pragma unroll
-  for (int mm = 0; mm < M; ++mm) acc[mm] = 0.0f;
-
-  for (int i0 = 0; i0 < nblk; i0 += 8 * U) {
-    v4u w0[U], w1[U], a0[U][M], a1[U][M];
-    u32 dw[U], da[U][M], sa[U][M];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int blk = i0 + 8 * u + c;
-      w0[u] = ld16(rq, (u32)((blk * 8 + r) * kUnit));
-      if (WT == kQ8_0) w1[u] = ld16(rq, (u32)((blk * 8 + r) * kUnit + 16));
-      dw[u] = ld2(rd, (u32)((blk * 8 + r) * 2));
-#pragma unroll
-      for (int mm = 0; mm < M; ++mm) {
-        const u32 base = (u32)(mm * arb + (int64_t)blk * ab);
-        if (AF == kActPer32) {
-          a0[u][mm] = ld16(ra, base + 8);
-          a1[u][mm] = ld16(ra, base + 24);
-          da[u][mm] = ld4(ra, base);
-          sa[u][mm] = ld4(ra, base + 4);
-        } else {
-          ld_q80_codes(ra, base, a0[u][mm], a1[u][mm]);
-          da[u][mm] = ld2(ra, base);
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int blk = i0 + 8 * u + c;
-      if (blk >= nblk) continue;
-      const float d = h2f(dw[u]);
-#pragma unroll
-      for (int mm = 0; mm < M; ++mm) {
-        int P;
-        if (WT == kQ8_0) {
-          P = sdot16(w1[u], a1[u][mm], sdot16(w0[u], a0[u][mm], 0));
-        } else {
-          // Q4_0: low nibbles are values 0..15, high nibbles 16..31; code = nibble - 8.
-          const v4u lo = w0[u] & 0x0F0F0F0Fu, hi = (w0[u] >> 4) & 0x0F0F0F0Fu;
+      } else {
+        for (int bb = b0; bb < b1; bb += 8) {
+          const int blk = bb + (r >> 3);
+          float v[4];
+          load4f(rx, (u32)((blk * 32 + 4 * (r & 7)) * 4), v);
+          float d;
           int sum;
-          if (AF == kActPer32) {
-            sum = (int)sa[u][mm];
-          } else {
-            const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
-            sum = sdot16(ones, a1[u][mm], sdot16(ones, a0[u][mm], 0));
+          const u32 packed = per32_quant(v, d, sum);
+          if (blk < b1) {
+            uint8_t* o = lds_act + (mm * nblk + blk) * 40;
+            *reinterpret_cast<u32*>(o + 8 + 4 * (r & 7)) = packed;
+            if ((r & 7) == 0) {
+              *reinterpret_cast<float*>(o) = d;
+              *reinterpret_cast<int32_t*>(o + 4) = sum;
+            }
           }
-          P = sdot16(hi, a1[u][mm], sdot16(lo, a0[u][mm], 0)) - 8 * sum;
         }
-        const float dA = AF == kActPer32 ? as_f(da[u][mm]) : h2f(da[u][mm]);
-        // generic order: (dw * da) * (float)P (kernels_generic.cpp:220,235)
-        acc[mm] += (d * dA) * (float)P;
+      }
+    }
+    __syncthreads();
+  }
+  float acc[M];
+#pragma unroll
+  for (int mm = 0; mm < M; ++mm) acc[mm] = 0.0f;
+
+  // plane buffer resources of this row group (64 rows x nblk blocks)
+  const int u0 = plane_unit(WT, 0), u1 = plane_unit(WT, 1);
+  const auto r0 = rsrc(p0 + G * nblk * 64 * u0, (u32)(nblk * 64 * u0));
+  const auto r1 = rsrc(p1 + G * nblk * 64 * u1, (u32)(nblk * 64 * u1));
+  __amdgpu_buffer_rsrc_t r2 = r0, r3 = r0;
+  if (WT == kQ6_K) {
+    r2 = rsrc(p2 + G * nblk * 64 * 16, (u32)(nblk * 64 * 16));
+    r3 = rsrc(p3 + G * nblk * 64 * 2, (u32)(nblk * 64 * 2));
+  }
+
+  for (int bb = b0; bb < b1; bb += U) {
+    if (WT == kQ4_K) {
+      v4u q[U][8], hd[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int b = bb + u < b1 ? bb + u : nblk;  // past the slice: loads return 0, unused
+#pragma unroll
+        for (int c = 0; c < 8; ++c) q[u][c] = ld16(r0, (u32)(((b * 8 + c) * 64 + r) * 16));
+        hd[u] = ld16(r1, (u32)((b * 64 + r) * 16));
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int b = bb + u;
+        if (b >= b1) break;
+        // the 8 6-bit scales and mins as bytes (get_scale_min_k4, quant_formats.h:62-70)
+        const u32 s0 = hd[u].y, s1 = hd[u].z, s2 = hd[u].w;
+        const u32 sc_lo = s0 & 0x3F3F3F3Fu, mn_lo = s1 & 0x3F3F3F3Fu;
+        const u32 sc_hi = (s2 & 0x0F0F0F0Fu) | (((s0 >> 6) & 0x03030303u) << 4);
+        const u32 mn_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | (((s1 >> 6) & 0x03030303u) << 4);
+        const float d = h2f(hd[u].x), dmin = h2f(hd[u].x >> 16);
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+          if (kSb) {
+            const uint8_t* ab = acts + (int64_t)mm * arb + (int64_t)b * 292;
+            int S = 0, Mn = 0;
+#pragma unroll
+            for (int jp = 0; jp < 4; ++jp) {
+              const v4u lo0 = q[u][2 * jp] & 0x0F0F0F0Fu, lo1 = q[u][2 * jp + 1] & 0x0F0F0F0Fu;
+              const v4u hi0 = (q[u][2 * jp] >> 4) & 0x0F0F0F0Fu, hi1 = (q[u][2 * jp + 1] >> 4) & 0x0F0F0F0Fu;
+              const int pe = sdot16(lo1, uld16(ab, 4 + 64 * jp + 16), sdot16(lo0, uld16(ab, 4 + 64 * jp), 0));
+              const int po = sdot16(hi1, uld16(ab, 4 + 64 * jp + 48), sdot16(hi0, uld16(ab, 4 + 64 * jp + 32), 0));
+              const u32 scw = jp < 2 ? sc_lo : sc_hi, mnw = jp < 2 ? mn_lo : mn_hi;
+              const int e = 16 * (jp & 1);
+              S += (int)bfe(scw, e, 8) * pe + (int)bfe(scw, e + 8, 8) * po;
+              const u32 bsw = uld(ab, 260 + 8 * jp), bsw2 = uld(ab, 264 + 8 * jp);  // bsums 4jp .. 4jp+3
+              const int bse = (int)(int16_t)(bsw & 0xFFFFu) + (int)(int16_t)(bsw >> 16);
+              const int bso = (int)(int16_t)(bsw2 & 0xFFFFu) + (int)(int16_t)(bsw2 >> 16);
+              Mn += (int)bfe(mnw, e, 8) * bse + (int)bfe(mnw, e + 8, 8) * bso;
+            }
+            float t = d * (float)S;
+            t = fmaf(-dmin, (float)Mn, t);
+            rec[(mm * nblk + b) * 64 + r] = t;
+            if (r == 0) dav[mm * nblk + b] = as_f(uld(ab, 0));
+            if (dbg != nullptr && n < dbg_n) {
+              int32_t* o = dbg + (((int64_t)mm * dbg_n + n) * nblk + b) * 2;
+              o[0] = S;
+              o[1] = Mn;
+            }
+          } else {
+            // per-32 activations, sub-block order j = 0..7 (kernels_generic.cpp:267-275)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const int jp = j >> 1;
+              const u32 base = (u32)((int64_t)mm * arb + ((int64_t)b * 8 + j) * 40);
+              const v4u w0 = (j & 1) ? ((q[u][2 * jp] >> 4) & 0x0F0F0F0Fu) : (q[u][2 * jp] & 0x0F0F0F0Fu);
+              const v4u w1 = (j & 1) ? ((q[u][2 * jp + 1] >> 4) & 0x0F0F0F0Fu) : (q[u][2 * jp + 1] & 0x0F0F0F0Fu);
+              const int P = sdot16(w1, uld16(acts, base + 24), sdot16(w0, uld16(acts, base + 8), 0));
+              const u32 scw = j < 4 ? sc_lo : sc_hi, mnw = j < 4 ? mn_lo : mn_hi;
+              const int sc = (int)bfe(scw, 8 * (j & 3), 8), mn = (int)bfe(mnw, 8 * (j & 3), 8);
+              const float ad = as_f(uld(acts, base));
+              const int sum = (int)uld(acts, base + 4);
+              const float t = (d * (float)sc) * (float)P - (dmin * (float)mn) * (float)sum;
+              acc[mm] = acc[mm] + ad * t;
+            }
+          }
+        }
+      }
+    } else if (WT == kQ6_K) {
+      v4u L[U][8], H[U][4], SC[U];
+      u32 DW[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int b = bb + u < b1 ? bb + u : nblk;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) L[u][c] = ld16(r0, (u32)(((b * 8 + c) * 64 + r) * 16));
+#pragma unroll
+        for (int c = 0; c < 4; ++c) H[u][c] = ld16(r1, (u32)(((b * 4 + c) * 64 + r) * 16));
+        SC[u] = ld16(r2, (u32)((b * 64 + r) * 16));
+        DW[u] = ld2(r3, (u32)((b * 64 + r) * 2));
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int b = bb + u;
+        if (b >= b1) break;
+        const float d = h2f(DW[u]);
+        // ql chunk c: half p = c/4, values 128p + 16(c%4) + i (low nibbles) and + 64
+        // (high); their top bits are qh chunk 2p + c%2 at bit pairs s and s+2,
+        // s = (c%4)/2 (quant_formats.cpp:192-216). Units u_lo = 8p + c%4, u_hi = u_lo + 4.
+        v4u qlo[8], qhi[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const int p = c >> 2, cc = c & 3, s = cc >> 1;
+          const v4u hb = H[u][2 * p + (c & 1)];
+          qlo[c] = (L[u][c] & 0x0F0F0F0Fu) | (((hb >> (2 * s)) & 0x03030303u) << 4);
+          qhi[c] = ((L[u][c] >> 4) & 0x0F0F0F0Fu) | (((hb >> (2 * s + 4)) & 0x03030303u) << 4);
+        }
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+          if (kSb) {
+            const uint8_t* ab = acts + (int64_t)mm * arb + (int64_t)b * 292;
+            int S = 0;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+              const int ulo = 8 * (c >> 2) + (c & 3), uhi = ulo + 4;
+              const u32 bsl = uld(ab, 260 + 4 * (ulo >> 1)), bsh = uld(ab, 260 + 4 * (uhi >> 1));
+              const int sl = (int)(int16_t)(bsl >> (16 * (ulo & 1))), sh = (int)(int16_t)(bsh >> (16 * (uhi & 1)));
+              const int plo = sdot16(qlo[c], uld16(ab, 4 + 16 * ulo), 0) - 32 * sl;
+              const int phi = sdot16(qhi[c], uld16(ab, 4 + 16 * uhi), 0) - 32 * sh;
+              const u32 wl = ulo < 4 ? SC[u].x : ulo < 8 ? SC[u].y : ulo < 12 ? SC[u].z : SC[u].w;
+              const u32 wh = uhi < 4 ? SC[u].x : uhi < 8 ? SC[u].y : uhi < 12 ? SC[u].z : SC[u].w;
+              S += sbfe(wl, 8 * (ulo & 3), 8) * plo + sbfe(wh, 8 * (uhi & 3), 8) * phi;
+            }
+            rec[(mm * nblk + b) * 64 + r] = d * (float)S;
+            if (r == 0) dav[mm * nblk + b] = as_f(uld(ab, 0));
+            if (dbg != nullptr && n < dbg_n) {
+              int32_t* o = dbg + (((int64_t)mm * dbg_n + n) * nblk + b) * 2;
+              o[0] = S;
+              o[1] = 0;
+            }
+          } else {
+            // per-32 activations, units of 16 in order (kernels_generic.cpp:299-306)
+            const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
+#pragma unroll
+            for (int uu = 0; uu < 16; ++uu) {
+              // unit uu = 8p + cc (+4 for high nibbles): chunk c = 4p + (uu % 4)
+              const int p = uu >> 3, cc = uu & 3, c = 4 * p + cc;
+              const v4u qv = (uu & 4) ? qhi[c] : qlo[c];
+              const u32 base = (u32)((int64_t)mm * arb + ((int64_t)b * 8 + uu / 2) * 40);
+              const v4u av = uld16(acts, base + 8 + 16 * (uu & 1));
+              const int P = sdot16(qv, av, 0) - 32 * sdot16(ones, av, 0);
+              const u32 sw = uu < 4 ? SC[u].x : uu < 8 ? SC[u].y : uu < 12 ? SC[u].z : SC[u].w;
+              const float ad = as_f(uld(acts, base));
+              acc[mm] = acc[mm] + ((ad * d) * (float)sbfe(sw, 8 * (uu & 3), 8)) * (float)P;
+            }
+          }
+        }
+      }
+    } else {  // Q8_0 / Q4_0: blocks of 32
+      constexpr int kChunks = WT == kQ8_0 ? 2 : 1;
+      constexpr int kAb = AF == kActPer32 ? 40 : 34;
+      v4u q[U][kChunks];
+      u32 DW[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int b = bb + u < b1 ? bb + u : nblk;
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) q[u][c] = ld16(r0, (u32)(((b * kChunks + c) * 64 + r) * 16));
+        DW[u] = ld2(r1, (u32)((b * 64 + r) * 2));
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int b = bb + u;
+        if (b >= b1) break;
+        const float dw = h2f(DW[u]);
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+          const u32 base = (u32)((int64_t)mm * arb + (int64_t)b * kAb);
+          v4u x0, x1;
+          act_codes32<AF>(acts, base, x0, x1);
+          int P;
+          if (WT == kQ8_0) {
+            P = sdot16(q[u][kChunks - 1], x1, sdot16(q[u][0], x0, 0));
+          } else {
+            // low nibbles are values 0..15, high nibbles 16..31; code = nibble - 8
+            int sum;
+            if (AF == kActPer32) {
+              sum = (int)uld(acts, base + 4);
+            } else {
+              const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
+              sum = sdot16(ones, x1, sdot16(ones, x0, 0));
+            }
+            P = sdot16((q[u][0] >> 4) & 0x0F0F0F0Fu, x1, sdot16(q[u][0] & 0x0F0F0F0Fu, x0, 0)) - 8 * sum;
+          }
+          const float da = AF == kActPer32 ? as_f(uld(acts, base)) : h2f(uld(acts, base & ~3u) >> (8 * (base & 3u)));
+          // generic order: acc += (dw * da) * (float)P (kernels_generic.cpp:220,235)
+          acc[mm] = acc[mm] + (dw * da) * (float)P;
+        }
       }
     }
   }
+
+  if (!kSb) {
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) rec[(wave * M + mm) * 64 + r] = acc[mm];
+  }
+  __syncthreads();
+  if (wave != 0) return;
 #pragma unroll
   for (int mm = 0; mm < M; ++mm) {
-    const float v = red8f(acc[mm]);
-    if (c == 0 && n >= n0 && n < n1) y[mm * ys + n] = bias ? v + bias[n] : v;
+    float v = 0.0f;
+    if (kSb) {
+      const float* tp = rec + mm * nblk * 64 + r;
+      const float* dp = dav + mm * nblk;
+      int b = 0;
+      for (; b + 4 <= nblk; b += 4) {
+        const float t0 = tp[b * 64], t1 = tp[(b + 1) * 64], t2 = tp[(b + 2) * 64], t3 = tp[(b + 3) * 64];
+        const float d0 = dp[b], d1 = dp[b + 1], d2 = dp[b + 2], d3 = dp[b + 3];
+        v = fmaf(d0, t0, v);
+        v = fmaf(d1, t1, v);
+        v = fmaf(d2, t2, v);
+        v = fmaf(d3, t3, v);
+      }
+      for (; b < nblk; ++b) v = fmaf(dp[b], tp[b * 64], v);
+    } else {
+#pragma unroll
+      for (int w = 0; w < W; ++w) v = v + rec[(w * M + mm) * 64 + r];
+    }
+    if (n >= n0 && n < n1) y[mm * ys + n] = bias ? v + bias[n] : v;
   }
 }
 
@@ -461,34 +521,35 @@ __global__ __launch_bounds__(256) void k_units(int t, int af, const uint8_t* p0,
   if (idx >= m * n * nu) return;
   const int64_t u = idx % nu, row = (idx / nu) % n, mm = idx / (nu * n);
   const uint8_t* a = acts + mm * arb;
-  const int64_t G = row / kRowGroup, r = row % kRowGroup;
   int s = 0;
   if (t == kQ8_0 || t == kQ4_0) {
-    const int unit = t == kQ8_0 ? 32 : 16;
-    const uint8_t* q = p0 + ((G * nblk + u) * kRowGroup + r) * unit;
     for (int i = 0; i < 32; ++i) {
-      const int w = t == kQ8_0 ? (int)(int8_t)q[i] : (int)((i < 16 ? (q[i] & 15) : (q[i - 16] >> 4))) - 8;
+      int w;
+      if (t == kQ8_0) {
+        w = (int)(int8_t)p0[plane_offset(t, 0, row, u, nblk, i)];
+      } else {
+        const uint8_t q = p0[plane_offset(t, 0, row, u, nblk, i % 16)];
+        w = (int)(i < 16 ? (q & 15) : (q >> 4)) - 8;
+      }
       s += w * act_code(af, a, u * 32 + i);
     }
   } else if (t == kQ4_K) {
     const int64_t b = u / 8;
     const int j = (int)(u % 8);
-    const uint8_t* qs = p0 + ((G * nblk + b) * kRowGroup + r) * 128 + 32 * (j / 2);
     for (int i = 0; i < 32; ++i) {
-      const int w = (j & 1) ? (qs[i] >> 4) : (qs[i] & 15);
+      const uint8_t q = p0[plane_offset(t, 0, row, b, nblk, 32 * (j / 2) + i)];
+      const int w = (j & 1) ? (q >> 4) : (q & 15);
       s += w * act_code(af, a, b * 256 + 32 * j + i);
     }
   } else {  // Q6_K: unit = 16 values 16*uu .. of super-block b
     const int64_t b = u / 16;
     const int uu = (int)(u % 16);
-    const uint8_t* ql = p0 + ((G * nblk + b) * kRowGroup + r) * 128;
-    const uint8_t* qh = p1 + ((G * nblk + b) * kRowGroup + r) * 64;
     for (int i = 0; i < 16; ++i) {
-      const int v = 16 * uu + i;          // value index in the super-block
+      const int v = 16 * uu + i;  // value index in the super-block
       const int half = v / 128, w = v % 128, quarter = w / 32, l = w % 32;
-      const int lb = ql[64 * half + l + (quarter & 1) * 32];
+      const int lb = p0[plane_offset(t, 0, row, b, nblk, 64 * half + l + (quarter & 1) * 32)];
       const int nib = quarter < 2 ? (lb & 15) : (lb >> 4);
-      const int hb = (qh[32 * half + l] >> (2 * quarter)) & 3;
+      const int hb = (p1[plane_offset(t, 1, row, b, nblk, 32 * half + l)] >> (2 * quarter)) & 3;
       s += ((nib | (hb << 4)) - 32) * act_code(af, a, b * 256 + v);
     }
   }
@@ -534,75 +595,86 @@ hipError_t launch_unpack(int t, uint8_t* dst, int64_t row_stride, int64_t n, int
   return hipGetLastError();
 }
 
-template <int AF, int M>
-static void gemv_q4k_m(const WeightDev& w, const uint8_t* acts, int64_t arb, int64_t n0, int64_t n1, float* y,
-                       int64_t ys, const float* bias, int32_t* dbg, hipStream_t s) {
-  constexpr int U = M == 1 ? 8 : (M == 2 ? 4 : 2);
-  const int64_t g0 = n0 / kRowGroup, g1 = (n1 + kRowGroup - 1) / kRowGroup;
-  hipLaunchKernelGGL((k_gemv_q4k<AF, M, U>), dim3((unsigned)(g1 - g0)), dim3(64), 0, s, w.plane[0], w.plane[1],
-                     (int)w.nblk, g0, n0, n1, acts, arb, y, ys, bias, dbg, w.n);
-}
+constexpr int kGemvWaves = 8;
 
-template <int AF, int M>
-static void gemv_q6k_m(const WeightDev& w, const uint8_t* acts, int64_t arb, int64_t n0, int64_t n1, float* y,
-                       int64_t ys, const float* bias, int32_t* dbg, hipStream_t s) {
-  constexpr int U = M == 1 ? 4 : 2;
+template <int WT, int AF, int M, bool kFuse>
+static hipError_t gemv_launch(const WeightDev& w, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
+                              int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
+                              hipStream_t s) {
+  constexpr int U = (WT == kQ8_0 || WT == kQ4_0) ? 8 : 2;
   const int64_t g0 = n0 / kRowGroup, g1 = (n1 + kRowGroup - 1) / kRowGroup;
-  hipLaunchKernelGGL((k_gemv_q6k<AF, M, U>), dim3((unsigned)(g1 - g0)), dim3(64), 0, s, w.plane[0], w.plane[1],
-                     w.plane[2], w.plane[3], (int)w.nblk, g0, n0, n1, acts, arb, y, ys, bias, dbg, w.n);
-}
-
-template <int WT, int AF, int M>
-static void gemv_b32_m(const WeightDev& w, const uint8_t* acts, int64_t arb, int64_t n0, int64_t n1, float* y,
-                       int64_t ys, const float* bias, hipStream_t s) {
-  constexpr int U = M == 1 ? 4 : 2;
-  const int64_t g0 = n0 / kRowGroup, g1 = (n1 + kRowGroup - 1) / kRowGroup;
-  hipLaunchKernelGGL((k_gemv_b32<WT, AF, M, U>), dim3((unsigned)(g1 - g0)), dim3(64), 0, s, w.plane[0], w.plane[1],
-                     (int)w.nblk, g0, n0, n1, acts, arb, y, ys, bias);
-}
-
-// M rows (1..4) of one pass.
-template <int M>
-static hipError_t gemv_pass(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t n0, int64_t n1,
-                            float* y, int64_t ys, const float* bias, int32_t* dbg, hipStream_t s) {
-  switch (w.dtype) {
-    case kQ4_K:
-      if (af == kActQ8_K) gemv_q4k_m<kActQ8_K, M>(w, acts, arb, n0, n1, y, ys, bias, dbg, s);
-      else gemv_q4k_m<kActPer32, M>(w, acts, arb, n0, n1, y, ys, bias, dbg, s);
-      break;
-    case kQ6_K:
-      if (af == kActQ8_K) gemv_q6k_m<kActQ8_K, M>(w, acts, arb, n0, n1, y, ys, bias, dbg, s);
-      else gemv_q6k_m<kActPer32, M>(w, acts, arb, n0, n1, y, ys, bias, dbg, s);
-      break;
-    case kQ8_0:
-      if (af == kActPer32) gemv_b32_m<kQ8_0, kActPer32, M>(w, acts, arb, n0, n1, y, ys, bias, s);
-      else gemv_b32_m<kQ8_0, kActQ8_0, M>(w, acts, arb, n0, n1, y, ys, bias, s);
-      break;
-    default:
-      if (af == kActPer32) gemv_b32_m<kQ4_0, kActPer32, M>(w, acts, arb, n0, n1, y, ys, bias, s);
-      else gemv_b32_m<kQ4_0, kActQ8_0, M>(w, acts, arb, n0, n1, y, ys, bias, s);
-      break;
+  size_t lds = AF == kActQ8_K ? (size_t)M * w.nblk * 65 * sizeof(float) : (size_t)kGemvWaves * M * 64 * sizeof(float);
+  if (kFuse) lds += (size_t)M * w.nblk * (AF == kActQ8_K ? 292 : 40);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  const void* fn = reinterpret_cast<const void*>(&k_gemv<WT, AF, M, kGemvWaves, U, kFuse>);
+  if (lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
   }
+  hipLaunchKernelGGL((k_gemv<WT, AF, M, kGemvWaves, U, kFuse>), dim3((unsigned)(g1 - g0)), dim3(64 * kGemvWaves), lds,
+                     s, w.plane[0], w.plane[1], w.plane[2], w.plane[3], (int)w.nblk, g0, n0, n1, acts, arb, x, xs, y,
+                     ys, bias, dbg, w.n);
   return hipGetLastError();
 }
 
-hipError_t launch_gemv(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
-                       float* y, int64_t ys, const float* bias, int32_t* dbg, hipStream_t s) {
+// M rows (1..4) of one pass; x != nullptr: fused quantization of fp32 rows.
+template <int M>
+static hipError_t gemv_pass(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
+                            int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
+                            hipStream_t s) {
+  if (x != nullptr) {
+    switch (w.dtype) {
+      case kQ4_K: return gemv_launch<kQ4_K, kActQ8_K, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, s);
+      case kQ6_K: return gemv_launch<kQ6_K, kActQ8_K, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, s);
+      case kQ8_0: return gemv_launch<kQ8_0, kActPer32, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, s);
+      default: return gemv_launch<kQ4_0, kActPer32, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, s);
+    }
+  }
+  switch (w.dtype) {
+    case kQ4_K:
+      return af == kActQ8_K ? gemv_launch<kQ4_K, kActQ8_K, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
+                            : gemv_launch<kQ4_K, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+    case kQ6_K:
+      return af == kActQ8_K ? gemv_launch<kQ6_K, kActQ8_K, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
+                            : gemv_launch<kQ6_K, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+    case kQ8_0:
+      return af == kActPer32 ? gemv_launch<kQ8_0, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
+                             : gemv_launch<kQ8_0, kActQ8_0, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+    default:
+      return af == kActPer32 ? gemv_launch<kQ4_0, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
+                             : gemv_launch<kQ4_0, kActQ8_0, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+  }
+}
+
+static hipError_t gemv_rows(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
+                            int64_t m, int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
+                            hipStream_t s) {
   for (int64_t r0 = 0; r0 < m; r0 += 4) {
     const int rows = (int)(m - r0 < 4 ? m - r0 : 4);
-    const uint8_t* a = acts + r0 * arb;
+    const uint8_t* a = acts ? acts + r0 * arb : nullptr;
+    const float* xx = x ? x + r0 * xs : nullptr;
     float* yy = y + r0 * ys;
     int32_t* dd = dbg ? dbg + r0 * w.n * w.nblk * 2 : nullptr;
     hipError_t e;
     switch (rows) {
-      case 1: e = gemv_pass<1>(w, af, a, arb, n0, n1, yy, ys, bias, dd, s); break;
-      case 2: e = gemv_pass<2>(w, af, a, arb, n0, n1, yy, ys, bias, dd, s); break;
-      case 3: e = gemv_pass<3>(w, af, a, arb, n0, n1, yy, ys, bias, dd, s); break;
-      default: e = gemv_pass<4>(w, af, a, arb, n0, n1, yy, ys, bias, dd, s); break;
+      case 1: e = gemv_pass<1>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
+      case 2: e = gemv_pass<2>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
+      case 3: e = gemv_pass<3>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
+      default: e = gemv_pass<4>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
     }
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+hipError_t launch_gemv(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
+                       float* y, int64_t ys, const float* bias, int32_t* dbg, hipStream_t s) {
+  return gemv_rows(w, af, acts, arb, nullptr, 0, m, n0, n1, y, ys, bias, dbg, s);
+}
+
+hipError_t launch_gemv_fused(const WeightDev& w, const float* x, int64_t xs, int64_t m, float* y, int64_t ys,
+                             const float* bias, hipStream_t s) {
+  return gemv_rows(w, -1, nullptr, 0, x, xs, m, 0, w.n, y, ys, bias, nullptr, s);
 }
 
 hipError_t launch_units(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int32_t* units,

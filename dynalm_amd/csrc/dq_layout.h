@@ -7,21 +7,23 @@
 //   Q4_K  {fp16 d, dmin; u8 scales[12]; u8 qs[128]}           144 B / 256
 //   Q6_K  {u8 ql[128]; u8 qh[64]; i8 scales[16]; fp16 d}      210 B / 256
 //
-// Device layout ("x8"): rows are taken in groups of 8 (n padded up to a multiple
-// of 8 with zero rows) and each block is split into planes; inside a plane the
-// 8 rows of a group are adjacent for every block:
-//   plane[p][((G * nblk + b) * 8 + r) * unit_p + byte]      G = n / 8, r = n % 8
-// so one wave, 8 lanes per row, reads a contiguous 1 KB of codes per load
-// instruction (Q4_K: the 128 B of qs of 8 rows; Q6_K: 128 B of ql; Q8_0: 4
-// blocks x 32 B ... per row), and the scale planes of 8 rows are 128 B or less.
-// Planes per type:
-//   Q4_K  0: qs 128 B        1: header {d, dmin, scales[12]} 16 B
-//   Q6_K  0: ql 128 B        1: qh 64 B    2: scales 16 B    3: d 2 B
-//   Q8_0  0: qs 32 B         1: d 2 B
-//   Q4_0  0: qs 16 B         1: d 2 B
-// The bytes of every plane are the block's bytes unchanged (a permutation of
-// the GGUF row bytes), so the device copy holds exactly the GGUF byte count
-// plus the zero padding rows.
+// Device layout: rows are taken in groups of 64 (n padded up to a multiple of 64
+// with zero rows) and each block is split into planes; inside a plane, for every
+// block b and 16-byte chunk c of a row's unit, the chunks of the 64 rows of a
+// group are adjacent:
+//   unit >= 16:  plane[p][(((G * nblk + b) * (unit / 16) + c) * 64 + r) * 16 + byte]
+//   unit <  16:  plane[p][((G * nblk + b) * 64 + r) * unit + byte]
+// with G = n / 64, r = n % 64. One wave, lane r <-> row r, then reads 1 KB
+// contiguous per 16-byte-per-lane load instruction, and all 64 lanes use the same
+// activation values at the same time (so those are wave-uniform scalar loads).
+// Planes per type (unit bytes per row and block):
+//   Q4_K  0: qs 128          1: header {d, dmin, scales[12]} 16
+//   Q6_K  0: ql 128          1: qh 64    2: scales 16    3: d 2
+//   Q8_0  0: qs 32           1: d 2
+//   Q4_0  0: qs 16           1: d 2
+// The bytes of every plane are the block's bytes unchanged (a permutation of the
+// GGUF row bytes), so the device copy holds exactly the GGUF byte count plus the
+// zero padding rows.
 #pragma once
 
 #include <stdint.h>
@@ -37,7 +39,7 @@ namespace dq {
 enum : int { kQ4_0 = 6, kQ8_0 = 10, kQ4_K = 14, kQ6_K = 16 };
 enum : int { kActPer32 = 0, kActQ8_0 = 1, kActQ8_K = 2 };
 
-constexpr int kRowGroup = 8;
+constexpr int kRowGroup = 64;
 constexpr int kMaxPlanes = 4;
 
 DQ_HD int block_elems(int t) { return (t == kQ4_K || t == kQ6_K) ? 256 : (t == kQ4_0 || t == kQ8_0) ? 32 : -1; }
@@ -71,6 +73,14 @@ DQ_HD void plane_of_byte(int t, int i, int* p, int* off) {
       if (i < 2) { *p = 1; *off = i; } else { *p = 0; *off = i - 2; }
       break;
   }
+}
+
+// Offset in plane p of byte `off` of the unit of row n, block b.
+DQ_HD int64_t plane_offset(int t, int p, int64_t n, int64_t b, int64_t nblk, int off) {
+  const int64_t G = n / kRowGroup, r = n % kRowGroup;
+  const int unit = plane_unit(t, p);
+  if (unit >= 16) return (((G * nblk + b) * (unit / 16) + off / 16) * kRowGroup + r) * 16 + off % 16;
+  return ((G * nblk + b) * kRowGroup + r) * unit + off;
 }
 
 DQ_HD int act_block_elems(int f) { return f == kActQ8_K ? 256 : (f == kActPer32 || f == kActQ8_0) ? 32 : -1; }

@@ -234,6 +234,23 @@ def test_matmul_end_to_end(cuda, t, m):
     assert ok, f"worst error ratio {worst:.3g}"
 
 
+@pytest.mark.parametrize("t", [O.Q8_0, O.Q4_0, O.Q4_K, O.Q6_K], ids=lambda t: O.TYPE_NAMES[t])
+@pytest.mark.parametrize("m", [1, 3, 6])
+def test_fused_decode_equals_quantize_then_gemv(cuda, t, m):
+    """dq_matmul's decode path quantizes inside the GEMV: bit-identical to the
+    standalone quantizer followed by dq_gemv on the same rows."""
+    from dynalm_amd import torch_ops as T
+
+    k, n = 2048, 130
+    w_rows = gguf_weights(t, n, k, 70 + t)
+    x = dev(activations(m, k, 71))
+    w = dq.Weight.upload(t, w_rows, k)
+    fmt = dq.act_format_for(t)
+    fused = host(T.matmul(w, x))
+    two = host(T.gemv(w, fmt, T.quantize(fmt, x)))
+    assert np.array_equal(fused.view(np.uint32), two.view(np.uint32))
+
+
 # ------------------------------------------------------- BASELINE full sizes
 
 
