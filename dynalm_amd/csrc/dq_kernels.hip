@@ -215,6 +215,411 @@ DQ_DEV void act_codes32(const uint8_t* __restrict__ a, u32 base, v4u& x0, v4u& x
   }
 }
 
+// ---- per-format weight chunks: the vector loads of U consecutive blocks of the
+// lane's row (blocks past the wave's slice read as zeros and are not used).
+struct Rsrcs {
+  __amdgpu_buffer_rsrc_t r0, r1, r2, r3;
+};
+
+template <int WT, int U>
+struct Chunk;
+
+template <int U>
+struct Chunk<kQ4_K, U> {
+  v4u q[U][8], hd[U];
+  DQ_DEV void load(const Rsrcs& rs, int bb, int b1, int nblk, int r) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int b = bb + u < b1 ? bb + u : nblk;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) q[u][c] = ld16(rs.r0, (u32)(((b * 8 + c) * 64 + r) * 16));
+      hd[u] = ld16(rs.r1, (u32)((b * 64 + r) * 16));
+    }
+  }
+};
+
+template <int U>
+struct Chunk<kQ6_K, U> {
+  v4u L[U][8], H[U][4], SC[U];
+  u32 DW[U];
+  DQ_DEV void load(const Rsrcs& rs, int bb, int b1, int nblk, int r) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int b = bb + u < b1 ? bb + u : nblk;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) L[u][c] = ld16(rs.r0, (u32)(((b * 8 + c) * 64 + r) * 16));
+#pragma unroll
+      for (int c = 0; c < 4; ++c) H[u][c] = ld16(rs.r1, (u32)(((b * 4 + c) * 64 + r) * 16));
+      SC[u] = ld16(rs.r2, (u32)((b * 64 + r) * 16));
+      DW[u] = ld2(rs.r3, (u32)((b * 64 + r) * 2));
+    }
+  }
+};
+
+template <int WT, int U>
+struct Chunk32 {  // Q8_0 (2 chunks of 16 B per block) and Q4_0 (1)
+  static constexpr int kC = WT == kQ8_0 ? 2 : 1;
+  v4u q[U][kC];
+  u32 DW[U];
+  DQ_DEV void load(const Rsrcs& rs, int bb, int b1, int nblk, int r) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int b = bb + u < b1 ? bb + u : nblk;
+#pragma unroll
+      for (int c = 0; c < kC; ++c) q[u][c] = ld16(rs.r0, (u32)(((b * kC + c) * 64 + r) * 16));
+      DW[u] = ld2(rs.r1, (u32)((b * 64 + r) * 2));
+    }
+  }
+};
+template <int U>
+struct Chunk<kQ8_0, U> : Chunk32<kQ8_0, U> {};
+template <int U>
+struct Chunk<kQ4_0, U> : Chunk32<kQ4_0, U> {};
+
+// Activations staged in LDS (both the plain and the fused path), 16-byte aligned
+// so that compute reads them with broadcast ds_read_b128 at wave-uniform addresses:
+//   Q8_K super-block (320 B):  d float @0, codes int8[256] @16, bsums int16[16] @272
+//   32-value block   (48 B):   d float @0, code sum int32 @4, codes int8[32] @16
+// (per-32 ActBlockQ8 and GGUF Q8_0 activations both stage as the latter; the GGUF
+// fp16 d converts exactly to float).
+constexpr int kStageQ8K = 320;
+constexpr int kStage32 = 48;
+
+DQ_DEV v4u lds16(const uint8_t* p) { return *reinterpret_cast<const v4u*>(p); }
+DQ_DEV u32 lds4(const uint8_t* p) { return *reinterpret_cast<const u32*>(p); }
+
+// Per-lane state the compute steps write: Q8_K t-terms and da go to LDS (rec,
+// dav); per-32 sums accumulate in acc.
+template <int M>
+struct Out {
+  float* rec;
+  float* dav;
+  float acc[M];
+  int32_t* dbg;
+  int64_t dbg_n, n;
+  int nblk, r;
+};
+
+template <int AF, int M, int U>
+DQ_DEV void compute(const Chunk<kQ4_K, U>& ch, int bb, const uint8_t* st, Out<M>& o) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int b = bb + u;
+    // the 8 6-bit scales and mins as bytes (get_scale_min_k4, quant_formats.h:62-70)
+    const u32 s0 = ch.hd[u].y, s1 = ch.hd[u].z, s2 = ch.hd[u].w;
+    const u32 sc_lo = s0 & 0x3F3F3F3Fu, mn_lo = s1 & 0x3F3F3F3Fu;
+    const u32 sc_hi = (s2 & 0x0F0F0F0Fu) | (((s0 >> 6) & 0x03030303u) << 4);
+    const u32 mn_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | (((s1 >> 6) & 0x03030303u) << 4);
+    const float d = h2f(ch.hd[u].x), dmin = h2f(ch.hd[u].x >> 16);
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) {
+      if (AF == kActQ8_K) {
+        const uint8_t* ab = st + (mm * o.nblk + b) * kStageQ8K;
+        int S = 0, Mn = 0;
+#pragma unroll
+        for (int jp = 0; jp < 4; ++jp) {
+          const v4u c0 = ch.q[u][2 * jp], c1 = ch.q[u][2 * jp + 1];
+          const uint8_t* cp = ab + 16 + 64 * jp;
+          const int pe = sdot16(c1 & 0x0F0F0F0Fu, lds16(cp + 16), sdot16(c0 & 0x0F0F0F0Fu, lds16(cp), 0));
+          const int po = sdot16((c1 >> 4) & 0x0F0F0F0Fu, lds16(cp + 48), sdot16((c0 >> 4) & 0x0F0F0F0Fu, lds16(cp + 32), 0));
+          const u32 scw = jp < 2 ? sc_lo : sc_hi, mnw = jp < 2 ? mn_lo : mn_hi;
+          const int e = 16 * (jp & 1);
+          S += (int)bfe(scw, e, 8) * pe + (int)bfe(scw, e + 8, 8) * po;
+          const u32 bsw = lds4(ab + 272 + 8 * jp), bsw2 = lds4(ab + 276 + 8 * jp);  // bsums 4jp .. 4jp+3
+          const int bse = (int)(int16_t)(bsw & 0xFFFFu) + (int)(int16_t)(bsw >> 16);
+          const int bso = (int)(int16_t)(bsw2 & 0xFFFFu) + (int)(int16_t)(bsw2 >> 16);
+          Mn += (int)bfe(mnw, e, 8) * bse + (int)bfe(mnw, e + 8, 8) * bso;
+        }
+        float t = d * (float)S;
+        t = fmaf(-dmin, (float)Mn, t);
+        o.rec[(mm * o.nblk + b) * 64 + o.r] = t;
+        if (o.r == 0) o.dav[mm * o.nblk + b] = as_f(lds4(ab));
+        if (o.dbg != nullptr && o.n < o.dbg_n) {
+          int32_t* p = o.dbg + (((int64_t)mm * o.dbg_n + o.n) * o.nblk + b) * 2;
+          p[0] = S;
+          p[1] = Mn;
+        }
+      } else {
+        // per-32 activations, sub-block order j = 0..7 (kernels_generic.cpp:267-275)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int jp = j >> 1;
+          const uint8_t* ab = st + (mm * o.nblk * 8 + b * 8 + j) * kStage32;
+          const v4u c0 = ch.q[u][2 * jp], c1 = ch.q[u][2 * jp + 1];
+          const v4u w0 = (j & 1) ? ((c0 >> 4) & 0x0F0F0F0Fu) : (c0 & 0x0F0F0F0Fu);
+          const v4u w1 = (j & 1) ? ((c1 >> 4) & 0x0F0F0F0Fu) : (c1 & 0x0F0F0F0Fu);
+          const int P = sdot16(w1, lds16(ab + 32), sdot16(w0, lds16(ab + 16), 0));
+          const u32 scw = j < 4 ? sc_lo : sc_hi, mnw = j < 4 ? mn_lo : mn_hi;
+          const int sc = (int)bfe(scw, 8 * (j & 3), 8), mn = (int)bfe(mnw, 8 * (j & 3), 8);
+          const float ad = as_f(lds4(ab));
+          const int sum = (int)lds4(ab + 4);
+          const float t = (d * (float)sc) * (float)P - (dmin * (float)mn) * (float)sum;
+          o.acc[mm] = o.acc[mm] + ad * t;
+        }
+      }
+    }
+  }
+}
+
+template <int AF, int M, int U>
+DQ_DEV void compute(const Chunk<kQ6_K, U>& ch, int bb, const uint8_t* st, Out<M>& o) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int b = bb + u;
+    const float d = h2f(ch.DW[u]);
+    // ql chunk c: half p = c/4, values 128p + 16(c%4) + i (low nibbles) and + 64
+    // (high); their top bits are qh chunk 2p + c%2 at bit pairs s and s+2,
+    // s = (c%4)/2 (quant_formats.cpp:192-216). Units u_lo = 8p + c%4, u_hi = u_lo + 4.
+    v4u qlo[8], qhi[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int p = c >> 2, cc = c & 3, s = cc >> 1;
+      const v4u hb = ch.H[u][2 * p + (c & 1)];
+      qlo[c] = (ch.L[u][c] & 0x0F0F0F0Fu) | (((hb >> (2 * s)) & 0x03030303u) << 4);
+      qhi[c] = ((ch.L[u][c] >> 4) & 0x0F0F0F0Fu) | (((hb >> (2 * s + 4)) & 0x03030303u) << 4);
+    }
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) {
+      if (AF == kActQ8_K) {
+        const uint8_t* ab = st + (mm * o.nblk + b) * kStageQ8K;
+        int S = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const int ulo = 8 * (c >> 2) + (c & 3), uhi = ulo + 4;
+          const u32 bsl = lds4(ab + 272 + 4 * (ulo >> 1)), bsh = lds4(ab + 272 + 4 * (uhi >> 1));
+          const int sl = (int)(int16_t)(bsl >> (16 * (ulo & 1))), sh = (int)(int16_t)(bsh >> (16 * (uhi & 1)));
+          const int plo = sdot16(qlo[c], lds16(ab + 16 + 16 * ulo), 0) - 32 * sl;
+          const int phi = sdot16(qhi[c], lds16(ab + 16 + 16 * uhi), 0) - 32 * sh;
+          const u32 wl = ulo < 4 ? ch.SC[u].x : ulo < 8 ? ch.SC[u].y : ulo < 12 ? ch.SC[u].z : ch.SC[u].w;
+          const u32 wh = uhi < 4 ? ch.SC[u].x : uhi < 8 ? ch.SC[u].y : uhi < 12 ? ch.SC[u].z : ch.SC[u].w;
+          S += sbfe(wl, 8 * (ulo & 3), 8) * plo + sbfe(wh, 8 * (uhi & 3), 8) * phi;
+        }
+        o.rec[(mm * o.nblk + b) * 64 + o.r] = d * (float)S;
+        if (o.r == 0) o.dav[mm * o.nblk + b] = as_f(lds4(ab));
+        if (o.dbg != nullptr && o.n < o.dbg_n) {
+          int32_t* p = o.dbg + (((int64_t)mm * o.dbg_n + o.n) * o.nblk + b) * 2;
+          p[0] = S;
+          p[1] = 0;
+        }
+      } else {
+        // per-32 activations, units of 16 in order (kernels_generic.cpp:299-306)
+        const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
+#pragma unroll
+        for (int uu = 0; uu < 16; ++uu) {
+          const int p = uu >> 3, cc = uu & 3, c = 4 * p + cc;  // unit uu lives in chunk c
+          const v4u qv = (uu & 4) ? qhi[c] : qlo[c];
+          const uint8_t* ab = st + (mm * o.nblk * 8 + b * 8 + uu / 2) * kStage32;
+          const v4u av = lds16(ab + 16 + 16 * (uu & 1));
+          const int P = sdot16(qv, av, 0) - 32 * sdot16(ones, av, 0);
+          const u32 sw = uu < 4 ? ch.SC[u].x : uu < 8 ? ch.SC[u].y : uu < 12 ? ch.SC[u].z : ch.SC[u].w;
+          o.acc[mm] = o.acc[mm] + ((as_f(lds4(ab)) * d) * (float)sbfe(sw, 8 * (uu & 3), 8)) * (float)P;
+        }
+      }
+    }
+  }
+}
+
+template <int WT, int AF, int M, int U>
+DQ_DEV void compute32(const Chunk32<WT, U>& ch, int bb, const uint8_t* st, Out<M>& o) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int b = bb + u;
+    const float dw = h2f(ch.DW[u]);
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) {
+      const uint8_t* ab = st + (mm * o.nblk + b) * kStage32;
+      const v4u x0 = lds16(ab + 16), x1 = lds16(ab + 32);
+      int P;
+      if (WT == kQ8_0) {
+        P = sdot16(ch.q[u][Chunk32<WT, U>::kC - 1], x1, sdot16(ch.q[u][0], x0, 0));
+      } else {
+        // low nibbles are values 0..15, high nibbles 16..31; code = nibble - 8
+        P = sdot16((ch.q[u][0] >> 4) & 0x0F0F0F0Fu, x1, sdot16(ch.q[u][0] & 0x0F0F0F0Fu, x0, 0)) -
+            8 * (int)lds4(ab + 4);
+      }
+      // generic order: acc += (dw * da) * (float)P (kernels_generic.cpp:220,235)
+      o.acc[mm] = o.acc[mm] + (dw * as_f(lds4(ab))) * (float)P;
+    }
+  }
+}
+template <int AF, int M, int U>
+DQ_DEV void compute(const Chunk<kQ8_0, U>& ch, int bb, const uint8_t* st, Out<M>& o) {
+  compute32<kQ8_0, AF, M, U>(ch, bb, st, o);
+}
+template <int AF, int M, int U>
+DQ_DEV void compute(const Chunk<kQ4_0, U>& ch, int bb, const uint8_t* st, Out<M>& o) {
+  compute32<kQ4_0, AF, M, U>(ch, bb, st, o);
+}
+
+// ---- staging a wave's slice of activations into LDS. Loads are issued first
+// (issue), the weight loads after them, then commit() waits for the activation
+// loads only (vector loads complete in order) and writes the staged layout.
+
+// Copies this wave's slice (weight blocks [b0, b1); bpu 32-value activation blocks
+// per weight block for per-32 formats) of M pre-quantized rows into the staged
+// LDS layout.
+template <int AF, int M>
+DQ_DEV void stage_acts(const uint8_t* __restrict__ acts, int64_t arb, int nblk, int b0, int b1, int bpu, int r,
+                       uint8_t* st) {
+  const auto ra = rsrc(acts, (u32)(M * arb));
+  for (int mm = 0; mm < M; ++mm) {
+    if (AF == kActQ8_K) {
+      for (int b = b0; b < b1; ++b) {
+        const u32 base = (u32)(mm * arb + (int64_t)b * 292);
+        uint8_t* o = st + (mm * nblk + b) * kStageQ8K;
+        for (int i = r; i < 73; i += 64) {
+          const u32 v = ld4(ra, base + 4 * i);
+          const int at = i == 0 ? 0 : (i <= 64 ? 16 + 4 * (i - 1) : 272 + 4 * (i - 65));
+          *reinterpret_cast<u32*>(o + at) = v;
+        }
+      }
+    } else {
+      for (int blk = b0 * bpu + r; blk < b1 * bpu; blk += 64) {
+        uint8_t* o = st + (mm * nblk * bpu + blk) * kStage32;
+        if (AF == kActPer32) {
+          const u32 base = (u32)(mm * arb + (int64_t)blk * 40);
+          const v2u ds = ld8(ra, base);
+          const v4u c0 = ld16(ra, base + 8), c1 = ld16(ra, base + 24);
+          *reinterpret_cast<v2u*>(o) = ds;
+          *reinterpret_cast<v4u*>(o + 16) = c0;
+          *reinterpret_cast<v4u*>(o + 32) = c1;
+        } else {  // GGUF Q8_0: fp16 d at 0, codes at 2 (the block is 2-byte aligned)
+          const u32 base = (u32)(mm * arb + (int64_t)blk * 34);
+          const u32 al = base & ~3u, sh = base & 3u;  // sh is 0 or 2
+          u32 w[10];
+#pragma unroll
+          for (int i = 0; i < 10; ++i) w[i] = ld4(ra, al + 4 * i);
+          u32 cw[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            // codes start at byte sh + 2 of w[]
+            cw[i] = sh == 0 ? __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2) : w[i + 1];
+          }
+          const float d = h2f(sh == 0 ? w[0] : (w[0] >> 16));
+          const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
+          const v4u c0 = {cw[0], cw[1], cw[2], cw[3]}, c1 = {cw[4], cw[5], cw[6], cw[7]};
+          const int sum = sdot16(ones, c1, sdot16(ones, c0, 0));
+          *reinterpret_cast<v2u*>(o) = v2u{as_u(d), (u32)sum};
+          *reinterpret_cast<v4u*>(o + 16) = c0;
+          *reinterpret_cast<v4u*>(o + 32) = c1;
+        }
+      }
+    }
+  }
+}
+
+// Activation loads of a wave's slice (one activation row) held in registers
+// between issue() and commit(), so they go out before the weight loads: vector
+// loads retire in order, so commit() waits for these loads only. Loops are
+// unrolled over at most 8 super-blocks / one block per lane, with predication.
+template <int AF>
+struct ActRegs {
+  u32 v[16];
+  DQ_DEV static bool fits(int nslice, int bpu) { return AF == kActQ8_K ? nslice <= 8 : nslice * bpu <= 64; }
+  // Q8_K: super-block b0 + i, dword j (0..72) -> lane j % 64, register 2i + j / 64.
+  // 32-value blocks: one block per lane (lane = block index in the slice).
+  DQ_DEV void issue(const uint8_t* __restrict__ acts, int64_t arb, int b0, int b1, int bpu, int r) {
+    const auto ra = rsrc(acts, (u32)arb);
+    if (AF == kActQ8_K) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const u32 base = (u32)((int64_t)(b0 + i < b1 ? b0 + i : b1) * 292);
+        v[2 * i] = b0 + i < b1 ? ld4(ra, base + 4 * r) : 0u;
+        v[2 * i + 1] = b0 + i < b1 && r < 9 ? ld4(ra, base + 4 * (64 + r)) : 0u;
+      }
+    } else {
+      const int nsl = (b1 - b0) * bpu;
+      const int blk = b0 * bpu + (r < nsl ? r : 0);
+      const u32 base = AF == kActPer32 ? (u32)((int64_t)blk * 40) : ((u32)((int64_t)blk * 34) & ~3u);
+#pragma unroll
+      for (int i = 0; i < 10; ++i) v[i] = ld4(ra, base + 4 * i);
+    }
+  }
+  DQ_DEV void commit(int64_t arb, int nblk, int b0, int b1, int bpu, int r, uint8_t* st) {
+    if (AF == kActQ8_K) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (b0 + i >= b1) break;
+        uint8_t* o = st + (b0 + i) * kStageQ8K;
+        // dword j of the block: 0 -> d @0, 1..64 -> codes @16, 65..72 -> bsums @272
+        *reinterpret_cast<u32*>(o + (r == 0 ? 0 : 16 + 4 * (r - 1))) = v[2 * i];
+        if (r < 9) *reinterpret_cast<u32*>(o + (r == 0 ? 16 + 4 * 63 : 272 + 4 * (r - 1))) = v[2 * i + 1];
+      }
+    } else {
+      const int nsl = (b1 - b0) * bpu;
+      if (r >= nsl) return;
+      const int blk = b0 * bpu + r;
+      uint8_t* o = st + blk * kStage32;
+      if (AF == kActPer32) {
+        *reinterpret_cast<v2u*>(o) = v2u{v[0], v[1]};
+        *reinterpret_cast<v4u*>(o + 16) = v4u{v[2], v[3], v[4], v[5]};
+        *reinterpret_cast<v4u*>(o + 32) = v4u{v[6], v[7], v[8], v[9]};
+      } else {  // GGUF Q8_0: fp16 d at byte 0, codes at byte 2 of the 2-byte-aligned block
+        const bool sh = (((int64_t)blk * 34) & 3) != 0;  // the block starts at byte 2 of v[0]
+        u32 cw[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) cw[i] = sh ? v[i + 1] : __builtin_amdgcn_alignbyte(v[i + 1], v[i], 2);
+        const float d = h2f(sh ? (v[0] >> 16) : v[0]);
+        const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
+        const v4u c0 = {cw[0], cw[1], cw[2], cw[3]}, c1 = {cw[4], cw[5], cw[6], cw[7]};
+        const int sum = sdot16(ones, c1, sdot16(ones, c0, 0));
+        *reinterpret_cast<v2u*>(o) = v2u{as_u(d), (u32)sum};
+        *reinterpret_cast<v4u*>(o + 16) = c0;
+        *reinterpret_cast<v4u*>(o + 32) = c1;
+      }
+    }
+  }
+};
+
+// Makes this wave's LDS writes visible to its own later LDS reads (each wave
+// stages and reads only its own slice, so no workgroup barrier is needed).
+DQ_DEV void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Quantize this wave's blocks [b0, b1) of M fp32 rows into the staged LDS layout
+// (the fused decode path), with the standalone quantizers' device functions.
+template <int AF, int M>
+DQ_DEV void quantize_slice(const float* __restrict__ x, int64_t xs, int nblk, int b0, int b1, int r, uint8_t* st) {
+  constexpr bool kSb = AF == kActQ8_K;
+  for (int mm = 0; mm < M; ++mm) {
+    const int64_t kk = (int64_t)nblk * (kSb ? 256 : 32);
+    const auto rx = rsrc(x + mm * xs, (u32)(kk * 4));
+    if (kSb) {
+      for (int b = b0; b < b1; ++b) {
+        float v[4];
+        load4f(rx, (u32)((b * 256 + 4 * r) * 4), v);
+        float d;
+        int bsum;
+        const u32 packed = q8k_quant(v, d, bsum);
+        uint8_t* o = st + (mm * nblk + b) * kStageQ8K;
+        *reinterpret_cast<u32*>(o + 16 + 4 * r) = packed;
+        if ((r & 3) == 0) *reinterpret_cast<int16_t*>(o + 272 + 2 * (r >> 2)) = (int16_t)bsum;
+        if (r == 0) *reinterpret_cast<float*>(o) = d;
+      }
+    } else {
+      for (int bb = b0; bb < b1; bb += 8) {
+        const int blk = bb + (r >> 3);
+        float v[4];
+        load4f(rx, (u32)((blk * 32 + 4 * (r & 7)) * 4), v);
+        float d;
+        int sum;
+        const u32 packed = per32_quant(v, d, sum);
+        if (blk < b1) {
+          uint8_t* o = st + (mm * nblk + blk) * kStage32;
+          *reinterpret_cast<u32*>(o + 16 + 4 * (r & 7)) = packed;
+          if ((r & 7) == 0) {
+            *reinterpret_cast<float*>(o) = d;
+            *reinterpret_cast<int32_t*>(o + 4) = sum;
+          }
+        }
+      }
+    }
+  }
+}
+
 // kFuse: the activations arrive as fp32 rows (x, row stride xs floats) and each
 // wave quantizes its own slice into LDS with the standalone quantizers' device
 // functions (q8k_quant / per32_quant), so the codes are the same bytes.
@@ -222,268 +627,111 @@ template <int WT, int AF, int M, int W, int U, bool kFuse>
 __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
                                                  const uint8_t* __restrict__ p2, const uint8_t* __restrict__ p3,
                                                  int nblk, int64_t g0, int64_t n0, int64_t n1,
-                                                 const uint8_t* __restrict__ acts_g, int64_t arb_g,
+                                                 const uint8_t* __restrict__ acts, int64_t arb,
                                                  const float* __restrict__ x, int64_t xs,
                                                  float* __restrict__ y, int64_t ys, const float* __restrict__ bias,
                                                  int32_t* __restrict__ dbg, int64_t dbg_n) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr bool kSb = AF == kActQ8_K;
-  // Q8_K: t-terms [M][nblk][64] then da [M][nblk]; per-32: slice sums [W][M][64];
-  // kFuse: then the quantized activation rows [M][row bytes]
-  float* rec = reinterpret_cast<float*>(smem);
-  float* dav = rec + M * nblk * 64;
+  // LDS: Q8_K t-terms [M][nblk][64] + da [M][nblk]  |  per-32 slice sums [W][M][64];
+  // then the staged activation rows [M][nblk (blocks of 32 for per-32)][stage bytes]
   const int r = threadIdx.x & 63, wave = wave_id();
   const int64_t G = g0 + blockIdx.x;
-  const int64_t n = G * kRowGroup + r;
-  const int b0 = wave * nblk / W, b1 = (wave + 1) * nblk / W;  // this wave's blocks
-  uint8_t* lds_act = smem + (kSb ? (size_t)M * nblk * 65 * 4 : (size_t)W * M * 64 * 4);
-  const int64_t arb = kFuse ? (int64_t)nblk * (kSb ? 292 : 40) : arb_g;
-  const uint8_t* acts = kFuse ? lds_act : acts_g;
-  if (kFuse) {
-    // quantize this wave's blocks of every activation row into LDS
-    for (int mm = 0; mm < M; ++mm) {
-      const int64_t kk = (int64_t)nblk * (kSb ? 256 : 32);
-      const auto rx = rsrc(x + mm * xs, (u32)(kk * 4));
-      if (kSb) {
-        for (int b = b0; b < b1; ++b) {
-          float v[4];
-          load4f(rx, (u32)((b * 256 + 4 * r) * 4), v);
-          float d;
-          int bsum;
-          const u32 packed = q8k_quant(v, d, bsum);
-          uint8_t* o = lds_act + (mm * nblk + b) * 292;
-          *reinterpret_cast<u32*>(o + 4 + 4 * r) = packed;
-          if ((r & 3) == 0) *reinterpret_cast<int16_t*>(o + 260 + 2 * (r >> 2)) = (int16_t)bsum;
-          if (r == 0) *reinterpret_cast<float*>(o) = d;
-        }
-      } else {
-        for (int bb = b0; bb < b1; bb += 8) {
-          const int blk = bb + (r >> 3);
-          float v[4];
-          load4f(rx, (u32)((blk * 32 + 4 * (r & 7)) * 4), v);
-          float d;
-          int sum;
-          const u32 packed = per32_quant(v, d, sum);
-          if (blk < b1) {
-            uint8_t* o = lds_act + (mm * nblk + blk) * 40;
-            *reinterpret_cast<u32*>(o + 8 + 4 * (r & 7)) = packed;
-            if ((r & 7) == 0) {
-              *reinterpret_cast<float*>(o) = d;
-              *reinterpret_cast<int32_t*>(o + 4) = sum;
-            }
-          }
-        }
-      }
-    }
-    __syncthreads();
-  }
-  float acc[M];
+  Out<M> o;
+  o.rec = reinterpret_cast<float*>(smem);
+  o.dav = o.rec + M * nblk * 64;
+  o.dbg = dbg;
+  o.dbg_n = dbg_n;
+  o.n = G * kRowGroup + r;
+  o.nblk = nblk;
+  o.r = r;
 #pragma unroll
-  for (int mm = 0; mm < M; ++mm) acc[mm] = 0.0f;
+  for (int mm = 0; mm < M; ++mm) o.acc[mm] = 0.0f;
+  const int b0 = wave * nblk / W, b1 = (wave + 1) * nblk / W;  // this wave's blocks
+  uint8_t* st = smem + (kSb ? ((size_t)M * nblk * 65 * 4 + 15) / 16 * 16 : (size_t)W * M * 64 * 4);
 
   // plane buffer resources of this row group (64 rows x nblk blocks)
   const int u0 = plane_unit(WT, 0), u1 = plane_unit(WT, 1);
-  const auto r0 = rsrc(p0 + G * nblk * 64 * u0, (u32)(nblk * 64 * u0));
-  const auto r1 = rsrc(p1 + G * nblk * 64 * u1, (u32)(nblk * 64 * u1));
-  __amdgpu_buffer_rsrc_t r2 = r0, r3 = r0;
+  Rsrcs rs;
+  rs.r0 = rsrc(p0 + G * nblk * 64 * u0, (u32)(nblk * 64 * u0));
+  rs.r1 = rsrc(p1 + G * nblk * 64 * u1, (u32)(nblk * 64 * u1));
+  rs.r2 = rs.r0;
+  rs.r3 = rs.r0;
   if (WT == kQ6_K) {
-    r2 = rsrc(p2 + G * nblk * 64 * 16, (u32)(nblk * 64 * 16));
-    r3 = rsrc(p3 + G * nblk * 64 * 2, (u32)(nblk * 64 * 2));
+    rs.r2 = rsrc(p2 + G * nblk * 64 * 16, (u32)(nblk * 64 * 16));
+    rs.r3 = rsrc(p3 + G * nblk * 64 * 2, (u32)(nblk * 64 * 2));
   }
 
-  for (int bb = b0; bb < b1; bb += U) {
-    if (WT == kQ4_K) {
-      v4u q[U][8], hd[U];
+  // activations for this slice: their loads go out first, so their latency hides
+  // behind the weight loads issued next; each wave stages only its own slice
+  const int bpu = (WT == kQ4_K || WT == kQ6_K) && !kSb ? 8 : 1;
+  float xv[2][4];
+  const bool pre = kFuse && kSb && M == 1 && b1 - b0 <= 2;
+  const bool held = !kFuse && M == 1 && ActRegs<AF>::fits(b1 - b0, bpu);
+  ActRegs<AF> ar;
+  if (pre) {
+    const auto rx = rsrc(x, (u32)(nblk * 256 * 4));
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int b = bb + u < b1 ? bb + u : nblk;  // past the slice: loads return 0, unused
+    for (int i = 0; i < 2; ++i) load4f(rx, (u32)(((b0 + i) * 256 + 4 * r) * 4), xv[i]);
+  } else if (held) {
+    ar.issue(acts, arb, b0, b1, bpu, r);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
+  Chunk<WT, U> c0;
+  const bool full0 = b0 + U <= b1;
+  if (full0) c0.load(rs, b0, b1, nblk, r);
+  __builtin_amdgcn_sched_barrier(0);
+  if (pre) {
 #pragma unroll
-        for (int c = 0; c < 8; ++c) q[u][c] = ld16(r0, (u32)(((b * 8 + c) * 64 + r) * 16));
-        hd[u] = ld16(r1, (u32)((b * 64 + r) * 16));
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int b = bb + u;
-        if (b >= b1) break;
-        // the 8 6-bit scales and mins as bytes (get_scale_min_k4, quant_formats.h:62-70)
-        const u32 s0 = hd[u].y, s1 = hd[u].z, s2 = hd[u].w;
-        const u32 sc_lo = s0 & 0x3F3F3F3Fu, mn_lo = s1 & 0x3F3F3F3Fu;
-        const u32 sc_hi = (s2 & 0x0F0F0F0Fu) | (((s0 >> 6) & 0x03030303u) << 4);
-        const u32 mn_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | (((s1 >> 6) & 0x03030303u) << 4);
-        const float d = h2f(hd[u].x), dmin = h2f(hd[u].x >> 16);
-#pragma unroll
-        for (int mm = 0; mm < M; ++mm) {
-          if (kSb) {
-            const uint8_t* ab = acts + (int64_t)mm * arb + (int64_t)b * 292;
-            int S = 0, Mn = 0;
-#pragma unroll
-            for (int jp = 0; jp < 4; ++jp) {
-              const v4u lo0 = q[u][2 * jp] & 0x0F0F0F0Fu, lo1 = q[u][2 * jp + 1] & 0x0F0F0F0Fu;
-              const v4u hi0 = (q[u][2 * jp] >> 4) & 0x0F0F0F0Fu, hi1 = (q[u][2 * jp + 1] >> 4) & 0x0F0F0F0Fu;
-              const int pe = sdot16(lo1, uld16(ab, 4 + 64 * jp + 16), sdot16(lo0, uld16(ab, 4 + 64 * jp), 0));
-              const int po = sdot16(hi1, uld16(ab, 4 + 64 * jp + 48), sdot16(hi0, uld16(ab, 4 + 64 * jp + 32), 0));
-              const u32 scw = jp < 2 ? sc_lo : sc_hi, mnw = jp < 2 ? mn_lo : mn_hi;
-              const int e = 16 * (jp & 1);
-              S += (int)bfe(scw, e, 8) * pe + (int)bfe(scw, e + 8, 8) * po;
-              const u32 bsw = uld(ab, 260 + 8 * jp), bsw2 = uld(ab, 264 + 8 * jp);  // bsums 4jp .. 4jp+3
-              const int bse = (int)(int16_t)(bsw & 0xFFFFu) + (int)(int16_t)(bsw >> 16);
-              const int bso = (int)(int16_t)(bsw2 & 0xFFFFu) + (int)(int16_t)(bsw2 >> 16);
-              Mn += (int)bfe(mnw, e, 8) * bse + (int)bfe(mnw, e + 8, 8) * bso;
-            }
-            float t = d * (float)S;
-            t = fmaf(-dmin, (float)Mn, t);
-            rec[(mm * nblk + b) * 64 + r] = t;
-            if (r == 0) dav[mm * nblk + b] = as_f(uld(ab, 0));
-            if (dbg != nullptr && n < dbg_n) {
-              int32_t* o = dbg + (((int64_t)mm * dbg_n + n) * nblk + b) * 2;
-              o[0] = S;
-              o[1] = Mn;
-            }
-          } else {
-            // per-32 activations, sub-block order j = 0..7 (kernels_generic.cpp:267-275)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const int jp = j >> 1;
-              const u32 base = (u32)((int64_t)mm * arb + ((int64_t)b * 8 + j) * 40);
-              const v4u w0 = (j & 1) ? ((q[u][2 * jp] >> 4) & 0x0F0F0F0Fu) : (q[u][2 * jp] & 0x0F0F0F0Fu);
-              const v4u w1 = (j & 1) ? ((q[u][2 * jp + 1] >> 4) & 0x0F0F0F0Fu) : (q[u][2 * jp + 1] & 0x0F0F0F0Fu);
-              const int P = sdot16(w1, uld16(acts, base + 24), sdot16(w0, uld16(acts, base + 8), 0));
-              const u32 scw = j < 4 ? sc_lo : sc_hi, mnw = j < 4 ? mn_lo : mn_hi;
-              const int sc = (int)bfe(scw, 8 * (j & 3), 8), mn = (int)bfe(mnw, 8 * (j & 3), 8);
-              const float ad = as_f(uld(acts, base));
-              const int sum = (int)uld(acts, base + 4);
-              const float t = (d * (float)sc) * (float)P - (dmin * (float)mn) * (float)sum;
-              acc[mm] = acc[mm] + ad * t;
-            }
-          }
-        }
-      }
-    } else if (WT == kQ6_K) {
-      v4u L[U][8], H[U][4], SC[U];
-      u32 DW[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int b = bb + u < b1 ? bb + u : nblk;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) L[u][c] = ld16(r0, (u32)(((b * 8 + c) * 64 + r) * 16));
-#pragma unroll
-        for (int c = 0; c < 4; ++c) H[u][c] = ld16(r1, (u32)(((b * 4 + c) * 64 + r) * 16));
-        SC[u] = ld16(r2, (u32)((b * 64 + r) * 16));
-        DW[u] = ld2(r3, (u32)((b * 64 + r) * 2));
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int b = bb + u;
-        if (b >= b1) break;
-        const float d = h2f(DW[u]);
-        // ql chunk c: half p = c/4, values 128p + 16(c%4) + i (low nibbles) and + 64
-        // (high); their top bits are qh chunk 2p + c%2 at bit pairs s and s+2,
-        // s = (c%4)/2 (quant_formats.cpp:192-216). Units u_lo = 8p + c%4, u_hi = u_lo + 4.
-        v4u qlo[8], qhi[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const int p = c >> 2, cc = c & 3, s = cc >> 1;
-          const v4u hb = H[u][2 * p + (c & 1)];
-          qlo[c] = (L[u][c] & 0x0F0F0F0Fu) | (((hb >> (2 * s)) & 0x03030303u) << 4);
-          qhi[c] = ((L[u][c] >> 4) & 0x0F0F0F0Fu) | (((hb >> (2 * s + 4)) & 0x03030303u) << 4);
-        }
-#pragma unroll
-        for (int mm = 0; mm < M; ++mm) {
-          if (kSb) {
-            const uint8_t* ab = acts + (int64_t)mm * arb + (int64_t)b * 292;
-            int S = 0;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-              const int ulo = 8 * (c >> 2) + (c & 3), uhi = ulo + 4;
-              const u32 bsl = uld(ab, 260 + 4 * (ulo >> 1)), bsh = uld(ab, 260 + 4 * (uhi >> 1));
-              const int sl = (int)(int16_t)(bsl >> (16 * (ulo & 1))), sh = (int)(int16_t)(bsh >> (16 * (uhi & 1)));
-              const int plo = sdot16(qlo[c], uld16(ab, 4 + 16 * ulo), 0) - 32 * sl;
-              const int phi = sdot16(qhi[c], uld16(ab, 4 + 16 * uhi), 0) - 32 * sh;
-              const u32 wl = ulo < 4 ? SC[u].x : ulo < 8 ? SC[u].y : ulo < 12 ? SC[u].z : SC[u].w;
-              const u32 wh = uhi < 4 ? SC[u].x : uhi < 8 ? SC[u].y : uhi < 12 ? SC[u].z : SC[u].w;
-              S += sbfe(wl, 8 * (ulo & 3), 8) * plo + sbfe(wh, 8 * (uhi & 3), 8) * phi;
-            }
-            rec[(mm * nblk + b) * 64 + r] = d * (float)S;
-            if (r == 0) dav[mm * nblk + b] = as_f(uld(ab, 0));
-            if (dbg != nullptr && n < dbg_n) {
-              int32_t* o = dbg + (((int64_t)mm * dbg_n + n) * nblk + b) * 2;
-              o[0] = S;
-              o[1] = 0;
-            }
-          } else {
-            // per-32 activations, units of 16 in order (kernels_generic.cpp:299-306)
-            const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
-#pragma unroll
-            for (int uu = 0; uu < 16; ++uu) {
-              // unit uu = 8p + cc (+4 for high nibbles): chunk c = 4p + (uu % 4)
-              const int p = uu >> 3, cc = uu & 3, c = 4 * p + cc;
-              const v4u qv = (uu & 4) ? qhi[c] : qlo[c];
-              const u32 base = (u32)((int64_t)mm * arb + ((int64_t)b * 8 + uu / 2) * 40);
-              const v4u av = uld16(acts, base + 8 + 16 * (uu & 1));
-              const int P = sdot16(qv, av, 0) - 32 * sdot16(ones, av, 0);
-              const u32 sw = uu < 4 ? SC[u].x : uu < 8 ? SC[u].y : uu < 12 ? SC[u].z : SC[u].w;
-              const float ad = as_f(uld(acts, base));
-              acc[mm] = acc[mm] + ((ad * d) * (float)sbfe(sw, 8 * (uu & 3), 8)) * (float)P;
-            }
-          }
-        }
-      }
-    } else {  // Q8_0 / Q4_0: blocks of 32
-      constexpr int kChunks = WT == kQ8_0 ? 2 : 1;
-      constexpr int kAb = AF == kActPer32 ? 40 : 34;
-      v4u q[U][kChunks];
-      u32 DW[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int b = bb + u < b1 ? bb + u : nblk;
-#pragma unroll
-        for (int c = 0; c < kChunks; ++c) q[u][c] = ld16(r0, (u32)(((b * kChunks + c) * 64 + r) * 16));
-        DW[u] = ld2(r1, (u32)((b * 64 + r) * 2));
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int b = bb + u;
-        if (b >= b1) break;
-        const float dw = h2f(DW[u]);
-#pragma unroll
-        for (int mm = 0; mm < M; ++mm) {
-          const u32 base = (u32)((int64_t)mm * arb + (int64_t)b * kAb);
-          v4u x0, x1;
-          act_codes32<AF>(acts, base, x0, x1);
-          int P;
-          if (WT == kQ8_0) {
-            P = sdot16(q[u][kChunks - 1], x1, sdot16(q[u][0], x0, 0));
-          } else {
-            // low nibbles are values 0..15, high nibbles 16..31; code = nibble - 8
-            int sum;
-            if (AF == kActPer32) {
-              sum = (int)uld(acts, base + 4);
-            } else {
-              const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
-              sum = sdot16(ones, x1, sdot16(ones, x0, 0));
-            }
-            P = sdot16((q[u][0] >> 4) & 0x0F0F0F0Fu, x1, sdot16(q[u][0] & 0x0F0F0F0Fu, x0, 0)) - 8 * sum;
-          }
-          const float da = AF == kActPer32 ? as_f(uld(acts, base)) : h2f(uld(acts, base & ~3u) >> (8 * (base & 3u)));
-          // generic order: acc += (dw * da) * (float)P (kernels_generic.cpp:220,235)
-          acc[mm] = acc[mm] + (dw * da) * (float)P;
-        }
+    for (int i = 0; i < 2; ++i) {
+      if (b0 + i < b1) {
+        float d;
+        int bsum;
+        const u32 packed = q8k_quant(xv[i], d, bsum);
+        uint8_t* ob = st + (b0 + i) * kStageQ8K;
+        *reinterpret_cast<u32*>(ob + 16 + 4 * r) = packed;
+        if ((r & 3) == 0) *reinterpret_cast<int16_t*>(ob + 272 + 2 * (r >> 2)) = (int16_t)bsum;
+        if (r == 0) *reinterpret_cast<float*>(ob) = d;
       }
     }
+  } else if (held) {
+    ar.commit(arb, nblk, b0, b1, bpu, r, st);
+  } else if (kFuse) {
+    quantize_slice<AF, M>(x, xs, nblk, b0, b1, r, st);
+  } else {
+    stage_acts<AF, M>(acts, arb, nblk, b0, b1, bpu, r, st);
+  }
+  wave_lds_sync();
+
+  int bb = b0;
+  if (full0) {
+    compute<AF, M, U>(c0, bb, st, o);
+    bb += U;
+  }
+  for (; bb + U <= b1; bb += U) {
+    Chunk<WT, U> c;
+    c.load(rs, bb, b1, nblk, r);
+    compute<AF, M, U>(c, bb, st, o);
+  }
+  for (; bb < b1; ++bb) {
+    Chunk<WT, 1> c;
+    c.load(rs, bb, b1, nblk, r);
+    compute<AF, M, 1>(c, bb, st, o);
   }
 
   if (!kSb) {
 #pragma unroll
-    for (int mm = 0; mm < M; ++mm) rec[(wave * M + mm) * 64 + r] = acc[mm];
+    for (int mm = 0; mm < M; ++mm) o.rec[(wave * M + mm) * 64 + r] = o.acc[mm];
   }
   __syncthreads();
   if (wave != 0) return;
+  const int64_t n = o.n;
 #pragma unroll
   for (int mm = 0; mm < M; ++mm) {
     float v = 0.0f;
     if (kSb) {
-      const float* tp = rec + mm * nblk * 64 + r;
-      const float* dp = dav + mm * nblk;
+      const float* tp = o.rec + mm * nblk * 64 + r;
+      const float* dp = o.dav + mm * nblk;
       int b = 0;
       for (; b + 4 <= nblk; b += 4) {
         const float t0 = tp[b * 64], t1 = tp[(b + 1) * 64], t2 = tp[(b + 2) * 64], t3 = tp[(b + 3) * 64];
@@ -496,7 +744,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
       for (; b < nblk; ++b) v = fmaf(dp[b], tp[b * 64], v);
     } else {
 #pragma unroll
-      for (int w = 0; w < W; ++w) v = v + rec[(w * M + mm) * 64 + r];
+      for (int w = 0; w < W; ++w) v = v + o.rec[(w * M + mm) * 64 + r];
     }
     if (n >= n0 && n < n1) y[mm * ys + n] = bias ? v + bias[n] : v;
   }
@@ -603,8 +851,11 @@ static hipError_t gemv_launch(const WeightDev& w, const uint8_t* acts, int64_t a
                               hipStream_t s) {
   constexpr int U = (WT == kQ8_0 || WT == kQ4_0) ? 8 : 2;
   const int64_t g0 = n0 / kRowGroup, g1 = (n1 + kRowGroup - 1) / kRowGroup;
-  size_t lds = AF == kActQ8_K ? (size_t)M * w.nblk * 65 * sizeof(float) : (size_t)kGemvWaves * M * 64 * sizeof(float);
-  if (kFuse) lds += (size_t)M * w.nblk * (AF == kActQ8_K ? 292 : 40);
+  size_t lds = AF == kActQ8_K ? ((size_t)M * w.nblk * 65 * sizeof(float) + 15) / 16 * 16
+                              : (size_t)kGemvWaves * M * 64 * sizeof(float);
+  // staged activations: Q8_K super-blocks of 320 B, or 32-value blocks of 48 B
+  lds += AF == kActQ8_K ? (size_t)M * w.nblk * 320
+                        : (size_t)M * w.nblk * (WT == kQ4_K || WT == kQ6_K ? 8 : 1) * 48;
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   const void* fn = reinterpret_cast<const void*>(&k_gemv<WT, AF, M, kGemvWaves, U, kFuse>);
   if (lds > 64 * 1024) {
