@@ -117,6 +117,53 @@ def cpu_baseline(w_host: np.ndarray, copies: int, budget_s: float) -> dict:
             "sample": f"{rows} of {N} rows of the Q4_K x sub-scaled GEMV (scalar oracle), scaled to N", "cpu": cpu}
 
 
+COPY_BYTES = 64 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_m1_gemm_m512_traffic.md")
+
+
+def pmc_leg(weights, x, acts, y, stream) -> None:
+    """Launches for the counter passes: the copy kernel first (COPY_BYTES read and
+    written, the calibration of FETCH_SIZE / WRITE_SIZE), then the measured kernels."""
+    import torch
+
+    import dynalm_amd as dq
+
+    src = torch.ones(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    nc = len(weights)
+    for i in range(2 * nc):
+        dq.matmul(weights[i % nc], x, 1, K, y, N, None, stream)
+    dq.act_quantize(dq.ACT_Q8_K, x, 1, K, K, acts, stream)
+    for i in range(2 * nc):
+        dq.gemv(weights[i % nc], dq.ACT_Q8_K, acts, 1, 0, N, y, N, None, stream)
+    m = 512
+    xg = torch.randn((m, K), device="cuda", dtype=torch.float32)
+    ag = torch.empty((m, Q8K_ROW), dtype=torch.uint8, device="cuda")
+    yg = torch.empty((m, N), dtype=torch.float32, device="cuda")
+    dq.act_quantize(dq.ACT_Q8_K, xg, m, K, K, ag, stream)
+    for i in range(4):
+        dq.gemm(weights[i % nc], dq.ACT_Q8_K, ag, m, 0, N, yg, N, None, stream)
+    torch.cuda.synchronize()
+    log("pmc leg done")
+
+
+def measured_traffic() -> dict:
+    """HBM bytes per launch of the measured kernels, as the committed counter summary
+    records them (lines `traffic <kernel> <bytes>`); empty if it is absent."""
+    out = {}
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic":
+                    out[parts[1]] = int(parts[2])
+    except OSError:
+        pass
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -125,8 +172,11 @@ def main() -> None:
     ap.add_argument("--copies", type=int, default=16, help="rotated weight copies (x 33 MB)")
     ap.add_argument("--gemm-m", type=int, default=512)
     ap.add_argument("--gemm-iters", type=int, default=50)
-    ap.add_argument("--cpu-seconds", type=float, default=1.5)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--pmc-leg", action="store_true",
+                    help="no timing: a 64 MiB copy kernel (counter calibration), then a few launches of each "
+                         "measured kernel, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path would shard the weight "
@@ -162,6 +212,10 @@ def main() -> None:
     def gemv_only(i: int) -> None:
         dq.gemv(weights[i % nc], dq.ACT_Q8_K, acts, 1, 0, N, y, N, None, stream)
 
+    if args.pmc_leg:
+        pmc_leg(weights, x, acts, y, stream)
+        return
+
     log(f"decode step x{args.steps} (warmup {args.warmup})")
     ms_step = time_launches(step, args.steps, args.warmup)
     log("GEMV on pre-quantized activations")
@@ -188,6 +242,7 @@ def main() -> None:
     ops = 2.0 * m * N * K
     tops = ops / (ms_gemm * 1e-3) / 1e12
 
+    traffic = measured_traffic()
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -216,7 +271,7 @@ def main() -> None:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": traffic.get("gemv_fused_m1"),
             "ms_per_launch": round(ms_step, 5),
         },
         "gemv_prequantized": {
@@ -232,7 +287,7 @@ def main() -> None:
             "tokens_per_s": round(m / (ms_gemm * 1e-3), 1),
             "roofline": {"kernel": "k_gemm_q4k", "bound": "mfma", "achieved": round(tops, 2),
                          "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4),
-                         "traffic": None},
+                         "traffic": traffic.get("gemm_m512")},
         },
     }
     if not args.no_cpu:

@@ -35,7 +35,7 @@ hipError_t launch_gemv_fused(const WeightDev& w, const float* x, int64_t xs, int
                              const float* bias, hipStream_t s);
 hipError_t launch_units(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int32_t* units,
                         int64_t nu, hipStream_t s);
-// int8 MFMA GEMM (Q4_K / Q6_K x Q8_K). Returns hipErrorInvalidValue for an
+// int8 MFMA GEMM (Q4_K x Q8_K). Returns hipErrorInvalidValue for an
 // unsupported pair.
 hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
                        float* y, int64_t ys, const float* bias, hipStream_t s);

@@ -124,10 +124,11 @@ DQ_API int dq_act_quantize(int fmt, const float* x, int64_t m, int64_t k, int64_
  * for r < m and i in [n0, n1). `acts`: m rows in format fmt, as dq_act_quantize
  * writes them. Replaces qmm::Kernels::gemv (dynacore/include/dynacore/cpu/qmm.h:125-126)
  * and DotQ8RowsNFn (dynacore/include/dynacore/cpu/cpu_kernels.h:53-54).
- * dq_gemv streams the weights once for up to DQ_GEMV_MAX_ROWS rows per pass; */
+ * Any m: the weights are streamed once per pass of up to 4 activation rows. */
 DQ_API int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0, int64_t n1, float* y,
                    int64_t y_stride, const float* bias, void* stream);
-/* dq_gemm runs the int8 MFMA GEMM (Q4_K / Q6_K with DQ_ACT_Q8_K); any m.
+/* dq_gemm runs the int8 MFMA GEMM (Q4_K weights with DQ_ACT_Q8_K activations;
+ * other pairs return DQ_UNSUPPORTED); any m.
  * Replaces qmm::Kernels::gemm (dynacore/include/dynacore/cpu/qmm.h:128-129). */
 DQ_API int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0, int64_t n1, float* y,
                    int64_t y_stride, const float* bias, void* stream);

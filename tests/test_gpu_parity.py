@@ -288,6 +288,100 @@ def test_q6k_full_size_down(cuda):
     assert np.array_equal(y[0, rows].view(np.uint32), want[0].view(np.uint32))
 
 
+def test_q4k_full_size_properties(cuda):
+    """Size-independent checks at config 3's full gate shape: the device copy unpacks to
+    the uploaded bytes; each row of an M=4 pass equals its own M=1 call; two row-range
+    calls reproduce the full call; the fused decode path equals quantize + GEMV."""
+    from dynalm_amd import torch_ops as T
+
+    k, n = 4096, 14336
+    w_rows = weight_rows(O.Q4_K, n, k, 31)
+    w = dq.Weight.upload(O.Q4_K, w_rows, k)
+    assert np.array_equal(w.download(), w_rows)
+    x = dev(activations(4, k, 32, outliers=False))
+    a = T.quantize(O.ACT_Q8_K, x)
+    y4 = host(T.gemv(w, O.ACT_Q8_K, a))
+    for r in range(4):
+        y1 = host(T.gemv(w, O.ACT_Q8_K, a[r:r + 1]))
+        assert np.array_equal(y1[0].view(np.uint32), y4[r].view(np.uint32))
+    out = torch.full((4, n), 777.0, device="cuda")
+    T.gemv(w, O.ACT_Q8_K, a, n0=0, n1=7168, out=out)
+    T.gemv(w, O.ACT_Q8_K, a, n0=7168, n1=n, out=out)
+    assert np.array_equal(host(out).view(np.uint32), y4.view(np.uint32))
+    assert np.array_equal(host(T.matmul(w, x)).view(np.uint32), y4.view(np.uint32))
+
+
+def test_config1_q8_0_gemv_4096(cuda):
+    """Config 1: Q8_0 4096x4096 weights from N(0, 0.02) (GGUF Q8_0 quantizer), one
+    N(0, 1) row, both activation contracts (dynacore per-32 and GGUF Q8_0)."""
+    from dynalm_amd import torch_ops as T
+
+    k = n = 4096
+    w_rows = gguf_weights(O.Q8_0, n, k, 101)
+    x = activations(1, k, 102, outliers=False)
+    w = dq.Weight.upload(O.Q8_0, w_rows, k)
+    for fmt in (O.ACT_PER32, O.ACT_Q8_0):
+        a = O.quantize_act(fmt, x)
+        y = host(T.gemv(w, fmt, dev(a)))
+        ok, worst = close(y, O.matmul(O.Q8_0, fmt, w_rows, a, k))
+        assert ok, f"{O.ACT_NAMES[fmt]}: worst error ratio {worst:.3g}"
+    y = host(T.matmul(w, dev(x)))
+    ok, worst = close(y, O.matmul(O.Q8_0, O.ACT_PER32, w_rows, O.quantize_act(O.ACT_PER32, x), k))
+    assert ok, f"matmul: worst error ratio {worst:.3g}"
+
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_config2_q4_0_gate_shape(cuda, m):
+    """Config 2: Q4_0 at K=4096, N=14336, M in {1, 4, 8}; sampled rows against the
+    oracle, through dq_matmul (per-32 activations quantized in the kernel)."""
+    from dynalm_amd import torch_ops as T
+
+    k, n = 4096, 14336
+    w_rows = gguf_weights(O.Q4_0, n, k, 200 + m)
+    x = activations(m, k, 210 + m, outliers=False)
+    w = dq.Weight.upload(O.Q4_0, w_rows, k)
+    y = host(T.matmul(w, dev(x)))
+    rows = np.random.default_rng(m).choice(n, 384, replace=False)
+    want = O.matmul(O.Q4_0, O.ACT_PER32, w_rows[rows], O.quantize_act(O.ACT_PER32, x), k)
+    ok, worst = close(y[:, rows], want)
+    assert ok, f"worst error ratio {worst:.3g}"
+
+
+QWEN_SHAPES = [  # (name, dtype, n, k) of one Qwen2.5-1.5B layer and the lm_head
+    ("q", O.Q4_K, 1536, 1536), ("k", O.Q4_K, 256, 1536), ("v", O.Q6_K, 256, 1536),
+    ("o", O.Q4_K, 1536, 1536), ("gate", O.Q4_K, 8960, 1536), ("down", O.Q6_K, 1536, 8960),
+]
+
+
+@pytest.mark.parametrize("shape", QWEN_SHAPES, ids=lambda s: s[0])
+def test_config5_qwen_layer_m16(cuda, shape):
+    """Config 5: the decode-step matmuls of a Qwen2.5-1.5B layer at M=16 through
+    dq_matmul (Q8_K activations, GEMV passes): bit-identical to the oracle."""
+    from dynalm_amd import torch_ops as T
+
+    _, t, n, k = shape
+    w_rows = gguf_weights(t, n, k, 300 + n + k)
+    x = activations(16, k, 301, outliers=False)
+    w = dq.Weight.upload(t, w_rows, k)
+    y = host(T.matmul(w, dev(x)))
+    want = O.matmul(t, O.ACT_Q8_K, w_rows, O.quantize_act(O.ACT_Q8_K, x), k)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+def test_config5_lm_head_m16(cuda):
+    """Config 5's lm_head: Q6_K 151936 x 1536 at M=16; sampled rows bit-identical."""
+    from dynalm_amd import torch_ops as T
+
+    k, n = 1536, 151936
+    w_rows = weight_rows(O.Q6_K, n, k, 400)
+    x = activations(16, k, 401, outliers=False)
+    w = dq.Weight.upload(O.Q6_K, w_rows, k)
+    y = host(T.matmul(w, dev(x)))
+    rows = np.concatenate([np.random.default_rng(2).choice(n, 256, replace=False), [0, n - 1]])
+    want = O.matmul(O.Q6_K, O.ACT_Q8_K, w_rows[rows], O.quantize_act(O.ACT_Q8_K, x), k)
+    assert np.array_equal(y[:, rows].view(np.uint32), want.view(np.uint32))
+
+
 # ------------------------------------------------------------- error paths
 
 
