@@ -17,7 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libdynaq.so")
 
-SOURCES = ["dq_kernels.hip", "dq_gemm.hip", "dq_api.cpp"]
+SOURCES = ["dq_kernels.hip", "dq_gemv.hip", "dq_gemm.hip", "dq_api.cpp"]
 ARCH = os.environ.get("DYNAQ_ARCH", "gfx950")
 
 # Device code: IEEE fp32 division/sqrt (the quantizers need correctly rounded
@@ -44,25 +44,29 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
+def _compile(cc: str, src: str, verbose: bool) -> str:
+    path = os.path.join(CSRC, src)
+    obj = os.path.join(LIB_DIR, os.path.splitext(src)[0] + ".o")
+    cmd = [cc, *HIP_FLAGS, "-x", "hip", "-c", path, "-o", obj, f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    out = "\n".join(l for l in (res.stdout + res.stderr).splitlines()
+                    if "packed-fp32-ops" not in l and "is not a recognized feature" not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src}:\n{out}")
+    if out.strip() and verbose:
+        print(out)
+    return obj
+
+
 def build(verbose: bool = False) -> str:
+    from concurrent.futures import ThreadPoolExecutor
+
     os.makedirs(LIB_DIR, exist_ok=True)
-    objs = []
     cc = hipcc()
-    for src in SOURCES:
-        path = os.path.join(CSRC, src)
-        obj = os.path.join(LIB_DIR, os.path.splitext(src)[0] + ".o")
-        lang = ["-x", "hip"] if src.endswith(".hip") else ["-x", "hip"]
-        cmd = [cc, *HIP_FLAGS, *lang, "-c", path, "-o", obj, f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}"]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        res = subprocess.run(cmd, capture_output=True, text=True)
-        out = "\n".join(l for l in (res.stdout + res.stderr).splitlines()
-                        if "packed-fp32-ops" not in l and "is not a recognized feature" not in l)
-        if res.returncode != 0:
-            raise RuntimeError(f"hipcc failed on {src}:\n{out}")
-        if out.strip() and verbose:
-            print(out)
-        objs.append(obj)
+    with ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
+        objs = list(pool.map(lambda src: _compile(cc, src, verbose), SOURCES))
     tmp = LIB + ".tmp"
     cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     res = subprocess.run(cmd, capture_output=True, text=True)

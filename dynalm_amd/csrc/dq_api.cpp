@@ -118,6 +118,7 @@ int upload_impl(int dtype, const void* rows, bool host, int64_t n, int64_t k, in
   d.n_pad = (n + dq::kRowGroup - 1) / dq::kRowGroup * dq::kRowGroup;
   d.nblk = k / dq::block_elems(dtype);
   hipError_t e = hipGetDevice(&d.device);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, d.device);
   int rc = DQ_OK;
   const uint8_t* src = static_cast<const uint8_t*>(rows);
   void* staging = nullptr;

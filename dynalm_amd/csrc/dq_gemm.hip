@@ -150,7 +150,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const v4u q = half == 0 ? (gq & 0x0F0F0F0Fu) : ((gq >> 4) & 0x0F0F0F0Fu);
+        // high nibbles are stored XOR 8 (dq_layout.h)
+        const v4u q = half == 0 ? (gq & 0x0F0F0F0Fu) : (((gq >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u);
         const int g = 2 * half + hh;
         const u32 sc = (u32)(half == 0 ? sca : scb);
         const u32 mn = (u32)(half == 0 ? mna : mnb) * 0x01010101u;

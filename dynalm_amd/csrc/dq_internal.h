@@ -12,6 +12,7 @@ namespace dq {
 struct WeightDev {
   int dtype = 0;
   int device = 0;
+  int cus = 256;           // compute units of the device (launch shapes)
   int64_t n = 0, k = 0;    // logical rows and values per row
   int64_t n_pad = 0;       // rows rounded up to a multiple of kRowGroup
   int64_t nblk = 0;        // blocks (super-blocks for K-quants) per row

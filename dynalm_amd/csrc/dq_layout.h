@@ -21,9 +21,12 @@
 //   Q6_K  0: ql 128          1: qh 64    2: scales 16    3: d 2
 //   Q8_0  0: qs 32           1: d 2
 //   Q4_0  0: qs 16           1: d 2
-// The bytes of every plane are the block's bytes unchanged (a permutation of the
-// GGUF row bytes), so the device copy holds exactly the GGUF byte count plus the
-// zero padding rows.
+// The bytes of every plane are the block's bytes (a permutation of the GGUF row
+// bytes), so the device copy holds exactly the GGUF byte count plus the zero
+// padding rows. One transform: in Q4_K's qs plane every byte has bit 7 flipped
+// (the high nibble XOR 8), so that `byte & 0xF0` read as int8 is 16 * (q - 8) for
+// the high nibble q, which a signed int8 dot product takes directly
+// (plane_xor; the unpack flips it back).
 #pragma once
 
 #include <stdint.h>
@@ -74,6 +77,9 @@ DQ_HD void plane_of_byte(int t, int i, int* p, int* off) {
       break;
   }
 }
+
+// XOR applied to every byte of plane p on upload (and undone on download).
+DQ_HD int plane_xor(int t, int p) { return t == kQ4_K && p == 0 ? 0x80 : 0; }
 
 // Offset in plane p of byte `off` of the unit of row n, block b.
 DQ_HD int64_t plane_offset(int t, int p, int64_t n, int64_t b, int64_t nblk, int off) {

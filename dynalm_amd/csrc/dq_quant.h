@@ -1,0 +1,74 @@
+// dq_quant.h -- device functions of the activation quantizers, shared by the
+// standalone quantizer kernels (dq_kernels.hip) and the GEMV's fused decode path
+// (dq_gemv.hip), so both write the same code bytes.
+//
+// Contracts: per-32 ActBlockQ8 dynacore/cpu/generic/kernels_generic.cpp:187-207;
+// one scale per 256 values (Q8_K) dynacore/cpu/avx2/kernels_avx2.cpp:638-644.
+#pragma once
+
+#include "dq_device.h"
+
+namespace dq {
+
+// ===================================================================== quantizers
+// One wave per 256 values of a row; lane l holds values 4l .. 4l+3.
+
+// Loads values [v0, v0 + 4) of a row through a buffer resource (zeros past the end).
+DQ_DEV void load4f(__amdgpu_buffer_rsrc_t r, u32 off, float v[4]) {
+  const v4u u = ld16(r, off);
+  v[0] = as_f(u.x);
+  v[1] = as_f(u.y);
+  v[2] = as_f(u.z);
+  v[3] = as_f(u.w);
+}
+
+// The comparison clamp of kernels_generic.cpp:199 (NaN goes to -L).
+DQ_DEV float clampl(float v, float l) { return v > -l ? (v < l ? v : l) : -l; }
+
+// 4 codes at inverse scale id, round half to even; returns the packed bytes and adds their sum.
+DQ_DEV u32 codes4_rne(const float v[4], float id, int& sum) {
+  u32 packed = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int c = (int)__builtin_rintf(clampl(v[i] * id, 127.0f));
+    c = c < -127 ? -127 : (c > 127 ? 127 : c);
+    sum += c;
+    packed |= ((u32)c & 0xFFu) << (8 * i);
+  }
+  return packed;
+}
+
+// Q8_K quantization of one 256-value super-block held 4 values per lane (lane l:
+// values 4l .. 4l+3): d = amax/127, codes round half to even at 1/d
+// (kernels_avx2.cpp:638-644). Returns the lane's 4 packed codes, d, and in every
+// lane the sum of the 16 codes of its 4-lane group (bsums[l / 4]).
+DQ_DEV u32 q8k_quant(const float v[4], float& d, int& bsum) {
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = max8f(amax);
+#pragma unroll
+  for (int s = 8; s < 64; s <<= 1) amax = fmaxf(amax, __shfl_xor(amax, s, 64));
+  d = amax / 127.0f;
+  const float id = d > 0 ? 1.0f / d : 0.0f;
+  int sum = 0;
+  const u32 packed = codes4_rne(v, id, sum);
+  sum += dpp<kQuadXor1>(sum);
+  sum += dpp<kQuadXor2>(sum);
+  bsum = sum;
+  return packed;
+}
+
+// Per-32 ActBlockQ8 quantization (kernels_generic.cpp:187-207) of 8 blocks held 4
+// values per lane (lanes 8i .. 8i+7 hold block i): returns the lane's packed codes,
+// the block's d and (in every lane of the block) the block's code sum.
+DQ_DEV u32 per32_quant(const float v[4], float& d, int& sum) {
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = max8f(amax);
+  d = amax / 127.0f;
+  const float id = d > 0 ? 1.0f / d : 0.0f;
+  int s = 0;
+  const u32 packed = codes4_rne(v, id, s);
+  sum = red8(s);
+  return packed;
+}
+
+}  // namespace dq
