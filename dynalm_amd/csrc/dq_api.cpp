@@ -284,7 +284,7 @@ int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
     return fail(DQ_UNSUPPORTED, "no GEMM kernel for weight type %d with activation format %d", w->dev.dtype, fmt);
   }
   if (m == 0 || n0 == n1) return DQ_OK;
-  if ((m + 255) / 256 > 65535) return fail(DQ_UNSUPPORTED, "m too large");
+  if ((m + 127) / 128 > 65535) return fail(DQ_UNSUPPORTED, "m too large");
   DQ_HIP(dq::launch_gemm(w->dev, fmt, static_cast<const uint8_t*>(acts), dq_act_row_bytes(fmt, w->dev.k), m, n0, n1, y,
                          y_stride, bias, as_stream(stream)),
          "gemm launch");

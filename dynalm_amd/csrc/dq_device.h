@@ -35,6 +35,10 @@ DQ_DEV uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f);
 DQ_DEV float as_f(u32 u) { return __builtin_bit_cast(float, u); }
 DQ_DEV u32 as_u(float f) { return __builtin_bit_cast(u32, f); }
 
+// Bit-field extracts (v_bfe_u32 / v_bfe_i32).
+DQ_DEV u32 bfe(u32 v, int off, int w) { return __builtin_amdgcn_ubfe(v, off, w); }
+DQ_DEV int sbfe(u32 v, int off, int w) { return __builtin_amdgcn_sbfe((int)v, off, w); }
+
 DQ_DEV int sdot4(u32 a, u32 b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 // sum_i a[i] * b[i] over 16 int8 lanes, added to c.
 DQ_DEV int sdot16(v4u a, v4u b, int c) {

@@ -37,8 +37,6 @@ DQ_DEV v4u uld16(const uint8_t* __restrict__ p, u32 off) {
   const v4ua v = *reinterpret_cast<const v4ua*>(p + off);
   return v4u{v.x, v.y, v.z, v.w};
 }
-DQ_DEV u32 bfe(u32 v, int off, int w) { return __builtin_amdgcn_ubfe(v, off, w); }
-DQ_DEV int sbfe(u32 v, int off, int w) { return __builtin_amdgcn_sbfe((int)v, off, w); }
 DQ_DEV int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // Activation codes 16c .. 16c+15 of a 32-value per-32 / GGUF-Q8_0 block at base (uniform).
