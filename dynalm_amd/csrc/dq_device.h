@@ -56,6 +56,7 @@ DQ_DEV int dpp(int v) {
 constexpr int kQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
 constexpr int kQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
 constexpr int kHalfMirror = 0x141;  // row_half_mirror: lane i <-> 7 - i in each 8
+constexpr int kRowRor8 = 0x128;     // row_ror:8: lane i <- lane (i + 8) % 16 of its row of 16
 
 // Exact integer sum over each aligned group of 8 lanes (every lane gets it).
 DQ_DEV int red8(int v) {

@@ -164,9 +164,10 @@ struct Out {
 // 16 * (q - 8) and a dot product seeded with 128 * s_j (the staged odd-sub-block
 // sum) is exactly 16 * P_j.
 template <int AF, int M, int U>
-DQ_DEV void compute(const Chunk<kQ4_K, U>& ch, int bb, const uint8_t* st, Out<M>& o) {
+DQ_DEV void compute(const Chunk<kQ4_K, U>& ch, int bb, const uint8_t* st, Out<M>& o, int nv = U) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
+    if (u >= nv) break;
     const int b = bb + u;
     // the 6-bit scales sc_j (bits 0..5 of byte j&3 of sc_lo / sc_hi) and the mins m_j
     // as clean bytes (get_scale_min_k4, quant_formats.h:62-70)
@@ -235,9 +236,10 @@ DQ_DEV void compute(const Chunk<kQ4_K, U>& ch, int bb, const uint8_t* st, Out<M>
 }
 
 template <int AF, int M, int U>
-DQ_DEV void compute(const Chunk<kQ6_K, U>& ch, int bb, const uint8_t* st, Out<M>& o) {
+DQ_DEV void compute(const Chunk<kQ6_K, U>& ch, int bb, const uint8_t* st, Out<M>& o, int nv = U) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
+    if (u >= nv) break;
     const int b = bb + u;
     const float d = h2f(ch.DW[u]);
     // ql chunk c: half p = c/4, values 128p + 16(c%4) + i (low nibbles) and + 64
@@ -293,9 +295,10 @@ DQ_DEV void compute(const Chunk<kQ6_K, U>& ch, int bb, const uint8_t* st, Out<M>
 }
 
 template <int WT, int AF, int M, int U>
-DQ_DEV void compute32(const Chunk32<WT, U>& ch, int bb, const uint8_t* st, Out<M>& o) {
+DQ_DEV void compute32(const Chunk32<WT, U>& ch, int bb, const uint8_t* st, Out<M>& o, int nv) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
+    if (u >= nv) break;
     const int b = bb + u;
     const float dw = h2f(ch.DW[u]);
 #pragma unroll
@@ -316,12 +319,12 @@ DQ_DEV void compute32(const Chunk32<WT, U>& ch, int bb, const uint8_t* st, Out<M
   }
 }
 template <int AF, int M, int U>
-DQ_DEV void compute(const Chunk<kQ8_0, U>& ch, int bb, const uint8_t* st, Out<M>& o) {
-  compute32<kQ8_0, AF, M, U>(ch, bb, st, o);
+DQ_DEV void compute(const Chunk<kQ8_0, U>& ch, int bb, const uint8_t* st, Out<M>& o, int nv = U) {
+  compute32<kQ8_0, AF, M, U>(ch, bb, st, o, nv);
 }
 template <int AF, int M, int U>
-DQ_DEV void compute(const Chunk<kQ4_0, U>& ch, int bb, const uint8_t* st, Out<M>& o) {
-  compute32<kQ4_0, AF, M, U>(ch, bb, st, o);
+DQ_DEV void compute(const Chunk<kQ4_0, U>& ch, int bb, const uint8_t* st, Out<M>& o, int nv = U) {
+  compute32<kQ4_0, AF, M, U>(ch, bb, st, o, nv);
 }
 
 // ---- staging a wave's slice of activations into LDS. Loads are issued first
@@ -384,22 +387,22 @@ DQ_DEV void stage_acts(const uint8_t* __restrict__ acts, int64_t arb, int nblk, 
 
 // Activation loads of a wave's slice (one activation row) held in registers
 // between issue() and commit(), so they go out before the weight loads: vector
-// loads retire in order, so commit() waits for these loads only. Loops are
-// unrolled over at most 8 super-blocks / one block per lane, with predication.
-template <int AF>
+// loads retire in order, so commit() waits for these loads only. Every load is
+// issued unconditionally (blocks past the slice read zeros through the buffer
+// bound), so no branch separates the loads from their uses and the compiler's
+// waits stay exact. Q8_K: at most E super-blocks; 32-value blocks: one per lane.
+template <int AF, int E>
 struct ActRegs {
-  u32 v[16];
-  DQ_DEV static bool fits(int nslice, int bpu) { return AF == kActQ8_K ? nslice <= 8 : nslice * bpu <= 64; }
-  // Q8_K: super-block b0 + i, dword j (0..72) -> lane j % 64, register 2i + j / 64.
-  // 32-value blocks: one block per lane (lane = block index in the slice).
+  u32 v[AF == kActQ8_K ? 2 * E : 10];
   DQ_DEV void issue(const uint8_t* __restrict__ acts, int64_t arb, int b0, int b1, int bpu, int r) {
     const auto ra = rsrc(acts, (u32)arb);
-    if (AF == kActQ8_K) {
+    if constexpr (AF == kActQ8_K) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const u32 base = (u32)((int64_t)(b0 + i < b1 ? b0 + i : b1) * 292);
-        v[2 * i] = b0 + i < b1 ? ld4(ra, base + 4 * r) : 0u;
-        v[2 * i + 1] = b0 + i < b1 && r < 9 ? ld4(ra, base + 4 * (64 + r)) : 0u;
+      for (int i = 0; i < E; ++i) {
+        const bool ok = b0 + i < b1;
+        const u32 base = (u32)((int64_t)(b0 + i) * 292);
+        v[2 * i] = ld4(ra, ok ? base + 4 * r : (u32)arb);
+        v[2 * i + 1] = ld4(ra, ok && r < 9 ? base + 4 * (64 + r) : (u32)arb);
       }
     } else {
       const int nsl = (b1 - b0) * bpu;
@@ -410,9 +413,9 @@ struct ActRegs {
     }
   }
   DQ_DEV void commit(int64_t arb, int nblk, int b0, int b1, int bpu, int r, uint8_t* st) {
-    if (AF == kActQ8_K) {
+    if constexpr (AF == kActQ8_K) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < E; ++i) {
         if (b0 + i >= b1) break;
         uint8_t* o = st + (b0 + i) * kStageQ8K;
         // dword j of the block: 0 -> d @0, 1..64 -> codes @16, 65..72 -> bsums @272
@@ -500,7 +503,10 @@ DQ_DEV void quantize_slice(const float* __restrict__ x, int64_t xs, int nblk, in
 // kFuse: the activations arrive as fp32 rows (x, row stride xs floats) and each
 // wave quantizes its own slice into LDS with the standalone quantizers' device
 // functions (q8k_quant / per32_quant), so the codes are the same bytes.
-template <int WT, int AF, int M, int W, int U, bool kFuse>
+// kEarly (one activation row only): 0 = activations staged by loops after the
+// first weight loads; E > 0 = each wave holds at most E Q8_K super-blocks (or, for
+// 32-value formats, at most 64 blocks) and loads them ahead of the weights.
+template <int WT, int AF, int M, int W, int U, bool kFuse, int kEarly>
 __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
                                                  const uint8_t* __restrict__ p2, const uint8_t* __restrict__ p3,
                                                  int nblk, int64_t g0, int64_t n0, int64_t n1,
@@ -539,54 +545,59 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
     rs.r3 = rsrc(p3 + G * nblk * 64 * 2, (u32)(nblk * 64 * 2));
   }
 
-  // activations for this slice: their loads go out first, so their latency hides
-  // behind the weight loads issued next; each wave stages only its own slice
+  // Activations of this slice first, so their latency hides behind the weight
+  // loads issued next (each wave stages only its own slice). With kEarly the
+  // activation loads and the first weight chunk are issued unconditionally, in
+  // straight-line code, so the waits before their uses count exactly these loads.
   const int bpu = (WT == kQ4_K || WT == kQ6_K) && !kSb ? 8 : 1;
-  float xv[2][4];
-  const bool pre = kFuse && kSb && M == 1 && b1 - b0 <= 2;
-  const bool held = !kFuse && M == 1 && ActRegs<AF>::fits(b1 - b0, bpu);
-  ActRegs<AF> ar;
-  if (pre) {
-    const auto rx = rsrc(x, (u32)(nblk * 256 * 4));
+  constexpr int kE = kEarly > 0 ? kEarly : 1;
+  float xv[kE][4];
+  ActRegs<AF, kE> ar;
+  if constexpr (kEarly > 0) {
+    if constexpr (kFuse) {  // Q8_K, one row: the fp32 values of this wave's super-blocks
+      const auto rx = rsrc(x, (u32)(nblk * 256 * 4));
 #pragma unroll
-    for (int i = 0; i < 2; ++i) load4f(rx, (u32)(((b0 + i) * 256 + 4 * r) * 4), xv[i]);
-  } else if (held) {
-    ar.issue(acts, arb, b0, b1, bpu, r);
+      for (int i = 0; i < kE; ++i) load4f(rx, (u32)(((b0 + i) * 256 + 4 * r) * 4), xv[i]);
+    } else {
+      ar.issue(acts, arb, b0, b1, bpu, r);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
   Chunk<WT, U> c0;
-  const bool full0 = b0 + U <= b1;
-  if (full0) c0.load(rs, b0, b1, nblk, r);
+  c0.load(rs, b0, b1, nblk, r);
   __builtin_amdgcn_sched_barrier(0);
-  if (pre) {
+  if constexpr (kEarly > 0) {
+    if constexpr (kFuse) {
+      // quantized unconditionally (so the loads above stay ahead of the weight
+      // loads); only a super-block of this slice is stored
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      if (b0 + i < b1) {
+      for (int i = 0; i < kE; ++i) {
         float d;
         int bsum;
         const u32 packed = q8k_quant(xv[i], d, bsum);
-        const int s32 = bsum + dpp<kHalfMirror>(bsum);
-        uint8_t* ob = st + (b0 + i) * kStageQ8K;
-        *reinterpret_cast<u32*>(ob + 16 + 4 * r) = packed;
-        if ((r & 3) == 0) *reinterpret_cast<int16_t*>(ob + 272 + 2 * (r >> 2)) = (int16_t)bsum;
-        if ((r & 7) == 0) stage_subsum(ob, r >> 3, s32);
-        if (r == 0) *reinterpret_cast<float*>(ob) = d;
+        const int s32 = bsum + dpp<kHalfMirror>(bsum);  // the other 4-lane group of the sub-block
+        if (b0 + i < b1) {
+          uint8_t* ob = st + (b0 + i) * kStageQ8K;
+          *reinterpret_cast<u32*>(ob + 16 + 4 * r) = packed;
+          if ((r & 3) == 0) *reinterpret_cast<int16_t*>(ob + 272 + 2 * (r >> 2)) = (int16_t)bsum;
+          if ((r & 7) == 0) stage_subsum(ob, r >> 3, s32);
+          if (r == 0) *reinterpret_cast<float*>(ob) = d;
+        }
       }
+    } else {
+      ar.commit(arb, nblk, b0, b1, bpu, r, st);
     }
-  } else if (held) {
-    ar.commit(arb, nblk, b0, b1, bpu, r, st);
-  } else if (kFuse) {
+  } else if constexpr (kFuse) {
     quantize_slice<AF, M>(x, xs, nblk, b0, b1, r, st);
   } else {
     stage_acts<AF, M>(acts, arb, nblk, b0, b1, bpu, r, st);
   }
   wave_lds_sync();
 
-  int bb = b0;
-  if (full0) {
-    compute<AF, M, U>(c0, bb, st, o);
-    bb += U;
-  }
+  // the first chunk holds blocks [b0, b0 + U); those at or past b1 read as zeros
+  const int nv0 = b1 - b0 < U ? b1 - b0 : U;
+  if (nv0 > 0) compute<AF, M, U>(c0, b0, st, o, nv0);
+  int bb = b0 + U;
   for (; bb + U <= b1; bb += U) {
     Chunk<WT, U> c;
     c.load(rs, bb, b1, nblk, r);
@@ -637,7 +648,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
 // the tail; with more row groups than CUs, 8-wave workgroups (two per CU) do
 // better. 16 waves leave 128 VGPRs per lane: K-quant passes of more than one
 // activation row need more and keep 8 waves.
-template <int WT, int AF, int M, bool kFuse, int W>
+template <int WT, int AF, int M, bool kFuse, int W, int kEarly>
 static hipError_t gemv_launch(const WeightDev& w, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
                               int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
                               hipStream_t s) {
@@ -651,15 +662,34 @@ static hipError_t gemv_launch(const WeightDev& w, const uint8_t* acts, int64_t a
   lds += AF == kActQ8_K ? (size_t)M * w.nblk * kStageQ8K
                         : (size_t)M * w.nblk * (WT == kQ4_K || WT == kQ6_K ? 8 : 1) * kStage32;
   if (lds > 160 * 1024) return hipErrorInvalidValue;
-  const void* fn = reinterpret_cast<const void*>(&k_gemv<WT, AF, M, W, U, kFuse>);
+  const void* fn = reinterpret_cast<const void*>(&k_gemv<WT, AF, M, W, U, kFuse, kEarly>);
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((k_gemv<WT, AF, M, W, U, kFuse>), dim3((unsigned)(g1 - g0)), dim3(64 * W), lds, s, w.plane[0],
+  hipLaunchKernelGGL((k_gemv<WT, AF, M, W, U, kFuse, kEarly>), dim3((unsigned)(g1 - g0)), dim3(64 * W), lds, s, w.plane[0],
                      w.plane[1], w.plane[2], w.plane[3], (int)w.nblk, g0, n0, n1, acts, arb, x, xs, y, ys, bias, dbg,
                      w.n);
   return hipGetLastError();
+}
+
+// The early-activation variant for W waves: Q8_K rows hold at most 2 super-blocks
+// per wave (fused or not); 32-value formats at most 64 blocks per wave (not fused).
+template <int WT, int AF, int M, bool kFuse, int W>
+static hipError_t gemv_early(const WeightDev& w, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
+                             int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
+                             hipStream_t s) {
+  const int64_t per_wave = (w.nblk + W - 1) / W;  // blocks of the largest slice
+  if constexpr (M == 1 && AF == kActQ8_K) {
+    if (per_wave == 1) return gemv_launch<WT, AF, M, kFuse, W, 1>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+    if (per_wave == 2) return gemv_launch<WT, AF, M, kFuse, W, 2>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+  } else if constexpr (M == 1 && !kFuse) {
+    const int64_t bpu = WT == kQ4_K || WT == kQ6_K ? 8 : 1;
+    if (per_wave * bpu <= 64) {
+      return gemv_launch<WT, AF, M, kFuse, W, 1>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+    }
+  }
+  return gemv_launch<WT, AF, M, kFuse, W, 0>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
 }
 
 template <int WT, int AF, int M, bool kFuse>
@@ -669,9 +699,9 @@ static hipError_t gemv_waves(const WeightDev& w, const uint8_t* acts, int64_t ar
   constexpr bool kWide = M == 1 || WT == kQ8_0 || WT == kQ4_0;
   const int64_t groups = (n1 + kRowGroup - 1) / kRowGroup - n0 / kRowGroup;
   if (kWide && groups <= w.cus) {
-    return gemv_launch<WT, AF, M, kFuse, kWide ? 16 : 8>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+    return gemv_early<WT, AF, M, kFuse, kWide ? 16 : 8>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
   }
-  return gemv_launch<WT, AF, M, kFuse, 8>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+  return gemv_early<WT, AF, M, kFuse, 8>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
 }
 
 // M rows (1..4) of one pass; x != nullptr: fused quantization of fp32 rows.

@@ -45,8 +45,11 @@ DQ_DEV u32 codes4_rne(const float v[4], float id, int& sum) {
 DQ_DEV u32 q8k_quant(const float v[4], float& d, int& bsum) {
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
   amax = max8f(amax);
-#pragma unroll
-  for (int s = 8; s < 64; s <<= 1) amax = fmaxf(amax, __shfl_xor(amax, s, 64));
+  amax = fmaxf(amax, as_f((u32)dpp<kRowRor8>((int)as_u(amax))));  // rows of 16 lanes
+  // the four row maxima (wave-uniform reads, no LDS round trip)
+  const float r0 = as_f(__builtin_amdgcn_readlane(as_u(amax), 0)), r1 = as_f(__builtin_amdgcn_readlane(as_u(amax), 16));
+  const float r2 = as_f(__builtin_amdgcn_readlane(as_u(amax), 32)), r3 = as_f(__builtin_amdgcn_readlane(as_u(amax), 48));
+  amax = fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
   d = amax / 127.0f;
   const float id = d > 0 ? 1.0f / d : 0.0f;
   int sum = 0;
