@@ -394,6 +394,8 @@ DQ_DEV void stage_acts(const uint8_t* __restrict__ acts, int64_t arb, int nblk, 
 template <int AF, int E>
 struct ActRegs {
   u32 v[AF == kActQ8_K ? 2 * E : 10];
+  v2u pd;      // per-32: {d, sum}
+  v4u pc[2];   // per-32: the 32 codes
   DQ_DEV void issue(const uint8_t* __restrict__ acts, int64_t arb, int b0, int b1, int bpu, int r) {
     const auto ra = rsrc(acts, (u32)arb);
     if constexpr (AF == kActQ8_K) {
@@ -407,17 +409,26 @@ struct ActRegs {
     } else {
       const int nsl = (b1 - b0) * bpu;
       const int blk = b0 * bpu + (r < nsl ? r : 0);
-      const u32 base = AF == kActPer32 ? (u32)((int64_t)blk * 40) : ((u32)((int64_t)blk * 34) & ~3u);
+      if constexpr (AF == kActPer32) {
+        const u32 base = (u32)((int64_t)blk * 40);
+        pd = ld8(ra, base);
+        pc[0] = ld16(ra, base + 8);
+        pc[1] = ld16(ra, base + 24);
+      } else {
+        const u32 base = (u32)((int64_t)blk * 34) & ~3u;
 #pragma unroll
-      for (int i = 0; i < 10; ++i) v[i] = ld4(ra, base + 4 * i);
+        for (int i = 0; i < 10; ++i) v[i] = ld4(ra, base + 4 * i);
+      }
     }
   }
-  DQ_DEV void commit(int64_t arb, int nblk, int b0, int b1, int bpu, int r, uint8_t* st) {
+  // The stores are unconditional: blocks outside the slice go to a per-lane dummy
+  // area (kDummyBytes at `dummy`), so the loads above have no conditional use that
+  // the compiler could sink them into (below the weight loads).
+  DQ_DEV void commit(int64_t arb, int nblk, int b0, int b1, int bpu, int r, uint8_t* st, uint8_t* dummy) {
     if constexpr (AF == kActQ8_K) {
 #pragma unroll
       for (int i = 0; i < E; ++i) {
-        if (b0 + i >= b1) break;
-        uint8_t* o = st + (b0 + i) * kStageQ8K;
+        uint8_t* o = b0 + i < b1 ? st + (b0 + i) * kStageQ8K : dummy;
         // dword j of the block: 0 -> d @0, 1..64 -> codes @16, 65..72 -> bsums @272
         *reinterpret_cast<u32*>(o + (r == 0 ? 0 : 16 + 4 * (r - 1))) = v[2 * i];
         if (r < 9) *reinterpret_cast<u32*>(o + (r == 0 ? 16 + 4 * 63 : 272 + 4 * (r - 1))) = v[2 * i + 1];
@@ -425,13 +436,12 @@ struct ActRegs {
       }
     } else {
       const int nsl = (b1 - b0) * bpu;
-      if (r >= nsl) return;
       const int blk = b0 * bpu + r;
-      uint8_t* o = st + blk * kStage32;
-      if (AF == kActPer32) {
-        *reinterpret_cast<v2u*>(o) = v2u{v[0], v[1]};
-        *reinterpret_cast<v4u*>(o + 16) = v4u{v[2], v[3], v[4], v[5]};
-        *reinterpret_cast<v4u*>(o + 32) = v4u{v[6], v[7], v[8], v[9]};
+      uint8_t* o = r < nsl ? st + blk * kStage32 : dummy + r * kStage32;
+      if constexpr (AF == kActPer32) {
+        *reinterpret_cast<v2u*>(o) = pd;
+        *reinterpret_cast<v4u*>(o + 16) = pc[0];
+        *reinterpret_cast<v4u*>(o + 32) = pc[1];
       } else {  // GGUF Q8_0: fp16 d at byte 0, codes at byte 2 of the 2-byte-aligned block
         const bool sh = (((int64_t)blk * 34) & 3) != 0;  // the block starts at byte 2 of v[0]
         u32 cw[8];
@@ -448,6 +458,11 @@ struct ActRegs {
     }
   }
 };
+
+// Per-lane dummy LDS area of the early-activation path (64 lanes x one 32-value
+// stage block; a Q8_K stage block fits too).
+constexpr int kDummyBytes = 64 * kStage32;
+static_assert(kDummyBytes >= kStageQ8K, "dummy area holds a Q8_K stage block");
 
 // Makes this wave's LDS writes visible to its own later LDS reads (each wave
 // stages and reads only its own slice, so no workgroup barrier is needed).
@@ -532,6 +547,8 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
   for (int mm = 0; mm < M; ++mm) o.acc[mm] = 0.0f;
   const int b0 = wave * nblk / W, b1 = (wave + 1) * nblk / W;  // this wave's blocks
   uint8_t* st = smem + (kSb ? ((size_t)M * nblk * 65 * 4 + 15) / 16 * 16 : (size_t)W * M * 64 * 4);
+  // bytes of the staged activation rows (the dummy area of the early path follows)
+  const int stage_bytes = kSb ? M * nblk * kStageQ8K : M * nblk * ((WT == kQ4_K || WT == kQ6_K) ? 8 : 1) * kStage32;
 
   // plane buffer resources of this row group (64 rows x nblk blocks)
   const int u0 = plane_unit(WT, 0), u1 = plane_unit(WT, 1);
@@ -585,7 +602,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
         }
       }
     } else {
-      ar.commit(arb, nblk, b0, b1, bpu, r, st);
+      ar.commit(arb, nblk, b0, b1, bpu, r, st, st + stage_bytes);
     }
   } else if constexpr (kFuse) {
     quantize_slice<AF, M>(x, xs, nblk, b0, b1, r, st);
@@ -661,6 +678,7 @@ static hipError_t gemv_launch(const WeightDev& w, const uint8_t* acts, int64_t a
   // staged activations: Q8_K super-blocks of kStageQ8K B, or 32-value blocks of kStage32 B
   lds += AF == kActQ8_K ? (size_t)M * w.nblk * kStageQ8K
                         : (size_t)M * w.nblk * (WT == kQ4_K || WT == kQ6_K ? 8 : 1) * kStage32;
+  if (kEarly > 0) lds += kDummyBytes;
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   const void* fn = reinterpret_cast<const void*>(&k_gemv<WT, AF, M, W, U, kFuse, kEarly>);
   if (lds > 64 * 1024) {
