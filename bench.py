@@ -117,6 +117,64 @@ def cpu_baseline(w_host: np.ndarray, copies: int, budget_s: float) -> dict:
             "sample": f"{rows} of {N} rows of the Q4_K x sub-scaled GEMV (scalar oracle), scaled to N", "cpu": cpu}
 
 
+# Config 5: Qwen2.5-1.5B-shaped decode step, M = 16: per layer (name, dtype, n, k)
+QWEN_LAYER = [("q", 14, 1536, 1536), ("k", 14, 256, 1536), ("v", 16, 256, 1536), ("o", 14, 1536, 1536),
+              ("gate", 14, 8960, 1536), ("up", 14, 8960, 1536), ("down", 16, 1536, 8960)]
+QWEN_LAYERS = 28
+QWEN_LM_HEAD = ("lm_head", 16, 151936, 1536)
+
+
+def random_rows(dtype: int, n: int, k: int, seed: int) -> np.ndarray:
+    """Random valid K-quant blocks (fp16 d, dmin in U(0.002, 0.02))."""
+    nb = k // 256
+    bb = 144 if dtype == 14 else 210
+    rng = np.random.default_rng(seed)
+    rows = rng.integers(0, 256, (n, nb, bb), dtype=np.uint8)
+    dd = rng.uniform(0.002, 0.02, (n, nb, 2)).astype(np.float16).view(np.uint8).reshape(n, nb, 4)
+    if dtype == 14:
+        rows[:, :, 0:4] = dd
+    else:
+        rows[:, :, 208:210] = dd[:, :, 0:2]
+    return rows.reshape(n, -1)
+
+
+def decode_stack(steps: int, stream: int) -> dict:
+    """Config 5: the 28-layer matmul stack plus lm_head of one decode step at M = 16,
+    every matmul through dq_matmul (Q8_K quantization on the GPU, then GEMV passes)."""
+    import torch
+
+    import dynalm_amd as dq
+
+    m = 16
+    uploads = {}
+    for name, t, n, k in QWEN_LAYER + [QWEN_LM_HEAD]:
+        rows = random_rows(t, n, k, sum(map(ord, name)))
+        src = torch.from_numpy(rows).cuda()
+        count = 1 if name == "lm_head" else QWEN_LAYERS
+        uploads[name] = [dq.Weight.upload_device(t, src, n, k, rows.shape[1], stream) for _ in range(count)]
+        del src
+    x = {k: torch.randn((m, k), device="cuda") for k in (1536, 8960)}
+    y = torch.empty((m, 151936), device="cuda")
+    total_bytes = sum(n * (k // 256) * (144 if t == 14 else 210) * (1 if name == "lm_head" else QWEN_LAYERS)
+                      for name, t, n, k in QWEN_LAYER + [QWEN_LM_HEAD])
+
+    def step(_i: int) -> None:
+        for layer in range(QWEN_LAYERS):
+            for name, t, n, k in QWEN_LAYER:
+                dq.matmul(uploads[name][layer], x[k], m, k, y, n, None, stream)
+        _, t, n, k = QWEN_LM_HEAD
+        dq.matmul(uploads["lm_head"][0], x[k], m, k, y, n, None, stream)
+
+    ms = time_launches(step, steps, 2)
+    out = {"workload": "config 5: Qwen2.5-1.5B decode-step matmul stack (28 layers + lm_head), M=16",
+           "ms_per_step": round(ms, 4), "weight_bytes": total_bytes,
+           "gbs": round(total_bytes / (ms * 1e-3) / 1e9, 1), "tokens_per_s": round(m / (ms * 1e-3), 1)}
+    for ws in uploads.values():
+        for w in ws:
+            w.free()
+    return out
+
+
 COPY_BYTES = 64 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_m1_gemm_m512_traffic.md")
 
@@ -174,6 +232,7 @@ def main() -> None:
     ap.add_argument("--gemm-iters", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--stack-steps", type=int, default=20, help="config 5 decode-stack steps (0: skip)")
     ap.add_argument("--pmc-leg", action="store_true",
                     help="no timing: a 64 MiB copy kernel (counter calibration), then a few launches of each "
                          "measured kernel, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
@@ -290,6 +349,9 @@ def main() -> None:
                          "traffic": traffic.get("gemm_m512")},
         },
     }
+    if args.stack_steps > 0:
+        log(f"config 5 decode stack x{args.stack_steps}")
+        result["decode_stack_m16"] = decode_stack(args.stack_steps, stream)
     if not args.no_cpu:
         log("CPU baseline")
         result["cpu_baseline"] = cpu_baseline(w_host, 4, args.cpu_seconds)

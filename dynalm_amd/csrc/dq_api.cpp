@@ -270,6 +270,12 @@ int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
   if (int rc = check_acts(w, fmt, acts, m); rc != DQ_OK) return rc;
   if (int rc = check_out(w, m, n0, n1, y, y_stride); rc != DQ_OK) return rc;
   if (m == 0 || n0 == n1) return DQ_OK;
+  if (dq::gemv_mma_supported(w->dev.dtype, fmt, m)) {
+    DQ_HIP(dq::launch_gemv_mma(w->dev, fmt, static_cast<const uint8_t*>(acts), dq_act_row_bytes(fmt, w->dev.k), m, n0,
+                               n1, y, y_stride, bias, as_stream(stream)),
+           "gemv launch");
+    return DQ_OK;
+  }
   DQ_HIP(dq::launch_gemv(w->dev, fmt, static_cast<const uint8_t*>(acts), dq_act_row_bytes(fmt, w->dev.k), m, n0, n1, y,
                          y_stride, bias, nullptr, as_stream(stream)),
          "gemv launch");
@@ -300,8 +306,15 @@ int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, f
   const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
   if (int rc = check_out(w, m, 0, w->dev.n, y, y_stride); rc != DQ_OK) return rc;
   hipStream_t s = as_stream(stream);
+  if (dq::gemv_mma_supported(w->dev.dtype, fmt, m)) {
+    // decode batch of 2..16 rows: quantize once, then the skinny MFMA GEMV
+    void* acts = nullptr;
+    if (int rc = scratch_get(w->dev.device, (size_t)(m * arb), s, &acts); rc != DQ_OK) return rc;
+    if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, x_stride, acts, stream); rc != DQ_OK) return rc;
+    return dq_gemv(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
+  }
   if (m <= DQ_GEMV_MAX_ROWS || !dq::gemm_supported(w->dev.dtype, fmt)) {
-    // decode: quantization fused into the GEMV (one launch per 4 rows)
+    // decode: quantization fused into the GEMV (one launch per pass of up to 8 rows)
     if (x == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
     if (m > 1 && x_stride < w->dev.k) {
       return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)w->dev.k);

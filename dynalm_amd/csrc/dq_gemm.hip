@@ -298,6 +298,217 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 }
 
+// ====================================================== skinny MFMA GEMV
+// Q4_K x Q8_K for 2..16 activation rows (decode batches): one workgroup per 16
+// weight rows, its W waves splitting the super-blocks. The activation rows are
+// the 16 rows of the MFMA A operand (rows past m read zeros), the 16 weight rows
+// its B columns, with the same sh / sl / m planes as the GEMM. Per super-block
+// each wave turns its exact S, Mn into t = fma(-dmin, Mn, d*S) in LDS; after a
+// barrier each lane chains acc = fma(da, t, acc) over the super-blocks in order
+// for its 4 outputs: the canonical order, so outputs are bit-identical to the
+// GEMV, the GEMM and the CPU oracle. 16 rows per workgroup give N/16 workgroups,
+// enough to fill the GPU for N down to ~1.5K rows at 8 waves.
+template <int W>
+__global__ __launch_bounds__(W * 64) void k_gemv_mma_q4k(const uint8_t* __restrict__ qs_plane,
+                                                         const uint8_t* __restrict__ hdr_plane, int nblk,
+                                                         int64_t n_pad, int64_t f0, int64_t n0, int64_t n1,
+                                                         const uint8_t* __restrict__ acts, int64_t arb, int m,
+                                                         float* __restrict__ y, int64_t ys,
+                                                         const float* __restrict__ bias) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  float* tt = reinterpret_cast<float*>(lds);  // [nblk][16 activation rows][16 weight rows]
+  float* dal = tt + nblk * 256;               // [nblk][16] activation d
+  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = l & 15, lg = l >> 4, hi = lg >> 1;
+  const int64_t n = (f0 + blockIdx.x) * 16 + li;  // this lane's weight row (B column)
+  const int64_t G = n / kRowGroup, r = n % kRowGroup;
+  const bool nok = n < n_pad;
+  const auto rq = rsrc(qs_plane + G * nblk * 8192, nok ? (u32)(nblk * 8192) : 0u);
+  const auto rh = rsrc(hdr_plane + G * nblk * 1024, nok ? (u32)(nblk * 1024) : 0u);
+  const auto ra = rsrc(acts, (u32)(m * arb));  // activation rows past m read zeros
+  const int b0 = wave * nblk / W, b1 = (wave + 1) * nblk / W;
+  const u32 shift = 4u * (u32)hi, flip = hi ? 0x08080808u : 0u;  // high nibbles are stored XOR 8
+
+  for (int b = b0; b < b1; ++b) {
+    // loads: header, the lane's 16 nibble bytes of each K-step, the activation codes
+    const v4u hd = ld16(rh, (u32)((b * 64 + r) * 16));
+    v4u q[4], a[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) q[s] = ld16(rq, (u32)(((b * 8 + 2 * s + (lg & 1)) * 64 + r) * 16));
+#pragma unroll
+    for (int s = 0; s < 4; ++s) a[s] = ld16(ra, (u32)(li * arb + (int64_t)b * 292 + 4 + 64 * s + 16 * lg));
+    const u32 dau = ld4(ra, (u32)(li * arb + (int64_t)b * 292));
+
+    // scales and mins of sub-blocks 2s + hi as bytes s (get_scale_min_k4, quant_formats.h:62-70)
+    const u32 sc_lo = hd.y & 0x3F3F3F3Fu, mn_lo = hd.z & 0x3F3F3F3Fu;
+    const u32 sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+    const u32 mn_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+    const u32 sc = __builtin_amdgcn_perm(sc_hi, sc_lo, sel_subblocks(hi));
+    const u32 KH = (sc >> 3) & 0x07070707u, KL = sc & 0x07070707u;
+    const u32 MN = __builtin_amdgcn_perm(mn_hi, mn_lo, sel_subblocks(hi));
+
+    v4i_t acc[3];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const v4u qb = ((q[s] >> shift) & 0x0F0F0F0Fu) ^ flip;
+      const u32 kh = __builtin_amdgcn_perm(0u, KH, sel_u16x2(s));
+      const u32 kl = __builtin_amdgcn_perm(0u, KL, sel_u16x2(s));
+      const u32 mm4 = __builtin_amdgcn_perm(0u, MN, sel_x4(s));
+      const v4u H = {mul_bytes(qb.x, kh), mul_bytes(qb.y, kh), mul_bytes(qb.z, kh), mul_bytes(qb.w, kh)};
+      const v4u Lo = {mul_bytes(qb.x, kl), mul_bytes(qb.y, kl), mul_bytes(qb.z, kl), mul_bytes(qb.w, kl)};
+      const v4u Mp = {mm4, mm4, mm4, mm4};
+      const v4i_t z = {0, 0, 0, 0};
+      acc[0] = mfma(a[s], H, s == 0 ? z : acc[0]);
+      acc[1] = mfma(a[s], Lo, s == 0 ? z : acc[1]);
+      acc[2] = mfma(a[s], Mp, s == 0 ? z : acc[2]);
+    }
+    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int S = acc[1][e] + (acc[0][e] << 3);
+      float t = d * (float)S;
+      t = fmaf(-dmin, (float)acc[2][e], t);
+      tt[(b * 16 + 4 * lg + e) * 16 + li] = t;
+    }
+    if (lg == 0) dal[b * 16 + li] = as_f(dau);
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // lane l: outputs (activation row 4 lg + e, weight row n), chained over the
+  // super-blocks in order
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int mm = 4 * lg + e;
+    float v = 0.0f;
+    for (int b = 0; b < nblk; ++b) v = fmaf(dal[b * 16 + mm], tt[(b * 16 + mm) * 16 + li], v);
+    if (mm < m && n >= n0 && n < n1) y[mm * ys + n] = bias ? v + bias[n] : v;
+  }
+}
+
+// Q6_K x Q8_K, 2..16 activation rows, same structure. A Q6_K sub-block is 16
+// values with its own signed 8-bit scale; in K-step s (64 values) lane group g of
+// the B operand holds exactly sub-block u = 4s + g. With the unsigned 6-bit codes
+// q (the -32 offset moved into a correction term),
+//   S = sum_u sc_u * P_u - 32 * sum_u sc_u * bsum_u,   P_u = sum over sub-block u of q * a,
+// P_u comes from one MFMA per sub-block whose A operand keeps only lane group u,
+// and sum_u sc_u * bsum_u from one MFMA whose B operand holds sc_u at every position
+// of sub-block u. Q6_K layout: dequantize_q6_K, quant_formats.cpp:192-216.
+template <int W>
+__global__ __launch_bounds__(W * 64) void k_gemv_mma_q6k(const uint8_t* __restrict__ ql_plane,
+                                                         const uint8_t* __restrict__ qh_plane,
+                                                         const uint8_t* __restrict__ sc_plane,
+                                                         const uint8_t* __restrict__ d_plane, int nblk,
+                                                         int64_t n_pad, int64_t f0, int64_t n0, int64_t n1,
+                                                         const uint8_t* __restrict__ acts, int64_t arb, int m,
+                                                         float* __restrict__ y, int64_t ys,
+                                                         const float* __restrict__ bias) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  float* tt = reinterpret_cast<float*>(lds);  // [nblk][16 activation rows][16 weight rows]
+  float* dal = tt + nblk * 256;               // [nblk][16] activation d
+  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = l & 15, lg = l >> 4;
+  const int64_t n = (f0 + blockIdx.x) * 16 + li;
+  const int64_t G = n / kRowGroup, r = n % kRowGroup;
+  const bool nok = n < n_pad;
+  const auto rl = rsrc(ql_plane + G * nblk * 8192, nok ? (u32)(nblk * 8192) : 0u);
+  const auto rh = rsrc(qh_plane + G * nblk * 4096, nok ? (u32)(nblk * 4096) : 0u);
+  const auto rs = rsrc(sc_plane + G * nblk * 1024, nok ? (u32)(nblk * 1024) : 0u);
+  const auto rd = rsrc(d_plane + G * nblk * 128, nok ? (u32)(nblk * 128) : 0u);
+  const auto ra = rsrc(acts, (u32)(m * arb));
+  const int b0 = wave * nblk / W, b1 = (wave + 1) * nblk / W;
+  const v4u zero = {0u, 0u, 0u, 0u};
+
+  for (int b = b0; b < b1; ++b) {
+    // lane (row li, group g): ql chunks g and 4 + g (values of K-steps 0, 1 and 2, 3 in
+    // the low and high nibbles), qh chunks g & 1 and 2 + (g & 1), the 16 scales, d
+    const v4u l0 = ld16(rl, (u32)(((b * 8 + lg) * 64 + r) * 16));
+    const v4u l1 = ld16(rl, (u32)(((b * 8 + 4 + lg) * 64 + r) * 16));
+    const v4u h0 = ld16(rh, (u32)(((b * 4 + (lg & 1)) * 64 + r) * 16));
+    const v4u h1 = ld16(rh, (u32)(((b * 4 + 2 + (lg & 1)) * 64 + r) * 16));
+    const v4u scw = ld16(rs, (u32)((b * 64 + r) * 16));
+    const u32 dw = ld2(rd, (u32)((b * 64 + r) * 2));
+    v4u a[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) a[s] = ld16(ra, (u32)(li * arb + (int64_t)b * 292 + 4 + 64 * s + 16 * lg));
+    const u32 dau = ld4(ra, (u32)(li * arb + (int64_t)b * 292));
+
+    v4i_t S = {0, 0, 0, 0}, C = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      // codes of sub-block 4s + g: quarter 2(s&1) + g/2 of half s/2
+      const v4u lo = (s >> 1) ? l1 : l0, hb = (s >> 1) ? h1 : h0;
+      const u32 qsh = 2u * (u32)(2 * (s & 1) + (lg >> 1));
+      const v4u q = ((lo >> (u32)(4 * (s & 1))) & 0x0F0F0F0Fu) | (((hb >> qsh) & 0x03030303u) << 4);
+      // scales of sub-blocks 4s .. 4s + 3 (signed bytes of scale dword s)
+      const u32 sw = s == 0 ? scw.x : s == 1 ? scw.y : s == 2 ? scw.z : scw.w;
+      const u32 mine = (u32)sbfe(sw, 8 * lg, 8) & 0xFFu;  // this lane group's scale
+      const u32 sc4 = mine * 0x01010101u;
+      const v4i_t z = {0, 0, 0, 0};
+      C = mfma(a[s], v4u{sc4, sc4, sc4, sc4}, C);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const v4u au = lg == u ? a[s] : zero;
+        const v4i_t P = mfma(au, q, z);
+        const int scu = sbfe(sw, 8 * u, 8);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[e] += scu * __builtin_amdgcn_sbfe(P[e], 0, 24);
+      }
+    }
+    const float d = h2f(dw);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tt[(b * 16 + 4 * lg + e) * 16 + li] = d * (float)(S[e] - 32 * C[e]);
+    if (lg == 0) dal[b * 16 + li] = as_f(dau);
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int mm = 4 * lg + e;
+    float v = 0.0f;
+    for (int b = 0; b < nblk; ++b) v = fmaf(dal[b * 16 + mm], tt[(b * 16 + mm) * 16 + li], v);
+    if (mm < m && n >= n0 && n < n1) y[mm * ys + n] = bias ? v + bias[n] : v;
+  }
+}
+
+hipError_t launch_gemv_mma(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0,
+                           int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s) {
+  if (!gemv_mma_supported(w.dtype, af, m)) return hipErrorInvalidValue;
+  if (n1 <= n0) return hipSuccess;
+  const size_t lds = (size_t)w.nblk * (256 + 16) * sizeof(float);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  const int64_t f0 = n0 / 16, f1 = (n1 + 15) / 16;
+  const bool wide = w.nblk >= 8;
+  const bool q6 = w.dtype == kQ6_K;
+  const void* fn = q6 ? (wide ? reinterpret_cast<const void*>(&k_gemv_mma_q6k<8>)
+                              : reinterpret_cast<const void*>(&k_gemv_mma_q6k<4>))
+                      : (wide ? reinterpret_cast<const void*>(&k_gemv_mma_q4k<8>)
+                              : reinterpret_cast<const void*>(&k_gemv_mma_q4k<4>));
+  if (lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  if (q6) {
+    if (wide) {
+      hipLaunchKernelGGL(k_gemv_mma_q6k<8>, dim3((unsigned)(f1 - f0)), dim3(512), lds, s, w.plane[0], w.plane[1],
+                         w.plane[2], w.plane[3], (int)w.nblk, w.n_pad, f0, n0, n1, acts, arb, (int)m, y, ys, bias);
+    } else {
+      hipLaunchKernelGGL(k_gemv_mma_q6k<4>, dim3((unsigned)(f1 - f0)), dim3(256), lds, s, w.plane[0], w.plane[1],
+                         w.plane[2], w.plane[3], (int)w.nblk, w.n_pad, f0, n0, n1, acts, arb, (int)m, y, ys, bias);
+    }
+  } else if (wide) {
+    hipLaunchKernelGGL(k_gemv_mma_q4k<8>, dim3((unsigned)(f1 - f0)), dim3(512), lds, s, w.plane[0], w.plane[1],
+                       (int)w.nblk, w.n_pad, f0, n0, n1, acts, arb, (int)m, y, ys, bias);
+  } else {
+    hipLaunchKernelGGL(k_gemv_mma_q4k<4>, dim3((unsigned)(f1 - f0)), dim3(256), lds, s, w.plane[0], w.plane[1],
+                       (int)w.nblk, w.n_pad, f0, n0, n1, acts, arb, (int)m, y, ys, bias);
+  }
+  return hipGetLastError();
+}
+
+bool gemv_mma_supported(int dtype, int af, int64_t m) {
+  return (dtype == kQ4_K || dtype == kQ6_K) && af == kActQ8_K && m >= 2 && m <= 16;
+}
+
 bool gemm_supported(int dtype, int af) { return dtype == kQ4_K && af == kActQ8_K; }
 
 hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,

@@ -337,48 +337,63 @@ DQ_DEV void compute(const Chunk<kQ4_0, U>& ch, int bb, const uint8_t* st, Out<M>
 template <int AF, int M>
 DQ_DEV void stage_acts(const uint8_t* __restrict__ acts, int64_t arb, int nblk, int b0, int b1, int bpu, int r,
                        uint8_t* st) {
+  // For each block the loads of all M rows go out together, then the stores:
+  // M loads in flight per round trip instead of one.
   const auto ra = rsrc(acts, (u32)(M * arb));
-  for (int mm = 0; mm < M; ++mm) {
-    if (AF == kActQ8_K) {
-      for (int b = b0; b < b1; ++b) {
+  if constexpr (AF == kActQ8_K) {
+    for (int b = b0; b < b1; ++b) {
+      u32 v[M][2];
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) {
         const u32 base = (u32)(mm * arb + (int64_t)b * 292);
-        uint8_t* o = st + (mm * nblk + b) * kStageQ8K;
-        for (int i = r; i < 73; i += 64) {
-          const u32 v = ld4(ra, base + 4 * i);
-          const int at = i == 0 ? 0 : (i <= 64 ? 16 + 4 * (i - 1) : 272 + 4 * (i - 65));
-          *reinterpret_cast<u32*>(o + at) = v;
-          if (i > 64) stage_subsum(o, i - 65, bsum_pair(v));
-        }
+        v[mm][0] = ld4(ra, base + 4 * r);
+        v[mm][1] = ld4(ra, r < 9 ? base + 4 * (64 + r) : (u32)(M * arb));
       }
-    } else {
-      for (int blk = b0 * bpu + r; blk < b1 * bpu; blk += 64) {
-        uint8_t* o = st + (mm * nblk * bpu + blk) * kStage32;
-        if (AF == kActPer32) {
-          const u32 base = (u32)(mm * arb + (int64_t)blk * 40);
-          const v2u ds = ld8(ra, base);
-          const v4u c0 = ld16(ra, base + 8), c1 = ld16(ra, base + 24);
-          *reinterpret_cast<v2u*>(o) = ds;
-          *reinterpret_cast<v4u*>(o + 16) = c0;
-          *reinterpret_cast<v4u*>(o + 32) = c1;
-        } else {  // GGUF Q8_0: fp16 d at 0, codes at 2 (the block is 2-byte aligned)
-          const u32 base = (u32)(mm * arb + (int64_t)blk * 34);
-          const u32 al = base & ~3u, sh = base & 3u;  // sh is 0 or 2
-          u32 w[10];
 #pragma unroll
-          for (int i = 0; i < 10; ++i) w[i] = ld4(ra, al + 4 * i);
-          u32 cw[8];
+      for (int mm = 0; mm < M; ++mm) {
+        uint8_t* o = st + (mm * nblk + b) * kStageQ8K;
+        // dword j of the block: 0 -> d @0, 1..64 -> codes @16, 65..72 -> bsums @272
+        *reinterpret_cast<u32*>(o + (r == 0 ? 0 : 16 + 4 * (r - 1))) = v[mm][0];
+        if (r < 9) *reinterpret_cast<u32*>(o + (r == 0 ? 16 + 4 * 63 : 272 + 4 * (r - 1))) = v[mm][1];
+        if (r >= 1 && r < 9) stage_subsum(o, r - 1, bsum_pair(v[mm][1]));
+      }
+    }
+  } else {
+    constexpr int kG = M < 4 ? M : 4;  // rows per batch of loads
+    for (int blk = b0 * bpu + r; blk < b1 * bpu; blk += 64) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            // codes start at byte sh + 2 of w[]
-            cw[i] = sh == 0 ? __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2) : w[i + 1];
+      for (int m0 = 0; m0 < M; m0 += kG) {
+        u32 w[kG][10];
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+          const int mm = m0 + g < M ? m0 + g : M - 1;
+          const u32 base = AF == kActPer32 ? (u32)(mm * arb + (int64_t)blk * 40)
+                                           : ((u32)(mm * arb + (int64_t)blk * 34) & ~3u);
+#pragma unroll
+          for (int i = 0; i < 10; ++i) w[g][i] = ld4(ra, base + 4 * i);
+        }
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+          const int mm = m0 + g;
+          if (mm >= M) break;
+          uint8_t* o = st + (mm * nblk * bpu + blk) * kStage32;
+          if constexpr (AF == kActPer32) {
+            *reinterpret_cast<v2u*>(o) = v2u{w[g][0], w[g][1]};
+            *reinterpret_cast<v4u*>(o + 16) = v4u{w[g][2], w[g][3], w[g][4], w[g][5]};
+            *reinterpret_cast<v4u*>(o + 32) = v4u{w[g][6], w[g][7], w[g][8], w[g][9]};
+          } else {  // GGUF Q8_0: fp16 d at 0, codes at 2 (the block is 2-byte aligned)
+            const bool sh = (((int64_t)mm * arb + (int64_t)blk * 34) & 3) != 0;
+            u32 cw[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) cw[i] = sh ? w[g][i + 1] : __builtin_amdgcn_alignbyte(w[g][i + 1], w[g][i], 2);
+            const float d = h2f(sh ? (w[g][0] >> 16) : w[g][0]);
+            const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
+            const v4u c0 = {cw[0], cw[1], cw[2], cw[3]}, c1 = {cw[4], cw[5], cw[6], cw[7]};
+            const int sum = sdot16(ones, c1, sdot16(ones, c0, 0));
+            *reinterpret_cast<v2u*>(o) = v2u{as_u(d), (u32)sum};
+            *reinterpret_cast<v4u*>(o + 16) = c0;
+            *reinterpret_cast<v4u*>(o + 32) = c1;
           }
-          const float d = h2f(sh == 0 ? w[0] : (w[0] >> 16));
-          const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
-          const v4u c0 = {cw[0], cw[1], cw[2], cw[3]}, c1 = {cw[4], cw[5], cw[6], cw[7]};
-          const int sum = sdot16(ones, c1, sdot16(ones, c0, 0));
-          *reinterpret_cast<v2u*>(o) = v2u{as_u(d), (u32)sum};
-          *reinterpret_cast<v4u*>(o + 16) = c0;
-          *reinterpret_cast<v4u*>(o + 32) = c1;
         }
       }
     }
@@ -476,17 +491,20 @@ DQ_DEV void wave_lds_sync() {
 // (the fused decode path), with the standalone quantizers' device functions.
 template <int AF, int M>
 DQ_DEV void quantize_slice(const float* __restrict__ x, int64_t xs, int nblk, int b0, int b1, int r, uint8_t* st) {
+  // For each block the fp32 loads of all M rows go out together, then the M
+  // quantizations: M loads in flight per round trip instead of one.
   constexpr bool kSb = AF == kActQ8_K;
-  for (int mm = 0; mm < M; ++mm) {
-    const int64_t kk = (int64_t)nblk * (kSb ? 256 : 32);
-    const auto rx = rsrc(x + mm * xs, (u32)(kk * 4));
-    if (kSb) {
-      for (int b = b0; b < b1; ++b) {
-        float v[4];
-        load4f(rx, (u32)((b * 256 + 4 * r) * 4), v);
+  const int64_t kk = (int64_t)nblk * (kSb ? 256 : 32);
+  if constexpr (kSb) {
+    for (int b = b0; b < b1; ++b) {
+      float v[M][4];
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) load4f(rsrc(x + mm * xs, (u32)(kk * 4)), (u32)((b * 256 + 4 * r) * 4), v[mm]);
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) {
         float d;
         int bsum;
-        const u32 packed = q8k_quant(v, d, bsum);
+        const u32 packed = q8k_quant(v[mm], d, bsum);
         const int s32 = bsum + dpp<kHalfMirror>(bsum);  // the other 4-lane group of the 32-value sub-block
         uint8_t* o = st + (mm * nblk + b) * kStageQ8K;
         *reinterpret_cast<u32*>(o + 16 + 4 * r) = packed;
@@ -494,14 +512,18 @@ DQ_DEV void quantize_slice(const float* __restrict__ x, int64_t xs, int nblk, in
         if ((r & 7) == 0) stage_subsum(o, r >> 3, s32);
         if (r == 0) *reinterpret_cast<float*>(o) = d;
       }
-    } else {
-      for (int bb = b0; bb < b1; bb += 8) {
-        const int blk = bb + (r >> 3);
-        float v[4];
-        load4f(rx, (u32)((blk * 32 + 4 * (r & 7)) * 4), v);
+    }
+  } else {
+    for (int bb = b0; bb < b1; bb += 8) {
+      const int blk = bb + (r >> 3);
+      float v[M][4];
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) load4f(rsrc(x + mm * xs, (u32)(kk * 4)), (u32)((blk * 32 + 4 * (r & 7)) * 4), v[mm]);
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) {
         float d;
         int sum;
-        const u32 packed = per32_quant(v, d, sum);
+        const u32 packed = per32_quant(v[mm], d, sum);
         if (blk < b1) {
           uint8_t* o = st + (mm * nblk + blk) * kStage32;
           *reinterpret_cast<u32*>(o + 16 + 4 * (r & 7)) = packed;
@@ -659,6 +681,19 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
 
 // ================================================================ launchers
 
+// LDS of one GEMV workgroup: Q8_K t-terms [M][nblk][64] + da [M][nblk], or the
+// per-32 slice sums [W][M][64]; the staged activation rows (Q8_K super-blocks of
+// kStageQ8K B, 32-value blocks of kStage32 B); the dummy area of the early path.
+constexpr size_t kGemvMaxLds = 160 * 1024;
+static size_t gemv_lds_bytes(int wt, int af, int m, int waves, int64_t nblk, bool early) {
+  size_t lds = af == kActQ8_K ? ((size_t)m * nblk * 65 * sizeof(float) + 15) / 16 * 16
+                              : (size_t)waves * m * 64 * sizeof(float);
+  lds += af == kActQ8_K ? (size_t)m * nblk * kStageQ8K
+                        : (size_t)m * nblk * (wt == kQ4_K || wt == kQ6_K ? 8 : 1) * kStage32;
+  if (early) lds += kDummyBytes;
+  return lds;
+}
+
 // Waves per workgroup. A workgroup holds one 64-row group; its waves split the
 // row's blocks. When all row groups fit on the GPU at once (one workgroup per
 // CU), 16 waves give each wave less work after its data lands, which shortens
@@ -673,13 +708,8 @@ static hipError_t gemv_launch(const WeightDev& w, const uint8_t* acts, int64_t a
   // wave step, one (or 4) when waves hold fewer blocks
   constexpr int U = (WT == kQ8_0 || WT == kQ4_0) ? (W >= 16 ? 4 : 8) : (W >= 16 ? 1 : 2);
   const int64_t g0 = n0 / kRowGroup, g1 = (n1 + kRowGroup - 1) / kRowGroup;
-  size_t lds = AF == kActQ8_K ? ((size_t)M * w.nblk * 65 * sizeof(float) + 15) / 16 * 16
-                              : (size_t)W * M * 64 * sizeof(float);
-  // staged activations: Q8_K super-blocks of kStageQ8K B, or 32-value blocks of kStage32 B
-  lds += AF == kActQ8_K ? (size_t)M * w.nblk * kStageQ8K
-                        : (size_t)M * w.nblk * (WT == kQ4_K || WT == kQ6_K ? 8 : 1) * kStage32;
-  if (kEarly > 0) lds += kDummyBytes;
-  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  const size_t lds = gemv_lds_bytes(WT, AF, M, W, w.nblk, kEarly > 0);
+  if (lds > kGemvMaxLds) return hipErrorInvalidValue;
   const void* fn = reinterpret_cast<const void*>(&k_gemv<WT, AF, M, W, U, kFuse, kEarly>);
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -722,7 +752,7 @@ static hipError_t gemv_waves(const WeightDev& w, const uint8_t* acts, int64_t ar
   return gemv_early<WT, AF, M, kFuse, 8>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
 }
 
-// M rows (1..4) of one pass; x != nullptr: fused quantization of fp32 rows.
+// M rows (1..4 or 8) of one pass; x != nullptr: fused quantization of fp32 rows.
 template <int M>
 static hipError_t gemv_pass(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
                             int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
@@ -751,11 +781,16 @@ static hipError_t gemv_pass(const WeightDev& w, int af, const uint8_t* acts, int
   }
 }
 
+// Passes of up to 8 activation rows (each pass streams the weights once); 8-row
+// passes when their LDS fits, else 4.
 static hipError_t gemv_rows(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
                             int64_t m, int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
                             hipStream_t s) {
-  for (int64_t r0 = 0; r0 < m; r0 += 4) {
-    const int rows = (int)(m - r0 < 4 ? m - r0 : 4);
+  const int paf = x != nullptr ? (w.dtype == kQ4_K || w.dtype == kQ6_K ? kActQ8_K : kActPer32) : af;
+  const bool can8 = gemv_lds_bytes(w.dtype, paf, 8, 8, w.nblk, false) <= kGemvMaxLds;
+  for (int64_t r0 = 0; r0 < m;) {
+    const int64_t left = m - r0;
+    const int rows = left >= 8 && can8 ? 8 : (int)(left < 4 ? left : 4);
     const uint8_t* a = acts ? acts + r0 * arb : nullptr;
     const float* xx = x ? x + r0 * xs : nullptr;
     float* yy = y + r0 * ys;
@@ -765,9 +800,11 @@ static hipError_t gemv_rows(const WeightDev& w, int af, const uint8_t* acts, int
       case 1: e = gemv_pass<1>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
       case 2: e = gemv_pass<2>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
       case 3: e = gemv_pass<3>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
-      default: e = gemv_pass<4>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
+      case 4: e = gemv_pass<4>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
+      default: e = gemv_pass<8>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
     }
     if (e != hipSuccess) return e;
+    r0 += rows;
   }
   return hipSuccess;
 }

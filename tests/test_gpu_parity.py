@@ -116,7 +116,7 @@ def test_integer_partials_bit_exact(cuda, pair):
 
 
 @pytest.mark.parametrize("pair", PAIRS, ids=pair_id)
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 16])
 def test_gemv_parity(cuda, pair, m):
     """BASELINE-distribution inputs (N(0, 0.02) weights with 1% outliers at 8 sigma,
     N(0, 1) activations): the north-star bar, 1e-4 relative / 1e-5 absolute."""
