@@ -11,8 +11,10 @@ dynalm/benchmarks/bench_decode_matmul.cpp:11-14 rotates layers). `value` is the
 step's algorithmic bytes (packed weights + quantized activations + fp32 output) per
 second. A second leg times the config 4 prefill GEMM (M=512) in int8 TOPS.
 
-Both `roofline` objects use per-kernel durations from HIP events on the launch
-stream over back-to-back launches of that kernel alone. `cpu_baseline` times the
+Both `roofline` objects use per-kernel durations from HIP events around one replay
+of a HIP graph that holds exactly K back-to-back launches of that kernel alone (the
+Python launch loop costs ~5 us per call, close to the kernel itself; its timing is
+reported beside). `cpu_baseline` times the
 kernel dynacore selects on x86 for this call (Q4_K x sub-scaled int8,
 dot_rows_n_sx_q4_K, dynacore/src/kernel/matmul_registry.cpp:139-165) compiled from
 the reference sources (oracle/_ref) on the host cores, on a bounded sample.
@@ -54,19 +56,50 @@ def random_q4k_rows(n: int, k: int, seed: int) -> np.ndarray:
 
 
 def time_launches(fn, iters: int, warmup: int) -> float:
-    """Average ms per call of fn(i) over `iters` back-to-back calls (HIP events on the current stream)."""
+    """Average ms per call of fn(i, stream) over `iters` back-to-back calls issued from
+    Python on the current stream (HIP events on that stream)."""
     import torch
 
+    stream = torch.cuda.current_stream().cuda_stream
     for i in range(warmup):
-        fn(i)
+        fn(i, stream)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for i in range(iters):
-        fn(i)
+        fn(i, stream)
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / iters
+
+
+def time_graph(fn, iters: int, warmup: int) -> float:
+    """Average ms per call of fn(i, stream) over exactly `iters` calls replayed from one
+    HIP graph. The calls are warmed up eagerly first (so that no library scratch is
+    allocated during capture), then captured on a side stream; the timed region is one
+    replay, bracketed by HIP events on the stream that launches it. This removes the
+    Python / ctypes launch cost (a few us per call) from the GPU timeline."""
+    import torch
+
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        for i in range(warmup):
+            fn(i, side.cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        for i in range(iters):
+            fn(i, side.cuda_stream)
+    g.replay()  # untimed: first replay uploads the graph
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    del g
+    return ms
 
 
 def cpu_baseline(w_host: np.ndarray, copies: int, budget_s: float) -> dict:
@@ -140,7 +173,8 @@ def random_rows(dtype: int, n: int, k: int, seed: int) -> np.ndarray:
 
 def decode_stack(steps: int, stream: int) -> dict:
     """Config 5: the 28-layer matmul stack plus lm_head of one decode step at M = 16,
-    every matmul through dq_matmul (Q8_K quantization on the GPU, then GEMV passes)."""
+    every matmul through dq_matmul (Q8_K quantization on the GPU, then the skinny
+    MFMA GEMV), timed as graph replays."""
     import torch
 
     import dynalm_amd as dq
@@ -158,14 +192,14 @@ def decode_stack(steps: int, stream: int) -> dict:
     total_bytes = sum(n * (k // 256) * (144 if t == 14 else 210) * (1 if name == "lm_head" else QWEN_LAYERS)
                       for name, t, n, k in QWEN_LAYER + [QWEN_LM_HEAD])
 
-    def step(_i: int) -> None:
+    def step(_i: int, st: int) -> None:
         for layer in range(QWEN_LAYERS):
             for name, t, n, k in QWEN_LAYER:
-                dq.matmul(uploads[name][layer], x[k], m, k, y, n, None, stream)
+                dq.matmul(uploads[name][layer], x[k], m, k, y, n, None, st)
         _, t, n, k = QWEN_LM_HEAD
-        dq.matmul(uploads["lm_head"][0], x[k], m, k, y, n, None, stream)
+        dq.matmul(uploads["lm_head"][0], x[k], m, k, y, n, None, st)
 
-    ms = time_launches(step, steps, 2)
+    ms = time_graph(step, steps, 2)
     out = {"workload": "config 5: Qwen2.5-1.5B decode-step matmul stack (28 layers + lm_head), M=16",
            "ms_per_step": round(ms, 4), "weight_bytes": total_bytes,
            "gbs": round(total_bytes / (ms * 1e-3) / 1e9, 1), "tokens_per_s": round(m / (ms * 1e-3), 1)}
@@ -265,21 +299,22 @@ def main() -> None:
     y = torch.empty((1, N), dtype=torch.float32, device="cuda")
     nc = args.copies
 
-    def step(i: int) -> None:
-        dq.matmul(weights[i % nc], x, 1, K, y, N, None, stream)
+    def step(i: int, st: int) -> None:
+        dq.matmul(weights[i % nc], x, 1, K, y, N, None, st)
 
-    def gemv_only(i: int) -> None:
-        dq.gemv(weights[i % nc], dq.ACT_Q8_K, acts, 1, 0, N, y, N, None, stream)
+    def gemv_only(i: int, st: int) -> None:
+        dq.gemv(weights[i % nc], dq.ACT_Q8_K, acts, 1, 0, N, y, N, None, st)
 
     if args.pmc_leg:
         pmc_leg(weights, x, acts, y, stream)
         return
 
     log(f"decode step x{args.steps} (warmup {args.warmup})")
-    ms_step = time_launches(step, args.steps, args.warmup)
+    ms_step = time_graph(step, args.steps, args.warmup)
+    ms_step_eager = time_launches(step, args.steps, args.warmup)
     log("GEMV on pre-quantized activations")
     dq.act_quantize(dq.ACT_Q8_K, x, 1, K, K, acts, stream)
-    ms_gemv = time_launches(gemv_only, args.steps, args.warmup)
+    ms_gemv = time_graph(gemv_only, args.steps, args.warmup)
     bytes_step = Q4K_ROW * N + Q8K_ROW + 4 * N
     value = bytes_step / (ms_step * 1e-3) / 1e9
     # the step is one kernel (k_gemv<Q4_K, Q8_K, M=1, fused quantization>): its launch time is ms_step
@@ -293,11 +328,11 @@ def main() -> None:
     yg = torch.empty((m, N), dtype=torch.float32, device="cuda")
     ng = min(4, nc)
 
-    def gemm(i: int) -> None:
-        dq.gemm(weights[i % ng], dq.ACT_Q8_K, ag, m, 0, N, yg, N, None, stream)
+    def gemm(i: int, st: int) -> None:
+        dq.gemm(weights[i % ng], dq.ACT_Q8_K, ag, m, 0, N, yg, N, None, st)
 
     log(f"GEMM M={m} x{args.gemm_iters}")
-    ms_gemm = time_launches(gemm, args.gemm_iters, 3)
+    ms_gemm = time_graph(gemm, args.gemm_iters, 3)
     ops = 2.0 * m * N * K
     tops = ops / (ms_gemm * 1e-3) / 1e12
 
@@ -310,6 +345,10 @@ def main() -> None:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
+        "ms_per_step_python_launches": round(ms_step_eager, 5),
+        "timing": "HIP events around one replay of a HIP graph holding exactly `steps` steps (eager "
+                  "warmup first); ms_per_step_python_launches is the same steps launched one by one "
+                  "from Python",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

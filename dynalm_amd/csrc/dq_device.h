@@ -24,6 +24,17 @@ DQ_DEV __amdgpu_buffer_rsrc_t rsrc(const void* p, u32 bytes) {
 DQ_DEV v4u ld16(__amdgpu_buffer_rsrc_t r, u32 off) {
   return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
+// Streaming loads of weight bytes that a launch reads exactly once: the nt cache
+// policy (bit 1 of the buffer instruction's cache-policy operand on gfx950) marks
+// the lines non-temporal, so the weight stream does not displace reused data
+// (activations, outputs) and is not retained in L2 / MALL after use.
+constexpr int kNonTemporal = 2;
+DQ_DEV v4u ld16nt(__amdgpu_buffer_rsrc_t r, u32 off) {
+  return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNonTemporal));
+}
+DQ_DEV u32 ld2nt(__amdgpu_buffer_rsrc_t r, u32 off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, kNonTemporal);
+}
 DQ_DEV v2u ld8(__amdgpu_buffer_rsrc_t r, u32 off) {
   return __builtin_bit_cast(v2u, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }

@@ -331,10 +331,10 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mma_q4k(const uint8_t* __restri
 
   for (int b = b0; b < b1; ++b) {
     // loads: header, the lane's 16 nibble bytes of each K-step, the activation codes
-    const v4u hd = ld16(rh, (u32)((b * 64 + r) * 16));
+    const v4u hd = ld16nt(rh, (u32)((b * 64 + r) * 16));
     v4u q[4], a[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) q[s] = ld16(rq, (u32)(((b * 8 + 2 * s + (lg & 1)) * 64 + r) * 16));
+    for (int s = 0; s < 4; ++s) q[s] = ld16nt(rq, (u32)(((b * 8 + 2 * s + (lg & 1)) * 64 + r) * 16));
 #pragma unroll
     for (int s = 0; s < 4; ++s) a[s] = ld16(ra, (u32)(li * arb + (int64_t)b * 292 + 4 + 64 * s + 16 * lg));
     const u32 dau = ld4(ra, (u32)(li * arb + (int64_t)b * 292));
@@ -421,12 +421,12 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mma_q6k(const uint8_t* __restri
   for (int b = b0; b < b1; ++b) {
     // lane (row li, group g): ql chunks g and 4 + g (values of K-steps 0, 1 and 2, 3 in
     // the low and high nibbles), qh chunks g & 1 and 2 + (g & 1), the 16 scales, d
-    const v4u l0 = ld16(rl, (u32)(((b * 8 + lg) * 64 + r) * 16));
-    const v4u l1 = ld16(rl, (u32)(((b * 8 + 4 + lg) * 64 + r) * 16));
-    const v4u h0 = ld16(rh, (u32)(((b * 4 + (lg & 1)) * 64 + r) * 16));
-    const v4u h1 = ld16(rh, (u32)(((b * 4 + 2 + (lg & 1)) * 64 + r) * 16));
-    const v4u scw = ld16(rs, (u32)((b * 64 + r) * 16));
-    const u32 dw = ld2(rd, (u32)((b * 64 + r) * 2));
+    const v4u l0 = ld16nt(rl, (u32)(((b * 8 + lg) * 64 + r) * 16));
+    const v4u l1 = ld16nt(rl, (u32)(((b * 8 + 4 + lg) * 64 + r) * 16));
+    const v4u h0 = ld16nt(rh, (u32)(((b * 4 + (lg & 1)) * 64 + r) * 16));
+    const v4u h1 = ld16nt(rh, (u32)(((b * 4 + 2 + (lg & 1)) * 64 + r) * 16));
+    const v4u scw = ld16nt(rs, (u32)((b * 64 + r) * 16));
+    const u32 dw = ld2nt(rd, (u32)((b * 64 + r) * 2));
     v4u a[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) a[s] = ld16(ra, (u32)(li * arb + (int64_t)b * 292 + 4 + 64 * s + 16 * lg));

@@ -78,9 +78,9 @@ struct Chunk<kQ4_K, U> {
     for (int u = 0; u < U; ++u) {
       const int b = bb + u < b1 ? bb + u : nblk;
       // header first: the scales are needed by the first sub-block pair
-      hd[u] = ld16(rs.r1, (u32)((b * 64 + r) * 16));
+      hd[u] = ld16nt(rs.r1, (u32)((b * 64 + r) * 16));
 #pragma unroll
-      for (int c = 0; c < 8; ++c) q[u][c] = ld16(rs.r0, (u32)(((b * 8 + c) * 64 + r) * 16));
+      for (int c = 0; c < 8; ++c) q[u][c] = ld16nt(rs.r0, (u32)(((b * 8 + c) * 64 + r) * 16));
     }
   }
 };
@@ -94,11 +94,11 @@ struct Chunk<kQ6_K, U> {
     for (int u = 0; u < U; ++u) {
       const int b = bb + u < b1 ? bb + u : nblk;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) L[u][c] = ld16(rs.r0, (u32)(((b * 8 + c) * 64 + r) * 16));
+      for (int c = 0; c < 8; ++c) L[u][c] = ld16nt(rs.r0, (u32)(((b * 8 + c) * 64 + r) * 16));
 #pragma unroll
-      for (int c = 0; c < 4; ++c) H[u][c] = ld16(rs.r1, (u32)(((b * 4 + c) * 64 + r) * 16));
-      SC[u] = ld16(rs.r2, (u32)((b * 64 + r) * 16));
-      DW[u] = ld2(rs.r3, (u32)((b * 64 + r) * 2));
+      for (int c = 0; c < 4; ++c) H[u][c] = ld16nt(rs.r1, (u32)(((b * 4 + c) * 64 + r) * 16));
+      SC[u] = ld16nt(rs.r2, (u32)((b * 64 + r) * 16));
+      DW[u] = ld2nt(rs.r3, (u32)((b * 64 + r) * 2));
     }
   }
 };
@@ -113,8 +113,8 @@ struct Chunk32 {  // Q8_0 (2 chunks of 16 B per block) and Q4_0 (1)
     for (int u = 0; u < U; ++u) {
       const int b = bb + u < b1 ? bb + u : nblk;
 #pragma unroll
-      for (int c = 0; c < kC; ++c) q[u][c] = ld16(rs.r0, (u32)(((b * kC + c) * 64 + r) * 16));
-      DW[u] = ld2(rs.r1, (u32)((b * 64 + r) * 2));
+      for (int c = 0; c < kC; ++c) q[u][c] = ld16nt(rs.r0, (u32)(((b * kC + c) * 64 + r) * 16));
+      DW[u] = ld2nt(rs.r1, (u32)((b * 64 + r) * 2));
     }
   }
 };
