@@ -173,8 +173,11 @@ def random_rows(dtype: int, n: int, k: int, seed: int) -> np.ndarray:
 
 def decode_stack(steps: int, stream: int) -> dict:
     """Config 5: the 28-layer matmul stack plus lm_head of one decode step at M = 16,
-    every matmul through dq_matmul (Q8_K quantization on the GPU, then the skinny
-    MFMA GEMV), timed as graph replays."""
+    in the order a transformer step issues it (dynalm/src/model/transformer.cpp:605-718):
+    per layer matmul_many(q, k, v) on the attention input, o, matmul_many(gate, up)
+    on the MLP input, down; then lm_head. Each call quantizes its input to Q8_K on
+    the GPU once and runs the skinny MFMA GEMV (grouped launches for the shared
+    inputs). Timed as one graph replay per `steps` steps."""
     import torch
 
     import dynalm_amd as dq
@@ -187,20 +190,28 @@ def decode_stack(steps: int, stream: int) -> dict:
         count = 1 if name == "lm_head" else QWEN_LAYERS
         uploads[name] = [dq.Weight.upload_device(t, src, n, k, rows.shape[1], stream) for _ in range(count)]
         del src
-    x = {k: torch.randn((m, k), device="cuda") for k in (1536, 8960)}
-    y = torch.empty((m, 151936), device="cuda")
+    xs = {stage: torch.randn((m, k), device="cuda") for stage, k in
+          (("attn", 1536), ("o", 1536), ("mlp", 1536), ("down", 8960))}
+    ys = {name: torch.empty((m, n), device="cuda") for name, _, n, _ in QWEN_LAYER + [QWEN_LM_HEAD]}
     total_bytes = sum(n * (k // 256) * (144 if t == 14 else 210) * (1 if name == "lm_head" else QWEN_LAYERS)
                       for name, t, n, k in QWEN_LAYER + [QWEN_LM_HEAD])
+    shapes = {name: (n, k) for name, _, n, k in QWEN_LAYER + [QWEN_LM_HEAD]}
+
+    def job(name: str, layer: int, stage: str):
+        n, k = shapes[name]
+        return (uploads[name][layer], xs[stage], m, k, ys[name], n, None)
 
     def step(_i: int, st: int) -> None:
         for layer in range(QWEN_LAYERS):
-            for name, t, n, k in QWEN_LAYER:
-                dq.matmul(uploads[name][layer], x[k], m, k, y, n, None, st)
-        _, t, n, k = QWEN_LM_HEAD
-        dq.matmul(uploads["lm_head"][0], x[k], m, k, y, n, None, st)
+            dq.matmul_many([job("q", layer, "attn"), job("k", layer, "attn"), job("v", layer, "attn")], st)
+            dq.matmul(*job("o", layer, "o"), st)
+            dq.matmul_many([job("gate", layer, "mlp"), job("up", layer, "mlp")], st)
+            dq.matmul(*job("down", layer, "down"), st)
+        dq.matmul(*job("lm_head", 0, "o"), st)
 
     ms = time_graph(step, steps, 2)
-    out = {"workload": "config 5: Qwen2.5-1.5B decode-step matmul stack (28 layers + lm_head), M=16",
+    out = {"workload": "config 5: Qwen2.5-1.5B decode-step matmul stack (28 layers + lm_head), M=16; per layer "
+                       "matmul_many(q,k,v), o, matmul_many(gate,up), down",
            "ms_per_step": round(ms, 4), "weight_bytes": total_bytes,
            "gbs": round(total_bytes / (ms * 1e-3) / 1e9, 1), "tokens_per_s": round(m / (ms * 1e-3), 1)}
     for ws in uploads.values():

@@ -16,6 +16,7 @@ dynacore/include/dynacore/device/device.h:89-161):
     gemv(w, fmt, acts, m, n0, n1, ...) qmm::Kernels::gemv / DotQ8RowsNFn
     gemm(w, fmt, acts, m, n0, n1, ...) qmm::Kernels::gemm
     matmul(w, x, m, ...)               Device::matmul
+    matmul_many(jobs)                  Device::matmul_many
 
 Errors raise DqError carrying dynacore's StatusCode value
 (dynacore/include/dynacore/base/status.h:19-32).
@@ -30,7 +31,8 @@ import numpy as np
 __all__ = [
     "Q4_0", "Q8_0", "Q4_K", "Q6_K", "ACT_PER32", "ACT_Q8_0", "ACT_Q8_K", "GEMV_MAX_ROWS",
     "DqError", "lib", "lib_path", "row_bytes", "act_row_bytes", "act_format_for", "Weight",
-    "act_quantize", "gemv", "gemm", "matmul", "partials_count", "debug_partials", "EXPORTS",
+    "act_quantize", "gemv", "gemm", "matmul", "matmul_many", "MatmulJob", "partials_count", "debug_partials",
+    "EXPORTS",
 ]
 
 Q4_0, Q8_0, Q4_K, Q6_K = 6, 10, 14, 16
@@ -70,6 +72,7 @@ EXPORTS = {
     "dq_gemv": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "dq_gemm": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "dq_matmul": (_I, [_P, _P, _I64, _I64, _P, _I64, _P, _P]),
+    "dq_matmul_many": (_I, [_P, _I64, _P]),
     "dq_partials_count": (_I, [_I, _I, _I64, C.POINTER(_I64), C.POINTER(_I64)]),
     "dq_debug_partials": (_I, [_P, _I, _P, _I64, _P, _P, _P]),
 }
@@ -190,6 +193,20 @@ def gemm(w: Weight, fmt: int, acts, m: int, n0: int, n1: int, y, y_stride: int, 
 
 def matmul(w: Weight, x, m: int, x_stride: int, y, y_stride: int, bias=None, stream: int = 0) -> None:
     _check(lib().dq_matmul(w.handle, _ptr(x), m, x_stride, _ptr(y), y_stride, _ptr(bias), stream))
+
+
+class MatmulJob(C.Structure):
+    """dq_matmul_job (include/dynaq.h): one matmul of matmul_many."""
+    _fields_ = [("w", _P), ("x", _P), ("m", _I64), ("x_stride", _I64), ("y", _P), ("y_stride", _I64),
+                ("bias", _P)]
+
+
+def matmul_many(jobs, stream: int = 0) -> None:
+    """jobs: sequence of (w, x, m, x_stride, y, y_stride, bias) tuples (Device::matmul_many)."""
+    arr = (MatmulJob * max(len(jobs), 1))()
+    for i, (w, x, m, xs, y, ys, bias) in enumerate(jobs):
+        arr[i] = MatmulJob(w.handle.value if isinstance(w, Weight) else w, _ptr(x), m, xs, _ptr(y), ys, _ptr(bias))
+    _check(lib().dq_matmul_many(C.cast(arr, _P), len(jobs), stream))
 
 
 def partials_count(dtype: int, fmt: int, k: int) -> tuple[int, int]:

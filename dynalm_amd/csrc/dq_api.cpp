@@ -328,6 +328,94 @@ int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, f
   return dq_gemm(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
 }
 
+int dq_matmul_many(const dq_matmul_job* jobs, int64_t n_jobs, void* stream) {
+  if (n_jobs < 0) return fail(DQ_INVALID_ARGUMENT, "n_jobs must be >= 0");
+  if (n_jobs == 0) return DQ_OK;
+  if (jobs == nullptr) return fail(DQ_INVALID_ARGUMENT, "null jobs");
+  // validation of every job first: nothing is launched for a call that fails
+  for (int64_t i = 0; i < n_jobs; ++i) {
+    const dq_matmul_job& j = jobs[i];
+    if (j.w == nullptr) return fail(DQ_INVALID_ARGUMENT, "job %lld: null weight", (long long)i);
+    if (j.m < 0) return fail(DQ_INVALID_ARGUMENT, "job %lld: m must be >= 0", (long long)i);
+    if (j.w->dev.device != jobs[0].w->dev.device) {
+      return fail(DQ_INVALID_ARGUMENT, "job %lld: weights of one call must be on one device", (long long)i);
+    }
+    if (j.m == 0) continue;
+    if (int rc = check_out(j.w, j.m, 0, j.w->dev.n, j.y, j.y_stride); rc != DQ_OK) return rc;
+    if (j.x == nullptr) return fail(DQ_INVALID_ARGUMENT, "job %lld: null x", (long long)i);
+    if (j.m > 1 && j.x_stride < j.w->dev.k) {
+      return fail(DQ_INVALID_ARGUMENT, "job %lld: x_stride %lld < k %lld", (long long)i, (long long)j.x_stride,
+                  (long long)j.w->dev.k);
+    }
+  }
+  hipStream_t s = as_stream(stream);
+  // the grouped jobs: decode-sized K-quant matmuls (the skinny MFMA GEMV)
+  std::vector<int64_t> grouped, others;
+  for (int64_t i = 0; i < n_jobs; ++i) {
+    const dq_matmul_job& j = jobs[i];
+    if (j.m == 0) continue;
+    const int fmt = dq_act_format_for(j.w->dev.dtype);
+    (dq::gemv_mma_supported(j.w->dev.dtype, fmt, j.m) ? grouped : others).push_back(i);
+  }
+  if (!grouped.empty()) {
+    // one quantized copy per distinct input (x, m, k, x_stride), as CpuDevice shares
+    // one buffer between jobs that read the same activations (cpu_device.cpp:561-599)
+    std::vector<int64_t> src(grouped.size()), off(grouped.size());
+    size_t bytes = 0;
+    for (size_t g = 0; g < grouped.size(); ++g) {
+      const dq_matmul_job& j = jobs[grouped[g]];
+      src[g] = (int64_t)g;
+      for (size_t h = 0; h < g; ++h) {
+        const dq_matmul_job& q = jobs[grouped[h]];
+        if (src[h] == (int64_t)h && q.x == j.x && q.m == j.m && q.w->dev.k == j.w->dev.k &&
+            (j.m == 1 || q.x_stride == j.x_stride)) {
+          src[g] = (int64_t)h;
+          break;
+        }
+      }
+      if (src[g] == (int64_t)g) {
+        off[g] = (int64_t)bytes;
+        bytes += (size_t)(j.m * dq_act_row_bytes(DQ_ACT_Q8_K, j.w->dev.k) + 255) / 256 * 256;
+      } else {
+        off[g] = off[src[g]];
+      }
+    }
+    void* scratch = nullptr;
+    if (int rc = scratch_get(jobs[0].w->dev.device, bytes, s, &scratch); rc != DQ_OK) return rc;
+    uint8_t* base = static_cast<uint8_t*>(scratch);
+    std::vector<dq::GemvJob> gj;
+    for (size_t g = 0; g < grouped.size(); ++g) {
+      const dq_matmul_job& j = jobs[grouped[g]];
+      const int64_t arb = dq_act_row_bytes(DQ_ACT_Q8_K, j.w->dev.k);
+      if (src[g] == (int64_t)g) {
+        if (int rc = dq_act_quantize(DQ_ACT_Q8_K, j.x, j.m, j.w->dev.k, j.x_stride, base + off[g], stream); rc != DQ_OK) {
+          return rc;
+        }
+      }
+      gj.push_back(dq::GemvJob{&j.w->dev, base + off[g], arb, j.m, j.y, j.y_stride, j.bias});
+    }
+    // one grouped launch per k (the jobs of a launch share the super-block count)
+    std::vector<bool> done(gj.size(), false);
+    std::vector<dq::GemvJob> batch;
+    for (size_t g = 0; g < gj.size(); ++g) {
+      if (done[g]) continue;
+      batch.clear();
+      for (size_t h = g; h < gj.size(); ++h) {
+        if (!done[h] && gj[h].w->nblk == gj[g].w->nblk) {
+          batch.push_back(gj[h]);
+          done[h] = true;
+        }
+      }
+      DQ_HIP(dq::launch_gemv_mma_many(batch.data(), (int)batch.size(), s), "grouped gemv launch");
+    }
+  }
+  for (int64_t i : others) {
+    const dq_matmul_job& j = jobs[i];
+    if (int rc = dq_matmul(j.w, j.x, j.m, j.x_stride, j.y, j.y_stride, j.bias, stream); rc != DQ_OK) return rc;
+  }
+  return DQ_OK;
+}
+
 int dq_partials_count(int dtype, int fmt, int64_t k, int64_t* units, int64_t* sb_terms) {
   if (!weight_type_ok(dtype) || !act_fmt_ok(fmt) || !pair_ok(dtype, fmt)) {
     return fail(DQ_UNSUPPORTED, "unsupported pair (%d, %d)", dtype, fmt);

@@ -50,6 +50,10 @@ DQ_DEV u32 as_u(float f) { return __builtin_bit_cast(u32, f); }
 DQ_DEV u32 bfe(u32 v, int off, int w) { return __builtin_amdgcn_ubfe(v, off, w); }
 DQ_DEV int sbfe(u32 v, int off, int w) { return __builtin_amdgcn_sbfe((int)v, off, w); }
 
+// The sum of the pair of int16 values in one dword (two Q8_K bsums: the code sum
+// of one 32-value sub-block).
+DQ_DEV int bsum_pair(u32 v) { return (int)(int16_t)(v & 0xFFFFu) + (int)(int16_t)(v >> 16); }
+
 DQ_DEV int sdot4(u32 a, u32 b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 // sum_i a[i] * b[i] over 16 int8 lanes, added to c.
 DQ_DEV int sdot16(v4u a, v4u b, int c) {

@@ -141,8 +141,6 @@ DQ_DEV void stage_subsum(uint8_t* o, int j, int s) {
   o[312 + j] = (uint8_t)(s & 127);
   if (j & 1) *reinterpret_cast<int32_t*>(o + 320 + 2 * (j - 1)) = s * 128;
 }
-// The sub-block sum of the pair of int16 bsums in one dword.
-DQ_DEV int bsum_pair(u32 v) { return (int)(int16_t)(v & 0xFFFFu) + (int)(int16_t)(v >> 16); }
 
 DQ_DEV v4u lds16(const uint8_t* p) { return *reinterpret_cast<const v4u*>(p); }
 DQ_DEV u32 lds4(const uint8_t* p) { return *reinterpret_cast<const u32*>(p); }

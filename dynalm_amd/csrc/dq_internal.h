@@ -45,5 +45,17 @@ bool gemm_supported(int dtype, int af);
 hipError_t launch_gemv_mma(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0,
                            int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s);
 bool gemv_mma_supported(int dtype, int af, int64_t m);
+// One matmul of a grouped skinny launch: y[r, i] (+ bias) for r < m, i < w->n.
+struct GemvJob {
+  const WeightDev* w;
+  const uint8_t* acts;  // m rows of Q8_K, arb bytes apart
+  int64_t arb, m;
+  float* y;
+  int64_t ys;
+  const float* bias;
+};
+// Grouped skinny MFMA GEMV: jobs of one K (same nblk), Q4_K / Q6_K, 2 <= m <= 16,
+// in launches of up to 8 jobs; hipErrorInvalidValue for any other job.
+hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s);
 
 }  // namespace dq

@@ -56,3 +56,18 @@ def partials(w: dq.Weight, fmt: int, acts: torch.Tensor):
     sb = torch.zeros((m, w.n, max(ns, 1)), dtype=torch.int32, device=acts.device)
     dq.debug_partials(w, fmt, acts, m, units, sb if ns else None, stream())
     return units, sb[:, :, :ns]
+
+
+def matmul_many(jobs) -> list[torch.Tensor]:
+    """jobs: sequence of (w, x[, bias]) with x [m, k] fp32 on the GPU; returns the y of each
+    (one dq_matmul_many call: a shared x is quantized once, decode-sized K-quant jobs of
+    one k run in grouped launches)."""
+    outs, spec = [], []
+    for job in jobs:
+        w, x = job[0], job[1]
+        bias = job[2] if len(job) > 2 else None
+        y = torch.empty((x.shape[0], w.n), dtype=torch.float32, device=x.device)
+        outs.append(y)
+        spec.append((w, x, x.shape[0], x.stride(0), y, y.stride(0), bias))
+    dq.matmul_many(spec, stream())
+    return outs

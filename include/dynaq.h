@@ -140,6 +140,32 @@ DQ_API int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int
 DQ_API int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, float* y, int64_t y_stride,
                      const float* bias, void* stream);
 
+/* One matmul of dq_matmul_many: y = x . w^T (+ bias) for m rows of x (x_stride
+ * floats apart, w's k values each) into y (y_stride floats apart). The fields are
+ * those of dynacore's Device::MatmulJob {x, w, y, bias}
+ * (dynacore/include/dynacore/device/device.h:165-168), with the shapes spelled out. */
+typedef struct dq_matmul_job {
+  const dq_weight* w;
+  const float* x;
+  int64_t m;
+  int64_t x_stride;
+  float* y;
+  int64_t y_stride;
+  const float* bias; /* NULL or w's n floats */
+} dq_matmul_job;
+
+/* Several independent matmuls on one stream, e.g. the projections that share one
+ * input (Q/K/V, gate/up) or the experts of an MoE layer. Jobs with the same x
+ * (pointer, m, k, x_stride) share one quantized copy; the decode-sized K-quant
+ * jobs (2 <= m <= 16) of one k run together in grouped skinny-GEMV launches (up to
+ * 8 jobs each, Q4_K and Q6_K mixed); every other job runs as dq_matmul runs it.
+ * Each job's y is bit-identical to dq_matmul on that job. Uses dq_matmul's
+ * per-device scratch. Replaces Device::matmul_many
+ * (dynacore/include/dynacore/device/device.h:169-171; CpuDevice::matmul_many,
+ * dynacore/cpu/cpu_device.cpp:500-692, which quantizes a shared input once and
+ * runs all jobs' row chunks in one parallel region). */
+DQ_API int dq_matmul_many(const dq_matmul_job* jobs, int64_t n_jobs, void* stream);
+
 /* Exact integer partials of every (activation row r < m, weight row i < n):
  * units[(r * n + i) * U + u] and sb[(r * n + i) * S + s], with U and S from
  * dq_partials_count; the meaning of each is that of the CPU reference's integer

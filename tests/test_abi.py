@@ -21,7 +21,7 @@ def declared_symbols() -> list[str]:
 
 def test_library_exports_every_declared_symbol():
     names = declared_symbols()
-    assert len(names) >= 15
+    assert len(names) >= 16
     lib = dq.lib()
     for n in names:
         assert hasattr(lib, n), n
@@ -82,3 +82,15 @@ def test_invalid_arguments_rejected_before_any_gpu_call():
 
 def test_version():
     assert b"gfx950" in dq.lib().dq_version()
+
+
+def test_matmul_many_validation_without_gpu():
+    """dq_matmul_many rejects a bad call with StatusCode values before any GPU work."""
+    lib = dq.lib()
+    assert lib.dq_matmul_many(None, 0, None) == 0
+    assert lib.dq_matmul_many(None, 1, None) == 1
+    assert lib.dq_matmul_many(None, -1, None) == 1
+    jobs = (dq.MatmulJob * 2)()
+    assert lib.dq_matmul_many(C.cast(jobs, C.c_void_p), 2, None) == 1
+    assert b"null weight" in lib.dq_last_error()
+    assert C.sizeof(dq.MatmulJob) == 56

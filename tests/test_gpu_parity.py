@@ -398,3 +398,46 @@ def test_error_paths(cuda):
     with pytest.raises(dq.DqError) as e:
         dq.gemm(w, dq.ACT_PER32, a, 1, 0, 8, y, 8)
     assert e.value.status == "unsupported"
+
+
+# ------------------------------------------------------------- matmul_many
+
+
+def test_matmul_many_groups_equal_single_matmuls(cuda):
+    """Device::matmul_many semantics (dynacore/include/dynacore/device/device.h:165-171):
+    Q/K/V-style jobs sharing one x (Q4_K, Q4_K, Q6_K; one with bias), a gate/up pair
+    on another x with another k, and jobs that take other paths (m = 1, m = 40) in one
+    call: every y bit-identical to its own dq_matmul and to the oracle."""
+    from dynalm_amd import torch_ops as T
+
+    m, k1, k2 = 16, 1536, 512
+    x1, x2 = activations(m, k1, 80), activations(m, k2, 81)
+    x3, x4 = activations(1, k1, 82), activations(40, k2, 83)
+    specs = [(O.Q4_K, 96, k1, x1), (O.Q4_K, 32, k1, x1), (O.Q6_K, 40, k1, x1),
+             (O.Q4_K, 72, k2, x2), (O.Q6_K, 72, k2, x2), (O.Q4_K, 24, k1, x3), (O.Q4_K, 130, k2, x4)]
+    rows = [gguf_weights(t, n, k, 90 + i, outlier_frac=0.01) for i, (t, n, k, _) in enumerate(specs)]
+    ws = [dq.Weight.upload(t, r, k) for (t, n, k, _), r in zip(specs, rows)]
+    bias = np.linspace(-1, 1, 96, dtype=np.float32)
+    xd = {id(x): dev(x) for (_, _, _, x) in specs}
+    jobs = []
+    for i, ((t, n, k, x), w) in enumerate(zip(specs, ws)):
+        jobs.append((w, xd[id(x)], dev(bias)) if i == 0 else (w, xd[id(x)]))
+    outs = [host(y) for y in T.matmul_many(jobs)]
+    for i, ((t, n, k, x), w, r) in enumerate(zip(specs, ws, rows)):
+        b = bias if i == 0 else None
+        single = host(T.matmul(w, xd[id(x)], bias=dev(b) if b is not None else None))
+        assert np.array_equal(outs[i].view(np.uint32), single.view(np.uint32)), f"job {i} differs from dq_matmul"
+        want = O.matmul(t, O.ACT_Q8_K, r, O.quantize_act(O.ACT_Q8_K, x), k, b)
+        assert np.array_equal(outs[i].view(np.uint32), want.view(np.uint32)), f"job {i} differs from the oracle"
+
+
+def test_matmul_many_rejects_before_launching(cuda):
+    """An invalid job fails the whole call before any launch (outputs untouched)."""
+    k = 512
+    w = dq.Weight.upload(O.Q4_K, gguf_weights(O.Q4_K, 64, k, 5), k)
+    x = dev(activations(4, k, 6))
+    y = torch.full((4, 64), 777.0, device="cuda")
+    with pytest.raises(dq.DqError) as e:
+        dq.matmul_many([(w, x, 4, k, y, 64, None), (w, x, 4, k - 1, y, 64, None)])
+    assert e.value.status == "invalid_argument"
+    assert np.all(host(y) == 777.0)
