@@ -170,6 +170,73 @@ int check_out(const dq_weight* w, int64_t m, int64_t n0, int64_t n1, float* y, i
   return DQ_OK;
 }
 
+// The fused skinny path: K-quant weights, 2 <= m <= 16, LDS for the weight's
+// super-blocks, and fp32 rows addressable with 32-bit offsets.
+bool skinny_fused_ok(const dq_weight* w, const float* x, int64_t m, int64_t x_stride) {
+  if (x == nullptr || !dq::gemv_mma_supported(w->dev.dtype, dq_act_format_for(w->dev.dtype), m)) return false;
+  if (!dq::gemv_mma_lds_ok(w->dev.nblk)) return false;
+  const int64_t xs = m > 1 ? x_stride : w->dev.k;
+  return m * xs * 4 < ((int64_t)1 << 32);
+}
+
+// Runs grouped skinny launches over jobs (decode-sized K-quant matmuls, fp32
+// inputs in GemvJob::x): batches of up to 8 jobs of one k; a batch whose
+// re-quantization work is small quantizes in the kernel, else each distinct input
+// of the batch is quantized once into the per-device scratch first.
+int run_skinny(std::vector<dq::GemvJob>& jobs, int device, hipStream_t s) {
+  std::vector<bool> done(jobs.size(), false);
+  std::vector<dq::GemvJob> batch;
+  for (size_t g = 0; g < jobs.size(); ++g) {
+    if (done[g]) continue;
+    batch.clear();
+    for (size_t h = g; h < jobs.size() && batch.size() < 8; ++h) {
+      if (!done[h] && jobs[h].w->nblk == jobs[g].w->nblk) {
+        batch.push_back(jobs[h]);
+        done[h] = true;
+      }
+    }
+    if (dq::skinny_units(batch.data(), (int)batch.size()) > dq::kSkinnyFuseMaxUnits) {
+      // one Q8_K copy per distinct input (x, m, k, stride), as CpuDevice shares one
+      // buffer between jobs that read the same activations (cpu_device.cpp:561-599)
+      const int64_t arb = dq_act_row_bytes(DQ_ACT_Q8_K, batch[0].w->k);
+      std::vector<size_t> off(batch.size());
+      std::vector<int64_t> src(batch.size());
+      size_t bytes = 0;
+      for (size_t i = 0; i < batch.size(); ++i) {
+        src[i] = (int64_t)i;
+        for (size_t h = 0; h < i; ++h) {
+          if (src[h] == (int64_t)h && batch[h].x == batch[i].x && batch[h].m == batch[i].m &&
+              batch[h].xs == batch[i].xs) {
+            src[i] = (int64_t)h;
+            break;
+          }
+        }
+        if (src[i] == (int64_t)i) {
+          off[i] = bytes;
+          bytes += (size_t)(batch[i].m * arb + 255) / 256 * 256;
+        } else {
+          off[i] = off[src[i]];
+        }
+      }
+      void* scratch = nullptr;
+      if (int rc = scratch_get(device, bytes, s, &scratch); rc != DQ_OK) return rc;
+      uint8_t* base = static_cast<uint8_t*>(scratch);
+      for (size_t i = 0; i < batch.size(); ++i) {
+        dq::GemvJob& j = batch[i];
+        if (src[i] == (int64_t)i) {
+          DQ_HIP(dq::launch_quantize(DQ_ACT_Q8_K, j.x, j.m, j.w->k, j.xs, base + off[i], arb, s), "quantize launch");
+        }
+        j.acts = base + off[i];
+        j.arb = arb;
+        j.x = nullptr;
+        j.xs = 0;
+      }
+    }
+    DQ_HIP(dq::launch_gemv_mma_many(batch.data(), (int)batch.size(), s), "grouped gemv launch");
+  }
+  return DQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -270,7 +337,7 @@ int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
   if (int rc = check_acts(w, fmt, acts, m); rc != DQ_OK) return rc;
   if (int rc = check_out(w, m, n0, n1, y, y_stride); rc != DQ_OK) return rc;
   if (m == 0 || n0 == n1) return DQ_OK;
-  if (dq::gemv_mma_supported(w->dev.dtype, fmt, m)) {
+  if (dq::gemv_mma_supported(w->dev.dtype, fmt, m) && dq::gemv_mma_lds_ok(w->dev.nblk)) {
     DQ_HIP(dq::launch_gemv_mma(w->dev, fmt, static_cast<const uint8_t*>(acts), dq_act_row_bytes(fmt, w->dev.k), m, n0,
                                n1, y, y_stride, bias, as_stream(stream)),
            "gemv launch");
@@ -306,8 +373,14 @@ int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, f
   const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
   if (int rc = check_out(w, m, 0, w->dev.n, y, y_stride); rc != DQ_OK) return rc;
   hipStream_t s = as_stream(stream);
+  if (skinny_fused_ok(w, x, m, x_stride)) {
+    // decode batch of 2..16 rows: the skinny MFMA GEMV (quantizing the fp32 rows in
+    // the kernel when that is cheap, else after one quantize launch)
+    std::vector<dq::GemvJob> j{dq::GemvJob{&w->dev, nullptr, 0, x, m > 1 ? x_stride : w->dev.k, m, y, y_stride, bias}};
+    return run_skinny(j, w->dev.device, s);
+  }
   if (dq::gemv_mma_supported(w->dev.dtype, fmt, m)) {
-    // decode batch of 2..16 rows: quantize once, then the skinny MFMA GEMV
+    // the same on pre-quantized rows (inputs whose offsets exceed 32 bits)
     void* acts = nullptr;
     if (int rc = scratch_get(w->dev.device, (size_t)(m * arb), s, &acts); rc != DQ_OK) return rc;
     if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, x_stride, acts, stream); rc != DQ_OK) return rc;
@@ -349,66 +422,21 @@ int dq_matmul_many(const dq_matmul_job* jobs, int64_t n_jobs, void* stream) {
     }
   }
   hipStream_t s = as_stream(stream);
-  // the grouped jobs: decode-sized K-quant matmuls (the skinny MFMA GEMV)
-  std::vector<int64_t> grouped, others;
+  // the grouped jobs: decode-sized K-quant matmuls (the skinny MFMA GEMV, which
+  // quantizes each job's fp32 rows itself); one launch per k for up to 8 jobs
+  std::vector<dq::GemvJob> grouped;
+  std::vector<int64_t> others;
   for (int64_t i = 0; i < n_jobs; ++i) {
     const dq_matmul_job& j = jobs[i];
     if (j.m == 0) continue;
-    const int fmt = dq_act_format_for(j.w->dev.dtype);
-    (dq::gemv_mma_supported(j.w->dev.dtype, fmt, j.m) ? grouped : others).push_back(i);
-  }
-  if (!grouped.empty()) {
-    // one quantized copy per distinct input (x, m, k, x_stride), as CpuDevice shares
-    // one buffer between jobs that read the same activations (cpu_device.cpp:561-599)
-    std::vector<int64_t> src(grouped.size()), off(grouped.size());
-    size_t bytes = 0;
-    for (size_t g = 0; g < grouped.size(); ++g) {
-      const dq_matmul_job& j = jobs[grouped[g]];
-      src[g] = (int64_t)g;
-      for (size_t h = 0; h < g; ++h) {
-        const dq_matmul_job& q = jobs[grouped[h]];
-        if (src[h] == (int64_t)h && q.x == j.x && q.m == j.m && q.w->dev.k == j.w->dev.k &&
-            (j.m == 1 || q.x_stride == j.x_stride)) {
-          src[g] = (int64_t)h;
-          break;
-        }
-      }
-      if (src[g] == (int64_t)g) {
-        off[g] = (int64_t)bytes;
-        bytes += (size_t)(j.m * dq_act_row_bytes(DQ_ACT_Q8_K, j.w->dev.k) + 255) / 256 * 256;
-      } else {
-        off[g] = off[src[g]];
-      }
-    }
-    void* scratch = nullptr;
-    if (int rc = scratch_get(jobs[0].w->dev.device, bytes, s, &scratch); rc != DQ_OK) return rc;
-    uint8_t* base = static_cast<uint8_t*>(scratch);
-    std::vector<dq::GemvJob> gj;
-    for (size_t g = 0; g < grouped.size(); ++g) {
-      const dq_matmul_job& j = jobs[grouped[g]];
-      const int64_t arb = dq_act_row_bytes(DQ_ACT_Q8_K, j.w->dev.k);
-      if (src[g] == (int64_t)g) {
-        if (int rc = dq_act_quantize(DQ_ACT_Q8_K, j.x, j.m, j.w->dev.k, j.x_stride, base + off[g], stream); rc != DQ_OK) {
-          return rc;
-        }
-      }
-      gj.push_back(dq::GemvJob{&j.w->dev, base + off[g], arb, j.m, j.y, j.y_stride, j.bias});
-    }
-    // one grouped launch per k (the jobs of a launch share the super-block count)
-    std::vector<bool> done(gj.size(), false);
-    std::vector<dq::GemvJob> batch;
-    for (size_t g = 0; g < gj.size(); ++g) {
-      if (done[g]) continue;
-      batch.clear();
-      for (size_t h = g; h < gj.size(); ++h) {
-        if (!done[h] && gj[h].w->nblk == gj[g].w->nblk) {
-          batch.push_back(gj[h]);
-          done[h] = true;
-        }
-      }
-      DQ_HIP(dq::launch_gemv_mma_many(batch.data(), (int)batch.size(), s), "grouped gemv launch");
+    if (skinny_fused_ok(j.w, j.x, j.m, j.x_stride)) {
+      grouped.push_back(dq::GemvJob{&j.w->dev, nullptr, 0, j.x, j.m > 1 ? j.x_stride : j.w->dev.k, j.m, j.y,
+                                    j.y_stride, j.bias});
+    } else {
+      others.push_back(i);
     }
   }
+  if (int rc = run_skinny(grouped, jobs[0].w->dev.device, s); rc != DQ_OK) return rc;
   for (int64_t i : others) {
     const dq_matmul_job& j = jobs[i];
     if (int rc = dq_matmul(j.w, j.x, j.m, j.x_stride, j.y, j.y_stride, j.bias, stream); rc != DQ_OK) return rc;

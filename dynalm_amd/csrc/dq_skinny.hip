@@ -1,0 +1,488 @@
+// dq_skinny.hip -- the decode-batch GEMV for gfx950: Q4_K / Q6_K weights x Q8_K
+// activations for 2..16 activation rows, on int8 MFMA (v_mfma_i32_16x16x64_i8), and
+// its grouped launches (one launch for several matmuls, dq_matmul_many).
+//
+// Arithmetic contract per super-block b (256 values), activation row mm, weight row n:
+//   Q4_K: S = sum_j sc_j P_j, Mn = sum_j m_j (code sum of sub-block j),
+//         t = fma(-dmin, (float)Mn, d * (float)S)      (kernels_avx2.cpp:976-1014)
+//   Q6_K: S = sum_u sc_u P_u over 16-value sub-blocks with codes q - 32,
+//         t = d * (float)S                              (kernels_avx2.cpp:1016-1058)
+// and y = the chain acc = fma(da_b, t_b, acc) over b in order: the library's
+// canonical fp32 order, so outputs are bit-identical to the M = 1 GEMV, the GEMM
+// and the CPU oracle.
+//
+// MFMA mapping: the 16 activation rows are the rows of the A operand (rows past m
+// read zeros), 16 weight rows the columns of B. Q4_K: the effective weight sc*q
+// (0..945) does not fit int8, so sc = 8 sh + sl and the B operands are sh*q and
+// sl*q (bytes <= 105, one packed 16-bit multiply per 4 nibbles); a third operand
+// holds m_j at every position of sub-block j, so its MFMA sum is exactly Mn.
+// Q6_K: in K-step s lane group g of B holds sub-block 4s + g; one MFMA per
+// sub-block with the A operand masked to that lane group gives P_u, and one with
+// sc_u at every position of sub-block u gives the -32 correction
+// (dequantize_q6_K layout, quant_formats.cpp:192-216).
+//
+// Workgroup: 8 waves over 16 * CT weight rows (CT MFMA column tiles) and all
+// super-blocks, wave w taking a contiguous slice of super-blocks. CT = 4 (a whole
+// 64-row group) reads each activation super-block once per 64 weight rows instead
+// of once per 16 (for launches with many workgroups); CT = 1 gives 4x the
+// workgroups for small matmuls and prefetches the next super-block's weights while
+// it computes the current one. Per super-block each wave writes its t-terms to
+// LDS; after one barrier all waves share the in-order chains of the 16 x 16 CT
+// outputs.
+//
+// kFused: the activations arrive as fp32 rows and each wave quantizes the 16 rows
+// of its super-block itself (d = amax / 127, codes round half to even at 1 / d:
+// dynacore/cpu/avx2/kernels_avx2.cpp:638-644), with the standalone quantizer's code
+// routine (codes4_rne, dq_quant.h) and an order-independent amax, so the codes are
+// the bytes k_quant_q8k writes. One launch then does what a quantize launch plus a
+// GEMV launch do.
+//
+// Grouping: the grid is the concatenation of the jobs' workgroup ranges; each
+// workgroup finds its job in a table passed by value, and Q4_K and Q6_K jobs mix
+// in one launch (as dynacore's Device::matmul_many runs every job's row chunks in
+// one parallel region, dynacore/cpu/cpu_device.cpp:500-692).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dq_device.h"
+#include "dq_internal.h"
+#include "dq_mfma.h"
+#include "dq_quant.h"
+
+namespace dq {
+
+namespace {
+
+struct SkinnyJob {
+  const uint8_t* p0;  // weight planes (dq_layout.h)
+  const uint8_t* p1;
+  const uint8_t* p2;
+  const uint8_t* p3;
+  int64_t n_pad, t0, n0, n1;  // rows (padded to 64), first tile, output row range
+  const uint8_t* acts;        // !kFused: m rows of Q8_K, arb bytes apart
+  int64_t arb;
+  const float* x;  // kFused: m rows of fp32, xs floats apart
+  int64_t xs;
+  float* y;
+  int64_t ys;
+  const float* bias;
+  int dtype, m;
+  int wg0;  // first workgroup of this job in the grid
+};
+constexpr int kSkinnyMaxJobs = 8;
+struct SkinnyGroup {
+  SkinnyJob job[kSkinnyMaxJobs];
+  int count;
+  int nblk;  // super-blocks per row, the same for every job of a group
+};
+
+constexpr int kSkinnyWaves = 8;
+
+// The activation operand of one super-block: lane (li, lg) holds the codes of
+// activation row li at values 64 s + 16 lg .. + 15 (K-step s), and row li's d.
+struct ActSB {
+  v4u a[4];
+  float da;
+};
+
+// fp32 values of one super-block for the fused path: x[li][64 s + 16 lg + 4 c + i].
+struct XSB {
+  v4u v[4][4];
+};
+
+template <bool kFused>
+struct ActSrc {
+  __amdgpu_buffer_rsrc_t r;
+  int64_t stride;  // bytes between rows
+  DQ_DEV void init(const SkinnyJob& J) {
+    if (kFused) {
+      r = rsrc(J.x, (u32)(J.m * J.xs * 4));
+      stride = J.xs * 4;
+    } else {
+      r = rsrc(J.acts, (u32)(J.m * J.arb));
+      stride = J.arb;
+    }
+  }
+};
+
+DQ_DEV void load_x(const ActSrc<true>& src, int b, int li, int lg, XSB& o) {
+  const u32 base = (u32)(li * src.stride + ((int64_t)b * 256 + 16 * lg) * 4);
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o.v[s][c] = ld16(src.r, base + (u32)((64 * s + 4 * c) * 4));
+}
+
+// Q8_K quantization of row li's super-block from the 64 values of each of the 4
+// lanes (li, 0..3): amax across them, d = amax / 127, codes RNE at 1 / d.
+DQ_DEV void quant_x(const XSB& x, ActSB& o) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(as_f(x.v[s][c].x)), fabsf(as_f(x.v[s][c].y))),
+                               fmaxf(fabsf(as_f(x.v[s][c].z)), fabsf(as_f(x.v[s][c].w)))));
+    }
+  amax = fmaxf(amax, __shfl_xor(amax, 16));
+  amax = fmaxf(amax, __shfl_xor(amax, 32));
+  const float d = amax / 127.0f;
+  const float id = d > 0 ? 1.0f / d : 0.0f;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    u32 w[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float v[4] = {as_f(x.v[s][c].x), as_f(x.v[s][c].y), as_f(x.v[s][c].z), as_f(x.v[s][c].w)};
+      int unused = 0;
+      w[c] = codes4_rne(v, id, unused);
+    }
+    o.a[s] = v4u{w[0], w[1], w[2], w[3]};
+  }
+  o.da = d;
+}
+
+DQ_DEV void load_codes(const ActSrc<false>& src, int b, int li, int lg, ActSB& o) {
+  const u32 base = (u32)(li * src.stride + (int64_t)b * 292);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) o.a[s] = ld16(src.r, base + 4 + 64 * s + 16 * lg);
+  o.da = as_f(ld4(src.r, base));
+}
+
+// ---- weights of one super-block for CT column tiles (row r0 + 16 ct + li of row group G)
+template <int WT, int CT>
+struct WSB;
+
+template <int CT>
+struct WSB<kQ4_K, CT> {
+  v4u hd[CT], q[CT][4];
+  DQ_DEV void load(const __amdgpu_buffer_rsrc_t& rq, const __amdgpu_buffer_rsrc_t& rh, int b, int r0, int li,
+                   int lg) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int r = r0 + 16 * ct + li;
+      hd[ct] = ld16nt(rh, (u32)((b * 64 + r) * 16));
+#pragma unroll
+      for (int s = 0; s < 4; ++s) q[ct][s] = ld16nt(rq, (u32)(((b * 8 + 2 * s + (lg & 1)) * 64 + r) * 16));
+    }
+  }
+};
+
+template <int CT>
+struct WSB<kQ6_K, CT> {
+  v4u l0[CT], l1[CT], h0[CT], h1[CT], sc[CT];
+  u32 dw[CT];
+  DQ_DEV void load(const __amdgpu_buffer_rsrc_t* rp, int b, int r0, int li, int lg) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int r = r0 + 16 * ct + li;
+      // lane (row, group g): ql chunks g and 4 + g (values of K-steps 0, 1 and 2, 3 in
+      // the low and high nibbles), qh chunks g & 1 and 2 + (g & 1), the 16 scales, d
+      l0[ct] = ld16nt(rp[0], (u32)(((b * 8 + lg) * 64 + r) * 16));
+      l1[ct] = ld16nt(rp[0], (u32)(((b * 8 + 4 + lg) * 64 + r) * 16));
+      h0[ct] = ld16nt(rp[1], (u32)(((b * 4 + (lg & 1)) * 64 + r) * 16));
+      h1[ct] = ld16nt(rp[1], (u32)(((b * 4 + 2 + (lg & 1)) * 64 + r) * 16));
+      sc[ct] = ld16nt(rp[2], (u32)((b * 64 + r) * 16));
+      dw[ct] = ld2nt(rp[3], (u32)((b * 64 + r) * 2));
+    }
+  }
+};
+
+// t-terms of column tile ct for one super-block (the 4 outputs of this lane:
+// activation rows 4 lg + e, weight row 16 ct + li of the tile).
+template <int CT>
+DQ_DEV void tterms(const WSB<kQ4_K, CT>& w, int ct, const ActSB& A, int lg, float t[4]) {
+  const int hi = lg >> 1;
+  const u32 shift = 4u * (u32)hi, flip = hi ? 0x08080808u : 0u;  // high nibbles are stored XOR 8
+  const v4u hd = w.hd[ct];
+  // scales and mins of sub-blocks 2s + hi as bytes s (get_scale_min_k4, quant_formats.h:62-70)
+  const u32 sc_lo = hd.y & 0x3F3F3F3Fu, mn_lo = hd.z & 0x3F3F3F3Fu;
+  const u32 sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+  const u32 mn_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+  const u32 sc = __builtin_amdgcn_perm(sc_hi, sc_lo, sel_subblocks(hi));
+  const u32 KH = (sc >> 3) & 0x07070707u, KL = sc & 0x07070707u;
+  const u32 MN = __builtin_amdgcn_perm(mn_hi, mn_lo, sel_subblocks(hi));
+  v4i_t acc[3];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const v4u qb = ((w.q[ct][s] >> shift) & 0x0F0F0F0Fu) ^ flip;
+    const u32 kh = __builtin_amdgcn_perm(0u, KH, sel_u16x2(s));
+    const u32 kl = __builtin_amdgcn_perm(0u, KL, sel_u16x2(s));
+    const u32 mm4 = __builtin_amdgcn_perm(0u, MN, sel_x4(s));
+    const v4u H = {mul_bytes(qb.x, kh), mul_bytes(qb.y, kh), mul_bytes(qb.z, kh), mul_bytes(qb.w, kh)};
+    const v4u Lo = {mul_bytes(qb.x, kl), mul_bytes(qb.y, kl), mul_bytes(qb.z, kl), mul_bytes(qb.w, kl)};
+    const v4u Mp = {mm4, mm4, mm4, mm4};
+    const v4i_t z = {0, 0, 0, 0};
+    acc[0] = mfma(A.a[s], H, s == 0 ? z : acc[0]);
+    acc[1] = mfma(A.a[s], Lo, s == 0 ? z : acc[1]);
+    acc[2] = mfma(A.a[s], Mp, s == 0 ? z : acc[2]);
+  }
+  const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int S = acc[1][e] + (acc[0][e] << 3);
+    const float u = d * (float)S;
+    t[e] = fmaf(-dmin, (float)acc[2][e], u);
+  }
+}
+
+template <int CT>
+DQ_DEV void tterms(const WSB<kQ6_K, CT>& w, int ct, const ActSB& A, int lg, float t[4]) {
+  const v4u zero = {0u, 0u, 0u, 0u};
+  v4i_t S = {0, 0, 0, 0}, C = {0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    // codes of sub-block 4s + g: quarter 2(s&1) + g/2 of half s/2
+    const v4u lo = (s >> 1) ? w.l1[ct] : w.l0[ct], hb = (s >> 1) ? w.h1[ct] : w.h0[ct];
+    const u32 qsh = 2u * (u32)(2 * (s & 1) + (lg >> 1));
+    const v4u q = ((lo >> (u32)(4 * (s & 1))) & 0x0F0F0F0Fu) | (((hb >> qsh) & 0x03030303u) << 4);
+    // scales of sub-blocks 4s .. 4s + 3 (signed bytes of scale dword s)
+    const u32 sw = s == 0 ? w.sc[ct].x : s == 1 ? w.sc[ct].y : s == 2 ? w.sc[ct].z : w.sc[ct].w;
+    const u32 mine = (u32)sbfe(sw, 8 * lg, 8) & 0xFFu;  // this lane group's scale
+    const u32 sc4 = mine * 0x01010101u;
+    const v4i_t z = {0, 0, 0, 0};
+    C = mfma(A.a[s], v4u{sc4, sc4, sc4, sc4}, C);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const v4u au = lg == u ? A.a[s] : zero;
+      const v4i_t P = mfma(au, q, z);
+      const int scu = sbfe(sw, 8 * u, 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S[e] += scu * __builtin_amdgcn_sbfe(P[e], 0, 24);
+    }
+  }
+  const float d = h2f(w.dw[ct]);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) t[e] = d * (float)(S[e] - 32 * C[e]);
+}
+
+template <int WT, int CT>
+struct WRes;
+template <int CT>
+struct WRes<kQ4_K, CT> {
+  __amdgpu_buffer_rsrc_t rq, rh;
+  DQ_DEV void init(const SkinnyJob& J, int64_t G, int nblk, bool ok) {
+    rq = rsrc(J.p0 + G * nblk * 8192, ok ? (u32)(nblk * 8192) : 0u);
+    rh = rsrc(J.p1 + G * nblk * 1024, ok ? (u32)(nblk * 1024) : 0u);
+  }
+  DQ_DEV void load(WSB<kQ4_K, CT>& w, int b, int r0, int li, int lg) const { w.load(rq, rh, b, r0, li, lg); }
+};
+template <int CT>
+struct WRes<kQ6_K, CT> {
+  __amdgpu_buffer_rsrc_t rp[4];
+  DQ_DEV void init(const SkinnyJob& J, int64_t G, int nblk, bool ok) {
+    rp[0] = rsrc(J.p0 + G * nblk * 8192, ok ? (u32)(nblk * 8192) : 0u);
+    rp[1] = rsrc(J.p1 + G * nblk * 4096, ok ? (u32)(nblk * 4096) : 0u);
+    rp[2] = rsrc(J.p2 + G * nblk * 1024, ok ? (u32)(nblk * 1024) : 0u);
+    rp[3] = rsrc(J.p3 + G * nblk * 128, ok ? (u32)(nblk * 128) : 0u);
+  }
+  DQ_DEV void load(WSB<kQ6_K, CT>& w, int b, int r0, int li, int lg) const { w.load(rp, b, r0, li, lg); }
+};
+
+// One wave's super-blocks [b0, b1) of one job: activations, weights, t-terms to LDS.
+// CT == 1 keeps the next super-block's weight loads in flight during the compute
+// (activation loads of b are issued before the weight loads of b + 1, so waiting
+// for them does not wait for the prefetch: loads retire in order).
+template <int WT, int CT, bool kFused>
+DQ_DEV void skinny_wave(const SkinnyJob& J, int nblk, int64_t G, int r0, bool ok, int b0, int b1, float* tt,
+                        float* dal, int li, int lg) {
+  constexpr int NC = 16 * CT;
+  WRes<WT, CT> res;
+  res.init(J, G, nblk, ok);
+  ActSrc<kFused> src;
+  src.init(J);
+  auto emit = [&](const WSB<WT, CT>& w, const ActSB& A, int b) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      float t[4];
+      tterms<CT>(w, ct, A, lg, t);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tt[(b * 16 + 4 * lg + e) * NC + 16 * ct + li] = t[e];
+    }
+    if (lg == 0) dal[b * 16 + li] = A.da;
+  };
+  auto act = [&](int b, ActSB& A) {
+    if constexpr (kFused) {
+      XSB x;
+      load_x(src, b, li, lg, x);
+      quant_x(x, A);
+    } else {
+      load_codes(src, b, li, lg, A);
+    }
+  };
+  if (b0 >= b1) return;
+  if constexpr (CT == 1) {
+    WSB<WT, CT> cur;
+    res.load(cur, b0, r0, li, lg);
+    for (int b = b0; b < b1; ++b) {
+      ActSB A;
+      act(b, A);
+      WSB<WT, CT> nxt;
+      res.load(nxt, b + 1 < b1 ? b + 1 : b, r0, li, lg);
+      emit(cur, A, b);
+      cur = nxt;
+    }
+  } else {
+    // CT == 4: the weight loads of all tiles first (the longer latency), then the
+    // activations (L2-resident), which keeps the fp32 values out of the weights'
+    // live range
+    for (int b = b0; b < b1; ++b) {
+      WSB<WT, CT> w;
+      res.load(w, b, r0, li, lg);
+      __builtin_amdgcn_sched_barrier(0);
+      ActSB A;
+      act(b, A);
+      emit(w, A, b);
+    }
+  }
+}
+
+template <int CT, bool kFused>
+__global__ __launch_bounds__(kSkinnyWaves * 64) void k_skinny(SkinnyGroup g) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int W = kSkinnyWaves;
+  constexpr int NC = 16 * CT;
+  const int wg = blockIdx.x;
+  int j = 0;
+  while (j + 1 < g.count && wg >= g.job[j + 1].wg0) ++j;
+  const SkinnyJob& J = g.job[j];
+  const int nblk = g.nblk;
+  float* tt = reinterpret_cast<float*>(lds);  // [nblk][16 activation rows][NC weight rows]
+  float* dal = tt + nblk * 16 * NC;           // [nblk][16] activation d
+  const int l = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = l & 15, lg = l >> 4;
+  const int64_t row0 = (J.t0 + (wg - J.wg0)) * NC;  // first weight row of the tile
+  const int64_t G = row0 / kRowGroup;
+  const int r0 = (int)(row0 % kRowGroup);
+  const bool ok = row0 < J.n_pad;
+  const int b0 = wave * nblk / W, b1 = (wave + 1) * nblk / W;
+  if (J.dtype == kQ6_K) {
+    skinny_wave<kQ6_K, CT, kFused>(J, nblk, G, r0, ok, b0, b1, tt, dal, li, lg);
+  } else {
+    skinny_wave<kQ4_K, CT, kFused>(J, nblk, G, r0, ok, b0, b1, tt, dal, li, lg);
+  }
+  __syncthreads();
+  // the in-order chains of the tile's 16 x NC outputs, shared by all waves
+  for (int o = threadIdx.x; o < 16 * NC; o += W * 64) {
+    const int mm = o / NC, c = o % NC;
+    float v = 0.0f;
+    for (int b = 0; b < nblk; ++b) v = fmaf(dal[b * 16 + mm], tt[(b * 16 + mm) * NC + c], v);
+    const int64_t n = row0 + c;
+    if (mm < J.m && n >= J.n0 && n < J.n1) J.y[mm * J.ys + n] = J.bias ? v + J.bias[n] : v;
+  }
+}
+
+size_t skinny_lds(int64_t nblk, int ct) { return (size_t)nblk * (16 * 16 * ct + 16) * sizeof(float); }
+constexpr size_t kSkinnyMaxLds = 160 * 1024;
+
+template <int CT, bool kFused>
+hipError_t skinny_launch(const SkinnyGroup& g, int wgs, hipStream_t s) {
+  const size_t lds = skinny_lds(g.nblk, CT);
+  if (lds > kSkinnyMaxLds) return hipErrorInvalidValue;
+  if (lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_skinny<CT, kFused>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((k_skinny<CT, kFused>), dim3((unsigned)wgs), dim3(kSkinnyWaves * 64), lds, s, g);
+  return hipGetLastError();
+}
+
+SkinnyJob skinny_job(const WeightDev& w, int64_t m, int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias) {
+  SkinnyJob J{};
+  J.p0 = w.plane[0];
+  J.p1 = w.plane[1];
+  J.p2 = w.plane[2];
+  J.p3 = w.plane[3];
+  J.n_pad = w.n_pad;
+  J.n0 = n0;
+  J.n1 = n1;
+  J.y = y;
+  J.ys = ys;
+  J.bias = bias;
+  J.dtype = w.dtype;
+  J.m = (int)m;
+  return J;
+}
+
+// Tiles of 64 rows when the group has work for very many workgroups (at 16-row
+// tiles at least 16 per CU, e.g. an LM head) and their LDS fits; else 16-row tiles.
+int skinny_ct(int64_t wgs16, int64_t nblk, int cus) {
+  return wgs16 >= 16 * (int64_t)cus && skinny_lds(nblk, 4) <= kSkinnyMaxLds ? 4 : 1;
+}
+
+hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t* last_row, bool fused, int cus,
+                        hipStream_t s) {
+  int64_t wgs16 = 0;
+  for (int i = 0; i < g.count; ++i) wgs16 += (last_row[i] + 15) / 16 - first_row[i] / 16;
+  const int ct = skinny_ct(wgs16, g.nblk, cus);
+  const int nc = 16 * ct;
+  int64_t wgs = 0;
+  for (int i = 0; i < g.count; ++i) {
+    g.job[i].t0 = first_row[i] / nc;
+    g.job[i].wg0 = (int)wgs;
+    wgs += (last_row[i] + nc - 1) / nc - first_row[i] / nc;
+  }
+  if (wgs >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+  if (ct == 4) return fused ? skinny_launch<4, true>(g, (int)wgs, s) : skinny_launch<4, false>(g, (int)wgs, s);
+  return fused ? skinny_launch<1, true>(g, (int)wgs, s) : skinny_launch<1, false>(g, (int)wgs, s);
+}
+
+}  // namespace
+
+bool gemv_mma_supported(int dtype, int af, int64_t m) {
+  return (dtype == kQ4_K || dtype == kQ6_K) && af == kActQ8_K && m >= 2 && m <= 16;
+}
+
+bool gemv_mma_lds_ok(int64_t nblk) { return skinny_lds(nblk, 1) <= kSkinnyMaxLds; }
+
+int64_t skinny_units(const GemvJob* jobs, int count) {
+  if (count <= 0) return 0;
+  int64_t wgs16 = 0;
+  for (int i = 0; i < count; ++i) wgs16 += (jobs[i].w->n + 15) / 16;
+  const int ct = skinny_ct(wgs16, jobs[0].w->nblk, jobs[0].w->cus);
+  int64_t wgs = 0;
+  for (int i = 0; i < count; ++i) wgs += (jobs[i].w->n + 16 * ct - 1) / (16 * ct);
+  return wgs * jobs[0].w->nblk;
+}
+
+hipError_t launch_gemv_mma(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0,
+                           int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s) {
+  if (!gemv_mma_supported(w.dtype, af, m)) return hipErrorInvalidValue;
+  if (n1 <= n0) return hipSuccess;
+  SkinnyGroup g;
+  g.job[0] = skinny_job(w, m, n0, n1, y, ys, bias);
+  g.job[0].acts = acts;
+  g.job[0].arb = arb;
+  g.count = 1;
+  g.nblk = (int)w.nblk;
+  return launch_group(g, &n0, &n1, false, w.cus, s);
+}
+
+hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s) {
+  for (int i0 = 0; i0 < count; i0 += kSkinnyMaxJobs) {
+    SkinnyGroup g;
+    g.count = count - i0 < kSkinnyMaxJobs ? count - i0 : kSkinnyMaxJobs;
+    g.nblk = (int)jobs[i0].w->nblk;
+    const bool fused = jobs[i0].x != nullptr;
+    int64_t first[kSkinnyMaxJobs], last[kSkinnyMaxJobs];
+    for (int i = 0; i < g.count; ++i) {
+      const GemvJob& q = jobs[i0 + i];
+      if (q.w->nblk != g.nblk || !gemv_mma_supported(q.w->dtype, kActQ8_K, q.m) || (q.x != nullptr) != fused) {
+        return hipErrorInvalidValue;
+      }
+      g.job[i] = skinny_job(*q.w, q.m, 0, q.w->n, q.y, q.ys, q.bias);
+      g.job[i].acts = q.acts;
+      g.job[i].arb = q.arb;
+      g.job[i].x = q.x;
+      g.job[i].xs = q.xs;
+      first[i] = 0;
+      last[i] = q.w->n;
+    }
+    const hipError_t e = launch_group(g, first, last, fused, jobs[i0].w->cus, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace dq

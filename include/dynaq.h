@@ -155,12 +155,11 @@ typedef struct dq_matmul_job {
 } dq_matmul_job;
 
 /* Several independent matmuls on one stream, e.g. the projections that share one
- * input (Q/K/V, gate/up) or the experts of an MoE layer. Jobs with the same x
- * (pointer, m, k, x_stride) share one quantized copy; the decode-sized K-quant
+ * input (Q/K/V, gate/up) or the experts of an MoE layer. The decode-sized K-quant
  * jobs (2 <= m <= 16) of one k run together in grouped skinny-GEMV launches (up to
- * 8 jobs each, Q4_K and Q6_K mixed); every other job runs as dq_matmul runs it.
- * Each job's y is bit-identical to dq_matmul on that job. Uses dq_matmul's
- * per-device scratch. Replaces Device::matmul_many
+ * 8 jobs each, Q4_K and Q6_K mixed) that quantize each job's fp32 rows in the
+ * kernel; every other job runs as dq_matmul runs it. Each job's y is
+ * bit-identical to dq_matmul on that job. Replaces Device::matmul_many
  * (dynacore/include/dynacore/device/device.h:169-171; CpuDevice::matmul_many,
  * dynacore/cpu/cpu_device.cpp:500-692, which quantizes a shared input once and
  * runs all jobs' row chunks in one parallel region). */
