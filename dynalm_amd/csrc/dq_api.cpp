@@ -170,19 +170,19 @@ int check_out(const dq_weight* w, int64_t m, int64_t n0, int64_t n1, float* y, i
   return DQ_OK;
 }
 
-// The fused skinny path: K-quant weights, 2 <= m <= 16, LDS for the weight's
-// super-blocks, and fp32 rows addressable with 32-bit offsets.
-bool skinny_fused_ok(const dq_weight* w, const float* x, int64_t m, int64_t x_stride) {
+// The skinny path from fp32 rows: K-quant weights, 2 <= m <= 64, LDS for the
+// weight's super-blocks, and fp32 rows addressable with 32-bit offsets.
+bool skinny_ok(const dq_weight* w, const float* x, int64_t m, int64_t x_stride) {
   if (x == nullptr || !dq::gemv_mma_supported(w->dev.dtype, dq_act_format_for(w->dev.dtype), m)) return false;
-  if (!dq::gemv_mma_lds_ok(w->dev.nblk)) return false;
+  if (!dq::gemv_mma_lds_ok(w->dev.nblk, m)) return false;
   const int64_t xs = m > 1 ? x_stride : w->dev.k;
   return m * xs * 4 < ((int64_t)1 << 32);
 }
 
-// Runs grouped skinny launches over jobs (decode-sized K-quant matmuls, fp32
-// inputs in GemvJob::x): batches of up to 8 jobs of one k; a batch whose
-// re-quantization work is small quantizes in the kernel, else each distinct input
-// of the batch is quantized once into the per-device scratch first.
+// Runs grouped skinny launches over jobs (K-quant matmuls of 2..64 rows, fp32
+// inputs in GemvJob::x): batches of up to 8 jobs of one k; a batch of at most 16
+// rows whose re-quantization work is small quantizes in the kernel, else each
+// distinct input of the batch is quantized once into the per-device scratch first.
 int run_skinny(std::vector<dq::GemvJob>& jobs, int device, hipStream_t s) {
   std::vector<bool> done(jobs.size(), false);
   std::vector<dq::GemvJob> batch;
@@ -195,7 +195,9 @@ int run_skinny(std::vector<dq::GemvJob>& jobs, int device, hipStream_t s) {
         done[h] = true;
       }
     }
-    if (dq::skinny_units(batch.data(), (int)batch.size()) > dq::kSkinnyFuseMaxUnits) {
+    int64_t mmax = 0;
+    for (const dq::GemvJob& j : batch) mmax = j.m > mmax ? j.m : mmax;
+    if (mmax > 16 || dq::skinny_units(batch.data(), (int)batch.size()) > dq::kSkinnyFuseMaxUnits) {
       // one Q8_K copy per distinct input (x, m, k, stride), as CpuDevice shares one
       // buffer between jobs that read the same activations (cpu_device.cpp:561-599)
       const int64_t arb = dq_act_row_bytes(DQ_ACT_Q8_K, batch[0].w->k);
@@ -337,10 +339,24 @@ int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
   if (int rc = check_acts(w, fmt, acts, m); rc != DQ_OK) return rc;
   if (int rc = check_out(w, m, n0, n1, y, y_stride); rc != DQ_OK) return rc;
   if (m == 0 || n0 == n1) return DQ_OK;
-  if (dq::gemv_mma_supported(w->dev.dtype, fmt, m) && dq::gemv_mma_lds_ok(w->dev.nblk)) {
-    DQ_HIP(dq::launch_gemv_mma(w->dev, fmt, static_cast<const uint8_t*>(acts), dq_act_row_bytes(fmt, w->dev.k), m, n0,
-                               n1, y, y_stride, bias, as_stream(stream)),
-           "gemv launch");
+  if (m >= 2 && dq::gemv_mma_supported(w->dev.dtype, fmt, 2) &&
+      dq::gemv_mma_lds_ok(w->dev.nblk, m < dq::kSkinnyMaxRows ? m : dq::kSkinnyMaxRows)) {
+    // K-quants x Q8_K: the skinny MFMA GEMV in passes of up to 64 rows (a last
+    // single row goes to the M = 1 GEMV)
+    const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
+    const uint8_t* a = static_cast<const uint8_t*>(acts);
+    for (int64_t r0 = 0; r0 < m; r0 += dq::kSkinnyMaxRows) {
+      const int64_t rows = m - r0 < dq::kSkinnyMaxRows ? m - r0 : dq::kSkinnyMaxRows;
+      if (rows == 1) {
+        DQ_HIP(dq::launch_gemv(w->dev, fmt, a + r0 * arb, arb, 1, n0, n1, y + r0 * y_stride, y_stride, bias, nullptr,
+                               as_stream(stream)),
+               "gemv launch");
+      } else {
+        DQ_HIP(dq::launch_gemv_mma(w->dev, fmt, a + r0 * arb, arb, rows, n0, n1, y + r0 * y_stride, y_stride, bias,
+                                   as_stream(stream)),
+               "gemv launch");
+      }
+    }
     return DQ_OK;
   }
   DQ_HIP(dq::launch_gemv(w->dev, fmt, static_cast<const uint8_t*>(acts), dq_act_row_bytes(fmt, w->dev.k), m, n0, n1, y,
@@ -372,15 +388,20 @@ int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, f
   const int fmt = dq_act_format_for(w->dev.dtype);
   const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
   if (int rc = check_out(w, m, 0, w->dev.n, y, y_stride); rc != DQ_OK) return rc;
+  if (x == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
+  if (m > 1 && x_stride < w->dev.k) {
+    return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)w->dev.k);
+  }
   hipStream_t s = as_stream(stream);
-  if (skinny_fused_ok(w, x, m, x_stride)) {
-    // decode batch of 2..16 rows: the skinny MFMA GEMV (quantizing the fp32 rows in
+  if (skinny_ok(w, x, m, x_stride)) {
+    // decode batches of 2..64 rows: the skinny MFMA GEMV (quantizing the fp32 rows in
     // the kernel when that is cheap, else after one quantize launch)
     std::vector<dq::GemvJob> j{dq::GemvJob{&w->dev, nullptr, 0, x, m > 1 ? x_stride : w->dev.k, m, y, y_stride, bias}};
     return run_skinny(j, w->dev.device, s);
   }
-  if (dq::gemv_mma_supported(w->dev.dtype, fmt, m)) {
-    // the same on pre-quantized rows (inputs whose offsets exceed 32 bits)
+  if (m > 1 && dq::gemv_mma_supported(w->dev.dtype, fmt, 2) && !(m > DQ_GEMV_MAX_ROWS && dq::gemm_supported(w->dev.dtype, fmt))) {
+    // K-quants without a GEMM for this size (Q6_K), or inputs whose offsets exceed
+    // 32 bits: quantize once, then skinny passes of up to 64 rows
     void* acts = nullptr;
     if (int rc = scratch_get(w->dev.device, (size_t)(m * arb), s, &acts); rc != DQ_OK) return rc;
     if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, x_stride, acts, stream); rc != DQ_OK) return rc;
@@ -429,7 +450,7 @@ int dq_matmul_many(const dq_matmul_job* jobs, int64_t n_jobs, void* stream) {
   for (int64_t i = 0; i < n_jobs; ++i) {
     const dq_matmul_job& j = jobs[i];
     if (j.m == 0) continue;
-    if (skinny_fused_ok(j.w, j.x, j.m, j.x_stride)) {
+    if (skinny_ok(j.w, j.x, j.m, j.x_stride)) {
       grouped.push_back(dq::GemvJob{&j.w->dev, nullptr, 0, j.x, j.m > 1 ? j.x_stride : j.w->dev.k, j.m, j.y,
                                     j.y_stride, j.bias});
     } else {

@@ -41,13 +41,14 @@ hipError_t launch_units(const WeightDev& w, int af, const uint8_t* acts, int64_t
 hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
                        float* y, int64_t ys, const float* bias, hipStream_t s);
 bool gemm_supported(int dtype, int af);
-// Skinny MFMA GEMV (Q4_K / Q6_K x Q8_K, 2 <= m <= 16) on pre-quantized Q8_K rows;
-// hipErrorInvalidValue otherwise.
+// Skinny MFMA GEMV (Q4_K / Q6_K x Q8_K, 2 <= m <= kSkinnyMaxRows) on pre-quantized
+// Q8_K rows; hipErrorInvalidValue otherwise.
 hipError_t launch_gemv_mma(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0,
                            int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s);
+constexpr int64_t kSkinnyMaxRows = 64;
 bool gemv_mma_supported(int dtype, int af, int64_t m);
-// Whether the skinny kernel's LDS holds the t-terms of nblk super-blocks.
-bool gemv_mma_lds_ok(int64_t nblk);
+// Whether the skinny kernel's LDS holds the t-terms of nblk super-blocks for m rows.
+bool gemv_mma_lds_ok(int64_t nblk, int64_t m);
 // One matmul of a grouped skinny launch: y[r, i] (+ bias) for r < m, i < w->n, from
 // either pre-quantized Q8_K rows (acts, arb bytes apart) or fp32 rows that the
 // kernel quantizes (x != nullptr, xs floats apart).
@@ -63,8 +64,8 @@ struct GemvJob {
   const float* bias;
 };
 // Grouped skinny MFMA GEMV: jobs of one K (same nblk) and one input kind (all
-// fused or none), Q4_K / Q6_K, 2 <= m <= 16, in launches of up to 8 jobs;
-// hipErrorInvalidValue for any other job.
+// fused or none), Q4_K / Q6_K, 2 <= m <= 64 (fused: m <= 16), in launches of up to
+// 8 jobs; hipErrorInvalidValue for any other job.
 hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s);
 // Work of one grouped launch of these jobs (<= 8, one nblk) in wave-sized units
 // (workgroups x super-blocks): each unit of a launch on fp32 rows quantizes 16

@@ -78,11 +78,13 @@ struct SkinnyGroup {
 
 constexpr int kSkinnyWaves = 8;
 
-// The activation operand of one super-block: lane (li, lg) holds the codes of
-// activation row li at values 64 s + 16 lg .. + 15 (K-step s), and row li's d.
+// The activation operand of one super-block for MT tiles of 16 activation rows:
+// lane (li, lg) holds the codes of activation row 16 mt + li at values
+// 64 s + 16 lg .. + 15 (K-step s), and that row's d.
+template <int MT>
 struct ActSB {
-  v4u a[4];
-  float da;
+  v4u a[MT][4];
+  float da[MT];
 };
 
 // fp32 values of one super-block for the fused path: x[li][64 s + 16 lg + 4 c + i].
@@ -115,7 +117,7 @@ DQ_DEV void load_x(const ActSrc<true>& src, int b, int li, int lg, XSB& o) {
 
 // Q8_K quantization of row li's super-block from the 64 values of each of the 4
 // lanes (li, 0..3): amax across them, d = amax / 127, codes RNE at 1 / d.
-DQ_DEV void quant_x(const XSB& x, ActSB& o) {
+DQ_DEV void quant_x(const XSB& x, ActSB<1>& o) {
   float amax = 0.0f;
 #pragma unroll
   for (int s = 0; s < 4; ++s)
@@ -137,16 +139,20 @@ DQ_DEV void quant_x(const XSB& x, ActSB& o) {
       int unused = 0;
       w[c] = codes4_rne(v, id, unused);
     }
-    o.a[s] = v4u{w[0], w[1], w[2], w[3]};
+    o.a[0][s] = v4u{w[0], w[1], w[2], w[3]};
   }
-  o.da = d;
+  o.da[0] = d;
 }
 
-DQ_DEV void load_codes(const ActSrc<false>& src, int b, int li, int lg, ActSB& o) {
-  const u32 base = (u32)(li * src.stride + (int64_t)b * 292);
+template <int MT>
+DQ_DEV void load_codes(const ActSrc<false>& src, int b, int li, int lg, ActSB<MT>& o) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s) o.a[s] = ld16(src.r, base + 4 + 64 * s + 16 * lg);
-  o.da = as_f(ld4(src.r, base));
+  for (int mt = 0; mt < MT; ++mt) {
+    const u32 base = (u32)((16 * mt + li) * src.stride + (int64_t)b * 292);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) o.a[mt][s] = ld16(src.r, base + 4 + 64 * s + 16 * lg);
+    o.da[mt] = as_f(ld4(src.r, base));
+  }
 }
 
 // ---- weights of one super-block for CT column tiles (row r0 + 16 ct + li of row group G)
@@ -188,10 +194,12 @@ struct WSB<kQ6_K, CT> {
   }
 };
 
-// t-terms of column tile ct for one super-block (the 4 outputs of this lane:
-// activation rows 4 lg + e, weight row 16 ct + li of the tile).
-template <int CT>
-DQ_DEV void tterms(const WSB<kQ4_K, CT>& w, int ct, const ActSB& A, int lg, float t[4]) {
+// t-terms of column tile ct for one super-block: for each activation tile mt the 4
+// outputs of this lane (activation rows 16 mt + 4 lg + e, weight row 16 ct + li of
+// the tile). The weight operands of a K-step are built once and multiplied with
+// every activation tile.
+template <int CT, int MT>
+DQ_DEV void tterms(const WSB<kQ4_K, CT>& w, int ct, const ActSB<MT>& A, int lg, float t[MT][4]) {
   const int hi = lg >> 1;
   const u32 shift = 4u * (u32)hi, flip = hi ? 0x08080808u : 0u;  // high nibbles are stored XOR 8
   const v4u hd = w.hd[ct];
@@ -202,7 +210,7 @@ DQ_DEV void tterms(const WSB<kQ4_K, CT>& w, int ct, const ActSB& A, int lg, floa
   const u32 sc = __builtin_amdgcn_perm(sc_hi, sc_lo, sel_subblocks(hi));
   const u32 KH = (sc >> 3) & 0x07070707u, KL = sc & 0x07070707u;
   const u32 MN = __builtin_amdgcn_perm(mn_hi, mn_lo, sel_subblocks(hi));
-  v4i_t acc[3];
+  v4i_t acc[MT][3];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const v4u qb = ((w.q[ct][s] >> shift) & 0x0F0F0F0Fu) ^ flip;
@@ -213,23 +221,33 @@ DQ_DEV void tterms(const WSB<kQ4_K, CT>& w, int ct, const ActSB& A, int lg, floa
     const v4u Lo = {mul_bytes(qb.x, kl), mul_bytes(qb.y, kl), mul_bytes(qb.z, kl), mul_bytes(qb.w, kl)};
     const v4u Mp = {mm4, mm4, mm4, mm4};
     const v4i_t z = {0, 0, 0, 0};
-    acc[0] = mfma(A.a[s], H, s == 0 ? z : acc[0]);
-    acc[1] = mfma(A.a[s], Lo, s == 0 ? z : acc[1]);
-    acc[2] = mfma(A.a[s], Mp, s == 0 ? z : acc[2]);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      acc[mt][0] = mfma(A.a[mt][s], H, s == 0 ? z : acc[mt][0]);
+      acc[mt][1] = mfma(A.a[mt][s], Lo, s == 0 ? z : acc[mt][1]);
+      acc[mt][2] = mfma(A.a[mt][s], Mp, s == 0 ? z : acc[mt][2]);
+    }
   }
   const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int S = acc[1][e] + (acc[0][e] << 3);
-    const float u = d * (float)S;
-    t[e] = fmaf(-dmin, (float)acc[2][e], u);
-  }
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int S = acc[mt][1][e] + (acc[mt][0][e] << 3);
+      const float u = d * (float)S;
+      t[mt][e] = fmaf(-dmin, (float)acc[mt][2][e], u);
+    }
 }
 
-template <int CT>
-DQ_DEV void tterms(const WSB<kQ6_K, CT>& w, int ct, const ActSB& A, int lg, float t[4]) {
+template <int CT, int MT>
+DQ_DEV void tterms(const WSB<kQ6_K, CT>& w, int ct, const ActSB<MT>& A, int lg, float t[MT][4]) {
   const v4u zero = {0u, 0u, 0u, 0u};
-  v4i_t S = {0, 0, 0, 0}, C = {0, 0, 0, 0};
+  v4i_t S[MT], C[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    S[mt] = v4i_t{0, 0, 0, 0};
+    C[mt] = v4i_t{0, 0, 0, 0};
+  }
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     // codes of sub-block 4s + g: quarter 2(s&1) + g/2 of half s/2
@@ -241,19 +259,24 @@ DQ_DEV void tterms(const WSB<kQ6_K, CT>& w, int ct, const ActSB& A, int lg, floa
     const u32 mine = (u32)sbfe(sw, 8 * lg, 8) & 0xFFu;  // this lane group's scale
     const u32 sc4 = mine * 0x01010101u;
     const v4i_t z = {0, 0, 0, 0};
-    C = mfma(A.a[s], v4u{sc4, sc4, sc4, sc4}, C);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const v4u au = lg == u ? A.a[s] : zero;
-      const v4i_t P = mfma(au, q, z);
-      const int scu = sbfe(sw, 8 * u, 8);
+    for (int mt = 0; mt < MT; ++mt) {
+      C[mt] = mfma(A.a[mt][s], v4u{sc4, sc4, sc4, sc4}, C[mt]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) S[e] += scu * __builtin_amdgcn_sbfe(P[e], 0, 24);
+      for (int u = 0; u < 4; ++u) {
+        const v4u au = lg == u ? A.a[mt][s] : zero;
+        const v4i_t P = mfma(au, q, z);
+        const int scu = sbfe(sw, 8 * u, 8);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[mt][e] += scu * __builtin_amdgcn_sbfe(P[e], 0, 24);
+      }
     }
   }
   const float d = h2f(w.dw[ct]);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) t[e] = d * (float)(S[e] - 32 * C[e]);
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[mt][e] = d * (float)(S[mt][e] - 32 * C[mt][e]);
 }
 
 template <int WT, int CT>
@@ -283,31 +306,37 @@ struct WRes<kQ6_K, CT> {
 // CT == 1 keeps the next super-block's weight loads in flight during the compute
 // (activation loads of b are issued before the weight loads of b + 1, so waiting
 // for them does not wait for the prefetch: loads retire in order).
-template <int WT, int CT, bool kFused>
+template <int WT, int CT, int MT, bool kFused>
 DQ_DEV void skinny_wave(const SkinnyJob& J, int nblk, int64_t G, int r0, bool ok, int b0, int b1, float* tt,
                         float* dal, int li, int lg) {
-  constexpr int NC = 16 * CT;
+  constexpr int NC = 16 * CT, NR = 16 * MT;
   WRes<WT, CT> res;
   res.init(J, G, nblk, ok);
   ActSrc<kFused> src;
   src.init(J);
-  auto emit = [&](const WSB<WT, CT>& w, const ActSB& A, int b) {
+  auto emit = [&](const WSB<WT, CT>& w, const ActSB<MT>& A, int b) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-      float t[4];
-      tterms<CT>(w, ct, A, lg, t);
+      float t[MT][4];
+      tterms<CT, MT>(w, ct, A, lg, t);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) tt[(b * 16 + 4 * lg + e) * NC + 16 * ct + li] = t[e];
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tt[(b * NR + 16 * mt + 4 * lg + e) * NC + 16 * ct + li] = t[mt][e];
     }
-    if (lg == 0) dal[b * 16 + li] = A.da;
+    if (lg == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) dal[b * NR + 16 * mt + li] = A.da[mt];
+    }
   };
-  auto act = [&](int b, ActSB& A) {
+  auto act = [&](int b, ActSB<MT>& A) {
     if constexpr (kFused) {
+      static_assert(MT == 1, "in-kernel quantization covers one activation tile");
       XSB x;
       load_x(src, b, li, lg, x);
       quant_x(x, A);
     } else {
-      load_codes(src, b, li, lg, A);
+      load_codes<MT>(src, b, li, lg, A);
     }
   };
   if (b0 >= b1) return;
@@ -315,7 +344,7 @@ DQ_DEV void skinny_wave(const SkinnyJob& J, int nblk, int64_t G, int r0, bool ok
     WSB<WT, CT> cur;
     res.load(cur, b0, r0, li, lg);
     for (int b = b0; b < b1; ++b) {
-      ActSB A;
+      ActSB<MT> A;
       act(b, A);
       WSB<WT, CT> nxt;
       res.load(nxt, b + 1 < b1 ? b + 1 : b, r0, li, lg);
@@ -330,25 +359,25 @@ DQ_DEV void skinny_wave(const SkinnyJob& J, int nblk, int64_t G, int r0, bool ok
       WSB<WT, CT> w;
       res.load(w, b, r0, li, lg);
       __builtin_amdgcn_sched_barrier(0);
-      ActSB A;
+      ActSB<MT> A;
       act(b, A);
       emit(w, A, b);
     }
   }
 }
 
-template <int CT, bool kFused>
+template <int CT, int MT, bool kFused>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void k_skinny(SkinnyGroup g) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int W = kSkinnyWaves;
-  constexpr int NC = 16 * CT;
+  constexpr int NC = 16 * CT, NR = 16 * MT;
   const int wg = blockIdx.x;
   int j = 0;
   while (j + 1 < g.count && wg >= g.job[j + 1].wg0) ++j;
   const SkinnyJob& J = g.job[j];
   const int nblk = g.nblk;
-  float* tt = reinterpret_cast<float*>(lds);  // [nblk][16 activation rows][NC weight rows]
-  float* dal = tt + nblk * 16 * NC;           // [nblk][16] activation d
+  float* tt = reinterpret_cast<float*>(lds);  // [nblk][NR activation rows][NC weight rows]
+  float* dal = tt + nblk * NR * NC;           // [nblk][NR] activation d
   const int l = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = l & 15, lg = l >> 4;
   const int64_t row0 = (J.t0 + (wg - J.wg0)) * NC;  // first weight row of the tile
@@ -357,34 +386,36 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void k_skinny(SkinnyGroup g) {
   const bool ok = row0 < J.n_pad;
   const int b0 = wave * nblk / W, b1 = (wave + 1) * nblk / W;
   if (J.dtype == kQ6_K) {
-    skinny_wave<kQ6_K, CT, kFused>(J, nblk, G, r0, ok, b0, b1, tt, dal, li, lg);
+    skinny_wave<kQ6_K, CT, MT, kFused>(J, nblk, G, r0, ok, b0, b1, tt, dal, li, lg);
   } else {
-    skinny_wave<kQ4_K, CT, kFused>(J, nblk, G, r0, ok, b0, b1, tt, dal, li, lg);
+    skinny_wave<kQ4_K, CT, MT, kFused>(J, nblk, G, r0, ok, b0, b1, tt, dal, li, lg);
   }
   __syncthreads();
-  // the in-order chains of the tile's 16 x NC outputs, shared by all waves
-  for (int o = threadIdx.x; o < 16 * NC; o += W * 64) {
+  // the in-order chains of the tile's NR x NC outputs, shared by all waves
+  for (int o = threadIdx.x; o < NR * NC; o += W * 64) {
     const int mm = o / NC, c = o % NC;
     float v = 0.0f;
-    for (int b = 0; b < nblk; ++b) v = fmaf(dal[b * 16 + mm], tt[(b * 16 + mm) * NC + c], v);
+    for (int b = 0; b < nblk; ++b) v = fmaf(dal[b * NR + mm], tt[(b * NR + mm) * NC + c], v);
     const int64_t n = row0 + c;
     if (mm < J.m && n >= J.n0 && n < J.n1) J.y[mm * J.ys + n] = J.bias ? v + J.bias[n] : v;
   }
 }
 
-size_t skinny_lds(int64_t nblk, int ct) { return (size_t)nblk * (16 * 16 * ct + 16) * sizeof(float); }
+size_t skinny_lds(int64_t nblk, int ct, int mt) {
+  return (size_t)nblk * (16 * mt * (16 * ct + 1)) * sizeof(float);
+}
 constexpr size_t kSkinnyMaxLds = 160 * 1024;
 
-template <int CT, bool kFused>
+template <int CT, int MT, bool kFused>
 hipError_t skinny_launch(const SkinnyGroup& g, int wgs, hipStream_t s) {
-  const size_t lds = skinny_lds(g.nblk, CT);
+  const size_t lds = skinny_lds(g.nblk, CT, MT);
   if (lds > kSkinnyMaxLds) return hipErrorInvalidValue;
   if (lds > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_skinny<CT, kFused>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_skinny<CT, MT, kFused>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((k_skinny<CT, kFused>), dim3((unsigned)wgs), dim3(kSkinnyWaves * 64), lds, s, g);
+  hipLaunchKernelGGL((k_skinny<CT, MT, kFused>), dim3((unsigned)wgs), dim3(kSkinnyWaves * 64), lds, s, g);
   return hipGetLastError();
 }
 
@@ -407,15 +438,22 @@ SkinnyJob skinny_job(const WeightDev& w, int64_t m, int64_t n0, int64_t n1, floa
 
 // Tiles of 64 rows when the group has work for very many workgroups (at 16-row
 // tiles at least 16 per CU, e.g. an LM head) and their LDS fits; else 16-row tiles.
-int skinny_ct(int64_t wgs16, int64_t nblk, int cus) {
-  return wgs16 >= 16 * (int64_t)cus && skinny_lds(nblk, 4) <= kSkinnyMaxLds ? 4 : 1;
+// More than 16 activation rows take 4 activation tiles and 16-row weight tiles.
+int skinny_ct(int64_t wgs16, int64_t nblk, int cus, int mt) {
+  return mt == 1 && wgs16 >= 16 * (int64_t)cus && skinny_lds(nblk, 4, 1) <= kSkinnyMaxLds ? 4 : 1;
 }
 
 hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t* last_row, bool fused, int cus,
                         hipStream_t s) {
+  int mmax = 0;
   int64_t wgs16 = 0;
-  for (int i = 0; i < g.count; ++i) wgs16 += (last_row[i] + 15) / 16 - first_row[i] / 16;
-  const int ct = skinny_ct(wgs16, g.nblk, cus);
+  for (int i = 0; i < g.count; ++i) {
+    wgs16 += (last_row[i] + 15) / 16 - first_row[i] / 16;
+    mmax = g.job[i].m > mmax ? g.job[i].m : mmax;
+  }
+  const int mt = mmax > 16 ? 4 : 1;
+  if (mt == 4 && fused) return hipErrorInvalidValue;
+  const int ct = skinny_ct(wgs16, g.nblk, cus, mt);
   const int nc = 16 * ct;
   int64_t wgs = 0;
   for (int i = 0; i < g.count; ++i) {
@@ -424,23 +462,26 @@ hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t*
     wgs += (last_row[i] + nc - 1) / nc - first_row[i] / nc;
   }
   if (wgs >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
-  if (ct == 4) return fused ? skinny_launch<4, true>(g, (int)wgs, s) : skinny_launch<4, false>(g, (int)wgs, s);
-  return fused ? skinny_launch<1, true>(g, (int)wgs, s) : skinny_launch<1, false>(g, (int)wgs, s);
+  if (mt == 4) return skinny_launch<1, 4, false>(g, (int)wgs, s);
+  if (ct == 4) return fused ? skinny_launch<4, 1, true>(g, (int)wgs, s) : skinny_launch<4, 1, false>(g, (int)wgs, s);
+  return fused ? skinny_launch<1, 1, true>(g, (int)wgs, s) : skinny_launch<1, 1, false>(g, (int)wgs, s);
 }
 
 }  // namespace
 
 bool gemv_mma_supported(int dtype, int af, int64_t m) {
-  return (dtype == kQ4_K || dtype == kQ6_K) && af == kActQ8_K && m >= 2 && m <= 16;
+  return (dtype == kQ4_K || dtype == kQ6_K) && af == kActQ8_K && m >= 2 && m <= kSkinnyMaxRows;
 }
 
-bool gemv_mma_lds_ok(int64_t nblk) { return skinny_lds(nblk, 1) <= kSkinnyMaxLds; }
+bool gemv_mma_lds_ok(int64_t nblk, int64_t m) { return skinny_lds(nblk, 1, m > 16 ? 4 : 1) <= kSkinnyMaxLds; }
 
 int64_t skinny_units(const GemvJob* jobs, int count) {
   if (count <= 0) return 0;
   int64_t wgs16 = 0;
   for (int i = 0; i < count; ++i) wgs16 += (jobs[i].w->n + 15) / 16;
-  const int ct = skinny_ct(wgs16, jobs[0].w->nblk, jobs[0].w->cus);
+  int64_t mmax = 0;
+  for (int i = 0; i < count; ++i) mmax = jobs[i].m > mmax ? jobs[i].m : mmax;
+  const int ct = skinny_ct(wgs16, jobs[0].w->nblk, jobs[0].w->cus, mmax > 16 ? 4 : 1);
   int64_t wgs = 0;
   for (int i = 0; i < count; ++i) wgs += (jobs[i].w->n + 16 * ct - 1) / (16 * ct);
   return wgs * jobs[0].w->nblk;

@@ -441,3 +441,31 @@ def test_matmul_many_rejects_before_launching(cuda):
         dq.matmul_many([(w, x, 4, k, y, 64, None), (w, x, 4, k - 1, y, 64, None)])
     assert e.value.status == "invalid_argument"
     assert np.all(host(y) == 777.0)
+
+
+# ------------------------------------------------- skinny MFMA GEMV, 17..64 rows and passes
+
+
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q6_K], ids=lambda t: O.TYPE_NAMES[t])
+@pytest.mark.parametrize("m", [17, 40, 64, 100, 129])
+def test_skinny_activation_tiles_and_passes(cuda, t, m):
+    """K-quant matmuls of 17..64 rows run the skinny MFMA kernel with 4 activation
+    tiles (rows past m read zeros); more rows run passes of 64 (a last single row on
+    the M = 1 GEMV): dq_gemv on pre-quantized rows and dq_matmul (Q6_K at any m,
+    Q4_K up to 64 rows) bit-identical to the oracle."""
+    from dynalm_amd import torch_ops as T
+
+    k, n = 1280, 80
+    w_rows = gguf_weights(t, n, k, 120 + m, outlier_frac=0.01)
+    x = activations(m, k, 121 + m)
+    a = O.quantize_act(O.ACT_Q8_K, x)
+    w = dq.Weight.upload(t, w_rows, k)
+    want = O.matmul(t, O.ACT_Q8_K, w_rows, a, k)
+    y = host(T.gemv(w, O.ACT_Q8_K, dev(a)))
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+    y2 = host(T.matmul(w, dev(x)))
+    if t == O.Q6_K or m <= 64:
+        assert np.array_equal(y2.view(np.uint32), want.view(np.uint32))
+    else:
+        ok, worst = close(y2, want)
+        assert ok, f"worst error ratio {worst:.3g}"
