@@ -220,6 +220,30 @@ def decode_stack(steps: int, stream: int) -> dict:
     return out
 
 
+def prefill_sweep(ms: list[int], weights, gen) -> list[dict]:
+    """Config 4's sweep: dq_matmul on M fp32 rows (Q8_K quantization on the GPU, then
+    the kernel dq_matmul dispatches to: the skinny MFMA GEMV up to 64 rows, the MFMA
+    GEMM above), K=4096 N=14336, rotated weights, graph replay."""
+    import torch
+
+    import dynalm_amd as dq
+
+    out = []
+    ng = min(4, len(weights))
+    for m in ms:
+        x = torch.randn((m, K), generator=gen, device="cuda", dtype=torch.float32)
+        y = torch.empty((m, N), dtype=torch.float32, device="cuda")
+        iters = max(10, min(50, 20000 // m))
+        log(f"prefill sweep M={m} x{iters}")
+        ms_call = time_graph(lambda i, st: dq.matmul(weights[i % ng], x, m, K, y, N, None, st), iters, 3)
+        tops = 2.0 * m * N * K / (ms_call * 1e-3) / 1e12
+        out.append({"m": m, "kernel": "skinny MFMA GEMV" if m <= 64 else "MFMA GEMM",
+                    "ms_per_call": round(ms_call, 4), "tops": round(tops, 1),
+                    "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2), "tokens_per_s": round(m / (ms_call * 1e-3), 1)})
+        del x, y
+    return out
+
+
 COPY_BYTES = 64 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_m1_gemm_m512_traffic.md")
 
@@ -275,6 +299,9 @@ def main() -> None:
     ap.add_argument("--copies", type=int, default=16, help="rotated weight copies (x 33 MB)")
     ap.add_argument("--gemm-m", type=int, default=512)
     ap.add_argument("--gemm-iters", type=int, default=50)
+    ap.add_argument("--sweep", default="64,128,512,2048",
+                    help="config 4 prefill sweep: dq_matmul (quantization + the kernel dq_matmul picks) at these M "
+                         "('' to skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--stack-steps", type=int, default=20, help="config 5 decode-stack steps (0: skip)")
@@ -399,6 +426,8 @@ def main() -> None:
                          "traffic": traffic.get("gemm_m512")},
         },
     }
+    if args.sweep:
+        result["prefill_sweep"] = prefill_sweep([int(v) for v in args.sweep.split(",")], weights, gen)
     if args.stack_steps > 0:
         log(f"config 5 decode stack x{args.stack_steps}")
         result["decode_stack_m16"] = decode_stack(args.stack_steps, stream)
