@@ -17,6 +17,8 @@ dynacore/include/dynacore/device/device.h:89-161):
     gemm(w, fmt, acts, m, n0, n1, ...) qmm::Kernels::gemm
     matmul(w, x, m, ...)               Device::matmul
     matmul_many(jobs)                  Device::matmul_many
+    act_mul(act, gate, up, ...)        Device::act_mul
+    matmul_gated(act, x, wg, wu, ...)  Device::matmul_gated
 
 Errors raise DqError carrying dynacore's StatusCode value
 (dynacore/include/dynacore/base/status.h:19-32).
@@ -32,12 +34,13 @@ __all__ = [
     "Q4_0", "Q8_0", "Q4_K", "Q6_K", "ACT_PER32", "ACT_Q8_0", "ACT_Q8_K", "GEMV_MAX_ROWS",
     "DqError", "lib", "lib_path", "row_bytes", "act_row_bytes", "act_format_for", "Weight",
     "act_quantize", "gemv", "gemm", "matmul", "matmul_many", "MatmulJob", "partials_count", "debug_partials",
-    "EXPORTS",
+    "SILU", "GELU", "GELU_TANH", "act_mul", "matmul_gated", "EXPORTS",
 ]
 
 Q4_0, Q8_0, Q4_K, Q6_K = 6, 10, 14, 16
 ACT_PER32, ACT_Q8_0, ACT_Q8_K = 0, 1, 2
 GEMV_MAX_ROWS = 16
+SILU, GELU, GELU_TANH = 0, 1, 2  # dq_activation (dynacore Activation, device/ops.h:14)
 
 STATUS_NAMES = {
     0: "ok", 1: "invalid_argument", 2: "not_found", 3: "already_exists", 4: "out_of_memory",
@@ -73,6 +76,8 @@ EXPORTS = {
     "dq_gemm": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "dq_matmul": (_I, [_P, _P, _I64, _I64, _P, _I64, _P, _P]),
     "dq_matmul_many": (_I, [_P, _I64, _P]),
+    "dq_act_mul": (_I, [_I, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P]),
+    "dq_matmul_gated": (_I, [_I, _P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P]),
     "dq_partials_count": (_I, [_I, _I, _I64, C.POINTER(_I64), C.POINTER(_I64)]),
     "dq_debug_partials": (_I, [_P, _I, _P, _I64, _P, _P, _P]),
 }
@@ -207,6 +212,19 @@ def matmul_many(jobs, stream: int = 0) -> None:
     for i, (w, x, m, xs, y, ys, bias) in enumerate(jobs):
         arr[i] = MatmulJob(w.handle.value if isinstance(w, Weight) else w, _ptr(x), m, xs, _ptr(y), ys, _ptr(bias))
     _check(lib().dq_matmul_many(C.cast(arr, _P), len(jobs), stream))
+
+
+def act_mul(act: int, gate, gate_stride: int, up, up_stride: int, m: int, n: int, out, out_stride: int,
+            stream: int = 0) -> None:
+    """out = act(gate) * up elementwise (Device::act_mul)."""
+    _check(lib().dq_act_mul(act, _ptr(gate), gate_stride, _ptr(up), up_stride, m, n, _ptr(out), out_stride, stream))
+
+
+def matmul_gated(act: int, x, m: int, x_stride: int, w_gate: Weight, w_up: Weight, out, out_stride: int,
+                 gate_scratch=None, up_scratch=None, scratch_stride: int = 0, stream: int = 0) -> None:
+    """out = act(x . w_gate^T) * (x . w_up^T) (Device::matmul_gated); scratch optional."""
+    _check(lib().dq_matmul_gated(act, _ptr(x), m, x_stride, w_gate.handle, w_up.handle, _ptr(out), out_stride,
+                                 _ptr(gate_scratch), _ptr(up_scratch), scratch_stride, stream))
 
 
 def partials_count(dtype: int, fmt: int, k: int) -> tuple[int, int]:

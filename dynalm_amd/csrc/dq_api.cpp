@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "../../include/dynaq.h"
+#include "dq_act.h"
 #include "dq_internal.h"
 
 struct dq_weight {
@@ -60,34 +61,38 @@ bool pair_ok(int t, int f) {
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
-// Per-device scratch for dq_matmul's quantized activations (grows, never shrinks).
+// Per-device scratch buffers (grow, never shrink): g_scratch holds dq_matmul's
+// quantized activations, g_fscratch the fp32 gate / up projections of
+// dq_matmul_gated's unfused path (which runs dq_matmul, so the two must differ).
 struct Scratch {
   std::mutex mu;
   std::vector<void*> ptr;
   std::vector<size_t> bytes;
 };
 Scratch g_scratch;
+Scratch g_fscratch;
 
-int scratch_get(int device, size_t need, hipStream_t s, void** out) {
-  std::lock_guard<std::mutex> lock(g_scratch.mu);
-  if ((int)g_scratch.ptr.size() <= device) {
-    g_scratch.ptr.resize(device + 1, nullptr);
-    g_scratch.bytes.resize(device + 1, 0);
+int scratch_get(Scratch& pool, int device, size_t need, hipStream_t s, void** out) {
+  std::lock_guard<std::mutex> lock(pool.mu);
+  if ((int)pool.ptr.size() <= device) {
+    pool.ptr.resize(device + 1, nullptr);
+    pool.bytes.resize(device + 1, 0);
   }
-  if (g_scratch.bytes[device] < need) {
-    if (g_scratch.ptr[device] != nullptr) {
+  if (pool.bytes[device] < need) {
+    if (pool.ptr[device] != nullptr) {
       DQ_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
-      DQ_HIP(hipFree(g_scratch.ptr[device]), "hipFree");
-      g_scratch.ptr[device] = nullptr;
-      g_scratch.bytes[device] = 0;
+      DQ_HIP(hipFree(pool.ptr[device]), "hipFree");
+      pool.ptr[device] = nullptr;
+      pool.bytes[device] = 0;
     }
     size_t sz = need < (1u << 20) ? (1u << 20) : need;
-    DQ_HIP(hipMalloc(&g_scratch.ptr[device], sz), "hipMalloc(scratch)");
-    g_scratch.bytes[device] = sz;
+    DQ_HIP(hipMalloc(&pool.ptr[device], sz), "hipMalloc(scratch)");
+    pool.bytes[device] = sz;
   }
-  *out = g_scratch.ptr[device];
+  *out = pool.ptr[device];
   return DQ_OK;
 }
+int scratch_get(int device, size_t need, hipStream_t s, void** out) { return scratch_get(g_scratch, device, need, s, out); }
 
 int validate_shape(int dtype, int64_t n, int64_t k) {
   if (!weight_type_ok(dtype)) return fail(DQ_UNSUPPORTED, "weight type %d is not supported", dtype);
@@ -190,7 +195,7 @@ int run_skinny(std::vector<dq::GemvJob>& jobs, int device, hipStream_t s) {
     if (done[g]) continue;
     batch.clear();
     for (size_t h = g; h < jobs.size() && batch.size() < 8; ++h) {
-      if (!done[h] && jobs[h].w->nblk == jobs[g].w->nblk) {
+      if (!done[h] && jobs[h].w->nblk == jobs[g].w->nblk && (jobs[h].wu != nullptr) == (jobs[g].wu != nullptr)) {
         batch.push_back(jobs[h]);
         done[h] = true;
       }
@@ -463,6 +468,73 @@ int dq_matmul_many(const dq_matmul_job* jobs, int64_t n_jobs, void* stream) {
     if (int rc = dq_matmul(j.w, j.x, j.m, j.x_stride, j.y, j.y_stride, j.bias, stream); rc != DQ_OK) return rc;
   }
   return DQ_OK;
+}
+
+int dq_act_mul(int act, const float* gate, int64_t gate_stride, const float* up, int64_t up_stride, int64_t m,
+               int64_t n, float* out, int64_t out_stride, void* stream) {
+  if (!dq::act_ok(act)) return fail(DQ_INVALID_ARGUMENT, "unknown activation %d", act);
+  if (m < 0 || n < 0) return fail(DQ_INVALID_ARGUMENT, "m and n must be >= 0");
+  if (m == 0 || n == 0) return DQ_OK;
+  if (gate == nullptr || up == nullptr || out == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
+  if (m > 1 && (gate_stride < n || up_stride < n || out_stride < n)) {
+    return fail(DQ_INVALID_ARGUMENT, "row strides (%lld, %lld, %lld) must be >= n %lld", (long long)gate_stride,
+                (long long)up_stride, (long long)out_stride, (long long)n);
+  }
+  const int64_t gs = m > 1 ? gate_stride : n, us = m > 1 ? up_stride : n, os = m > 1 ? out_stride : n;
+  DQ_HIP(dq::launch_act_mul(act, gate, gs, up, us, m, n, out, os, as_stream(stream)), "act_mul launch");
+  return DQ_OK;
+}
+
+int dq_matmul_gated(int act, const float* x, int64_t m, int64_t x_stride, const dq_weight* w_gate,
+                    const dq_weight* w_up, float* out, int64_t out_stride, float* gate_scratch, float* up_scratch,
+                    int64_t scratch_stride, void* stream) {
+  if (!dq::act_ok(act)) return fail(DQ_INVALID_ARGUMENT, "unknown activation %d", act);
+  if (w_gate == nullptr || w_up == nullptr) return fail(DQ_INVALID_ARGUMENT, "null weight");
+  if (m < 0) return fail(DQ_INVALID_ARGUMENT, "m must be >= 0");
+  const dq::WeightDev &g = w_gate->dev, &u = w_up->dev;
+  if (g.n != u.n || g.k != u.k) {
+    return fail(DQ_INVALID_ARGUMENT, "gate [%lld, %lld] and up [%lld, %lld] differ in shape", (long long)g.n,
+                (long long)g.k, (long long)u.n, (long long)u.k);
+  }
+  if (g.device != u.device) return fail(DQ_INVALID_ARGUMENT, "gate and up weights are on different devices");
+  if ((gate_scratch == nullptr) != (up_scratch == nullptr)) {
+    return fail(DQ_INVALID_ARGUMENT, "gate_scratch and up_scratch are both given or both NULL");
+  }
+  if (m == 0) return DQ_OK;
+  if (x == nullptr) return fail(DQ_INVALID_ARGUMENT, "null x");
+  if (m > 1 && x_stride < g.k) return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)g.k);
+  if (int rc = check_out(w_gate, m, 0, g.n, out, out_stride); rc != DQ_OK) return rc;
+  if (gate_scratch != nullptr && m > 1 && scratch_stride < g.n) {
+    return fail(DQ_INVALID_ARGUMENT, "scratch_stride %lld < n %lld", (long long)scratch_stride, (long long)g.n);
+  }
+  hipStream_t s = as_stream(stream);
+  const bool same = g.dtype == u.dtype;
+  if (same && m == 1 && dq::gemv_gated_supported(g, u)) {
+    // decode, one row: both weights' row groups in one GEMV launch
+    DQ_HIP(dq::launch_gemv_gated(g, u, act, x, out, s), "gated gemv launch");
+    return DQ_OK;
+  }
+  if (same && m <= dq::kSkinnyGatedMaxRows && skinny_ok(w_gate, x, m, x_stride) && dq::gemv_mma_lds_ok(g.nblk, m, true)) {
+    // decode batches: the skinny MFMA GEMV over both weights, act(g) * u in its chains
+    std::vector<dq::GemvJob> j{
+        dq::GemvJob{&g, nullptr, 0, x, m > 1 ? x_stride : g.k, m, out, m > 1 ? out_stride : g.n, nullptr, &u, act}};
+    return run_skinny(j, g.device, s);
+  }
+  // the unfused sequence of Device::matmul_gated (device.h:194-199)
+  float* gp = gate_scratch;
+  float* up = up_scratch;
+  int64_t ss = m > 1 ? scratch_stride : g.n;
+  if (gp == nullptr) {
+    const int64_t plane = (m * g.n + 63) / 64 * 64;
+    void* p = nullptr;
+    if (int rc = scratch_get(g_fscratch, g.device, (size_t)(2 * plane) * sizeof(float), s, &p); rc != DQ_OK) return rc;
+    gp = static_cast<float*>(p);
+    up = gp + plane;
+    ss = g.n;
+  }
+  const dq_matmul_job jobs[2] = {{w_gate, x, m, x_stride, gp, ss, nullptr}, {w_up, x, m, x_stride, up, ss, nullptr}};
+  if (int rc = dq_matmul_many(jobs, 2, stream); rc != DQ_OK) return rc;
+  return dq_act_mul(act, gp, ss, up, ss, m, g.n, out, out_stride, stream);
 }
 
 int dq_partials_count(int dtype, int fmt, int64_t k, int64_t* units, int64_t* sb_terms) {

@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "dq_act.h"
 #include "dq_device.h"
 #include "dq_internal.h"
 #include "dq_quant.h"
@@ -541,22 +542,35 @@ DQ_DEV void quantize_slice(const float* __restrict__ x, int64_t xs, int nblk, in
 // kEarly (one activation row only): 0 = activations staged by loops after the
 // first weight loads; E > 0 = each wave holds at most E Q8_K super-blocks (or, for
 // 32-value formats, at most 64 blocks) and loads them ahead of the weights.
-template <int WT, int AF, int M, int W, int U, bool kFuse, int kEarly>
+// kGated (K-quants, one fused row): q0..q3 are a second weight of the same type and
+// shape (the up projection); waves W/2.. run it over the same row group with their
+// own LDS regions, and y = act(x . gate) * (x . up) (dynacore's Device::matmul_gated,
+// dynacore/include/dynacore/device/device.h:188-199).
+template <int WT, int AF, int M, int W, int U, bool kFuse, int kEarly, bool kGated = false>
 __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
                                                  const uint8_t* __restrict__ p2, const uint8_t* __restrict__ p3,
                                                  int nblk, int64_t g0, int64_t n0, int64_t n1,
                                                  const uint8_t* __restrict__ acts, int64_t arb,
                                                  const float* __restrict__ x, int64_t xs,
                                                  float* __restrict__ y, int64_t ys, const float* __restrict__ bias,
-                                                 int32_t* __restrict__ dbg, int64_t dbg_n) {
+                                                 int32_t* __restrict__ dbg, int64_t dbg_n,
+                                                 const uint8_t* __restrict__ q0, const uint8_t* __restrict__ q1,
+                                                 const uint8_t* __restrict__ q2, const uint8_t* __restrict__ q3,
+                                                 int act) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr bool kSb = AF == kActQ8_K;
+  static_assert(!kGated || (kSb && M == 1 && kFuse), "the gated GEMV takes one fp32 row and K-quant weights");
   // LDS: Q8_K t-terms [M][nblk][64] + da [M][nblk]  |  per-32 slice sums [W][M][64];
-  // then the staged activation rows [M][nblk (blocks of 32 for per-32)][stage bytes]
+  // then the staged activation rows [M][nblk (blocks of 32 for per-32)][stage bytes].
+  // kGated: one t-term region and one stage region per weight.
+  constexpr int WH = kGated ? W / 2 : W;  // waves per weight
   const int r = threadIdx.x & 63, wave = wave_id();
+  const int half = kGated && wave >= WH ? 1 : 0;
+  const int wl = wave - half * WH;
   const int64_t G = g0 + blockIdx.x;
+  const size_t region = kSb ? ((size_t)M * nblk * 65 * 4 + 15) / 16 * 16 : (size_t)W * M * 64 * 4;
   Out<M> o;
-  o.rec = reinterpret_cast<float*>(smem);
+  o.rec = reinterpret_cast<float*>(smem + half * region);
   o.dav = o.rec + M * nblk * 64;
   o.dbg = dbg;
   o.dbg_n = dbg_n;
@@ -565,21 +579,25 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
   o.r = r;
 #pragma unroll
   for (int mm = 0; mm < M; ++mm) o.acc[mm] = 0.0f;
-  const int b0 = wave * nblk / W, b1 = (wave + 1) * nblk / W;  // this wave's blocks
-  uint8_t* st = smem + (kSb ? ((size_t)M * nblk * 65 * 4 + 15) / 16 * 16 : (size_t)W * M * 64 * 4);
+  const int b0 = wl * nblk / WH, b1 = (wl + 1) * nblk / WH;  // this wave's blocks
   // bytes of the staged activation rows (the dummy area of the early path follows)
   const int stage_bytes = kSb ? M * nblk * kStageQ8K : M * nblk * ((WT == kQ4_K || WT == kQ6_K) ? 8 : 1) * kStage32;
+  uint8_t* st = smem + (kGated ? 2 : 1) * region + half * stage_bytes;
 
   // plane buffer resources of this row group (64 rows x nblk blocks)
   const int u0 = plane_unit(WT, 0), u1 = plane_unit(WT, 1);
+  const uint8_t* w0 = half ? q0 : p0;
+  const uint8_t* w1 = half ? q1 : p1;
   Rsrcs rs;
-  rs.r0 = rsrc(p0 + G * nblk * 64 * u0, (u32)(nblk * 64 * u0));
-  rs.r1 = rsrc(p1 + G * nblk * 64 * u1, (u32)(nblk * 64 * u1));
+  rs.r0 = rsrc(w0 + G * nblk * 64 * u0, (u32)(nblk * 64 * u0));
+  rs.r1 = rsrc(w1 + G * nblk * 64 * u1, (u32)(nblk * 64 * u1));
   rs.r2 = rs.r0;
   rs.r3 = rs.r0;
   if (WT == kQ6_K) {
-    rs.r2 = rsrc(p2 + G * nblk * 64 * 16, (u32)(nblk * 64 * 16));
-    rs.r3 = rsrc(p3 + G * nblk * 64 * 2, (u32)(nblk * 64 * 2));
+    const uint8_t* w2 = half ? q2 : p2;
+    const uint8_t* w3 = half ? q3 : p3;
+    rs.r2 = rsrc(w2 + G * nblk * 64 * 16, (u32)(nblk * 64 * 16));
+    rs.r3 = rsrc(w3 + G * nblk * 64 * 2, (u32)(nblk * 64 * 2));
   }
 
   // Activations of this slice first, so their latency hides behind the weight
@@ -653,27 +671,38 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
   __syncthreads();
   if (wave != 0) return;
   const int64_t n = o.n;
+  // the canonical chain acc = fma(da_b, t_b, acc) over a t-term region
+  auto chain = [&](const float* rec, int mm) {
+    const float* tp = rec + mm * nblk * 64 + r;
+    const float* dp = rec + M * nblk * 64 + mm * nblk;
+    float v = 0.0f;
+    int b = 0;
+    for (; b + 4 <= nblk; b += 4) {
+      const float t0 = tp[b * 64], t1 = tp[(b + 1) * 64], t2 = tp[(b + 2) * 64], t3 = tp[(b + 3) * 64];
+      const float d0 = dp[b], d1 = dp[b + 1], d2 = dp[b + 2], d3 = dp[b + 3];
+      v = fmaf(d0, t0, v);
+      v = fmaf(d1, t1, v);
+      v = fmaf(d2, t2, v);
+      v = fmaf(d3, t3, v);
+    }
+    for (; b < nblk; ++b) v = fmaf(dp[b], tp[b * 64], v);
+    return v;
+  };
 #pragma unroll
   for (int mm = 0; mm < M; ++mm) {
     float v = 0.0f;
     if (kSb) {
-      const float* tp = o.rec + mm * nblk * 64 + r;
-      const float* dp = o.dav + mm * nblk;
-      int b = 0;
-      for (; b + 4 <= nblk; b += 4) {
-        const float t0 = tp[b * 64], t1 = tp[(b + 1) * 64], t2 = tp[(b + 2) * 64], t3 = tp[(b + 3) * 64];
-        const float d0 = dp[b], d1 = dp[b + 1], d2 = dp[b + 2], d3 = dp[b + 3];
-        v = fmaf(d0, t0, v);
-        v = fmaf(d1, t1, v);
-        v = fmaf(d2, t2, v);
-        v = fmaf(d3, t3, v);
-      }
-      for (; b < nblk; ++b) v = fmaf(dp[b], tp[b * 64], v);
+      v = chain(o.rec, mm);
     } else {
 #pragma unroll
       for (int w = 0; w < W; ++w) v = v + o.rec[(w * M + mm) * 64 + r];
     }
-    if (n >= n0 && n < n1) y[mm * ys + n] = bias ? v + bias[n] : v;
+    if constexpr (kGated) {
+      const float vu = chain(reinterpret_cast<const float*>(smem + region), mm);
+      if (n >= n0 && n < n1) y[mm * ys + n] = act_apply(act, v) * vu;
+    } else {
+      if (n >= n0 && n < n1) y[mm * ys + n] = bias ? v + bias[n] : v;
+    }
   }
 }
 
@@ -715,7 +744,7 @@ static hipError_t gemv_launch(const WeightDev& w, const uint8_t* acts, int64_t a
   }
   hipLaunchKernelGGL((k_gemv<WT, AF, M, W, U, kFuse, kEarly>), dim3((unsigned)(g1 - g0)), dim3(64 * W), lds, s, w.plane[0],
                      w.plane[1], w.plane[2], w.plane[3], (int)w.nblk, g0, n0, n1, acts, arb, x, xs, y, ys, bias, dbg,
-                     w.n);
+                     w.n, nullptr, nullptr, nullptr, nullptr, 0);
   return hipGetLastError();
 }
 
@@ -805,6 +834,51 @@ static hipError_t gemv_rows(const WeightDev& w, int af, const uint8_t* acts, int
     r0 += rows;
   }
   return hipSuccess;
+}
+
+// The gated M = 1 GEMV: one workgroup per 64-row group holds both weights' rows,
+// W / 2 waves each, so the launch streams gate and up together and writes only
+// act(g) * u. 16-wave workgroups while the row groups fit on the CUs at once.
+template <int WT, int W, int kEarly>
+static hipError_t gated_launch(const WeightDev& wg, const WeightDev& wu, int act, const float* x, float* y,
+                               hipStream_t s) {
+  constexpr int U = W >= 16 ? 1 : 2;
+  const int64_t groups = (wg.n + kRowGroup - 1) / kRowGroup;
+  const size_t lds = 2 * gemv_lds_bytes(WT, kActQ8_K, 1, W, wg.nblk, false) + (kEarly > 0 ? kDummyBytes : 0);
+  if (lds > kGemvMaxLds) return hipErrorInvalidValue;
+  const void* fn = reinterpret_cast<const void*>(&k_gemv<WT, kActQ8_K, 1, W, U, true, kEarly, true>);
+  if (lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((k_gemv<WT, kActQ8_K, 1, W, U, true, kEarly, true>), dim3((unsigned)groups), dim3(64 * W), lds, s,
+                     wg.plane[0], wg.plane[1], wg.plane[2], wg.plane[3], (int)wg.nblk, (int64_t)0, (int64_t)0, wg.n,
+                     nullptr, (int64_t)0, x, wg.k, y, wg.n, nullptr, nullptr, wg.n, wu.plane[0], wu.plane[1],
+                     wu.plane[2], wu.plane[3], act);
+  return hipGetLastError();
+}
+
+template <int WT, int W>
+static hipError_t gated_waves(const WeightDev& wg, const WeightDev& wu, int act, const float* x, float* y,
+                              hipStream_t s) {
+  const int64_t per_wave = (wg.nblk + W / 2 - 1) / (W / 2);
+  if (per_wave == 1) return gated_launch<WT, W, 1>(wg, wu, act, x, y, s);
+  if (per_wave == 2) return gated_launch<WT, W, 2>(wg, wu, act, x, y, s);
+  return gated_launch<WT, W, 0>(wg, wu, act, x, y, s);
+}
+
+bool gemv_gated_supported(const WeightDev& wg, const WeightDev& wu) {
+  if ((wg.dtype != kQ4_K && wg.dtype != kQ6_K) || wu.dtype != wg.dtype || wu.n != wg.n || wu.k != wg.k) return false;
+  return 2 * gemv_lds_bytes(wg.dtype, kActQ8_K, 1, 16, wg.nblk, false) + kDummyBytes <= kGemvMaxLds &&
+         wg.k * 4 < ((int64_t)1 << 32);
+}
+
+hipError_t launch_gemv_gated(const WeightDev& wg, const WeightDev& wu, int act, const float* x, float* y,
+                             hipStream_t s) {
+  if (!gemv_gated_supported(wg, wu) || !act_ok(act)) return hipErrorInvalidValue;
+  const bool wide = (wg.n + kRowGroup - 1) / kRowGroup <= wg.cus;
+  if (wg.dtype == kQ4_K) return wide ? gated_waves<kQ4_K, 16>(wg, wu, act, x, y, s) : gated_waves<kQ4_K, 8>(wg, wu, act, x, y, s);
+  return wide ? gated_waves<kQ6_K, 16>(wg, wu, act, x, y, s) : gated_waves<kQ6_K, 8>(wg, wu, act, x, y, s);
 }
 
 hipError_t launch_gemv(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,

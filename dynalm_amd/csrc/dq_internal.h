@@ -47,11 +47,15 @@ hipError_t launch_gemv_mma(const WeightDev& w, int af, const uint8_t* acts, int6
                            int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s);
 constexpr int64_t kSkinnyMaxRows = 64;
 bool gemv_mma_supported(int dtype, int af, int64_t m);
-// Whether the skinny kernel's LDS holds the t-terms of nblk super-blocks for m rows.
-bool gemv_mma_lds_ok(int64_t nblk, int64_t m);
+// Gated jobs (two weights per workgroup) take at most one activation tile.
+constexpr int64_t kSkinnyGatedMaxRows = 16;
+// Whether the skinny kernel's LDS holds the t-terms of nblk super-blocks for m rows
+// (gated: of two weights).
+bool gemv_mma_lds_ok(int64_t nblk, int64_t m, bool gated = false);
 // One matmul of a grouped skinny launch: y[r, i] (+ bias) for r < m, i < w->n, from
 // either pre-quantized Q8_K rows (acts, arb bytes apart) or fp32 rows that the
-// kernel quantizes (x != nullptr, xs floats apart).
+// kernel quantizes (x != nullptr, xs floats apart). wu != nullptr: a gated job,
+// y[r, i] = act(x . w^T) * (x . wu^T) with wu of w's type and shape and no bias.
 struct GemvJob {
   const WeightDev* w;
   const uint8_t* acts;
@@ -62,6 +66,8 @@ struct GemvJob {
   float* y;
   int64_t ys;
   const float* bias;
+  const WeightDev* wu = nullptr;
+  int act = 0;
 };
 // Grouped skinny MFMA GEMV: jobs of one K (same nblk) and one input kind (all
 // fused or none), Q4_K / Q6_K, 2 <= m <= 64 (fused: m <= 16), in launches of up to
@@ -73,5 +79,14 @@ hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s);
 // when this is large.
 int64_t skinny_units(const GemvJob* jobs, int count);
 constexpr int64_t kSkinnyFuseMaxUnits = 1024;
+// The gated M = 1 decode GEMV: y[i] = act(x . wg_i) * (x . wu_i) for one fp32 row x,
+// K-quant weights of one type and shape, activations quantized in the kernel.
+// hipErrorInvalidValue when the pair or its LDS is not supported.
+bool gemv_gated_supported(const WeightDev& wg, const WeightDev& wu);
+hipError_t launch_gemv_gated(const WeightDev& wg, const WeightDev& wu, int act, const float* x, float* y,
+                             hipStream_t s);
+// out[r, c] = act(g[r, c]) * u[r, c] for r < m, c < n (strides in floats).
+hipError_t launch_act_mul(int act, const float* g, int64_t gs, const float* u, int64_t us, int64_t m, int64_t n,
+                          float* out, int64_t os, hipStream_t s);
 
 }  // namespace dq

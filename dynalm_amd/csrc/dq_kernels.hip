@@ -12,6 +12,7 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include "dq_act.h"
 #include "dq_device.h"
 #include "dq_internal.h"
 #include "dq_quant.h"
@@ -161,6 +162,37 @@ __global__ __launch_bounds__(256) void k_units(int t, int af, const uint8_t* p0,
   units[idx] = s;
 }
 
+// ===================================================================== act_mul
+// out[r, c] = act(g[r, c]) * u[r, c] (dynacore/cpu/cpu_device.cpp:1912-1930): the
+// unfused tail of the gated projection. Thread t of a 256-thread block handles 4
+// columns of one row (one 16-byte load of each input when kVec), rows in the grid's
+// y dimension and then in steps of gridDim.y.
+// (no __restrict__: out may alias an input; each element is read before it is written)
+template <bool kVec>
+__global__ __launch_bounds__(256) void k_act_mul(int act, const float* g, int64_t gs, const float* u, int64_t us,
+                                                 int64_t m, int64_t n, float* o, int64_t os) {
+  const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (c >= n) return;
+  for (int64_t r = blockIdx.y; r < m; r += gridDim.y) {
+    const float* gr = g + r * gs + c;
+    const float* ur = u + r * us + c;
+    float* orow = o + r * os + c;
+    if (kVec) {
+      const float4 gv = *reinterpret_cast<const float4*>(gr);
+      const float4 uv = *reinterpret_cast<const float4*>(ur);
+      float4 ov;
+      ov.x = act_apply(act, gv.x) * uv.x;
+      ov.y = act_apply(act, gv.y) * uv.y;
+      ov.z = act_apply(act, gv.z) * uv.z;
+      ov.w = act_apply(act, gv.w) * uv.w;
+      *reinterpret_cast<float4*>(orow) = ov;
+    } else {
+      const int64_t e = n - c < 4 ? n - c : 4;
+      for (int64_t i = 0; i < e; ++i) orow[i] = act_apply(act, gr[i]) * ur[i];
+    }
+  }
+}
+
 // ================================================================ launchers
 
 static inline dim3 grid1(int64_t total, int block) { return dim3((unsigned)((total + block - 1) / block)); }
@@ -197,6 +229,22 @@ hipError_t launch_unpack(int t, uint8_t* dst, int64_t row_stride, int64_t n, int
   const int64_t total = n * nblk * block_bytes(t);
   if (total == 0) return hipSuccess;
   hipLaunchKernelGGL(k_repack<false>, grid1(total, 256), dim3(256), 0, s, t, nullptr, dst, row_stride, n, nblk, pl);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_mul(int act, const float* g, int64_t gs, const float* u, int64_t us, int64_t m, int64_t n,
+                          float* out, int64_t os, hipStream_t s) {
+  if (m == 0 || n == 0) return hipSuccess;
+  if (!act_ok(act)) return hipErrorInvalidValue;
+  const auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  const bool vec = n % 4 == 0 && (m == 1 || (gs % 4 == 0 && us % 4 == 0 && os % 4 == 0)) && al16(g) && al16(u) &&
+                   al16(out);
+  const dim3 grid((unsigned)((n + 1023) / 1024), (unsigned)(m < 65535 ? m : 65535));
+  if (vec) {
+    hipLaunchKernelGGL(k_act_mul<true>, grid, dim3(256), 0, s, act, g, gs, u, us, m, n, out, os);
+  } else {
+    hipLaunchKernelGGL(k_act_mul<false>, grid, dim3(256), 0, s, act, g, gs, u, us, m, n, out, os);
+  }
   return hipGetLastError();
 }
 

@@ -41,9 +41,18 @@
 // workgroup finds its job in a table passed by value, and Q4_K and Q6_K jobs mix
 // in one launch (as dynacore's Device::matmul_many runs every job's row chunks in
 // one parallel region, dynacore/cpu/cpu_device.cpp:500-692).
+//
+// kGated: a job carries a second weight of the same type and shape (the up
+// projection) and writes act(x . Wg^T) * (x . Wu^T), the gated MLP projection of
+// dynacore's Device::matmul_gated (dynacore/include/dynacore/device/device.h:188-199).
+// Each wave multiplies one activation super-block with both weights' tiles, the
+// t-terms of both go to LDS, and the chains end in act(g) * u: one launch and no
+// gate / up round trip through memory, as CpuDevice's decode path applies the
+// activation per 16-column chunk (dynacore/cpu/cpu_device.cpp:1940-1984).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "dq_act.h"
 #include "dq_device.h"
 #include "dq_internal.h"
 #include "dq_mfma.h"
@@ -54,10 +63,8 @@ namespace dq {
 namespace {
 
 struct SkinnyJob {
-  const uint8_t* p0;  // weight planes (dq_layout.h)
-  const uint8_t* p1;
-  const uint8_t* p2;
-  const uint8_t* p3;
+  const uint8_t* p[4];        // weight planes (dq_layout.h)
+  const uint8_t* pu[4];       // kGated: the up projection's planes (same type and shape)
   int64_t n_pad, t0, n0, n1;  // rows (padded to 64), first tile, output row range
   const uint8_t* acts;        // !kFused: m rows of Q8_K, arb bytes apart
   int64_t arb;
@@ -67,6 +74,7 @@ struct SkinnyJob {
   int64_t ys;
   const float* bias;
   int dtype, m;
+  int act;  // kGated: the activation applied to the gate projection
   int wg0;  // first workgroup of this job in the grid
 };
 constexpr int kSkinnyMaxJobs = 8;
@@ -284,36 +292,50 @@ struct WRes;
 template <int CT>
 struct WRes<kQ4_K, CT> {
   __amdgpu_buffer_rsrc_t rq, rh;
-  DQ_DEV void init(const SkinnyJob& J, int64_t G, int nblk, bool ok) {
-    rq = rsrc(J.p0 + G * nblk * 8192, ok ? (u32)(nblk * 8192) : 0u);
-    rh = rsrc(J.p1 + G * nblk * 1024, ok ? (u32)(nblk * 1024) : 0u);
+  DQ_DEV void init(const uint8_t* const* p, int64_t G, int nblk, bool ok) {
+    rq = rsrc(p[0] + G * nblk * 8192, ok ? (u32)(nblk * 8192) : 0u);
+    rh = rsrc(p[1] + G * nblk * 1024, ok ? (u32)(nblk * 1024) : 0u);
   }
   DQ_DEV void load(WSB<kQ4_K, CT>& w, int b, int r0, int li, int lg) const { w.load(rq, rh, b, r0, li, lg); }
 };
 template <int CT>
 struct WRes<kQ6_K, CT> {
   __amdgpu_buffer_rsrc_t rp[4];
-  DQ_DEV void init(const SkinnyJob& J, int64_t G, int nblk, bool ok) {
-    rp[0] = rsrc(J.p0 + G * nblk * 8192, ok ? (u32)(nblk * 8192) : 0u);
-    rp[1] = rsrc(J.p1 + G * nblk * 4096, ok ? (u32)(nblk * 4096) : 0u);
-    rp[2] = rsrc(J.p2 + G * nblk * 1024, ok ? (u32)(nblk * 1024) : 0u);
-    rp[3] = rsrc(J.p3 + G * nblk * 128, ok ? (u32)(nblk * 128) : 0u);
+  DQ_DEV void init(const uint8_t* const* p, int64_t G, int nblk, bool ok) {
+    rp[0] = rsrc(p[0] + G * nblk * 8192, ok ? (u32)(nblk * 8192) : 0u);
+    rp[1] = rsrc(p[1] + G * nblk * 4096, ok ? (u32)(nblk * 4096) : 0u);
+    rp[2] = rsrc(p[2] + G * nblk * 1024, ok ? (u32)(nblk * 1024) : 0u);
+    rp[3] = rsrc(p[3] + G * nblk * 128, ok ? (u32)(nblk * 128) : 0u);
   }
   DQ_DEV void load(WSB<kQ6_K, CT>& w, int b, int r0, int li, int lg) const { w.load(rp, b, r0, li, lg); }
 };
 
-// One wave's super-blocks [b0, b1) of one job: activations, weights, t-terms to LDS.
+// One wave's super-blocks [b0, b1) of one job: activations, weights, t-terms to LDS
+// (kGated: the up projection's t-terms to tu, from the same activation operand).
 // CT == 1 keeps the next super-block's weight loads in flight during the compute
 // (activation loads of b are issued before the weight loads of b + 1, so waiting
 // for them does not wait for the prefetch: loads retire in order).
-template <int WT, int CT, int MT, bool kFused>
+template <int WT, int CT, int MT, bool kFused, bool kGated>
 DQ_DEV void skinny_wave(const SkinnyJob& J, int nblk, int64_t G, int r0, bool ok, int b0, int b1, float* tt,
-                        float* dal, int li, int lg) {
+                        float* tu, float* dal, int li, int lg) {
   constexpr int NC = 16 * CT, NR = 16 * MT;
-  WRes<WT, CT> res;
-  res.init(J, G, nblk, ok);
+  static_assert(!kGated || CT == 1, "gated jobs run 16-row tiles");
+  WRes<WT, CT> res, resu;
+  res.init(J.p, G, nblk, ok);
+  if constexpr (kGated) resu.init(J.pu, G, nblk, ok);
   ActSrc<kFused> src;
   src.init(J);
+  auto emit_t = [&](const WSB<WT, CT>& w, const ActSB<MT>& A, int b, float* to) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      float t[MT][4];
+      tterms<CT, MT>(w, ct, A, lg, t);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) to[(b * NR + 16 * mt + 4 * lg + e) * NC + 16 * ct + li] = t[mt][e];
+    }
+  };
   auto emit = [&](const WSB<WT, CT>& w, const ActSB<MT>& A, int b) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
@@ -340,7 +362,25 @@ DQ_DEV void skinny_wave(const SkinnyJob& J, int nblk, int64_t G, int r0, bool ok
     }
   };
   if (b0 >= b1) return;
-  if constexpr (CT == 1) {
+  if constexpr (kGated) {
+    // the up tile of b loads while the gate tile of b computes, the gate tile of
+    // b + 1 while the up tile computes: two weight tiles live at a time, as in
+    // the single-weight pipeline below
+    WSB<WT, CT> cur;
+    res.load(cur, b0, r0, li, lg);
+    for (int b = b0; b < b1; ++b) {
+      ActSB<MT> A;
+      act(b, A);
+      WSB<WT, CT> up;
+      resu.load(up, b, r0, li, lg);
+      __builtin_amdgcn_sched_barrier(0);
+      emit(cur, A, b);
+      __builtin_amdgcn_sched_barrier(0);
+      res.load(cur, b + 1 < b1 ? b + 1 : b, r0, li, lg);
+      __builtin_amdgcn_sched_barrier(0);
+      emit_t(up, A, b, tu);
+    }
+  } else if constexpr (CT == 1) {
     WSB<WT, CT> cur;
     res.load(cur, b0, r0, li, lg);
     for (int b = b0; b < b1; ++b) {
@@ -366,7 +406,7 @@ DQ_DEV void skinny_wave(const SkinnyJob& J, int nblk, int64_t G, int r0, bool ok
   }
 }
 
-template <int CT, int MT, bool kFused>
+template <int CT, int MT, bool kFused, bool kGated>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void k_skinny(SkinnyGroup g) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int W = kSkinnyWaves;
@@ -376,8 +416,9 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void k_skinny(SkinnyGroup g) {
   while (j + 1 < g.count && wg >= g.job[j + 1].wg0) ++j;
   const SkinnyJob& J = g.job[j];
   const int nblk = g.nblk;
-  float* tt = reinterpret_cast<float*>(lds);  // [nblk][NR activation rows][NC weight rows]
-  float* dal = tt + nblk * NR * NC;           // [nblk][NR] activation d
+  float* tt = reinterpret_cast<float*>(lds);        // [nblk][NR activation rows][NC weight rows]
+  float* tu = tt + (kGated ? nblk * NR * NC : 0);  // kGated: the up projection's, same shape
+  float* dal = tu + nblk * NR * NC;                // [nblk][NR] activation d
   const int l = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = l & 15, lg = l >> 4;
   const int64_t row0 = (J.t0 + (wg - J.wg0)) * NC;  // first weight row of the tile
@@ -386,45 +427,52 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void k_skinny(SkinnyGroup g) {
   const bool ok = row0 < J.n_pad;
   const int b0 = wave * nblk / W, b1 = (wave + 1) * nblk / W;
   if (J.dtype == kQ6_K) {
-    skinny_wave<kQ6_K, CT, MT, kFused>(J, nblk, G, r0, ok, b0, b1, tt, dal, li, lg);
+    skinny_wave<kQ6_K, CT, MT, kFused, kGated>(J, nblk, G, r0, ok, b0, b1, tt, tu, dal, li, lg);
   } else {
-    skinny_wave<kQ4_K, CT, MT, kFused>(J, nblk, G, r0, ok, b0, b1, tt, dal, li, lg);
+    skinny_wave<kQ4_K, CT, MT, kFused, kGated>(J, nblk, G, r0, ok, b0, b1, tt, tu, dal, li, lg);
   }
   __syncthreads();
   // the in-order chains of the tile's NR x NC outputs, shared by all waves
   for (int o = threadIdx.x; o < NR * NC; o += W * 64) {
     const int mm = o / NC, c = o % NC;
-    float v = 0.0f;
-    for (int b = 0; b < nblk; ++b) v = fmaf(dal[b * NR + mm], tt[(b * NR + mm) * NC + c], v);
+    float v = 0.0f, vu = 0.0f;
+    for (int b = 0; b < nblk; ++b) {
+      const float da = dal[b * NR + mm];
+      v = fmaf(da, tt[(b * NR + mm) * NC + c], v);
+      if (kGated) vu = fmaf(da, tu[(b * NR + mm) * NC + c], vu);
+    }
     const int64_t n = row0 + c;
-    if (mm < J.m && n >= J.n0 && n < J.n1) J.y[mm * J.ys + n] = J.bias ? v + J.bias[n] : v;
+    if (mm < J.m && n >= J.n0 && n < J.n1) {
+      if (kGated) {
+        J.y[mm * J.ys + n] = act_apply(J.act, v) * vu;
+      } else {
+        J.y[mm * J.ys + n] = J.bias ? v + J.bias[n] : v;
+      }
+    }
   }
 }
 
-size_t skinny_lds(int64_t nblk, int ct, int mt) {
-  return (size_t)nblk * (16 * mt * (16 * ct + 1)) * sizeof(float);
+size_t skinny_lds(int64_t nblk, int ct, int mt, bool gated = false) {
+  return (size_t)nblk * (16 * mt * (16 * ct * (gated ? 2 : 1) + 1)) * sizeof(float);
 }
 constexpr size_t kSkinnyMaxLds = 160 * 1024;
 
-template <int CT, int MT, bool kFused>
+template <int CT, int MT, bool kFused, bool kGated = false>
 hipError_t skinny_launch(const SkinnyGroup& g, int wgs, hipStream_t s) {
-  const size_t lds = skinny_lds(g.nblk, CT, MT);
+  const size_t lds = skinny_lds(g.nblk, CT, MT, kGated);
   if (lds > kSkinnyMaxLds) return hipErrorInvalidValue;
   if (lds > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_skinny<CT, MT, kFused>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_skinny<CT, MT, kFused, kGated>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((k_skinny<CT, MT, kFused>), dim3((unsigned)wgs), dim3(kSkinnyWaves * 64), lds, s, g);
+  hipLaunchKernelGGL((k_skinny<CT, MT, kFused, kGated>), dim3((unsigned)wgs), dim3(kSkinnyWaves * 64), lds, s, g);
   return hipGetLastError();
 }
 
 SkinnyJob skinny_job(const WeightDev& w, int64_t m, int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias) {
   SkinnyJob J{};
-  J.p0 = w.plane[0];
-  J.p1 = w.plane[1];
-  J.p2 = w.plane[2];
-  J.p3 = w.plane[3];
+  for (int i = 0; i < 4; ++i) J.p[i] = w.plane[i];
   J.n_pad = w.n_pad;
   J.n0 = n0;
   J.n1 = n1;
@@ -443,8 +491,8 @@ int skinny_ct(int64_t wgs16, int64_t nblk, int cus, int mt) {
   return mt == 1 && wgs16 >= 16 * (int64_t)cus && skinny_lds(nblk, 4, 1) <= kSkinnyMaxLds ? 4 : 1;
 }
 
-hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t* last_row, bool fused, int cus,
-                        hipStream_t s) {
+hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t* last_row, bool fused, bool gated,
+                        int cus, hipStream_t s) {
   int mmax = 0;
   int64_t wgs16 = 0;
   for (int i = 0; i < g.count; ++i) {
@@ -453,7 +501,7 @@ hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t*
   }
   const int mt = mmax > 16 ? 4 : 1;
   if (mt == 4 && fused) return hipErrorInvalidValue;
-  const int ct = skinny_ct(wgs16, g.nblk, cus, mt);
+  const int ct = gated ? 1 : skinny_ct(wgs16, g.nblk, cus, mt);
   const int nc = 16 * ct;
   int64_t wgs = 0;
   for (int i = 0; i < g.count; ++i) {
@@ -462,6 +510,11 @@ hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t*
     wgs += (last_row[i] + nc - 1) / nc - first_row[i] / nc;
   }
   if (wgs >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+  if (gated) {
+    // one activation tile: with four, two weights' operands exceed the register file
+    if (mt == 4) return hipErrorInvalidValue;
+    return fused ? skinny_launch<1, 1, true, true>(g, (int)wgs, s) : skinny_launch<1, 1, false, true>(g, (int)wgs, s);
+  }
   if (mt == 4) return skinny_launch<1, 4, false>(g, (int)wgs, s);
   if (ct == 4) return fused ? skinny_launch<4, 1, true>(g, (int)wgs, s) : skinny_launch<4, 1, false>(g, (int)wgs, s);
   return fused ? skinny_launch<1, 1, true>(g, (int)wgs, s) : skinny_launch<1, 1, false>(g, (int)wgs, s);
@@ -473,7 +526,9 @@ bool gemv_mma_supported(int dtype, int af, int64_t m) {
   return (dtype == kQ4_K || dtype == kQ6_K) && af == kActQ8_K && m >= 2 && m <= kSkinnyMaxRows;
 }
 
-bool gemv_mma_lds_ok(int64_t nblk, int64_t m) { return skinny_lds(nblk, 1, m > 16 ? 4 : 1) <= kSkinnyMaxLds; }
+bool gemv_mma_lds_ok(int64_t nblk, int64_t m, bool gated) {
+  return skinny_lds(nblk, 1, m > 16 ? 4 : 1, gated) <= kSkinnyMaxLds;
+}
 
 int64_t skinny_units(const GemvJob* jobs, int count) {
   if (count <= 0) return 0;
@@ -481,7 +536,7 @@ int64_t skinny_units(const GemvJob* jobs, int count) {
   for (int i = 0; i < count; ++i) wgs16 += (jobs[i].w->n + 15) / 16;
   int64_t mmax = 0;
   for (int i = 0; i < count; ++i) mmax = jobs[i].m > mmax ? jobs[i].m : mmax;
-  const int ct = skinny_ct(wgs16, jobs[0].w->nblk, jobs[0].w->cus, mmax > 16 ? 4 : 1);
+  const int ct = jobs[0].wu != nullptr ? 1 : skinny_ct(wgs16, jobs[0].w->nblk, jobs[0].w->cus, mmax > 16 ? 4 : 1);
   int64_t wgs = 0;
   for (int i = 0; i < count; ++i) wgs += (jobs[i].w->n + 16 * ct - 1) / (16 * ct);
   return wgs * jobs[0].w->nblk;
@@ -497,7 +552,7 @@ hipError_t launch_gemv_mma(const WeightDev& w, int af, const uint8_t* acts, int6
   g.job[0].arb = arb;
   g.count = 1;
   g.nblk = (int)w.nblk;
-  return launch_group(g, &n0, &n1, false, w.cus, s);
+  return launch_group(g, &n0, &n1, false, false, w.cus, s);
 }
 
 hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s) {
@@ -505,14 +560,23 @@ hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s) {
     SkinnyGroup g;
     g.count = count - i0 < kSkinnyMaxJobs ? count - i0 : kSkinnyMaxJobs;
     g.nblk = (int)jobs[i0].w->nblk;
-    const bool fused = jobs[i0].x != nullptr;
+    const bool fused = jobs[i0].x != nullptr, gated = jobs[i0].wu != nullptr;
     int64_t first[kSkinnyMaxJobs], last[kSkinnyMaxJobs];
     for (int i = 0; i < g.count; ++i) {
       const GemvJob& q = jobs[i0 + i];
-      if (q.w->nblk != g.nblk || !gemv_mma_supported(q.w->dtype, kActQ8_K, q.m) || (q.x != nullptr) != fused) {
+      if (q.w->nblk != g.nblk || !gemv_mma_supported(q.w->dtype, kActQ8_K, q.m) || (q.x != nullptr) != fused ||
+          (q.wu != nullptr) != gated) {
+        return hipErrorInvalidValue;
+      }
+      if (gated && (q.wu->dtype != q.w->dtype || q.wu->n != q.w->n || q.wu->k != q.w->k || q.bias != nullptr ||
+                    !act_ok(q.act) || q.m > kSkinnyGatedMaxRows)) {
         return hipErrorInvalidValue;
       }
       g.job[i] = skinny_job(*q.w, q.m, 0, q.w->n, q.y, q.ys, q.bias);
+      if (gated) {
+        for (int p = 0; p < 4; ++p) g.job[i].pu[p] = q.wu->plane[p];
+        g.job[i].act = q.act;
+      }
       g.job[i].acts = q.acts;
       g.job[i].arb = q.arb;
       g.job[i].x = q.x;
@@ -520,7 +584,7 @@ hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s) {
       first[i] = 0;
       last[i] = q.w->n;
     }
-    const hipError_t e = launch_group(g, first, last, fused, jobs[i0].w->cus, s);
+    const hipError_t e = launch_group(g, first, last, fused, gated, jobs[i0].w->cus, s);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

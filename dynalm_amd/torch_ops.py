@@ -71,3 +71,22 @@ def matmul_many(jobs) -> list[torch.Tensor]:
         spec.append((w, x, x.shape[0], x.stride(0), y, y.stride(0), bias))
     dq.matmul_many(spec, stream())
     return outs
+
+
+def act_mul(act: int, gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """act(gate) * up for [m, n] fp32 tensors on the GPU (Device::act_mul)."""
+    m, n = gate.shape
+    o = torch.empty((m, n), dtype=torch.float32, device=gate.device) if out is None else out
+    dq.act_mul(act, gate, gate.stride(0), up, up.stride(0), m, n, o, o.stride(0), stream())
+    return o
+
+
+def matmul_gated(act: int, x: torch.Tensor, w_gate: dq.Weight, w_up: dq.Weight, out: torch.Tensor | None = None,
+                 scratch: tuple[torch.Tensor, torch.Tensor] | None = None) -> torch.Tensor:
+    """act(x . w_gate^T) * (x . w_up^T) for x [m, k] fp32 on the GPU (Device::matmul_gated)."""
+    m = x.shape[0]
+    o = torch.empty((m, w_gate.n), dtype=torch.float32, device=x.device) if out is None else out
+    gs, us = scratch if scratch is not None else (None, None)
+    dq.matmul_gated(act, x, m, x.stride(0), w_gate, w_up, o, o.stride(0), gs, us,
+                    gs.stride(0) if gs is not None else 0, stream())
+    return o

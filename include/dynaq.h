@@ -165,6 +165,40 @@ typedef struct dq_matmul_job {
  * runs all jobs' row chunks in one parallel region). */
 DQ_API int dq_matmul_many(const dq_matmul_job* jobs, int64_t n_jobs, void* stream);
 
+/* Activations of the gated MLP projection: dynacore::Activation
+ * (dynacore/include/dynacore/device/ops.h:14), with the reference's fp32 formulas
+ * (dynacore/cpu/cpu_device.cpp:117-134): SiLU x / (1 + e^-x) through exp_nonpos
+ * (dynacore/include/dynacore/base/fast_exp.h:16-35), bit-identical to the
+ * reference; GELU 0.5 x (1 + erf(x / sqrt 2)) and its tanh form, within a few ulp
+ * of the reference (device erff / tanhf). */
+typedef enum dq_activation {
+  DQ_SILU = 0,
+  DQ_GELU = 1,
+  DQ_GELU_TANH = 2,
+} dq_activation;
+
+/* out[r * out_stride + c] = act(gate[r * gate_stride + c]) * up[r * up_stride + c]
+ * for r < m, c < n (fp32). Replaces Device::act_mul
+ * (dynacore/include/dynacore/device/device.h:186-187; CpuDevice::act_mul,
+ * dynacore/cpu/cpu_device.cpp:1912-1930). out may alias gate or up. */
+DQ_API int dq_act_mul(int act, const float* gate, int64_t gate_stride, const float* up, int64_t up_stride, int64_t m,
+                      int64_t n, float* out, int64_t out_stride, void* stream);
+
+/* out = act(x . w_gate^T) * (x . w_up^T): the gated MLP projection (SwiGLU /
+ * GeGLU) of m rows of x (x_stride floats apart, k values each); w_gate and w_up
+ * have the same n and k; out has out_stride floats per row; no bias. Replaces
+ * Device::matmul_gated (dynacore/include/dynacore/device/device.h:188-199;
+ * CpuDevice::matmul_gated, dynacore/cpu/cpu_device.cpp:1931-2072).
+ *   - Q4_K / Q6_K weights of one type, m <= 16: one fused launch that streams both
+ *     weights and writes only act(g) * u (no gate / up round trip);
+ *   - otherwise both projections as dq_matmul computes them, into gate_scratch and
+ *     up_scratch (m rows of scratch_stride floats each, clobbered), then dq_act_mul.
+ *     NULL scratch pointers (both) select a per-device library buffer.
+ * Every path gives the bits of act(dq_matmul(x, w_gate)) * dq_matmul(x, w_up). */
+DQ_API int dq_matmul_gated(int act, const float* x, int64_t m, int64_t x_stride, const dq_weight* w_gate,
+                           const dq_weight* w_up, float* out, int64_t out_stride, float* gate_scratch,
+                           float* up_scratch, int64_t scratch_stride, void* stream);
+
 /* Exact integer partials of every (activation row r < m, weight row i < n):
  * units[(r * n + i) * U + u] and sb[(r * n + i) * S + s], with U and S from
  * dq_partials_count; the meaning of each is that of the CPU reference's integer

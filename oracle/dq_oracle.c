@@ -758,3 +758,48 @@ void dqo_fill_bytes(uint64_t seed, uint8_t* out, int64_t n) {
     for (int j = 0; j < 8 && i + j < n; ++j) out[i + j] = (uint8_t)(v >> (8 * j));
   }
 }
+
+/* ---------------------------------------------------------- activations */
+
+/* fast_exp.h:16-35: the comparison clamp (NaN -> -87), round to nearest through
+ * 1.5 * 2^23, r = x - n ln2 in two parts, Horner degree 6, times 2^n. With
+ * -ffp-contract=off each product and sum rounds where written. */
+float dqo_exp_nonpos(float x) {
+  x = x > -87.0f ? (x < 88.0f ? x : 88.0f) : -87.0f;
+  const float n = (x * 1.44269504088896341f + 12582912.0f) - 12582912.0f;
+  const float r = x - n * 0.693145751953125f - n * 1.428606765330187e-06f;
+  float p = 1.0f / 720;
+  p = p * r + 1.0f / 120;
+  p = p * r + 1.0f / 24;
+  p = p * r + 1.0f / 6;
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  const uint32_t bits = (uint32_t)((int32_t)n + 127) << 23;
+  float scale;
+  memcpy(&scale, &bits, 4);
+  return p * scale;
+}
+
+/* cpu_device.cpp:117-128: silu(x) = x * (x >= 0 ? 1 : e) / (1 + e), e = e^-|x|;
+ * gelu(x) = 0.5 x (1 + erf(x / sqrt 2)); gelu_tanh with sqrt(2 / pi). */
+static float act1(int act, float x) {
+  switch (act) {
+    case DQO_SILU: {
+      const float e = dqo_exp_nonpos(-fabsf(x));
+      return x * (x >= 0.0f ? 1.0f : e) / (1.0f + e);
+    }
+    case DQO_GELU:
+      return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+    default: {
+      const float kc = 0.7978845608028654f;
+      return 0.5f * x * (1.0f + tanhf(kc * (x + 0.044715f * x * x * x)));
+    }
+  }
+}
+
+int dqo_activation(int act, const float* x, float* y, int64_t n) {
+  if (act != DQO_SILU && act != DQO_GELU && act != DQO_GELU_TANH) return -1;
+  for (int64_t i = 0; i < n; ++i) y[i] = act1(act, x[i]);
+  return 0;
+}

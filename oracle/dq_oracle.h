@@ -107,6 +107,15 @@ float dqo_dot(int wtype, int fmt, const void* wrow, const void* arow, int64_t k)
 int dqo_matmul(int wtype, int fmt, const void* w, int64_t w_row_bytes, int64_t n, const void* acts,
                int64_t a_row_bytes, int64_t m, int64_t k, float* y, int64_t y_stride, const float* bias);
 
+/* Activations of the gated MLP projection (dynacore Activation, ops.h:14):
+ * 0 SiLU, 1 GELU (erf form), 2 GELU (tanh form). */
+enum { DQO_SILU = 0, DQO_GELU = 1, DQO_GELU_TANH = 2 };
+/* e^x for x <= 0 by Cody-Waite reduction and a degree-6 polynomial, plain
+ * multiplies and adds (dynacore/include/dynacore/base/fast_exp.h:16-35). */
+float dqo_exp_nonpos(float x);
+/* y[i] = act(x[i]) (dynacore/cpu/cpu_device.cpp:117-134); -1 for an unknown act. */
+int dqo_activation(int act, const float* x, float* y, int64_t n);
+
 /* Deterministic inputs: splitmix64 stream, Box-Muller normals in double, cast to
  * fp32. A fraction outlier_frac of positions (chosen from the same stream) is set
  * to +-outlier_sigma * std. */

@@ -55,6 +55,8 @@ def _load_oracle():
         "dqo_matmul": (C.c_int, [C.c_int, C.c_int, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _P]),
         "dqo_fill_normal": (None, [C.c_uint64, _P, _I64, C.c_double, C.c_double, C.c_double, C.c_double]),
         "dqo_fill_bytes": (None, [C.c_uint64, _P, _I64]),
+        "dqo_exp_nonpos": (C.c_float, [C.c_float]),
+        "dqo_activation": (C.c_int, [C.c_int, _P, _P, _I64]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -196,6 +198,34 @@ def matmul(wtype: int, fmt: int, w: np.ndarray, a: np.ndarray, k: int, bias: np.
     return y
 
 
+# ------------------------------------------------------------ activations
+
+
+SILU, GELU, GELU_TANH = 0, 1, 2
+
+
+def exp_nonpos(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    return np.array([lib().dqo_exp_nonpos(float(v)) for v in x], np.float32)
+
+
+def activation(act: int, x: np.ndarray) -> np.ndarray:
+    """act(x) elementwise (dynacore Activation: 0 SiLU, 1 GELU, 2 GELU-tanh)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    _check(lib().dqo_activation(act, _ptr(x), _ptr(y), x.size), "dqo_activation")
+    return y
+
+
+def matmul_gated(act: int, wt_gate: int, wt_up: int, fmt: int, w_gate: np.ndarray, w_up: np.ndarray, a: np.ndarray,
+                 k: int) -> np.ndarray:
+    """act(x . w_gate^T) * (x . w_up^T) on quantized activations a (Device::matmul_gated,
+    dynacore/include/dynacore/device/device.h:188-199; the product in fp32)."""
+    g = matmul(wt_gate, fmt, w_gate, a, k)
+    u = matmul(wt_up, fmt, w_up, a, k)
+    return (activation(act, g) * u).astype(np.float32)
+
+
 # ------------------------------------------------------------ reference
 
 
@@ -228,6 +258,7 @@ def ref():
             "ref_dot_rows_n": (C.c_int, [C.c_int, C.c_int, _P, _I64, _I64, _I64, _P, _I64, C.c_int, _I64, _P, _I64, _P]),
             "ref_bench_gemv": (_I64, [C.c_int, C.c_int, C.POINTER(_P), C.c_int, _I64, _I64, _P, _I64, C.c_int, _I64, _P,
                                       C.c_int, C.c_int]),
+            "ref_exp_nonpos": (C.c_float, [C.c_float]),
         }
         for name, (res, args) in sig.items():
             f = getattr(r, name)

@@ -8,6 +8,7 @@
 //   dynacore/src/quantization/quant_formats.cpp:12-222      dequantize_*, quantize_q8_0
 //   dynacore/cpu/generic/kernels_generic.cpp:187-310        quantize_act, dot_rows_* (generic)
 //   dynacore/cpu/avx2/kernels_avx2.cpp:610-1440             AVX2 quantizers and dots
+//   dynacore/include/dynacore/base/fast_exp.h:16-35         exp_nonpos (SiLU)
 // Used to pin the C oracle (tests) and, on the GPU box, as the timed CPU
 // baseline ("reference" kind) of bench.py.
 
@@ -19,6 +20,7 @@
 #include <thread>
 #include <vector>
 
+#include "dynacore/base/fast_exp.h"
 #include "dynacore/cpu/cpu_kernels.h"
 #include "dynacore/hardware/cpu_info.h"
 #include "dynacore/quantization/quant_formats.h"
@@ -182,5 +184,9 @@ int64_t ref_bench_gemv(int kind, int dtype, const void* const* w_copies, int nco
   const auto t1 = std::chrono::steady_clock::now();
   return std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
 }
+
+// e^x for x <= 0 (dynacore/include/dynacore/base/fast_exp.h:16-35), the exp of the
+// reference's SiLU (dynacore/cpu/cpu_device.cpp:117-123).
+float ref_exp_nonpos(float x) { return dynacore::exp_nonpos(x); }
 
 }  // extern "C"

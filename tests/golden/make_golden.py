@@ -14,6 +14,8 @@ only (data, no code):
   dot_<t>      generic dot_rows_<t> (kernels_generic.cpp:216-310) on per-32 activations
   sbdot_<t>    AVX2 dot_rows_sb_<t> (kernels_avx2.cpp:976-1058), sxdot_<t> AVX2
                dot_rows_sx_<t> (kernels_avx2.cpp:1117-1216)
+  expnp        exp_nonpos of seeded and boundary inputs (base/fast_exp.h:16-35), the
+               exponential of the reference's SiLU (cpu_device.cpp:117-123)
 """
 from __future__ import annotations
 
@@ -93,6 +95,15 @@ def main() -> None:
         if t in (O.Q4_K, O.Q6_K):
             out[f"sbdot_{name}"] = np.stack([O.ref_dot_rows(2, t, w[i], out["act_sb"], K) for i in range(3)], 1)
             out[f"sxdot_{name}"] = np.stack([O.ref_dot_rows(3, t, w[i], out["act_sx"], K) for i in range(3)], 1)
+
+    rng = np.random.default_rng(20261202)
+    ex = np.concatenate([
+        -rng.exponential(6.0, 4096), -rng.uniform(0.0, 1.0, 1024), np.linspace(-90.0, 0.0, 1801),
+        np.array([0.0, -0.0, -87.0, -86.99999, -87.00001, -88.0, -100.0, -1e-30, -1e-45, -np.log(2.0), 1.0, 88.0,
+                  100.0, -np.inf, np.nan]),
+    ]).astype(np.float32)
+    out["expnp_x"] = ex
+    out["expnp_y"] = np.array([r.ref_exp_nonpos(float(v)) for v in ex], np.float32)
     path = os.path.join(HERE, "reference_vectors.npz")
     np.savez_compressed(path, **out)
     print(path, os.path.getsize(path), "bytes")

@@ -94,3 +94,16 @@ def test_matmul_many_validation_without_gpu():
     assert lib.dq_matmul_many(C.cast(jobs, C.c_void_p), 2, None) == 1
     assert b"null weight" in lib.dq_last_error()
     assert C.sizeof(dq.MatmulJob) == 56
+
+
+def test_gated_validation_without_gpu():
+    """dq_act_mul / dq_matmul_gated reject bad arguments with StatusCode values before any GPU work."""
+    lib = dq.lib()
+    assert lib.dq_act_mul(dq.SILU, None, 0, None, 0, 0, 8, None, 0, None) == 0   # empty: nothing to do
+    assert lib.dq_act_mul(3, None, 0, None, 0, 1, 8, None, 0, None) == 1
+    assert b"activation" in lib.dq_last_error()
+    assert lib.dq_act_mul(dq.GELU, None, 0, None, 0, 2, 8, None, 0, None) == 1
+    assert lib.dq_act_mul(dq.GELU, None, 0, None, 0, -1, 8, None, 0, None) == 1
+    assert lib.dq_matmul_gated(7, None, 1, 0, None, None, None, 0, None, None, 0, None) == 1
+    assert lib.dq_matmul_gated(dq.SILU, None, 1, 0, None, None, None, 0, None, None, 0, None) == 1
+    assert b"null weight" in lib.dq_last_error()

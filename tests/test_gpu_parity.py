@@ -469,3 +469,151 @@ def test_skinny_activation_tiles_and_passes(cuda, t, m):
     else:
         ok, worst = close(y2, want)
         assert ok, f"worst error ratio {worst:.3g}"
+
+
+# ------------------------------------------------------ act_mul, matmul_gated
+
+ACTS = [O.SILU, O.GELU, O.GELU_TANH]
+ACT_IDS = ["silu", "gelu", "gelu_tanh"]
+
+
+def _act_expect(act: int, g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    return (O.activation(act, g) * u).astype(np.float32)
+
+
+def _act_check(act: int, got: np.ndarray, g: np.ndarray, u: np.ndarray, what: str) -> None:
+    """SiLU bit-exact (the reference's exp_nonpos and fp32 steps); GELU forms within 1e-6 relative of
+    max(|g|, 1) * |u| (device erff / tanhf against the host libm)."""
+    want = _act_expect(act, g, u)
+    if act == O.SILU:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), what
+    else:
+        bound = 1e-6 * np.maximum(np.abs(g.astype(np.float64)), 1.0) * np.abs(u) + 1e-30
+        with np.errstate(invalid="ignore"):
+            ok = (got == want) | (np.abs(got.astype(np.float64) - want) <= bound)  # == covers equal infinities
+        assert np.all(ok), f"{what}: {np.argwhere(~ok)[:5].tolist()}"
+
+
+def _act_inputs(m: int, n: int, seed: int) -> tuple[np.ndarray, np.ndarray]:
+    rng = np.random.default_rng(seed)
+    g = (rng.standard_normal((m, n)) * 6.0).astype(np.float32)
+    u = rng.standard_normal((m, n)).astype(np.float32)
+    special = np.array([0.0, -0.0, 1e-30, -1e-30, 87.0, -87.0, -88.0, -100.0, 100.0, 20.0, -20.0, 3e38, -3e38],
+                       np.float32)
+    g.ravel()[:special.size] = special
+    return g, u
+
+
+@pytest.mark.parametrize("act", ACTS, ids=ACT_IDS)
+@pytest.mark.parametrize("m,n,pad", [(1, 4096, 0), (5, 1000, 0), (7, 1024, 12), (300, 96, 4)])
+def test_act_mul_parity(cuda, act, m, n, pad):
+    """Device::act_mul (dynacore/cpu/cpu_device.cpp:1912-1930): vector and scalar paths, strided rows."""
+    from dynalm_amd import torch_ops as T
+
+    g, u = _act_inputs(m, n, 10 * m + n)
+    gd = torch.zeros((m, n + pad), device="cuda")
+    ud = torch.zeros((m, n + 2 * pad), device="cuda")
+    gd[:, :n] = dev(g)
+    ud[:, :n] = dev(u)
+    out = torch.full((m, n + pad), 5.0, device="cuda")
+    T.act_mul(act, gd[:, :n], ud[:, :n], out=out[:, :n])
+    res = host(out)
+    _act_check(act, res[:, :n], g, u, "act_mul")
+    assert np.all(res[:, n:] == 5.0)
+    # in place: out aliases gate
+    T.act_mul(act, gd[:, :n], ud[:, :n], out=gd[:, :n])
+    assert np.array_equal(host(gd)[:, :n].view(np.uint32), res[:, :n].view(np.uint32))
+
+
+def _gated_case(tg, tu, n, k, seed):
+    rg = gguf_weights(tg, n, k, seed, outlier_frac=0.01)
+    ru = gguf_weights(tu, n, k, seed + 1, outlier_frac=0.01)
+    return rg, ru, dq.Weight.upload(tg, rg, k), dq.Weight.upload(tu, ru, k)
+
+
+@pytest.mark.parametrize("act", ACTS, ids=ACT_IDS)
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q6_K], ids=lambda t: O.TYPE_NAMES[t])
+@pytest.mark.parametrize("m", [1, 3, 16, 40, 100])
+def test_matmul_gated_parity(cuda, act, t, m):
+    """Device::matmul_gated (dynacore/include/dynacore/device/device.h:188-199): the fused M = 1 GEMV
+    (m = 1), the fused skinny kernel (m <= 16) and the unfused sequence (m > 16) against the oracle's
+    act(x . Wg^T) * (x . Wu^T); and bit-identical to act_mul over two dq_matmul calls on the GPU."""
+    from dynalm_amd import torch_ops as T
+
+    n, k = 200, 1280
+    rg, ru, wg, wu = _gated_case(t, t, n, k, 300 + m)
+    x = activations(m, k, 310 + m)
+    xd = dev(x)
+    out = host(T.matmul_gated(act, xd, wg, wu))
+    a = O.quantize_act(O.ACT_Q8_K, x)
+    g = O.matmul(t, O.ACT_Q8_K, rg, a, k)
+    u = O.matmul(t, O.ACT_Q8_K, ru, a, k)
+    _act_check(act, out, g, u, f"gated m={m}")
+    comp = host(T.act_mul(act, T.matmul(wg, xd), T.matmul(wu, xd)))
+    assert np.array_equal(out.view(np.uint32), comp.view(np.uint32)), "fused differs from act_mul(matmul, matmul)"
+
+
+@pytest.mark.parametrize("m", [1, 8, 70])
+def test_matmul_gated_mixed_types_and_scratch(cuda, m):
+    """Gate and up of different types (Q4_K / Q6_K: the unfused sequence), strided x and out, and
+    caller-given scratch of a wider stride; Q8_0 weights (per-32 activations) as well."""
+    from dynalm_amd import torch_ops as T
+
+    n, k = 136, 768
+    rg, ru, wg, wu = _gated_case(O.Q4_K, O.Q6_K, n, k, 400 + m)
+    x = activations(m, k, 410 + m)
+    xp = torch.zeros((m, k + 8), device="cuda")
+    xp[:, :k] = dev(x)
+    out = torch.full((m, n + 3), 9.0, device="cuda")
+    gs = torch.empty((m, n + 16), device="cuda")
+    us = torch.empty((m, n + 16), device="cuda")
+    T.matmul_gated(O.SILU, xp[:, :k], wg, wu, out=out[:, :n], scratch=(gs, us))
+    res = host(out)
+    a = O.quantize_act(O.ACT_Q8_K, x)
+    _act_check(O.SILU, res[:, :n], O.matmul(O.Q4_K, O.ACT_Q8_K, rg, a, k), O.matmul(O.Q6_K, O.ACT_Q8_K, ru, a, k),
+               "mixed")
+    assert np.all(res[:, n:] == 9.0)
+    # Q8_0 pair: per-32 activations, library scratch
+    rg8, ru8, wg8, wu8 = _gated_case(O.Q8_0, O.Q8_0, n, k, 420 + m)
+    got = host(T.matmul_gated(O.GELU_TANH, xp[:, :k], wg8, wu8))
+    a8 = O.quantize_act(O.ACT_PER32, x)
+    g8 = O.matmul(O.Q8_0, O.ACT_PER32, rg8, a8, k)
+    u8 = O.matmul(O.Q8_0, O.ACT_PER32, ru8, a8, k)
+    want = _act_expect(O.GELU_TANH, g8, u8)
+    close(got, want)
+
+
+def test_matmul_gated_full_size_m1(cuda):
+    """BASELINE's shape as a gate / up pair (Q4_K, K = 4096, N = 14336, M = 1): bit-identical to
+    act_mul over the two single matmuls, and to the oracle on sampled rows."""
+    from dynalm_amd import torch_ops as T
+
+    n, k = 14336, 4096
+    rg, ru, wg, wu = _gated_case(O.Q4_K, O.Q4_K, n, k, 500)
+    x = activations(1, k, 501)
+    xd = dev(x)
+    out = host(T.matmul_gated(O.SILU, xd, wg, wu))
+    comp = host(T.act_mul(O.SILU, T.matmul(wg, xd), T.matmul(wu, xd)))
+    assert np.array_equal(out.view(np.uint32), comp.view(np.uint32))
+    rows = np.random.default_rng(502).choice(n, 64, replace=False)
+    a = O.quantize_act(O.ACT_Q8_K, x)
+    g = O.matmul(O.Q4_K, O.ACT_Q8_K, rg[rows], a, k)
+    u = O.matmul(O.Q4_K, O.ACT_Q8_K, ru[rows], a, k)
+    _act_check(O.SILU, out[:, rows], g, u, "sampled rows")
+
+
+def test_matmul_gated_rejects(cuda):
+    from dynalm_amd import torch_ops as T
+
+    k = 512
+    wg = dq.Weight.upload(O.Q4_K, gguf_weights(O.Q4_K, 64, k, 5), k)
+    wu = dq.Weight.upload(O.Q4_K, gguf_weights(O.Q4_K, 128, k, 6), k)
+    x = dev(activations(2, k, 7))
+    with pytest.raises(dq.DqError) as e:
+        T.matmul_gated(O.SILU, x, wg, wu)
+    assert e.value.status == "invalid_argument"
+    y = torch.empty((2, 64), device="cuda")
+    with pytest.raises(dq.DqError):
+        dq.matmul_gated(O.SILU, x, 2, k, wg, wg, y, 64, gate_scratch=y)
+    with pytest.raises(dq.DqError):
+        dq.matmul_gated(5, x, 2, k, wg, wg, y, 64)

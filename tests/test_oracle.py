@@ -381,3 +381,90 @@ def test_live_reference_generic_dots(t):
     y = O.matmul(t, O.ACT_PER32, w, a, k)
     ref = np.stack([O.ref_dot_rows(0, t, w[i], a, k) for i in range(6)], 1)
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+
+
+# ----------------------------------------------------------- activations
+
+
+def test_exp_nonpos_golden(gold):
+    """Bit-equal to the reference's exp_nonpos (base/fast_exp.h:16-35), boundary and NaN inputs included."""
+    y = O.exp_nonpos(gold["expnp_x"])
+    assert np.array_equal(y.view(np.uint32), gold["expnp_y"].view(np.uint32))
+
+
+def test_exp_nonpos_vs_double_exp():
+    x = np.concatenate([np.linspace(-87.0, 0.0, 20001), -np.random.default_rng(5).exponential(3.0, 20000)])
+    x = x[x >= -87.0].astype(np.float32)
+    y = O.exp_nonpos(x).astype(np.float64)
+    ex = np.exp(x.astype(np.float64))
+    assert np.max(np.abs(y - ex) / ex) < 3e-7
+    assert O.exp_nonpos(np.array([0.0], np.float32))[0] == 1.0
+    # clamp: below -87 (and NaN, -inf) the value at -87
+    lo = O.exp_nonpos(np.array([-87.0, -88.0, -1e9, -np.inf, np.nan], np.float32))
+    assert np.all(lo == lo[0]) and abs(lo[0] / np.exp(-87.0) - 1) < 3e-7
+
+
+def _act_double(act: int, x: np.ndarray) -> np.ndarray:
+    import math
+    xd = x.astype(np.float64)
+    if act == O.SILU:
+        return xd / (1.0 + np.exp(-xd))
+    if act == O.GELU:
+        return 0.5 * xd * (1.0 + np.array([math.erf(v / math.sqrt(2.0)) for v in xd]))
+    return 0.5 * xd * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (xd + 0.044715 * xd ** 3)))
+
+
+@pytest.mark.parametrize("act", [O.SILU, O.GELU, O.GELU_TANH], ids=["silu", "gelu", "gelu_tanh"])
+def test_activations_closed_forms(act):
+    """Within fp32 rounding of the textbook forms: SiLU x sigmoid(x); GELU with erf; GELU's tanh form
+    (cpu_device.cpp:117-128)."""
+    rng = np.random.default_rng(7 + act)
+    x = np.concatenate([rng.normal(0.0, 4.0, 20000), np.linspace(-30.0, 30.0, 6001), [0.0, -0.0, 1e-30, -1e-30]])
+    x = x.astype(np.float32)
+    y = O.activation(act, x)
+    ref = _act_double(act, x)
+    scale = np.maximum(np.abs(x.astype(np.float64)), 1.0)
+    bound = 3e-7 if act == O.SILU else 2.5e-7
+    assert np.max(np.abs(y - ref) / scale) < bound
+    if act == O.SILU:  # the exponential is exp_nonpos: relative accuracy holds down to the clamp
+        keep = np.abs(ref) > 1e-30
+        assert np.max(np.abs(y[keep] - ref[keep]) / np.abs(ref[keep])) < 5e-7
+    big = np.array([40.0, 1000.0], np.float32)
+    assert np.array_equal(O.activation(act, big), big)
+    assert O.activation(act, np.array([0.0], np.float32))[0] == 0.0
+
+
+def test_silu_rounding_sequence(gold):
+    """SiLU's fp32 sequence x * (x >= 0 ? 1 : e) / (1 + e) on the reference's own e^-|x| values: each
+    step one IEEE rounding, so numpy float32 steps on the golden exponentials give the same bits."""
+    e_in = gold["expnp_x"]
+    sel = np.isfinite(e_in) & (e_in <= 0) & (e_in >= -87)
+    e = gold["expnp_y"][sel]
+    mag = -e_in[sel]
+    for sign in (1.0, -1.0):
+        x = (np.float32(sign) * mag).astype(np.float32)
+        num = np.where(x >= 0, np.float32(1.0), e).astype(np.float32)
+        want = ((x * num).astype(np.float32) / (np.float32(1.0) + e).astype(np.float32)).astype(np.float32)
+        got = O.activation(O.SILU, x)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_activation_rejects_unknown():
+    with pytest.raises(ValueError):
+        O.activation(3, np.zeros(4, np.float32))
+
+
+@pytest.mark.parametrize("act", [O.SILU, O.GELU, O.GELU_TANH], ids=["silu", "gelu", "gelu_tanh"])
+def test_matmul_gated_vs_double(act):
+    """act(x . Wg^T) * (x . Wu^T) against double-precision dots of the dequantized operands."""
+    k, n = 512, 12
+    wg = weight_rows(O.Q4_K, n, k, 61)
+    wu = weight_rows(O.Q6_K, n, k, 62)
+    a = O.quantize_act(O.ACT_Q8_K, activations(3, k, 63))
+    y = O.matmul_gated(act, O.Q4_K, O.Q6_K, O.ACT_Q8_K, wg, wu, a, k)
+    xa = np.stack([O.dequantize_act(O.ACT_Q8_K, a[i], k).ravel() for i in range(3)]).astype(np.float64)
+    g = xa @ np.stack([O.dequantize(O.Q4_K, wg[i], k).ravel() for i in range(n)]).astype(np.float64).T
+    u = xa @ np.stack([O.dequantize(O.Q6_K, wu[i], k).ravel() for i in range(n)]).astype(np.float64).T
+    ref = _act_double(act, g.astype(np.float32).ravel()).reshape(g.shape) * u
+    scale = np.maximum(np.abs(g), 1.0) * np.maximum(np.abs(u), 1.0)
+    assert np.max(np.abs(y - ref) / scale) < 1e-4
