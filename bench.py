@@ -174,10 +174,11 @@ def random_rows(dtype: int, n: int, k: int, seed: int) -> np.ndarray:
 def decode_stack(steps: int, stream: int) -> dict:
     """Config 5: the 28-layer matmul stack plus lm_head of one decode step at M = 16,
     in the order a transformer step issues it (dynalm/src/model/transformer.cpp:605-718):
-    per layer matmul_many(q, k, v) on the attention input, o, matmul_many(gate, up)
-    on the MLP input, down; then lm_head. Each call quantizes its input to Q8_K on
-    the GPU once and runs the skinny MFMA GEMV (grouped launches for the shared
-    inputs). Timed as one graph replay per `steps` steps."""
+    per layer matmul_many(q, k, v) on the attention input, o, matmul_gated(SiLU, gate,
+    up) on the MLP input (the compiler's gate/up/act_mul fusion,
+    dynacore/include/dynacore/ir/passes.h:79), down on its output; then lm_head. Each
+    call quantizes its input to Q8_K on the GPU (in the kernel for the small ones) and
+    runs the skinny MFMA GEMV. Timed as one graph replay per `steps` steps."""
     import torch
 
     import dynalm_amd as dq
@@ -205,13 +206,14 @@ def decode_stack(steps: int, stream: int) -> dict:
         for layer in range(QWEN_LAYERS):
             dq.matmul_many([job("q", layer, "attn"), job("k", layer, "attn"), job("v", layer, "attn")], st)
             dq.matmul(*job("o", layer, "o"), st)
-            dq.matmul_many([job("gate", layer, "mlp"), job("up", layer, "mlp")], st)
+            dq.matmul_gated(dq.SILU, xs["mlp"], m, 1536, uploads["gate"][layer], uploads["up"][layer], xs["down"],
+                            8960, stream=st)
             dq.matmul(*job("down", layer, "down"), st)
         dq.matmul(*job("lm_head", 0, "o"), st)
 
     ms = time_graph(step, steps, 2)
     out = {"workload": "config 5: Qwen2.5-1.5B decode-step matmul stack (28 layers + lm_head), M=16; per layer "
-                       "matmul_many(q,k,v), o, matmul_many(gate,up), down",
+                       "matmul_many(q,k,v), o, matmul_gated(silu, gate, up), down",
            "ms_per_step": round(ms, 4), "weight_bytes": total_bytes,
            "gbs": round(total_bytes / (ms * 1e-3) / 1e9, 1), "tokens_per_s": round(m / (ms * 1e-3), 1)}
     for ws in uploads.values():
@@ -358,6 +360,25 @@ def main() -> None:
     # the step is one kernel (k_gemv<Q4_K, Q8_K, M=1, fused quantization>): its launch time is ms_step
     achieved = value
 
+    # ---- the gated pair at the step's shape: act(x . Wg^T) * (x . Wu^T), one launch
+    pairs = [(weights[2 * j], weights[2 * j + 1]) for j in range(nc // 2)]
+    yq = torch.empty((1, N), dtype=torch.float32, device="cuda")
+
+    def gated(i: int, st: int) -> None:
+        wg, wu = pairs[i % len(pairs)]
+        dq.matmul_gated(dq.SILU, x, 1, K, wg, wu, y, N, stream=st)
+
+    def two_matmuls(i: int, st: int) -> None:
+        wg, wu = pairs[i % len(pairs)]
+        dq.matmul(wg, x, 1, K, y, N, None, st)
+        dq.matmul(wu, x, 1, K, yq, N, None, st)
+
+    ms_gated = ms_two = None
+    if pairs:
+        log(f"gated pair x{args.steps // 2}")
+        ms_gated = time_graph(gated, args.steps // 2, args.warmup)
+        ms_two = time_graph(two_matmuls, args.steps // 2, args.warmup)
+
     # ---- prefill GEMM, M = 512
     m = args.gemm_m
     xg = torch.randn((m, K), generator=gen, device="cuda", dtype=torch.float32)
@@ -426,6 +447,16 @@ def main() -> None:
                          "traffic": traffic.get("gemm_m512")},
         },
     }
+    if ms_gated is not None:
+        gbytes = 2 * Q4K_ROW * N + Q8K_ROW + 4 * N
+        result["gated_m1"] = {
+            "workload": "dq_matmul_gated(SiLU) M=1, Q4_K gate and up K=4096 N=14336 (one launch: "
+                        "k_gemv<Q4_K, Q8_K, M=1, fused, gated>)",
+            "ms_per_call": round(ms_gated, 5),
+            "gbs": round(gbytes / (ms_gated * 1e-3) / 1e9, 2),
+            "pct_peak_hbm": round(100 * gbytes / (ms_gated * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+            "ms_two_matmuls": round(ms_two, 5),
+        }
     if args.sweep:
         result["prefill_sweep"] = prefill_sweep([int(v) for v in args.sweep.split(",")], weights, gen)
     if args.stack_steps > 0:

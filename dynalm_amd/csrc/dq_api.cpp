@@ -514,7 +514,7 @@ int dq_matmul_gated(int act, const float* x, int64_t m, int64_t x_stride, const 
     DQ_HIP(dq::launch_gemv_gated(g, u, act, x, out, s), "gated gemv launch");
     return DQ_OK;
   }
-  if (same && m <= dq::kSkinnyGatedMaxRows && skinny_ok(w_gate, x, m, x_stride) && dq::gemv_mma_lds_ok(g.nblk, m, true)) {
+  if (same && skinny_ok(w_gate, x, m, x_stride) && dq::gemv_mma_lds_ok(g.nblk, m, true)) {
     // decode batches: the skinny MFMA GEMV over both weights, act(g) * u in its chains
     std::vector<dq::GemvJob> j{
         dq::GemvJob{&g, nullptr, 0, x, m > 1 ? x_stride : g.k, m, out, m > 1 ? out_stride : g.n, nullptr, &u, act}};

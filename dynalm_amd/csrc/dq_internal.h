@@ -47,8 +47,6 @@ hipError_t launch_gemv_mma(const WeightDev& w, int af, const uint8_t* acts, int6
                            int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s);
 constexpr int64_t kSkinnyMaxRows = 64;
 bool gemv_mma_supported(int dtype, int af, int64_t m);
-// Gated jobs (two weights per workgroup) take at most one activation tile.
-constexpr int64_t kSkinnyGatedMaxRows = 16;
 // Whether the skinny kernel's LDS holds the t-terms of nblk super-blocks for m rows
 // (gated: of two weights).
 bool gemv_mma_lds_ok(int64_t nblk, int64_t m, bool gated = false);

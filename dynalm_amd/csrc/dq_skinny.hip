@@ -45,10 +45,11 @@
 // kGated: a job carries a second weight of the same type and shape (the up
 // projection) and writes act(x . Wg^T) * (x . Wu^T), the gated MLP projection of
 // dynacore's Device::matmul_gated (dynacore/include/dynacore/device/device.h:188-199).
-// Each wave multiplies one activation super-block with both weights' tiles, the
+// Half the waves of a workgroup run the gate tile and half the up tile of the same
+// 16 rows (each wave the single-weight pipeline over twice the super-blocks), the
 // t-terms of both go to LDS, and the chains end in act(g) * u: one launch and no
 // gate / up round trip through memory, as CpuDevice's decode path applies the
-// activation per 16-column chunk (dynacore/cpu/cpu_device.cpp:1940-1984).
+// activation per 16-column chunk (dynacore/cpu/cpu_device.cpp:1940-1979).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -310,32 +311,19 @@ struct WRes<kQ6_K, CT> {
   DQ_DEV void load(WSB<kQ6_K, CT>& w, int b, int r0, int li, int lg) const { w.load(rp, b, r0, li, lg); }
 };
 
-// One wave's super-blocks [b0, b1) of one job: activations, weights, t-terms to LDS
-// (kGated: the up projection's t-terms to tu, from the same activation operand).
-// CT == 1 keeps the next super-block's weight loads in flight during the compute
-// (activation loads of b are issued before the weight loads of b + 1, so waiting
-// for them does not wait for the prefetch: loads retire in order).
-template <int WT, int CT, int MT, bool kFused, bool kGated>
-DQ_DEV void skinny_wave(const SkinnyJob& J, int nblk, int64_t G, int r0, bool ok, int b0, int b1, float* tt,
-                        float* tu, float* dal, int li, int lg) {
+// One wave's super-blocks [b0, b1) of one weight (planes p) of a job: activations,
+// weights, t-terms to LDS. CT == 1 keeps the next super-block's weight loads in
+// flight during the compute (activation loads of b are issued before the weight
+// loads of b + 1, so waiting for them does not wait for the prefetch: loads retire
+// in order).
+template <int WT, int CT, int MT, bool kFused>
+DQ_DEV void skinny_wave(const SkinnyJob& J, const uint8_t* const* p, int nblk, int64_t G, int r0, bool ok, int b0,
+                        int b1, float* tt, float* dal, int li, int lg) {
   constexpr int NC = 16 * CT, NR = 16 * MT;
-  static_assert(!kGated || CT == 1, "gated jobs run 16-row tiles");
-  WRes<WT, CT> res, resu;
-  res.init(J.p, G, nblk, ok);
-  if constexpr (kGated) resu.init(J.pu, G, nblk, ok);
+  WRes<WT, CT> res;
+  res.init(p, G, nblk, ok);
   ActSrc<kFused> src;
   src.init(J);
-  auto emit_t = [&](const WSB<WT, CT>& w, const ActSB<MT>& A, int b, float* to) {
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      float t[MT][4];
-      tterms<CT, MT>(w, ct, A, lg, t);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) to[(b * NR + 16 * mt + 4 * lg + e) * NC + 16 * ct + li] = t[mt][e];
-    }
-  };
   auto emit = [&](const WSB<WT, CT>& w, const ActSB<MT>& A, int b) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
@@ -362,25 +350,7 @@ DQ_DEV void skinny_wave(const SkinnyJob& J, int nblk, int64_t G, int r0, bool ok
     }
   };
   if (b0 >= b1) return;
-  if constexpr (kGated) {
-    // the up tile of b loads while the gate tile of b computes, the gate tile of
-    // b + 1 while the up tile computes: two weight tiles live at a time, as in
-    // the single-weight pipeline below
-    WSB<WT, CT> cur;
-    res.load(cur, b0, r0, li, lg);
-    for (int b = b0; b < b1; ++b) {
-      ActSB<MT> A;
-      act(b, A);
-      WSB<WT, CT> up;
-      resu.load(up, b, r0, li, lg);
-      __builtin_amdgcn_sched_barrier(0);
-      emit(cur, A, b);
-      __builtin_amdgcn_sched_barrier(0);
-      res.load(cur, b + 1 < b1 ? b + 1 : b, r0, li, lg);
-      __builtin_amdgcn_sched_barrier(0);
-      emit_t(up, A, b, tu);
-    }
-  } else if constexpr (CT == 1) {
+  if constexpr (CT == 1) {
     WSB<WT, CT> cur;
     res.load(cur, b0, r0, li, lg);
     for (int b = b0; b < b1; ++b) {
@@ -418,18 +388,26 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void k_skinny(SkinnyGroup g) {
   const int nblk = g.nblk;
   float* tt = reinterpret_cast<float*>(lds);        // [nblk][NR activation rows][NC weight rows]
   float* tu = tt + (kGated ? nblk * NR * NC : 0);  // kGated: the up projection's, same shape
-  float* dal = tu + nblk * NR * NC;                // [nblk][NR] activation d
+  float* dal = tu + nblk * NR * NC;                // [nblk][NR] activation d (kGated: twice)
   const int l = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = l & 15, lg = l >> 4;
   const int64_t row0 = (J.t0 + (wg - J.wg0)) * NC;  // first weight row of the tile
   const int64_t G = row0 / kRowGroup;
   const int r0 = (int)(row0 % kRowGroup);
   const bool ok = row0 < J.n_pad;
-  const int b0 = wave * nblk / W, b1 = (wave + 1) * nblk / W;
+  // kGated: waves W/2.. run the up projection over the same tile, each half with its
+  // own t-term and activation-d regions (both halves write the same d values)
+  constexpr int WH = kGated ? W / 2 : W;
+  const int half = kGated && wave >= WH ? 1 : 0;
+  const int wl = wave - half * WH;
+  const int b0 = wl * nblk / WH, b1 = (wl + 1) * nblk / WH;
+  const uint8_t* const* planes = half ? J.pu : J.p;
+  float* tw = half ? tu : tt;
+  float* dw = dal + half * nblk * NR;
   if (J.dtype == kQ6_K) {
-    skinny_wave<kQ6_K, CT, MT, kFused, kGated>(J, nblk, G, r0, ok, b0, b1, tt, tu, dal, li, lg);
+    skinny_wave<kQ6_K, CT, MT, kFused>(J, planes, nblk, G, r0, ok, b0, b1, tw, dw, li, lg);
   } else {
-    skinny_wave<kQ4_K, CT, MT, kFused, kGated>(J, nblk, G, r0, ok, b0, b1, tt, tu, dal, li, lg);
+    skinny_wave<kQ4_K, CT, MT, kFused>(J, planes, nblk, G, r0, ok, b0, b1, tw, dw, li, lg);
   }
   __syncthreads();
   // the in-order chains of the tile's NR x NC outputs, shared by all waves
@@ -453,7 +431,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void k_skinny(SkinnyGroup g) {
 }
 
 size_t skinny_lds(int64_t nblk, int ct, int mt, bool gated = false) {
-  return (size_t)nblk * (16 * mt * (16 * ct * (gated ? 2 : 1) + 1)) * sizeof(float);
+  return (size_t)nblk * (16 * mt * (16 * ct + 1)) * (gated ? 2 : 1) * sizeof(float);
 }
 constexpr size_t kSkinnyMaxLds = 160 * 1024;
 
@@ -511,8 +489,7 @@ hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t*
   }
   if (wgs >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
   if (gated) {
-    // one activation tile: with four, two weights' operands exceed the register file
-    if (mt == 4) return hipErrorInvalidValue;
+    if (mt == 4) return skinny_launch<1, 4, false, true>(g, (int)wgs, s);
     return fused ? skinny_launch<1, 1, true, true>(g, (int)wgs, s) : skinny_launch<1, 1, false, true>(g, (int)wgs, s);
   }
   if (mt == 4) return skinny_launch<1, 4, false>(g, (int)wgs, s);
@@ -569,7 +546,7 @@ hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s) {
         return hipErrorInvalidValue;
       }
       if (gated && (q.wu->dtype != q.w->dtype || q.wu->n != q.w->n || q.wu->k != q.w->k || q.bias != nullptr ||
-                    !act_ok(q.act) || q.m > kSkinnyGatedMaxRows)) {
+                    !act_ok(q.act))) {
         return hipErrorInvalidValue;
       }
       g.job[i] = skinny_job(*q.w, q.m, 0, q.w->n, q.y, q.ys, q.bias);

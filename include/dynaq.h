@@ -189,7 +189,7 @@ DQ_API int dq_act_mul(int act, const float* gate, int64_t gate_stride, const flo
  * have the same n and k; out has out_stride floats per row; no bias. Replaces
  * Device::matmul_gated (dynacore/include/dynacore/device/device.h:188-199;
  * CpuDevice::matmul_gated, dynacore/cpu/cpu_device.cpp:1931-2072).
- *   - Q4_K / Q6_K weights of one type, m <= 16: one fused launch that streams both
+ *   - Q4_K / Q6_K weights of one type, m <= 64: one fused launch that streams both
  *     weights and writes only act(g) * u (no gate / up round trip);
  *   - otherwise both projections as dq_matmul computes them, into gate_scratch and
  *     up_scratch (m rows of scratch_stride floats each, clobbered), then dq_act_mul.
