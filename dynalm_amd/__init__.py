@@ -19,6 +19,8 @@ dynacore/include/dynacore/device/device.h:89-161):
     matmul_many(jobs)                  Device::matmul_many
     act_mul(act, gate, up, ...)        Device::act_mul
     matmul_gated(act, x, wg, wu, ...)  Device::matmul_gated
+    GgufFile.open(path)                dynalm's GgufFile::open / open_parts (host mmap + parse)
+    GgufFile.upload(name)              Device::upload of a GGUF tensor
 
 Errors raise DqError carrying dynacore's StatusCode value
 (dynacore/include/dynacore/base/status.h:19-32).
@@ -34,7 +36,7 @@ __all__ = [
     "Q4_0", "Q8_0", "Q4_K", "Q6_K", "ACT_PER32", "ACT_Q8_0", "ACT_Q8_K", "GEMV_MAX_ROWS",
     "DqError", "lib", "lib_path", "row_bytes", "act_row_bytes", "act_format_for", "Weight",
     "act_quantize", "gemv", "gemm", "matmul", "matmul_many", "MatmulJob", "partials_count", "debug_partials",
-    "SILU", "GELU", "GELU_TANH", "act_mul", "matmul_gated", "EXPORTS",
+    "SILU", "GELU", "GELU_TANH", "act_mul", "matmul_gated", "GgufFile", "GgufTensor", "EXPORTS",
 ]
 
 Q4_0, Q8_0, Q4_K, Q6_K = 6, 10, 14, 16
@@ -77,6 +79,14 @@ EXPORTS = {
     "dq_matmul": (_I, [_P, _P, _I64, _I64, _P, _I64, _P, _P]),
     "dq_matmul_many": (_I, [_P, _I64, _P]),
     "dq_act_mul": (_I, [_I, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P]),
+    "dq_gguf_open": (_I, [C.c_char_p, C.POINTER(_P)]),
+    "dq_gguf_close": (_I, [_P]),
+    "dq_gguf_info": (_I, [_P, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64), C.POINTER(_I64), C.POINTER(_I64)]),
+    "dq_gguf_find_tensor": (_I64, [_P, C.c_char_p]),
+    "dq_gguf_tensor_info": (_I, [_P, _I64, _P]),
+    "dq_gguf_get_uint": (_I, [_P, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "dq_gguf_get_string": (_I, [_P, C.c_char_p, C.POINTER(C.c_char_p), C.POINTER(_I64)]),
+    "dq_gguf_upload_weight": (_I, [_P, _I64, _P, C.POINTER(_P)]),
     "dq_matmul_gated": (_I, [_I, _P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P]),
     "dq_partials_count": (_I, [_I, _I, _I64, C.POINTER(_I64), C.POINTER(_I64)]),
     "dq_debug_partials": (_I, [_P, _I, _P, _I64, _P, _P, _P]),
@@ -111,7 +121,7 @@ def lib() -> C.CDLL:
 
 def _check(rc: int) -> None:
     if rc != 0:
-        raise DqError(rc, lib().dq_last_error().decode())
+        raise DqError(rc, lib().dq_last_error().decode(errors="replace"))
 
 
 def _ptr(x) -> int | None:
@@ -235,3 +245,90 @@ def partials_count(dtype: int, fmt: int, k: int) -> tuple[int, int]:
 
 def debug_partials(w: Weight, fmt: int, acts, m: int, units, sb=None, stream: int = 0) -> None:
     _check(lib().dq_debug_partials(w.handle, fmt, _ptr(acts), m, _ptr(units), _ptr(sb), stream))
+
+
+# ------------------------------------------------------------------ GGUF files
+
+
+class GgufTensor(C.Structure):
+    """dq_gguf_tensor (include/dynaq.h): one entry of the tensor directory."""
+    _fields_ = [("name", C.c_char_p), ("ggml_type", C.c_uint32), ("dtype", C.c_int32), ("n_dims", C.c_int32),
+                ("dims", _I64 * 4), ("offset", C.c_uint64), ("nbytes", C.c_uint64), ("part", C.c_int32),
+                ("data", _P)]
+
+    @property
+    def shape(self) -> tuple[int, ...]:
+        return tuple(int(self.dims[d]) for d in range(self.n_dims))
+
+
+class GgufFile:
+    """A GGUF model mapped read-only (all parts of a split model): dynalm's GgufFile
+    (dynalm/src/loader/gguf/gguf.h:77-125) over the library's parser."""
+
+    def __init__(self, handle: int):
+        self._h = C.c_void_p(handle)
+
+    @classmethod
+    def open(cls, path: str) -> "GgufFile":
+        h = _P()
+        _check(lib().dq_gguf_open(os.fsencode(path), C.byref(h)))
+        return cls(h.value)
+
+    def close(self) -> None:
+        if self._h:
+            lib().dq_gguf_close(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def info(self) -> dict:
+        v, a, n, p = C.c_uint32(), C.c_uint64(), _I64(), _I64()
+        _check(lib().dq_gguf_info(self._h, C.byref(v), C.byref(a), C.byref(n), C.byref(p)))
+        return {"version": v.value, "alignment": a.value, "n_tensors": n.value, "n_parts": p.value}
+
+    def tensor(self, i: int) -> GgufTensor:
+        t = GgufTensor()
+        _check(lib().dq_gguf_tensor_info(self._h, i, C.byref(t)))
+        return t
+
+    def tensors(self) -> list[GgufTensor]:
+        return [self.tensor(i) for i in range(self.info()["n_tensors"])]
+
+    def find(self, name: str) -> int:
+        return int(lib().dq_gguf_find_tensor(self._h, name.encode()))
+
+    def get_uint(self, key: str) -> int:
+        v = C.c_uint64()
+        _check(lib().dq_gguf_get_uint(self._h, key.encode(), C.byref(v)))
+        return v.value
+
+    def get_string(self, key: str) -> str:
+        p, n = C.c_char_p(), _I64()
+        _check(lib().dq_gguf_get_string(self._h, key.encode(), C.byref(p), C.byref(n)))
+        return C.string_at(p, n.value).decode()
+
+    def data(self, name: str) -> bytes:
+        """The tensor's bytes as they lie in the file."""
+        i = self.find(name)
+        if i < 0:
+            raise DqError(2, f"tensor {name!r} not found")
+        t = self.tensor(i)
+        return C.string_at(t.data, t.nbytes)
+
+    def upload(self, name: str, stream: int = 0) -> "Weight":
+        i = self.find(name)
+        if i < 0:
+            raise DqError(2, f"tensor {name!r} not found")
+        h = _P()
+        _check(lib().dq_gguf_upload_weight(self._h, i, stream, C.byref(h)))
+        return Weight(h.value)

@@ -38,6 +38,20 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+}  // namespace
+
+int dq::set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+namespace {
+
 int hip_fail(hipError_t e, const char* what) {
   const int code = e == hipErrorOutOfMemory ? DQ_OUT_OF_MEMORY : DQ_INTERNAL;
   return fail(code, "%s: %s", what, hipGetErrorString(e));

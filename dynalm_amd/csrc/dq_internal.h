@@ -20,6 +20,9 @@ struct WeightDev {
   int64_t plane_bytes[kMaxPlanes] = {0, 0, 0, 0};
 };
 
+// Records the calling thread's error message (dq_last_error) and returns code.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
 hipError_t launch_quantize(int af, const float* x, int64_t m, int64_t k, int64_t x_stride, uint8_t* out, int64_t orb,
                            hipStream_t s);
 hipError_t launch_repack(int t, const uint8_t* src, int64_t row_stride, int64_t n, int64_t nblk, uint8_t* const* planes,

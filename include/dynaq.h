@@ -199,6 +199,49 @@ DQ_API int dq_matmul_gated(int act, const float* x, int64_t m, int64_t x_stride,
                            const dq_weight* w_up, float* out, int64_t out_stride, float* gate_scratch,
                            float* up_scratch, int64_t scratch_stride, void* stream);
 
+/* ---- GGUF files ----------------------------------------------------------
+ * A GGUF v2 / v3 model mapped read-only (mmap): header, metadata and tensor
+ * directory parsed with every length and offset checked against the file
+ * (dynalm/src/loader/gguf/gguf.h:65-125, gguf.cpp:248-343). Opening the first part
+ * of a split model (NAME-00001-of-0000N.gguf) opens all its parts
+ * (dynalm/src/loader/gguf/gguf_model.cpp:291-331); metadata is the first part's.
+ * Status codes: DQ_NOT_FOUND / DQ_IO_ERROR for files that cannot be opened,
+ * DQ_CORRUPT for malformed contents, DQ_UNSUPPORTED for other versions and
+ * unknown tensor types. */
+typedef struct dq_gguf dq_gguf;
+
+/* One tensor of the directory (TensorInfo, gguf.h:65-72). dims are in engine order,
+ * outermost first (a weight of n rows of k values: dims {n, k}); dtype is the
+ * dq_dtype of the four weight types, else -1; data points into the mapping and
+ * stays valid until dq_gguf_close. */
+typedef struct dq_gguf_tensor {
+  const char* name;
+  uint32_t ggml_type;
+  int32_t dtype;
+  int32_t n_dims;
+  int64_t dims[4];
+  uint64_t offset; /* absolute, in its part */
+  uint64_t nbytes;
+  int32_t part;
+  const void* data;
+} dq_gguf_tensor;
+
+DQ_API int dq_gguf_open(const char* path, dq_gguf** out);
+DQ_API int dq_gguf_close(dq_gguf* g);
+DQ_API int dq_gguf_info(const dq_gguf* g, uint32_t* version, uint64_t* alignment, int64_t* n_tensors,
+                        int64_t* n_parts);
+/* Index of the tensor called name, or -1 (GgufFile::find_tensor). */
+DQ_API int64_t dq_gguf_find_tensor(const dq_gguf* g, const char* name);
+DQ_API int dq_gguf_tensor_info(const dq_gguf* g, int64_t i, dq_gguf_tensor* out);
+/* Metadata getters (GgufFile::get_uint / get_string, gguf.h:93,97): integers of any
+ * width that are >= 0; strings as (pointer into the mapping, length). */
+DQ_API int dq_gguf_get_uint(const dq_gguf* g, const char* key, uint64_t* out);
+DQ_API int dq_gguf_get_string(const dq_gguf* g, const char* key, const char** str, int64_t* len);
+/* Upload tensor i (Q4_0 / Q8_0 / Q4_K / Q6_K, two or more dims; the outer dims are
+ * its rows) from the mapping into a device weight, as dq_weight_upload does
+ * (Device::upload of GgufFile::load_tensor's view, gguf.cpp:457-466). */
+DQ_API int dq_gguf_upload_weight(const dq_gguf* g, int64_t i, void* stream, dq_weight** out);
+
 /* Exact integer partials of every (activation row r < m, weight row i < n):
  * units[(r * n + i) * U + u] and sb[(r * n + i) * S + s], with U and S from
  * dq_partials_count; the meaning of each is that of the CPU reference's integer

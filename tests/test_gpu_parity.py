@@ -617,3 +617,41 @@ def test_matmul_gated_rejects(cuda):
         dq.matmul_gated(O.SILU, x, 2, k, wg, wg, y, 64, gate_scratch=y)
     with pytest.raises(dq.DqError):
         dq.matmul_gated(5, x, 2, k, wg, wg, y, 64)
+
+
+# ------------------------------------------------------------- GGUF uploads
+
+
+def test_gguf_upload_round_trip(cuda, tmp_path):
+    """Weights uploaded from a GGUF file (one file and a 3-part split model) download back to the
+    file's bytes, and multiply bit-identically to the same rows uploaded from memory."""
+    from dynalm_amd import torch_ops as T
+    from gguf_writer import GGML_Q4_0, GGML_Q4_K, GGML_Q6_K, GGML_Q8_0, GgufWriter, split_names
+
+    specs = {"q4k": (GGML_Q4_K, O.Q4_K, 96, 512), "q6k": (GGML_Q6_K, O.Q6_K, 64, 768),
+             "q80": (GGML_Q8_0, O.Q8_0, 40, 96), "q40": (GGML_Q4_0, O.Q4_0, 24, 160)}
+    w = GgufWriter(3, 64)
+    rows = {}
+    for i, (name, (gt, t, n, k)) in enumerate(specs.items()):
+        rows[name] = gguf_weights(t, n, k, 700 + i, outlier_frac=0.01)
+        w.tensor(name, gt, [n, k], rows[name].tobytes())
+    experts = gguf_weights(O.Q4_K, 3 * 32, 256, 710)
+    w.tensor("exps", GGML_Q4_K, [3, 32, 256], experts.tobytes())
+    single = tmp_path / "m.gguf"
+    single.write_bytes(w.to_bytes())
+    parts = [tmp_path / p for p in split_names("m", 3)]
+    for p, b in zip(parts, w.split(3)):
+        p.write_bytes(b)
+    for path in (single, parts[0]):
+        with dq.GgufFile.open(str(path)) as g:
+            for name, (gt, t, n, k) in specs.items():
+                wd = g.upload(name)
+                assert (wd.dtype, wd.n, wd.k) == (t, n, k)
+                assert np.array_equal(wd.download(), rows[name]), name
+                m = 3
+                x = dev(activations(m, k, 720))
+                direct = dq.Weight.upload(t, rows[name], k)
+                a, b = host(T.matmul(wd, x)), host(T.matmul(direct, x))
+                assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), name
+            we = g.upload("exps")
+            assert (we.n, we.k) == (96, 256) and np.array_equal(we.download(), experts)
