@@ -33,14 +33,14 @@ import os
 import numpy as np
 
 __all__ = [
-    "Q4_0", "Q8_0", "Q4_K", "Q6_K", "ACT_PER32", "ACT_Q8_0", "ACT_Q8_K", "GEMV_MAX_ROWS",
+    "Q4_0", "Q8_0", "Q4_K", "Q6_K", "ACT_PER32", "ACT_Q8_0", "ACT_Q8_K", "ACT_SX", "GEMV_MAX_ROWS", "matmul_act",
     "DqError", "lib", "lib_path", "row_bytes", "act_row_bytes", "act_format_for", "Weight",
     "act_quantize", "gemv", "gemm", "matmul", "matmul_many", "MatmulJob", "partials_count", "debug_partials",
     "SILU", "GELU", "GELU_TANH", "act_mul", "matmul_gated", "GgufFile", "GgufTensor", "EXPORTS",
 ]
 
 Q4_0, Q8_0, Q4_K, Q6_K = 6, 10, 14, 16
-ACT_PER32, ACT_Q8_0, ACT_Q8_K = 0, 1, 2
+ACT_PER32, ACT_Q8_0, ACT_Q8_K, ACT_SX = 0, 1, 2, 3
 GEMV_MAX_ROWS = 16
 SILU, GELU, GELU_TANH = 0, 1, 2  # dq_activation (dynacore Activation, device/ops.h:14)
 
@@ -78,6 +78,7 @@ EXPORTS = {
     "dq_gemm": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "dq_matmul": (_I, [_P, _P, _I64, _I64, _P, _I64, _P, _P]),
     "dq_matmul_many": (_I, [_P, _I64, _P]),
+    "dq_matmul_act": (_I, [_P, _I, _P, _I64, _I64, _P, _I64, _P, _P]),
     "dq_act_mul": (_I, [_I, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P]),
     "dq_gguf_open": (_I, [C.c_char_p, C.POINTER(_P)]),
     "dq_gguf_close": (_I, [_P]),
@@ -208,6 +209,11 @@ def gemm(w: Weight, fmt: int, acts, m: int, n0: int, n1: int, y, y_stride: int, 
 
 def matmul(w: Weight, x, m: int, x_stride: int, y, y_stride: int, bias=None, stream: int = 0) -> None:
     _check(lib().dq_matmul(w.handle, _ptr(x), m, x_stride, _ptr(y), y_stride, _ptr(bias), stream))
+
+
+def matmul_act(w: Weight, fmt: int, x, m: int, x_stride: int, y, y_stride: int, bias=None, stream: int = 0) -> None:
+    """y = x . w^T (+ bias) under activation contract fmt (ACT_SX: dynacore's sub-scaled int8)."""
+    _check(lib().dq_matmul_act(w.handle, fmt, _ptr(x), m, x_stride, _ptr(y), y_stride, _ptr(bias), stream))
 
 
 class MatmulJob(C.Structure):

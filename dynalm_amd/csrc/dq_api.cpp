@@ -64,13 +64,13 @@ int hip_fail(hipError_t e, const char* what) {
   } while (0)
 
 bool weight_type_ok(int t) { return t == DQ_Q4_0 || t == DQ_Q8_0 || t == DQ_Q4_K || t == DQ_Q6_K; }
-bool act_fmt_ok(int f) { return f == DQ_ACT_PER32 || f == DQ_ACT_Q8_0 || f == DQ_ACT_Q8_K; }
+bool act_fmt_ok(int f) { return f == DQ_ACT_PER32 || f == DQ_ACT_Q8_0 || f == DQ_ACT_Q8_K || f == DQ_ACT_SX; }
 
 // The (weight, activation) pairs with kernels: the per-32 formats with Q8_0 / Q4_0
-// (dynacore's kInt8Per32 contract), Q8_K and per-32 with the K-quants.
+// (dynacore's kInt8Per32 contract); Q8_K, sub-scaled and per-32 with the K-quants.
 bool pair_ok(int t, int f) {
   if (t == DQ_Q8_0 || t == DQ_Q4_0) return f == DQ_ACT_PER32 || f == DQ_ACT_Q8_0;
-  return f == DQ_ACT_Q8_K || f == DQ_ACT_PER32;
+  return f == DQ_ACT_Q8_K || f == DQ_ACT_SX || f == DQ_ACT_PER32;
 }
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
@@ -549,6 +549,32 @@ int dq_matmul_gated(int act, const float* x, int64_t m, int64_t x_stride, const 
   const dq_matmul_job jobs[2] = {{w_gate, x, m, x_stride, gp, ss, nullptr}, {w_up, x, m, x_stride, up, ss, nullptr}};
   if (int rc = dq_matmul_many(jobs, 2, stream); rc != DQ_OK) return rc;
   return dq_act_mul(act, gp, ss, up, ss, m, g.n, out, out_stride, stream);
+}
+
+int dq_matmul_act(const dq_weight* w, int fmt, const float* x, int64_t m, int64_t x_stride, float* y, int64_t y_stride,
+                  const float* bias, void* stream) {
+  if (w == nullptr) return fail(DQ_INVALID_ARGUMENT, "null weight");
+  if (!act_fmt_ok(fmt)) return fail(DQ_UNSUPPORTED, "activation format %d is not supported", fmt);
+  if (!pair_ok(w->dev.dtype, fmt)) {
+    return fail(DQ_UNSUPPORTED, "activation format %d is not supported with weight type %d", fmt, w->dev.dtype);
+  }
+  if (m < 0) return fail(DQ_INVALID_ARGUMENT, "m must be >= 0");
+  if (m == 0) return DQ_OK;
+  if (int rc = check_out(w, m, 0, w->dev.n, y, y_stride); rc != DQ_OK) return rc;
+  if (x == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
+  if (m > 1 && x_stride < w->dev.k) {
+    return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)w->dev.k);
+  }
+  const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
+  if (arb < 0) return fail(DQ_INVALID_ARGUMENT, "k %lld is not a multiple of the activation block", (long long)w->dev.k);
+  hipStream_t s = as_stream(stream);
+  void* acts = nullptr;
+  if (int rc = scratch_get(w->dev.device, (size_t)(m * arb), s, &acts); rc != DQ_OK) return rc;
+  if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, acts, stream); rc != DQ_OK) return rc;
+  if (m > DQ_GEMV_MAX_ROWS && dq::gemm_supported(w->dev.dtype, fmt)) {
+    return dq_gemm(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
+  }
+  return dq_gemv(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
 }
 
 int dq_partials_count(int dtype, int fmt, int64_t k, int64_t* units, int64_t* sb_terms) {

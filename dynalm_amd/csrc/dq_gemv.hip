@@ -133,8 +133,14 @@ struct Chunk<kQ4_0, U> : Chunk32<kQ4_0, U> {};
 //   32-value block   (48 B):   d float @0, code sum int32 @4, codes int8[32] @16
 // (per-32 ActBlockQ8 and GGUF Q8_0 activations both stage as the latter; the GGUF
 // fp16 d converts exactly to float).
+//   sub-scaled super-block (352 B): u float @0, codes int8[256] @16, the block
+//       multipliers m_j int32[8] @272, m_j * s_j int32[8] @304 (s_j the code sum of
+//       32-value block j), and 128 s_j of the odd blocks int32[4] @336
 constexpr int kStageQ8K = 336;
+constexpr int kStageSX = 352;
 constexpr int kStage32 = 48;
+// Staged bytes per super-block of the 256-value activation formats.
+constexpr int stage_sb(int af) { return af == kActSX ? kStageSX : kStageQ8K; }
 
 // Writes the derived forms of sub-block sum s of sub-block j of a staged Q8_K block.
 DQ_DEV void stage_subsum(uint8_t* o, int j, int s) {
@@ -208,6 +214,37 @@ DQ_DEV void compute(const Chunk<kQ4_K, U>& ch, int bb, const uint8_t* st, Out<M>
           p[0] = S;
           p[1] = Mn;
         }
+      } else if (AF == kActSX) {
+        // sub-scaled (kernels_avx2.cpp:1117-1163): S = sum_j sc_j m_j P_j in 64 bits,
+        // Mn = sum_j mn_j (m_j s_j); the Q8_K pair's canonical order with u for da
+        const uint8_t* ab = st + (mm * o.nblk + b) * kStageSX;
+        const v4u codd = lds16(ab + 336);  // 128 s_j, j = 1, 3, 5, 7
+        const v4i mul0 = __builtin_bit_cast(v4i, lds16(ab + 272)), mul1 = __builtin_bit_cast(v4i, lds16(ab + 288));
+        const v4i ms0 = __builtin_bit_cast(v4i, lds16(ab + 304)), ms1 = __builtin_bit_cast(v4i, lds16(ab + 320));
+        int64_t S = 0;
+#pragma unroll
+        for (int jp = 0; jp < 4; ++jp) {
+          const v4u c0 = ch.q[u][2 * jp], c1 = ch.q[u][2 * jp + 1];
+          const uint8_t* cp = ab + 16 + 64 * jp;
+          const int pe = sdot16(c1 & 0x0F0F0F0Fu, lds16(cp + 16), sdot16(c0 & 0x0F0F0F0Fu, lds16(cp), 0));
+          const int x16 = sdot16(c1 & 0xF0F0F0F0u, lds16(cp + 48), sdot16(c0 & 0xF0F0F0F0u, lds16(cp + 32), (int)codd[jp]));
+          const int po = x16 >> 4;
+          const u32 scw = jp < 2 ? sc_lo : sc_hi;
+          const int e = 16 * (jp & 1);
+          const v4i mj = jp < 2 ? mul0 : mul1;
+          S += (int64_t)pe * (int)(bfe(scw, e, 6) * (u32)mj[2 * (jp & 1)]);
+          S += (int64_t)po * (int)(bfe(scw, e + 8, 6) * (u32)mj[2 * (jp & 1) + 1]);
+        }
+        int Mn = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          Mn += (int)bfe(mn_lo, 8 * j, 8) * ms0[j];
+          Mn += (int)bfe(mn_hi, 8 * j, 8) * ms1[j];
+        }
+        float t = d * (float)S;
+        t = fmaf(-dmin, (float)Mn, t);
+        o.rec[(mm * o.nblk + b) * 64 + o.r] = t;
+        if (o.r == 0) o.dav[mm * o.nblk + b] = as_f(lds4(ab));
       } else {
         // per-32 activations, sub-block order j = 0..7 (kernels_generic.cpp:267-275)
 #pragma unroll
@@ -275,6 +312,27 @@ DQ_DEV void compute(const Chunk<kQ6_K, U>& ch, int bb, const uint8_t* st, Out<M>
           p[0] = S;
           p[1] = 0;
         }
+      } else if (AF == kActSX) {
+        // sub-scaled (kernels_avx2.cpp:1165-1216): S = sum_u sc_u m_(u/2) P_u in 64 bits,
+        // the 16-value code sums for the -32 correction from the staged codes
+        const uint8_t* ab = st + (mm * o.nblk + b) * kStageSX;
+        const v4i mul0 = __builtin_bit_cast(v4i, lds16(ab + 272)), mul1 = __builtin_bit_cast(v4i, lds16(ab + 288));
+        const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
+        int64_t S = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const int ulo = 8 * (c >> 2) + (c & 3), uhi = ulo + 4;
+          const v4u alo = lds16(ab + 16 + 16 * ulo), ahi = lds16(ab + 16 + 16 * uhi);
+          const int plo = sdot16(qlo[c], alo, 0) - 32 * sdot16(ones, alo, 0);
+          const int phi = sdot16(qhi[c], ahi, 0) - 32 * sdot16(ones, ahi, 0);
+          const u32 wl = ulo < 4 ? ch.SC[u].x : ulo < 8 ? ch.SC[u].y : ulo < 12 ? ch.SC[u].z : ch.SC[u].w;
+          const u32 wh = uhi < 4 ? ch.SC[u].x : uhi < 8 ? ch.SC[u].y : uhi < 12 ? ch.SC[u].z : ch.SC[u].w;
+          const int mlo = (ulo >> 1) < 4 ? mul0[(ulo >> 1) & 3] : mul1[(ulo >> 1) & 3];
+          const int mhi = (uhi >> 1) < 4 ? mul0[(uhi >> 1) & 3] : mul1[(uhi >> 1) & 3];
+          S += (int64_t)plo * (sbfe(wl, 8 * (ulo & 3), 8) * mlo) + (int64_t)phi * (sbfe(wh, 8 * (uhi & 3), 8) * mhi);
+        }
+        o.rec[(mm * o.nblk + b) * 64 + o.r] = d * (float)S;
+        if (o.r == 0) o.dav[mm * o.nblk + b] = as_f(lds4(ab));
       } else {
         // per-32 activations, units of 16 in order (kernels_generic.cpp:299-306)
         const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
@@ -339,7 +397,34 @@ DQ_DEV void stage_acts(const uint8_t* __restrict__ acts, int64_t arb, int nblk, 
   // For each block the loads of all M rows go out together, then the stores:
   // M loads in flight per round trip instead of one.
   const auto ra = rsrc(acts, (u32)(M * arb));
-  if constexpr (AF == kActQ8_K) {
+  if constexpr (AF == kActSX) {
+    // lane r: codes dword r; lanes 0..4 also u and the m pairs. The block sums s_j
+    // come from the codes (8 lanes per 32-value block), m_j from lane 1 + j / 2.
+    for (int b = b0; b < b1; ++b) {
+      u32 v[M][2];
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) {
+        const u32 base = (u32)(mm * arb + (int64_t)b * 320);
+        v[mm][0] = ld4(ra, base + 4 * r);
+        v[mm][1] = ld4(ra, base + 256 + 4 * (r < 5 ? r : 0));
+      }
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) {
+        uint8_t* o = st + (mm * nblk + b) * kStageSX;
+        const int j = r >> 3;
+        const int sj = red8(sdot4(v[mm][0], 0x01010101u, 0));
+        const u32 mw = (u32)__shfl((int)v[mm][1], 1 + (j >> 1));
+        const int mj = (int)(int16_t)(mw >> (16 * (j & 1)));
+        *reinterpret_cast<u32*>(o + 16 + 4 * r) = v[mm][0];
+        if (r == 0) *reinterpret_cast<u32*>(o) = v[mm][1];
+        if ((r & 7) == 0) {
+          *reinterpret_cast<int*>(o + 272 + 4 * j) = mj;
+          *reinterpret_cast<int*>(o + 304 + 4 * j) = mj * sj;
+          if (j & 1) *reinterpret_cast<int*>(o + 336 + 4 * (j >> 1)) = 128 * sj;
+        }
+      }
+    }
+  } else if constexpr (AF == kActQ8_K) {
     for (int b = b0; b < b1; ++b) {
       u32 v[M][2];
 #pragma unroll
@@ -558,8 +643,9 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
                                                  const uint8_t* __restrict__ q2, const uint8_t* __restrict__ q3,
                                                  int act) {
   extern __shared__ __align__(16) uint8_t smem[];
-  constexpr bool kSb = AF == kActQ8_K;
+  constexpr bool kSb = AF == kActQ8_K || AF == kActSX;
   static_assert(!kGated || (kSb && M == 1 && kFuse), "the gated GEMV takes one fp32 row and K-quant weights");
+  static_assert(AF != kActSX || (!kFuse && kEarly == 0), "sub-scaled activations arrive quantized and staged by loops");
   // LDS: Q8_K t-terms [M][nblk][64] + da [M][nblk]  |  per-32 slice sums [W][M][64];
   // then the staged activation rows [M][nblk (blocks of 32 for per-32)][stage bytes].
   // kGated: one t-term region and one stage region per weight.
@@ -581,7 +667,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
   for (int mm = 0; mm < M; ++mm) o.acc[mm] = 0.0f;
   const int b0 = wl * nblk / WH, b1 = (wl + 1) * nblk / WH;  // this wave's blocks
   // bytes of the staged activation rows (the dummy area of the early path follows)
-  const int stage_bytes = kSb ? M * nblk * kStageQ8K : M * nblk * ((WT == kQ4_K || WT == kQ6_K) ? 8 : 1) * kStage32;
+  const int stage_bytes = kSb ? M * nblk * stage_sb(AF) : M * nblk * ((WT == kQ4_K || WT == kQ6_K) ? 8 : 1) * kStage32;
   uint8_t* st = smem + (kGated ? 2 : 1) * region + half * stage_bytes;
 
   // plane buffer resources of this row group (64 rows x nblk blocks)
@@ -713,9 +799,9 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
 // kStageQ8K B, 32-value blocks of kStage32 B); the dummy area of the early path.
 constexpr size_t kGemvMaxLds = 160 * 1024;
 static size_t gemv_lds_bytes(int wt, int af, int m, int waves, int64_t nblk, bool early) {
-  size_t lds = af == kActQ8_K ? ((size_t)m * nblk * 65 * sizeof(float) + 15) / 16 * 16
-                              : (size_t)waves * m * 64 * sizeof(float);
-  lds += af == kActQ8_K ? (size_t)m * nblk * kStageQ8K
+  const bool sb = af == kActQ8_K || af == kActSX;
+  size_t lds = sb ? ((size_t)m * nblk * 65 * sizeof(float) + 15) / 16 * 16 : (size_t)waves * m * 64 * sizeof(float);
+  lds += sb ? (size_t)m * nblk * stage_sb(af)
                         : (size_t)m * nblk * (wt == kQ4_K || wt == kQ6_K ? 8 : 1) * kStage32;
   if (early) lds += kDummyBytes;
   return lds;
@@ -758,7 +844,7 @@ static hipError_t gemv_early(const WeightDev& w, const uint8_t* acts, int64_t ar
   if constexpr (M == 1 && AF == kActQ8_K) {
     if (per_wave == 1) return gemv_launch<WT, AF, M, kFuse, W, 1>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
     if (per_wave == 2) return gemv_launch<WT, AF, M, kFuse, W, 2>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
-  } else if constexpr (M == 1 && !kFuse) {
+  } else if constexpr (M == 1 && !kFuse && AF != kActSX) {
     const int64_t bpu = WT == kQ4_K || WT == kQ6_K ? 8 : 1;
     if (per_wave * bpu <= 64) {
       return gemv_launch<WT, AF, M, kFuse, W, 1>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
@@ -794,9 +880,11 @@ static hipError_t gemv_pass(const WeightDev& w, int af, const uint8_t* acts, int
   }
   switch (w.dtype) {
     case kQ4_K:
+      if (af == kActSX) return gemv_waves<kQ4_K, kActSX, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
       return af == kActQ8_K ? gemv_waves<kQ4_K, kActQ8_K, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
                             : gemv_waves<kQ4_K, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
     case kQ6_K:
+      if (af == kActSX) return gemv_waves<kQ6_K, kActSX, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
       return af == kActQ8_K ? gemv_waves<kQ6_K, kActQ8_K, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
                             : gemv_waves<kQ6_K, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
     case kQ8_0:

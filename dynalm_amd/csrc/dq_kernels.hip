@@ -36,6 +36,29 @@ __global__ __launch_bounds__(64) void k_quant_q8k(const float* __restrict__ x, i
   if (l == 0) *reinterpret_cast<float*>(o) = d;
 }
 
+// Sub-scaled ActSuperQ8 (320 B per 256 values: codes @0, u @256, m int16[8] @260,
+// ms float[8] @276 with ms = (u m) sum, 12 zero bytes), one wave per super-block.
+__global__ __launch_bounds__(64) void k_quant_sx(const float* __restrict__ x, int64_t x_stride, int64_t k,
+                                                 uint8_t* __restrict__ out, int64_t orb) {
+  const int l = threadIdx.x;
+  const int64_t sb = blockIdx.x, row = blockIdx.y;
+  const auto rx = rsrc(x + row * x_stride, (u32)(k * 4));
+  float v[4];
+  load4f(rx, (u32)((sb * 256 + 4 * l) * 4), v);
+  float u;
+  int m, sum;
+  const u32 packed = sx_quant(v, u, m, sum);
+  uint8_t* o = out + row * orb + sb * 320;
+  *reinterpret_cast<u32*>(o + 4 * l) = packed;
+  if ((l & 7) == 0) {
+    const int b = l >> 3;
+    *reinterpret_cast<int16_t*>(o + 260 + 2 * b) = (int16_t)m;
+    *reinterpret_cast<float*>(o + 276 + 4 * b) = (u * (float)m) * (float)sum;
+  }
+  if (l == 0) *reinterpret_cast<float*>(o + 256) = u;
+  if (l >= 1 && l <= 3) *reinterpret_cast<u32*>(o + 304 + 4 * l) = 0u;
+}
+
 // Per-32 blocks (ActBlockQ8 40 B or GGUF Q8_0 34 B): 8 lanes per block.
 template <int AF>
 __global__ __launch_bounds__(64) void k_quant_b32(const float* __restrict__ x, int64_t x_stride, int64_t k,
@@ -116,6 +139,7 @@ DQ_DEV int act_code(int af, const uint8_t* a, int64_t i) {
   switch (af) {
     case kActPer32: return (int8_t)a[(i / 32) * 40 + 8 + i % 32];
     case kActQ8_0: return (int8_t)a[(i / 32) * 34 + 2 + i % 32];
+    case kActSX: return (int8_t)a[(i / 256) * 320 + i % 256];
     default: return (int8_t)a[(i / 256) * 292 + 4 + i % 256];
   }
 }
@@ -202,6 +226,8 @@ hipError_t launch_quantize(int af, const float* x, int64_t m, int64_t k, int64_t
   if (m == 0 || k == 0) return hipSuccess;
   if (af == kActQ8_K) {
     hipLaunchKernelGGL(k_quant_q8k, dim3((unsigned)(k / 256), (unsigned)m), dim3(64), 0, s, x, x_stride, k, out, orb);
+  } else if (af == kActSX) {
+    hipLaunchKernelGGL(k_quant_sx, dim3((unsigned)(k / 256), (unsigned)m), dim3(64), 0, s, x, x_stride, k, out, orb);
   } else if (af == kActPer32) {
     hipLaunchKernelGGL(k_quant_b32<kActPer32>, dim3((unsigned)((k + 255) / 256), (unsigned)m), dim3(64), 0, s, x,
                        x_stride, k, out, orb);

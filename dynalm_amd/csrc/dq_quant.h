@@ -3,7 +3,8 @@
 // (dq_gemv.hip), so both write the same code bytes.
 //
 // Contracts: per-32 ActBlockQ8 dynacore/cpu/generic/kernels_generic.cpp:187-207;
-// one scale per 256 values (Q8_K) dynacore/cpu/avx2/kernels_avx2.cpp:638-644.
+// one scale per 256 values (Q8_K) dynacore/cpu/avx2/kernels_avx2.cpp:638-644;
+// sub-scaled ActSuperQ8 dynacore/cpu/avx2/kernels_avx2.cpp:1077-1096.
 #pragma once
 
 #include "dq_device.h"
@@ -71,6 +72,31 @@ DQ_DEV u32 per32_quant(const float v[4], float& d, int& sum) {
   int s = 0;
   const u32 packed = codes4_rne(v, id, s);
   sum = red8(s);
+  return packed;
+}
+
+// Sub-scaled ActSuperQ8 quantization (kernels_avx2.cpp:1077-1096) of one 256-value
+// super-block held 4 values per lane (lanes 8b .. 8b+7 hold 32-value block b):
+// u = amax256 / (127 * 128); the block's multiplier m = clamp(ceil(amax32 / (127 u)),
+// 1, 128) (1 when u == 0); codes round half to even at scale u * m. Returns the
+// lane's packed codes, u, and (in every lane of the block) m and the code sum.
+DQ_DEV u32 sx_quant(const float v[4], float& u, int& m, int& sum) {
+  const float a32 = max8f(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  float amax = fmaxf(a32, as_f((u32)dpp<kRowRor8>((int)as_u(a32))));  // rows of 16 lanes
+  const float r0 = as_f(__builtin_amdgcn_readlane(as_u(amax), 0)), r1 = as_f(__builtin_amdgcn_readlane(as_u(amax), 16));
+  const float r2 = as_f(__builtin_amdgcn_readlane(as_u(amax), 32)), r3 = as_f(__builtin_amdgcn_readlane(as_u(amax), 48));
+  amax = fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+  u = amax / (127.0f * 128.0f);
+  m = 1;
+  if (u > 0) {
+    const int c = (int)ceilf(a32 / (127.0f * u));
+    m = c < 1 ? 1 : (c > 128 ? 128 : c);
+  }
+  const float s = u * (float)m;
+  const float id = s > 0 ? 1.0f / s : 0.0f;
+  int cs = 0;
+  const u32 packed = codes4_rne(v, id, cs);
+  sum = red8(cs);
   return packed;
 }
 

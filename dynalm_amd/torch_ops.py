@@ -49,6 +49,15 @@ def matmul(w: dq.Weight, x: torch.Tensor, bias: torch.Tensor | None = None,
     return y
 
 
+def matmul_act(w: dq.Weight, fmt: int, x: torch.Tensor, bias: torch.Tensor | None = None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """x . w^T under activation contract fmt (one quantize launch, then the GEMV / GEMM)."""
+    m = x.shape[0]
+    y = torch.empty((m, w.n), dtype=torch.float32, device=x.device) if out is None else out
+    dq.matmul_act(w, fmt, x, m, x.stride(0), y, y.stride(0), bias, stream())
+    return y
+
+
 def partials(w: dq.Weight, fmt: int, acts: torch.Tensor):
     m = acts.shape[0]
     nu, ns = dq.partials_count(w.dtype, fmt, w.k)

@@ -74,11 +74,21 @@ typedef enum dq_dtype {
  *   DQ_ACT_Q8_K   GGUF block_q8_K {float d; int8 q[256]; int16 bsums[16]}, 292 B per 256,
  *                 d = amax256/127, codes round half to even
  *                 (dynacore/include/dynacore/quantization/quant_formats.h:30,
- *                  dynacore/cpu/avx2/kernels_avx2.cpp:638-644). */
+ *                  dynacore/cpu/avx2/kernels_avx2.cpp:638-644);
+ *   DQ_ACT_SX     dynacore ActSuperQ8 {int8 q[256]; float u; int16 m[8]; float ms[8];
+ *                 int32 pad[3]}, 320 B per 256: sub-scaled activations (DD-077), dynacore's
+ *                 validated default for K-quant decode rows on x86. u = amax256/(127*128),
+ *                 per 32 values the smallest m in 1..128 with amax32 <= 127*u*m, codes round
+ *                 half to even at u*m, ms = (u*m)*sum
+ *                 (dynacore/include/dynacore/cpu/cpu_kernels.h:56-70,
+ *                  dynacore/cpu/avx2/kernels_avx2.cpp:1077-1096). With Q4_K / Q6_K only; the
+ *                 kernels form S = sum sc_j*m_j*P_j exactly (64 bits) and the mins term from
+ *                 the integer m_j*sum_j. */
 typedef enum dq_act_format {
   DQ_ACT_PER32 = 0,
   DQ_ACT_Q8_0 = 1,
   DQ_ACT_Q8_K = 2,
+  DQ_ACT_SX = 3,
 } dq_act_format;
 
 /* Activation rows at or below which dq_matmul runs the GEMV kernels. */
@@ -139,6 +149,14 @@ DQ_API int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int
  * dynacore/cpu/cpu_device.cpp:869-1177). Uses a per-device scratch buffer. */
 DQ_API int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, float* y, int64_t y_stride,
                      const float* bias, void* stream);
+
+/* y = x . w^T (+ bias) with the activations quantized to format fmt (the caller's
+ * choice of dynacore's activation contract, which KernelPlan makes per matmul:
+ * dynacore/include/dynacore/kernel/kernel_plan.h:50-92). One quantize launch into
+ * the per-device scratch, then dq_gemv (dq_gemm where it supports the pair and
+ * m > DQ_GEMV_MAX_ROWS). Replaces Device::matmul under a chosen contract. */
+DQ_API int dq_matmul_act(const dq_weight* w, int fmt, const float* x, int64_t m, int64_t x_stride, float* y,
+                         int64_t y_stride, const float* bias, void* stream);
 
 /* One matmul of dq_matmul_many: y = x . w^T (+ bias) for m rows of x (x_stride
  * floats apart, w's k values each) into y (y_stride floats apart). The fields are

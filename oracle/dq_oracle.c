@@ -519,7 +519,8 @@ static int pair_ok(int wtype, int fmt) {
 int dqo_partials_count(int wtype, int fmt, int64_t k, int64_t* units, int64_t* sb_terms) {
   if (!pair_ok(wtype, fmt) || dqo_row_bytes(wtype, k) < 0 || dqo_act_row_bytes(fmt, k) < 0) return -1;
   *units = wtype == DQO_Q6_K ? k / 16 : k / 32;
-  *sb_terms = (wtype == DQO_Q4_K || wtype == DQO_Q6_K) && fmt != DQO_ACT_PER32 ? 2 * (k / 256) : 0;
+  *sb_terms = !(wtype == DQO_Q4_K || wtype == DQO_Q6_K) || fmt == DQO_ACT_PER32 ? 0
+              : fmt == DQO_ACT_SX ? 3 * (k / 256) : 2 * (k / 256);
   return 0;
 }
 
@@ -568,7 +569,10 @@ static void weight_codes(int wtype, const uint8_t* w, int64_t b, int8_t* q) {
  *   Q6_K: P_u over 16 values (kernels_generic.cpp:282-310)
  *   Q4_K x Q8_K: S = sum_j sc_j P_j, Mn = sum_j m_j sum_j (kernels_avx2.cpp:976-1014)
  *   Q6_K x Q8_K: S = sum_u sc_u P_u (kernels_avx2.cpp:1019-1058)
- *   x sub-scaled: S = sum sc * m_b * P (kernels_avx2.cpp:1117-1216), Mn as Q8_K. */
+ *   x sub-scaled: S = sum sc * m_b * P (kernels_avx2.cpp:1117-1216) in 64 bits (it can
+ *     exceed 2^31: 8 * 63 * 128 * 32 * 15 * 127), reported as its low and high
+ *     words; Mn = sum_j m_j * (m_b * sum_b of the sub-block's codes), the exact
+ *     integer behind the reference's ms_b = u * m_b * sum_b (kernels_avx2.cpp:1087-1092). */
 int dqo_partials(int wtype, int fmt, const void* wrow, const void* arow, int64_t k, int32_t* units, int32_t* sb) {
   int64_t nu, ns;
   if (dqo_partials_count(wtype, fmt, k, &nu, &ns) != 0) return -1;
@@ -588,7 +592,8 @@ int dqo_partials(int wtype, int fmt, const void* wrow, const void* arow, int64_t
   for (int64_t b = 0; b < k / 256; ++b) {
     weight_codes(wtype, w, b, q);
     const uint8_t* blk = w + b * (wtype == DQO_Q4_K ? 144 : 210);
-    int32_t S = 0, Mn = 0;
+    int64_t S = 0;
+    int32_t Mn = 0;
     for (int u = 0; u < 256 / ul; ++u) {
       int32_t p = 0;
       for (int t = 0; t < ul; ++t) p += (int32_t)q[ul * u + t] * act_code(fmt, a, 256 * b + ul * u + t);
@@ -598,15 +603,22 @@ int dqo_partials(int wtype, int fmt, const void* wrow, const void* arow, int64_t
         uint8_t sc, mn;
         dqo_scale_min_k4(u, blk + 4, &sc, &mn);
         scale = sc;
-        if (ns) Mn += (int32_t)mn * act_sum32(fmt, a, 8 * b + u);
+        if (ns) {
+          const int32_t mb = fmt == DQO_ACT_SX ? rd16s(a + b * 320 + 260 + 2 * u) : 1;
+          Mn += (int32_t)mn * (mb * act_sum32(fmt, a, 8 * b + u));
+        }
       } else {
         scale = (int8_t)blk[192 + u];
       }
       if (fmt == DQO_ACT_SX) scale *= rd16s(a + b * 320 + 260 + 2 * (u * ul / 32));
-      S += scale * p;
+      S += (int64_t)scale * p;
     }
-    if (ns) {
-      sb[2 * b] = S;
+    if (ns && fmt == DQO_ACT_SX) {
+      sb[3 * b] = (int32_t)(uint32_t)((uint64_t)S & 0xFFFFFFFFu);
+      sb[3 * b + 1] = (int32_t)(S >> 32);
+      sb[3 * b + 2] = Mn;
+    } else if (ns) {
+      sb[2 * b] = (int32_t)S;
       sb[2 * b + 1] = Mn;
     }
   }
@@ -620,8 +632,8 @@ float dqo_dot(int wtype, int fmt, const void* wrow, const void* arow, int64_t k)
   const uint8_t* w = (const uint8_t*)wrow;
   const uint8_t* a = (const uint8_t*)arow;
   int32_t units[4096 / 16 + 16];
-  int32_t sb[2];
-  float acc = 0.0f, corr = 0.0f;
+  int32_t sb[3];
+  float acc = 0.0f;
 
   if (wtype == DQO_Q8_0 || wtype == DQO_Q4_0) {
     /* dot_rows_q8_0 / dot_rows_q4_0 (kernels_generic.cpp:216-239):
@@ -675,15 +687,14 @@ float dqo_dot(int wtype, int fmt, const void* wrow, const void* arow, int64_t k)
         float u = d * (float)sb[0];
         u = fmaf(-dmin, (float)sb[1], u);
         acc = fmaf(da, u, acc);
-      } else { /* sub-scaled, kernels_avx2.cpp:1221-1268 */
-        const uint8_t* ab = a + b * 320;
-        const float u = rdf(ab + 256);
-        acc = fmaf((float)sb[0], d * u, acc);
-        for (int j = 0; j < 8; ++j) {
-          uint8_t sc, mn;
-          dqo_scale_min_k4(j, blk + 4, &sc, &mn);
-          corr = fmaf(dmin * (float)mn, rdf(ab + 276 + 4 * j), corr);
-        }
+      } else {
+        /* sub-scaled (kernels_avx2.cpp:1117-1163): the exact S and Mn of
+         * dqo_partials in the canonical order of the Q8_K pair, u in place of da. */
+        const float u = rdf(a + b * 320 + 256);
+        const int64_t S = (int64_t)(((uint64_t)(uint32_t)sb[1] << 32) | (uint32_t)sb[0]);
+        float t = d * (float)S;
+        t = fmaf(-dmin, (float)sb[2], t);
+        acc = fmaf(u, t, acc);
       }
     } else { /* Q6_K */
       const float d = dqo_fp16_to_fp32(rd16(blk + 208));
@@ -704,11 +715,12 @@ float dqo_dot(int wtype, int fmt, const void* wrow, const void* arow, int64_t k)
         acc = fmaf(da, u, acc);
       } else {
         const float u = rdf(a + b * 320 + 256);
-        acc = fmaf((float)sb[0], d * u, acc);
+        const int64_t S = (int64_t)(((uint64_t)(uint32_t)sb[1] << 32) | (uint32_t)sb[0]);
+        acc = fmaf(u, d * (float)S, acc);
       }
     }
   }
-  return acc - corr;
+  return acc;
 }
 
 int dqo_matmul(int wtype, int fmt, const void* w, int64_t w_row_bytes, int64_t n, const void* acts,

@@ -8,6 +8,8 @@ cross-checks (GEMV vs GEMM on the same inputs, row-range splits).
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -655,3 +657,89 @@ def test_gguf_upload_round_trip(cuda, tmp_path):
                 assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), name
             we = g.upload("exps")
             assert (we.n, we.k) == (96, 256) and np.array_equal(we.download(), experts)
+
+
+# ------------------------------------------- sub-scaled activations (DD-077)
+
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_vectors.npz")
+
+
+def _gold():
+    with np.load(GOLDEN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.mark.parametrize("k", [256, 4096, 14336])
+def test_quantize_sx_bit_exact(cuda, k):
+    """dynacore's quantize_act_sx (kernels_avx2.cpp:1077-1096): zero, constant, outlier and tie rows."""
+    x = activations(6, k, 1100 + k)
+    x[1, :] = 0.0
+    x[2, :] = 3.0                                         # every multiplier 128, every code 127
+    x[3, :64] *= 1e-4                                     # small blocks beside large ones: m from 1 up
+    x[4, 5] = 3.0e38
+    x[5, :32] = np.linspace(-15.5, 15.5, 32)
+    assert np.array_equal(quant_gpu(O.ACT_SX, x, stride_pad=5), O.quantize_act(O.ACT_SX, x))
+
+
+def test_quantize_sx_matches_reference_golden(cuda):
+    gold = _gold()
+    assert np.array_equal(quant_gpu(O.ACT_SX, gold["act_x"]), gold["act_sx"])
+
+
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q6_K], ids=lambda t: O.TYPE_NAMES[t])
+@pytest.mark.parametrize("m", [1, 3, 8, 11])
+def test_gemv_sx_parity(cuda, t, m):
+    """Sub-scaled GEMV: bit-identical to the oracle's canonical order; integer unit partials exact."""
+    from dynalm_amd import torch_ops as T
+
+    k, n = 1280, 200
+    rows = gguf_weights(t, n, k, 1200 + m, outlier_frac=0.01)
+    x = activations(m, k, 1210 + m)
+    a = O.quantize_act(O.ACT_SX, x)
+    w = dq.Weight.upload(t, rows, k)
+    y = host(T.gemv(w, O.ACT_SX, dev(a)))
+    want = O.matmul(t, O.ACT_SX, rows, a, k)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+    units, _ = T.partials(w, O.ACT_SX, dev(a))
+    want_u, _ = O.partials(t, O.ACT_SX, rows, a, k)
+    assert np.array_equal(host(units), want_u)
+    # dq_matmul_act: quantization on the GPU, then the same kernel
+    ya = host(T.matmul_act(w, O.ACT_SX, dev(x)))
+    assert np.array_equal(ya.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q6_K], ids=lambda t: O.TYPE_NAMES[t])
+def test_gemv_sx_vs_reference_avx2(cuda, t):
+    """Against the reference's own sub-scaled AVX2 kernel (golden sxdot_*, the contract dynacore runs
+    by default on x86): fp32 reorderings only."""
+    from dynalm_amd import torch_ops as T
+
+    gold = _gold()
+    name = O.TYPE_NAMES[t]
+    w = dq.Weight.upload(t, gold[f"w_{name}"], 512)
+    y = host(T.gemv(w, O.ACT_SX, dev(gold["act_sx"])))
+    ref = gold[f"sxdot_{name}"]
+    assert np.max(np.abs(y - ref)) <= 1e-5 * np.abs(ref).max()
+
+
+def test_gemv_sx_s_beyond_int32(cuda):
+    """Constant inputs and extreme Q4_K weights push S = sum sc m P past 2^31; the GPU keeps it exact."""
+    from dynalm_amd import torch_ops as T
+
+    k = 512
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[4:8] = 0xFF
+    blk[12:16] = 0x0F
+    blk[16:] = 0xFF
+    rows = np.tile(np.tile(blk, k // 256)[None, :], (64, 1))
+    rows[1::2, 16:144] = 0x77                               # a second code pattern on odd rows
+    x = np.full((2, k), 3.0, np.float32)
+    x[1] *= -1.0
+    a = O.quantize_act(O.ACT_SX, x)
+    w = dq.Weight.upload(O.Q4_K, rows, k)
+    y = host(T.gemv(w, O.ACT_SX, dev(a)))
+    want = O.matmul(O.Q4_K, O.ACT_SX, rows, a, k)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+    assert abs(float(want[0, 0])) > 0

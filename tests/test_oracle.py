@@ -284,10 +284,17 @@ def test_partials_brute_force(t, fmt):
                         mult = list(a[r, b * 320 + 260:b * 320 + 276].copy().view(np.int16))
                     nunit = 256 // ul
                     S = sum(int(scale[u]) * int(mult[u * ul // 32]) * int(prod[r, n, b * nunit + u]) for u in range(nunit))
-                    assert sb[r, n, 2 * b] == S
-                    if t == O.Q4_K:
-                        sums = ac[r, b * 256:(b + 1) * 256].reshape(8, 32).sum(-1)
-                        assert sb[r, n, 2 * b + 1] == sum(int(mins[j]) * int(sums[j]) for j in range(8))
+                    sums = ac[r, b * 256:(b + 1) * 256].reshape(8, 32).sum(-1)
+                    Mn = sum(int(mins[j]) * int(mult[j]) * int(sums[j]) for j in range(8))
+                    if fmt == O.ACT_SX:  # S in 64 bits: low and high words, then Mn
+                        got = (int(sb[r, n, 3 * b + 1]) << 32) | (int(sb[r, n, 3 * b]) & 0xFFFFFFFF)
+                        assert got == S
+                        if t == O.Q4_K:
+                            assert sb[r, n, 3 * b + 2] == Mn
+                    else:
+                        assert sb[r, n, 2 * b] == S
+                        if t == O.Q4_K:
+                            assert sb[r, n, 2 * b + 1] == Mn
 
 
 # -------------------------------------------------------------------- dots
@@ -468,3 +475,30 @@ def test_matmul_gated_vs_double(act):
     ref = _act_double(act, g.astype(np.float32).ravel()).reshape(g.shape) * u
     scale = np.maximum(np.abs(g), 1.0) * np.maximum(np.abs(u), 1.0)
     assert np.max(np.abs(y - ref) / scale) < 1e-4
+
+
+def _q4k_extreme_row(k: int) -> np.ndarray:
+    """Q4_K row with every scale 63, every min 0, every code 15 and d = 1: the largest S."""
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[4:8] = 0xFF      # sc_0..3 = 63 and the top bits of sc_4..7
+    blk[12:16] = 0x0F    # low bits of sc_4..7 (mins stay 0)
+    blk[16:] = 0xFF
+    return np.tile(blk, k // 256)[None, :]
+
+
+def test_subscaled_s_exceeds_int32():
+    """Sub-scaled S = sum sc * m_b * P exceeds 2^31 for constant inputs and extreme weights; the
+    oracle keeps it exact (64 bits) and the dot matches the double product."""
+    k = 256
+    w = _q4k_extreme_row(k)
+    assert [_scale_min_bitfields(bytes(w[0, 4:16]), j) for j in range(8)] == [(63, 0)] * 8
+    x = np.full((1, k), 3.0, np.float32)
+    a = O.quantize_act(O.ACT_SX, x)
+    assert np.all(a[0, 260:276].view(np.int16) == 128) and np.all(a[0, :256].view(np.int8) == 127)
+    _, sb = O.partials(O.Q4_K, O.ACT_SX, w, a, k)
+    S = (int(sb[0, 0, 1]) << 32) | (int(sb[0, 0, 0]) & 0xFFFFFFFF)
+    assert S == 8 * 63 * 128 * 32 * 15 * 127 > 2 ** 31
+    y = O.matmul(O.Q4_K, O.ACT_SX, w, a, k)
+    ref = float(O.dequantize_act(O.ACT_SX, a, k).astype(np.float64) @ O.dequantize(O.Q4_K, w[0], k).ravel())
+    assert abs(float(y[0, 0]) - ref) <= 1e-6 * abs(ref)
