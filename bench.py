@@ -224,7 +224,7 @@ def decode_stack(steps: int, stream: int) -> dict:
 
 def prefill_sweep(ms: list[int], weights, gen) -> list[dict]:
     """Config 4's sweep: dq_matmul on M fp32 rows (Q8_K quantization on the GPU, then
-    the kernel dq_matmul dispatches to: the skinny MFMA GEMV up to 64 rows, the MFMA
+    the kernel dq_matmul dispatches to: the skinny MFMA GEMV up to 16 rows, the MFMA
     GEMM above), K=4096 N=14336, rotated weights, graph replay."""
     import torch
 
@@ -239,7 +239,7 @@ def prefill_sweep(ms: list[int], weights, gen) -> list[dict]:
         log(f"prefill sweep M={m} x{iters}")
         ms_call = time_graph(lambda i, st: dq.matmul(weights[i % ng], x, m, K, y, N, None, st), iters, 3)
         tops = 2.0 * m * N * K / (ms_call * 1e-3) / 1e12
-        out.append({"m": m, "kernel": "skinny MFMA GEMV" if m <= 64 else "MFMA GEMM",
+        out.append({"m": m, "kernel": "skinny MFMA GEMV" if m <= 16 else "MFMA GEMM",
                     "ms_per_call": round(ms_call, 4), "tops": round(tops, 1),
                     "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2), "tokens_per_s": round(m / (ms_call * 1e-3), 1)})
         del x, y
@@ -442,7 +442,7 @@ def main() -> None:
             "tops": round(tops, 2),
             "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2),
             "tokens_per_s": round(m / (ms_gemm * 1e-3), 1),
-            "roofline": {"kernel": "k_gemm_q4k", "bound": "mfma", "achieved": round(tops, 2),
+            "roofline": {"kernel": "dq::k_gemm_q4k_big<4, 2, 4>", "bound": "mfma", "achieved": round(tops, 2),
                          "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4),
                          "traffic": traffic.get("gemm_m512")},
         },

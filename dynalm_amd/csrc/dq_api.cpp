@@ -189,10 +189,14 @@ int check_out(const dq_weight* w, int64_t m, int64_t n0, int64_t n1, float* y, i
   return DQ_OK;
 }
 
-// The skinny path from fp32 rows: K-quant weights, 2 <= m <= 64, LDS for the
-// weight's super-blocks, and fp32 rows addressable with 32-bit offsets.
+// The skinny path from fp32 rows: K-quant weights, 2 <= m <= 64 (m <= DQ_GEMV_MAX_ROWS
+// where the pair has a GEMM, which is faster above that: 21-23 us against 31-43 us
+// for 24..64 rows at K=4096, N=14336), LDS for the weight's super-blocks, and fp32
+// rows addressable with 32-bit offsets.
 bool skinny_ok(const dq_weight* w, const float* x, int64_t m, int64_t x_stride) {
-  if (x == nullptr || !dq::gemv_mma_supported(w->dev.dtype, dq_act_format_for(w->dev.dtype), m)) return false;
+  const int fmt = dq_act_format_for(w->dev.dtype);
+  if (x == nullptr || !dq::gemv_mma_supported(w->dev.dtype, fmt, m)) return false;
+  if (m > DQ_GEMV_MAX_ROWS && dq::gemm_supported(w->dev.dtype, fmt)) return false;
   if (!dq::gemv_mma_lds_ok(w->dev.nblk, m)) return false;
   const int64_t xs = m > 1 ? x_stride : w->dev.k;
   return m * xs * 4 < ((int64_t)1 << 32);

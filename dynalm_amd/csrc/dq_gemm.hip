@@ -1,5 +1,5 @@
 // dq_gemm.hip -- prefill GEMM for Q4_K weights x Q8_K activations on gfx950 int8
-// MFMA (v_mfma_i32_16x16x64_i8).
+// MFMA (v_mfma_i32_16x16x64_i8) with the mins on fp16 MFMA (v_mfma_f32_16x16x16_f16).
 //
 // Per super-block b (256 values) and output (m, n), the arithmetic contract is
 // the exact integer pair of the reference's super-block kernel
@@ -10,32 +10,51 @@
 //   u = d * (float)S;  u = fma(-dmin, (float)Mn, u);  acc = fma(da, u, acc)
 // (the same order as the GEMV kernels and the CPU oracle).
 //
-// The effective integer weight sc*q (0..945) does not fit int8. With
+// S: the effective integer weight sc*q (0..945) does not fit int8. With
 // sc = 8*sh + sl (sh, sl in 0..7), sh*q and sl*q are at most 105, so each fits a
 // byte and a packed 16-bit multiply of four nibble bytes by sh (or sl) makes four
-// of them at once without carries. Three int8 MFMA accumulations per output give
-//   S = 8 * sum(sh*q*a) + sum(sl*q*a)   and   Mn = sum(m_j * a)
-// exactly in int32 (the third operand holds m_j at every position of sub-block j).
+// of them at once without carries. Two int8 MFMA chains per output give
+//   S = 8 * sum(sh*q*a) + sum(sl*q*a)
+// exactly in int32.
+// Mn: the Q8_K block carries the code sums of its 16-value groups (|bsum| <= 2048,
+// exact in fp16) and m_j <= 63, so one fp16 MFMA over the 16 bsums against m_j
+// sums 16 integer products of at most 2^17 each to at most 2^21: every partial sum
+// is an integer below 2^24, so the fp32 result is exactly (float)Mn.
 //
-// Tiling: a workgroup of 8 waves (two per SIMD, so one wave's MFMAs overlap the
-// other's dequantization and epilogue) computes 128 activation rows x 128 weight
-// rows; wave (wm, wn) owns 64 activation rows x 32 weight rows (4 x 2 MFMA tiles
-// of 16 x 16). Per super-block the activation codes (32 KB) and the weight
-// nibbles as clean bytes (32 KB) are staged in LDS, double-buffered: while the
-// waves multiply super-block b, the global loads of b + 2 are in flight and the
-// registers holding b + 1 are written to the other buffer, with one barrier per
-// super-block. 16-byte chunks are XOR-swizzled so that the MFMA operand reads hit
-// distinct LDS banks.
+// Two kernel families, both with 16 x 16 output tiles per MFMA and one wave owning
+// 64 activation rows x 16*NT weight rows:
+// - k_gemm_q4k<WM, NT> (up to 128 rows): 4 waves, one per SIMD. Per super-block a
+//   wave holds its 64 rows' activation operands (16 KB) in registers and walks its
+//   NT weight tiles; for each it unpacks the nibbles, scales and mins of 16 weight
+//   rows itself (three stages: LDS reads of tile nt + 2, unpacking of nt + 1, MFMAs
+//   of nt). Activation codes (swizzled), nibbles and headers reach LDS by
+//   direct-to-LDS buffer loads into two buffers (loads of b + 1 issued when b
+//   starts, one barrier per super-block).
+// - k_gemm_q4k_big<WM, WN, NT> (more rows): WM x WN waves, two per SIMD. Each
+//   16-row weight tile is unpacked once per workgroup into the sh*q / sl*q bytes of
+//   the MFMA operand layout in LDS (phase 1), then every wave runs its MFMAs and
+//   epilogues reading them (phase 2, software-pipelined: a tile's epilogue runs
+//   after the next tile's MFMAs are issued).
+// On gfx950 the matrix core hides about two VALU operations per MFMA and little
+// more (measured with microbenchmarks on MI355X), so the kernels are arranged to
+// keep the VALU work per MFMA low rather than to overlap large VALU phases.
 //
-// MFMA operand layout (16x16x64 i8): lane l supplies row (A) / column (B) l%16
-// and 16 K-values of lane group l/16; the result lane l holds column l%16, rows
-// 4*(l/16) .. 4*(l/16)+3. K-step s of a super-block covers values 64s .. 64s+63,
-// lane group g the 16 values 64s + 16g .., which are values 16(g&1) .. of
-// sub-block 2s + g/2 (dynacore/src/quantization/quant_formats.cpp:150-167).
+// MFMA operand layout (16x16x64 i8): lane l supplies row (A) / column (B) l%16 and
+// 16 K-values of lane group g = l/16; the result lane l holds column l%16, rows
+// 4g .. 4g+3. The 256 values of a super-block are dealt to (K-step s, lane group
+// g) so that each lane's 16 values are one half of one 16-byte nibble chunk of the
+// weight row: chunk c = g + 4*(s>>1), low nibbles for even s, high for odd s. Chunk
+// c holds values 64(c>>1) + 16(c&1) + i (low) and the same + 32 (high)
+// (dynacore/src/quantization/quant_formats.cpp:150-167), so lane group g at step
+// s covers values 16*q .. 16*q + 15 with q = 4(g>>1) + (g&1) + 8(s>>1) + 2(s&1),
+// all of sub-block j = 2(g>>1) + 4(s>>1) + (s&1). The activation operand takes the
+// same 16 values, so the product is the plain dot product in a permuted K order.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include <type_traits>
+#include <algorithm>
+#include <array>
+#include <cstdlib>
 
 #include "dq_device.h"
 #include "dq_internal.h"
@@ -45,226 +64,310 @@ namespace dq {
 
 namespace {
 
-constexpr int kBM = 128;       // activation rows per workgroup
-constexpr int kBN = 128;       // weight rows per workgroup (two 64-row groups)
-constexpr int kThreads = 512;  // 8 waves: 2 along M (64 rows each) x 4 along N (32 rows each)
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
 
-// LDS layout (bytes). Operands of one super-block, two buffers:
-constexpr int kLdsA = 0;                       // [4 K-steps][128 rows][4 chunks of 16 B] activation codes
-constexpr int kLdsQ = kLdsA + 4 * kBM * 64;    // [128 rows][16 chunks of 16 B] nibbles as bytes, value order
-constexpr int kBuf = kLdsQ + kBN * 256;        // 65536
-// Scales of one super-block, a ring of three (the delayed epilogue reads b - 1
-// while b + 1 is being written):
-constexpr int kLdsH = 0;                       // [128 rows] Q4_K header {d, dmin, scales[12]}
-constexpr int kLdsDA = kLdsH + kBN * 16;       // [128 rows] activation scale d (float)
-constexpr int kRing = kLdsDA + kBM * 4;        // 2560
-constexpr int kLdsBytes = 2 * kBuf + 3 * kRing;  // 138752
+constexpr int kThreads = 256;  // 4 waves, one per SIMD
 
-DQ_DEV void lds_st16(uint8_t* lds, int off, v4u v) { *reinterpret_cast<v4u*>(lds + off) = v; }
-DQ_DEV v4u lds_ld16(const uint8_t* lds, int off) { return *reinterpret_cast<const v4u*>(lds + off); }
-
-// Swizzled byte offsets of the 16-byte chunks.
-DQ_DEV int a_off(int s, int row, int g) { return ((s * kBM + row) * 4 + (g ^ ((row >> 2) & 3))) * 16; }
-DQ_DEV int q_off(int row, int k) { return (row * 16 + (k ^ (row & 15))) * 16; }
-
-// Global loads of one super-block held in registers until they are written to LDS
-// (the activation codes go to LDS directly).
-struct Stage {
-  v4u q[2];  // qs chunk (t >> 6) & 7 of row t & 63 of the tile's row group i
+// LDS layout of one super-block's operands (bytes); two such buffers.
+template <int WM, int NT>
+struct Cfg {
+  static constexpr int kWN = 4 / WM;               // waves along the weight rows
+  static constexpr int kBM = 64 * WM;              // activation rows per workgroup
+  static constexpr int kBN = kWN * 16 * NT;        // weight rows per workgroup
+  static constexpr int kWB = (kBN + 63) / 64;      // 64-row load blocks of weight rows
+  static constexpr int kWRows = 64 * kWB;
+  static constexpr int kA = 0;                     // [kBM][16 chunks][16 B] codes, chunk q at slot q ^ (row & 15)
+  static constexpr int kW = kA + kBM * 256;        // [8 chunks][kWRows][16 B] nibbles as in the weight plane
+  static constexpr int kH = kW + 8 * kWRows * 16;  // [kWRows][16 B] Q4_K headers {d, dmin, scales[12]}
+  static constexpr int kBS = kH + kWRows * 16;     // [kBM][16] bsums as fp16
+  static constexpr int kDA = kBS + kBM * 32;       // [kBM] activation scale d (float)
+  static constexpr int kBuf = kDA + kBM * 4;
+  static constexpr int kLds = 2 * kBuf;
 };
+
+DQ_DEV v4u lds_ld16(const uint8_t* lds, int off) { return *reinterpret_cast<const v4u*>(lds + off); }
+DQ_DEV v2u lds_ld8(const uint8_t* lds, int off) { return *reinterpret_cast<const v2u*>(lds + off); }
+
+DQ_DEV f4_t mfma_h(h4_t a, h4_t b, f4_t c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
+
+// Direct-to-LDS buffer load: lane l's `bytes` land at lds_dst + l * bytes.
+DQ_DEV void ld_lds16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_dst, u32 voff, u32 soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_dst, 16, voff, soff, 0, 0);
+}
+DQ_DEV void ld_lds4(__amdgpu_buffer_rsrc_t r, uint8_t* lds_dst, u32 voff, u32 soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_dst, 4, voff, soff, 0, 0);
+}
+
+// Eight int16 bsums -> eight fp16 (exact: |bsum| <= 2048).
+DQ_DEV v4u bsums_f16(v4u v) {
+  v4u o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const _Float16 lo = (_Float16)(short)(v[i] & 0xFFFFu), hi = (_Float16)(short)(v[i] >> 16);
+    o[i] = (u32)__builtin_bit_cast(uint16_t, lo) | ((u32)__builtin_bit_cast(uint16_t, hi) << 16);
+  }
+  return o;
+}
+
+// The B side of one 16-row weight tile: raw LDS words, then the MFMA operands.
+struct RawB {
+  v4u hd, w0, w1;  // header; nibble chunks lg and lg + 4 of the lane's row
+};
+struct PrepB {
+  v4u H[4], L[4];  // sh*q and sl*q bytes of the 4 K-steps
+  h4_t mb;         // m_{2lg}, m_{2lg}, m_{2lg+1}, m_{2lg+1} (fp16)
+  float d, dmin;
+};
+
+// m_{2lg}, m_{2lg}, m_{2lg+1}, m_{2lg+1} of a Q4_K header as fp16 ((1024 + m) - 1024,
+// exact), the B operand of the mins MFMA for lane group lg (selector sel_mn).
+DQ_DEV h4_t mins_f16(v4u hd, u32 sel_mn) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  const u32 mn_lo = hd.z & 0x3F3F3F3Fu;
+  const u32 mn_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+  const u32 mm = __builtin_amdgcn_perm(0u, __builtin_amdgcn_perm(mn_hi, mn_lo, sel_mn), 0x0C010C00u) | 0x64006400u;
+  const h2_t mf = __builtin_bit_cast(h2_t, mm) - h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
+  const u32 mfu = __builtin_bit_cast(u32, mf);
+  return __builtin_bit_cast(h4_t, v2u{__builtin_amdgcn_perm(mfu, mfu, 0x01000100u),
+                                      __builtin_amdgcn_perm(mfu, mfu, 0x03020302u)});
+}
+
+// Unpacks one tile's header and nibbles for this lane (lane group lg: sub-block
+// scale bytes selected by sel_sc, mins by sel_mn).
+DQ_DEV PrepB prep_tile(const RawB& r, u32 sel_sc, u32 sel_mn) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  PrepB p;
+  p.d = h2f(r.hd.x);
+  p.dmin = h2f(r.hd.x >> 16);
+  // get_scale_min_k4 (dynacore/include/dynacore/quantization/quant_formats.h:62-70)
+  // for all eight sub-blocks as bytes: sc_lo / mn_lo j = 0..3, sc_hi / mn_hi j = 4..7
+  const u32 sc_lo = r.hd.y & 0x3F3F3F3Fu, mn_lo = r.hd.z & 0x3F3F3F3Fu;
+  const u32 sc_hi = (r.hd.w & 0x0F0F0F0Fu) | ((r.hd.y >> 2) & 0x30303030u);
+  const u32 mn_hi = ((r.hd.w >> 4) & 0x0F0F0F0Fu) | ((r.hd.z >> 2) & 0x30303030u);
+  const u32 sc = __builtin_amdgcn_perm(sc_hi, sc_lo, sel_sc);  // byte s: scale of step s
+  const u32 SH = (sc >> 3) & 0x07070707u, SL = sc & 0x07070707u;
+  // m_{2lg}, m_{2lg+1} as fp16: (1024 + m) - 1024, exact
+  const u32 mm = __builtin_amdgcn_perm(0u, __builtin_amdgcn_perm(mn_hi, mn_lo, sel_mn), 0x0C010C00u) | 0x64006400u;
+  const h2_t mf = __builtin_bit_cast(h2_t, mm) - h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
+  const u32 mfu = __builtin_bit_cast(u32, mf);
+  p.mb = __builtin_bit_cast(h4_t, v2u{__builtin_amdgcn_perm(mfu, mfu, 0x01000100u),
+                                      __builtin_amdgcn_perm(mfu, mfu, 0x03020302u)});
+  // the 4 steps' nibbles as bytes (high nibbles are stored XOR 8, dq_layout.h)
+  v4u qb[4];
+  qb[0] = r.w0 & 0x0F0F0F0Fu;
+  qb[1] = ((r.w0 >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+  qb[2] = r.w1 & 0x0F0F0F0Fu;
+  qb[3] = ((r.w1 >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const u32 kh = __builtin_amdgcn_perm(0u, SH, sel_u16x2(s));
+    const u32 kl = __builtin_amdgcn_perm(0u, SL, sel_u16x2(s));
+    p.H[s] = v4u{mul_bytes(qb[s].x, kh), mul_bytes(qb[s].y, kh), mul_bytes(qb[s].z, kh), mul_bytes(qb[s].w, kh)};
+    p.L[s] = v4u{mul_bytes(qb[s].x, kl), mul_bytes(qb[s].y, kl), mul_bytes(qb[s].z, kl), mul_bytes(qb[s].w, kl)};
+  }
+  return p;
+}
 
 }  // namespace
 
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_q4k(
+template <int WM, int NT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_q4k(
     const uint8_t* __restrict__ qs_plane, const uint8_t* __restrict__ hdr_plane, int nb, int64_t n_pad, int64_t nt0,
     int64_t n0, int64_t n1, const uint8_t* __restrict__ acts, int64_t arb, int64_t m, float* __restrict__ y, int64_t ys,
-    const float* __restrict__ bias) {
+    const float* __restrict__ bias, int tiles_n, int tiles_m) {
+  using C = Cfg<WM, NT>;
   extern __shared__ __align__(16) uint8_t lds[];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave & 1, wn = wave >> 1;  // this wave's 64 activation rows and 32 weight rows
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave % WM, wn = wave / WM;
   const int li = lane & 15, lg = lane >> 4;
-  const int64_t nbase = nt0 + (int64_t)blockIdx.x * kBN;  // first weight row of the tile (multiple of 64)
-  const int64_t mbase = (int64_t)blockIdx.y * kBM;
-  const int64_t mrows = m - mbase < kBM ? m - mbase : kBM;
+
+  // Tile order: workgroup i runs on XCD i % 8; consecutive logical tiles (the
+  // activation tiles of one weight tile) go to one XCD so that its L2 serves the
+  // weight tile to all of them.
+  int L = blockIdx.x;
+  const int per = (tiles_n * tiles_m) / 8;
+  if (L < 8 * per) L = (L % 8) * per + L / 8;
+  const int tn = __builtin_amdgcn_readfirstlane(L / tiles_m);
+  const int tm = __builtin_amdgcn_readfirstlane(L - tn * tiles_m);
+  const int64_t nbase = nt0 + (int64_t)tn * C::kBN;  // first weight row of the tile
+  const int64_t mbase = (int64_t)tm * C::kBM;
+  const int64_t mrows = m - mbase < C::kBM ? m - mbase : C::kBM;
 
   // ---- global sources (buffer resources: reads past the end return zeros)
   const auto ra = rsrc(acts + mbase * arb, (u32)(mrows * arb));
-  // the tile's two 64-row groups of the weight layout (dq_layout.h)
-  const int64_t G0 = nbase / kRowGroup;
-  const bool g0ok = nbase < n_pad, g1ok = nbase + kRowGroup < n_pad;
-  const auto rq0 = rsrc(qs_plane + G0 * nb * 8192, g0ok ? (u32)(nb * 8192) : 0u);
-  const auto rq1 = rsrc(qs_plane + (G0 + 1) * nb * 8192, g1ok ? (u32)(nb * 8192) : 0u);
-  const auto rh0 = rsrc(hdr_plane + G0 * nb * 1024, g0ok ? (u32)(nb * 1024) : 0u);
-  const auto rh1 = rsrc(hdr_plane + (G0 + 1) * nb * 1024, g1ok ? (u32)(nb * 1024) : 0u);
+  const int64_t G0 = nbase >> 6;
+  const int goff = (int)(nbase & 63);
+  const int64_t gl = n_pad / kRowGroup - G0;
+  const int64_t gspan = gl < C::kWB + 1 ? gl : C::kWB + 1;
+  const auto rq = rsrc(qs_plane + G0 * nb * 8192, (u32)(gspan * nb * 8192));
+  const auto rh = rsrc(hdr_plane + G0 * nb * 1024, (u32)(gspan * nb * 1024));
 
-  // Activation codes straight to LDS: instruction i of wave w fills the 1 KB
-  // [K-step s = i][rows 16 w .. 16 w + 15] of the buffer, lane l the 16-byte slot
-  // l, which holds row 16 w + l / 4, chunk (l & 3) ^ ((row >> 2) & 3) (a_off).
-  const int arow = 16 * wave + (lane >> 2);
-  const int achunk = (lane & 3) ^ ((arow >> 2) & 3);
-  auto load_a = [&](int b, auto par) {
-    uint8_t* L = lds + decltype(par)::value * kBuf;
+  // Per-lane source offsets (super-block 0).
+  u32 woff[C::kWB], hoff[C::kWB];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          ra, (__attribute__((address_space(3))) void*)(L + kLdsA + (s * kBM + 16 * wave) * 64), 16,
-          (u32)(arow * arb + (int64_t)b * 292 + 4 + 64 * s + 16 * achunk), 0, 0, 0);
-    }
-    // headers (waves 0, 1: one 64-row group each, 1 KB contiguous in the weight
-    // layout) and activation scales (waves 2, 3: 64 rows each) into ring slot b % 3
-    uint8_t* R = lds + 2 * kBuf + (b % 3) * kRing;
-    if (wave < 2) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wave == 0 ? rh0 : rh1,
-                                               (__attribute__((address_space(3))) void*)(R + kLdsH + 1024 * wave),
-                                               16, (u32)((b * 64 + lane) * 16), 0, 0, 0);
-    } else if (wave < 4) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          ra, (__attribute__((address_space(3))) void*)(R + kLdsDA + 256 * (wave - 2)), 4,
-          (u32)((64 * (wave - 2) + lane) * arb + (int64_t)b * 292), 0, 0, 0);
-    }
-  };
-  // staging roles of thread t for the weight bytes
-  const int qc = (t >> 6) & 7, qr = t & 63;  // qs chunk qc of row qr of row group i (i = 0, 1)
-  Stage st;
-  auto load = [&](int b) {
-    st.q[0] = ld16(rq0, (u32)(((b * 8 + qc) * 64 + qr) * 16));
-    st.q[1] = ld16(rq1, (u32)(((b * 8 + qc) * 64 + qr) * 16));
-  };
-  auto store = [&](int b, auto par) {
-    uint8_t* L = lds + decltype(par)::value * kBuf;
-    // qs chunk qc holds values 64(qc/2) + 16(qc&1) + i (low nibbles, sub-block qc & ~1)
-    // and the same + 32 (high nibbles, stored XOR 8, dq_layout.h)
-    const int klo = 4 * (qc >> 1) + (qc & 1);
+  for (int k = 0; k < C::kWB; ++k) {
+    const int rr = goff + 64 * k + lane;
+    woff[k] = (u32)((rr >> 6) * nb * 8192 + (rr & 63) * 16);
+    hoff[k] = (u32)((rr >> 6) * nb * 1024 + (rr & 63) * 16);
+  }
+  constexpr int kAI = C::kBM / 16;  // activation-code load instructions per wave (4 rows each)
+  u32 aoff[kAI];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int row = 64 * i + qr;
-      lds_st16(L, kLdsQ + q_off(row, klo), st.q[i] & 0x0F0F0F0Fu);
-      lds_st16(L, kLdsQ + q_off(row, klo + 2), ((st.q[i] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u);
-    }
-  };
+  for (int j = 0; j < kAI; ++j) {
+    const int row = 4 * (wave * kAI + j) + (lane >> 4);
+    const int q = (lane & 15) ^ (row & 15);
+    aoff[j] = (u32)(row * arb + 4 + 16 * q);
+  }
+  const bool bs_role = t < 2 * C::kBM;
+  const int bs_row = t >> 1, bs_half = t & 1;
+  const u32 bs_off = (u32)(bs_row * arb + 260 + 16 * bs_half);
 
-  v4i_t acc[3][4][2];  // [sh plane, sl plane, m plane][m tile][n tile]
-  float accf[4][2][4];
+  auto issue = [&](int b, uint8_t* Lb) {
+    // activation codes
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+    for (int j = 0; j < kAI; ++j) ld_lds16(ra, Lb + C::kA + 4 * (wave * kAI + j) * 256, aoff[j], (u32)(b * 292));
+    // weight nibbles: wave w stages chunks 2w and 2w + 1 of every 64-row block
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int cc = 0; cc < 2; ++cc) {
+      const int c = 2 * wave + cc;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) accf[mt][nt][e] = 0.0f;
-    }
-
-  // Epilogue of super-block b: exact S, Mn -> fp32 (canonical order).
-  auto epilogue = [&](int b) {
-    const uint8_t* R = lds + 2 * kBuf + (b % 3) * kRing;
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const u32 h = *reinterpret_cast<const u32*>(R + kLdsH + 16 * (32 * wn + 16 * nt + li));
-      const float d = h2f(h), dmin = h2f(h >> 16);
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const v4u dav = lds_ld16(R, kLdsDA + 4 * (64 * wm + 16 * mt + 4 * lg));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int S = acc[1][mt][nt][e] + (acc[0][mt][nt][e] << 3);
-          const int Mn = acc[2][mt][nt][e];
-          float u = d * (float)S;
-          u = fmaf(-dmin, (float)Mn, u);
-          accf[mt][nt][e] = fmaf(as_f(dav[e]), u, accf[mt][nt][e]);
+      for (int k = 0; k < C::kWB; ++k) {
+        if (k + 1 < C::kWB || 64 * k + lane < C::kBN) {
+          ld_lds16(rq, Lb + C::kW + (c * C::kWRows + 64 * k) * 16, woff[k], (u32)(b * 8192 + c * 1024));
         }
       }
     }
+    // headers
+#pragma unroll
+    for (int k = 0; k < C::kWB; ++k) {
+      if (k % 4 == wave && (k + 1 < C::kWB || 64 * k + lane < C::kBN)) {
+        ld_lds16(rh, Lb + C::kH + 64 * k * 16, hoff[k], (u32)(b * 1024));
+      }
+    }
+    // activation scales
+#pragma unroll
+    for (int k = 0; k < C::kBM / 64; ++k) {
+      if (wave == 3 - k) ld_lds4(ra, Lb + C::kDA + 256 * k, (u32)((64 * k + lane) * arb), (u32)(b * 292));
+    }
+  };
+  auto bs_load = [&](int b) -> v4u { return bs_role ? ld16(ra, bs_off + (u32)(b * 292)) : v4u{0, 0, 0, 0}; };
+  auto bs_store = [&](v4u v, uint8_t* Lb) {
+    if (bs_role) *reinterpret_cast<v4u*>(Lb + C::kBS + bs_row * 32 + 16 * bs_half) = bsums_f16(v);
   };
 
-  // K-step s of the super-block in buffer L: 24 MFMAs; the first step starts the
-  // accumulators from zero.
-  const int hi = lg >> 1;  // this lane group's sub-blocks are 2s + hi
-  u32 KH[2], KL[2], MN[2];  // per weight row: bytes s = sh, sl, m of sub-block 2s + hi
-  auto kstep = [&](const uint8_t* L, int s, bool first) {
-    v4u a[4];
+  // ---- per-lane LDS read offsets
+  const int qlg = 4 * (lg >> 1) + (lg & 1);
+  const int arow = 64 * wm + li;
+  int a_rd[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) a[mt] = lds_ld16(L, kLdsA + a_off(s, 64 * wm + 16 * mt + li, lg));
+  for (int s = 0; s < 4; ++s) a_rd[s] = C::kA + arow * 256 + 16 * ((qlg ^ li) ^ (8 * (s >> 1) + 2 * (s & 1)));
+  const int bs_rd = C::kBS + arow * 32 + 8 * lg;
+  const int da_rd = C::kDA + (64 * wm + 4 * lg) * 4;
+  const int wrow = 16 * NT * wn + li;
+  const int w_rd = C::kW + (lg * C::kWRows + wrow) * 16;
+  const int h_rd = C::kH + wrow * 16;
+  // v_perm selectors: this lane's sub-block scales (j = 2h, 2h+1, 4+2h, 5+2h with
+  // h = lg >> 1) and mins (j = 2lg, 2lg + 1)
+  const u32 sel_sc = (lg >> 1) ? 0x07060302u : 0x05040100u;
+  const u32 sel_mn = 0x0C0C0000u | ((u32)(2 * lg + 1) << 8) | (u32)(2 * lg);
+  auto load_b = [&](const uint8_t* Lc, int nt) -> RawB {
+    return RawB{lds_ld16(Lc, h_rd + nt * 256), lds_ld16(Lc, w_rd + nt * 256),
+                lds_ld16(Lc, w_rd + nt * 256 + 4 * C::kWRows * 16)};
+  };
+  auto prep_b = [&](const RawB& r) -> PrepB { return prep_tile(r, sel_sc, sel_mn); };
+
+  f4_t acc[NT][4];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const v4u q = lds_ld16(L, kLdsQ + q_off(32 * wn + 16 * nt + li, 4 * s + lg));
-      const u32 kh = __builtin_amdgcn_perm(0u, KH[nt], sel_u16x2(s));
-      const u32 kl = __builtin_amdgcn_perm(0u, KL[nt], sel_u16x2(s));
-      const u32 mm4 = __builtin_amdgcn_perm(0u, MN[nt], sel_x4(s));
-      const v4u H = {mul_bytes(q.x, kh), mul_bytes(q.y, kh), mul_bytes(q.z, kh), mul_bytes(q.w, kh)};
-      const v4u Lo = {mul_bytes(q.x, kl), mul_bytes(q.y, kl), mul_bytes(q.z, kl), mul_bytes(q.w, kl)};
-      const v4u Mp = {mm4, mm4, mm4, mm4};
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[nt][mt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // ---- prologue: super-block 0 into buffer 0
+  {
+    issue(0, lds);
+    const v4u v = bs_load(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    bs_store(v, lds);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+#pragma unroll 1
+  for (int b = 0; b < nb; ++b) {
+    const uint8_t* Lc = lds + (b & 1) * C::kBuf;
+    uint8_t* Ln = lds + ((b & 1) ^ 1) * C::kBuf;
+    v4u bsn = {0, 0, 0, 0};
+    if (b + 1 < nb) {
+      issue(b + 1, Ln);
+      bsn = bs_load(b + 1);
+    }
+
+    // this super-block's activation operands
+    v4u a[4][4];
+    h4_t am[4];
+    f4_t da[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) a[mt][s] = lds_ld16(Lc, a_rd[s] + mt * 16 * 256);
+      am[mt] = __builtin_bit_cast(h4_t, lds_ld8(Lc, bs_rd + mt * 16 * 32));
+      da[mt] = __builtin_bit_cast(f4_t, lds_ld16(Lc, da_rd + mt * 16 * 4));
+    }
+
+    // Three stages over the weight tiles, one region per tile: the LDS reads of
+    // tile nt + 2, the unpacking of tile nt + 1 and the MFMAs and epilogues of tile
+    // nt. The scheduling barrier between regions keeps the compiler from hoisting
+    // every tile's operands at once (which would exceed the register file).
+    RawB raw[NT];
+    PrepB pb[NT];
+    raw[0] = load_b(Lc, 0);
+    if (NT > 1) raw[1] = load_b(Lc, 1);
+    pb[0] = prep_b(raw[0]);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (nt + 2 < NT) raw[nt + 2] = load_b(Lc, nt + 2);
+      if (nt + 1 < NT) pb[nt + 1] = prep_b(raw[nt + 1]);
+      v4i_t tH[4], tL[4];
+      f4_t tM[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         const v4i_t z = {0, 0, 0, 0};
-        acc[0][mt][nt] = mfma(a[mt], H, first ? z : acc[0][mt][nt]);
-        acc[1][mt][nt] = mfma(a[mt], Lo, first ? z : acc[1][mt][nt]);
-        acc[2][mt][nt] = mfma(a[mt], Mp, first ? z : acc[2][mt][nt]);
-      }
-    }
-  };
-
-  load_a(0, std::integral_constant<int, 0>{});
-  load(0);
-  store(0, std::integral_constant<int, 0>{});
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  // Waves 4..7 (one per SIMD, beside one of waves 0..3) run each super-block's
-  // epilogue at the start of the next one, so that on every SIMD one wave's
-  // epilogue overlaps the other wave's MFMAs.
-  // Waves 4..7 (one per SIMD, beside one of waves 0..3) run each super-block's
-  // epilogue at the start of the next one, so that on every SIMD one wave's
-  // epilogue overlaps the other wave's MFMAs.
-  const bool late = wave >= 4;
-  // One super-block; P = b & 1 is a compile-time constant so that every LDS
-  // address is a per-lane base plus an immediate offset.
-  auto iter = [&](int b, auto par) {
-    constexpr int P = decltype(par)::value;
-    const uint8_t* L = lds + P * kBuf;
-    const uint8_t* R = lds + 2 * kBuf + (b % 3) * kRing;
-    if (late && b > 0) epilogue(b - 1);
-    // next super-block's loads: activation codes into the other LDS buffer, the
-    // rest into registers (written at the end of this iteration)
-    if (b + 1 < nb) {
-      load_a(b + 1, std::integral_constant<int, 1 - P>{});
-      load(b + 1);
-    }
-
-    // the scales and mins of this lane's two weight rows (get_scale_min_k4,
-    // quant_formats.h:62-70) for its sub-blocks 2s + hi, as bytes s
+        tH[mt] = mfma(a[mt][0], pb[nt].H[0], z);
+        tL[mt] = mfma(a[mt][0], pb[nt].L[0], z);
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const v4u hd = lds_ld16(R, kLdsH + 16 * (32 * wn + 16 * nt + li));
-      const u32 sc_lo = hd.y & 0x3F3F3F3Fu, mn_lo = hd.z & 0x3F3F3F3Fu;
-      const u32 sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
-      const u32 mn_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
-      const u32 sc = __builtin_amdgcn_perm(sc_hi, sc_lo, sel_subblocks(hi));
-      KH[nt] = (sc >> 3) & 0x07070707u;
-      KL[nt] = sc & 0x07070707u;
-      MN[nt] = __builtin_amdgcn_perm(mn_hi, mn_lo, sel_subblocks(hi));
+        for (int s = 1; s < 4; ++s) {
+          tH[mt] = mfma(a[mt][s], pb[nt].H[s], tH[mt]);
+          tL[mt] = mfma(a[mt][s], pb[nt].L[s], tL[mt]);
+        }
+        tM[mt] = mfma_h(am[mt], pb[nt].mb, f4_t{0.0f, 0.0f, 0.0f, 0.0f});
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int S = tL[mt][e] + (tH[mt][e] << 3);
+          float u = pb[nt].d * (float)S;
+          u = fmaf(-pb[nt].dmin, tM[mt][e], u);
+          acc[nt][mt][e] = fmaf(da[mt][e], u, acc[nt][mt][e]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
 
-    kstep(L, 0, true);
-#pragma unroll 1
-    for (int s = 1; s < 4; ++s) kstep(L, s, false);
-    if (!late) epilogue(b);
-
-    // ---- stage super-block b + 1 (its activation codes are already on their way)
-    if (b + 1 < nb) store(b + 1, std::integral_constant<int, 1 - P>{});
+    if (b + 1 < nb) {
+      __builtin_amdgcn_s_waitcnt(0);
+      bs_store(bsn, Ln);
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-  };
-  int b = 0;
-  for (; b + 1 < nb; b += 2) {
-    iter(b, std::integral_constant<int, 0>{});
-    iter(b + 1, std::integral_constant<int, 1>{});
   }
-  if (b < nb) iter(b, std::integral_constant<int, 0>{});
-  if (late) epilogue(nb - 1);
 
   // ---- store
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int64_t n = nbase + 32 * wn + 16 * nt + li;
+  for (int nt = 0; nt < NT; ++nt) {
+    const int64_t n = nbase + 16 * NT * wn + 16 * nt + li;
     if (n < n0 || n >= n1) continue;
     const float bn_ = bias ? bias[n] : 0.0f;
 #pragma unroll
@@ -272,7 +375,236 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int64_t mm = mbase + 64 * wm + 16 * mt + 4 * lg + e;
-        if (mm < m) y[mm * ys + n] = bias ? accf[mt][nt][e] + bn_ : accf[mt][nt][e];
+        if (mm < m) y[mm * ys + n] = bias ? acc[nt][mt][e] + bn_ : acc[nt][mt][e];
+      }
+    }
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// Large-M kernel: WM x WN waves (two per SIMD), each owning 64 activation rows x
+// 16 NT weight rows. Per super-block the B operands are built once per workgroup:
+// each wave unpacks 16-row weight tiles into the sh*q / sl*q bytes of the MFMA
+// operand layout and stores them in LDS, so the VALU work per MFMA left in the
+// compute phase is the fp32 epilogue, about two operations per MFMA.
+template <int WM, int WN, int NT>
+struct Big {
+  static constexpr int kWaves = WM * WN, kThreads = 64 * kWaves;
+  static constexpr int kBM = 64 * WM, kBN = 16 * NT * WN;  // activation rows x weight rows
+  static constexpr int kTiles = NT * WN;                    // 16-row weight tiles
+  static constexpr int kPrep = kTiles / kWaves;             // tiles unpacked per wave
+  static constexpr int kGroups = kBN / 64;                  // 64-row groups of the weight layout
+  static constexpr int kA = 0;                        // [kBM rows][16 slots][16 B] codes, chunk q at slot q ^ (row & 15)
+  static constexpr int kHL = kA + kBM * 256;          // [tiles][4 steps][H, L][64 lanes][16 B] B operands
+  static constexpr int kW = kHL + kTiles * 8192;      // [8 chunks][kBN rows][16 B] nibbles as in the weight plane
+  static constexpr int kH = kW + 8 * kBN * 16;        // [kBN rows][16 B] headers
+  static constexpr int kBS = kH + kBN * 16;           // [kBM rows][16] bsums (int16)
+  static constexpr int kDA = kBS + kBM * 32;          // [2][kBM rows] activation scale d (two buffers)
+  static constexpr int kLds = kDA + 2 * kBM * 4;
+  static_assert(kPrep >= 1 && kTiles % kWaves == 0, "each wave unpacks whole tiles");
+  static_assert(kBN % 64 == 0 && kBM / 32 == kWaves && (8 * kGroups) % kWaves == 0, "staging roles");
+  static_assert(kLds <= 160 * 1024, "LDS");
+};
+
+template <int WM, int WN, int NT>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_q4k_big(
+    const uint8_t* __restrict__ qs_plane, const uint8_t* __restrict__ hdr_plane, int nb, int64_t n_pad, int64_t nt0,
+    int64_t n0, int64_t n1, const uint8_t* __restrict__ acts, int64_t arb, int64_t m, float* __restrict__ y, int64_t ys,
+    const float* __restrict__ bias, int tiles_n, int tiles_m) {
+  using C = Big<WM, WN, NT>;
+  constexpr int kBM = C::kBM, kBN = C::kBN, kA = C::kA, kHL = C::kHL, kW = C::kW, kH = C::kH, kBS = C::kBS,
+                kDA = C::kDA;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave % WM, wn = wave / WM;  // 64 activation rows x 16 NT weight rows per wave
+  const int li = lane & 15, lg = lane >> 4;
+
+  int L = blockIdx.x;
+  const int per = (tiles_n * tiles_m) / 8;
+  if (L < 8 * per) L = (L % 8) * per + L / 8;
+  const int tn = __builtin_amdgcn_readfirstlane(L / tiles_m);
+  const int tm = __builtin_amdgcn_readfirstlane(L - tn * tiles_m);
+  const int64_t nbase = nt0 + (int64_t)tn * kBN;  // multiple of 64
+  const int64_t mbase = (int64_t)tm * kBM;
+  const int64_t mrows = m - mbase < kBM ? m - mbase : kBM;
+
+  const auto ra = rsrc(acts + mbase * arb, (u32)(mrows * arb));
+  const int64_t G0 = nbase >> 6;
+  const int64_t gl = n_pad / kRowGroup - G0;
+  const int64_t gspan = gl < C::kGroups ? gl : C::kGroups;
+  const auto rq = rsrc(qs_plane + G0 * nb * 8192, (u32)(gspan * nb * 8192));
+  const auto rh = rsrc(hdr_plane + G0 * nb * 1024, (u32)(gspan * nb * 1024));
+
+  // ---- staging roles (direct-to-LDS, per super-block)
+  // activation codes: wave w, instruction j fills rows 4 (8w + j) .. + 3; the
+  // per-lane part of the source offset repeats with period 4 in j
+  u32 aoff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 4 * (8 * wave + j) + (lane >> 4);
+    aoff[j] = (u32)(row * arb + 4 + 16 * ((lane & 15) ^ (row & 15)));
+  }
+  // bsums: wave w fills rows 32 w .. 32 w + 31
+  const u32 bsoff = (u32)((32 * wave + (lane >> 1)) * arb + 260 + 16 * (lane & 1));
+  constexpr int kWI = 8 * C::kGroups / C::kWaves;  // nibble instructions per wave
+  auto issue = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ld_lds16(ra, lds + kA + 4 * (8 * wave + j) * 256, aoff[j & 3], (u32)(b * 292 + (j >> 2) * 16 * arb));
+    }
+    // nibbles: instruction i = kWI w + j stages chunk i / kGroups of 64-row group i % kGroups
+#pragma unroll
+    for (int j = 0; j < kWI; ++j) {
+      const int i = kWI * wave + j, c = i / C::kGroups, k = i % C::kGroups;
+      ld_lds16(rq, lds + kW + (c * kBN + 64 * k) * 16, (u32)(k * nb * 8192 + lane * 16), (u32)(b * 8192 + c * 1024));
+    }
+    if (wave < C::kGroups) {
+      ld_lds16(rh, lds + kH + 64 * wave * 16, (u32)(wave * nb * 1024 + lane * 16), (u32)(b * 1024));
+    }
+    ld_lds16(ra, lds + kBS + 32 * wave * 32, bsoff, (u32)(b * 292));
+    constexpr int kDI = kBM / 64;  // activation-scale instructions, on the last waves
+    if (wave >= C::kWaves - kDI) {
+      const int k = wave - (C::kWaves - kDI);
+      ld_lds4(ra, lds + kDA + (b & 1) * kBM * 4 + 256 * k, (u32)((64 * k + lane) * arb), (u32)(b * 292));
+    }
+  };
+
+  // ---- per-lane LDS read offsets
+  const int qlg = 4 * (lg >> 1) + (lg & 1);
+  const int arow = 64 * wm + li;
+  int a_rd[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) a_rd[s] = kA + arow * 256 + 16 * ((qlg ^ li) ^ (8 * (s >> 1) + 2 * (s & 1)));
+  const int bs_rd = kBS + arow * 32 + 8 * lg;
+  const int da_rd = kDA + (64 * wm + 4 * lg) * 4;
+  const u32 sel_sc = (lg >> 1) ? 0x07060302u : 0x05040100u;
+  const u32 sel_mn = 0x0C0C0000u | ((u32)(2 * lg + 1) << 8) | (u32)(2 * lg);
+
+  f4_t acc[NT][4];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[nt][mt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  issue(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  struct Sc {
+    float d, dmin;
+    h4_t mb;
+  };
+  struct Tacc {
+    v4i_t H, L;
+    f4_t M;
+  };
+
+#pragma unroll 1
+  for (int b = 0; b < nb; ++b) {
+    // ---- phase 1: B operands of this wave's weight tiles into LDS; this wave's
+    // activation operands and the scales of its NT weight tiles into registers
+#pragma unroll
+    for (int i = 0; i < C::kPrep; ++i) {
+      const int p = C::kPrep * wave + i;
+      const int row = 16 * p + li;
+      const RawB r{lds_ld16(lds, kH + row * 16), lds_ld16(lds, kW + (lg * kBN + row) * 16),
+                   lds_ld16(lds, kW + ((lg + 4) * kBN + row) * 16)};
+      const PrepB q = prep_tile(r, sel_sc, sel_mn);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        *reinterpret_cast<v4u*>(lds + kHL + ((p * 4 + s) * 2 + 0) * 1024 + lane * 16) = q.H[s];
+        *reinterpret_cast<v4u*>(lds + kHL + ((p * 4 + s) * 2 + 1) * 1024 + lane * 16) = q.L[s];
+      }
+    }
+    v4u a[4][4];
+    h4_t am[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) a[mt][s] = lds_ld16(lds, a_rd[s] + mt * 16 * 256);
+      const v2u bs = lds_ld8(lds, bs_rd + mt * 16 * 32);
+      const v4u bsf = bsums_f16(v4u{bs.x, bs.y, 0, 0});
+      am[mt] = __builtin_bit_cast(h4_t, v2u{bsf.x, bsf.y});
+    }
+    Sc sc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const v4u hd = lds_ld16(lds, kH + (16 * NT * wn + 16 * nt + li) * 16);
+      sc[nt] = Sc{h2f(hd.x), h2f(hd.x >> 16), mins_f16(hd, sel_mn)};
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // ---- the next super-block's loads go into the buffers just read (the
+    // activation scales, read in the compute phase, have two buffers)
+    if (b + 1 < nb) issue(b + 1);
+    const int da_buf = (b & 1) * kBM * 4;
+
+    // ---- phase 2: MFMAs and the fp32 epilogue, software-pipelined: each 16 x 16
+    // tile's epilogue runs after the next tile's MFMAs are issued (its results are
+    // complete by then). Per tile the 4 H-chain MFMAs run before the 4 L-chain ones,
+    // so the next weight tile's H operands load during the last tile's L chain and
+    // its L operands during the first tile's H chain.
+    auto load4 = [&](int tile, int hl) {
+      v4u r[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) r[s] = lds_ld16(lds, kHL + ((tile * 4 + s) * 2 + hl) * 1024 + lane * 16);
+      return std::array<v4u, 4>{r[0], r[1], r[2], r[3]};
+    };
+    auto epi = [&](const Tacc& r, const Sc& c, int nt, int mt) {
+      const f4_t da = __builtin_bit_cast(f4_t, lds_ld16(lds, da_buf + da_rd + mt * 16 * 4));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int S = r.L[e] + (r.H[e] << 3);
+        float u = c.d * (float)S;
+        u = fmaf(-c.dmin, r.M[e], u);
+        acc[nt][mt][e] = fmaf(da[e], u, acc[nt][mt][e]);
+      }
+    };
+    std::array<v4u, 4> Hc = load4(NT * wn, 0), Lc = load4(NT * wn, 1), Hn, Ln;
+    Tacc prev;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        Tacc cur;
+        const v4i_t z = {0, 0, 0, 0};
+        cur.H = mfma(a[mt][0], Hc[0], z);
+#pragma unroll
+        for (int s = 1; s < 4; ++s) cur.H = mfma(a[mt][s], Hc[s], cur.H);
+        if (mt == 0 && nt > 0) Lc = Ln;
+        if (mt == 3 && nt + 1 < NT) Hn = load4(NT * wn + nt + 1, 0);
+        cur.L = mfma(a[mt][0], Lc[0], z);
+#pragma unroll
+        for (int s = 1; s < 4; ++s) cur.L = mfma(a[mt][s], Lc[s], cur.L);
+        cur.M = mfma_h(am[mt], sc[nt].mb, f4_t{0.0f, 0.0f, 0.0f, 0.0f});
+        if (nt + mt > 0) {
+          const int pn = mt ? nt : nt - 1, pm = mt ? mt - 1 : 3;
+          epi(prev, sc[pn], pn, pm);
+        }
+        prev = cur;
+        if (mt == 3 && nt + 1 < NT) Hc = Hn;
+      }
+      if (nt + 1 < NT) Ln = load4(NT * wn + nt + 1, 1);
+    }
+    epi(prev, sc[NT - 1], NT - 1, 3);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // ---- store
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int64_t n = nbase + 16 * NT * wn + 16 * nt + li;
+    if (n < n0 || n >= n1) continue;
+    const float bn_ = bias ? bias[n] : 0.0f;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t mm = mbase + 64 * wm + 16 * mt + 4 * lg + e;
+        if (mm < m) y[mm * ys + n] = bias ? acc[nt][mt][e] + bn_ : acc[nt][mt][e];
       }
     }
   }
@@ -280,23 +612,89 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
 bool gemm_supported(int dtype, int af) { return dtype == kQ4_K && af == kActQ8_K; }
 
+namespace {
+
+template <int WM, int NT>
+hipError_t launch_cfg(const WeightDev& w, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
+                      float* y, int64_t ys, const float* bias, hipStream_t s) {
+  using C = Cfg<WM, NT>;
+  static_assert(C::kLds <= 160 * 1024, "LDS");
+  static bool attr_set[64] = {};
+  const int dev = w.device < 64 ? w.device : 63;
+  if (!attr_set[dev]) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_q4k<WM, NT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds);
+    if (e != hipSuccess) return e;
+    attr_set[dev] = true;
+  }
+  const int64_t nt0 = (n0 / kRowGroup) * kRowGroup;
+  const int64_t tiles_n = (n1 - nt0 + C::kBN - 1) / C::kBN;
+  const int64_t tiles_m = (m + C::kBM - 1) / C::kBM;
+  // buffer offsets are 32-bit: one tile's weight span and activation rows must fit
+  if ((int64_t)(C::kWB + 1) * w.nblk * 8192 >= (1ll << 32) || (int64_t)C::kBM * arb >= (1ll << 32) ||
+      tiles_n * tiles_m >= (1ll << 31)) {
+    return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL((k_gemm_q4k<WM, NT>), dim3((unsigned)(tiles_n * tiles_m)), dim3(kThreads), C::kLds, s,
+                     w.plane[0], w.plane[1], (int)w.nblk, w.n_pad, nt0, n0, n1, acts, arb, m, y, ys, bias,
+                     (int)tiles_n, (int)tiles_m);
+  return hipGetLastError();
+}
+
+template <int WM, int WN, int NT>
+hipError_t launch_big(const WeightDev& w, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
+                      float* y, int64_t ys, const float* bias, hipStream_t s) {
+  using C = Big<WM, WN, NT>;
+  static bool attr_set[64] = {};
+  const int dev = w.device < 64 ? w.device : 63;
+  if (!attr_set[dev]) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_q4k_big<WM, WN, NT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds);
+    if (e != hipSuccess) return e;
+    attr_set[dev] = true;
+  }
+  const int64_t nt0 = (n0 / kRowGroup) * kRowGroup;
+  const int64_t tiles_n = (n1 - nt0 + C::kBN - 1) / C::kBN;
+  const int64_t tiles_m = (m + C::kBM - 1) / C::kBM;
+  if ((int64_t)C::kGroups * w.nblk * 8192 >= (1ll << 32) || (int64_t)C::kBM * arb >= (1ll << 32) ||
+      tiles_n * tiles_m >= (1ll << 31)) {
+    return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL((k_gemm_q4k_big<WM, WN, NT>), dim3((unsigned)(tiles_n * tiles_m)), dim3(C::kThreads), C::kLds, s,
+                     w.plane[0], w.plane[1], (int)w.nblk, w.n_pad, nt0, n0, n1, acts, arb, m, y, ys, bias,
+                     (int)tiles_n, (int)tiles_m);
+  return hipGetLastError();
+}
+
+}  // namespace
+
 hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
                        float* y, int64_t ys, const float* bias, hipStream_t s) {
   if (!gemm_supported(w.dtype, af)) return hipErrorInvalidValue;
   if (m == 0 || n1 <= n0) return hipSuccess;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_q4k),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-    if (e != hipSuccess) return e;
-    attr_set = true;
+  const int cus = w.cus > 0 ? w.cus : 256;
+  const int64_t rows = n1 - (n0 / kRowGroup) * kRowGroup;
+  if (m > 128) {
+    // the 8-wave 256 x 128 tile when its grid fills the GPU (M = 512 at N = 14336:
+    // 224 workgroups, one round), else the 4-wave 128 x 64 tile (two per CU)
+    const int64_t wgs = (rows + 127) / 128 * ((m + 255) / 256);
+    if (wgs * 8 >= (int64_t)cus * 7) return launch_big<4, 2, 4>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+    return launch_big<2, 2, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s);
   }
-  const int64_t nt0 = (n0 / kRowGroup) * kRowGroup;
-  const int64_t ntiles = (n1 - nt0 + kBN - 1) / kBN;
-  const int64_t mtiles = (m + kBM - 1) / kBM;
-  hipLaunchKernelGGL(k_gemm_q4k, dim3((unsigned)ntiles, (unsigned)mtiles), dim3(kThreads), kLdsBytes, s, w.plane[0],
-                     w.plane[1], (int)w.nblk, w.n_pad, nt0, n0, n1, acts, arb, m, y, ys, bias);
-  return hipGetLastError();
+  // up to 128 rows: the 4-wave kernel with 64 or 128 activation rows; the weight-tile
+  // width is picked by rounds of workgroups over the CUs times the per-wave work
+  // (NT weight tiles plus a fixed share)
+  const int wm = m > 64 ? 2 : 1;
+  const int64_t tm = (m + 64 * wm - 1) / (64 * wm);
+  const int64_t bn2 = (4 / wm) * 32, bn1 = (4 / wm) * 16;
+  const int64_t cost2 = ((rows + bn2 - 1) / bn2 * tm + cus - 1) / cus * 3;
+  const int64_t cost1 = ((rows + bn1 - 1) / bn1 * tm + cus - 1) / cus * 2;
+  if (wm == 2) {
+    return cost2 <= cost1 ? launch_cfg<2, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s)
+                          : launch_cfg<2, 1>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+  }
+  return cost2 <= cost1 ? launch_cfg<1, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s)
+                        : launch_cfg<1, 1>(w, acts, arb, m, n0, n1, y, ys, bias, s);
 }
 
 }  // namespace dq

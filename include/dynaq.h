@@ -174,7 +174,8 @@ typedef struct dq_matmul_job {
 
 /* Several independent matmuls on one stream, e.g. the projections that share one
  * input (Q/K/V, gate/up) or the experts of an MoE layer. The decode-sized K-quant
- * jobs (2 <= m <= 16) of one k run together in grouped skinny-GEMV launches (up to
+ * jobs (Q4_K: 2 <= m <= 16; Q6_K: 2 <= m <= 64) of one k run together in grouped
+ * skinny-GEMV launches (up to
  * 8 jobs each, Q4_K and Q6_K mixed) that quantize each job's fp32 rows in the
  * kernel; every other job runs as dq_matmul runs it. Each job's y is
  * bit-identical to dq_matmul on that job. Replaces Device::matmul_many
@@ -207,7 +208,8 @@ DQ_API int dq_act_mul(int act, const float* gate, int64_t gate_stride, const flo
  * have the same n and k; out has out_stride floats per row; no bias. Replaces
  * Device::matmul_gated (dynacore/include/dynacore/device/device.h:188-199;
  * CpuDevice::matmul_gated, dynacore/cpu/cpu_device.cpp:1931-2072).
- *   - Q4_K / Q6_K weights of one type, m <= 64: one fused launch that streams both
+ *   - Q4_K weights with m <= 16, or Q6_K weights with m <= 64 (of one type): one
+ *     fused launch that streams both
  *     weights and writes only act(g) * u (no gate / up round trip);
  *   - otherwise both projections as dq_matmul computes them, into gate_scratch and
  *     up_scratch (m rows of scratch_stride floats each, clobbered), then dq_act_mul.
