@@ -216,6 +216,66 @@ def test_gemm_row_range_and_tails(cuda):
     assert np.array_equal(y[:, 9:170].view(np.uint32), want[:, 9:170].view(np.uint32))
 
 
+def _q8k_set_group(a: np.ndarray, row: int, k: int, group: int, code: int) -> None:
+    """Sets the 16 codes of 16-value group `group` of a Q8_K row to `code` and its bsum
+    to match (the block layout: float d, int8 q[256], int16 bsums[16])."""
+    blk, g = divmod(group, 16)
+    o = blk * 292
+    a[row, o + 4 + 16 * g: o + 4 + 16 * g + 16] = np.uint8(code & 0xFF)
+    a[row, o + 260 + 2 * g: o + 262 + 2 * g] = np.array([16 * code], np.int16).view(np.uint8)
+
+
+@pytest.mark.parametrize("m,n0,n1", [(512, 0, 14336), (300, 5, 14300)])
+def test_gemm_big_tile(cuda, m, n0, n1):
+    """The 8-wave 256 x 128 GEMM kernel (the grid at N=14336 fills the GPU): every
+    output bit-identical to the skinny / M=1 GEMV path on the same Q8_K rows, sampled
+    rows bit-identical to the oracle; a partial second activation tile (m=300) and a
+    row range that cuts both end tiles."""
+    from dynalm_amd import torch_ops as T
+
+    k, n = 512, 14336
+    w_rows = weight_rows(O.Q4_K, n, k, 77 + m, edge=True)
+    a = O.quantize_act(O.ACT_Q8_K, activations(m, k, 78 + m))
+    w = dq.Weight.upload(O.Q4_K, w_rows, k)
+    bias = np.linspace(-3, 3, n, dtype=np.float32)
+    ad = dev(a)
+    out = torch.full((m, n), 777.0, device="cuda")
+    T.gemm(w, O.ACT_Q8_K, ad, n0=n0, n1=n1, bias=dev(bias), out=out)
+    yg = host(out)
+    yv = host(T.gemv(w, O.ACT_Q8_K, ad, bias=dev(bias)))
+    assert np.all(yg[:, :n0] == 777.0) and np.all(yg[:, n1:] == 777.0)
+    assert np.array_equal(yg[:, n0:n1].view(np.uint32), yv[:, n0:n1].view(np.uint32))
+    cols = np.random.default_rng(m).choice(np.arange(n0, n1), 96, replace=False)
+    want = O.matmul(O.Q4_K, O.ACT_Q8_K, w_rows[cols], a, k, bias[cols])
+    assert np.array_equal(yg[:, cols].view(np.uint32), want.view(np.uint32))
+
+
+def test_gemm_extreme_codes(cuda):
+    """Saturated operands in every GEMM kernel: codes +127 / -127 in whole rows, a
+    16-value group of -128 codes (a valid ggml Q8_K code, bsum -2048: exact in fp16),
+    saturated 6-bit scales and mins. S and the mins term reach their largest
+    magnitudes; outputs stay bit-identical to the oracle and the GEMV."""
+    from dynalm_amd import torch_ops as T
+
+    k, n = 512, 14336
+    w_rows = weight_rows(O.Q4_K, n, k, 91, edge=True)
+    w_rows.reshape(n, k // 256, 144)[::3, :, 4:16] = 0xFF  # sc = m = 63 in every third row
+    w = dq.Weight.upload(O.Q4_K, w_rows, k)
+    cols = np.random.default_rng(5).choice(n, 64, replace=False)
+    for m in (40, 96, 512):  # the 4-wave kernel at 64 and 128 rows, the big kernel
+        a = O.quantize_act(O.ACT_Q8_K, activations(m, k, 92 + m))
+        a[0] = O.quantize_act(O.ACT_Q8_K, np.full((1, k), 3.0, np.float32))[0]
+        a[1] = O.quantize_act(O.ACT_Q8_K, np.full((1, k), -3.0, np.float32))[0]
+        for g in range(0, k // 16, 5):
+            _q8k_set_group(a, 2, k, g, -128)
+        ad = dev(a)
+        yg = host(T.gemm(w, O.ACT_Q8_K, ad))
+        yv = host(T.gemv(w, O.ACT_Q8_K, ad))
+        assert np.array_equal(yg.view(np.uint32), yv.view(np.uint32)), f"m={m}"
+        want = O.matmul(O.Q4_K, O.ACT_Q8_K, w_rows[cols], a, k)
+        assert np.array_equal(yg[:, cols].view(np.uint32), want.view(np.uint32)), f"m={m}"
+
+
 # ------------------------------------------------------------------ matmul
 
 
