@@ -593,18 +593,48 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     __syncthreads();
   }
 
-  // ---- store
+  // ---- store, through LDS (free after the last barrier): the wave's 64 x 16 NT
+  // tile is written in MFMA order (rows padded by 4 floats, so the four lane groups
+  // hit distinct banks) and read back as 16-byte row pieces, so each store
+  // instruction writes 4 rows of 64 NT contiguous bytes instead of 64-byte pieces.
+  {
+    constexpr int kRow = 16 * NT + 4;  // floats per staged row
+    static_assert(C::kWaves * 64 * kRow * 4 <= C::kLds, "staged output fits the LDS");
+    float* tile = reinterpret_cast<float*>(lds) + wave * 64 * kRow;
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int64_t n = nbase + 16 * NT * wn + 16 * nt + li;
-    if (n < n0 || n >= n1) continue;
-    const float bn_ = bias ? bias[n] : 0.0f;
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t mm = mbase + 64 * wm + 16 * mt + 4 * lg + e;
-        if (mm < m) y[mm * ys + n] = bias ? acc[nt][mt][e] + bn_ : acc[nt][mt][e];
+        for (int e = 0; e < 4; ++e) tile[(16 * mt + 4 * lg + e) * kRow + 16 * nt + li] = acc[nt][mt][e];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    constexpr int kLanesPerRow = 16 * NT / 4;  // 16-byte pieces per row
+    constexpr int kRowsPerStep = 64 / kLanesPerRow;
+    const int pr = lane / kLanesPerRow, pc = 4 * (lane % kLanesPerRow);
+    const int64_t n = nbase + 16 * NT * wn + pc;  // first of this lane's 4 columns
+    const bool vec = ((reinterpret_cast<uintptr_t>(y) | (uintptr_t)(ys * 4)) & 15) == 0 && n >= n0 && n + 4 <= n1;
+    f4_t bv = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (bias) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) bv[c] = n + c >= n0 && n + c < n1 ? bias[n + c] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 64 / kRowsPerStep; ++i) {
+      const int row = kRowsPerStep * i + pr;
+      const int64_t mm = mbase + 64 * wm + row;
+      if (mm >= m) continue;
+      f4_t v = *reinterpret_cast<const f4_t*>(tile + row * kRow + pc);
+      if (bias) v = v + bv;
+      float* dst = y + mm * ys + n;
+      if (vec) {
+        *reinterpret_cast<f4_t*>(dst) = v;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (n + c >= n0 && n + c < n1) dst[c] = v[c];
+        }
       }
     }
   }
