@@ -64,11 +64,16 @@ int hip_fail(hipError_t e, const char* what) {
   } while (0)
 
 bool weight_type_ok(int t) { return t == DQ_Q4_0 || t == DQ_Q8_0 || t == DQ_Q4_K || t == DQ_Q6_K; }
-bool act_fmt_ok(int f) { return f == DQ_ACT_PER32 || f == DQ_ACT_Q8_0 || f == DQ_ACT_Q8_K || f == DQ_ACT_SX; }
+bool act_fmt_ok(int f) {
+  return f == DQ_ACT_PER32 || f == DQ_ACT_Q8_0 || f == DQ_ACT_Q8_K || f == DQ_ACT_SX || f == DQ_ACT_Q16;
+}
 
 // The (weight, activation) pairs with kernels: the per-32 formats with Q8_0 / Q4_0
-// (dynacore's kInt8Per32 contract); Q8_K, sub-scaled and per-32 with the K-quants.
+// (dynacore's kInt8Per32 contract); Q8_K, sub-scaled and per-32 with the K-quants;
+// int16 with Q8_0, Q4_K and Q6_K (the types dynacore has int16 kernels for,
+// dynacore/cpu/avx2/kernels_avx2.cpp:1957-1960).
 bool pair_ok(int t, int f) {
+  if (f == DQ_ACT_Q16) return t == DQ_Q8_0 || t == DQ_Q4_K || t == DQ_Q6_K;
   if (t == DQ_Q8_0 || t == DQ_Q4_0) return f == DQ_ACT_PER32 || f == DQ_ACT_Q8_0;
   return f == DQ_ACT_Q8_K || f == DQ_ACT_SX || f == DQ_ACT_PER32;
 }

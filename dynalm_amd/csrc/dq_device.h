@@ -63,6 +63,19 @@ DQ_DEV int sdot16(v4u a, v4u b, int c) {
   return sdot4(a.w, b.w, c);
 }
 
+// sum_i a[i] * b[i] over 16 uint8 lanes, added to c (v_dot4_u32_u8).
+DQ_DEV u32 udot16(v4u a, v4u b, u32 c) {
+  c = __builtin_amdgcn_udot4(a.x, b.x, c, false);
+  c = __builtin_amdgcn_udot4(a.y, b.y, c, false);
+  c = __builtin_amdgcn_udot4(a.z, b.z, c, false);
+  return __builtin_amdgcn_udot4(a.w, b.w, c, false);
+}
+// The two int16 halves of a, added to c (v_dot2_i32_i16 against (1, 1)).
+DQ_DEV int sdot2w(u32 a, int c) {
+  typedef short s2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), s2{1, 1}, c, false);
+}
+
 // DPP lane moves inside rows of 16 lanes.
 template <int kCtrl>
 DQ_DEV int dpp(int v) {

@@ -136,9 +136,16 @@ struct Chunk<kQ4_0, U> : Chunk32<kQ4_0, U> {};
 //   sub-scaled super-block (352 B): u float @0, codes int8[256] @16, the block
 //       multipliers m_j int32[8] @272, m_j * s_j int32[8] @304 (s_j the code sum of
 //       32-value block j), and 128 s_j of the odd blocks int32[4] @336
+//   int16 32-value block (80 B): d float @0, code sum int32 @4, the code sums of
+//       values 0..15 and 16..31 int32 @8, @12, and each code split as 256 hi + lo:
+//       hi int8[32] @16, lo uint8[32] @48 (dynacore's split_act16,
+//       dynacore/cpu/generic/kernels_generic.cpp:334-350)
 constexpr int kStageQ8K = 336;
 constexpr int kStageSX = 352;
 constexpr int kStage32 = 48;
+constexpr int kStage16 = 80;
+// Staged bytes per 32-value block of the per-32 activation formats.
+constexpr int stage_b32(int af) { return af == kActQ16 ? kStage16 : kStage32; }
 // Staged bytes per super-block of the 256-value activation formats.
 constexpr int stage_sb(int af) { return af == kActSX ? kStageSX : kStageQ8K; }
 
@@ -159,6 +166,7 @@ struct Out {
   float* rec;
   float* dav;
   float acc[M];
+  float cor[M];  // Q4_K x int16: the mins term, subtracted at the end
   int32_t* dbg;
   int64_t dbg_n, n;
   int nblk, r;
@@ -245,6 +253,28 @@ DQ_DEV void compute(const Chunk<kQ4_K, U>& ch, int bb, const uint8_t* st, Out<M>
         t = fmaf(-dmin, (float)Mn, t);
         o.rec[(mm * o.nblk + b) * 64 + o.r] = t;
         if (o.r == 0) o.dav[mm * o.nblk + b] = as_f(lds4(ab));
+      } else if (AF == kActQ16) {
+        // int16 activations (kernels_avx2.cpp:1697-1729): P_j = sum q a over the
+        // 32 values of sub-block j, exactly 256 sum(q hi) + sum(q lo) (the nibbles
+        // are valid signed and unsigned bytes); acc += (float)(sc_j P_j) (d da) and
+        // the mins term dmin (m_j da (float)sum) gathered apart and subtracted
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int jp = j >> 1;
+          const uint8_t* ab = st + (mm * o.nblk * 8 + b * 8 + j) * kStage16;
+          const v4u c0 = ch.q[u][2 * jp], c1 = ch.q[u][2 * jp + 1];
+          const v4u q0 = (j & 1) ? ((c0 >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u : c0 & 0x0F0F0F0Fu;
+          const v4u q1 = (j & 1) ? ((c1 >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u : c1 & 0x0F0F0F0Fu;
+          const int ph = sdot16(q1, lds16(ab + 32), sdot16(q0, lds16(ab + 16), 0));
+          const int pl = (int)udot16(q1, lds16(ab + 64), udot16(q0, lds16(ab + 48), 0u));
+          const int P = ph * 256 + pl;
+          const u32 scw = j < 4 ? sc_lo : sc_hi;
+          const u32 mnw = j < 4 ? mn_lo : mn_hi;
+          const int sc = (int)bfe(scw, 8 * (j & 3), 6), mn = (int)bfe(mnw, 8 * (j & 3), 8);
+          const float ad = as_f(lds4(ab));
+          o.acc[mm] = o.acc[mm] + (float)(sc * P) * (d * ad);
+          o.cor[mm] = o.cor[mm] + dmin * (((float)mn * ad) * (float)(int)lds4(ab + 4));
+        }
       } else {
         // per-32 activations, sub-block order j = 0..7 (kernels_generic.cpp:267-275)
 #pragma unroll
@@ -333,6 +363,20 @@ DQ_DEV void compute(const Chunk<kQ6_K, U>& ch, int bb, const uint8_t* st, Out<M>
         }
         o.rec[(mm * o.nblk + b) * 64 + o.r] = d * (float)S;
         if (o.r == 0) o.dav[mm * o.nblk + b] = as_f(lds4(ab));
+      } else if (AF == kActQ16) {
+        // int16 activations (kernels_avx2.cpp:1732-1765): per 16-value unit the exact
+        // P = sum (q - 32) a = 256 sum(q hi) + sum(q lo) - 32 sum(a); acc += (float)(sc P) (d da)
+#pragma unroll
+        for (int uu = 0; uu < 16; ++uu) {
+          const int p = uu >> 3, cc = uu & 3, c = 4 * p + cc;  // unit uu lives in chunk c
+          const v4u qv = (uu & 4) ? qhi[c] : qlo[c];
+          const uint8_t* ab = st + (mm * o.nblk * 8 + b * 8 + uu / 2) * kStage16;
+          const int h = uu & 1;
+          const int P = sdot16(qv, lds16(ab + 16 + 16 * h), 0) * 256 + (int)udot16(qv, lds16(ab + 48 + 16 * h), 0u) -
+                        32 * (int)lds4(ab + 8 + 4 * h);
+          const u32 sw = uu < 4 ? ch.SC[u].x : uu < 8 ? ch.SC[u].y : uu < 12 ? ch.SC[u].z : ch.SC[u].w;
+          o.acc[mm] = o.acc[mm] + (float)(sbfe(sw, 8 * (uu & 3), 8) * P) * (d * as_f(lds4(ab)));
+        }
       } else {
         // per-32 activations, units of 16 in order (kernels_generic.cpp:299-306)
         const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
@@ -360,6 +404,20 @@ DQ_DEV void compute32(const Chunk32<WT, U>& ch, int bb, const uint8_t* st, Out<M
     const float dw = h2f(ch.DW[u]);
 #pragma unroll
     for (int mm = 0; mm < M; ++mm) {
+      if (AF == kActQ16) {
+        // int16 activations, Q8_0 (kernels_avx2.cpp:1662-1676): the exact
+        // P = sum q a = 256 sum(q hi) + sum(q (lo - 128)) + 128 sum(q); acc += (float)P (dw da)
+        const uint8_t* ab = st + (mm * o.nblk + b) * kStage16;
+        const v4u q0 = ch.q[u][0], q1 = ch.q[u][Chunk32<WT, U>::kC - 1];
+        const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
+        const v4u flip = {0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
+        const int ph = sdot16(q1, lds16(ab + 32), sdot16(q0, lds16(ab + 16), 0));
+        const int pl = sdot16(q1, lds16(ab + 64) ^ flip, sdot16(q0, lds16(ab + 48) ^ flip, 0));
+        const int sq = sdot16(q1, ones, sdot16(q0, ones, 0));
+        const int P = ph * 256 + pl + 128 * sq;
+        o.acc[mm] = o.acc[mm] + (float)P * (dw * as_f(lds4(ab)));
+        continue;
+      }
       const uint8_t* ab = st + (mm * o.nblk + b) * kStage32;
       const v4u x0 = lds16(ab + 16), x1 = lds16(ab + 32);
       int P;
@@ -440,6 +498,31 @@ DQ_DEV void stage_acts(const uint8_t* __restrict__ acts, int64_t arb, int nblk, 
         *reinterpret_cast<u32*>(o + (r == 0 ? 0 : 16 + 4 * (r - 1))) = v[mm][0];
         if (r < 9) *reinterpret_cast<u32*>(o + (r == 0 ? 16 + 4 * 63 : 272 + 4 * (r - 1))) = v[mm][1];
         if (r >= 1 && r < 9) stage_subsum(o, r - 1, bsum_pair(v[mm][1]));
+      }
+    }
+  } else if constexpr (AF == kActQ16) {
+    // lane r: one 32-value block per round; the int16 codes split into bytes
+    for (int blk = b0 * bpu + r; blk < b1 * bpu; blk += 64) {
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) {
+        const u32 base = (u32)(mm * arb + (int64_t)blk * 72);
+        const v2u ds = ld8(ra, base);
+        const v4u w0 = ld16(ra, base + 8), w1 = ld16(ra, base + 24), w2 = ld16(ra, base + 40), w3 = ld16(ra, base + 56);
+        const u32 w[16] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w, w2.x, w2.y, w2.z, w2.w, w3.x, w3.y, w3.z, w3.w};
+        u32 hi[8], lo[8];
+        int a16[2] = {0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          lo[i] = __builtin_amdgcn_perm(w[2 * i + 1], w[2 * i], 0x06040200u);
+          hi[i] = __builtin_amdgcn_perm(w[2 * i + 1], w[2 * i], 0x07050301u);
+          a16[i >> 2] = sdot2w(w[2 * i + 1], sdot2w(w[2 * i], a16[i >> 2]));
+        }
+        uint8_t* o = st + (mm * nblk * bpu + blk) * kStage16;
+        *reinterpret_cast<v4u*>(o) = v4u{ds.x, ds.y, (u32)a16[0], (u32)a16[1]};
+        *reinterpret_cast<v4u*>(o + 16) = v4u{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<v4u*>(o + 32) = v4u{hi[4], hi[5], hi[6], hi[7]};
+        *reinterpret_cast<v4u*>(o + 48) = v4u{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<v4u*>(o + 64) = v4u{lo[4], lo[5], lo[6], lo[7]};
       }
     }
   } else {
@@ -645,7 +728,8 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr bool kSb = AF == kActQ8_K || AF == kActSX;
   static_assert(!kGated || (kSb && M == 1 && kFuse), "the gated GEMV takes one fp32 row and K-quant weights");
-  static_assert(AF != kActSX || (!kFuse && kEarly == 0), "sub-scaled activations arrive quantized and staged by loops");
+  static_assert((AF != kActSX && AF != kActQ16) || (!kFuse && kEarly == 0),
+                "sub-scaled and int16 activations arrive quantized and staged by loops");
   // LDS: Q8_K t-terms [M][nblk][64] + da [M][nblk]  |  per-32 slice sums [W][M][64];
   // then the staged activation rows [M][nblk (blocks of 32 for per-32)][stage bytes].
   // kGated: one t-term region and one stage region per weight.
@@ -664,10 +748,11 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
   o.nblk = nblk;
   o.r = r;
 #pragma unroll
-  for (int mm = 0; mm < M; ++mm) o.acc[mm] = 0.0f;
+  for (int mm = 0; mm < M; ++mm) o.acc[mm] = o.cor[mm] = 0.0f;
   const int b0 = wl * nblk / WH, b1 = (wl + 1) * nblk / WH;  // this wave's blocks
   // bytes of the staged activation rows (the dummy area of the early path follows)
-  const int stage_bytes = kSb ? M * nblk * stage_sb(AF) : M * nblk * ((WT == kQ4_K || WT == kQ6_K) ? 8 : 1) * kStage32;
+  const int stage_bytes =
+      kSb ? M * nblk * stage_sb(AF) : M * nblk * ((WT == kQ4_K || WT == kQ6_K) ? 8 : 1) * stage_b32(AF);
   uint8_t* st = smem + (kGated ? 2 : 1) * region + half * stage_bytes;
 
   // plane buffer resources of this row group (64 rows x nblk blocks)
@@ -752,7 +837,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
 
   if (!kSb) {
 #pragma unroll
-    for (int mm = 0; mm < M; ++mm) o.rec[(wave * M + mm) * 64 + r] = o.acc[mm];
+    for (int mm = 0; mm < M; ++mm) o.rec[(wave * M + mm) * 64 + r] = AF == kActQ16 ? o.acc[mm] - o.cor[mm] : o.acc[mm];
   }
   __syncthreads();
   if (wave != 0) return;
@@ -802,7 +887,7 @@ static size_t gemv_lds_bytes(int wt, int af, int m, int waves, int64_t nblk, boo
   const bool sb = af == kActQ8_K || af == kActSX;
   size_t lds = sb ? ((size_t)m * nblk * 65 * sizeof(float) + 15) / 16 * 16 : (size_t)waves * m * 64 * sizeof(float);
   lds += sb ? (size_t)m * nblk * stage_sb(af)
-                        : (size_t)m * nblk * (wt == kQ4_K || wt == kQ6_K ? 8 : 1) * kStage32;
+                        : (size_t)m * nblk * (wt == kQ4_K || wt == kQ6_K ? 8 : 1) * stage_b32(af);
   if (early) lds += kDummyBytes;
   return lds;
 }
@@ -844,7 +929,7 @@ static hipError_t gemv_early(const WeightDev& w, const uint8_t* acts, int64_t ar
   if constexpr (M == 1 && AF == kActQ8_K) {
     if (per_wave == 1) return gemv_launch<WT, AF, M, kFuse, W, 1>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
     if (per_wave == 2) return gemv_launch<WT, AF, M, kFuse, W, 2>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
-  } else if constexpr (M == 1 && !kFuse && AF != kActSX) {
+  } else if constexpr (M == 1 && !kFuse && AF != kActSX && AF != kActQ16) {
     const int64_t bpu = WT == kQ4_K || WT == kQ6_K ? 8 : 1;
     if (per_wave * bpu <= 64) {
       return gemv_launch<WT, AF, M, kFuse, W, 1>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
@@ -881,13 +966,16 @@ static hipError_t gemv_pass(const WeightDev& w, int af, const uint8_t* acts, int
   switch (w.dtype) {
     case kQ4_K:
       if (af == kActSX) return gemv_waves<kQ4_K, kActSX, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+      if (af == kActQ16) return gemv_waves<kQ4_K, kActQ16, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
       return af == kActQ8_K ? gemv_waves<kQ4_K, kActQ8_K, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
                             : gemv_waves<kQ4_K, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
     case kQ6_K:
       if (af == kActSX) return gemv_waves<kQ6_K, kActSX, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+      if (af == kActQ16) return gemv_waves<kQ6_K, kActQ16, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
       return af == kActQ8_K ? gemv_waves<kQ6_K, kActQ8_K, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
                             : gemv_waves<kQ6_K, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
     case kQ8_0:
+      if (af == kActQ16) return gemv_waves<kQ8_0, kActQ16, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
       return af == kActPer32 ? gemv_waves<kQ8_0, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
                              : gemv_waves<kQ8_0, kActQ8_0, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
     default:

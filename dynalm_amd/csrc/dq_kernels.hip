@@ -59,7 +59,7 @@ __global__ __launch_bounds__(64) void k_quant_sx(const float* __restrict__ x, in
   if (l >= 1 && l <= 3) *reinterpret_cast<u32*>(o + 304 + 4 * l) = 0u;
 }
 
-// Per-32 blocks (ActBlockQ8 40 B or GGUF Q8_0 34 B): 8 lanes per block.
+// Per-32 blocks (ActBlockQ8 40 B, GGUF Q8_0 34 B or ActBlockQ16 72 B): 8 lanes per block.
 template <int AF>
 __global__ __launch_bounds__(64) void k_quant_b32(const float* __restrict__ x, int64_t x_stride, int64_t k,
                                                   uint8_t* __restrict__ out, int64_t orb) {
@@ -73,7 +73,21 @@ __global__ __launch_bounds__(64) void k_quant_b32(const float* __restrict__ x, i
   amax = max8f(amax);
   const float d = amax / 127.0f;
   const bool valid = blk * 32 < k;
-  if (AF == kActPer32) {
+  if (AF == kActQ16) {
+    float dd;
+    int sum;
+    const v2u codes = q16_quant(v, dd, sum);
+    if (valid) {
+      uint8_t* o = out + row * orb + blk * 72;
+      u32* oc = reinterpret_cast<u32*>(o + 8 + 8 * (l & 7));  // rows are only 4-byte aligned
+      oc[0] = codes.x;
+      oc[1] = codes.y;
+      if ((l & 7) == 0) {
+        *reinterpret_cast<float*>(o) = dd;
+        *reinterpret_cast<int32_t*>(o + 4) = sum;
+      }
+    }
+  } else if (AF == kActPer32) {
     float dd;
     int sum;
     const u32 packed = per32_quant(v, dd, sum);
@@ -140,6 +154,7 @@ DQ_DEV int act_code(int af, const uint8_t* a, int64_t i) {
     case kActPer32: return (int8_t)a[(i / 32) * 40 + 8 + i % 32];
     case kActQ8_0: return (int8_t)a[(i / 32) * 34 + 2 + i % 32];
     case kActSX: return (int8_t)a[(i / 256) * 320 + i % 256];
+    case kActQ16: return (int)*reinterpret_cast<const int16_t*>(a + (i / 32) * 72 + 8 + 2 * (i % 32));
     default: return (int8_t)a[(i / 256) * 292 + 4 + i % 256];
   }
 }
@@ -228,6 +243,9 @@ hipError_t launch_quantize(int af, const float* x, int64_t m, int64_t k, int64_t
     hipLaunchKernelGGL(k_quant_q8k, dim3((unsigned)(k / 256), (unsigned)m), dim3(64), 0, s, x, x_stride, k, out, orb);
   } else if (af == kActSX) {
     hipLaunchKernelGGL(k_quant_sx, dim3((unsigned)(k / 256), (unsigned)m), dim3(64), 0, s, x, x_stride, k, out, orb);
+  } else if (af == kActQ16) {
+    hipLaunchKernelGGL(k_quant_b32<kActQ16>, dim3((unsigned)((k + 255) / 256), (unsigned)m), dim3(64), 0, s, x,
+                       x_stride, k, out, orb);
   } else if (af == kActPer32) {
     hipLaunchKernelGGL(k_quant_b32<kActPer32>, dim3((unsigned)((k + 255) / 256), (unsigned)m), dim3(64), 0, s, x,
                        x_stride, k, out, orb);

@@ -4,7 +4,8 @@
 //
 // Contracts: per-32 ActBlockQ8 dynacore/cpu/generic/kernels_generic.cpp:187-207;
 // one scale per 256 values (Q8_K) dynacore/cpu/avx2/kernels_avx2.cpp:638-644;
-// sub-scaled ActSuperQ8 dynacore/cpu/avx2/kernels_avx2.cpp:1077-1096.
+// sub-scaled ActSuperQ8 dynacore/cpu/avx2/kernels_avx2.cpp:1077-1096;
+// int16 ActBlockQ16 dynacore/cpu/avx2/kernels_avx2.cpp:1631-1652.
 #pragma once
 
 #include "dq_device.h"
@@ -98,6 +99,30 @@ DQ_DEV u32 sx_quant(const float v[4], float& u, int& m, int& sum) {
   const u32 packed = codes4_rne(v, id, cs);
   sum = red8(cs);
   return packed;
+}
+
+// int16 ActBlockQ16 quantization (kernels_avx2.cpp:1631-1652) of 8 blocks held 4
+// values per lane (lanes 8i .. 8i+7 hold block i): d = amax32 / 32767, codes round
+// half to even at 1/d as int32 (values that are not finite or outside the int32
+// range become INT32_MIN, as cvtps_epi32 makes them); the stored int16 codes
+// saturate (packs_epi32) and the sum is that of the int32 codes. Returns the lane's
+// 4 int16 codes packed in two dwords, the block's d and (every lane) its sum.
+DQ_DEV v2u q16_quant(const float v[4], float& d, int& sum) {
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = max8f(amax);
+  d = amax / 32767.0f;
+  const float id = d > 0 ? 1.0f / d : 0.0f;
+  int s = 0;
+  u32 h[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float r = __builtin_rintf(v[i] * id);
+    const int c = (r >= -2147483648.0f && r < 2147483648.0f) ? (int)r : (int)0x80000000u;
+    s += c;
+    h[i] = (u32)(c < -32768 ? -32768 : (c > 32767 ? 32767 : c)) & 0xFFFFu;
+  }
+  sum = red8(s);
+  return v2u{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
 }
 
 }  // namespace dq

@@ -83,12 +83,20 @@ typedef enum dq_dtype {
  *                 (dynacore/include/dynacore/cpu/cpu_kernels.h:56-70,
  *                  dynacore/cpu/avx2/kernels_avx2.cpp:1077-1096). With Q4_K / Q6_K only; the
  *                 kernels form S = sum sc_j*m_j*P_j exactly (64 bits) and the mins term from
- *                 the integer m_j*sum_j. */
+ *                 the integer m_j*sum_j;
+ *   DQ_ACT_Q16    dynacore ActBlockQ16 {float d; int32 sum; int16 q[32]}, 72 B per 32 values:
+ *                 int16 activations (DD-076), dynacore's contract for inputs with outlier
+ *                 channels (the FFN down projection). d = amax32/32767, codes round half to
+ *                 even (saturated to int16), sum = the sum of the codes
+ *                 (dynacore/include/dynacore/cpu/cpu_kernels.h:72-82,
+ *                  dynacore/cpu/avx2/kernels_avx2.cpp:1631-1652). With Q8_0, Q4_K and Q6_K;
+ *                 the kernels form each 32-value (Q6_K: 16-value) integer dot exactly. */
 typedef enum dq_act_format {
   DQ_ACT_PER32 = 0,
   DQ_ACT_Q8_0 = 1,
   DQ_ACT_Q8_K = 2,
   DQ_ACT_SX = 3,
+  DQ_ACT_Q16 = 4,
 } dq_act_format;
 
 /* Activation rows at or below which dq_matmul runs the GEMV kernels. */

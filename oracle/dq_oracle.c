@@ -44,7 +44,7 @@ int64_t dqo_row_bytes(int dtype, int64_t k) {
 
 int64_t dqo_act_block_elems(int fmt) {
   switch (fmt) {
-    case DQO_ACT_PER32: case DQO_ACT_Q8_0: return 32;
+    case DQO_ACT_PER32: case DQO_ACT_Q8_0: case DQO_ACT_Q16: return 32;
     case DQO_ACT_Q8_K: case DQO_ACT_SX: return 256;
     default: return -1;
   }
@@ -56,6 +56,7 @@ static int64_t act_block_bytes(int fmt) {
     case DQO_ACT_Q8_0: return 34;   /* quant_formats.h:23 */
     case DQO_ACT_Q8_K: return 292;  /* quant_formats.h:30 */
     case DQO_ACT_SX: return 320;    /* cpu_kernels.h:62-69 */
+    case DQO_ACT_Q16: return 72;    /* cpu_kernels.h:77-82 */
     default: return -1;
   }
 }
@@ -247,6 +248,11 @@ int dqo_dequantize_act(int fmt, const void* a, float* y, int64_t n) {
         }
         break;
       }
+      case DQO_ACT_Q16: {
+        const float d = rdf(b);
+        for (int j = 0; j < 32; ++j) y[j] = d * (float)rd16s(b + 8 + 2 * j);
+        break;
+      }
       default: return -1;
     }
   }
@@ -350,6 +356,28 @@ static void quantize_sx_block(const float* x, uint8_t* out) {
   }
 }
 
+/* int16 ActBlockQ16 (quantize_act16, kernels_avx2.cpp:1631-1652): d = amax32/32767
+ * (fp32), id = 1/d (0 when d == 0), r = x*id rounded half to even; the int32
+ * conversion gives INT32_MIN for NaN and out-of-range r (cvtps_epi32); sum = the
+ * wrapping int32 sum of those codes; the stored codes saturate to int16
+ * (packs_epi32). amax here never takes a NaN (the reference's AVX2 max does,
+ * depending on the NaN's lane: NaN inputs are outside this format's parity). */
+static void quantize_q16_block(const float* x, uint8_t* out) {
+  const float d = abs_max(x, 32) / 32767.0f;
+  const float id = d > 0 ? 1.0f / d : 0.0f;
+  uint32_t sum = 0;
+  for (int i = 0; i < 32; ++i) {
+    const float r = rintf(x[i] * id);
+    const int32_t c = (r >= -2147483648.0f && r < 2147483648.0f) ? (int32_t)r : INT32_MIN;
+    sum += (uint32_t)c;
+    const int16_t q = (int16_t)(c < -32768 ? -32768 : (c > 32767 ? 32767 : c));
+    memcpy(out + 8 + 2 * i, &q, 2);
+  }
+  const int32_t s = (int32_t)sum;
+  memcpy(out, &d, 4);
+  memcpy(out + 4, &s, 4);
+}
+
 int dqo_quantize_act(int fmt, const float* x, void* out, int64_t n) {
   const int64_t be = dqo_act_block_elems(fmt), bb = act_block_bytes(fmt);
   if (be <= 0 || n % be != 0) return -1;
@@ -360,6 +388,7 @@ int dqo_quantize_act(int fmt, const float* x, void* out, int64_t n) {
       case DQO_ACT_Q8_0: quantize_q8_0_block(x, o); break;
       case DQO_ACT_Q8_K: quantize_q8_K_block(x, o); break;
       case DQO_ACT_SX: quantize_sx_block(x, o); break;
+      case DQO_ACT_Q16: quantize_q16_block(x, o); break;
       default: return -1;
     }
   }
@@ -509,6 +538,7 @@ int dqo_encode_weight_rows(int dtype, const float* x, int64_t rows, int64_t n, v
 /* ------------------------------------------------------------- partials */
 
 static int pair_ok(int wtype, int fmt) {
+  if (fmt == DQO_ACT_Q16) return wtype == DQO_Q8_0 || wtype == DQO_Q4_K || wtype == DQO_Q6_K;
   switch (wtype) {
     case DQO_Q8_0: case DQO_Q4_0: return fmt == DQO_ACT_PER32 || fmt == DQO_ACT_Q8_0;
     case DQO_Q4_K: case DQO_Q6_K: return fmt == DQO_ACT_PER32 || fmt == DQO_ACT_Q8_K || fmt == DQO_ACT_SX;
@@ -519,18 +549,19 @@ static int pair_ok(int wtype, int fmt) {
 int dqo_partials_count(int wtype, int fmt, int64_t k, int64_t* units, int64_t* sb_terms) {
   if (!pair_ok(wtype, fmt) || dqo_row_bytes(wtype, k) < 0 || dqo_act_row_bytes(fmt, k) < 0) return -1;
   *units = wtype == DQO_Q6_K ? k / 16 : k / 32;
-  *sb_terms = !(wtype == DQO_Q4_K || wtype == DQO_Q6_K) || fmt == DQO_ACT_PER32 ? 0
+  *sb_terms = !(wtype == DQO_Q4_K || wtype == DQO_Q6_K) || fmt == DQO_ACT_PER32 || fmt == DQO_ACT_Q16 ? 0
               : fmt == DQO_ACT_SX ? 3 * (k / 256) : 2 * (k / 256);
   return 0;
 }
 
 /* Activation codes of value i of a quantized row. */
-static int8_t act_code(int fmt, const uint8_t* a, int64_t i) {
+static int32_t act_code(int fmt, const uint8_t* a, int64_t i) {
   switch (fmt) {
     case DQO_ACT_PER32: return (int8_t)a[(i / 32) * 40 + 8 + i % 32];
     case DQO_ACT_Q8_0: return (int8_t)a[(i / 32) * 34 + 2 + i % 32];
     case DQO_ACT_Q8_K: return (int8_t)a[(i / 256) * 292 + 4 + i % 256];
     case DQO_ACT_SX: return (int8_t)a[(i / 256) * 320 + i % 256];
+    case DQO_ACT_Q16: return rd16s(a + (i / 32) * 72 + 8 + 2 * (i % 32));
     default: return 0;
   }
 }
@@ -539,6 +570,7 @@ static int8_t act_code(int fmt, const uint8_t* a, int64_t i) {
 static int32_t act_sum32(int fmt, const uint8_t* a, int64_t b) {
   switch (fmt) {
     case DQO_ACT_PER32: return rdi(a + b * 40 + 4);
+    case DQO_ACT_Q16: return rdi(a + b * 72 + 4);
     case DQO_ACT_Q8_K: {
       const uint8_t* blk = a + (b / 8) * 292;
       const int j = (int)(b % 8);
@@ -634,6 +666,45 @@ float dqo_dot(int wtype, int fmt, const void* wrow, const void* arow, int64_t k)
   int32_t units[4096 / 16 + 16];
   int32_t sb[3];
   float acc = 0.0f;
+
+  if (fmt == DQO_ACT_Q16) {
+    /* int16 activations: the arithmetic of dot_rows16_* (kernels_avx2.cpp:1662-1765)
+     * in one accumulator. Per unit the exact integer P (32 values; Q6_K 16) times
+     * the integer sub-block scale, acc = fma((float)(sc*P), d*da, acc); Q4_K's mins
+     * term cor += dmin*((m*da)*(float)sum) apart, returned as acc - cor. */
+    float cor = 0.0f;
+    for (int64_t b = 0; b < (wtype == DQO_Q8_0 ? k / 32 : k / 256); ++b) {
+      if (wtype == DQO_Q8_0) {
+        int32_t p = 0;
+        for (int t = 0; t < 32; ++t) p += (int32_t)(int8_t)w[b * 34 + 2 + t] * act_code(fmt, a, 32 * b + t);
+        const float dw = dqo_fp16_to_fp32(rd16(w + b * 34));
+        acc = fmaf((float)p, dw * rdf(a + b * 72), acc);
+        continue;
+      }
+      const uint8_t* blk = w + b * (wtype == DQO_Q4_K ? 144 : 210);
+      if (dqo_partials(wtype, fmt, blk, a + b * 8 * 72, 256, units, sb) != 0) return NAN;
+      if (wtype == DQO_Q4_K) {
+        const float d = dqo_fp16_to_fp32(rd16(blk)), dmin = dqo_fp16_to_fp32(rd16(blk + 2));
+        for (int j = 0; j < 8; ++j) {
+          uint8_t sc, mn;
+          dqo_scale_min_k4(j, blk + 4, &sc, &mn);
+          const uint8_t* ab = a + (b * 8 + j) * 72;
+          const float ad = rdf(ab);
+          acc = fmaf((float)((int32_t)sc * units[j]), d * ad, acc);
+          const float t1 = (float)mn * ad;
+          const float t2 = t1 * (float)rdi(ab + 4);
+          cor = cor + dmin * t2;
+        }
+      } else {
+        const float d = dqo_fp16_to_fp32(rd16(blk + 208));
+        for (int u = 0; u < 16; ++u) {
+          const float ad = rdf(a + (b * 8 + u / 2) * 72);
+          acc = fmaf((float)((int32_t)(int8_t)blk[192 + u] * units[u]), d * ad, acc);
+        }
+      }
+    }
+    return acc - cor;
+  }
 
   if (wtype == DQO_Q8_0 || wtype == DQO_Q4_0) {
     /* dot_rows_q8_0 / dot_rows_q4_0 (kernels_generic.cpp:216-239):

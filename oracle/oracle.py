@@ -20,9 +20,9 @@ ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libdynacore_ref.so")
 
 Q4_0, Q8_0, Q4_K, Q6_K, Q8_K = 6, 10, 14, 16, 17
-ACT_PER32, ACT_Q8_0, ACT_Q8_K, ACT_SX = 0, 1, 2, 3
+ACT_PER32, ACT_Q8_0, ACT_Q8_K, ACT_SX, ACT_Q16 = 0, 1, 2, 3, 4
 TYPE_NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q6_K: "q6_K", Q8_K: "q8_K"}
-ACT_NAMES = {ACT_PER32: "per32", ACT_Q8_0: "q8_0", ACT_Q8_K: "q8_K", ACT_SX: "sx"}
+ACT_NAMES = {ACT_PER32: "per32", ACT_Q8_0: "q8_0", ACT_Q8_K: "q8_K", ACT_SX: "sx", ACT_Q16: "q16"}
 
 _P = C.c_void_p
 _I64 = C.c_int64
@@ -259,6 +259,9 @@ def ref():
             "ref_bench_gemv": (_I64, [C.c_int, C.c_int, C.POINTER(_P), C.c_int, _I64, _I64, _P, _I64, C.c_int, _I64, _P,
                                       C.c_int, C.c_int]),
             "ref_exp_nonpos": (C.c_float, [C.c_float]),
+            "ref_quantize_act16": (C.c_int, [_P, _P, _I64]),
+            "ref_split_act16": (C.c_int, [_P, _P, _I64]),
+            "ref_dot_rows16": (C.c_int, [C.c_int, _P, _P, _I64, C.c_int, _I64, _P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(r, name)
@@ -270,7 +273,7 @@ def ref():
 
 def ref_quantize(kind: str, x: np.ndarray) -> np.ndarray:
     """The reference's quantizers on one row: 'q8_0' (GGUF), 'per32' (generic),
-    'per32_avx2', 'sb' (AVX2 super-block, ActBlockQ8 layout), 'sx' (AVX2)."""
+    'per32_avx2', 'sb' (AVX2 super-block, ActBlockQ8 layout), 'sx' (AVX2), 'q16' (AVX2 int16)."""
     r = ref()
     x = np.ascontiguousarray(x, dtype=np.float32).ravel()
     k = x.size
@@ -286,6 +289,9 @@ def ref_quantize(kind: str, x: np.ndarray) -> np.ndarray:
     elif kind == "sx":
         out = np.empty(k // 256 * 320, np.uint8)
         _check(r.ref_quantize_act_sx(_ptr(x), _ptr(out), k), kind)
+    elif kind == "q16":
+        out = np.empty(k // 32 * 72, np.uint8)
+        _check(r.ref_quantize_act16(_ptr(x), _ptr(out), k), kind)
     else:
         raise ValueError(kind)
     return out
@@ -308,4 +314,24 @@ def ref_dot_rows(kind: int, dtype: int, w_row: np.ndarray, acts: np.ndarray, k: 
     out = np.empty(m, np.float32)
     rc = r.ref_dot_rows(kind, dtype, _ptr(w_row), _ptr(acts), acts.shape[1], m, k, _ptr(out))
     _check(rc, "ref_dot_rows")
+    return out
+
+
+def ref_split_act16(a: np.ndarray) -> np.ndarray:
+    """The reference's split_act16 of int16 blocks: d, sum, hi int8[32], lo uint8[32] per 72 B."""
+    r = ref()
+    a = np.ascontiguousarray(a, dtype=np.uint8).ravel()
+    out = np.empty_like(a)
+    _check(r.ref_split_act16(_ptr(a), _ptr(out), a.size // 72), "ref_split_act16")
+    return out
+
+
+def ref_dot_rows16(dtype: int, w_row: np.ndarray, acts: np.ndarray, k: int) -> np.ndarray:
+    """The reference's AVX2 int16 row dots (dot_rows16_*); acts [m<=4, k/32*72 bytes]."""
+    r = ref()
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8).ravel()
+    acts = np.ascontiguousarray(np.atleast_2d(acts), dtype=np.uint8)
+    m = acts.shape[0]
+    out = np.empty(m, np.float32)
+    _check(r.ref_dot_rows16(dtype, _ptr(w_row), _ptr(acts), acts.shape[1], m, k, _ptr(out)), "ref_dot_rows16")
     return out

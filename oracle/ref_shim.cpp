@@ -8,6 +8,8 @@
 //   dynacore/src/quantization/quant_formats.cpp:12-222      dequantize_*, quantize_q8_0
 //   dynacore/cpu/generic/kernels_generic.cpp:187-310        quantize_act, dot_rows_* (generic)
 //   dynacore/cpu/avx2/kernels_avx2.cpp:610-1440             AVX2 quantizers and dots
+//   dynacore/cpu/avx2/kernels_avx2.cpp:1631-1765            quantize_act16, dot_rows16_*
+//   dynacore/cpu/generic/kernels_generic.cpp:334-346        split_act16
 //   dynacore/include/dynacore/base/fast_exp.h:16-35         exp_nonpos (SiLU)
 // Used to pin the C oracle (tests) and, on the GPU box, as the timed CPU
 // baseline ("reference" kind) of bench.py.
@@ -112,6 +114,35 @@ int ref_quantize_act_sx(const float* x, void* out, int64_t n) {
   const CpuKernels& k = avx2_table();
   if (n % 256 != 0 || !k.quantize_act_sx) return -1;
   k.quantize_act_sx(x, static_cast<ActBlockQ8*>(out), n);
+  return 0;
+}
+
+// int16 activations (ActBlockQ16, AVX2 quantize_act16) and their split-byte form
+// (ActBlockQ16S, generic split_act16).
+int ref_quantize_act16(const float* x, void* out, int64_t n) {
+  const CpuKernels& k = avx2_table();
+  if (n % 32 != 0 || !k.quantize_act16) return -1;
+  k.quantize_act16(x, static_cast<ActBlockQ16*>(out), n);
+  return 0;
+}
+
+int ref_split_act16(const void* in, void* out, int64_t nblocks) {
+  const CpuKernels& k = generic_table();
+  if (!k.split_act16) return -1;
+  k.split_act16(static_cast<const ActBlockQ16*>(in), static_cast<ActBlockQ16S*>(out), nblocks);
+  return 0;
+}
+
+// out[r] = dot(w row, int16 act row r), r < m <= 4 (AVX2 DotQ16RowsFn).
+int ref_dot_rows16(int dtype, const void* w, const void* acts, int64_t act_row_bytes, int m, int64_t k, float* out) {
+  if (!valid_type(dtype) || m < 1 || m > kDotRowsMax) return -1;
+  DotQ16RowsFn fn = avx2_table().dot_q16_rows_for(static_cast<DType>(dtype));
+  if (!fn) return -2;
+  std::vector<const ActBlockQ16*> p(static_cast<size_t>(m));
+  for (int r = 0; r < m; ++r) {
+    p[static_cast<size_t>(r)] = reinterpret_cast<const ActBlockQ16*>(static_cast<const uint8_t*>(acts) + r * act_row_bytes);
+  }
+  fn(w, p.data(), m, k, out);
   return 0;
 }
 

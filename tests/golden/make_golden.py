@@ -16,6 +16,11 @@ only (data, no code):
                dot_rows_sx_<t> (kernels_avx2.cpp:1117-1216)
   expnp        exp_nonpos of seeded and boundary inputs (base/fast_exp.h:16-35), the
                exponential of the reference's SiLU (cpu_device.cpp:117-123)
+  q16_x, act_q16  int16 activations (AVX2 quantize_act16, kernels_avx2.cpp:1631-1652) of
+               the act_x rows and of an edge row (ties, a zero block, +-inf, full-scale
+               codes); split_q16 their split_act16 bytes (kernels_generic.cpp:334-346)
+  q16dot_<t>   AVX2 dot_rows16_<t> (kernels_avx2.cpp:1662-1765) on act_q16, t in
+               q8_0, q4_K, q6_K
 """
 from __future__ import annotations
 
@@ -63,6 +68,21 @@ def activations(rows: int, k: int, seed: int) -> np.ndarray:
     return np.ascontiguousarray(x, dtype=np.float32)
 
 
+def q16_edge_row(k: int) -> np.ndarray:
+    """Edge cases of the int16 quantizer: x * (32767 / amax) on exact ties (amax =
+    32767 gives id = 1), a zero block, a block with +inf and -inf (d = inf, id = 0),
+    full-scale values of both signs, tiny values."""
+    x = O.normal(77, k).astype(np.float32)
+    x[0:32] = np.concatenate([np.arange(-7.5, 8.5, 1.0), np.arange(100.5, 116.5, 1.0)]).astype(np.float32)
+    x[0] = -32767.0
+    x[32:64] = 0.0
+    x[64 + 5] = np.inf
+    x[64 + 9] = -np.inf
+    x[96:128] = np.where(np.arange(32) % 2 == 0, 1.0, -1.0).astype(np.float32) * np.float32(3.0e4)
+    x[128:160] *= np.float32(1e-30)
+    return x
+
+
 def main() -> None:
     r = O.ref()
     if r is None:
@@ -95,6 +115,16 @@ def main() -> None:
         if t in (O.Q4_K, O.Q6_K):
             out[f"sbdot_{name}"] = np.stack([O.ref_dot_rows(2, t, w[i], out["act_sb"], K) for i in range(3)], 1)
             out[f"sxdot_{name}"] = np.stack([O.ref_dot_rows(3, t, w[i], out["act_sx"], K) for i in range(3)], 1)
+
+    q16x = np.concatenate([x, q16_edge_row(K)[None]], 0)
+    out["q16_x"] = q16x
+    out["act_q16"] = np.stack([O.ref_quantize("q16", row) for row in q16x])
+    out["split_q16"] = np.stack([O.ref_split_act16(a) for a in out["act_q16"]])
+    for t in (O.Q8_0, O.Q4_K, O.Q6_K):
+        name = O.TYPE_NAMES[t]
+        w = out[f"w_{name}"]
+        dots = [O.ref_dot_rows16(t, w[i], out["act_q16"][r0:r0 + 4], K) for i in range(3) for r0 in (0, 4)]
+        out[f"q16dot_{name}"] = np.stack([np.concatenate(dots[2 * i:2 * i + 2]) for i in range(3)], 1)
 
     rng = np.random.default_rng(20261202)
     ex = np.concatenate([

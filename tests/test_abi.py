@@ -55,6 +55,14 @@ def test_sizes():
     assert dq.partials_count(dq.Q4_K, dq.ACT_Q8_K, 4096) == (128, 32)
     assert dq.partials_count(dq.Q6_K, dq.ACT_Q8_K, 4096) == (256, 32)
     assert dq.partials_count(dq.Q8_0, dq.ACT_PER32, 4096) == (128, 0)
+    # int16 activations: ActBlockQ16 (dynacore/include/dynacore/cpu/cpu_kernels.h:77-82)
+    assert dq.act_row_bytes(dq.ACT_Q16, 4096) == 128 * 72
+    assert dq.act_row_bytes(dq.ACT_Q16, 96) == 3 * 72
+    assert dq.partials_count(dq.Q4_K, dq.ACT_Q16, 4096) == (128, 0)
+    assert dq.partials_count(dq.Q6_K, dq.ACT_Q16, 4096) == (256, 0)
+    assert dq.partials_count(dq.Q8_0, dq.ACT_Q16, 4096) == (128, 0)
+    with pytest.raises(dq.DqError):
+        dq.partials_count(dq.Q4_0, dq.ACT_Q16, 256)  # no int16 kernel for Q4_0 in the reference either
 
 
 def _upload_status(dtype, n, k, row_bytes):

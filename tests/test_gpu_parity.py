@@ -803,3 +803,148 @@ def test_gemv_sx_s_beyond_int32(cuda):
     want = O.matmul(O.Q4_K, O.ACT_SX, rows, a, k)
     assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
     assert abs(float(want[0, 0])) > 0
+
+
+# ------------------------------------------------ int16 activations (DD-076)
+
+
+def _q16_bound(t: int, rows: np.ndarray, a: np.ndarray, k: int) -> tuple[np.ndarray, np.ndarray]:
+    """The double-precision product of the dequantized weights and activations and the
+    sum of |terms|: the reference's own int16 bound is |y - ref| <= 1e-5 * mag
+    (test_int_kernels.cpp:181-193)."""
+    wf = O.dequantize(t, rows, k).astype(np.float64)
+    af = O.dequantize_act(O.ACT_Q16, a, k).astype(np.float64)
+    return af @ wf.T, np.abs(af) @ np.abs(wf).T
+
+
+@pytest.mark.parametrize("k", [256, 4096, 14336])
+def test_quantize_q16_bit_exact(cuda, k):
+    """dynacore's quantize_act16 (kernels_avx2.cpp:1631-1652): zero, tie, huge, subnormal,
+    +-inf (d = inf, id = 0, the INT32_MIN code) and outlier rows."""
+    x = activations(6, k, 1300 + k)
+    x[1, :] = 0.0
+    x[2, :32] = np.linspace(-15.5, 15.5, 32)
+    x[2, 7] = 32767.0                                     # d = 1: exact ties
+    x[3, 40] = 3.0e38
+    x[3, 41] = -1.0e-39
+    x[4, 70] = np.inf
+    x[4, 100] = -np.inf
+    x[5, :] *= np.float32(1e4)
+    assert np.array_equal(quant_gpu(O.ACT_Q16, x, stride_pad=7), O.quantize_act(O.ACT_Q16, x))
+
+
+def test_quantize_q16_matches_reference_golden(cuda):
+    gold = _gold()
+    assert np.array_equal(quant_gpu(O.ACT_Q16, gold["q16_x"]), gold["act_q16"])
+
+
+Q16_TYPES = [O.Q8_0, O.Q4_K, O.Q6_K]
+
+
+@pytest.mark.parametrize("t", Q16_TYPES, ids=lambda t: O.TYPE_NAMES[t])
+@pytest.mark.parametrize("m", [1, 3, 4, 5, 8, 11])
+def test_gemv_q16_parity(cuda, t, m):
+    """int16 GEMV: within the reference's bound of the exact product and of the oracle;
+    integer unit partials bit-exact; dq_matmul_act (GPU quantization) gives the same bits."""
+    from dynalm_amd import torch_ops as T
+
+    k, n = 1280, 200
+    rows = weight_rows(t, n, k, 1400 + m, edge=True)
+    x = activations(m, k, 1410 + m)
+    x[:, 7::97] *= np.float32(60.0)                       # outlier channels, the reason for int16
+    a = O.quantize_act(O.ACT_Q16, x)
+    w = dq.Weight.upload(t, rows, k)
+    y = host(T.gemv(w, O.ACT_Q16, dev(a)))
+    want = O.matmul(t, O.ACT_Q16, rows, a, k)
+    exact, mag = _q16_bound(t, rows, a, k)
+    assert np.all(np.abs(y - exact) <= 1e-5 * mag + 1e-30)
+    assert np.all(np.abs(y.astype(np.float64) - want) <= 2e-6 * mag + 1e-30)
+    units, _ = T.partials(w, O.ACT_Q16, dev(a))
+    want_u, _ = O.partials(t, O.ACT_Q16, rows, a, k)
+    assert np.array_equal(host(units), want_u)
+    ya = host(T.matmul_act(w, O.ACT_Q16, dev(x)))
+    assert np.array_equal(ya.view(np.uint32), y.view(np.uint32))
+
+
+def _q16_exact_case(t: int, n: int, k: int, seed: int) -> tuple[np.ndarray, np.ndarray]:
+    """Weights with d = dmin = 1 and small scales, activation blocks with d = 1 and one
+    full-scale code (+-32767, -32768) per 32 values: every partial sum is an integer
+    below 2^24, so any summation order gives the same fp32 bits and the result is the
+    exact integer dot. Pins the split of each code into 256 hi + lo at the extremes."""
+    rng = np.random.default_rng(seed)
+    one = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    rows = O.random_bytes(seed, n * O.row_bytes(t, k)).reshape(n, -1).copy()
+    if t == O.Q8_0:
+        blk = rows.reshape(n, -1, 34)
+        blk[:, :, 0:2] = one
+        blk[:, :, 2:] = rng.integers(-31, 32, blk[:, :, 2:].shape).astype(np.int8).view(np.uint8)
+    elif t == O.Q4_K:
+        blk = rows.reshape(n, -1, 144)
+        blk[:, :, 0:2] = one
+        blk[:, :, 2:4] = one
+        # 6-bit scales 0..3 and mins 0..31 for sub-blocks 0..3 (bytes 4..11); sub-blocks
+        # 4..7 take scale low bits from bytes 12..15 and high bits from bytes 4..11's top
+        blk[:, :, 4:8] = rng.integers(0, 4, blk[:, :, 4:8].shape)
+        blk[:, :, 8:12] = rng.integers(0, 32, blk[:, :, 8:12].shape)
+        blk[:, :, 12:16] = rng.integers(0, 4, blk[:, :, 12:16].shape) | (rng.integers(0, 2, blk[:, :, 12:16].shape) << 4)
+    else:
+        blk = rows.reshape(n, -1, 210)
+        blk[:, :, 208:210] = one
+        blk[:, :, 192:208] = rng.integers(-1, 2, blk[:, :, 192:208].shape).astype(np.int8).view(np.uint8)
+    m = 3
+    a = np.zeros((m, k // 32, 72), np.uint8)
+    a[:, :, 0:4] = np.frombuffer(np.float32(1.0).tobytes(), np.uint8)
+    codes = np.zeros((m, k // 32, 32), np.int16)
+    pos = rng.integers(0, 32, (m, k // 32))
+    val = rng.choice(np.array([-32768, 32767, -32767, 255, -256, 256], np.int16), (m, k // 32))
+    np.put_along_axis(codes, pos[..., None], val[..., None], -1)
+    a[:, :, 8:] = codes.view(np.uint8).reshape(m, k // 32, 64)
+    a[:, :, 4:8] = codes.astype(np.int32).sum(-1, keepdims=True, dtype=np.int32).view(np.uint8)
+    return rows, a.reshape(m, -1)
+
+
+@pytest.mark.parametrize("t", Q16_TYPES, ids=lambda t: O.TYPE_NAMES[t])
+def test_gemv_q16_exact_integers(cuda, t):
+    from dynalm_amd import torch_ops as T
+
+    k, n = 256, 256
+    rows, a = _q16_exact_case(t, n, k, 1500 + t)
+    want = O.matmul(t, O.ACT_Q16, rows, a, k)
+    exact, _ = _q16_bound(t, rows, a, k)
+    assert np.array_equal(want, exact.astype(np.float32))  # the case is exact in fp32
+    assert np.all(np.abs(exact) < 2.0**24)
+    w = dq.Weight.upload(t, rows, k)
+    y = host(T.gemv(w, O.ACT_Q16, dev(a)))
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", Q16_TYPES, ids=lambda t: O.TYPE_NAMES[t])
+def test_gemv_q16_vs_reference_avx2(cuda, t):
+    """Against the reference's AVX2 dot_rows16_* (golden q16dot_*): fp32 order only."""
+    from dynalm_amd import torch_ops as T
+
+    gold = _gold()
+    name = O.TYPE_NAMES[t]
+    rows = gold[f"w_{name}"]
+    a = gold["act_q16"][:4]                                # the edge row holds +-inf (no finite result)
+    w = dq.Weight.upload(t, rows, 512)
+    y = host(T.gemv(w, O.ACT_Q16, dev(a)))
+    _, mag = _q16_bound(t, rows, a, 512)
+    assert np.all(np.abs(y - gold[f"q16dot_{name}"][:4]) <= 1e-5 * mag)
+
+
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q6_K], ids=lambda t: O.TYPE_NAMES[t])
+def test_gemv_q16_ffn_down_size(cuda, t):
+    """The int16 contract's matmul: the FFN down projection, K = 14336 (config 4's
+    intermediate size), 5 rows (a 4-row pass and a 1-row pass), 320 sampled outputs."""
+    from dynalm_amd import torch_ops as T
+
+    k, n = 14336, 320
+    rows = gguf_weights(t, n, k, 1600 + t, outlier_frac=0.01)
+    x = activations(5, k, 1601)
+    x[:, 11::211] *= np.float32(80.0)
+    w = dq.Weight.upload(t, rows, k)
+    y = host(T.matmul_act(w, O.ACT_Q16, dev(x)))
+    a = O.quantize_act(O.ACT_Q16, x)
+    exact, mag = _q16_bound(t, rows, a, k)
+    assert np.all(np.abs(y - exact) <= 1e-5 * mag)

@@ -108,6 +108,55 @@ def test_act_quantizers_golden(gold, kind, fmt):
     assert np.array_equal(O.quantize_act(fmt, gold["act_x"]), gold[f"act_{kind}"])
 
 
+def test_act_q16_golden(gold):
+    """int16 activations bit-equal to the reference's AVX2 quantize_act16 on the
+    seeded rows and the edge row (ties, zero block, +-inf, full scale, tiny values)."""
+    assert np.array_equal(O.quantize_act(O.ACT_Q16, gold["q16_x"]), gold["act_q16"])
+
+
+def test_q16_invariants_and_split(gold):
+    """test_int_kernels.cpp:166-178: |x - d q| <= d (0.5 + 3e-7 |q|), sum == sum(q), the
+    amax element at +-32767; and the reference's split_act16 bytes are q = 256 hi + lo
+    with hi = q >> 8 (signed) and lo = q & 255, the decomposition the GPU kernels use."""
+    x = activations(6, 1024, 12)
+    a = O.quantize_act(O.ACT_Q16, x).reshape(6, -1, 72)
+    d = a[:, :, 0:4].copy().view(np.float32)[..., 0].astype(np.float64)
+    s = a[:, :, 4:8].copy().view(np.int32)[..., 0]
+    q = a[:, :, 8:].copy().view(np.int16).astype(np.int64)
+    xb = x.reshape(6, -1, 32).astype(np.float64)
+    assert np.all(np.abs(xb - d[..., None] * q) <= d[..., None] * (0.5 + 3e-7 * np.abs(q)) + 1e-12)
+    assert np.array_equal(q.sum(-1), s)
+    amax_at = np.abs(xb).argmax(-1)
+    qa = np.take_along_axis(q, amax_at[..., None], -1)[..., 0]
+    assert np.all(np.abs(qa[d > 0]) == 32767)
+    sp = gold["split_q16"].reshape(-1, 72)
+    g = gold["act_q16"].reshape(-1, 72)
+    assert np.array_equal(sp[:, :8], g[:, :8])
+    q = g[:, 8:].copy().view(np.int16).astype(np.int64)
+    hi = sp[:, 8:40].view(np.int8).astype(np.int64)
+    lo = sp[:, 40:72].astype(np.int64)
+    assert np.array_equal(256 * hi + lo, q)
+    assert np.array_equal(hi, q >> 8) and np.array_equal(lo, q & 255)
+
+
+def test_q16_edge_codes():
+    """Ties round half to even at d = 1; +-inf give d = inf, id = 0 and the INT32_MIN
+    code of cvtps_epi32 (saturated to -32768; two of them wrap the sum to 0)."""
+    x = np.zeros((1, 64), np.float32)
+    x[0, 0] = 32767.0
+    x[0, 1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 32766.5, -32766.5]
+    x[0, 32 + 3] = np.inf
+    a = O.quantize_act(O.ACT_Q16, x)[0]
+    q = a[8:72].copy().view(np.int16)
+    assert a[:4].view(np.float32)[0] == 1.0
+    assert list(q[1:9]) == [0, 2, 2, 0, -2, -2, 32766, -32766]
+    b = a[72:]
+    assert b[:4].view(np.float32)[0] == np.inf
+    assert b[4:8].view(np.int32)[0] == -2**31
+    qb = b[8:].copy().view(np.int16)
+    assert qb[3] == -32768 and not np.any(np.delete(qb, 3))
+
+
 def test_act_q8_K_golden(gold):
     x = gold["act_x"]
     mine = O.quantize_act(O.ACT_Q8_K, x).reshape(x.shape[0], -1, 292)
@@ -246,12 +295,15 @@ def _act_codes(fmt: int, a: np.ndarray, k: int) -> np.ndarray:
         return a.reshape(a.shape[0], -1, 34)[:, :, 2:].view(np.int8).reshape(a.shape[0], k).astype(np.int64)
     if fmt == O.ACT_Q8_K:
         return a.reshape(a.shape[0], -1, 292)[:, :, 4:260].view(np.int8).reshape(a.shape[0], k).astype(np.int64)
+    if fmt == O.ACT_Q16:
+        return a.reshape(a.shape[0], -1, 72)[:, :, 8:].copy().view(np.int16).reshape(a.shape[0], k).astype(np.int64)
     return a.reshape(a.shape[0], -1, 320)[:, :, :256].view(np.int8).reshape(a.shape[0], k).astype(np.int64)
 
 
 PAIRS_ALL = [(O.Q8_0, O.ACT_PER32), (O.Q8_0, O.ACT_Q8_0), (O.Q4_0, O.ACT_PER32), (O.Q4_0, O.ACT_Q8_0),
              (O.Q4_K, O.ACT_PER32), (O.Q4_K, O.ACT_Q8_K), (O.Q4_K, O.ACT_SX),
-             (O.Q6_K, O.ACT_PER32), (O.Q6_K, O.ACT_Q8_K), (O.Q6_K, O.ACT_SX)]
+             (O.Q6_K, O.ACT_PER32), (O.Q6_K, O.ACT_Q8_K), (O.Q6_K, O.ACT_SX),
+             (O.Q8_0, O.ACT_Q16), (O.Q4_K, O.ACT_Q16), (O.Q6_K, O.ACT_Q16)]
 
 
 @pytest.mark.parametrize("t,fmt", PAIRS_ALL, ids=lambda p: str(p))
@@ -320,6 +372,25 @@ def test_q8K_and_sx_dots_vs_reference_avx2(gold, t):
     assert np.max(np.abs(ys - gold[f"sxdot_{name}"])) <= 1e-5 * np.abs(gold[f"sxdot_{name}"]).max()
 
 
+@pytest.mark.parametrize("t", (O.Q8_0, O.Q4_K, O.Q6_K), ids=lambda t: O.TYPE_NAMES[t])
+def test_q16_dots_vs_reference_avx2(gold, t):
+    """int16 dots vs the reference's AVX2 dot_rows16_* on the same bytes: the same
+    exact integers, fp32 lane order only (1e-5 of the sum of |terms|,
+    test_int_kernels.cpp:181-193); the edge row included."""
+    name = O.TYPE_NAMES[t]
+    w = gold[f"w_{name}"]
+    a = gold["act_q16"]
+    y = O.matmul(t, O.ACT_Q16, w, a, 512)
+    mag = np.abs(O.dequantize_act(O.ACT_Q16, a, 512).astype(np.float64)) @ np.abs(O.dequantize(t, w, 512).astype(np.float64)).T
+    fin = np.isfinite(mag)
+    assert fin[:4].all()
+    assert np.all(np.abs(y - gold[f"q16dot_{name}"])[fin] <= 1e-5 * mag[fin])
+    # the edge row holds +-inf inputs (a block with d = inf): no finite result on either
+    # side; whether inf or NaN depends on how the products are grouped (the reference's
+    # 8 lanes give 0 * inf = NaN in lanes without the inf's code)
+    assert not np.isfinite(y[4]).any() and not np.isfinite(gold[f"q16dot_{name}"][4]).any()
+
+
 @pytest.mark.parametrize("t,fmt", PAIRS_ALL, ids=lambda p: str(p))
 def test_dots_within_double_bound(t, fmt):
     """|y - y_double| <= 1e-5 * sum|w_i x_i| against the double product of the
@@ -374,7 +445,8 @@ def test_encoders_error_bound(t):
 @pytest.mark.parametrize("seed", [1, 2, 3])
 def test_live_reference_quantizers(seed):
     x = activations(3, 2048, seed)
-    for kind, fmt in (("q8_0", O.ACT_Q8_0), ("per32", O.ACT_PER32), ("per32_avx2", O.ACT_PER32), ("sx", O.ACT_SX)):
+    for kind, fmt in (("q8_0", O.ACT_Q8_0), ("per32", O.ACT_PER32), ("per32_avx2", O.ACT_PER32), ("sx", O.ACT_SX),
+                      ("q16", O.ACT_Q16)):
         ref = np.stack([O.ref_quantize(kind, x[i]) for i in range(3)])
         assert np.array_equal(O.quantize_act(fmt, x), ref), kind
 
