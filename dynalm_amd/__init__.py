@@ -37,6 +37,7 @@ __all__ = [
     "DqError", "lib", "lib_path", "row_bytes", "act_row_bytes", "act_format_for", "Weight",
     "act_quantize", "gemv", "gemm", "matmul", "matmul_many", "MatmulJob", "partials_count", "debug_partials",
     "SILU", "GELU", "GELU_TANH", "act_mul", "matmul_gated", "GgufFile", "GgufTensor", "EXPORTS",
+    "MatmulShape", "External",
 ]
 
 Q4_0, Q8_0, Q4_K, Q6_K = 6, 10, 14, 16
@@ -91,6 +92,12 @@ EXPORTS = {
     "dq_matmul_gated": (_I, [_I, _P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P]),
     "dq_partials_count": (_I, [_I, _I, _I64, C.POINTER(_I64), C.POINTER(_I64)]),
     "dq_debug_partials": (_I, [_P, _I, _P, _I64, _P, _P, _P]),
+    "dq_external_create": (_I, [_I, _I64, _I64, C.POINTER(_P)]),
+    "dq_external_free": (_I, [_P]),
+    "dq_external_eligible": (_I, [_P, _P, _P]),
+    "dq_external_run": (_I, [_P, _P, _I64, _I64, _P, _I, _I64, _I64, _I64, _P, _P, _I64]),
+    "dq_external_forget": (_I, [_P, _P]),
+    "dq_external_get_stats": (_I, [_P, _P]),
 }
 
 
@@ -338,3 +345,70 @@ class GgufFile:
         h = _P()
         _check(lib().dq_gguf_upload_weight(self._h, i, stream, C.byref(h)))
         return Weight(h.value)
+
+
+class MatmulShape(C.Structure):
+    """dq_matmul_shape (dynacore MatmulShape, kernel/matmul_registry.h:87-91)."""
+    _fields_ = [("m", _I64), ("n", _I64), ("k", _I64), ("dtype", C.c_int32), ("x_dense", C.c_int32)]
+
+
+class ExternalStats(C.Structure):
+    _fields_ = [("runs", _I64), ("uploads", _I64), ("hits", _I64), ("evictions", _I64), ("resident_bytes", _I64),
+                ("resident_weights", _I64)]
+
+
+def external_eligible(shape: MatmulShape, weight: int, adapter: "External | None" = None) -> bool:
+    """dq_external_eligible: a pure shape rule (no GPU needed with adapter None)."""
+    h = adapter._h if adapter is not None else None
+    return bool(lib().dq_external_eligible(h, C.byref(shape), weight))
+
+
+class External:
+    """dq_external: matmuls on host (numpy) arrays, with device copies of the weights
+    kept across calls (the ExternalMatmulKernel shape of dynacore's CpuDevice)."""
+
+    def __init__(self, device: int = 0, min_rows: int = 1, max_resident_bytes: int = 0):
+        h = _P()
+        _check(lib().dq_external_create(device, min_rows, max_resident_bytes, C.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if self._h:
+            _check(lib().dq_external_free(self._h))
+            self._h = _P()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def eligible(self, m: int, n: int, k: int, dtype: int, weight: int, x_dense: bool = True) -> bool:
+        return external_eligible(MatmulShape(m, n, k, dtype, int(x_dense)), weight, self)
+
+    def run(self, x, w_rows, dtype: int, k: int, bias=None, y=None):
+        """x: [m, k] float32 (row stride from the array), w_rows: [n, row_bytes] uint8
+        GGUF rows; returns y [m, n] float32 (or fills the given y)."""
+        import numpy as np
+
+        assert x.dtype == np.float32 and x.ndim == 2 and x.strides[1] == 4
+        assert w_rows.dtype == np.uint8 and w_rows.ndim == 2 and w_rows.strides[1] == 1
+        m, n = x.shape[0], w_rows.shape[0]
+        if y is None:
+            y = np.empty((m, n), np.float32)
+        assert y.dtype == np.float32 and y.strides[1] == 4
+        b = None
+        if bias is not None:
+            bias = np.ascontiguousarray(bias, np.float32)
+            b = bias.ctypes.data
+        _check(lib().dq_external_run(self._h, x.ctypes.data, m, x.strides[0] // 4, w_rows.ctypes.data, dtype, n, k,
+                                     w_rows.strides[0], b, y.ctypes.data, y.strides[0] // 4))
+        return y
+
+    def forget(self, w_rows) -> None:
+        _check(lib().dq_external_forget(self._h, w_rows.ctypes.data))
+
+    def stats(self) -> dict:
+        st = ExternalStats()
+        _check(lib().dq_external_get_stats(self._h, C.byref(st)))
+        return {f: getattr(st, f) for f, _ in ExternalStats._fields_}

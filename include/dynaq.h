@@ -270,6 +270,53 @@ DQ_API int dq_gguf_get_string(const dq_gguf* g, const char* key, const char** st
  * (Device::upload of GgufFile::load_tensor's view, gguf.cpp:457-466). */
 DQ_API int dq_gguf_upload_weight(const dq_gguf* g, int64_t i, void* stream, dq_weight** out);
 
+/* ---- host-memory adapter ------------------------------------------------
+ * The shape of dynacore's run-time extension point ExternalMatmulKernel
+ * {name, eligible(const MatmulShape&, const void* weight), run(x, w, bias*, y)}
+ * (dynacore/include/dynacore/cpu/cpu_device.h:22-30), which CpuDevice consults
+ * before its built-in kernels (dynacore/cpu/cpu_device.cpp:810-826,909-911), for
+ * an engine whose tensors live in host memory. A dq_external keeps one device copy
+ * per weight it is given, keyed by the weight's host address, type, shape and row
+ * stride (as CpuDevice keys its packed copies by data pointer and (n, k),
+ * dynacore/include/dynacore/cpu/cpu_device.h:135-143), dropping the least recently
+ * used copies beyond max_resident_bytes (0: no limit). A weight's host rows must
+ * not change while a copy of them is kept (dq_external_forget drops it). Calls on
+ * one dq_external are serialized; results are those of dq_matmul on the same rows. */
+typedef struct dq_external dq_external;
+
+/* MatmulShape (dynacore/include/dynacore/kernel/matmul_registry.h:87-91). */
+typedef struct dq_matmul_shape {
+  int64_t m, n, k;
+  int32_t dtype;
+  int32_t x_dense; /* x rows are contiguous (row stride == k floats) */
+} dq_matmul_shape;
+
+typedef struct dq_external_stats {
+  int64_t runs;             /* completed dq_external_run calls */
+  int64_t uploads;          /* weights copied to the device */
+  int64_t hits;             /* runs that found their weight's copy */
+  int64_t evictions;        /* copies dropped for the byte limit */
+  int64_t resident_bytes;   /* device bytes of the copies kept now */
+  int64_t resident_weights; /* copies kept now */
+} dq_external_stats;
+
+/* An adapter on GPU `device` whose eligible() accepts m >= min_rows (>= 1). */
+DQ_API int dq_external_create(int device, int64_t min_rows, int64_t max_resident_bytes, dq_external** out);
+DQ_API int dq_external_free(dq_external* e);
+/* 1 if run() takes this shape, else 0; reads no tensor data and needs no GPU
+ * (e may be NULL: min_rows 1). The rules are dq_matmul's (validate_matmul_shape,
+ * dynacore/src/kernel/matmul_registry.cpp:264-278) for the four weight types. */
+DQ_API int dq_external_eligible(const dq_external* e, const dq_matmul_shape* s, const void* weight);
+/* y[r, i] = x[r, :] . w[i, :] (+ bias[i]) for host x (m rows, x_stride floats apart),
+ * host GGUF weight rows w (n rows of k values, w_row_bytes apart), host bias (n
+ * floats or NULL) and host y (m rows, y_stride floats apart). Returns when y is
+ * written. */
+DQ_API int dq_external_run(dq_external* e, const float* x, int64_t m, int64_t x_stride, const void* w, int dtype,
+                           int64_t n, int64_t k, int64_t w_row_bytes, const float* bias, float* y, int64_t y_stride);
+/* Drops the device copies of host weight rows `weight` (DQ_NOT_FOUND if none). */
+DQ_API int dq_external_forget(dq_external* e, const void* weight);
+DQ_API int dq_external_get_stats(dq_external* e, dq_external_stats* out);
+
 /* Exact integer partials of every (activation row r < m, weight row i < n):
  * units[(r * n + i) * U + u] and sb[(r * n + i) * S + s], with U and S from
  * dq_partials_count; the meaning of each is that of the CPU reference's integer
