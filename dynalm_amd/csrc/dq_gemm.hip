@@ -552,8 +552,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
       for (int s = 0; s < 4; ++s) r[s] = lds_ld16(lds, kHL + ((tile * 4 + s) * 2 + hl) * 1024 + lane * 16);
       return std::array<v4u, 4>{r[0], r[1], r[2], r[3]};
     };
-    auto epi = [&](const Tacc& r, const Sc& c, int nt, int mt) {
-      const f4_t da = __builtin_bit_cast(f4_t, lds_ld16(lds, da_buf + da_rd + mt * 16 * 4));
+    auto epi = [&](const Tacc& r, const Sc& c, int nt, int mt, f4_t da) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int S = r.L[e] + (r.H[e] << 3);
@@ -562,14 +561,26 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
         acc[nt][mt][e] = fmaf(da[e], u, acc[nt][mt][e]);
       }
     };
+    // The two waves of a SIMD (w and w + 4) leave the barrier together; starting
+    // the second ~128 clocks later lets one wave's MFMA burst run while the other
+    // runs its epilogue (measured: -5% at M = 512 and 2048).
+    if (C::kWaves == 8 && wave >= 4) __builtin_amdgcn_s_sleep(2);
     std::array<v4u, 4> Hc = load4(NT * wn, 0), Lc = load4(NT * wn, 1), Hn, Ln;
     Tacc prev;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
+        const int pn = mt ? nt : nt - 1, pm = mt ? mt - 1 : 3;
+        // the activation scales of the previous tile's epilogue, read before this
+        // tile's MFMAs so that they have landed when the epilogue runs
+        f4_t dp = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (nt + mt > 0) dp = __builtin_bit_cast(f4_t, lds_ld16(lds, da_buf + da_rd + pm * 16 * 4));
         Tacc cur;
         const v4i_t z = {0, 0, 0, 0};
+        // a wave issuing its MFMA burst goes first, so bursts of the two waves of a
+        // SIMD do not interleave (and end together)
+        __builtin_amdgcn_s_setprio(1);
         cur.H = mfma(a[mt][0], Hc[0], z);
 #pragma unroll
         for (int s = 1; s < 4; ++s) cur.H = mfma(a[mt][s], Hc[s], cur.H);
@@ -579,16 +590,14 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
         for (int s = 1; s < 4; ++s) cur.L = mfma(a[mt][s], Lc[s], cur.L);
         cur.M = mfma_h(am[mt], sc[nt].mb, f4_t{0.0f, 0.0f, 0.0f, 0.0f});
-        if (nt + mt > 0) {
-          const int pn = mt ? nt : nt - 1, pm = mt ? mt - 1 : 3;
-          epi(prev, sc[pn], pn, pm);
-        }
+        __builtin_amdgcn_s_setprio(0);
+        if (nt + mt > 0) epi(prev, sc[pn], pn, pm, dp);
         prev = cur;
         if (mt == 3 && nt + 1 < NT) Hc = Hn;
       }
       if (nt + 1 < NT) Ln = load4(NT * wn + nt + 1, 1);
     }
-    epi(prev, sc[NT - 1], NT - 1, 3);
+    epi(prev, sc[NT - 1], NT - 1, 3, __builtin_bit_cast(f4_t, lds_ld16(lds, da_buf + da_rd + 3 * 16 * 4)));
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
