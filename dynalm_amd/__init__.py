@@ -33,7 +33,7 @@ import os
 import numpy as np
 
 __all__ = [
-    "Q4_0", "Q8_0", "Q4_K", "Q6_K", "ACT_PER32", "ACT_Q8_0", "ACT_Q8_K", "ACT_SX", "ACT_Q16", "GEMV_MAX_ROWS", "matmul_act",
+    "Q4_0", "Q8_0", "Q4_K", "Q6_K", "ACT_PER32", "ACT_Q8_0", "ACT_Q8_K", "ACT_SX", "ACT_Q16", "ACT_F32", "GEMV_MAX_ROWS", "matmul_act",
     "DqError", "lib", "lib_path", "row_bytes", "act_row_bytes", "act_format_for", "Weight",
     "act_quantize", "gemv", "gemm", "matmul", "matmul_many", "MatmulJob", "partials_count", "debug_partials",
     "SILU", "GELU", "GELU_TANH", "act_mul", "matmul_gated", "GgufFile", "GgufTensor", "EXPORTS",
@@ -41,7 +41,7 @@ __all__ = [
 ]
 
 Q4_0, Q8_0, Q4_K, Q6_K = 6, 10, 14, 16
-ACT_PER32, ACT_Q8_0, ACT_Q8_K, ACT_SX, ACT_Q16 = 0, 1, 2, 3, 4
+ACT_PER32, ACT_Q8_0, ACT_Q8_K, ACT_SX, ACT_Q16, ACT_F32 = 0, 1, 2, 3, 4, 5
 GEMV_MAX_ROWS = 16
 SILU, GELU, GELU_TANH = 0, 1, 2  # dq_activation (dynacore Activation, device/ops.h:14)
 

@@ -65,7 +65,8 @@ int hip_fail(hipError_t e, const char* what) {
 
 bool weight_type_ok(int t) { return t == DQ_Q4_0 || t == DQ_Q8_0 || t == DQ_Q4_K || t == DQ_Q6_K; }
 bool act_fmt_ok(int f) {
-  return f == DQ_ACT_PER32 || f == DQ_ACT_Q8_0 || f == DQ_ACT_Q8_K || f == DQ_ACT_SX || f == DQ_ACT_Q16;
+  return f == DQ_ACT_PER32 || f == DQ_ACT_Q8_0 || f == DQ_ACT_Q8_K || f == DQ_ACT_SX || f == DQ_ACT_Q16 ||
+         f == DQ_ACT_F32;
 }
 
 // The (weight, activation) pairs with kernels: the per-32 formats with Q8_0 / Q4_0
@@ -73,6 +74,7 @@ bool act_fmt_ok(int f) {
 // int16 with Q8_0, Q4_K and Q6_K (the types dynacore has int16 kernels for,
 // dynacore/cpu/avx2/kernels_avx2.cpp:1957-1960).
 bool pair_ok(int t, int f) {
+  if (f == DQ_ACT_F32) return true;  // every weight type has an fp32 row kernel (vec_dot_*)
   if (f == DQ_ACT_Q16) return t == DQ_Q8_0 || t == DQ_Q4_K || t == DQ_Q6_K;
   if (t == DQ_Q8_0 || t == DQ_Q4_0) return f == DQ_ACT_PER32 || f == DQ_ACT_Q8_0;
   return f == DQ_ACT_Q8_K || f == DQ_ACT_SX || f == DQ_ACT_PER32;
@@ -357,6 +359,12 @@ int dq_act_quantize(int fmt, const float* x, int64_t m, int64_t k, int64_t x_str
   if (m > 1 && x_stride < k) return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)k);
   if (k * 4 >= ((int64_t)1 << 32) || m > 65535) return fail(DQ_UNSUPPORTED, "activation shape too large");
   if (reinterpret_cast<uintptr_t>(out) % 4 != 0) return fail(DQ_INVALID_ARGUMENT, "out must be 4-byte aligned");
+  if (fmt == DQ_ACT_F32) {  // no quantization: the rows, densely
+    DQ_HIP(hipMemcpy2DAsync(out, (size_t)orb, x, (size_t)(m > 1 ? x_stride : k) * 4, (size_t)orb, (size_t)m,
+                            hipMemcpyDeviceToDevice, as_stream(stream)),
+           "row copy");
+    return DQ_OK;
+  }
   DQ_HIP(dq::launch_quantize(fmt, x, m, k, x_stride, static_cast<uint8_t*>(out), orb, as_stream(stream)),
          "quantize launch");
   return DQ_OK;
@@ -577,6 +585,15 @@ int dq_matmul_act(const dq_weight* w, int fmt, const float* x, int64_t m, int64_
   const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
   if (arb < 0) return fail(DQ_INVALID_ARGUMENT, "k %lld is not a multiple of the activation block", (long long)w->dev.k);
   hipStream_t s = as_stream(stream);
+  if (fmt == DQ_ACT_F32) {
+    // fp32 activations: the GEMV reads the caller's rows in place
+    const int64_t xrb = (m > 1 ? x_stride : w->dev.k) * 4;
+    if (m * xrb >= ((int64_t)1 << 32)) return fail(DQ_UNSUPPORTED, "activations exceed 4 GiB");
+    DQ_HIP(dq::launch_gemv(w->dev, fmt, reinterpret_cast<const uint8_t*>(x), xrb, m, 0, w->dev.n, y, y_stride, bias,
+                           nullptr, s),
+           "gemv launch");
+    return DQ_OK;
+  }
   void* acts = nullptr;
   if (int rc = scratch_get(w->dev.device, (size_t)(m * arb), s, &acts); rc != DQ_OK) return rc;
   if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, acts, stream); rc != DQ_OK) return rc;
@@ -587,7 +604,7 @@ int dq_matmul_act(const dq_weight* w, int fmt, const float* x, int64_t m, int64_
 }
 
 int dq_partials_count(int dtype, int fmt, int64_t k, int64_t* units, int64_t* sb_terms) {
-  if (!weight_type_ok(dtype) || !act_fmt_ok(fmt) || !pair_ok(dtype, fmt)) {
+  if (!weight_type_ok(dtype) || !act_fmt_ok(fmt) || !pair_ok(dtype, fmt) || fmt == DQ_ACT_F32) {
     return fail(DQ_UNSUPPORTED, "unsupported pair (%d, %d)", dtype, fmt);
   }
   if (dq_row_bytes(dtype, k) < 0 || dq_act_row_bytes(fmt, k) < 0) return fail(DQ_INVALID_ARGUMENT, "bad k");

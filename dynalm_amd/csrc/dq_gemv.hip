@@ -144,8 +144,29 @@ constexpr int kStageQ8K = 336;
 constexpr int kStageSX = 352;
 constexpr int kStage32 = 48;
 constexpr int kStage16 = 80;
+constexpr int kStageF32 = 144;
 // Staged bytes per 32-value block of the per-32 activation formats.
-constexpr int stage_b32(int af) { return af == kActQ16 ? kStage16 : kStage32; }
+constexpr int stage_b32(int af) { return af == kActQ16 ? kStage16 : af == kActF32 ? kStageF32 : kStage32; }
+
+// fp32 activations (the reference's kF32 contract, dynacore/cpu/generic/kernels_generic.cpp:67-150):
+// a staged 32-value block is the 32 floats @0 and their sum, added in index order, @128.
+// The four bytes of a dword as floats (v_cvt_f32_ubyte0..3).
+DQ_DEV void ubytes_f32(u32 w, float* f) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) f[e] = (float)((w >> (8 * e)) & 0xFFu);
+}
+// dot + sum_{i < n} q[i] * x[i] in index order, x from a staged block (wave-uniform
+// LDS address: broadcast reads); every product and sum rounds where written.
+template <int N>
+DQ_DEV float dot_f32(float dot, const float* q, const uint8_t* x) {
+#pragma unroll
+  for (int i = 0; i < N; i += 4) {
+    const v4u xv = *reinterpret_cast<const v4u*>(x + 4 * i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dot = dot + q[i + e] * as_f(xv[e]);
+  }
+  return dot;
+}
 // Staged bytes per super-block of the 256-value activation formats.
 constexpr int stage_sb(int af) { return af == kActSX ? kStageSX : kStageQ8K; }
 
@@ -190,6 +211,37 @@ DQ_DEV void compute(const Chunk<kQ4_K, U>& ch, int bb, const uint8_t* st, Out<M>
     const u32 mn_lo = s1 & 0x3F3F3F3Fu;
     const u32 mn_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
     const float d = h2f(ch.hd[u].x), dmin = h2f(ch.hd[u].x >> 16);
+    if constexpr (AF == kActF32) {
+      // vec_dot_q4_K (kernels_generic.cpp:108-130): per 64 values, dot_lo / sum_lo over
+      // the low nibbles (sub-block 2jp) and dot_hi / sum_hi over the high ones (2jp + 1),
+      // then sum += d*sc*dot - dmin*m*sum_x for each
+#pragma unroll
+      for (int jp = 0; jp < 4; ++jp) {
+        float qlo[32], qhi[32];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const v4u c = ch.q[u][2 * jp + h];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            ubytes_f32(c[w] & 0x0F0F0F0Fu, qlo + 16 * h + 4 * w);
+            ubytes_f32(((c[w] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u, qhi + 16 * h + 4 * w);
+          }
+        }
+        const u32 scw = jp < 2 ? sc_lo : sc_hi, mnw = jp < 2 ? mn_lo : mn_hi;
+        const int e = 16 * (jp & 1);
+        const float sl = (float)bfe(scw, e, 6), sh = (float)bfe(scw, e + 8, 6);
+        const float ml = (float)bfe(mnw, e, 8), mh = (float)bfe(mnw, e + 8, 8);
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+          const uint8_t* al = st + (mm * o.nblk * 8 + b * 8 + 2 * jp) * kStageF32;
+          const uint8_t* ah = al + kStageF32;
+          const float dlo = dot_f32<32>(0.0f, qlo, al), dhi = dot_f32<32>(0.0f, qhi, ah);
+          o.acc[mm] = o.acc[mm] + ((d * sl) * dlo - (dmin * ml) * as_f(lds4(al + 128)));
+          o.acc[mm] = o.acc[mm] + ((d * sh) * dhi - (dmin * mh) * as_f(lds4(ah + 128)));
+        }
+      }
+      continue;
+    }
 #pragma unroll
     for (int mm = 0; mm < M; ++mm) {
       if (AF == kActQ8_K) {
@@ -308,6 +360,34 @@ DQ_DEV void compute(const Chunk<kQ6_K, U>& ch, int bb, const uint8_t* st, Out<M>
     if (u >= nv) break;
     const int b = bb + u;
     const float d = h2f(ch.DW[u]);
+    if constexpr (AF == kActF32) {
+      // vec_dot_q6_K (kernels_generic.cpp:132-150): per 16-value unit u (values 16u ..
+      // 16u + 15) s_u = sum (q - 32) x in index order; sum += d*sc_u*s_u, units in order.
+      // ql chunk c: half p = c/4, values 128p + 16(c%4) + i (low nibbles) and + 64
+      // (high); top bits from qh chunk 2p + c%2, bit pairs s and s+2 (s = (c%4)/2).
+#pragma unroll
+      for (int uu = 0; uu < 16; ++uu) {
+        const int p = uu >> 3, cc = uu & 3, c = 4 * p + cc, sh = cc >> 1;
+        const v4u hb = ch.H[u][2 * p + (c & 1)];
+        const v4u qv = (uu & 4) ? ((ch.L[u][c] >> 4) & 0x0F0F0F0Fu) | (((hb >> (2 * sh + 4)) & 0x03030303u) << 4)
+                                : (ch.L[u][c] & 0x0F0F0F0Fu) | (((hb >> (2 * sh)) & 0x03030303u) << 4);
+        float q[16];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          ubytes_f32(qv[w], q + 4 * w);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) q[4 * w + e] = q[4 * w + e] - 32.0f;
+        }
+        const u32 sw = uu < 4 ? ch.SC[u].x : uu < 8 ? ch.SC[u].y : uu < 12 ? ch.SC[u].z : ch.SC[u].w;
+        const float ds = d * (float)sbfe(sw, 8 * (uu & 3), 8);
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+          const uint8_t* ab = st + (mm * o.nblk * 8 + b * 8 + uu / 2) * kStageF32 + 64 * (uu & 1);
+          o.acc[mm] = o.acc[mm] + ds * dot_f32<16>(0.0f, q, ab);
+        }
+      }
+      continue;
+    }
     // ql chunk c: half p = c/4, values 128p + 16(c%4) + i (low nibbles) and + 64
     // (high); their top bits are qh chunk 2p + c%2 at bit pairs s and s+2,
     // s = (c%4)/2 (quant_formats.cpp:192-216). Units u_lo = 8p + c%4, u_hi = u_lo + 4.
@@ -402,6 +482,52 @@ DQ_DEV void compute32(const Chunk32<WT, U>& ch, int bb, const uint8_t* st, Out<M
     if (u >= nv) break;
     const int b = bb + u;
     const float dw = h2f(ch.DW[u]);
+    if constexpr (AF == kActF32) {
+      float q[32];
+      if (WT == kQ8_0) {
+        // vec_dot_q8_0 (kernels_generic.cpp:67-76): s = sum q x in index order
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[16 * c + 4 * w + e] = (float)(int)sbfe(ch.q[u][c][w], 8 * e, 8);
+      } else {
+        // vec_dot_q4_0 (kernels_generic.cpp:78-90): for j < 16 the low nibble of byte j
+        // (value j) and then its high nibble (value j + 16) go into one sum
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          float lo[4], hi[4];
+          ubytes_f32(ch.q[u][0][w] & 0x0F0F0F0Fu, lo);
+          ubytes_f32((ch.q[u][0][w] >> 4) & 0x0F0F0F0Fu, hi);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            q[2 * (4 * w + e)] = lo[e] - 8.0f;
+            q[2 * (4 * w + e) + 1] = hi[e] - 8.0f;
+          }
+        }
+      }
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) {
+        const uint8_t* ab = st + (mm * o.nblk + b) * kStageF32;
+        float sum = 0.0f;
+        if (WT == kQ8_0) {
+          sum = dot_f32<32>(0.0f, q, ab);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 16; j += 4) {
+            const v4u xl = *reinterpret_cast<const v4u*>(ab + 4 * j), xh = *reinterpret_cast<const v4u*>(ab + 64 + 4 * j);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              sum = sum + q[2 * (j + e)] * as_f(xl[e]);
+              sum = sum + q[2 * (j + e) + 1] * as_f(xh[e]);
+            }
+          }
+        }
+        o.acc[mm] = o.acc[mm] + dw * sum;
+      }
+      continue;
+    }
 #pragma unroll
     for (int mm = 0; mm < M; ++mm) {
       if (AF == kActQ16) {
@@ -498,6 +624,26 @@ DQ_DEV void stage_acts(const uint8_t* __restrict__ acts, int64_t arb, int nblk, 
         *reinterpret_cast<u32*>(o + (r == 0 ? 0 : 16 + 4 * (r - 1))) = v[mm][0];
         if (r < 9) *reinterpret_cast<u32*>(o + (r == 0 ? 16 + 4 * 63 : 272 + 4 * (r - 1))) = v[mm][1];
         if (r >= 1 && r < 9) stage_subsum(o, r - 1, bsum_pair(v[mm][1]));
+      }
+    }
+  } else if constexpr (AF == kActF32) {
+    // lane r: one 32-value block of fp32 values per round, and their sum in index order
+    for (int blk = b0 * bpu + r; blk < b1 * bpu; blk += 64) {
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) {
+        const u32 base = (u32)(mm * arb + (int64_t)blk * 128);
+        v4u w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = ld16(ra, base + 16 * i);
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sum = sum + as_f(w[i][e]);
+        uint8_t* o = st + (mm * nblk * bpu + blk) * kStageF32;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *reinterpret_cast<v4u*>(o + 16 * i) = w[i];
+        *reinterpret_cast<v4u*>(o + 128) = v4u{as_u(sum), 0u, 0u, 0u};
       }
     }
   } else if constexpr (AF == kActQ16) {
@@ -728,8 +874,8 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr bool kSb = AF == kActQ8_K || AF == kActSX;
   static_assert(!kGated || (kSb && M == 1 && kFuse), "the gated GEMV takes one fp32 row and K-quant weights");
-  static_assert((AF != kActSX && AF != kActQ16) || (!kFuse && kEarly == 0),
-                "sub-scaled and int16 activations arrive quantized and staged by loops");
+  static_assert((AF != kActSX && AF != kActQ16 && AF != kActF32) || (!kFuse && kEarly == 0),
+                "sub-scaled, int16 and fp32 activations arrive ready and are staged by loops");
   // LDS: Q8_K t-terms [M][nblk][64] + da [M][nblk]  |  per-32 slice sums [W][M][64];
   // then the staged activation rows [M][nblk (blocks of 32 for per-32)][stage bytes].
   // kGated: one t-term region and one stage region per weight.
@@ -929,7 +1075,7 @@ static hipError_t gemv_early(const WeightDev& w, const uint8_t* acts, int64_t ar
   if constexpr (M == 1 && AF == kActQ8_K) {
     if (per_wave == 1) return gemv_launch<WT, AF, M, kFuse, W, 1>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
     if (per_wave == 2) return gemv_launch<WT, AF, M, kFuse, W, 2>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
-  } else if constexpr (M == 1 && !kFuse && AF != kActSX && AF != kActQ16) {
+  } else if constexpr (M == 1 && !kFuse && AF != kActSX && AF != kActQ16 && AF != kActF32) {
     const int64_t bpu = WT == kQ4_K || WT == kQ6_K ? 8 : 1;
     if (per_wave * bpu <= 64) {
       return gemv_launch<WT, AF, M, kFuse, W, 1>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
@@ -967,18 +1113,22 @@ static hipError_t gemv_pass(const WeightDev& w, int af, const uint8_t* acts, int
     case kQ4_K:
       if (af == kActSX) return gemv_waves<kQ4_K, kActSX, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
       if (af == kActQ16) return gemv_waves<kQ4_K, kActQ16, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+      if (af == kActF32) return gemv_waves<kQ4_K, kActF32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
       return af == kActQ8_K ? gemv_waves<kQ4_K, kActQ8_K, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
                             : gemv_waves<kQ4_K, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
     case kQ6_K:
       if (af == kActSX) return gemv_waves<kQ6_K, kActSX, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
       if (af == kActQ16) return gemv_waves<kQ6_K, kActQ16, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+      if (af == kActF32) return gemv_waves<kQ6_K, kActF32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
       return af == kActQ8_K ? gemv_waves<kQ6_K, kActQ8_K, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
                             : gemv_waves<kQ6_K, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
     case kQ8_0:
       if (af == kActQ16) return gemv_waves<kQ8_0, kActQ16, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+      if (af == kActF32) return gemv_waves<kQ8_0, kActF32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
       return af == kActPer32 ? gemv_waves<kQ8_0, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
                              : gemv_waves<kQ8_0, kActQ8_0, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
     default:
+      if (af == kActF32) return gemv_waves<kQ4_0, kActF32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
       return af == kActPer32 ? gemv_waves<kQ4_0, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
                              : gemv_waves<kQ4_0, kActQ8_0, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
   }
@@ -990,10 +1140,13 @@ static hipError_t gemv_rows(const WeightDev& w, int af, const uint8_t* acts, int
                             int64_t m, int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
                             hipStream_t s) {
   const int paf = x != nullptr ? (w.dtype == kQ4_K || w.dtype == kQ6_K ? kActQ8_K : kActPer32) : af;
-  const bool can8 = gemv_lds_bytes(w.dtype, paf, 8, 8, w.nblk, false) <= kGemvMaxLds;
+  // rows per pass: 8, 4, 2 or 1, the most whose staged activations fit the LDS
+  int pmax = 8;
+  while (pmax > 1 && gemv_lds_bytes(w.dtype, paf, pmax, 16, w.nblk, false) > kGemvMaxLds) pmax /= 2;
   for (int64_t r0 = 0; r0 < m;) {
     const int64_t left = m - r0;
-    const int rows = left >= 8 && can8 ? 8 : (int)(left < 4 ? left : 4);
+    const int cap = pmax < 4 ? pmax : 4;
+    const int rows = left >= 8 && pmax >= 8 ? 8 : (int)(left < cap ? left : cap);
     const uint8_t* a = acts ? acts + r0 * arb : nullptr;
     const float* xx = x ? x + r0 * xs : nullptr;
     float* yy = y + r0 * ys;

@@ -40,7 +40,7 @@
 namespace dq {
 
 enum : int { kQ4_0 = 6, kQ8_0 = 10, kQ4_K = 14, kQ6_K = 16 };
-enum : int { kActPer32 = 0, kActQ8_0 = 1, kActQ8_K = 2, kActSX = 3, kActQ16 = 4 };
+enum : int { kActPer32 = 0, kActQ8_0 = 1, kActQ8_K = 2, kActSX = 3, kActQ16 = 4, kActF32 = 5 };
 
 constexpr int kRowGroup = 64;
 constexpr int kMaxPlanes = 4;
@@ -90,10 +90,11 @@ DQ_HD int64_t plane_offset(int t, int p, int64_t n, int64_t b, int64_t nblk, int
 }
 
 DQ_HD int act_block_elems(int f) {
-  return (f == kActQ8_K || f == kActSX) ? 256 : (f == kActPer32 || f == kActQ8_0 || f == kActQ16) ? 32 : -1;
+  return (f == kActQ8_K || f == kActSX) ? 256 : (f == kActPer32 || f == kActQ8_0 || f == kActQ16 || f == kActF32) ? 32 : -1;
 }
 DQ_HD int act_block_bytes(int f) {
-  return f == kActPer32 ? 40 : f == kActQ8_0 ? 34 : f == kActQ8_K ? 292 : f == kActSX ? 320 : f == kActQ16 ? 72 : -1;
+  return f == kActPer32 ? 40 : f == kActQ8_0 ? 34 : f == kActQ8_K ? 292 : f == kActSX ? 320 : f == kActQ16 ? 72
+         : f == kActF32 ? 128 : -1;
 }
 
 }  // namespace dq

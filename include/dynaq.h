@@ -90,13 +90,21 @@ typedef enum dq_dtype {
  *                 even (saturated to int16), sum = the sum of the codes
  *                 (dynacore/include/dynacore/cpu/cpu_kernels.h:72-82,
  *                  dynacore/cpu/avx2/kernels_avx2.cpp:1631-1652). With Q8_0, Q4_K and Q6_K;
- *                 the kernels form each 32-value (Q6_K: 16-value) integer dot exactly. */
+ *                 the kernels form each 32-value (Q6_K: 16-value) integer dot exactly;
+ *   DQ_ACT_F32    no quantization: fp32 rows of k floats (4k bytes), dynacore's kF32
+ *                 contract (f32_row_dot, the reference-accuracy fallback and x86 prefill
+ *                 default, dynacore/src/kernel/matmul_registry.cpp:51-54) with the arithmetic
+ *                 of vec_dot_* (dynacore/cpu/generic/kernels_generic.cpp:67-150): each
+ *                 block's fp32 dot in index order, scaled and added block by block. With
+ *                 every weight type; dq_act_quantize copies the rows, there are no integer
+ *                 partials. */
 typedef enum dq_act_format {
   DQ_ACT_PER32 = 0,
   DQ_ACT_Q8_0 = 1,
   DQ_ACT_Q8_K = 2,
   DQ_ACT_SX = 3,
   DQ_ACT_Q16 = 4,
+  DQ_ACT_F32 = 5,
 } dq_act_format;
 
 /* Activation rows at or below which dq_matmul runs the GEMV kernels. */

@@ -44,7 +44,7 @@ int64_t dqo_row_bytes(int dtype, int64_t k) {
 
 int64_t dqo_act_block_elems(int fmt) {
   switch (fmt) {
-    case DQO_ACT_PER32: case DQO_ACT_Q8_0: case DQO_ACT_Q16: return 32;
+    case DQO_ACT_PER32: case DQO_ACT_Q8_0: case DQO_ACT_Q16: case DQO_ACT_F32: return 32;
     case DQO_ACT_Q8_K: case DQO_ACT_SX: return 256;
     default: return -1;
   }
@@ -57,6 +57,7 @@ static int64_t act_block_bytes(int fmt) {
     case DQO_ACT_Q8_K: return 292;  /* quant_formats.h:30 */
     case DQO_ACT_SX: return 320;    /* cpu_kernels.h:62-69 */
     case DQO_ACT_Q16: return 72;    /* cpu_kernels.h:77-82 */
+    case DQO_ACT_F32: return 128;   /* 32 floats */
     default: return -1;
   }
 }
@@ -253,6 +254,7 @@ int dqo_dequantize_act(int fmt, const void* a, float* y, int64_t n) {
         for (int j = 0; j < 32; ++j) y[j] = d * (float)rd16s(b + 8 + 2 * j);
         break;
       }
+      case DQO_ACT_F32: memcpy(y, b, 128); break;
       default: return -1;
     }
   }
@@ -389,6 +391,7 @@ int dqo_quantize_act(int fmt, const float* x, void* out, int64_t n) {
       case DQO_ACT_Q8_K: quantize_q8_K_block(x, o); break;
       case DQO_ACT_SX: quantize_sx_block(x, o); break;
       case DQO_ACT_Q16: quantize_q16_block(x, o); break;
+      case DQO_ACT_F32: memcpy(o, x, 128); break;
       default: return -1;
     }
   }
@@ -538,6 +541,7 @@ int dqo_encode_weight_rows(int dtype, const float* x, int64_t rows, int64_t n, v
 /* ------------------------------------------------------------- partials */
 
 static int pair_ok(int wtype, int fmt) {
+  if (fmt == DQO_ACT_F32) return 0; /* no integer partials; the dots have their own path */
   if (fmt == DQO_ACT_Q16) return wtype == DQO_Q8_0 || wtype == DQO_Q4_K || wtype == DQO_Q6_K;
   switch (wtype) {
     case DQO_Q8_0: case DQO_Q4_0: return fmt == DQO_ACT_PER32 || fmt == DQO_ACT_Q8_0;
@@ -659,7 +663,77 @@ int dqo_partials(int wtype, int fmt, const void* wrow, const void* arow, int64_t
 
 /* ------------------------------------------------------------------ dots */
 
+/* fp32 activations: the generic vec_dot_* (kernels_generic.cpp:67-150), every fp32
+ * operation rounding where written (the generic tier has no FMA contraction). */
+static float vec_dot_f32(int wtype, const uint8_t* w, const float* x, int64_t k) {
+  float sum = 0.0f;
+  if (wtype == DQO_Q8_0 || wtype == DQO_Q4_0) {
+    const int64_t bb = wtype == DQO_Q8_0 ? 34 : 18;
+    for (int64_t i = 0; i < k / 32; ++i, x += 32) {
+      const uint8_t* b = w + i * bb;
+      float s = 0.0f;
+      if (wtype == DQO_Q8_0) {
+        for (int j = 0; j < 32; ++j) s = s + (float)(int8_t)b[2 + j] * x[j];
+      } else {
+        for (int j = 0; j < 16; ++j) {
+          s = s + (float)((b[2 + j] & 0x0F) - 8) * x[j];
+          s = s + (float)((b[2 + j] >> 4) - 8) * x[j + 16];
+        }
+      }
+      sum = sum + dqo_fp16_to_fp32(rd16(b)) * s;
+    }
+    return sum;
+  }
+  for (int64_t i = 0; i < k / 256; ++i) {
+    if (wtype == DQO_Q4_K) {
+      const uint8_t* b = w + i * 144;
+      const float d = dqo_fp16_to_fp32(rd16(b)), dmin = dqo_fp16_to_fp32(rd16(b + 2));
+      const uint8_t* q = b + 16;
+      for (int j = 0, is = 0; j < 256; j += 64, is += 2, q += 32, x += 64) {
+        uint8_t sc, m;
+        float dot_lo = 0.0f, sum_lo = 0.0f, dot_hi = 0.0f, sum_hi = 0.0f;
+        for (int l = 0; l < 32; ++l) {
+          dot_lo = dot_lo + (float)(q[l] & 0xF) * x[l];
+          sum_lo = sum_lo + x[l];
+          dot_hi = dot_hi + (float)(q[l] >> 4) * x[l + 32];
+          sum_hi = sum_hi + x[l + 32];
+        }
+        dqo_scale_min_k4(is, b + 4, &sc, &m);
+        sum = sum + ((d * (float)sc) * dot_lo - (dmin * (float)m) * sum_lo);
+        dqo_scale_min_k4(is + 1, b + 4, &sc, &m);
+        sum = sum + ((d * (float)sc) * dot_hi - (dmin * (float)m) * sum_hi);
+      }
+    } else { /* Q6_K */
+      const uint8_t* b = w + i * 210;
+      const float d = dqo_fp16_to_fp32(rd16(b + 208));
+      const uint8_t* ql = b;
+      const uint8_t* qh = b + 128;
+      const int8_t* sc = (const int8_t*)(b + 192);
+      for (int part = 0; part < 2; ++part, ql += 64, qh += 32, sc += 8, x += 128) {
+        float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int l = 0; l < 32; ++l) {
+          const int is = l / 16;
+          const int q1 = ((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+          const int q2 = ((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+          const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+          const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+          s[is + 0] = s[is + 0] + (float)q1 * x[l];
+          s[is + 2] = s[is + 2] + (float)q2 * x[l + 32];
+          s[is + 4] = s[is + 4] + (float)q3 * x[l + 64];
+          s[is + 6] = s[is + 6] + (float)q4 * x[l + 96];
+        }
+        for (int g = 0; g < 8; ++g) sum = sum + (d * (float)sc[g]) * s[g];
+      }
+    }
+  }
+  return sum;
+}
+
 float dqo_dot(int wtype, int fmt, const void* wrow, const void* arow, int64_t k) {
+  if (fmt == DQO_ACT_F32) {
+    if (dqo_row_bytes(wtype, k) < 0 || k % 32 != 0) return NAN;
+    return vec_dot_f32(wtype, (const uint8_t*)wrow, (const float*)arow, k);
+  }
   if (!pair_ok(wtype, fmt) || dqo_row_bytes(wtype, k) < 0 || dqo_act_row_bytes(fmt, k) < 0) return NAN;
   const uint8_t* w = (const uint8_t*)wrow;
   const uint8_t* a = (const uint8_t*)arow;
@@ -796,7 +870,7 @@ float dqo_dot(int wtype, int fmt, const void* wrow, const void* arow, int64_t k)
 
 int dqo_matmul(int wtype, int fmt, const void* w, int64_t w_row_bytes, int64_t n, const void* acts,
                int64_t a_row_bytes, int64_t m, int64_t k, float* y, int64_t y_stride, const float* bias) {
-  if (!pair_ok(wtype, fmt) || dqo_row_bytes(wtype, k) < 0 || dqo_act_row_bytes(fmt, k) < 0) return -1;
+  if ((fmt != DQO_ACT_F32 && !pair_ok(wtype, fmt)) || dqo_row_bytes(wtype, k) < 0 || dqo_act_row_bytes(fmt, k) < 0) return -1;
   for (int64_t r = 0; r < m; ++r) {
     for (int64_t i = 0; i < n; ++i) {
       const float v = dqo_dot(wtype, fmt, (const uint8_t*)w + i * w_row_bytes, (const uint8_t*)acts + r * a_row_bytes, k);

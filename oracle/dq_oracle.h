@@ -65,6 +65,7 @@ enum {
   DQO_ACT_Q8_K = 2,  /* BlockQ8_K {float d; int8 q[256]; int16 bsums[16]}, 292 B / 256 (quant_formats.h:30) */
   DQO_ACT_SX = 3,    /* ActSuperQ8 sub-scaled, 320 B / 256 (cpu_kernels.h:62-70) */
   DQO_ACT_Q16 = 4,   /* ActBlockQ16 {float d; int32 sum; int16 q[32]}, 72 B / 32 (cpu_kernels.h:72-82) */
+  DQO_ACT_F32 = 5,   /* no quantization: fp32 rows (the kF32 contract, vec_dot_*) */
 };
 
 int64_t dqo_block_elems(int dtype);

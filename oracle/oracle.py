@@ -20,9 +20,9 @@ ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libdynacore_ref.so")
 
 Q4_0, Q8_0, Q4_K, Q6_K, Q8_K = 6, 10, 14, 16, 17
-ACT_PER32, ACT_Q8_0, ACT_Q8_K, ACT_SX, ACT_Q16 = 0, 1, 2, 3, 4
+ACT_PER32, ACT_Q8_0, ACT_Q8_K, ACT_SX, ACT_Q16, ACT_F32 = 0, 1, 2, 3, 4, 5
 TYPE_NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_K", Q6_K: "q6_K", Q8_K: "q8_K"}
-ACT_NAMES = {ACT_PER32: "per32", ACT_Q8_0: "q8_0", ACT_Q8_K: "q8_K", ACT_SX: "sx", ACT_Q16: "q16"}
+ACT_NAMES = {ACT_PER32: "per32", ACT_Q8_0: "q8_0", ACT_Q8_K: "q8_K", ACT_SX: "sx", ACT_Q16: "q16", ACT_F32: "f32"}
 
 _P = C.c_void_p
 _I64 = C.c_int64
@@ -262,6 +262,7 @@ def ref():
             "ref_quantize_act16": (C.c_int, [_P, _P, _I64]),
             "ref_split_act16": (C.c_int, [_P, _P, _I64]),
             "ref_dot_rows16": (C.c_int, [C.c_int, _P, _P, _I64, C.c_int, _I64, _P]),
+            "ref_vec_dot": (C.c_int, [C.c_int, C.c_int, _P, _P, _I64, _P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(r, name)
@@ -335,3 +336,13 @@ def ref_dot_rows16(dtype: int, w_row: np.ndarray, acts: np.ndarray, k: int) -> n
     out = np.empty(m, np.float32)
     _check(r.ref_dot_rows16(dtype, _ptr(w_row), _ptr(acts), acts.shape[1], m, k, _ptr(out)), "ref_dot_rows16")
     return out
+
+
+def ref_vec_dot(tier: int, dtype: int, w_row: np.ndarray, x: np.ndarray, k: int) -> float:
+    """The reference's fp32-activation vec_dot (tier 0 generic, 1 AVX2) of one row."""
+    r = ref()
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8).ravel()
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.empty(1, np.float32)
+    _check(r.ref_vec_dot(tier, dtype, _ptr(w_row), _ptr(x), k, _ptr(out)), "ref_vec_dot")
+    return float(out[0])

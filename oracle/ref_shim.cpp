@@ -10,6 +10,7 @@
 //   dynacore/cpu/avx2/kernels_avx2.cpp:610-1440             AVX2 quantizers and dots
 //   dynacore/cpu/avx2/kernels_avx2.cpp:1631-1765            quantize_act16, dot_rows16_*
 //   dynacore/cpu/generic/kernels_generic.cpp:334-346        split_act16
+//   dynacore/cpu/generic/kernels_generic.cpp:67-150         vec_dot_* (fp32 activations)
 //   dynacore/include/dynacore/base/fast_exp.h:16-35         exp_nonpos (SiLU)
 // Used to pin the C oracle (tests) and, on the GPU box, as the timed CPU
 // baseline ("reference" kind) of bench.py.
@@ -130,6 +131,17 @@ int ref_split_act16(const void* in, void* out, int64_t nblocks) {
   const CpuKernels& k = generic_table();
   if (!k.split_act16) return -1;
   k.split_act16(static_cast<const ActBlockQ16*>(in), static_cast<ActBlockQ16S*>(out), nblocks);
+  return 0;
+}
+
+// fp32 activations: vec_dot of one weight row and one fp32 row (tier 0 generic,
+// 1 AVX2; kernels_generic.cpp:67-150, kernels_avx2.cpp:240-364).
+int ref_vec_dot(int tier, int dtype, const void* w, const float* x, int64_t k, float* out) {
+  if (!valid_type(dtype) || dtype == 17) return -1;
+  const CpuKernels& t = tier ? avx2_table() : generic_table();
+  VecDotFn fn = t.vec_dot_for(static_cast<DType>(dtype));
+  if (!fn) return -2;
+  *out = fn(w, x, k);
   return 0;
 }
 

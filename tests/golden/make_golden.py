@@ -21,6 +21,8 @@ only (data, no code):
                codes); split_q16 their split_act16 bytes (kernels_generic.cpp:334-346)
   q16dot_<t>   AVX2 dot_rows16_<t> (kernels_avx2.cpp:1662-1765) on act_q16, t in
                q8_0, q4_K, q6_K
+  vecdot_<t>   generic vec_dot_<t> (kernels_generic.cpp:67-150) of the w_<t> rows and the
+               fp32 act_x rows (the kF32 contract, no activation quantization)
 """
 from __future__ import annotations
 
@@ -125,6 +127,11 @@ def main() -> None:
         w = out[f"w_{name}"]
         dots = [O.ref_dot_rows16(t, w[i], out["act_q16"][r0:r0 + 4], K) for i in range(3) for r0 in (0, 4)]
         out[f"q16dot_{name}"] = np.stack([np.concatenate(dots[2 * i:2 * i + 2]) for i in range(3)], 1)
+
+    for t in TYPES:
+        name = O.TYPE_NAMES[t]
+        out[f"vecdot_{name}"] = np.array([[O.ref_vec_dot(0, t, out[f"w_{name}"][i], x[r], K) for i in range(3)]
+                                          for r in range(ROWS)], np.float32)
 
     rng = np.random.default_rng(20261202)
     ex = np.concatenate([

@@ -63,6 +63,12 @@ def test_sizes():
     assert dq.partials_count(dq.Q8_0, dq.ACT_Q16, 4096) == (128, 0)
     with pytest.raises(dq.DqError):
         dq.partials_count(dq.Q4_0, dq.ACT_Q16, 256)  # no int16 kernel for Q4_0 in the reference either
+    # fp32 activations (the kF32 contract): the rows themselves, no integer partials
+    assert dq.act_row_bytes(dq.ACT_F32, 4096) == 4096 * 4
+    assert dq.act_row_bytes(dq.ACT_F32, 100) == -1
+    with pytest.raises(dq.DqError) as e:
+        dq.partials_count(dq.Q4_K, dq.ACT_F32, 256)
+    assert e.value.status == "unsupported"
 
 
 def _upload_status(dtype, n, k, row_bytes):

@@ -948,3 +948,74 @@ def test_gemv_q16_ffn_down_size(cuda, t):
     a = O.quantize_act(O.ACT_Q16, x)
     exact, mag = _q16_bound(t, rows, a, k)
     assert np.all(np.abs(y - exact) <= 1e-5 * mag)
+
+
+# ------------------------------------- fp32 activations (the kF32 contract)
+
+
+def _f32_bound(t: int, rows: np.ndarray, x: np.ndarray, k: int) -> tuple[np.ndarray, np.ndarray]:
+    wf = O.dequantize(t, rows, k).astype(np.float64)
+    xf = x.astype(np.float64)
+    return xf @ wf.T, np.abs(xf) @ np.abs(wf).T
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", list(O.TYPE_NAMES)[:4], ids=lambda t: O.TYPE_NAMES[t])
+@pytest.mark.parametrize("m", [1, 3, 4, 5, 8, 11])
+def test_gemv_f32_parity(cuda, t, m):
+    """vec_dot_* arithmetic on the GPU: each block's fp32 dot in index order, blocks
+    added per wave slice and slices in order, so only the cross-slice additions differ
+    from the oracle's (the reference generic order): within 2e-6 of the sum of |terms| of
+    the oracle and 1e-5 of the exact product; dq_act_quantize copies the rows."""
+    from dynalm_amd import torch_ops as T
+
+    k, n = 1280, 200
+    rows = weight_rows(t, n, k, 1950 + m, edge=True)
+    x = activations(m, k, 1960 + m)
+    w = dq.Weight.upload(t, rows, k)
+    a = T.quantize(O.ACT_F32, dev(x))
+    assert np.array_equal(host(a).view(np.float32), x)
+    y = host(T.gemv(w, O.ACT_F32, a))
+    want = O.matmul(t, O.ACT_F32, rows, O.quantize_act(O.ACT_F32, x), k)
+    exact, mag = _f32_bound(t, rows, x, k)
+    assert np.all(np.abs(y.astype(np.float64) - want) <= 2e-6 * mag + 1e-30)
+    assert np.all(np.abs(y - exact) <= 1e-5 * mag + 1e-30)
+    # dq_matmul_act reads strided rows in place and adds the bias
+    xs = np.zeros((m, k + 5), np.float32)
+    xs[:, :k] = x
+    bias = O.normal(1970 + m, n)
+    ya = host(T.matmul_act(w, O.ACT_F32, dev(xs)[:, :k], bias=dev(bias)))
+    assert np.array_equal(ya.view(np.uint32), (y + bias).view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", list(O.TYPE_NAMES)[:4], ids=lambda t: O.TYPE_NAMES[t])
+def test_gemv_f32_vs_reference_golden(cuda, t):
+    """Against the reference's own generic vec_dot outputs (golden vecdot_*)."""
+    from dynalm_amd import torch_ops as T
+
+    gold = _gold()
+    name = O.TYPE_NAMES[t]
+    rows = gold[f"w_{name}"]
+    w = dq.Weight.upload(t, rows, 512)
+    y = host(T.matmul_act(w, O.ACT_F32, dev(gold["act_x"])))
+    _, mag = _f32_bound(t, rows, gold["act_x"], 512)
+    assert np.all(np.abs(y - gold[f"vecdot_{name}"]) <= 2e-6 * mag)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q6_K], ids=lambda t: O.TYPE_NAMES[t])
+def test_gemv_f32_large_k_passes(cuda, t):
+    """K = 14336 (the FFN down projection): the staged fp32 rows fill the LDS at 2 rows, so
+    5 rows run in passes of 2, 2 and 1."""
+    from dynalm_amd import torch_ops as T
+
+    k, n = 14336, 256
+    rows = gguf_weights(t, n, k, 1980 + t, outlier_frac=0.01)
+    x = activations(5, k, 1981)
+    w = dq.Weight.upload(t, rows, k)
+    y = host(T.matmul_act(w, O.ACT_F32, dev(x)))
+    exact, mag = _f32_bound(t, rows, x, k)
+    assert np.all(np.abs(y - exact) <= 1e-5 * mag)
+    y1 = host(T.matmul_act(w, O.ACT_F32, dev(x[4:5])))
+    assert np.array_equal(y1.view(np.uint32), y[4:5].view(np.uint32))

@@ -391,6 +391,28 @@ def test_q16_dots_vs_reference_avx2(gold, t):
     assert not np.isfinite(y[4]).any() and not np.isfinite(gold[f"q16dot_{name}"][4]).any()
 
 
+@pytest.mark.parametrize("t", TYPES, ids=lambda t: O.TYPE_NAMES[t])
+def test_f32_dots_golden_bit_exact(gold, t):
+    """fp32 activations (the kF32 contract): bit-equal to the reference's generic vec_dot_*."""
+    name = O.TYPE_NAMES[t]
+    y = O.matmul(t, O.ACT_F32, gold[f"w_{name}"], O.quantize_act(O.ACT_F32, gold["act_x"]), 512)
+    assert np.array_equal(y.view(np.uint32), gold[f"vecdot_{name}"].view(np.uint32))
+
+
+@pytest.mark.parametrize("t", TYPES, ids=lambda t: O.TYPE_NAMES[t])
+def test_f32_dots_within_double_bound(t):
+    """The fp32 dots against the double product of the dequantized weights and the fp32
+    rows: 1e-5 of the sum of |terms| (edge weight blocks, outlier channels)."""
+    k = 1024
+    w = weight_rows(t, 5, k, 320 + t, edge=True)
+    x = activations(3, k, 321)
+    y = O.matmul(t, O.ACT_F32, w, O.quantize_act(O.ACT_F32, x), k)
+    wf = O.dequantize(t, w, k).astype(np.float64)
+    xf = x.astype(np.float64)
+    assert np.all(np.abs(y - xf @ wf.T) <= 1e-5 * (np.abs(xf) @ np.abs(wf).T) + 1e-30)
+    assert np.array_equal(O.dequantize_act(O.ACT_F32, O.quantize_act(O.ACT_F32, x), k), x)
+
+
 @pytest.mark.parametrize("t,fmt", PAIRS_ALL, ids=lambda p: str(p))
 def test_dots_within_double_bound(t, fmt):
     """|y - y_double| <= 1e-5 * sum|w_i x_i| against the double product of the
@@ -449,6 +471,21 @@ def test_live_reference_quantizers(seed):
                       ("q16", O.ACT_Q16)):
         ref = np.stack([O.ref_quantize(kind, x[i]) for i in range(3)])
         assert np.array_equal(O.quantize_act(fmt, x), ref), kind
+
+
+@needs_ref
+@pytest.mark.parametrize("t", TYPES, ids=lambda t: O.TYPE_NAMES[t])
+def test_live_reference_vec_dot(t):
+    """fp32 activations: generic vec_dot bit-equal, AVX2 vec_dot within its fp32 reordering."""
+    k = 2048
+    w = weight_rows(t, 4, k, 520 + t, edge=True)
+    x = activations(3, k, 521)
+    y = O.matmul(t, O.ACT_F32, w, O.quantize_act(O.ACT_F32, x), k)
+    gen = np.array([[O.ref_vec_dot(0, t, w[i], x[r], k) for i in range(4)] for r in range(3)], np.float32)
+    avx = np.array([[O.ref_vec_dot(1, t, w[i], x[r], k) for i in range(4)] for r in range(3)], np.float32)
+    assert np.array_equal(y.view(np.uint32), gen.view(np.uint32))
+    mag = np.abs(x.astype(np.float64)) @ np.abs(O.dequantize(t, w, k).astype(np.float64)).T
+    assert np.all(np.abs(avx - y) <= 1e-5 * mag)
 
 
 @needs_ref
