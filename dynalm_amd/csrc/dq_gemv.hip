@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "dq_act.h"
 #include "dq_device.h"
 #include "dq_internal.h"
@@ -860,7 +862,7 @@ DQ_DEV void quantize_slice(const float* __restrict__ x, int64_t xs, int nblk, in
 // shape (the up projection); waves W/2.. run it over the same row group with their
 // own LDS regions, and y = act(x . gate) * (x . up) (dynacore's Device::matmul_gated,
 // dynacore/include/dynacore/device/device.h:188-199).
-template <int WT, int AF, int M, int W, int U, bool kFuse, int kEarly, bool kGated = false>
+template <int WT, int AF, int M, int W, int U, bool kFuse, int kEarly, bool kGated = false, bool kSplit = false>
 __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
                                                  const uint8_t* __restrict__ p2, const uint8_t* __restrict__ p3,
                                                  int nblk, int64_t g0, int64_t n0, int64_t n1,
@@ -870,7 +872,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
                                                  int32_t* __restrict__ dbg, int64_t dbg_n,
                                                  const uint8_t* __restrict__ q0, const uint8_t* __restrict__ q1,
                                                  const uint8_t* __restrict__ q2, const uint8_t* __restrict__ q3,
-                                                 int act) {
+                                                 int act, int splits, float* __restrict__ part) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr bool kSb = AF == kActQ8_K || AF == kActSX;
   static_assert(!kGated || (kSb && M == 1 && kFuse), "the gated GEMV takes one fp32 row and K-quant weights");
@@ -883,7 +885,9 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
   const int r = threadIdx.x & 63, wave = wave_id();
   const int half = kGated && wave >= WH ? 1 : 0;
   const int wl = wave - half * WH;
-  const int64_t G = g0 + blockIdx.x;
+  // split-K (splits > 1): workgroup L takes K-range L % splits of row group L / splits
+  const int sk = kSplit ? (int)(blockIdx.x % (unsigned)splits) : 0;
+  const int64_t G = g0 + (kSplit ? (int64_t)(blockIdx.x / (unsigned)splits) : (int64_t)blockIdx.x);
   const size_t region = kSb ? ((size_t)M * nblk * 65 * 4 + 15) / 16 * 16 : (size_t)W * M * 64 * 4;
   Out<M> o;
   o.rec = reinterpret_cast<float*>(smem + half * region);
@@ -895,7 +899,8 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
   o.r = r;
 #pragma unroll
   for (int mm = 0; mm < M; ++mm) o.acc[mm] = o.cor[mm] = 0.0f;
-  const int b0 = wl * nblk / WH, b1 = (wl + 1) * nblk / WH;  // this wave's blocks
+  const int kb0 = kSplit ? sk * nblk / splits : 0, kb1 = kSplit ? (sk + 1) * nblk / splits : nblk;  // this workgroup's blocks
+  const int b0 = kb0 + wl * (kb1 - kb0) / WH, b1 = kb0 + (wl + 1) * (kb1 - kb0) / WH;  // this wave's
   // bytes of the staged activation rows (the dummy area of the early path follows)
   const int stage_bytes =
       kSb ? M * nblk * stage_sb(AF) : M * nblk * ((WT == kQ4_K || WT == kQ6_K) ? 8 : 1) * stage_b32(AF);
@@ -986,6 +991,30 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
     for (int mm = 0; mm < M; ++mm) o.rec[(wave * M + mm) * 64 + r] = AF == kActQ16 ? o.acc[mm] - o.cor[mm] : o.acc[mm];
   }
   __syncthreads();
+  if constexpr (kSplit) {
+    static_assert(!kGated, "gated launches are not split");
+    // Publish this workgroup's part, finished by k_split_finish: the t-terms and
+    // scales of blocks [kb0, kb1) in [G][M][nblk][65] (Q8_K / sub-scaled), or the row
+    // sums of its slices, added in wave order, in [G][splits][M][64].
+    if constexpr (kSb) {
+      const int nb = kb1 - kb0;
+      for (int i = wave; i < M * nb; i += W) {
+        const int mm = i / nb, b = kb0 + i % nb;
+        float* pe = part + ((G * M + mm) * nblk + b) * 65;
+        pe[r] = o.rec[(mm * nblk + b) * 64 + r];
+        if (r == 0) pe[64] = o.dav[mm * nblk + b];
+      }
+    } else if (wave == 0) {
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) v = v + o.rec[(w * M + mm) * 64 + r];
+        part[((G * splits + sk) * M + mm) * 64 + r] = v;
+      }
+    }
+    return;
+  }
   if (wave != 0) return;
   const int64_t n = o.n;
   // the canonical chain acc = fma(da_b, t_b, acc) over a t-term region
@@ -1023,6 +1052,28 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
   }
 }
 
+// Completes split-K rows (one 64-lane workgroup per row group, lane r = row): the
+// canonical chain acc = fma(da, t, acc) over all blocks in order (Q8_K and
+// sub-scaled parts), or the sum of the splits' row sums in split order.
+template <bool kSb, int M>
+__global__ __launch_bounds__(64) void k_split_finish(const float* __restrict__ part, int nblk, int splits, int64_t g0,
+                                                     int64_t n0, int64_t n1, float* __restrict__ y, int64_t ys,
+                                                     const float* __restrict__ bias) {
+  const int r = threadIdx.x;
+  const int64_t G = g0 + blockIdx.x, n = G * kRowGroup + r;
+#pragma unroll
+  for (int mm = 0; mm < M; ++mm) {
+    float v = 0.0f;
+    if constexpr (kSb) {
+      const float* pe = part + (G * M + mm) * nblk * 65;
+      for (int b = 0; b < nblk; ++b) v = fmaf(pe[b * 65 + 64], pe[b * 65 + r], v);
+    } else {
+      for (int q = 0; q < splits; ++q) v = v + part[((G * splits + q) * M + mm) * 64 + r];
+    }
+    if (n >= n0 && n < n1) y[mm * ys + n] = bias ? v + bias[n] : v;
+  }
+}
+
 // ================================================================ launchers
 
 // LDS of one GEMV workgroup: Q8_K t-terms [M][nblk][64] + da [M][nblk], or the
@@ -1044,44 +1095,90 @@ static size_t gemv_lds_bytes(int wt, int af, int m, int waves, int64_t nblk, boo
 // the tail; with more row groups than CUs, 8-wave workgroups (two per CU) do
 // better. 16 waves leave 128 VGPRs per lane: K-quant passes of more than one
 // activation row need more and keep 8 waves.
-template <int WT, int AF, int M, bool kFuse, int W, int kEarly>
+// Split-K state of one launch: the number of K-ranges per row group and the
+// per-device part buffer (splits == 1: none).
+struct Split {
+  int splits = 1;
+  float* part = nullptr;
+};
+
+// Per-device split-K part buffers, grown on demand. Split launches that overlap on
+// one device from different streams race on it, as the library's other per-device
+// scratch does.
+struct SplitBufs {
+  float* part = nullptr;
+  size_t bytes = 0;
+};
+static std::mutex g_split_mu;
+static SplitBufs g_split[64];
+
+static hipError_t split_bufs(int device, size_t bytes, Split& sp) {
+  std::lock_guard<std::mutex> lock(g_split_mu);
+  SplitBufs& b = g_split[device < 64 ? device : 63];
+  if (b.bytes < bytes) {
+    hipError_t e = hipDeviceSynchronize();  // earlier launches may still use the old buffer
+    if (e != hipSuccess) return e;
+    if (b.part != nullptr && (e = hipFree(b.part)) != hipSuccess) return e;
+    b.part = nullptr;
+    b.bytes = 0;
+    const size_t sz = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    if ((e = hipMalloc(reinterpret_cast<void**>(&b.part), sz)) != hipSuccess) return e;
+    b.bytes = sz;
+  }
+  sp.part = b.part;
+  return hipSuccess;
+}
+
+template <int WT, int AF, int M, bool kFuse, int W, int kEarly, bool kSplit>
 static hipError_t gemv_launch(const WeightDev& w, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
                               int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
-                              hipStream_t s) {
+                              const Split& sp, hipStream_t s) {
   // blocks per chunk of vector loads: two super-blocks (or 8 32-value blocks) per
   // wave step, one (or 4) when waves hold fewer blocks
   constexpr int U = (WT == kQ8_0 || WT == kQ4_0) ? (W >= 16 ? 4 : 8) : (W >= 16 ? 1 : 2);
   const int64_t g0 = n0 / kRowGroup, g1 = (n1 + kRowGroup - 1) / kRowGroup;
   const size_t lds = gemv_lds_bytes(WT, AF, M, W, w.nblk, kEarly > 0);
   if (lds > kGemvMaxLds) return hipErrorInvalidValue;
-  const void* fn = reinterpret_cast<const void*>(&k_gemv<WT, AF, M, W, U, kFuse, kEarly>);
+  const void* fn = reinterpret_cast<const void*>(&k_gemv<WT, AF, M, W, U, kFuse, kEarly, false, kSplit>);
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((k_gemv<WT, AF, M, W, U, kFuse, kEarly>), dim3((unsigned)(g1 - g0)), dim3(64 * W), lds, s, w.plane[0],
-                     w.plane[1], w.plane[2], w.plane[3], (int)w.nblk, g0, n0, n1, acts, arb, x, xs, y, ys, bias, dbg,
-                     w.n, nullptr, nullptr, nullptr, nullptr, 0);
+  hipLaunchKernelGGL((k_gemv<WT, AF, M, W, U, kFuse, kEarly, false, kSplit>), dim3((unsigned)((g1 - g0) * sp.splits)),
+                     dim3(64 * W),
+                     lds, s, w.plane[0], w.plane[1], w.plane[2], w.plane[3], (int)w.nblk, g0, n0, n1, acts, arb, x, xs,
+                     y, ys, bias, dbg, w.n, nullptr, nullptr, nullptr, nullptr, 0, sp.splits, sp.part);
+  if (kSplit) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_split_finish<AF == kActQ8_K || AF == kActSX, M>), dim3((unsigned)(g1 - g0)), dim3(64), 0, s,
+                       sp.part, (int)w.nblk, sp.splits, g0, n0, n1, y, ys, bias);
+  }
   return hipGetLastError();
 }
 
 // The early-activation variant for W waves: Q8_K rows hold at most 2 super-blocks
 // per wave (fused or not); 32-value formats at most 64 blocks per wave (not fused).
-template <int WT, int AF, int M, bool kFuse, int W>
+template <int WT, int AF, int M, bool kFuse, int W, bool kSplit>
 static hipError_t gemv_early(const WeightDev& w, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
                              int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
-                             hipStream_t s) {
-  const int64_t per_wave = (w.nblk + W - 1) / W;  // blocks of the largest slice
+                             const Split& sp, hipStream_t s) {
+  const int64_t per_split = (w.nblk + sp.splits - 1) / sp.splits;
+  const int64_t per_wave = (per_split + W - 1) / W;  // blocks of the largest slice
   if constexpr (M == 1 && AF == kActQ8_K) {
-    if (per_wave == 1) return gemv_launch<WT, AF, M, kFuse, W, 1>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
-    if (per_wave == 2) return gemv_launch<WT, AF, M, kFuse, W, 2>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+    if (per_wave == 1) {
+      return gemv_launch<WT, AF, M, kFuse, W, 1, kSplit>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, sp, s);
+    }
+    if (per_wave == 2) {
+      return gemv_launch<WT, AF, M, kFuse, W, 2, kSplit>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, sp, s);
+    }
   } else if constexpr (M == 1 && !kFuse && AF != kActSX && AF != kActQ16 && AF != kActF32) {
     const int64_t bpu = WT == kQ4_K || WT == kQ6_K ? 8 : 1;
     if (per_wave * bpu <= 64) {
-      return gemv_launch<WT, AF, M, kFuse, W, 1>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+      return gemv_launch<WT, AF, M, kFuse, W, 1, kSplit>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, sp, s);
     }
   }
-  return gemv_launch<WT, AF, M, kFuse, W, 0>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+  return gemv_launch<WT, AF, M, kFuse, W, 0, kSplit>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, sp, s);
 }
 
 template <int WT, int AF, int M, bool kFuse>
@@ -1090,10 +1187,35 @@ static hipError_t gemv_waves(const WeightDev& w, const uint8_t* acts, int64_t ar
                              hipStream_t s) {
   constexpr bool kWide = M == 1 || WT == kQ8_0 || WT == kQ4_0;
   const int64_t groups = (n1 + kRowGroup - 1) / kRowGroup - n0 / kRowGroup;
-  if (kWide && groups <= w.cus) {
-    return gemv_early<WT, AF, M, kFuse, kWide ? 16 : 8>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+  // Fewer row groups than half the CUs (e.g. N = 4096: 64 groups): split each row's
+  // blocks into up to 8 K-ranges over 8-wave workgroups (at least one block per
+  // wave), so the launch covers the CUs, and finish the rows in a second launch.
+  // Measured: it pays for the VALU-heavy fp32 and int16 formats (Q6_K K=14336 N=4096
+  // fp32: 75 -> 21 us); the int8 formats stream faster unsplit with 16 waves (21.8 us
+  // there, 26.7 split, the finishing launch included).
+  constexpr bool kSplitOk = AF == kActF32 || AF == kActQ16;
+  const int cus = w.cus > 0 ? w.cus : 256;
+  int splits = 1;
+  if (kSplitOk && groups * 2 <= cus) {
+    splits = (int)(cus / groups);
+    if (splits > 8) splits = 8;
+    while (splits > 1 && w.nblk / splits < 8) --splits;
   }
-  return gemv_early<WT, AF, M, kFuse, 8>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+  if (splits > 1) {
+    constexpr bool kSb = AF == kActQ8_K || AF == kActSX;
+    const int64_t gtot = w.n_pad / kRowGroup;
+    const size_t part = kSb ? (size_t)gtot * M * w.nblk * 65 * 4 : (size_t)gtot * splits * M * 64 * 4;
+    Split sp;
+    sp.splits = splits;
+    const hipError_t e = split_bufs(w.device, part, sp);
+    if (e != hipSuccess) return e;
+    return gemv_early<WT, AF, M, kFuse, 8, true>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, sp, s);
+  }
+  const Split none;
+  if (kWide && groups <= w.cus) {
+    return gemv_early<WT, AF, M, kFuse, kWide ? 16 : 8, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, none, s);
+  }
+  return gemv_early<WT, AF, M, kFuse, 8, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, none, s);
 }
 
 // M rows (1..4 or 8) of one pass; x != nullptr: fused quantization of fp32 rows.
@@ -1183,7 +1305,7 @@ static hipError_t gated_launch(const WeightDev& wg, const WeightDev& wu, int act
   hipLaunchKernelGGL((k_gemv<WT, kActQ8_K, 1, W, U, true, kEarly, true>), dim3((unsigned)groups), dim3(64 * W), lds, s,
                      wg.plane[0], wg.plane[1], wg.plane[2], wg.plane[3], (int)wg.nblk, (int64_t)0, (int64_t)0, wg.n,
                      nullptr, (int64_t)0, x, wg.k, y, wg.n, nullptr, nullptr, wg.n, wu.plane[0], wu.plane[1],
-                     wu.plane[2], wu.plane[3], act);
+                     wu.plane[2], wu.plane[3], act, 1, nullptr);
   return hipGetLastError();
 }
 

@@ -1019,3 +1019,40 @@ def test_gemv_f32_large_k_passes(cuda, t):
     assert np.all(np.abs(y - exact) <= 1e-5 * mag)
     y1 = host(T.matmul_act(w, O.ACT_F32, dev(x[4:5])))
     assert np.array_equal(y1.view(np.uint32), y[4:5].view(np.uint32))
+
+
+# ------------------------------------------------- split-K GEMV (small N)
+
+
+@pytest.mark.parametrize("pair", [(O.Q4_K, O.ACT_Q8_K), (O.Q6_K, O.ACT_Q8_K), (O.Q4_K, O.ACT_SX),
+                                  (O.Q8_0, O.ACT_PER32), (O.Q4_0, O.ACT_Q8_0), (O.Q6_K, O.ACT_Q16),
+                                  (O.Q4_K, O.ACT_F32)], ids=pair_id)
+@pytest.mark.parametrize("m", [1, 3])
+def test_gemv_split_k(cuda, pair, m):
+    """Few row groups (N = 256: 4 groups on 256 CUs) split each row's blocks over up to 8
+    workgroups; the last one to finish completes the row. Q8_K and sub-scaled rows keep
+    the canonical chain over all blocks (bit-identical to the oracle), the other formats
+    add the parts in split order (tolerance). Run twice (the row counters reset
+    themselves) and on a row range."""
+    from dynalm_amd import torch_ops as T
+
+    t, fmt = pair
+    k, n = 4096, 256
+    rows = gguf_weights(t, n, k, 2000 + t + fmt, outlier_frac=0.01)
+    x = activations(m, k, 2010 + m)
+    a = O.quantize_act(fmt, x)
+    w = dq.Weight.upload(t, rows, k)
+    ad = dev(a)
+    y1 = host(T.gemv(w, fmt, ad))
+    y2 = host(T.gemv(w, fmt, ad))
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    want = O.matmul(t, fmt, rows, a, k)
+    if fmt in (O.ACT_Q8_K, O.ACT_SX):
+        assert np.array_equal(y1.view(np.uint32), want.view(np.uint32))
+    else:
+        af = O.dequantize_act(fmt, a, k).astype(np.float64)
+        mag = np.abs(af) @ np.abs(O.dequantize(t, rows, k).astype(np.float64)).T
+        assert np.all(np.abs(y1.astype(np.float64) - want) <= 2e-6 * mag + 1e-30)
+    yr = host(T.gemv(w, fmt, ad, n0=70, n1=200))
+    assert np.array_equal(yr[:, 70:200].view(np.uint32), y1[:, 70:200].view(np.uint32))
+    assert not yr[:, :70].any() and not yr[:, 200:].any()
