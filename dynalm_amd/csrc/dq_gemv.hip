@@ -992,19 +992,10 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
   }
   __syncthreads();
   if constexpr (kSplit) {
-    static_assert(!kGated, "gated launches are not split");
-    // Publish this workgroup's part, finished by k_split_finish: the t-terms and
-    // scales of blocks [kb0, kb1) in [G][M][nblk][65] (Q8_K / sub-scaled), or the row
-    // sums of its slices, added in wave order, in [G][splits][M][64].
-    if constexpr (kSb) {
-      const int nb = kb1 - kb0;
-      for (int i = wave; i < M * nb; i += W) {
-        const int mm = i / nb, b = kb0 + i % nb;
-        float* pe = part + ((G * M + mm) * nblk + b) * 65;
-        pe[r] = o.rec[(mm * nblk + b) * 64 + r];
-        if (r == 0) pe[64] = o.dav[mm * nblk + b];
-      }
-    } else if (wave == 0) {
+    static_assert(!kGated && !kSb, "split launches: per-32 style formats");
+    // Publish this workgroup's row sums (its slices added in wave order) in
+    // [G][splits][M][64]; k_split_finish adds the splits in order.
+    if (wave == 0) {
 #pragma unroll
       for (int mm = 0; mm < M; ++mm) {
         float v = 0.0f;
@@ -1053,23 +1044,17 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
 }
 
 // Completes split-K rows (one 64-lane workgroup per row group, lane r = row): the
-// canonical chain acc = fma(da, t, acc) over all blocks in order (Q8_K and
-// sub-scaled parts), or the sum of the splits' row sums in split order.
-template <bool kSb, int M>
-__global__ __launch_bounds__(64) void k_split_finish(const float* __restrict__ part, int nblk, int splits, int64_t g0,
-                                                     int64_t n0, int64_t n1, float* __restrict__ y, int64_t ys,
+// sum of the splits' row sums in split order, plus the bias.
+template <int M>
+__global__ __launch_bounds__(64) void k_split_finish(const float* __restrict__ part, int splits, int64_t g0, int64_t n0,
+                                                     int64_t n1, float* __restrict__ y, int64_t ys,
                                                      const float* __restrict__ bias) {
   const int r = threadIdx.x;
   const int64_t G = g0 + blockIdx.x, n = G * kRowGroup + r;
 #pragma unroll
   for (int mm = 0; mm < M; ++mm) {
     float v = 0.0f;
-    if constexpr (kSb) {
-      const float* pe = part + (G * M + mm) * nblk * 65;
-      for (int b = 0; b < nblk; ++b) v = fmaf(pe[b * 65 + 64], pe[b * 65 + r], v);
-    } else {
-      for (int q = 0; q < splits; ++q) v = v + part[((G * splits + q) * M + mm) * 64 + r];
-    }
+    for (int q = 0; q < splits; ++q) v = v + part[((G * splits + q) * M + mm) * 64 + r];
     if (n >= n0 && n < n1) y[mm * ys + n] = bias ? v + bias[n] : v;
   }
 }
@@ -1096,7 +1081,7 @@ static size_t gemv_lds_bytes(int wt, int af, int m, int waves, int64_t nblk, boo
 // better. 16 waves leave 128 VGPRs per lane: K-quant passes of more than one
 // activation row need more and keep 8 waves.
 // Split-K state of one launch: the number of K-ranges per row group and the
-// per-device part buffer (splits == 1: none).
+// per-device buffer of their row sums (splits == 1: none).
 struct Split {
   int splits = 1;
   float* part = nullptr;
@@ -1151,8 +1136,8 @@ static hipError_t gemv_launch(const WeightDev& w, const uint8_t* acts, int64_t a
   if (kSplit) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_split_finish<AF == kActQ8_K || AF == kActSX, M>), dim3((unsigned)(g1 - g0)), dim3(64), 0, s,
-                       sp.part, (int)w.nblk, sp.splits, g0, n0, n1, y, ys, bias);
+    hipLaunchKernelGGL((k_split_finish<M>), dim3((unsigned)(g1 - g0)), dim3(64), 0, s, sp.part, sp.splits, g0, n0, n1, y,
+                       ys, bias);
   }
   return hipGetLastError();
 }
@@ -1201,15 +1186,16 @@ static hipError_t gemv_waves(const WeightDev& w, const uint8_t* acts, int64_t ar
     if (splits > 8) splits = 8;
     while (splits > 1 && w.nblk / splits < 8) --splits;
   }
-  if (splits > 1) {
-    constexpr bool kSb = AF == kActQ8_K || AF == kActSX;
-    const int64_t gtot = w.n_pad / kRowGroup;
-    const size_t part = kSb ? (size_t)gtot * M * w.nblk * 65 * 4 : (size_t)gtot * splits * M * 64 * 4;
-    Split sp;
-    sp.splits = splits;
-    const hipError_t e = split_bufs(w.device, part, sp);
-    if (e != hipSuccess) return e;
-    return gemv_early<WT, AF, M, kFuse, 8, true>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, sp, s);
+  if constexpr (kSplitOk) {
+    if (splits > 1) {
+      const int64_t gtot = w.n_pad / kRowGroup;
+      const size_t part = (size_t)gtot * splits * M * 64 * 4;
+      Split sp;
+      sp.splits = splits;
+      const hipError_t e = split_bufs(w.device, part, sp);
+      if (e != hipSuccess) return e;
+      return gemv_early<WT, AF, M, kFuse, 8, true>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, sp, s);
+    }
   }
   const Split none;
   if (kWide && groups <= w.cus) {
