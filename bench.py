@@ -133,8 +133,17 @@ def cpu_baseline(w_host: np.ndarray, copies: int, budget_s: float) -> dict:
         ns = r.ref_bench_gemv(3, O.Q4_K, ptrs, copies, Q4K_ROW, N, acts.ctypes.data, acts.size, 1, K, y.ctypes.data,
                               cores, iters)
         sec = ns / iters / 1e9
+        # one thread as well (the scalar-core rate), on a shorter sample
+        ns1 = r.ref_bench_gemv(3, O.Q4_K, ptrs, copies, Q4K_ROW, N, acts.ctypes.data, acts.size, 1, K, y.ctypes.data,
+                               1, 1)
+        iters1 = max(2, int(0.25 * budget_s / max(ns1 / 1e9, 1e-6)))
+        ns1 = r.ref_bench_gemv(3, O.Q4_K, ptrs, copies, Q4K_ROW, N, acts.ctypes.data, acts.size, 1, K, y.ctypes.data,
+                               1, iters1)
+        sec1 = ns1 / iters1 / 1e9
         return {"value": round(nbytes / sec / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "reference",
                 "ms_per_call": round(sec * 1e3, 4), "tokens_per_s": round(1.0 / sec, 1),
+                "one_thread": {"value": round(nbytes / sec1 / 1e9, 2), "ms_per_call": round(sec1 * 1e3, 4),
+                               "calls": iters1},
                 "sample": f"{iters} calls of the full K=4096 N=14336 M=1 Q4_K GEMV, dynacore AVX2 "
                           f"dot_rows_n_sx_q4_K (sub-scaled int8 activations, its x86 default), {cores} threads "
                           f"over 16-row units, {copies} rotated weight copies",
