@@ -649,7 +649,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
   }
 }
 
-bool gemm_supported(int dtype, int af) { return dtype == kQ4_K && af == kActQ8_K; }
+bool gemm_supported(int dtype, int af) { return (dtype == kQ4_K && af == kActQ8_K) || gemm_b32_supported(dtype, af); }
 
 namespace {
 
@@ -709,6 +709,7 @@ hipError_t launch_big(const WeightDev& w, const uint8_t* acts, int64_t arb, int6
 
 hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
                        float* y, int64_t ys, const float* bias, hipStream_t s) {
+  if (gemm_b32_supported(w.dtype, af)) return launch_gemm_b32(w, af, acts, arb, m, n0, n1, y, ys, bias, s);
   if (!gemm_supported(w.dtype, af)) return hipErrorInvalidValue;
   if (m == 0 || n1 <= n0) return hipSuccess;
   const int cus = w.cus > 0 ? w.cus : 256;

@@ -1,0 +1,207 @@
+// dq_gemm_b32.hip -- prefill GEMM for the 32-value block types (Q8_0, Q4_0) x per-32
+// activations (ActBlockQ8) on gfx950 int8 MFMA (v_mfma_i32_16x16x32_i8).
+//
+// Arithmetic: the reference's generic per-32 dot (dynacore/cpu/generic/kernels_generic.cpp:216-239):
+// per block b the exact integer P_b = sum_{i<32} w_i a_i, then acc = acc + (dw*da)*(float)P_b
+// over the blocks in order. One MFMA with K = 32 forms P_b of a 16 x 16 tile, so every
+// output runs exactly that sequence and the result is bit-identical to the CPU oracle
+// (and to the GEMV only up to its slice-sum order). Q4_0 codes are the nibbles minus 8:
+// the MFMA takes the raw nibbles (valid int8) and P_b = P_raw - 8 * sum(a_i), with the
+// code sum of the activation block.
+//
+// Workgroup: 4 waves over a 64 x 64 tile (activation rows x one 64-row weight group),
+// each wave 32 x 32 (2 x 2 MFMA tiles), one LDS stage of 8 blocks at a time: with 41 KB
+// three workgroups share a CU and hide each other's loads (measured: a double-buffered
+// stage, one workgroup per CU, was 1.4-1.8x slower at M = 512). Per stage the weight codes (the
+// plane layout: per block and 16-byte chunk 64 rows x 16 B, 1 KB contiguous), their fp16
+// scales and the 320 activation bytes of each of the 64 rows reach LDS by direct-to-LDS
+// buffer loads (rows and blocks past the ends read as zeros); the activation scales and
+// sums are then gathered into [block][row] arrays so that a lane reads the four rows of
+// its MFMA result with one 16-byte read. The epilogue (4 VALU per output and block) is
+// the bound; the MFMA work is an eighth of it.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dq_device.h"
+#include "dq_internal.h"
+#include "dq_mfma.h"
+
+namespace dq {
+
+namespace {
+
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kKB = 8;                      // blocks per stage
+constexpr int kARow = kKB * 40;             // staged activation bytes per row
+constexpr int kA = 0;                       // [64 rows][kKB * 40 B] activation blocks as stored
+constexpr int kB = kA + 64 * kARow;         // [kKB][2 chunks][64 rows][16 B] weight codes
+constexpr int kD = kB + kKB * 2 * 64 * 16;  // [kKB][64 rows] fp16 weight scales
+constexpr int kDA = kD + kKB * 64 * 2;      // [kKB][64 rows] activation scales (float)
+constexpr int kSA = kDA + kKB * 64 * 4;     // [kKB][64 rows] activation code sums (int)
+constexpr int kStage = kSA + kKB * 64 * 4;
+constexpr int kLds = kStage;  // single-buffered: 41 KB, three workgroups per CU overlap each other
+
+DQ_DEV void ld_lds16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_dst, u32 voff, u32 soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_dst, 16, voff, soff, 0, 0);
+}
+
+DQ_DEV v4i_t mfma32(v2u a, v2u b, v4i_t c) {
+  return __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), c, 0, 0, 0);
+}
+
+template <int WT>
+__global__ __launch_bounds__(256) void k_gemm_b32(const uint8_t* __restrict__ qs_plane, const uint8_t* __restrict__ d_plane,
+                                                  int nblk, int64_t g0, int64_t n0, int64_t n1,
+                                                  const uint8_t* __restrict__ acts, int64_t arb, int64_t m,
+                                                  float* __restrict__ y, int64_t ys, const float* __restrict__ bias,
+                                                  int tiles_n, int tiles_m) {
+  constexpr int kC = WT == kQ8_0 ? 2 : 1;  // 16-byte code chunks per block and row
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave & 1, wn = wave >> 1;  // 32 x 32 quarter of the tile
+  const int li = lane & 15, lg = lane >> 4;
+
+  // XCD-aware order: the activation tiles of one weight group run on one XCD
+  int L = blockIdx.x;
+  const int per = (tiles_n * tiles_m) / 8;
+  if (L < 8 * per) L = (L % 8) * per + L / 8;
+  const int tn = __builtin_amdgcn_readfirstlane(L / tiles_m);
+  const int tm = __builtin_amdgcn_readfirstlane(L - tn * tiles_m);
+  const int64_t G = g0 + tn;
+  const int64_t mbase = (int64_t)tm * 64;
+  const int64_t mrows = m - mbase < 64 ? m - mbase : 64;
+
+  const auto ra = rsrc(acts + mbase * arb, (u32)(mrows * arb));
+  const auto rq = rsrc(qs_plane + G * nblk * 64 * 16 * kC, (u32)(nblk * 64 * 16 * kC));
+  const auto rd = rsrc(d_plane + G * nblk * 64 * 2, (u32)(nblk * 64 * 2));
+
+  f4_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // staging of blocks [b, b + kKB) into buffer buf: direct-to-LDS loads only
+  auto issue = [&](int b, int buf) {
+    uint8_t* base = lds + buf * kStage;
+    // activations: piece p (16 B) of the 64 x kARow region is row p / 20, byte 16 (p % 20)
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+      const int p = (wave * 5 + i) * 64 + lane, row = p / 20;
+      ld_lds16(ra, base + kA + (wave * 5 + i) * 1024, (u32)(row * arb + 16 * (p % 20)), (u32)(b * 40));
+    }
+    // weight codes: one 1 KB instruction per (block, chunk)
+#pragma unroll
+    for (int i = 0; i < 4 * kC / 2; ++i) {
+      const int q = wave * (4 * kC / 2) + i;  // (block, chunk) = (q / kC, q % kC)
+      ld_lds16(rq, base + kB + q * 1024, (u32)(lane * 16), (u32)((b * kC + q) * 1024));
+    }
+    if (wave == 0) ld_lds16(rd, base + kD, (u32)(lane * 16), (u32)(b * 128));
+  };
+  // the activation scales and code sums of a landed stage as [block][row]
+  auto gather = [&](int buf) {
+    uint8_t* base = lds + buf * kStage;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int idx = t + 256 * i, j = idx >> 6, row = idx & 63;
+      const v2u ds = *reinterpret_cast<const v2u*>(base + kA + row * kARow + j * 40);
+      *reinterpret_cast<u32*>(base + kDA + idx * 4) = ds.x;
+      *reinterpret_cast<u32*>(base + kSA + idx * 4) = ds.y;
+    }
+  };
+
+  for (int b = 0, buf = 0; b < nblk; b += kKB) {
+    issue(b, buf);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    gather(buf);
+    __syncthreads();
+    const uint8_t* base = lds + buf * kStage;
+    const int nj = nblk - b < kKB ? nblk - b : kKB;
+    for (int j = 0; j < nj; ++j) {
+      v2u af[2], bf[2];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const int row = 32 * wm + 16 * rt + li;
+        af[rt] = *reinterpret_cast<const v2u*>(base + kA + row * kARow + j * 40 + 8 + 8 * lg);
+      }
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const int col = 32 * wn + 16 * ct + li;
+        if (WT == kQ8_0) {
+          bf[ct] = *reinterpret_cast<const v2u*>(base + kB + ((j * 2 + (lg >> 1)) * 64 + col) * 16 + 8 * (lg & 1));
+        } else {
+          // values 0..15 are the low nibbles of bytes 0..15, 16..31 the high ones
+          const v2u raw = *reinterpret_cast<const v2u*>(base + kB + (j * 64 + col) * 16 + 8 * (lg & 1));
+          bf[ct] = lg < 2 ? v2u{raw.x & 0x0F0F0F0Fu, raw.y & 0x0F0F0F0Fu}
+                          : v2u{(raw.x >> 4) & 0x0F0F0F0Fu, (raw.y >> 4) & 0x0F0F0F0Fu};
+        }
+      }
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const int r0 = 32 * wm + 16 * rt + 4 * lg;  // rows r0 .. r0 + 3 of this lane's results
+        const f4_t da = *reinterpret_cast<const f4_t*>(base + kDA + (j * 64 + r0) * 4);
+        v4i_t sa = {0, 0, 0, 0};
+        if (WT == kQ4_0) sa = *reinterpret_cast<const v4i_t*>(base + kSA + (j * 64 + r0) * 4);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          const int col = 32 * wn + 16 * ct + li;
+          const float dw = h2f(*reinterpret_cast<const uint16_t*>(base + kD + (j * 64 + col) * 2));
+          const v4i_t p = mfma32(af[rt], bf[ct], v4i_t{0, 0, 0, 0});
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int pe = WT == kQ4_0 ? p[e] - 8 * sa[e] : p[e];
+            const float t1 = dw * da[e];
+            const float t2 = t1 * (float)pe;
+            acc[rt][ct][e] = acc[rt][ct][e] + t2;
+          }
+        }
+      }
+    }
+    __syncthreads();  // the stage is free for the next loads
+  }
+
+  // ---- store
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) {
+    const int64_t n = G * kRowGroup + 32 * wn + 16 * ct + li;
+    if (n < n0 || n >= n1) continue;
+    const float bn = bias ? bias[n] : 0.0f;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t mm = mbase + 32 * wm + 16 * rt + 4 * lg + e;
+        if (mm < m) y[mm * ys + n] = bias ? acc[rt][ct][e] + bn : acc[rt][ct][e];
+      }
+    }
+  }
+}
+
+}  // namespace
+
+bool gemm_b32_supported(int dtype, int af) { return (dtype == kQ8_0 || dtype == kQ4_0) && af == kActPer32; }
+
+hipError_t launch_gemm_b32(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0,
+                           int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s) {
+  if (!gemm_b32_supported(w.dtype, af)) return hipErrorInvalidValue;
+  if (m == 0 || n1 <= n0) return hipSuccess;
+  const int64_t g0 = n0 / kRowGroup, g1 = (n1 + kRowGroup - 1) / kRowGroup;
+  const int64_t tiles_n = g1 - g0, tiles_m = (m + 63) / 64;
+  // 32-bit buffer offsets: one row group's codes and 64 activation rows
+  if (w.nblk * 64 * 32 >= ((int64_t)1 << 31) || 64 * arb >= ((int64_t)1 << 32) || tiles_n * tiles_m >= ((int64_t)1 << 31)) {
+    return hipErrorInvalidValue;
+  }
+  if (w.dtype == kQ8_0) {
+    hipLaunchKernelGGL(k_gemm_b32<kQ8_0>, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), kLds, s, w.plane[0],
+                       w.plane[1], (int)w.nblk, g0, n0, n1, acts, arb, m, y, ys, bias, (int)tiles_n, (int)tiles_m);
+  } else {
+    hipLaunchKernelGGL(k_gemm_b32<kQ4_0>, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), kLds, s, w.plane[0],
+                       w.plane[1], (int)w.nblk, g0, n0, n1, acts, arb, m, y, ys, bias, (int)tiles_n, (int)tiles_m);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace dq

@@ -44,6 +44,10 @@ hipError_t launch_units(const WeightDev& w, int af, const uint8_t* acts, int64_t
 hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
                        float* y, int64_t ys, const float* bias, hipStream_t s);
 bool gemm_supported(int dtype, int af);
+// The 32-value block GEMM (Q8_0 / Q4_0 x per-32 ActBlockQ8) that launch_gemm dispatches to.
+hipError_t launch_gemm_b32(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0,
+                           int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s);
+bool gemm_b32_supported(int dtype, int af);
 // Skinny MFMA GEMV (Q4_K / Q6_K x Q8_K, 2 <= m <= kSkinnyMaxRows) on pre-quantized
 // Q8_K rows; hipErrorInvalidValue otherwise.
 hipError_t launch_gemv_mma(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0,

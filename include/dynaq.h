@@ -153,14 +153,17 @@ DQ_API int dq_act_quantize(int fmt, const float* x, int64_t m, int64_t k, int64_
  * Any m: the weights are streamed once per pass of up to 4 activation rows. */
 DQ_API int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0, int64_t n1, float* y,
                    int64_t y_stride, const float* bias, void* stream);
-/* dq_gemm runs the int8 MFMA GEMM (Q4_K weights with DQ_ACT_Q8_K activations;
- * other pairs return DQ_UNSUPPORTED); any m.
+/* dq_gemm runs the int8 MFMA GEMM: Q4_K weights with DQ_ACT_Q8_K activations, and
+ * Q8_0 / Q4_0 weights with DQ_ACT_PER32 (each output in the reference's generic
+ * per-32 block order, kernels_generic.cpp:216-239); other pairs return
+ * DQ_UNSUPPORTED; any m.
  * Replaces qmm::Kernels::gemm (dynacore/include/dynacore/cpu/qmm.h:128-129). */
 DQ_API int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0, int64_t n1, float* y,
                    int64_t y_stride, const float* bias, void* stream);
 
-/* y = x . w^T (+ bias): quantize x with dq_act_format_for(w), then GEMV for
- * m <= DQ_GEMV_MAX_ROWS, else GEMM. Replaces Device::matmul
+/* y = x . w^T (+ bias): quantize x with dq_act_format_for(w), then GEMV or GEMM by
+ * m (Q4_K: GEMM above DQ_GEMV_MAX_ROWS; Q8_0 / Q4_0: GEMM from 32 rows; Q6_K: the
+ * skinny MFMA GEMV in passes of 64 rows). Replaces Device::matmul
  * (dynacore/include/dynacore/device/device.h:161; CpuDevice::matmul,
  * dynacore/cpu/cpu_device.cpp:869-1177). Uses a per-device scratch buffer. */
 DQ_API int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, float* y, int64_t y_stride,
@@ -169,8 +172,8 @@ DQ_API int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_st
 /* y = x . w^T (+ bias) with the activations quantized to format fmt (the caller's
  * choice of dynacore's activation contract, which KernelPlan makes per matmul:
  * dynacore/include/dynacore/kernel/kernel_plan.h:50-92). One quantize launch into
- * the per-device scratch, then dq_gemv (dq_gemm where it supports the pair and
- * m > DQ_GEMV_MAX_ROWS). Replaces Device::matmul under a chosen contract. */
+ * the per-device scratch, then dq_gemv (dq_gemm where it supports the pair at this
+ * m, as dq_matmul chooses). Replaces Device::matmul under a chosen contract. */
 DQ_API int dq_matmul_act(const dq_weight* w, int fmt, const float* x, int64_t m, int64_t x_stride, float* y,
                          int64_t y_stride, const float* bias, void* stream);
 

@@ -458,7 +458,7 @@ def test_error_paths(cuda):
         dq.gemv(w, dq.ACT_PER32, a, 1, 0, 9, y, 8)
     assert e.value.status == "invalid_argument"
     with pytest.raises(dq.DqError) as e:
-        dq.gemm(w, dq.ACT_PER32, a, 1, 0, 8, y, 8)
+        dq.gemm(w, dq.ACT_Q8_0, a, 1, 0, 8, y, 8)  # the block GEMM takes per-32 ActBlockQ8 only
     assert e.value.status == "unsupported"
 
 
@@ -1052,3 +1052,51 @@ def test_gemv_split_k(cuda, pair, m):
     yr = host(T.gemv(w, fmt, ad, n0=70, n1=200))
     assert np.array_equal(yr[:, 70:200].view(np.uint32), y1[:, 70:200].view(np.uint32))
     assert not yr[:, :70].any() and not yr[:, 200:].any()
+
+
+# ------------------------------------------- Q8_0 / Q4_0 GEMM (per-32 activations)
+
+
+@pytest.mark.parametrize("t", [O.Q8_0, O.Q4_0], ids=lambda t: O.TYPE_NAMES[t])
+@pytest.mark.parametrize("m,n,k", [(17, 200, 1280), (64, 256, 4096), (130, 320, 512), (300, 64, 96)])
+def test_gemm_b32_bit_exact(cuda, t, m, n, k):
+    """The block GEMM runs the generic per-block sequence acc = acc + (dw*da)*(float)P_b for
+    every output (kernels_generic.cpp:216-239): bit-identical to the oracle, edge weight
+    blocks and partial tiles (rows, weight rows and a 3-block K) included; through
+    dq_matmul (quantize + GEMM from 32 rows, the GEMV below) with a bias."""
+    from dynalm_amd import torch_ops as T
+
+    rows = weight_rows(t, n, k, 2100 + m + t, edge=True)
+    x = activations(m, k, 2110 + m)
+    a = O.quantize_act(O.ACT_PER32, x)
+    w = dq.Weight.upload(t, rows, k)
+    y = host(T.gemm(w, O.ACT_PER32, dev(a)))
+    want = O.matmul(t, O.ACT_PER32, rows, a, k)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+    bias = O.normal(2120 + m, n)
+    ym = host(T.matmul(w, dev(x), dev(bias)))
+    if m >= 32:
+        assert np.array_equal(ym.view(np.uint32), (want + bias).view(np.uint32))
+    else:
+        ok, worst = close(ym, want + bias)
+        assert ok, worst
+
+
+def test_gemm_b32_row_range_and_saturated_codes(cuda):
+    """A row range (unaligned ends) leaves the other outputs untouched; +-127 activations
+    against -128 / +127 Q8_0 codes (the largest block sums) stay exact."""
+    from dynalm_amd import torch_ops as T
+
+    k, n, m = 512, 192, 70
+    rows = weight_rows(O.Q8_0, n, k, 2130, edge=True).reshape(n, -1, 34)
+    rows[::3, :, 2:] = 0x80                                   # code -128
+    rows[1::3, :, 2:] = 0x7F
+    rows = rows.reshape(n, -1)
+    x = activations(m, k, 2131)
+    x[::2] = np.where(np.arange(k) % 2 == 0, 1.0, -1.0).astype(np.float32)  # every code +-127
+    a = O.quantize_act(O.ACT_PER32, x)
+    w = dq.Weight.upload(O.Q8_0, rows, k)
+    y = host(T.gemm(w, O.ACT_PER32, dev(a), n0=37, n1=150))
+    want = O.matmul(O.Q8_0, O.ACT_PER32, rows, a, k)
+    assert np.array_equal(y[:, 37:150].view(np.uint32), want[:, 37:150].view(np.uint32))
+    assert not y[:, :37].any() and not y[:, 150:].any()
