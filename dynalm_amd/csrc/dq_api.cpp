@@ -201,18 +201,27 @@ int check_out(const dq_weight* w, int64_t m, int64_t n0, int64_t n1, float* y, i
 // for 24..64 rows at K=4096, N=14336), LDS for the weight's super-blocks, and fp32
 // rows addressable with 32-bit offsets.
 // Whether dq_matmul / dq_matmul_act run m rows of this pair on a GEMM: above
-// DQ_GEMV_MAX_ROWS for Q4_K x Q8_K, from 32 rows for the 32-value block GEMM (Q8_0 /
+// DQ_GEMV_MAX_ROWS for Q4_K x Q8_K; from 32 rows for the 32-value block GEMM (Q8_0 /
 // Q4_0 x per-32; measured at K = 4096: 48-62 us for any m up to 128, where the GEMV
-// takes 31-33 us at 16 rows and 62-65 us at 32).
-bool use_gemm(int dtype, int fmt, int64_t m) {
-  if (!dq::gemm_supported(dtype, fmt)) return false;
-  return dtype == DQ_Q8_0 || dtype == DQ_Q4_0 ? m >= 32 : m > DQ_GEMV_MAX_ROWS;
+// takes 31-33 us at 16 rows and 62-65 us at 32); Q6_K x Q8_K above 64 rows, and above
+// 16 where the skinny GEMV's LDS does not hold the row's super-blocks (K = 14336:
+// 110 us against 171-611 us for 17..64 rows) or the weight has 4096 rows or more (the
+// GEMM's grid fills the CUs: 35 vs 45 us at K = 4096, N = 14336; with N = 1536 it
+// loses, 70 vs 23 us).
+bool use_gemm(const dq::WeightDev& w, int fmt, int64_t m) {
+  if (!dq::gemm_supported(w.dtype, fmt)) return false;
+  if (w.dtype == DQ_Q8_0 || w.dtype == DQ_Q4_0) return m >= 32;
+  if (w.dtype == DQ_Q6_K) {
+    return m > dq::kSkinnyMaxRows ||
+           (m > DQ_GEMV_MAX_ROWS && (!dq::gemv_mma_lds_ok(w.nblk, m) || w.n >= 4096));
+  }
+  return m > DQ_GEMV_MAX_ROWS;
 }
 
 bool skinny_ok(const dq_weight* w, const float* x, int64_t m, int64_t x_stride) {
   const int fmt = dq_act_format_for(w->dev.dtype);
   if (x == nullptr || !dq::gemv_mma_supported(w->dev.dtype, fmt, m)) return false;
-  if (use_gemm(w->dev.dtype, fmt, m)) return false;
+  if (use_gemm(w->dev, fmt, m)) return false;
   if (!dq::gemv_mma_lds_ok(w->dev.nblk, m)) return false;
   const int64_t xs = m > 1 ? x_stride : w->dev.k;
   return m * xs * 4 < ((int64_t)1 << 32);
@@ -444,7 +453,7 @@ int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, f
     std::vector<dq::GemvJob> j{dq::GemvJob{&w->dev, nullptr, 0, x, m > 1 ? x_stride : w->dev.k, m, y, y_stride, bias}};
     return run_skinny(j, w->dev.device, s);
   }
-  if (m > 1 && dq::gemv_mma_supported(w->dev.dtype, fmt, 2) && !use_gemm(w->dev.dtype, fmt, m)) {
+  if (m > 1 && dq::gemv_mma_supported(w->dev.dtype, fmt, 2) && !use_gemm(w->dev, fmt, m)) {
     // K-quants without a GEMM for this size (Q6_K), or inputs whose offsets exceed
     // 32 bits: quantize once, then skinny passes of up to 64 rows
     void* acts = nullptr;
@@ -452,7 +461,7 @@ int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, f
     if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, x_stride, acts, stream); rc != DQ_OK) return rc;
     return dq_gemv(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
   }
-  if (!use_gemm(w->dev.dtype, fmt, m)) {
+  if (!use_gemm(w->dev, fmt, m)) {
     // decode: quantization fused into the GEMV (one launch per pass of up to 8 rows)
     if (x == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
     if (m > 1 && x_stride < w->dev.k) {
@@ -606,7 +615,7 @@ int dq_matmul_act(const dq_weight* w, int fmt, const float* x, int64_t m, int64_
   void* acts = nullptr;
   if (int rc = scratch_get(w->dev.device, (size_t)(m * arb), s, &acts); rc != DQ_OK) return rc;
   if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, acts, stream); rc != DQ_OK) return rc;
-  if (use_gemm(w->dev.dtype, fmt, m)) {
+  if (use_gemm(w->dev, fmt, m)) {
     return dq_gemm(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
   }
   return dq_gemv(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);

@@ -1,4 +1,4 @@
-// dq_gemm.hip -- prefill GEMM for Q4_K weights x Q8_K activations on gfx950 int8
+// dq_gemm.hip -- prefill GEMM for Q4_K and Q6_K weights x Q8_K activations on gfx950 int8
 // MFMA (v_mfma_i32_16x16x64_i8) with the mins on fp16 MFMA (v_mfma_f32_16x16x16_f16).
 //
 // Per super-block b (256 values) and output (m, n), the arithmetic contract is
@@ -165,6 +165,52 @@ DQ_DEV PrepB prep_tile(const RawB& r, u32 sel_sc, u32 sel_mn) {
     const u32 kl = __builtin_amdgcn_perm(0u, SL, sel_u16x2(s));
     p.H[s] = v4u{mul_bytes(qb[s].x, kh), mul_bytes(qb[s].y, kh), mul_bytes(qb[s].z, kh), mul_bytes(qb[s].w, kh)};
     p.L[s] = v4u{mul_bytes(qb[s].x, kl), mul_bytes(qb[s].y, kl), mul_bytes(qb[s].z, kl), mul_bytes(qb[s].w, kl)};
+  }
+  return p;
+}
+
+// Q6_K: w = sc_u (q - 32) (|w| <= 4096) of four codes (bytes of q, 0..63) with the
+// unit scale sc (-128..127), split exactly into int8 operands w = 64 wh + wl with
+// wh = floor(w / 64) in -64..64 and wl in 0..63; 16-bit lane arithmetic, two codes per
+// operation.
+DQ_DEV void q6_split(u32 q, int sc, u32& H, u32& L) {
+  typedef short s2 __attribute__((ext_vector_type(2)));
+  const s2 e = __builtin_bit_cast(s2, __builtin_amdgcn_perm(0u, q, 0x0C010C00u));  // codes 0, 1
+  const s2 o = __builtin_bit_cast(s2, __builtin_amdgcn_perm(0u, q, 0x0C030C02u));  // codes 2, 3
+  const s2 k = {(short)sc, (short)sc}, c = {(short)(-32 * sc), (short)(-32 * sc)};
+  const s2 we = e * k + c, wo = o * k + c;
+  const s2 he = we >> (short)6, ho = wo >> (short)6;
+  const s2 m63 = {63, 63};
+  const s2 le = we & m63, lo = wo & m63;
+  H = __builtin_amdgcn_perm(__builtin_bit_cast(u32, ho), __builtin_bit_cast(u32, he), 0x06040200u);
+  L = __builtin_amdgcn_perm(__builtin_bit_cast(u32, lo), __builtin_bit_cast(u32, le), 0x06040200u);
+}
+
+// The B operands of one Q6_K tile row for lane group lg: K-step s takes unit lg + 4s,
+// the low (even s) or high (odd s) nibbles of ql chunk lg + 4(s>>1) -- values
+// 128p + 16(c%4) + i (+ 64 for the high nibbles) with p = c/4
+// (dynacore/src/quantization/quant_formats.cpp:192-216) -- with their top two bits
+// from qh chunk 2p + c%2, bit pair (c%4)/2 (+2 for the high nibbles).
+DQ_DEV PrepB prep_tile_q6(v4u scw, v4u w0, v4u w1, v4u h0, v4u h1, int lg) {
+  PrepB p;
+  p.d = 0.0f;
+  p.dmin = 0.0f;
+  const int sh = 2 * (lg >> 1);
+  v4u q[4];
+  q[0] = (w0 & 0x0F0F0F0Fu) | (((h0 >> sh) & 0x03030303u) << 4);
+  q[1] = ((w0 >> 4) & 0x0F0F0F0Fu) | (((h0 >> (sh + 4)) & 0x03030303u) << 4);
+  q[2] = (w1 & 0x0F0F0F0Fu) | (((h1 >> sh) & 0x03030303u) << 4);
+  q[3] = ((w1 >> 4) & 0x0F0F0F0Fu) | (((h1 >> (sh + 4)) & 0x03030303u) << 4);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int sc = sbfe(scw[s], 8 * lg, 8);  // scale byte lg + 4s
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      u32 h, l;
+      q6_split(q[s][w], sc, h, l);
+      p.H[s][w] = h;
+      p.L[s][w] = l;
+    }
   }
   return p;
 }
@@ -388,8 +434,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 // each wave unpacks 16-row weight tiles into the sh*q / sl*q bytes of the MFMA
 // operand layout and stores them in LDS, so the VALU work per MFMA left in the
 // compute phase is the fp32 epilogue, about two operations per MFMA.
-template <int WM, int WN, int NT>
+template <int WT, int WM, int WN, int NT>
 struct Big {
+  static constexpr bool kQ6 = WT == kQ6_K;
   static constexpr int kWaves = WM * WN, kThreads = 64 * kWaves;
   static constexpr int kBM = 64 * WM, kBN = 16 * NT * WN;  // activation rows x weight rows
   static constexpr int kTiles = NT * WN;                    // 16-row weight tiles
@@ -397,24 +444,28 @@ struct Big {
   static constexpr int kGroups = kBN / 64;                  // 64-row groups of the weight layout
   static constexpr int kA = 0;                        // [kBM rows][16 slots][16 B] codes, chunk q at slot q ^ (row & 15)
   static constexpr int kHL = kA + kBM * 256;          // [tiles][4 steps][H, L][64 lanes][16 B] B operands
-  static constexpr int kW = kHL + kTiles * 8192;      // [8 chunks][kBN rows][16 B] nibbles as in the weight plane
-  static constexpr int kH = kW + 8 * kBN * 16;        // [kBN rows][16 B] headers
-  static constexpr int kBS = kH + kBN * 16;           // [kBM rows][16] bsums (int16)
-  static constexpr int kDA = kBS + kBM * 32;          // [2][kBM rows] activation scale d (two buffers)
+  static constexpr int kW = kHL + kTiles * 8192;      // [8 chunks][kBN rows][16 B] nibbles (Q6_K: ql) as in the plane
+  static constexpr int kH = kW + 8 * kBN * 16;        // [kBN rows][16 B] headers (Q6_K: the 16 scales)
+  static constexpr int kQH = kH + kBN * 16;           // Q6_K: [4 chunks][kBN rows][16 B] qh
+  static constexpr int kBS = kQH + (kQ6 ? 4 * kBN * 16 : 0);  // Q4_K: [kBM rows][16] bsums; Q6_K: [kBN] fp16 d
+  static constexpr int kDA = kBS + (kQ6 ? kBN * 2 : kBM * 32);  // [2][kBM rows] activation scale d (two buffers)
   static constexpr int kLds = kDA + 2 * kBM * 4;
   static_assert(kPrep >= 1 && kTiles % kWaves == 0, "each wave unpacks whole tiles");
-  static_assert(kBN % 64 == 0 && kBM / 32 == kWaves && (8 * kGroups) % kWaves == 0, "staging roles");
+  static_assert(kBN % 64 == 0 && (8 * kGroups) % kWaves == 0, "staging roles");
+  static_assert(kQ6 ? (4 * kGroups) % kWaves == 0 : kBM / 32 == kWaves, "staging roles");
   static_assert(kLds <= 160 * 1024, "LDS");
 };
 
-template <int WM, int WN, int NT>
+template <int WT, int WM, int WN, int NT>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_q4k_big(
-    const uint8_t* __restrict__ qs_plane, const uint8_t* __restrict__ hdr_plane, int nb, int64_t n_pad, int64_t nt0,
+    const uint8_t* __restrict__ qs_plane, const uint8_t* __restrict__ hdr_plane, const uint8_t* __restrict__ plane2,
+    const uint8_t* __restrict__ plane3, int nb, int64_t n_pad, int64_t nt0,
     int64_t n0, int64_t n1, const uint8_t* __restrict__ acts, int64_t arb, int64_t m, float* __restrict__ y, int64_t ys,
     const float* __restrict__ bias, int tiles_n, int tiles_m) {
-  using C = Big<WM, WN, NT>;
-  constexpr int kBM = C::kBM, kBN = C::kBN, kA = C::kA, kHL = C::kHL, kW = C::kW, kH = C::kH, kBS = C::kBS,
-                kDA = C::kDA;
+  using C = Big<WT, WM, WN, NT>;
+  constexpr bool kQ6 = C::kQ6;
+  constexpr int kBM = C::kBM, kBN = C::kBN, kA = C::kA, kHL = C::kHL, kW = C::kW, kH = C::kH, kQH = C::kQH,
+                kBS = C::kBS, kDA = C::kDA;
   extern __shared__ __align__(16) uint8_t lds[];
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -434,8 +485,13 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
   const int64_t G0 = nbase >> 6;
   const int64_t gl = n_pad / kRowGroup - G0;
   const int64_t gspan = gl < C::kGroups ? gl : C::kGroups;
+  // Q4_K planes: qs (128 B per row and super-block), header (16 B). Q6_K: ql (128 B),
+  // qh (64 B), scales (16 B), d (2 B).
   const auto rq = rsrc(qs_plane + G0 * nb * 8192, (u32)(gspan * nb * 8192));
-  const auto rh = rsrc(hdr_plane + G0 * nb * 1024, (u32)(gspan * nb * 1024));
+  const uint8_t* hp = kQ6 ? plane2 : hdr_plane;
+  const auto rh = rsrc(hp + G0 * nb * 1024, (u32)(gspan * nb * 1024));
+  const auto rqh = rsrc((kQ6 ? hdr_plane : qs_plane) + G0 * nb * 4096, (u32)(gspan * nb * 4096));
+  const auto rd6 = rsrc((kQ6 ? plane3 : qs_plane) + G0 * nb * 128, (u32)(gspan * nb * 128));
 
   // ---- staging roles (direct-to-LDS, per super-block)
   // activation codes: wave w, instruction j fills rows 4 (8w + j) .. + 3; the
@@ -463,7 +519,21 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     if (wave < C::kGroups) {
       ld_lds16(rh, lds + kH + 64 * wave * 16, (u32)(wave * nb * 1024 + lane * 16), (u32)(b * 1024));
     }
-    ld_lds16(ra, lds + kBS + 32 * wave * 32, bsoff, (u32)(b * 292));
+    if constexpr (kQ6) {
+      // qh: instruction i = kHI w + j stages chunk i / kGroups of group i % kGroups
+      constexpr int kHI = 4 * C::kGroups / C::kWaves;
+#pragma unroll
+      for (int j = 0; j < kHI; ++j) {
+        const int i = kHI * wave + j, c = i / C::kGroups, k = i % C::kGroups;
+        ld_lds16(rqh, lds + kQH + (c * kBN + 64 * k) * 16, (u32)(k * nb * 4096 + lane * 16), (u32)(b * 4096 + c * 1024));
+      }
+      // d: 64 rows x 2 B per group, one 4-byte piece per lane
+      if (wave == 0 && lane < 32 * C::kGroups) {
+        ld_lds4(rd6, lds + kBS, (u32)((lane >> 5) * nb * 128 + 4 * (lane & 31)), (u32)(b * 128));
+      }
+    } else {
+      ld_lds16(ra, lds + kBS + 32 * wave * 32, bsoff, (u32)(b * 292));
+    }
     constexpr int kDI = kBM / 64;  // activation-scale instructions, on the last waves
     if (wave >= C::kWaves - kDI) {
       const int k = wave - (C::kWaves - kDI);
@@ -476,7 +546,11 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
   const int arow = 64 * wm + li;
   int a_rd[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) a_rd[s] = kA + arow * 256 + 16 * ((qlg ^ li) ^ (8 * (s >> 1) + 2 * (s & 1)));
+  for (int s = 0; s < 4; ++s) {
+    // Q4_K: chunk qlg + 8(s>>1) + 2(s&1); Q6_K: unit lg + 4s (see prep_tile_q6)
+    a_rd[s] = kQ6 ? kA + arow * 256 + 16 * ((lg ^ li) ^ (4 * s))
+                  : kA + arow * 256 + 16 * ((qlg ^ li) ^ (8 * (s >> 1) + 2 * (s & 1)));
+  }
   const int bs_rd = kBS + arow * 32 + 8 * lg;
   const int da_rd = kDA + (64 * wm + 4 * lg) * 4;
   const u32 sel_sc = (lg >> 1) ? 0x07060302u : 0x05040100u;
@@ -509,9 +583,17 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     for (int i = 0; i < C::kPrep; ++i) {
       const int p = C::kPrep * wave + i;
       const int row = 16 * p + li;
-      const RawB r{lds_ld16(lds, kH + row * 16), lds_ld16(lds, kW + (lg * kBN + row) * 16),
-                   lds_ld16(lds, kW + ((lg + 4) * kBN + row) * 16)};
-      const PrepB q = prep_tile(r, sel_sc, sel_mn);
+      PrepB q;
+      if constexpr (kQ6) {
+        q = prep_tile_q6(lds_ld16(lds, kH + row * 16), lds_ld16(lds, kW + (lg * kBN + row) * 16),
+                         lds_ld16(lds, kW + ((lg + 4) * kBN + row) * 16),
+                         lds_ld16(lds, kQH + ((lg & 1) * kBN + row) * 16),
+                         lds_ld16(lds, kQH + ((2 + (lg & 1)) * kBN + row) * 16), lg);
+      } else {
+        const RawB r{lds_ld16(lds, kH + row * 16), lds_ld16(lds, kW + (lg * kBN + row) * 16),
+                     lds_ld16(lds, kW + ((lg + 4) * kBN + row) * 16)};
+        q = prep_tile(r, sel_sc, sel_mn);
+      }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         *reinterpret_cast<v4u*>(lds + kHL + ((p * 4 + s) * 2 + 0) * 1024 + lane * 16) = q.H[s];
@@ -524,15 +606,22 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) a[mt][s] = lds_ld16(lds, a_rd[s] + mt * 16 * 256);
-      const v2u bs = lds_ld8(lds, bs_rd + mt * 16 * 32);
-      const v4u bsf = bsums_f16(v4u{bs.x, bs.y, 0, 0});
-      am[mt] = __builtin_bit_cast(h4_t, v2u{bsf.x, bsf.y});
+      if constexpr (!kQ6) {
+        const v2u bs = lds_ld8(lds, bs_rd + mt * 16 * 32);
+        const v4u bsf = bsums_f16(v4u{bs.x, bs.y, 0, 0});
+        am[mt] = __builtin_bit_cast(h4_t, v2u{bsf.x, bsf.y});
+      }
     }
     Sc sc[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const v4u hd = lds_ld16(lds, kH + (16 * NT * wn + 16 * nt + li) * 16);
-      sc[nt] = Sc{h2f(hd.x), h2f(hd.x >> 16), mins_f16(hd, sel_mn)};
+      const int row = 16 * NT * wn + 16 * nt + li;
+      if constexpr (kQ6) {
+        sc[nt] = Sc{h2f(*reinterpret_cast<const uint16_t*>(lds + kBS + 2 * row)), 0.0f, h4_t{}};
+      } else {
+        const v4u hd = lds_ld16(lds, kH + row * 16);
+        sc[nt] = Sc{h2f(hd.x), h2f(hd.x >> 16), mins_f16(hd, sel_mn)};
+      }
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -555,10 +644,16 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     auto epi = [&](const Tacc& r, const Sc& c, int nt, int mt, f4_t da) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int S = r.L[e] + (r.H[e] << 3);
-        float u = c.d * (float)S;
-        u = fmaf(-c.dmin, r.M[e], u);
-        acc[nt][mt][e] = fmaf(da[e], u, acc[nt][mt][e]);
+        if constexpr (kQ6) {
+          // S = 64 sum(wh a) + sum(wl a); u = d (float)S; acc = fma(da, u, acc)
+          const int S = r.L[e] + (r.H[e] << 6);
+          acc[nt][mt][e] = fmaf(da[e], c.d * (float)S, acc[nt][mt][e]);
+        } else {
+          const int S = r.L[e] + (r.H[e] << 3);
+          float u = c.d * (float)S;
+          u = fmaf(-c.dmin, r.M[e], u);
+          acc[nt][mt][e] = fmaf(da[e], u, acc[nt][mt][e]);
+        }
       }
     };
     // The two waves of a SIMD (w and w + 4) leave the barrier together; starting
@@ -589,7 +684,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
         cur.L = mfma(a[mt][0], Lc[0], z);
 #pragma unroll
         for (int s = 1; s < 4; ++s) cur.L = mfma(a[mt][s], Lc[s], cur.L);
-        cur.M = mfma_h(am[mt], sc[nt].mb, f4_t{0.0f, 0.0f, 0.0f, 0.0f});
+        if constexpr (!kQ6) cur.M = mfma_h(am[mt], sc[nt].mb, f4_t{0.0f, 0.0f, 0.0f, 0.0f});
         __builtin_amdgcn_s_setprio(0);
         if (nt + mt > 0) epi(prev, sc[pn], pn, pm, dp);
         prev = cur;
@@ -649,7 +744,9 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
   }
 }
 
-bool gemm_supported(int dtype, int af) { return (dtype == kQ4_K && af == kActQ8_K) || gemm_b32_supported(dtype, af); }
+bool gemm_supported(int dtype, int af) {
+  return ((dtype == kQ4_K || dtype == kQ6_K) && af == kActQ8_K) || gemm_b32_supported(dtype, af);
+}
 
 namespace {
 
@@ -680,14 +777,14 @@ hipError_t launch_cfg(const WeightDev& w, const uint8_t* acts, int64_t arb, int6
   return hipGetLastError();
 }
 
-template <int WM, int WN, int NT>
+template <int WT, int WM, int WN, int NT>
 hipError_t launch_big(const WeightDev& w, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
                       float* y, int64_t ys, const float* bias, hipStream_t s) {
-  using C = Big<WM, WN, NT>;
+  using C = Big<WT, WM, WN, NT>;
   static bool attr_set[64] = {};
   const int dev = w.device < 64 ? w.device : 63;
   if (!attr_set[dev]) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_q4k_big<WM, WN, NT>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_q4k_big<WT, WM, WN, NT>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds);
     if (e != hipSuccess) return e;
     attr_set[dev] = true;
@@ -699,9 +796,9 @@ hipError_t launch_big(const WeightDev& w, const uint8_t* acts, int64_t arb, int6
       tiles_n * tiles_m >= (1ll << 31)) {
     return hipErrorInvalidValue;
   }
-  hipLaunchKernelGGL((k_gemm_q4k_big<WM, WN, NT>), dim3((unsigned)(tiles_n * tiles_m)), dim3(C::kThreads), C::kLds, s,
-                     w.plane[0], w.plane[1], (int)w.nblk, w.n_pad, nt0, n0, n1, acts, arb, m, y, ys, bias,
-                     (int)tiles_n, (int)tiles_m);
+  hipLaunchKernelGGL((k_gemm_q4k_big<WT, WM, WN, NT>), dim3((unsigned)(tiles_n * tiles_m)), dim3(C::kThreads), C::kLds,
+                     s, w.plane[0], w.plane[1], w.plane[2], w.plane[3], (int)w.nblk, w.n_pad, nt0, n0, n1, acts, arb, m,
+                     y, ys, bias, (int)tiles_n, (int)tiles_m);
   return hipGetLastError();
 }
 
@@ -714,12 +811,17 @@ hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t 
   if (m == 0 || n1 <= n0) return hipSuccess;
   const int cus = w.cus > 0 ? w.cus : 256;
   const int64_t rows = n1 - (n0 / kRowGroup) * kRowGroup;
-  if (m > 128) {
+  if (w.dtype == kQ6_K || m > 128) {
     // the 8-wave 256 x 128 tile when its grid fills the GPU (M = 512 at N = 14336:
-    // 224 workgroups, one round), else the 4-wave 128 x 64 tile (two per CU)
+    // 224 workgroups, one round), else the 4-wave 128 x 64 tile (two per CU); Q6_K has
+    // only these kernels
     const int64_t wgs = (rows + 127) / 128 * ((m + 255) / 256);
-    if (wgs * 8 >= (int64_t)cus * 7) return launch_big<4, 2, 4>(w, acts, arb, m, n0, n1, y, ys, bias, s);
-    return launch_big<2, 2, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+    if (w.dtype == kQ6_K) {
+      if (wgs * 8 >= (int64_t)cus * 7) return launch_big<kQ6_K, 4, 2, 4>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+      return launch_big<kQ6_K, 2, 2, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+    }
+    if (wgs * 8 >= (int64_t)cus * 7) return launch_big<kQ4_K, 4, 2, 4>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+    return launch_big<kQ4_K, 2, 2, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s);
   }
   // up to 128 rows: the 4-wave kernel with 64 or 128 activation rows; the weight-tile
   // width is picked by rounds of workgroups over the CUs times the per-wave work

@@ -153,7 +153,7 @@ DQ_API int dq_act_quantize(int fmt, const float* x, int64_t m, int64_t k, int64_
  * Any m: the weights are streamed once per pass of up to 4 activation rows. */
 DQ_API int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0, int64_t n1, float* y,
                    int64_t y_stride, const float* bias, void* stream);
-/* dq_gemm runs the int8 MFMA GEMM: Q4_K weights with DQ_ACT_Q8_K activations, and
+/* dq_gemm runs the int8 MFMA GEMM: Q4_K and Q6_K weights with DQ_ACT_Q8_K activations, and
  * Q8_0 / Q4_0 weights with DQ_ACT_PER32 (each output in the reference's generic
  * per-32 block order, kernels_generic.cpp:216-239); other pairs return
  * DQ_UNSUPPORTED; any m.
@@ -162,8 +162,8 @@ DQ_API int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int
                    int64_t y_stride, const float* bias, void* stream);
 
 /* y = x . w^T (+ bias): quantize x with dq_act_format_for(w), then GEMV or GEMM by
- * m (Q4_K: GEMM above DQ_GEMV_MAX_ROWS; Q8_0 / Q4_0: GEMM from 32 rows; Q6_K: the
- * skinny MFMA GEMV in passes of 64 rows). Replaces Device::matmul
+ * m (Q4_K: GEMM above DQ_GEMV_MAX_ROWS; Q8_0 / Q4_0: GEMM from 32 rows; Q6_K: GEMM
+ * above 64 rows, or above 16 for weights of >= 4096 rows or long K). Replaces Device::matmul
  * (dynacore/include/dynacore/device/device.h:161; CpuDevice::matmul,
  * dynacore/cpu/cpu_device.cpp:869-1177). Uses a per-device scratch buffer. */
 DQ_API int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, float* y, int64_t y_stride,

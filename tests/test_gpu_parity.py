@@ -1100,3 +1100,54 @@ def test_gemm_b32_row_range_and_saturated_codes(cuda):
     want = O.matmul(O.Q8_0, O.ACT_PER32, rows, a, k)
     assert np.array_equal(y[:, 37:150].view(np.uint32), want[:, 37:150].view(np.uint32))
     assert not y[:, :37].any() and not y[:, 150:].any()
+
+
+# ------------------------------------------------------------- Q6_K GEMM
+
+
+@pytest.mark.parametrize("m,n,k", [(65, 300, 512), (200, 128, 1280), (512, 256, 2048), (300, 14336, 256)])
+def test_gemm_q6k_bit_exact(cuda, m, n, k):
+    """Q6_K x Q8_K on the large GEMM kernels: w = sc (q - 32) split exactly into int8
+    operands 64 wh + wl, S = 64 sum(wh a) + sum(wl a) per super-block, combined in the
+    canonical order u = d (float)S, acc = fma(da, u, acc): bit-identical to the oracle and
+    to the GEMV (edge blocks: saturated and negative scales, d = 0)."""
+    from dynalm_amd import torch_ops as T
+
+    rows = weight_rows(O.Q6_K, n, k, 2200 + m, edge=True)
+    x = activations(m, k, 2210 + m)
+    a = O.quantize_act(O.ACT_Q8_K, x)
+    w = dq.Weight.upload(O.Q6_K, rows, k)
+    ad = dev(a)
+    y = host(T.gemm(w, O.ACT_Q8_K, ad))
+    want = O.matmul(O.Q6_K, O.ACT_Q8_K, rows, a, k)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+    yv = host(T.gemv(w, O.ACT_Q8_K, ad[:5]))
+    assert np.array_equal(yv.view(np.uint32), y[:5].view(np.uint32))
+
+
+def test_gemm_q6k_extreme_codes_and_route(cuda):
+    """Saturated operands (codes 0 and 63, scales -128 and 127, activations +-127 and
+    -128-free Q8_K rows) stay exact; dq_matmul sends 40 rows at K = 14336 (whose super-
+    blocks do not fit the skinny kernel's LDS) to the GEMM, and 70 rows at any K."""
+    from dynalm_amd import torch_ops as T
+
+    k, n, m = 512, 192, 80
+    rows = weight_rows(O.Q6_K, n, k, 2230, edge=True).reshape(n, -1, 210)
+    rows[::4, :, 0:192] = 0x00                                 # ql = qh = 0: code 0 (q - 32 = -32)
+    rows[1::4, :, 0:192] = 0xFF                                # code 63
+    rows[::4, :, 192:208] = 0x80                               # scale -128
+    rows[1::4, :, 192:208] = 0x7F
+    rows = rows.reshape(n, -1)
+    x = activations(m, k, 2231)
+    x[::3] = np.where(np.arange(k) % 2 == 0, 1.0, -1.0).astype(np.float32)
+    a = O.quantize_act(O.ACT_Q8_K, x)
+    w = dq.Weight.upload(O.Q6_K, rows, k)
+    y = host(T.gemm(w, O.ACT_Q8_K, dev(a)))
+    assert np.array_equal(y.view(np.uint32), O.matmul(O.Q6_K, O.ACT_Q8_K, rows, a, k).view(np.uint32))
+    for k2, m2 in ((14336, 40), (1024, 70)):
+        rows2 = gguf_weights(O.Q6_K, 256, k2, 2240 + m2, outlier_frac=0.01)
+        x2 = activations(m2, k2, 2241)
+        w2 = dq.Weight.upload(O.Q6_K, rows2, k2)
+        y2 = host(T.matmul(w2, dev(x2)))
+        want2 = O.matmul(O.Q6_K, O.ACT_Q8_K, rows2, O.quantize_act(O.ACT_Q8_K, x2), k2)
+        assert np.array_equal(y2.view(np.uint32), want2.view(np.uint32))
