@@ -255,6 +255,42 @@ def prefill_sweep(ms: list[int], weights, gen) -> list[dict]:
     return out
 
 
+def prefill_other_types(gen) -> list[dict]:
+    """dq_matmul at M = 512 for the other weight types of a Q4_K_M / Q8_0 / Q4_0 model:
+    Q6_K FFN down (K=14336 N=4096) on the Q6_K GEMM, Q8_0 4096 x 4096 and Q4_0
+    K=4096 N=14336 on the 32-value block GEMM (quantization included, 2 rotated copies)."""
+    import torch
+
+    import dynalm_amd as dq
+
+    out = []
+    m = 512
+    for name, dtype, n, k in (("q6_K", dq.Q6_K, 4096, 14336), ("q8_0", dq.Q8_0, 4096, 4096),
+                              ("q4_0", dq.Q4_0, 14336, 4096)):
+        rb = k // 256 * 210 if dtype == dq.Q6_K else k // 32 * (34 if dtype == dq.Q8_0 else 18)
+        rng = np.random.default_rng(dtype)
+        ws = []
+        for _ in range(2):
+            rows = rng.integers(0, 256, (n, rb), dtype=np.uint8)
+            if dtype == dq.Q6_K:
+                rows = random_rows(16, n, k, int(rng.integers(1 << 30)))
+            else:  # fp16 d in U(0.002, 0.02) at the start of each block
+                bb = 34 if dtype == dq.Q8_0 else 18
+                blk = rows.reshape(n, -1, bb)
+                blk[:, :, 0:2] = rng.uniform(0.002, 0.02, blk.shape[:2]).astype(np.float16).view(np.uint8).reshape(
+                    n, -1, 2)
+            ws.append(dq.Weight.upload(dtype, rows, k))
+        x = torch.randn((m, k), generator=gen, device="cuda", dtype=torch.float32)
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        log(f"prefill {name} M={m}")
+        ms_call = time_graph(lambda i, st: dq.matmul(ws[i % 2], x, m, k, y, n, None, st), 20, 3)
+        tops = 2.0 * m * n * k / (ms_call * 1e-3) / 1e12
+        out.append({"weights": f"{name} K={k} N={n}", "m": m, "ms_per_call": round(ms_call, 4), "tops": round(tops, 1),
+                    "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2)})
+        del ws, x, y
+    return out
+
+
 COPY_BYTES = 64 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_m1_gemm_m512_traffic.md")
 
@@ -468,6 +504,8 @@ def main() -> None:
         }
     if args.sweep:
         result["prefill_sweep"] = prefill_sweep([int(v) for v in args.sweep.split(",")], weights, gen)
+    if args.sweep:
+        result["prefill_other_types_m512"] = prefill_other_types(gen)
     if args.stack_steps > 0:
         log(f"config 5 decode stack x{args.stack_steps}")
         result["decode_stack_m16"] = decode_stack(args.stack_steps, stream)
