@@ -81,9 +81,11 @@ hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s);
 // Work of one grouped launch of these jobs (<= 8, one nblk) in wave-sized units
 // (workgroups x super-blocks): each unit of a launch on fp32 rows quantizes 16
 // activation rows of one super-block again, so the caller quantizes once instead
-// when this is large.
+// when this is large. The in-kernel quantization lengthens every wave's critical
+// path: at M = 16 a 1536 x 1536 Q4_K matmul (576 units) ran 7.8 us fused and
+// 1.8 + 3.8 us as a quantize launch plus the GEMV, so only small launches fuse.
 int64_t skinny_units(const GemvJob* jobs, int count);
-constexpr int64_t kSkinnyFuseMaxUnits = 1024;
+constexpr int64_t kSkinnyFuseMaxUnits = 128;
 // The gated M = 1 decode GEMV: y[i] = act(x . wg_i) * (x . wu_i) for one fp32 row x,
 // K-quant weights of one type and shape, activations quantized in the kernel.
 // hipErrorInvalidValue when the pair or its LDS is not supported.

@@ -21,7 +21,7 @@
 // sc_u at every position of sub-block u gives the -32 correction
 // (dequantize_q6_K layout, quant_formats.cpp:192-216).
 //
-// Workgroup: 8 waves over 16 * CT weight rows (CT MFMA column tiles) and all
+// Workgroup: 4 or 8 waves over 16 * CT weight rows (CT MFMA column tiles) and all
 // super-blocks, wave w taking a contiguous slice of super-blocks. CT = 4 (a whole
 // 64-row group) reads each activation super-block once per 64 weight rows instead
 // of once per 16 (for launches with many workgroups); CT = 1 gives 4x the
@@ -376,10 +376,10 @@ DQ_DEV void skinny_wave(const SkinnyJob& J, const uint8_t* const* p, int nblk, i
   }
 }
 
-template <int CT, int MT, bool kFused, bool kGated>
-__global__ __launch_bounds__(kSkinnyWaves * 64) void k_skinny(SkinnyGroup g) {
+// W waves per workgroup (4 or 8; launch_group picks it from the launch's shape).
+template <int CT, int MT, bool kFused, bool kGated, int W>
+__global__ __launch_bounds__(W * 64) void k_skinny(SkinnyGroup g) {
   extern __shared__ __align__(16) uint8_t lds[];
-  constexpr int W = kSkinnyWaves;
   constexpr int NC = 16 * CT, NR = 16 * MT;
   const int wg = blockIdx.x;
   int j = 0;
@@ -414,6 +414,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void k_skinny(SkinnyGroup g) {
   for (int o = threadIdx.x; o < NR * NC; o += W * 64) {
     const int mm = o / NC, c = o % NC;
     float v = 0.0f, vu = 0.0f;
+#pragma unroll 8
     for (int b = 0; b < nblk; ++b) {
       const float da = dal[b * NR + mm];
       v = fmaf(da, tt[(b * NR + mm) * NC + c], v);
@@ -435,16 +436,16 @@ size_t skinny_lds(int64_t nblk, int ct, int mt, bool gated = false) {
 }
 constexpr size_t kSkinnyMaxLds = 160 * 1024;
 
-template <int CT, int MT, bool kFused, bool kGated = false>
+template <int CT, int MT, bool kFused, bool kGated = false, int W = kSkinnyWaves>
 hipError_t skinny_launch(const SkinnyGroup& g, int wgs, hipStream_t s) {
   const size_t lds = skinny_lds(g.nblk, CT, MT, kGated);
   if (lds > kSkinnyMaxLds) return hipErrorInvalidValue;
   if (lds > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_skinny<CT, MT, kFused, kGated>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_skinny<CT, MT, kFused, kGated, W>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((k_skinny<CT, MT, kFused, kGated>), dim3((unsigned)wgs), dim3(kSkinnyWaves * 64), lds, s, g);
+  hipLaunchKernelGGL((k_skinny<CT, MT, kFused, kGated, W>), dim3((unsigned)wgs), dim3(W * 64), lds, s, g);
   return hipGetLastError();
 }
 
@@ -488,13 +489,21 @@ hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t*
     wgs += (last_row[i] + nc - 1) / nc - first_row[i] / nc;
   }
   if (wgs >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+  // Waves per workgroup: launches of more tiles than CUs whose tiles have few
+  // super-blocks (at most 12, gate and up counted), and the 64-row tiles, run 4
+  // waves so that more workgroups are resident (measured at M = 16: gate 8960 x 1536
+  // 7.3 -> 6.7 us, gated 13.3 -> 11.2 us, a 151936 x 1536 Q6_K LM head 80 -> 68 us).
+  const bool four = ct == 4 || (!fused && mt == 1 && wgs > cus && g.nblk * (gated ? 2 : 1) <= 12);
   if (gated) {
     if (mt == 4) return skinny_launch<1, 4, false, true>(g, (int)wgs, s);
-    return fused ? skinny_launch<1, 1, true, true>(g, (int)wgs, s) : skinny_launch<1, 1, false, true>(g, (int)wgs, s);
+    if (fused) return skinny_launch<1, 1, true, true>(g, (int)wgs, s);
+    return four ? skinny_launch<1, 1, false, true, 4>(g, (int)wgs, s) : skinny_launch<1, 1, false, true>(g, (int)wgs, s);
   }
   if (mt == 4) return skinny_launch<1, 4, false>(g, (int)wgs, s);
-  if (ct == 4) return fused ? skinny_launch<4, 1, true>(g, (int)wgs, s) : skinny_launch<4, 1, false>(g, (int)wgs, s);
-  return fused ? skinny_launch<1, 1, true>(g, (int)wgs, s) : skinny_launch<1, 1, false>(g, (int)wgs, s);
+  if (ct == 4) return fused ? skinny_launch<4, 1, true, false, 4>(g, (int)wgs, s)
+                            : skinny_launch<4, 1, false, false, 4>(g, (int)wgs, s);
+  if (fused) return skinny_launch<1, 1, true>(g, (int)wgs, s);
+  return four ? skinny_launch<1, 1, false, false, 4>(g, (int)wgs, s) : skinny_launch<1, 1, false>(g, (int)wgs, s);
 }
 
 }  // namespace

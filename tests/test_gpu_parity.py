@@ -533,6 +533,33 @@ def test_skinny_activation_tiles_and_passes(cuda, t, m):
         assert ok, f"worst error ratio {worst:.3g}"
 
 
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q6_K], ids=lambda t: O.TYPE_NAMES[t])
+@pytest.mark.parametrize("m,n,k", [(16, 1536, 8960), (2, 200, 4096), (9, 40, 14336)])
+def test_skinny_long_rows_bit_exact(cuda, t, m, n, k):
+    """Pre-quantized matmuls of few 16-row tiles and long rows (the FFN down
+    projection's shape: 96 tiles of 35 super-blocks; 3 tiles of 56): bit-identical to
+    the oracle, with a bias, and with an output row range that leaves the other rows
+    untouched."""
+    from dynalm_amd import torch_ops as T
+
+    seed = 1300 + m + t
+    w_rows = gguf_weights(t, n, k, seed, outlier_frac=0.01)
+    x = activations(m, k, seed + 1)
+    a = O.quantize_act(O.ACT_Q8_K, x)
+    bias = O.normal(seed + 2, n)
+    w = dq.Weight.upload(t, w_rows, k)
+    want = O.matmul(t, O.ACT_Q8_K, w_rows, a, k, bias=bias)
+    y = host(T.gemv(w, O.ACT_Q8_K, dev(a), bias=dev(bias)))
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+    n0, n1 = 5, n - 3
+    out = torch.full((m, n), 777.0, device="cuda")
+    y2 = host(T.gemv(w, O.ACT_Q8_K, dev(a), n0=n0, n1=n1, bias=dev(bias), out=out))
+    assert np.array_equal(y2[:, n0:n1].view(np.uint32), want[:, n0:n1].view(np.uint32))
+    assert np.all(y2[:, :n0] == 777.0) and np.all(y2[:, n1:] == 777.0)
+    y3 = host(T.matmul(w, dev(x), bias=dev(bias)))
+    assert np.array_equal(y3.view(np.uint32), want.view(np.uint32))
+
+
 # ------------------------------------------------------ act_mul, matmul_gated
 
 ACTS = [O.SILU, O.GELU, O.GELU_TANH]
