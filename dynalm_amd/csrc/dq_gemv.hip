@@ -1142,7 +1142,7 @@ static hipError_t gemv_launch(const WeightDev& w, const uint8_t* acts, int64_t a
   return hipGetLastError();
 }
 
-// The early-activation variant for W waves: Q8_K rows hold at most 2 super-blocks
+// The early-activation variant for W waves: Q8_K rows hold at most 4 super-blocks
 // per wave (fused or not); 32-value formats at most 64 blocks per wave (not fused).
 template <int WT, int AF, int M, bool kFuse, int W, bool kSplit>
 static hipError_t gemv_early(const WeightDev& w, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
@@ -1156,6 +1156,9 @@ static hipError_t gemv_early(const WeightDev& w, const uint8_t* acts, int64_t ar
     }
     if (per_wave == 2) {
       return gemv_launch<WT, AF, M, kFuse, W, 2, kSplit>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, sp, s);
+    }
+    if (per_wave <= 4) {  // long rows on few row groups (an FFN down projection, K = 14336)
+      return gemv_launch<WT, AF, M, kFuse, W, 4, kSplit>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, sp, s);
     }
   } else if constexpr (M == 1 && !kFuse && AF != kActSX && AF != kActQ16 && AF != kActF32) {
     const int64_t bpu = WT == kQ4_K || WT == kQ6_K ? 8 : 1;
