@@ -1178,13 +1178,17 @@ static hipError_t gemv_waves(const WeightDev& w, const uint8_t* acts, int64_t ar
   // Fewer row groups than half the CUs (e.g. N = 4096: 64 groups): split each row's
   // blocks into up to 8 K-ranges over 8-wave workgroups (at least one block per
   // wave), so the launch covers the CUs, and finish the rows in a second launch.
-  // Measured: it pays for the VALU-heavy fp32 and int16 formats (Q6_K K=14336 N=4096
-  // fp32: 75 -> 21 us); the int8 formats stream faster unsplit with 16 waves (21.8 us
-  // there, 26.7 split, the finishing launch included).
-  constexpr bool kSplitOk = AF == kActF32 || AF == kActQ16;
+  // Only the formats whose rows are sums of per-slice sums (per-32 blocks: int8,
+  // int16, fp32) split; the Q8_K and sub-scaled super-block formats keep their
+  // in-order chain. The int8 per-32 formats split only long rows (K >= 8192).
+  // Measured (dq_matmul, N = 4096): fp32 Q6_K K=14336 75 -> 21 us; Q8_0 K=14336
+  // M=1 / 4 22.5 -> 15.1 / 30.7 -> 23.7 us; at K = 4096 the int8 formats were slower
+  // split (Q8_0 M=4 10.8 -> 14.3 us, Q4_0 M=1 5.6 -> 6.9 us).
+  constexpr bool kSplitOk = AF != kActQ8_K && AF != kActSX;
+  constexpr bool kInt8 = AF == kActPer32 || AF == kActQ8_0;
   const int cus = w.cus > 0 ? w.cus : 256;
   int splits = 1;
-  if (kSplitOk && groups * 2 <= cus) {
+  if (kSplitOk && groups * 2 <= cus && (!kInt8 || w.k >= 8192)) {
     splits = (int)(cus / groups);
     if (splits > 8) splits = 8;
     while (splits > 1 && w.nblk / splits < 8) --splits;

@@ -1053,17 +1053,19 @@ def test_gemv_f32_large_k_passes(cuda, t):
 
 @pytest.mark.parametrize("pair", [(O.Q6_K, O.ACT_Q16), (O.Q4_K, O.ACT_Q16), (O.Q8_0, O.ACT_Q16),
                                   (O.Q4_K, O.ACT_F32), (O.Q6_K, O.ACT_F32), (O.Q8_0, O.ACT_F32),
-                                  (O.Q4_0, O.ACT_F32)], ids=pair_id)
+                                  (O.Q4_0, O.ACT_F32), (O.Q8_0, O.ACT_PER32), (O.Q4_0, O.ACT_Q8_0),
+                                  (O.Q4_K, O.ACT_PER32)], ids=pair_id)
 @pytest.mark.parametrize("m", [1, 3])
 def test_gemv_split_k(cuda, pair, m):
-    """Few row groups (N = 256: 4 groups on 256 CUs): the fp32 and int16 GEMVs split each
-    row's blocks over 2..8 workgroups and add the parts in split order in a second
-    launch. Within 2e-6 of the sum of |terms| of the oracle; the same bits on a second
-    run and on a row range (the same split)."""
+    """Few row groups (N = 256: 4 groups on 256 CUs): the fp32 and int16 GEMVs, and the
+    int8 per-32 ones on long rows (K = 8192 here), split each row's blocks over 2..8
+    workgroups and add the parts in split order in a second launch. Within 2e-6 of the
+    sum of |terms| of the oracle; the same bits on a second run and on a row range
+    (the same split)."""
     from dynalm_amd import torch_ops as T
 
     t, fmt = pair
-    k, n = 4096, 256
+    k, n = (8192 if fmt in (O.ACT_PER32, O.ACT_Q8_0) else 4096), 256
     rows = gguf_weights(t, n, k, 2000 + t + fmt, outlier_frac=0.01)
     x = activations(m, k, 2010 + m)
     a = O.quantize_act(fmt, x)
@@ -1073,9 +1075,13 @@ def test_gemv_split_k(cuda, pair, m):
     y2 = host(T.gemv(w, fmt, ad))
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
     want = O.matmul(t, fmt, rows, a, k)
-    af = O.dequantize_act(fmt, a, k).astype(np.float64)
-    mag = np.abs(af) @ np.abs(O.dequantize(t, rows, k).astype(np.float64)).T
-    assert np.all(np.abs(y1.astype(np.float64) - want) <= 2e-6 * mag + 1e-30)
+    if fmt in (O.ACT_PER32, O.ACT_Q8_0):  # the int8 dots: the library's fp32 bar
+        ok, worst = close(y1, want)
+        assert ok, f"worst error ratio {worst:.3g}"
+    else:
+        af = O.dequantize_act(fmt, a, k).astype(np.float64)
+        mag = np.abs(af) @ np.abs(O.dequantize(t, rows, k).astype(np.float64)).T
+        assert np.all(np.abs(y1.astype(np.float64) - want) <= 2e-6 * mag + 1e-30)
     yr = host(T.gemv(w, fmt, ad, n0=70, n1=200))
     assert np.array_equal(yr[:, 70:200].view(np.uint32), y1[:, 70:200].view(np.uint32))
     assert not yr[:, :70].any() and not yr[:, 200:].any()
