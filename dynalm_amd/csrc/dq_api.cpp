@@ -20,10 +20,6 @@
 #include "dq_act.h"
 #include "dq_internal.h"
 
-struct dq_weight {
-  dq::WeightDev dev;
-};
-
 namespace {
 
 thread_local std::string g_err;
@@ -83,8 +79,11 @@ bool pair_ok(int t, int f) {
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 // Per-device scratch buffers (grow, never shrink): g_scratch holds dq_matmul's
-// quantized activations, g_fscratch the fp32 gate / up projections of
-// dq_matmul_gated's unfused path (which runs dq_matmul, so the two must differ).
+// quantized activations (and split-K row sums after them when a region is carved
+// from it), g_fscratch the fp32 gate / up projections of dq_matmul_gated's unfused
+// path (which runs dq_matmul, so the two must differ). A pool is shared by every
+// stream of its device: growing it waits for the whole device before the old buffer
+// is freed, since a launch on another stream may still read it.
 struct Scratch {
   std::mutex mu;
   std::vector<void*> ptr;
@@ -93,15 +92,17 @@ struct Scratch {
 Scratch g_scratch;
 Scratch g_fscratch;
 
-int scratch_get(Scratch& pool, int device, size_t need, hipStream_t s, void** out) {
+int scratch_get(Scratch& pool, int device, size_t need, void** out) {
   std::lock_guard<std::mutex> lock(pool.mu);
   if ((int)pool.ptr.size() <= device) {
     pool.ptr.resize(device + 1, nullptr);
     pool.bytes.resize(device + 1, 0);
   }
   if (pool.bytes[device] < need) {
+    dq::DeviceScope ds(device);
+    DQ_HIP(ds.err, "hipSetDevice");
     if (pool.ptr[device] != nullptr) {
-      DQ_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
+      DQ_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
       DQ_HIP(hipFree(pool.ptr[device]), "hipFree");
       pool.ptr[device] = nullptr;
       pool.bytes[device] = 0;
@@ -113,7 +114,32 @@ int scratch_get(Scratch& pool, int device, size_t need, hipStream_t s, void** ou
   *out = pool.ptr[device];
   return DQ_OK;
 }
-int scratch_get(int device, size_t need, hipStream_t s, void** out) { return scratch_get(g_scratch, device, need, s, out); }
+int scratch_get(int device, size_t need, void** out) { return scratch_get(g_scratch, device, need, out); }
+
+constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
+// The quantized-activation buffer of one matmul: the start of the caller's region,
+// or the per-device pool.
+int acts_buffer(int device, size_t need, const dq::Region& r, void** out) {
+  if (r.base == nullptr) return scratch_get(device, need, out);
+  if (need > r.bytes) {
+    return fail(DQ_RESOURCE_EXHAUSTED, "activations need %zu bytes of scratch, the region holds %zu", need, r.bytes);
+  }
+  *out = r.base;
+  return DQ_OK;
+}
+
+// The split-K workspace after `used` bytes of the caller's region (none: the GEMV's
+// own per-device buffer).
+dq::Workspace split_ws(const dq::Region& r, size_t used) {
+  dq::Workspace ws;
+  if (r.base != nullptr) {
+    const size_t off = round256(used);
+    ws.p = r.base + (off < r.bytes ? off : r.bytes);
+    ws.bytes = off < r.bytes ? r.bytes - off : 0;
+  }
+  return ws;
+}
 
 int validate_shape(int dtype, int64_t n, int64_t k) {
   if (!weight_type_ok(dtype)) return fail(DQ_UNSUPPORTED, "weight type %d is not supported", dtype);
@@ -231,7 +257,7 @@ bool skinny_ok(const dq_weight* w, const float* x, int64_t m, int64_t x_stride) 
 // inputs in GemvJob::x): batches of up to 8 jobs of one k; a batch of at most 16
 // rows whose re-quantization work is small quantizes in the kernel, else each
 // distinct input of the batch is quantized once into the per-device scratch first.
-int run_skinny(std::vector<dq::GemvJob>& jobs, int device, hipStream_t s) {
+int run_skinny(std::vector<dq::GemvJob>& jobs, int device, hipStream_t s, const dq::Region& r) {
   std::vector<bool> done(jobs.size(), false);
   std::vector<dq::GemvJob> batch;
   for (size_t g = 0; g < jobs.size(); ++g) {
@@ -269,7 +295,7 @@ int run_skinny(std::vector<dq::GemvJob>& jobs, int device, hipStream_t s) {
         }
       }
       void* scratch = nullptr;
-      if (int rc = scratch_get(device, bytes, s, &scratch); rc != DQ_OK) return rc;
+      if (int rc = acts_buffer(device, bytes, r, &scratch); rc != DQ_OK) return rc;
       uint8_t* base = static_cast<uint8_t*>(scratch);
       for (size_t i = 0; i < batch.size(); ++i) {
         dq::GemvJob& j = batch[i];
@@ -288,6 +314,80 @@ int run_skinny(std::vector<dq::GemvJob>& jobs, int device, hipStream_t s) {
 }
 
 }  // namespace
+
+namespace dq {
+
+size_t matmul_scratch_bytes(const dq_weight* w, int fmt, int64_t m) {
+  const int f = fmt < 0 ? dq_act_format_for(w->dev.dtype) : fmt;
+  if (f == DQ_ACT_F32) return gemv_split_bytes(w->dev, f, m < 8 ? m : 8);  // the rows are read in place
+  const size_t acts = round256((size_t)(m * dq_act_row_bytes(f, w->dev.k)));
+  return acts + gemv_split_bytes(w->dev, f, m < 8 ? m : 8);
+}
+
+int matmul_impl(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, float* y, int64_t y_stride,
+                const float* bias, hipStream_t s, const Region& r) {
+  const int fmt = dq_act_format_for(w->dev.dtype);
+  const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
+  if (skinny_ok(w, x, m, x_stride)) {
+    // decode batches of 2..64 rows: the skinny MFMA GEMV (quantizing the fp32 rows in
+    // the kernel when that is cheap, else after one quantize launch)
+    std::vector<GemvJob> j{GemvJob{&w->dev, nullptr, 0, x, m > 1 ? x_stride : w->dev.k, m, y, y_stride, bias}};
+    return run_skinny(j, w->dev.device, s, r);
+  }
+  void* stream = static_cast<void*>(s);
+  if (m > 1 && gemv_mma_supported(w->dev.dtype, fmt, 2) && !use_gemm(w->dev, fmt, m)) {
+    // K-quants without a GEMM for this size (Q6_K), or inputs whose offsets exceed
+    // 32 bits: quantize once, then skinny passes of up to 64 rows
+    void* acts = nullptr;
+    if (int rc = acts_buffer(w->dev.device, (size_t)(m * arb), r, &acts); rc != DQ_OK) return rc;
+    if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, x_stride, acts, stream); rc != DQ_OK) return rc;
+    return dq_gemv(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
+  }
+  if (!use_gemm(w->dev, fmt, m)) {
+    // decode: quantization fused into the GEMV (one launch per pass of up to 8 rows);
+    // split-K row sums in the region when one is given
+    const Workspace ws = split_ws(r, 0);
+    DQ_HIP(launch_gemv_fused(w->dev, x, x_stride, m, y, y_stride, bias, s, r.base ? &ws : nullptr), "gemv launch");
+    return DQ_OK;
+  }
+  void* acts = nullptr;
+  if (int rc = acts_buffer(w->dev.device, (size_t)(m * arb), r, &acts); rc != DQ_OK) return rc;
+  if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, x_stride, acts, stream); rc != DQ_OK) return rc;
+  return dq_gemm(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
+}
+
+int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int64_t x_stride, float* y,
+                    int64_t y_stride, const float* bias, hipStream_t s, const Region& r) {
+  const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
+  void* stream = static_cast<void*>(s);
+  if (fmt == DQ_ACT_F32) {
+    // fp32 activations: the GEMV reads the caller's rows in place
+    const int64_t xrb = (m > 1 ? x_stride : w->dev.k) * 4;
+    if (m * xrb >= ((int64_t)1 << 32)) return fail(DQ_UNSUPPORTED, "activations exceed 4 GiB");
+    const Workspace ws = split_ws(r, 0);
+    DQ_HIP(launch_gemv(w->dev, fmt, reinterpret_cast<const uint8_t*>(x), xrb, m, 0, w->dev.n, y, y_stride, bias,
+                       nullptr, s, r.base ? &ws : nullptr),
+           "gemv launch");
+    return DQ_OK;
+  }
+  void* acts = nullptr;
+  if (int rc = acts_buffer(w->dev.device, (size_t)(m * arb), r, &acts); rc != DQ_OK) return rc;
+  if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, acts, stream); rc != DQ_OK) return rc;
+  if (use_gemm(w->dev, fmt, m)) {
+    return dq_gemm(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
+  }
+  // only a GEMV that splits K needs more than the activations
+  if (r.base == nullptr || gemv_splits(w->dev, fmt) == 1) {
+    return dq_gemv(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
+  }
+  const Workspace ws = split_ws(r, (size_t)(m * arb));
+  DQ_HIP(launch_gemv(w->dev, fmt, static_cast<const uint8_t*>(acts), arb, m, 0, w->dev.n, y, y_stride, bias, nullptr,
+                     s, &ws),
+         "gemv launch");
+  return DQ_OK;
+}
+
+}  // namespace dq
 
 extern "C" {
 
@@ -439,41 +539,12 @@ int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, f
   if (w == nullptr) return fail(DQ_INVALID_ARGUMENT, "null weight");
   if (m < 0) return fail(DQ_INVALID_ARGUMENT, "m must be >= 0");
   if (m == 0) return DQ_OK;
-  const int fmt = dq_act_format_for(w->dev.dtype);
-  const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
   if (int rc = check_out(w, m, 0, w->dev.n, y, y_stride); rc != DQ_OK) return rc;
   if (x == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
   if (m > 1 && x_stride < w->dev.k) {
     return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)w->dev.k);
   }
-  hipStream_t s = as_stream(stream);
-  if (skinny_ok(w, x, m, x_stride)) {
-    // decode batches of 2..64 rows: the skinny MFMA GEMV (quantizing the fp32 rows in
-    // the kernel when that is cheap, else after one quantize launch)
-    std::vector<dq::GemvJob> j{dq::GemvJob{&w->dev, nullptr, 0, x, m > 1 ? x_stride : w->dev.k, m, y, y_stride, bias}};
-    return run_skinny(j, w->dev.device, s);
-  }
-  if (m > 1 && dq::gemv_mma_supported(w->dev.dtype, fmt, 2) && !use_gemm(w->dev, fmt, m)) {
-    // K-quants without a GEMM for this size (Q6_K), or inputs whose offsets exceed
-    // 32 bits: quantize once, then skinny passes of up to 64 rows
-    void* acts = nullptr;
-    if (int rc = scratch_get(w->dev.device, (size_t)(m * arb), s, &acts); rc != DQ_OK) return rc;
-    if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, x_stride, acts, stream); rc != DQ_OK) return rc;
-    return dq_gemv(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
-  }
-  if (!use_gemm(w->dev, fmt, m)) {
-    // decode: quantization fused into the GEMV (one launch per pass of up to 8 rows)
-    if (x == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
-    if (m > 1 && x_stride < w->dev.k) {
-      return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)w->dev.k);
-    }
-    DQ_HIP(dq::launch_gemv_fused(w->dev, x, x_stride, m, y, y_stride, bias, s), "gemv launch");
-    return DQ_OK;
-  }
-  void* acts = nullptr;
-  if (int rc = scratch_get(w->dev.device, (size_t)(m * arb), s, &acts); rc != DQ_OK) return rc;
-  if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, x_stride, acts, stream); rc != DQ_OK) return rc;
-  return dq_gemm(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
+  return dq::matmul_impl(w, x, m, x_stride, y, y_stride, bias, as_stream(stream), dq::Region{});
 }
 
 int dq_matmul_many(const dq_matmul_job* jobs, int64_t n_jobs, void* stream) {
@@ -511,7 +582,7 @@ int dq_matmul_many(const dq_matmul_job* jobs, int64_t n_jobs, void* stream) {
       others.push_back(i);
     }
   }
-  if (int rc = run_skinny(grouped, jobs[0].w->dev.device, s); rc != DQ_OK) return rc;
+  if (int rc = run_skinny(grouped, jobs[0].w->dev.device, s, dq::Region{}); rc != DQ_OK) return rc;
   for (int64_t i : others) {
     const dq_matmul_job& j = jobs[i];
     if (int rc = dq_matmul(j.w, j.x, j.m, j.x_stride, j.y, j.y_stride, j.bias, stream); rc != DQ_OK) return rc;
@@ -567,7 +638,7 @@ int dq_matmul_gated(int act, const float* x, int64_t m, int64_t x_stride, const 
     // decode batches: the skinny MFMA GEMV over both weights, act(g) * u in its chains
     std::vector<dq::GemvJob> j{
         dq::GemvJob{&g, nullptr, 0, x, m > 1 ? x_stride : g.k, m, out, m > 1 ? out_stride : g.n, nullptr, &u, act}};
-    return run_skinny(j, g.device, s);
+    return run_skinny(j, g.device, s, dq::Region{});
   }
   // the unfused sequence of Device::matmul_gated (device.h:194-199)
   float* gp = gate_scratch;
@@ -576,7 +647,7 @@ int dq_matmul_gated(int act, const float* x, int64_t m, int64_t x_stride, const 
   if (gp == nullptr) {
     const int64_t plane = (m * g.n + 63) / 64 * 64;
     void* p = nullptr;
-    if (int rc = scratch_get(g_fscratch, g.device, (size_t)(2 * plane) * sizeof(float), s, &p); rc != DQ_OK) return rc;
+    if (int rc = scratch_get(g_fscratch, g.device, (size_t)(2 * plane) * sizeof(float), &p); rc != DQ_OK) return rc;
     gp = static_cast<float*>(p);
     up = gp + plane;
     ss = g.n;
@@ -600,25 +671,10 @@ int dq_matmul_act(const dq_weight* w, int fmt, const float* x, int64_t m, int64_
   if (m > 1 && x_stride < w->dev.k) {
     return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)w->dev.k);
   }
-  const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
-  if (arb < 0) return fail(DQ_INVALID_ARGUMENT, "k %lld is not a multiple of the activation block", (long long)w->dev.k);
-  hipStream_t s = as_stream(stream);
-  if (fmt == DQ_ACT_F32) {
-    // fp32 activations: the GEMV reads the caller's rows in place
-    const int64_t xrb = (m > 1 ? x_stride : w->dev.k) * 4;
-    if (m * xrb >= ((int64_t)1 << 32)) return fail(DQ_UNSUPPORTED, "activations exceed 4 GiB");
-    DQ_HIP(dq::launch_gemv(w->dev, fmt, reinterpret_cast<const uint8_t*>(x), xrb, m, 0, w->dev.n, y, y_stride, bias,
-                           nullptr, s),
-           "gemv launch");
-    return DQ_OK;
+  if (dq_act_row_bytes(fmt, w->dev.k) < 0) {
+    return fail(DQ_INVALID_ARGUMENT, "k %lld is not a multiple of the activation block", (long long)w->dev.k);
   }
-  void* acts = nullptr;
-  if (int rc = scratch_get(w->dev.device, (size_t)(m * arb), s, &acts); rc != DQ_OK) return rc;
-  if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, acts, stream); rc != DQ_OK) return rc;
-  if (use_gemm(w->dev, fmt, m)) {
-    return dq_gemm(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
-  }
-  return dq_gemv(w, fmt, acts, m, 0, w->dev.n, y, y_stride, bias, stream);
+  return dq::matmul_act_impl(w, fmt, x, m, x_stride, y, y_stride, bias, as_stream(stream), dq::Region{});
 }
 
 int dq_partials_count(int dtype, int fmt, int64_t k, int64_t* units, int64_t* sb_terms) {
@@ -644,7 +700,7 @@ int dq_debug_partials(const dq_weight* w, int fmt, const void* acts, int64_t m, 
   if (ns > 0) {
     // The GEMV kernel writes its exact super-block reductions; y goes to scratch.
     void* yscratch = nullptr;
-    if (int rc = scratch_get(w->dev.device, (size_t)(m * w->dev.n * 4), s, &yscratch); rc != DQ_OK) return rc;
+    if (int rc = scratch_get(w->dev.device, (size_t)(m * w->dev.n * 4), &yscratch); rc != DQ_OK) return rc;
     DQ_HIP(dq::launch_gemv(w->dev, fmt, static_cast<const uint8_t*>(acts), arb, m, 0, w->dev.n,
                            static_cast<float*>(yscratch), w->dev.n, nullptr, sb, s),
            "gemv launch");

@@ -81,19 +81,7 @@ int hip_status(hipError_t e, const char* what) {
                        hipGetErrorString(e));
 }
 
-// Makes `device` current for the scope and restores the caller's device.
-struct DeviceScope {
-  int prev = -1;
-  hipError_t err = hipSuccess;
-  explicit DeviceScope(int device) {
-    err = hipGetDevice(&prev);
-    if (err == hipSuccess && prev != device) err = hipSetDevice(device);
-  }
-  ~DeviceScope() {
-    int cur = -1;
-    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-  }
-};
+using dq::DeviceScope;
 
 int grow(dq_external* e, size_t host, size_t dev) {
   if (e->h_bytes < host) {

@@ -1080,6 +1080,36 @@ static size_t gemv_lds_bytes(int wt, int af, int m, int waves, int64_t nblk, boo
 // the tail; with more row groups than CUs, 8-wave workgroups (two per CU) do
 // better. 16 waves leave 128 VGPRs per lane: K-quant passes of more than one
 // activation row need more and keep 8 waves.
+// K-ranges per row of a GEMV launch of weight w under activation format af (1: no
+// split). Fewer row groups than half the CUs (e.g. N = 4096: 64 groups): each row's
+// blocks split into up to 8 K-ranges over 8-wave workgroups (at least 8 blocks per
+// range), so the launch covers the CUs, and a second launch finishes the rows. Only
+// the formats whose rows are sums of per-slice sums (per-32 blocks: int8, int16,
+// fp32) split; the Q8_K and sub-scaled super-block formats keep their in-order chain.
+// The int8 per-32 formats split only long rows (K >= 8192). Measured (dq_matmul,
+// N = 4096): fp32 Q6_K K=14336 75 -> 21 us; Q8_0 K=14336 M=1 / 4 22.5 -> 15.1 /
+// 30.7 -> 23.7 us; at K = 4096 the int8 formats were slower split (Q8_0 M=4 10.8 ->
+// 14.3 us, Q4_0 M=1 5.6 -> 6.9 us). The count depends on the weight and the device
+// only, so every row-range call of one weight partitions K alike.
+int gemv_splits(const WeightDev& w, int af) {
+  if (af == kActQ8_K || af == kActSX) return 1;
+  const bool int8 = af == kActPer32 || af == kActQ8_0;
+  const int64_t groups = w.n_pad / kRowGroup;
+  const int cus = w.cus > 0 ? w.cus : 256;
+  int splits = 1;
+  if (groups * 2 <= cus && (!int8 || w.k >= 8192)) {
+    splits = (int)(cus / groups);
+    if (splits > 8) splits = 8;
+    while (splits > 1 && w.nblk / splits < 8) --splits;
+  }
+  return splits;
+}
+
+size_t gemv_split_bytes(const WeightDev& w, int af, int64_t m_pass) {
+  const int splits = gemv_splits(w, af);
+  return splits > 1 ? (size_t)(w.n_pad / kRowGroup) * splits * (size_t)m_pass * 64 * 4 : 0;
+}
+
 // Split-K state of one launch: the number of K-ranges per row group and the
 // per-device buffer of their row sums (splits == 1: none).
 struct Split {
@@ -1101,7 +1131,9 @@ static hipError_t split_bufs(int device, size_t bytes, Split& sp) {
   std::lock_guard<std::mutex> lock(g_split_mu);
   SplitBufs& b = g_split[device < 64 ? device : 63];
   if (b.bytes < bytes) {
-    hipError_t e = hipDeviceSynchronize();  // earlier launches may still use the old buffer
+    DeviceScope ds(device);
+    if (ds.err != hipSuccess) return ds.err;
+    hipError_t e = hipDeviceSynchronize();  // launches on any stream may still use the old buffer
     if (e != hipSuccess) return e;
     if (b.part != nullptr && (e = hipFree(b.part)) != hipSuccess) return e;
     b.part = nullptr;
@@ -1172,35 +1204,26 @@ static hipError_t gemv_early(const WeightDev& w, const uint8_t* acts, int64_t ar
 template <int WT, int AF, int M, bool kFuse>
 static hipError_t gemv_waves(const WeightDev& w, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
                              int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
-                             hipStream_t s) {
+                             const Workspace* ws, hipStream_t s) {
   constexpr bool kWide = M == 1 || WT == kQ8_0 || WT == kQ4_0;
-  const int64_t groups = (n1 + kRowGroup - 1) / kRowGroup - n0 / kRowGroup;
-  // Fewer row groups than half the CUs (e.g. N = 4096: 64 groups): split each row's
-  // blocks into up to 8 K-ranges over 8-wave workgroups (at least one block per
-  // wave), so the launch covers the CUs, and finish the rows in a second launch.
-  // Only the formats whose rows are sums of per-slice sums (per-32 blocks: int8,
-  // int16, fp32) split; the Q8_K and sub-scaled super-block formats keep their
-  // in-order chain. The int8 per-32 formats split only long rows (K >= 8192).
-  // Measured (dq_matmul, N = 4096): fp32 Q6_K K=14336 75 -> 21 us; Q8_0 K=14336
-  // M=1 / 4 22.5 -> 15.1 / 30.7 -> 23.7 us; at K = 4096 the int8 formats were slower
-  // split (Q8_0 M=4 10.8 -> 14.3 us, Q4_0 M=1 5.6 -> 6.9 us).
-  constexpr bool kSplitOk = AF != kActQ8_K && AF != kActSX;
-  constexpr bool kInt8 = AF == kActPer32 || AF == kActQ8_0;
-  const int cus = w.cus > 0 ? w.cus : 256;
-  int splits = 1;
-  if (kSplitOk && groups * 2 <= cus && (!kInt8 || w.k >= 8192)) {
-    splits = (int)(cus / groups);
-    if (splits > 8) splits = 8;
-    while (splits > 1 && w.nblk / splits < 8) --splits;
-  }
-  if constexpr (kSplitOk) {
+  // The launch shape (waves per workgroup, K-ranges per row) comes from the weight's
+  // row groups, not from [n0, n1): a row's slices, and so its fp32 sum order, do not
+  // depend on how the caller partitions the rows (qmm.h:35-36).
+  const int64_t groups = w.n_pad / kRowGroup;
+  const int splits = gemv_splits(w, AF);
+  if constexpr (AF != kActQ8_K && AF != kActSX) {
     if (splits > 1) {
-      const int64_t gtot = w.n_pad / kRowGroup;
-      const size_t part = (size_t)gtot * splits * M * 64 * 4;
+      const size_t part = (size_t)groups * splits * M * 64 * 4;
       Split sp;
       sp.splits = splits;
-      const hipError_t e = split_bufs(w.device, part, sp);
-      if (e != hipSuccess) return e;
+      if (ws != nullptr && ws->p != nullptr) {
+        // the caller's region (no allocation on this path)
+        if (ws->bytes < part) return hipErrorInvalidValue;
+        sp.part = reinterpret_cast<float*>(ws->p);
+      } else {
+        const hipError_t e = split_bufs(w.device, part, sp);
+        if (e != hipSuccess) return e;
+      }
       return gemv_early<WT, AF, M, kFuse, 8, true>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, sp, s);
     }
   }
@@ -1215,37 +1238,37 @@ static hipError_t gemv_waves(const WeightDev& w, const uint8_t* acts, int64_t ar
 template <int M>
 static hipError_t gemv_pass(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
                             int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
-                            hipStream_t s) {
+                            const Workspace* ws, hipStream_t s) {
   if (x != nullptr) {
     switch (w.dtype) {
-      case kQ4_K: return gemv_waves<kQ4_K, kActQ8_K, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, s);
-      case kQ6_K: return gemv_waves<kQ6_K, kActQ8_K, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, s);
-      case kQ8_0: return gemv_waves<kQ8_0, kActPer32, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, s);
-      default: return gemv_waves<kQ4_0, kActPer32, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, s);
+      case kQ4_K: return gemv_waves<kQ4_K, kActQ8_K, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      case kQ6_K: return gemv_waves<kQ6_K, kActQ8_K, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      case kQ8_0: return gemv_waves<kQ8_0, kActPer32, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      default: return gemv_waves<kQ4_0, kActPer32, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
     }
   }
   switch (w.dtype) {
     case kQ4_K:
-      if (af == kActSX) return gemv_waves<kQ4_K, kActSX, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
-      if (af == kActQ16) return gemv_waves<kQ4_K, kActQ16, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
-      if (af == kActF32) return gemv_waves<kQ4_K, kActF32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
-      return af == kActQ8_K ? gemv_waves<kQ4_K, kActQ8_K, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
-                            : gemv_waves<kQ4_K, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+      if (af == kActSX) return gemv_waves<kQ4_K, kActSX, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      if (af == kActQ16) return gemv_waves<kQ4_K, kActQ16, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      if (af == kActF32) return gemv_waves<kQ4_K, kActF32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      return af == kActQ8_K ? gemv_waves<kQ4_K, kActQ8_K, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s)
+                            : gemv_waves<kQ4_K, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
     case kQ6_K:
-      if (af == kActSX) return gemv_waves<kQ6_K, kActSX, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
-      if (af == kActQ16) return gemv_waves<kQ6_K, kActQ16, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
-      if (af == kActF32) return gemv_waves<kQ6_K, kActF32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
-      return af == kActQ8_K ? gemv_waves<kQ6_K, kActQ8_K, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
-                            : gemv_waves<kQ6_K, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+      if (af == kActSX) return gemv_waves<kQ6_K, kActSX, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      if (af == kActQ16) return gemv_waves<kQ6_K, kActQ16, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      if (af == kActF32) return gemv_waves<kQ6_K, kActF32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      return af == kActQ8_K ? gemv_waves<kQ6_K, kActQ8_K, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s)
+                            : gemv_waves<kQ6_K, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
     case kQ8_0:
-      if (af == kActQ16) return gemv_waves<kQ8_0, kActQ16, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
-      if (af == kActF32) return gemv_waves<kQ8_0, kActF32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
-      return af == kActPer32 ? gemv_waves<kQ8_0, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
-                             : gemv_waves<kQ8_0, kActQ8_0, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+      if (af == kActQ16) return gemv_waves<kQ8_0, kActQ16, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      if (af == kActF32) return gemv_waves<kQ8_0, kActF32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      return af == kActPer32 ? gemv_waves<kQ8_0, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s)
+                             : gemv_waves<kQ8_0, kActQ8_0, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
     default:
-      if (af == kActF32) return gemv_waves<kQ4_0, kActF32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
-      return af == kActPer32 ? gemv_waves<kQ4_0, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s)
-                             : gemv_waves<kQ4_0, kActQ8_0, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, s);
+      if (af == kActF32) return gemv_waves<kQ4_0, kActF32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      return af == kActPer32 ? gemv_waves<kQ4_0, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s)
+                             : gemv_waves<kQ4_0, kActQ8_0, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
   }
 }
 
@@ -1253,7 +1276,7 @@ static hipError_t gemv_pass(const WeightDev& w, int af, const uint8_t* acts, int
 // passes when their LDS fits, else 4.
 static hipError_t gemv_rows(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
                             int64_t m, int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
-                            hipStream_t s) {
+                            const Workspace* ws, hipStream_t s) {
   const int paf = x != nullptr ? (w.dtype == kQ4_K || w.dtype == kQ6_K ? kActQ8_K : kActPer32) : af;
   // rows per pass: 8, 4, 2 or 1, the most whose staged activations fit the LDS
   int pmax = 8;
@@ -1268,11 +1291,11 @@ static hipError_t gemv_rows(const WeightDev& w, int af, const uint8_t* acts, int
     int32_t* dd = dbg ? dbg + r0 * w.n * w.nblk * 2 : nullptr;
     hipError_t e;
     switch (rows) {
-      case 1: e = gemv_pass<1>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
-      case 2: e = gemv_pass<2>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
-      case 3: e = gemv_pass<3>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
-      case 4: e = gemv_pass<4>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
-      default: e = gemv_pass<8>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, s); break;
+      case 1: e = gemv_pass<1>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, ws, s); break;
+      case 2: e = gemv_pass<2>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, ws, s); break;
+      case 3: e = gemv_pass<3>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, ws, s); break;
+      case 4: e = gemv_pass<4>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, ws, s); break;
+      default: e = gemv_pass<8>(w, af, a, arb, xx, xs, n0, n1, yy, ys, bias, dd, ws, s); break;
     }
     if (e != hipSuccess) return e;
     r0 += rows;
@@ -1326,13 +1349,13 @@ hipError_t launch_gemv_gated(const WeightDev& wg, const WeightDev& wu, int act, 
 }
 
 hipError_t launch_gemv(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
-                       float* y, int64_t ys, const float* bias, int32_t* dbg, hipStream_t s) {
-  return gemv_rows(w, af, acts, arb, nullptr, 0, m, n0, n1, y, ys, bias, dbg, s);
+                       float* y, int64_t ys, const float* bias, int32_t* dbg, hipStream_t s, const Workspace* ws) {
+  return gemv_rows(w, af, acts, arb, nullptr, 0, m, n0, n1, y, ys, bias, dbg, ws, s);
 }
 
 hipError_t launch_gemv_fused(const WeightDev& w, const float* x, int64_t xs, int64_t m, float* y, int64_t ys,
-                             const float* bias, hipStream_t s) {
-  return gemv_rows(w, -1, nullptr, 0, x, xs, m, 0, w.n, y, ys, bias, nullptr, s);
+                             const float* bias, hipStream_t s, const Workspace* ws) {
+  return gemv_rows(w, -1, nullptr, 0, x, xs, m, 0, w.n, y, ys, bias, nullptr, ws, s);
 }
 
 }  // namespace dq

@@ -23,6 +23,31 @@ struct WeightDev {
 // Records the calling thread's error message (dq_last_error) and returns code.
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
+// Makes `device` current for the scope and restores the previous device after.
+struct DeviceScope {
+  int prev = -1;
+  hipError_t err = hipSuccess;
+  explicit DeviceScope(int device) {
+    err = hipGetDevice(&prev);
+    if (err == hipSuccess && prev != device) err = hipSetDevice(device);
+  }
+  ~DeviceScope() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+  DeviceScope(const DeviceScope&) = delete;
+  DeviceScope& operator=(const DeviceScope&) = delete;
+};
+
+// A device region for a launch's temporaries (split-K row sums). p == nullptr: the
+// library's per-device buffer, grown with hipMalloc on demand; otherwise the
+// caller's region of `bytes` bytes (a launch that needs more fails with
+// hipErrorInvalidValue and allocates nothing).
+struct Workspace {
+  uint8_t* p = nullptr;
+  size_t bytes = 0;
+};
+
 hipError_t launch_quantize(int af, const float* x, int64_t m, int64_t k, int64_t x_stride, uint8_t* out, int64_t orb,
                            hipStream_t s);
 hipError_t launch_repack(int t, const uint8_t* src, int64_t row_stride, int64_t n, int64_t nblk, uint8_t* const* planes,
@@ -32,11 +57,17 @@ hipError_t launch_unpack(int t, uint8_t* dst, int64_t row_stride, int64_t n, int
 // dbg (nullable): per (row, weight row, super-block) the exact S and Mn of the
 // K-quant x Q8_K kernels.
 hipError_t launch_gemv(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
-                       float* y, int64_t ys, const float* bias, int32_t* dbg, hipStream_t s);
+                       float* y, int64_t ys, const float* bias, int32_t* dbg, hipStream_t s,
+                       const Workspace* ws = nullptr);
 // Decode matmul with the activation quantization fused into the GEMV (fp32 rows x,
 // row stride xs floats; the weight's activation format, dq_act_format_for).
 hipError_t launch_gemv_fused(const WeightDev& w, const float* x, int64_t xs, int64_t m, float* y, int64_t ys,
-                             const float* bias, hipStream_t s);
+                             const float* bias, hipStream_t s, const Workspace* ws = nullptr);
+// K-ranges per row of the GEMV on this weight under activation format af (1: no
+// split-K), and the bytes of row sums a pass of up to m_pass rows then needs (0 when
+// it does not split). Both depend on the weight and the device only.
+int gemv_splits(const WeightDev& w, int af);
+size_t gemv_split_bytes(const WeightDev& w, int af, int64_t m_pass);
 hipError_t launch_units(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int32_t* units,
                         int64_t nu, hipStream_t s);
 // int8 MFMA GEMM (Q4_K x Q8_K). Returns hipErrorInvalidValue for an
@@ -96,4 +127,29 @@ hipError_t launch_gemv_gated(const WeightDev& wg, const WeightDev& wu, int act, 
 hipError_t launch_act_mul(int act, const float* g, int64_t gs, const float* u, int64_t us, int64_t m, int64_t n,
                           float* out, int64_t os, hipStream_t s);
 
+// Where one matmul keeps its temporaries (quantized activations at the start,
+// split-K row sums after them): base == nullptr selects the library's per-device
+// buffers (grown with hipMalloc, shared by the device's streams); otherwise the
+// caller's device region of `bytes` bytes, and nothing is allocated.
+struct Region {
+  uint8_t* base = nullptr;
+  size_t bytes = 0;
+};
+
+}  // namespace dq
+
+// The library's weight handle (include/dynaq.h).
+struct dq_weight {
+  dq::WeightDev dev;
+};
+
+namespace dq {
+// Bytes of temporaries dq_matmul (fmt < 0) or dq_matmul_act (format fmt) needs for
+// m rows of w in a fixed region: an upper bound over the routes either may take.
+size_t matmul_scratch_bytes(const dq_weight* w, int fmt, int64_t m);
+// dq_matmul / dq_matmul_act with their temporaries in r (arguments validated).
+int matmul_impl(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, float* y, int64_t y_stride,
+                const float* bias, hipStream_t s, const Region& r);
+int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int64_t x_stride, float* y,
+                    int64_t y_stride, const float* bias, hipStream_t s, const Region& r);
 }  // namespace dq
