@@ -37,7 +37,7 @@ __all__ = [
     "DqError", "lib", "lib_path", "row_bytes", "act_row_bytes", "act_format_for", "Weight",
     "act_quantize", "gemv", "gemm", "matmul", "matmul_many", "MatmulJob", "partials_count", "debug_partials",
     "SILU", "GELU", "GELU_TANH", "act_mul", "matmul_gated", "GgufFile", "GgufTensor", "EXPORTS",
-    "MatmulShape", "External",
+    "MatmulShape", "External", "matmul_noalloc", "NOALLOC_SCRATCH_BYTES",
 ]
 
 Q4_0, Q8_0, Q4_K, Q6_K = 6, 10, 14, 16
@@ -78,6 +78,7 @@ EXPORTS = {
     "dq_gemv": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "dq_gemm": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "dq_matmul": (_I, [_P, _P, _I64, _I64, _P, _I64, _P, _P]),
+    "dq_matmul_noalloc": (_I, [_P, _P, _I64, _I64, _P, _I64, _P, _P]),
     "dq_matmul_many": (_I, [_P, _I64, _P]),
     "dq_matmul_act": (_I, [_P, _I, _P, _I64, _I64, _P, _I64, _P, _P]),
     "dq_act_mul": (_I, [_I, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P]),
@@ -216,6 +217,14 @@ def gemm(w: Weight, fmt: int, acts, m: int, n0: int, n1: int, y, y_stride: int, 
 
 def matmul(w: Weight, x, m: int, x_stride: int, y, y_stride: int, bias=None, stream: int = 0) -> None:
     _check(lib().dq_matmul(w.handle, _ptr(x), m, x_stride, _ptr(y), y_stride, _ptr(bias), stream))
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20  # DQ_NOALLOC_SCRATCH_BYTES
+
+
+def matmul_noalloc(w: Weight, x, m: int, x_stride: int, y, y_stride: int, bias=None, stream: int = 0) -> None:
+    """dq_matmul with its temporaries in the library's static device array (no allocation)."""
+    _check(lib().dq_matmul_noalloc(w.handle, _ptr(x), m, x_stride, _ptr(y), y_stride, _ptr(bias), stream))
 
 
 def matmul_act(w: Weight, fmt: int, x, m: int, x_stride: int, y, y_stride: int, bias=None, stream: int = 0) -> None:

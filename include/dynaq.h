@@ -169,6 +169,20 @@ DQ_API int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int
 DQ_API int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, float* y, int64_t y_stride,
                      const float* bias, void* stream);
 
+/* Bytes of the static device array dq_matmul_noalloc keeps its temporaries in (one per GPU). */
+#define DQ_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* dq_matmul without any device allocation: the same kernels and bits as dq_matmul,
+ * with the quantized activations and split-K row sums in a static device array of
+ * DQ_NOALLOC_SCRATCH_BYTES per GPU instead of buffers grown with hipMalloc. No
+ * counterpart in the reference; it is for callers that cannot allocate (code under
+ * HIP graph capture, serving loops that forbid hipMalloc). Calls needing more
+ * scratch than the array holds (Q4_K with K = 4096: more than 3,591 rows) return
+ * DQ_RESOURCE_EXHAUSTED before launching anything. Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (unordered streams or threads) race. */
+DQ_API int dq_matmul_noalloc(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, float* y,
+                             int64_t y_stride, const float* bias, void* stream);
+
 /* y = x . w^T (+ bias) with the activations quantized to format fmt (the caller's
  * choice of dynacore's activation contract, which KernelPlan makes per matmul:
  * dynacore/include/dynacore/kernel/kernel_plan.h:50-92). One quantize launch into
