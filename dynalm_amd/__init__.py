@@ -37,7 +37,8 @@ __all__ = [
     "DqError", "lib", "lib_path", "row_bytes", "act_row_bytes", "act_format_for", "Weight",
     "act_quantize", "gemv", "gemm", "matmul", "matmul_many", "MatmulJob", "partials_count", "debug_partials",
     "SILU", "GELU", "GELU_TANH", "act_mul", "matmul_gated", "GgufFile", "GgufTensor", "EXPORTS",
-    "MatmulShape", "External", "matmul_noalloc", "NOALLOC_SCRATCH_BYTES",
+    "MatmulShape", "External", "matmul_noalloc", "NOALLOC_SCRATCH_BYTES", "Plan", "Selection",
+    "plan_defaults", "plan_ffn_down", "select", "matmul_plan", "KERNEL_NAMES",
 ]
 
 Q4_0, Q8_0, Q4_K, Q6_K = 6, 10, 14, 16
@@ -99,6 +100,11 @@ EXPORTS = {
     "dq_external_run": (_I, [_P, _P, _I64, _I64, _P, _I, _I64, _I64, _I64, _P, _P, _I64]),
     "dq_external_forget": (_I, [_P, _P]),
     "dq_external_get_stats": (_I, [_P, _P]),
+    "dq_external_set_plan": (_I, [_P, _P]),
+    "dq_plan_defaults": (_I, [_P]),
+    "dq_plan_ffn_down": (_I, [_P, _P]),
+    "dq_select": (_I, [_P, _P, _P]),
+    "dq_matmul_plan": (_I, [_P, _P, _P, _I64, _I64, _P, _I64, _P, _P]),
 }
 
 
@@ -361,6 +367,58 @@ class MatmulShape(C.Structure):
     _fields_ = [("m", _I64), ("n", _I64), ("k", _I64), ("dtype", C.c_int32), ("x_dense", C.c_int32)]
 
 
+# dq_kernel: dynacore MatmulKernelId values (kernel/matmul_registry.h:33-51)
+KERNEL_INT8_SUBSCALED, KERNEL_INT8_SUPERBLOCK, KERNEL_INT8_PER32 = 7, 8, 9
+KERNEL_INT16_ROWS, KERNEL_F32_EXPAND_GEMM, KERNEL_F32_ROW_DOT = 13, 14, 15
+KERNEL_NAMES = {7: "int8_subscaled", 8: "int8_superblock", 9: "int8_per32", 13: "int16_rows", 14: "f32_expand_gemm",
+                15: "f32_row_dot"}
+
+
+class Plan(C.Structure):
+    """dq_plan: KernelPlan's matmul knobs (kernel/kernel_plan.h:34-148)."""
+    _fields_ = [("expand_min_rows", C.c_int32), ("int8_decode_max_rows", C.c_int32),
+                ("int16_decode_max_rows", C.c_int32), ("int8_superblock_min_rows", C.c_int32),
+                ("int8_superblock_max_rows", C.c_int32), ("int8_subscale_min_rows", C.c_int32),
+                ("matmul_disabled", C.c_uint32)]
+
+    def as_dict(self) -> dict:
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
+class Selection(C.Structure):
+    """dq_selection: the kernel (dq_kernel) and the activation format it quantizes x to."""
+    _fields_ = [("kernel", C.c_int32), ("act", C.c_int32)]
+
+
+def plan_defaults() -> Plan:
+    """KernelPlan::defaults() without environment overrides."""
+    p = Plan()
+    _check(lib().dq_plan_defaults(C.byref(p)))
+    return p
+
+
+def plan_ffn_down(base: Plan | None = None) -> Plan:
+    """The FFN down projection's plan derived from base (transformer.cpp:541-550)."""
+    p = Plan()
+    _check(lib().dq_plan_ffn_down(C.byref(base) if base is not None else None, C.byref(p)))
+    return p
+
+
+def select(m: int, n: int, k: int, dtype: int, plan: Plan | None = None, x_dense: bool = True) -> Selection:
+    """select_matmul over this library's kernels (no GPU needed)."""
+    out = Selection()
+    shape = MatmulShape(m, n, k, dtype, int(x_dense))
+    _check(lib().dq_select(C.byref(shape), C.byref(plan) if plan is not None else None, C.byref(out)))
+    return out
+
+
+def matmul_plan(w: Weight, plan: Plan | None, x, m: int, x_stride: int, y, y_stride: int, bias=None,
+                stream: int = 0) -> None:
+    """Device::matmul under a KernelPlan (None: the defaults)."""
+    _check(lib().dq_matmul_plan(w.handle, C.byref(plan) if plan is not None else None, _ptr(x), m, x_stride, _ptr(y),
+                                y_stride, _ptr(bias), stream))
+
+
 class ExternalStats(C.Structure):
     _fields_ = [("runs", _I64), ("uploads", _I64), ("hits", _I64), ("evictions", _I64), ("resident_bytes", _I64),
                 ("resident_weights", _I64)]
@@ -413,6 +471,10 @@ class External:
         _check(lib().dq_external_run(self._h, x.ctypes.data, m, x.strides[0] // 4, w_rows.ctypes.data, dtype, n, k,
                                      w_rows.strides[0], b, y.ctypes.data, y.strides[0] // 4))
         return y
+
+    def set_plan(self, plan: Plan | None) -> None:
+        """Device::set_kernel_plan for the adapter (None: the defaults)."""
+        _check(lib().dq_external_set_plan(self._h, C.byref(plan) if plan is not None else None))
 
     def forget(self, w_rows) -> None:
         _check(lib().dq_external_forget(self._h, w_rows.ctypes.data))

@@ -18,7 +18,8 @@ LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libdynaq.so")
 
 SOURCES = ["dq_kernels.hip", "dq_gemv.hip", "dq_gemm.hip", "dq_gemm_b32.hip", "dq_skinny.hip", "dq_api.cpp",
-           "dq_gguf.cpp", "dq_external.cpp", "dq_noalloc.hip"]
+           "dq_gguf.cpp", "dq_external.cpp", "dq_noalloc.hip",
+           "dq_plan.cpp"]
 ARCH = os.environ.get("DYNAQ_ARCH", "gfx950")
 
 # Device code: IEEE fp32 division/sqrt (the quantizers need correctly rounded

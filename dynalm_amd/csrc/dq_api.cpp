@@ -387,6 +387,30 @@ int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int6
   return DQ_OK;
 }
 
+int matmul_sel_impl(const dq_weight* w, const dq_selection& sel, const float* x, int64_t m, int64_t x_stride,
+                    float* y, int64_t y_stride, const float* bias, hipStream_t s, const Region& r) {
+  const int t = w->dev.dtype;
+  switch (sel.kernel) {
+    case DQ_KERNEL_INT8_SUPERBLOCK:  // Q8_K, the K-quants' dq_matmul routes
+      if (t == DQ_Q4_K || t == DQ_Q6_K) return matmul_impl(w, x, m, x_stride, y, y_stride, bias, s, r);
+      break;
+    case DQ_KERNEL_INT8_PER32:  // per-32: dq_matmul's routes for Q8_0 / Q4_0
+      if (t == DQ_Q8_0 || t == DQ_Q4_0) return matmul_impl(w, x, m, x_stride, y, y_stride, bias, s, r);
+      break;
+    default:
+      break;
+  }
+  if (!pair_ok(t, sel.act)) {
+    return fail(DQ_UNSUPPORTED, "kernel %d (activation format %d) does not take weight type %d", sel.kernel, sel.act, t);
+  }
+  return matmul_act_impl(w, sel.act, x, m, x_stride, y, y_stride, bias, s, r);
+}
+
+size_t sel_scratch_bytes(const dq_weight* w, const dq_selection& sel, int64_t m) {
+  const size_t a = matmul_scratch_bytes(w, -1, m), b = matmul_scratch_bytes(w, sel.act, m);
+  return a > b ? a : b;
+}
+
 }  // namespace dq
 
 extern "C" {
@@ -545,6 +569,21 @@ int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, f
     return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)w->dev.k);
   }
   return dq::matmul_impl(w, x, m, x_stride, y, y_stride, bias, as_stream(stream), dq::Region{});
+}
+
+int dq_matmul_plan(const dq_weight* w, const dq_plan* plan, const float* x, int64_t m, int64_t x_stride, float* y,
+                   int64_t y_stride, const float* bias, void* stream) {
+  if (w == nullptr) return fail(DQ_INVALID_ARGUMENT, "null weight");
+  if (m < 0) return fail(DQ_INVALID_ARGUMENT, "m must be >= 0");
+  if (m == 0) return DQ_OK;
+  if (int rc = check_out(w, m, 0, w->dev.n, y, y_stride); rc != DQ_OK) return rc;
+  if (x == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
+  if (m > 1 && x_stride < w->dev.k) {
+    return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)w->dev.k);
+  }
+  const dq_matmul_shape shape{m, w->dev.n, w->dev.k, w->dev.dtype, (int32_t)(m == 1 || x_stride == w->dev.k)};
+  const dq_selection sel = dq::select(shape, plan != nullptr ? *plan : dq::default_plan());
+  return dq::matmul_sel_impl(w, sel, x, m, x_stride, y, y_stride, bias, as_stream(stream), dq::Region{});
 }
 
 int dq_matmul_many(const dq_matmul_job* jobs, int64_t n_jobs, void* stream) {

@@ -9,9 +9,12 @@
 // type, shape and row stride, as CpuDevice keys its prepacked copies by data pointer
 // and (n, k) (dynacore/include/dynacore/cpu/cpu_device.h:135-143,188-206); copies
 // of the least recently used weights are dropped when a byte limit is set. x goes
-// in and y comes back through pinned staging buffers on the adapter's own stream,
-// and dq_matmul does the work in between, so results are those of dq_matmul on the
-// same rows. A call returns when y is written.
+// in and y comes back through pinned staging buffers on the adapter's own stream.
+// In between, the kernel dynacore would select under the adapter's KernelPlan runs
+// (dq_select; the defaults until dq_external_set_plan, Device::set_kernel_plan), so
+// the accuracy class is the reference's, and results are dq_matmul_plan's on the
+// same rows. The adapter's temporaries live in its own device buffer, so adapters
+// on one GPU never share them. A call returns when y is written.
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -70,8 +73,9 @@ struct dq_external {
   // staging: pinned host and device buffers, grown on demand
   void* h_stage = nullptr;
   size_t h_bytes = 0;
-  void* d_stage = nullptr;
+  void* d_stage = nullptr;  // x, y, bias, then this adapter's matmul temporaries
   size_t d_bytes = 0;
+  dq_plan plan = dq::default_plan();  // Device::set_kernel_plan
 };
 
 namespace {
@@ -224,19 +228,29 @@ int dq_external_run(dq_external* e, const float* x, int64_t m, int64_t x_stride,
   std::lock_guard<std::mutex> lock(e->mu);
   DeviceScope ds(e->device);
   if (ds.err != hipSuccess) return hip_status(ds.err, "hipSetDevice");
-  // dense device rows: x [m][k], y [m][n], bias [n]; one pinned buffer for x and y
-  const size_t xb = (size_t)(m * k) * 4, yb = (size_t)(m * n) * 4, bb = bias ? (size_t)n * 4 : 0;
-  const size_t xo = 0, yo = (xb + 255) / 256 * 256, bo = yo + (yb + 255) / 256 * 256;
-  if (int rc = grow(e, xb > yb ? xb : yb, bo + bb); rc != DQ_OK) return rc;
   dq_weight* h = nullptr;
   bool transient = false;
   if (int rc = weight_for(e, Key{w, dtype, n, k, w_row_bytes}, &h, &transient); rc != DQ_OK) return rc;
+  // The kernel under the adapter's plan, chosen from the caller's layout of x (as
+  // CpuDevice::matmul chooses, cpu_device.cpp:869-897).
+  const dq_matmul_shape shape{m, n, k, dtype, (int32_t)(m == 1 || x_stride == k)};
+  const dq_selection sel = dq::select(shape, e->plan);
+  // dense device rows: x [m][k], y [m][n], bias [n], then the matmul's temporaries
+  // (this adapter's own: adapters never share scratch); one pinned buffer for x and y
+  const size_t xb = (size_t)(m * k) * 4, yb = (size_t)(m * n) * 4, bb = bias ? (size_t)n * 4 : 0;
+  const size_t xo = 0, yo = (xb + 255) / 256 * 256, bo = yo + (yb + 255) / 256 * 256;
+  const size_t so = bo + (bb + 255) / 256 * 256, sb = dq::sel_scratch_bytes(h, sel, m);
+  int rc = grow(e, xb > yb ? xb : yb, so + sb);
+  if (rc != DQ_OK) {
+    if (transient) dq_weight_free(h);
+    return rc;
+  }
   auto* hs = static_cast<float*>(e->h_stage);
   auto* dbase = static_cast<uint8_t*>(e->d_stage);
   float* dx = reinterpret_cast<float*>(dbase + xo);
   float* dy = reinterpret_cast<float*>(dbase + yo);
   float* dbias = bias ? reinterpret_cast<float*>(dbase + bo) : nullptr;
-  int rc = DQ_OK;
+  const dq::Region region{dbase + so, sb};
   hipError_t r = hipSuccess;
   if (bias != nullptr) r = hipMemcpyAsync(dbias, bias, bb, hipMemcpyHostToDevice, e->stream);
   for (int64_t i = 0; i < m; ++i) std::memcpy(hs + i * k, x + i * (m > 1 ? x_stride : k), (size_t)k * 4);
@@ -246,7 +260,7 @@ int dq_external_run(dq_external* e, const float* x, int64_t m, int64_t x_stride,
   if (r != hipSuccess) {
     rc = hip_status(r, "adapter input copy");
   } else {
-    rc = dq_matmul(h, dx, m, k, dy, n, dbias, e->stream);
+    rc = dq::matmul_sel_impl(h, sel, dx, m, k, dy, n, dbias, e->stream, region);
   }
   if (rc == DQ_OK) {
     r = hipMemcpyAsync(hs, dy, yb, hipMemcpyDeviceToHost, e->stream);
@@ -280,6 +294,13 @@ int dq_external_forget(dq_external* e, const void* weight) {
     it = next;
   }
   return found ? DQ_OK : dq::set_error(DQ_NOT_FOUND, "no device copy of that weight");
+}
+
+int dq_external_set_plan(dq_external* e, const dq_plan* plan) {
+  if (e == nullptr) return dq::set_error(DQ_INVALID_ARGUMENT, "null adapter");
+  std::lock_guard<std::mutex> lock(e->mu);
+  e->plan = plan != nullptr ? *plan : dq::default_plan();
+  return DQ_OK;
 }
 
 int dq_external_get_stats(dq_external* e, dq_external_stats* out) {

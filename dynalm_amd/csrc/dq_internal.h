@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/dynaq.h"
 #include "dq_layout.h"
 
 namespace dq {
@@ -152,4 +153,13 @@ int matmul_impl(const dq_weight* w, const float* x, int64_t m, int64_t x_stride,
                 const float* bias, hipStream_t s, const Region& r);
 int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int64_t x_stride, float* y,
                     int64_t y_stride, const float* bias, hipStream_t s, const Region& r);
+// KernelPlan::defaults() (without environment overrides) and select_matmul over this
+// library's kernels (dq_plan.cpp).
+dq_plan default_plan();
+dq_selection select(const dq_matmul_shape& s, const dq_plan& p);
+// Runs selection sel for m rows of w (arguments validated), temporaries in r.
+int matmul_sel_impl(const dq_weight* w, const dq_selection& sel, const float* x, int64_t m, int64_t x_stride,
+                    float* y, int64_t y_stride, const float* bias, hipStream_t s, const Region& r);
+// Bytes of temporaries matmul_sel_impl needs for this selection in a fixed region.
+size_t sel_scratch_bytes(const dq_weight* w, const dq_selection& sel, int64_t m);
 }  // namespace dq

@@ -252,6 +252,75 @@ DQ_API int dq_matmul_gated(int act, const float* x, int64_t m, int64_t x_stride,
                            const dq_weight* w_up, float* out, int64_t out_stride, float* gate_scratch,
                            float* up_scratch, int64_t scratch_stride, void* stream);
 
+/* ---- accuracy classes: dynacore's KernelPlan and select_matmul -----------
+ * Which activation contract a matmul runs under is dynacore's per-call kernel
+ * selection (select_matmul, dynacore/src/kernel/matmul_registry.cpp:94-191,287-429)
+ * from the step's KernelPlan (dynacore/include/dynacore/kernel/kernel_plan.h:29-192).
+ * dq_select restates it for this library's kernels and dq_matmul_plan runs the
+ * result; under the default plan a Q4_K / Q6_K decode row is sub-scaled int8
+ * (validated), Q8_0 / Q4_0 up to 4 rows per-32 int8, larger batches fp32, and the
+ * super-block (Q8_K) class that dq_matmul runs is opt-in, as in the reference. */
+
+/* MatmulShape (dynacore/include/dynacore/kernel/matmul_registry.h:87-91). */
+typedef struct dq_matmul_shape {
+  int64_t m, n, k;
+  int32_t dtype;
+  int32_t x_dense; /* x rows are contiguous (row stride == k floats) */
+} dq_matmul_shape;
+
+/* The kernels: dynacore::MatmulKernelId values (dynacore/include/dynacore/kernel/
+ * matmul_registry.h:33-51) of the ones this library implements on the GPU; the
+ * others (interleaved-copy, qmm, SME, external) do not exist here. */
+typedef enum dq_kernel {
+  DQ_KERNEL_INT8_SUBSCALED = 7,   /* kInt8Subscaled: DQ_ACT_SX, K-quants (validated, DD-077) */
+  DQ_KERNEL_INT8_SUPERBLOCK = 8,  /* kInt8Superblock: DQ_ACT_Q8_K, K-quants (fails DD-053: opt-in) */
+  DQ_KERNEL_INT8_PER32 = 9,       /* kInt8Per32: DQ_ACT_PER32 (validated, DD-053) */
+  DQ_KERNEL_INT16_ROWS = 13,      /* kInt16Rows: DQ_ACT_Q16, Q8_0 / Q4_K / Q6_K (validated, DD-076) */
+  DQ_KERNEL_F32_EXPAND_GEMM = 14, /* kF32ExpandGemm: fp32 activations, dense x (reference class) */
+  DQ_KERNEL_F32_ROW_DOT = 15,     /* kF32RowDot: fp32 activations (reference class) */
+} dq_kernel;
+
+/* The matmul knobs of KernelPlan that choose among these kernels, with the
+ * reference's meaning and names (kernel_plan.h:34-92); matmul_disabled is a mask
+ * of (1u << dq_kernel), as KernelPlan::matmul_disabled (kernel_plan.h:144-148). */
+typedef struct dq_plan {
+  int32_t expand_min_rows;
+  int32_t int8_decode_max_rows;
+  int32_t int16_decode_max_rows;
+  int32_t int8_superblock_min_rows;
+  int32_t int8_superblock_max_rows;
+  int32_t int8_subscale_min_rows;
+  uint32_t matmul_disabled;
+} dq_plan;
+
+/* A selection: the kernel and the activation format it quantizes x to (DQ_ACT_F32
+ * for the fp32 kernels), as MatmulSelection {id, act} (matmul_registry.h:143-151). */
+typedef struct dq_selection {
+  int32_t kernel;
+  int32_t act;
+} dq_selection;
+
+/* KernelPlan::defaults() without its environment overrides (kernel_plan.cpp:22-90):
+ * expand 2, int8 decode 4 rows, int16 0, super-block off (min 0, max 8), sub-scaled
+ * from 1 row, nothing disabled. */
+DQ_API int dq_plan_defaults(dq_plan* out);
+/* The plan the model uses for the FFN down projection (dynalm/src/model/
+ * transformer.cpp:541-550, with int8_ffn_down off and int16_ffn_down on): no int8
+ * activations; int16 for up to max(int8_decode_max_rows, int8_superblock_max_rows)
+ * rows while int8 decode is on. */
+DQ_API int dq_plan_ffn_down(const dq_plan* base, dq_plan* out);
+/* select_matmul (dynacore/src/kernel/matmul_registry.cpp:287-429) over this
+ * library's kernels; plan NULL: the defaults. A pure function; needs no GPU.
+ * DQ_INVALID_ARGUMENT for shapes validate_matmul_shape rejects. */
+DQ_API int dq_select(const dq_matmul_shape* s, const dq_plan* plan, dq_selection* out);
+/* y = x . w^T (+ bias) under the kernel dq_select picks for this call (plan NULL:
+ * the defaults): Device::matmul with the step's KernelPlan (device.h:95,161).
+ * dq_matmul is this call under the all-integer plan {int8_decode_max_rows and
+ * int8_superblock_max_rows unbounded, int8_superblock_min_rows 1,
+ * int8_subscale_min_rows 0}. */
+DQ_API int dq_matmul_plan(const dq_weight* w, const dq_plan* plan, const float* x, int64_t m, int64_t x_stride,
+                          float* y, int64_t y_stride, const float* bias, void* stream);
+
 /* ---- GGUF files ----------------------------------------------------------
  * A GGUF v2 / v3 model mapped read-only (mmap): header, metadata and tensor
  * directory parsed with every length and offset checked against the file
@@ -306,15 +375,12 @@ DQ_API int dq_gguf_upload_weight(const dq_gguf* g, int64_t i, void* stream, dq_w
  * dynacore/include/dynacore/cpu/cpu_device.h:135-143), dropping the least recently
  * used copies beyond max_resident_bytes (0: no limit). A weight's host rows must
  * not change while a copy of them is kept (dq_external_forget drops it). Calls on
- * one dq_external are serialized; results are those of dq_matmul on the same rows. */
+ * one dq_external are serialized. run() selects its kernel as dq_matmul_plan does,
+ * under the adapter's plan (dq_external_set_plan; dynacore's defaults at creation,
+ * so the accuracy class is the reference's), and its results are dq_matmul_plan's
+ * on the same rows. Each adapter keeps its own device scratch: adapters on one GPU
+ * do not share temporaries. */
 typedef struct dq_external dq_external;
-
-/* MatmulShape (dynacore/include/dynacore/kernel/matmul_registry.h:87-91). */
-typedef struct dq_matmul_shape {
-  int64_t m, n, k;
-  int32_t dtype;
-  int32_t x_dense; /* x rows are contiguous (row stride == k floats) */
-} dq_matmul_shape;
 
 typedef struct dq_external_stats {
   int64_t runs;             /* completed dq_external_run calls */
@@ -341,6 +407,11 @@ DQ_API int dq_external_run(dq_external* e, const float* x, int64_t m, int64_t x_
 /* Drops the device copies of host weight rows `weight` (DQ_NOT_FOUND if none). */
 DQ_API int dq_external_forget(dq_external* e, const void* weight);
 DQ_API int dq_external_get_stats(dq_external* e, dq_external_stats* out);
+/* The plan run() selects kernels with, as Device::set_kernel_plan (dynacore/include/
+ * dynacore/device/device.h:95): an engine calls it where it sets the device's plan
+ * (per step, and around the FFN down projection, transformer.cpp:538-550). A new
+ * adapter starts with dq_plan_defaults. NULL: the defaults. */
+DQ_API int dq_external_set_plan(dq_external* e, const dq_plan* plan);
 
 /* Exact integer partials of every (activation row r < m, weight row i < n):
  * units[(r * n + i) * U + u] and sb[(r * n + i) * S + s], with U and S from

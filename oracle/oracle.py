@@ -263,6 +263,8 @@ def ref():
             "ref_split_act16": (C.c_int, [_P, _P, _I64]),
             "ref_dot_rows16": (C.c_int, [C.c_int, _P, _P, _I64, C.c_int, _I64, _P]),
             "ref_vec_dot": (C.c_int, [C.c_int, C.c_int, _P, _P, _I64, _P]),
+            "ref_select_matmul": (C.c_int, [_I64, _I64, _I64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                            C.c_int, C.c_int, C.c_uint32, C.POINTER(C.c_int)]),
         }
         for name, (res, args) in sig.items():
             f = getattr(r, name)

@@ -12,6 +12,7 @@
 //   dynacore/cpu/generic/kernels_generic.cpp:334-346        split_act16
 //   dynacore/cpu/generic/kernels_generic.cpp:67-150         vec_dot_* (fp32 activations)
 //   dynacore/include/dynacore/base/fast_exp.h:16-35         exp_nonpos (SiLU)
+//   dynacore/src/kernel/matmul_registry.cpp:287-429         select_matmul (kernel choice)
 // Used to pin the C oracle (tests) and, on the GPU box, as the timed CPU
 // baseline ("reference" kind) of bench.py.
 
@@ -26,6 +27,8 @@
 #include "dynacore/base/fast_exp.h"
 #include "dynacore/cpu/cpu_kernels.h"
 #include "dynacore/hardware/cpu_info.h"
+#include "dynacore/kernel/kernel_plan.h"
+#include "dynacore/kernel/matmul_registry.h"
 #include "dynacore/quantization/quant_formats.h"
 #include "dynacore/tensor/dtype.h"
 #include "dynacore/tensor/fp16.h"
@@ -66,6 +69,44 @@ std::vector<const ActBlockQ8*> row_ptrs(const void* acts, int64_t row_bytes, int
 extern "C" {
 
 int ref_has_avx2(void) { return cpu_info().features.avx2 ? 1 : 0; }
+
+// select_matmul under a KernelPlan whose matmul knobs are given (the rest at the
+// struct's defaults, no environment) and the MatmulCaps of an int8-accelerated
+// backend without interleaved copies, qmm, SME or external kernels whose kernel
+// table has: quantize_act / _sb / _sx / 16; per-32 row dots for Q4_0, Q8_0, Q4_K,
+// Q6_K; super-block and sub-scaled dots for Q4_K, Q6_K; int16 dots for Q8_0, Q4_K,
+// Q6_K. Returns the MatmulKernelId and writes the MatmulActFormat to *act.
+int ref_select_matmul(int64_t m, int64_t n, int64_t k, int dtype, int x_dense, int expand_min_rows,
+                      int int8_decode_max_rows, int int16_decode_max_rows, int int8_superblock_min_rows,
+                      int int8_superblock_max_rows, int int8_subscale_min_rows, uint32_t disabled, int* act) {
+  if (!valid_type(dtype) || dtype == 17) return -1;
+  const DType wt = static_cast<DType>(dtype);
+  MatmulShape s;
+  s.m = m;
+  s.n = n;
+  s.k = k;
+  s.weight = wt;
+  s.x_dense = x_dense != 0;
+  KernelPlan p;
+  p.expand_min_rows = expand_min_rows;
+  p.int8_decode_max_rows = int8_decode_max_rows;
+  p.int16_decode_max_rows = int16_decode_max_rows;
+  p.int8_superblock_min_rows = int8_superblock_min_rows;
+  p.int8_superblock_max_rows = int8_superblock_max_rows;
+  p.int8_subscale_min_rows = int8_subscale_min_rows;
+  p.matmul_disabled = disabled;
+  const bool kq = wt == DType::kQ4_K || wt == DType::kQ6_K;
+  MatmulCaps c;
+  c.int8_accelerated = true;
+  c.quantize_act = c.quantize_act_sb = c.quantize_act_sx = c.quantize_act16 = true;
+  c.dot_q8_rows = true;
+  c.dot_q8_sb_rows = kq;
+  c.dot_q8_sx_rows = kq;
+  c.dot_q16_rows = wt != DType::kQ4_0;
+  const MatmulSelection sel = select_matmul(s, p, c);
+  if (act != nullptr) *act = static_cast<int>(sel.act);
+  return static_cast<int>(sel.id);
+}
 int ref_physical_cores(void) { return static_cast<int>(cpu_info().physical_cores); }
 int ref_logical_cores(void) { return static_cast<int>(cpu_info().logical_cores); }
 

@@ -4,8 +4,9 @@ over host arrays, with device copies of the weights kept across calls.
 
 The reference's own test of the extension point (dynacore/tests/test_matmul_registry.cpp:679-728)
 checks that eligibility is a pure shape rule and that run's results match a double
-reference within 1e-6; here run must equal dq_matmul on the same rows bit for bit, and
-the oracle within the fp32 bar. Eligibility needs no GPU and runs on the CPU.
+reference within 1e-6; here run must equal dq_matmul_plan under the adapter's plan (the
+defaults unless set) on the same rows bit for bit, and the oracle under the selected
+activation contract within the fp32 bar. Eligibility needs no GPU and runs on the CPU.
 """
 from __future__ import annotations
 
@@ -44,15 +45,21 @@ def _torch():
     return pytest.importorskip("torch")
 
 
-def _dq_matmul(t, rows, k, x, bias):
-    """dq_matmul on device copies of the same rows (the path run() wraps)."""
+def _dq_matmul(t, rows, k, x, bias, plan=None):
+    """dq_matmul_plan on device copies of the same rows (the path run() wraps)."""
     torch = _torch()
     from dynalm_amd import torch_ops as T
 
     w = dq.Weight.upload(t, rows, k)
-    xd = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    if x.strides[0] != 4 * k:
+        # a view of wider rows: keep the caller's row stride on the device (the layout
+        # decides between the fp32 expand and row kernels)
+        xd = torch.from_numpy(np.ascontiguousarray(x.base)).cuda()[:, :k]
+    else:
+        xd = torch.from_numpy(np.ascontiguousarray(x)).cuda()
     bd = torch.from_numpy(bias).cuda() if bias is not None else None
-    y = T.matmul(w, xd, bd)
+    y = torch.empty((x.shape[0], w.n), device="cuda")
+    dq.matmul_plan(w, plan, xd, x.shape[0], xd.stride(0), y, y.stride(0), bd, T.stream())
     torch.cuda.synchronize()
     return y.cpu().numpy()
 
@@ -76,9 +83,10 @@ def test_run_equals_dq_matmul(cuda, t, m):
     ad.run(xs[:, :k], padded, t, k, bias=bias, y=ybuf[:, :n])
     assert np.isnan(ybuf[:, n:]).all()
     y = ybuf[:, :n]
-    want = _dq_matmul(t, rows, k, x, bias)
+    want = _dq_matmul(t, rows, k, xs[:, :k], bias)
     assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
-    fmt = O.ACT_Q8_K if t in (O.Q4_K, O.Q6_K) else O.ACT_PER32
+    # the selection is made on the caller's layout of x (strided here)
+    fmt = dq.select(m, n, k, t, x_dense=m == 1).act
     ok, worst = close(y, O.matmul(t, fmt, rows, O.quantize_act(fmt, x), k, bias=bias))
     assert ok, worst
     st = ad.stats()
@@ -149,3 +157,76 @@ def test_min_rows_policy_and_rejected_calls(cuda):
     assert e.value.status == "invalid_argument"
     assert ad.stats()["runs"] == 0
     ad.close()
+
+
+@pytest.mark.gpu
+def test_set_plan_selects_the_contract(cuda):
+    """Device::set_kernel_plan: the FFN down plan moves a Q6_K decode call to int16
+    activations; the all-integer plan reproduces dq_matmul (the super-block class)
+    bit for bit; NULL restores the defaults (sub-scaled)."""
+    torch = _torch()
+    from dynalm_amd import torch_ops as T
+
+    k, n, m = 1536, 256, 4
+    rows = gguf_weights(O.Q6_K, n, k, 2000, outlier_frac=0.01)
+    x = activations(m, k, 2001)
+    x[:, 5::61] *= np.float32(50.0)  # outlier channels, as the down projection's input has
+    ad = dq.External(0)
+    y_def = ad.run(x, rows, dq.Q6_K, k)
+    assert np.array_equal(y_def.view(np.uint32), _dq_matmul(O.Q6_K, rows, k, x, None).view(np.uint32))
+    assert np.array_equal(y_def.view(np.uint32),
+                          O.matmul(O.Q6_K, O.ACT_SX, rows, O.quantize_act(O.ACT_SX, x), k).view(np.uint32))
+    down = dq.plan_ffn_down()
+    ad.set_plan(down)
+    y16 = ad.run(x, rows, dq.Q6_K, k)
+    assert np.array_equal(y16.view(np.uint32), _dq_matmul(O.Q6_K, rows, k, x, None, down).view(np.uint32))
+    want16 = O.matmul(O.Q6_K, O.ACT_Q16, rows, O.quantize_act(O.ACT_Q16, x), k)
+    xa = O.dequantize_act(O.ACT_Q16, O.quantize_act(O.ACT_Q16, x), k).astype(np.float64)
+    mag = np.abs(xa) @ np.abs(O.dequantize(O.Q6_K, rows, k).astype(np.float64).reshape(n, k)).T
+    assert np.all(np.abs(y16 - want16) <= 2e-6 * mag + 1e-30)
+    allint = dq.Plan(2, 1 << 30, 0, 1, 1 << 30, 0, 0)
+    ad.set_plan(allint)
+    yq = ad.run(x, rows, dq.Q6_K, k)
+    w = dq.Weight.upload(O.Q6_K, rows, k)
+    ref = T.matmul(w, torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    assert np.array_equal(yq.view(np.uint32), ref.cpu().numpy().view(np.uint32))
+    ad.set_plan(None)
+    assert np.array_equal(ad.run(x, rows, dq.Q6_K, k).view(np.uint32), y_def.view(np.uint32))
+    ad.close()
+
+
+@pytest.mark.gpu
+def test_two_adapters_do_not_share_scratch(cuda):
+    """Each adapter keeps its own temporaries: two adapters run from two threads at once
+    (their own streams, different shapes and plans) give the bits of running alone."""
+    import threading
+
+    k = 4096
+    wa = gguf_weights(O.Q8_0, 1024, k, 2100)
+    wb = gguf_weights(O.Q4_K, 768, k, 2101)
+    xa = activations(40, k, 2102)
+    xb = activations(3, k, 2103)
+    a, b = dq.External(0), dq.External(0)
+    b.set_plan(dq.Plan(2, 1 << 30, 0, 1, 1 << 30, 0, 0))  # Q8_K: quantize + skinny GEMV
+    want_a, want_b = a.run(xa, wa, dq.Q8_0, k), b.run(xb, wb, dq.Q4_K, k)
+    errors = []
+
+    def loop(ad, x, w, t, want):
+        try:
+            for _ in range(25):
+                if not np.array_equal(ad.run(x, w, t, k).view(np.uint32), want.view(np.uint32)):
+                    errors.append(t)
+                    return
+        except Exception as e:  # noqa: BLE001 -- reported below
+            errors.append(repr(e))
+
+    th = [threading.Thread(target=loop, args=(a, xa, wa, dq.Q8_0, want_a)),
+          threading.Thread(target=loop, args=(b, xb, wb, dq.Q4_K, want_b))]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert not errors, errors
+    a.close()
+    b.close()
