@@ -323,6 +323,55 @@ def pmc_leg(weights, x, acts, y, stream) -> None:
     log("pmc leg done")
 
 
+def ceilings(steps: int, warmup: int) -> dict:
+    """The two ceilings the headline kernels are quoted against, measured here with
+    libdqceil.so (dynalm_amd/csrc/dq_ceiling.hip): the decode GEMV's loads alone
+    (same grid, same per-wave runs and offsets, no arithmetic) over 33 MB and over
+    132 MB (four times K at the same launch shape), rotated over copies totalling
+    528 MB as the GEMV is; and back-to-back int8 MFMAs on every SIMD."""
+    import ctypes as C
+
+    import torch
+
+    lib = C.CDLL(os.path.join(ROOT, "dynalm_amd", "lib", "libdqceil.so"))
+    lib.dqc_read_q4k.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    lib.dqc_mfma_rate.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.POINTER(C.c_double), C.c_void_p]
+    groups, waves = N // 64, 16
+    out = {"kernel": "dqc_read_q4k: the GEMV's nontemporal dwordx4 loads (8 KB codes + 1 KB headers per super-block "
+                     "and 64 rows) and one fp32 store per row, no arithmetic",
+           "launch": f"{groups} workgroups x {waves} waves (one per 64-row group, as k_gemv)"}
+    for label, nblk, copies in (("33MB", K // 256, 16), ("132MB", 4 * K // 256, 4)):
+        qs = [torch.full((groups * nblk * 8192,), 1, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+        hd = [torch.full((groups * nblk * 1024,), 1, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+        y = torch.empty(groups * 64, dtype=torch.float32, device="cuda")
+
+        def read(i: int, st: int) -> None:
+            rc = lib.dqc_read_q4k(qs[i % copies].data_ptr(), hd[i % copies].data_ptr(), groups, nblk, waves,
+                                  y.data_ptr(), st)
+            assert rc == 0, f"dqc_read_q4k: {rc}"
+
+        ms = time_graph(read, steps, warmup)
+        nbytes = groups * nblk * (8192 + 1024) + groups * 64 * 4
+        out[label] = {"bytes": nbytes, "blocks_per_wave": nblk // waves, "copies": copies,
+                      "ms_per_launch": round(ms, 5), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        del qs, hd, y
+    torch.cuda.empty_cache()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    mfma = {"launch": f"{cus} workgroups x 8 waves (two per SIMD), 8 independent accumulators per wave"}
+    for label, kind, iters in (("16x16x64", 0, 4000), ("32x32x32", 1, 2000)):
+        buf = torch.empty(cus * 512, dtype=torch.int32, device="cuda")
+        ops = C.c_double(0.0)
+
+        def rate(i: int, st: int) -> None:
+            rc = lib.dqc_mfma_rate(cus, iters, kind, buf.data_ptr(), C.byref(ops), st)
+            assert rc == 0, f"dqc_mfma_rate: {rc}"
+
+        ms = time_graph(rate, 5, 2)
+        mfma[label] = {"ms_per_launch": round(ms, 4), "tops": round(ops.value / (ms * 1e-3) / 1e12, 1)}
+    out["mfma"] = mfma
+    return out
+
+
 def measured_traffic() -> dict:
     """HBM bytes per launch of the measured kernels, as the committed counter summary
     records them (lines `traffic <kernel> <bytes>`); empty if it is absent."""
@@ -440,6 +489,11 @@ def main() -> None:
     ops = 2.0 * m * N * K
     tops = ops / (ms_gemm * 1e-3) / 1e12
 
+    log("ceilings: plain read at the GEMV's launch shape, int8 MFMA rate")
+    ceil = ceilings(args.steps, args.warmup)
+    read_ceiling = ceil["33MB"]["gbs"]
+    mfma_ceiling = ceil["mfma"]["16x16x64"]["tops"]
+
     traffic = measured_traffic()
     result = {
         "metric": METRIC,
@@ -465,6 +519,10 @@ def main() -> None:
             "algorithmic_bytes_per_step": bytes_step,
         },
         "pct_peak_hbm": round(100 * value / PEAK_HBM_GBS, 2),
+        "read_ceiling_gbs": read_ceiling,
+        "pct_of_read_ceiling": round(100 * value / read_ceiling, 2),
+        "mfma_ceiling_tops": mfma_ceiling,
+        "ceilings": ceil,
         "tokens_per_s": round(1e3 / ms_step, 1),
         "roofline": {
             "kernel": "dq::k_gemv<Q4_K, Q8_K, M=1, fused quantization>",
@@ -486,6 +544,7 @@ def main() -> None:
             "ms_per_launch": round(ms_gemm, 4),
             "tops": round(tops, 2),
             "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2),
+            "pct_of_mfma_ceiling": round(100 * tops / mfma_ceiling, 2),
             "tokens_per_s": round(m / (ms_gemm * 1e-3), 1),
             "roofline": {"kernel": "dq::k_gemm_q4k_big<4, 2, 4>", "bound": "mfma", "achieved": round(tops, 2),
                          "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4),

@@ -1,4 +1,6 @@
-"""Builds libdynaq.so (the C-ABI library) in-tree with hipcc for gfx950.
+"""Builds libdynaq.so (the C-ABI library) in-tree with hipcc for gfx950, and
+libdqceil.so, the benchmark's ceiling probes (a plain read at the decode GEMV's
+launch shape and an int8 MFMA rate loop; bench.py loads it, the library does not).
 
     python -m dynalm_amd.build          # or dynalm_amd.build.build()
 
@@ -16,6 +18,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libdynaq.so")
+CEIL_LIB = os.path.join(LIB_DIR, "libdqceil.so")
+CEIL_SOURCES = ["dq_ceiling.hip"]
 
 SOURCES = ["dq_kernels.hip", "dq_gemv.hip", "dq_gemm.hip", "dq_gemm_b32.hip", "dq_skinny.hip", "dq_api.cpp",
            "dq_gguf.cpp", "dq_external.cpp", "dq_noalloc.hip",
@@ -67,15 +71,17 @@ def build(verbose: bool = False) -> str:
 
     os.makedirs(LIB_DIR, exist_ok=True)
     cc = hipcc()
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
-        objs = list(pool.map(lambda src: _compile(cc, src, verbose), SOURCES))
-    tmp = LIB + ".tmp"
-    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
-    os.replace(tmp, LIB)
-    for o in objs:
+    srcs = SOURCES + CEIL_SOURCES
+    with ThreadPoolExecutor(max_workers=len(srcs)) as pool:
+        objs = dict(zip(srcs, pool.map(lambda src: _compile(cc, src, verbose), srcs)))
+    for lib, group in ((LIB, SOURCES), (CEIL_LIB, CEIL_SOURCES)):
+        tmp = lib + ".tmp"
+        cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *(objs[s] for s in group)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
+        os.replace(tmp, lib)
+    for o in objs.values():
         os.remove(o)
     return LIB
 

@@ -250,13 +250,26 @@ DQ_DEV void compute(const Chunk<kQ4_K, U>& ch, int bb, const uint8_t* st, Out<M>
         const uint8_t* ab = st + (mm * o.nblk + b) * kStageQ8K;
         const v4u sj = lds16(ab + 304);   // s_j >> 7 (j = 0..3, 4..7), s_j & 127 (0..3, 4..7)
         const v4u codd = lds16(ab + 320);  // 128 s_j, j = 1, 3, 5, 7
+        // One row, one super-block per chunk (the decode launch): all sixteen code
+        // reads are issued here, before the first wait on the weights, so a wave whose
+        // weights land last computes without further LDS round trips (64 VGPRs).
+        constexpr bool kAll = M == 1 && U == 1;
+        v4u av[kAll ? 16 : 1];
+        if constexpr (kAll) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) av[i] = lds16(ab + 16 + 16 * i);
+          __builtin_amdgcn_sched_barrier(0);
+        }
         int S = 0;
 #pragma unroll
         for (int jp = 0; jp < 4; ++jp) {
           const v4u c0 = ch.q[u][2 * jp], c1 = ch.q[u][2 * jp + 1];
           const uint8_t* cp = ab + 16 + 64 * jp;
-          const int pe = sdot16(c1 & 0x0F0F0F0Fu, lds16(cp + 16), sdot16(c0 & 0x0F0F0F0Fu, lds16(cp), 0));
-          const int x16 = sdot16(c1 & 0xF0F0F0F0u, lds16(cp + 48), sdot16(c0 & 0xF0F0F0F0u, lds16(cp + 32), (int)codd[jp]));
+          const v4u a0 = kAll ? av[kAll ? 4 * jp : 0] : lds16(cp), a1 = kAll ? av[kAll ? 4 * jp + 1 : 0] : lds16(cp + 16);
+          const v4u a2 = kAll ? av[kAll ? 4 * jp + 2 : 0] : lds16(cp + 32);
+          const v4u a3 = kAll ? av[kAll ? 4 * jp + 3 : 0] : lds16(cp + 48);
+          const int pe = sdot16(c1 & 0x0F0F0F0Fu, a1, sdot16(c0 & 0x0F0F0F0Fu, a0, 0));
+          const int x16 = sdot16(c1 & 0xF0F0F0F0u, a3, sdot16(c0 & 0xF0F0F0F0u, a2, (int)codd[jp]));
           const int po = x16 >> 4;
           const u32 scw = jp < 2 ? sc_lo : sc_hi;
           const int e = 16 * (jp & 1);
@@ -1014,6 +1027,22 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
     const float* dp = rec + M * nblk * 64 + mm * nblk;
     float v = 0.0f;
     int b = 0;
+    if (nblk <= 16) {
+      // short rows (K <= 4096): every read first, then the sixteen dependent FMAs
+      // (indices past the row repeat its last block and are not used)
+      float t[16], dv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int bc = i < nblk ? i : nblk - 1;
+        t[i] = tp[bc * 64];
+        dv[i] = dp[bc];
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (i < nblk) v = fmaf(dv[i], t[i], v);
+      }
+      return v;
+    }
     for (; b + 4 <= nblk; b += 4) {
       const float t0 = tp[b * 64], t1 = tp[(b + 1) * 64], t2 = tp[(b + 2) * 64], t3 = tp[(b + 3) * 64];
       const float d0 = dp[b], d1 = dp[b + 1], d2 = dp[b + 2], d3 = dp[b + 3];

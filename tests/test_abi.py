@@ -36,6 +36,24 @@ def test_exports_are_the_only_public_symbols():
     assert {s for s in public if s.startswith("dq_")} == set(declared_symbols())
 
 
+def test_ceiling_probe_library_is_separate():
+    """bench.py's ceiling probes live in their own library: it loads and exports its
+    two entry points and rejects bad launches on the host; libdynaq exports none of them."""
+    import subprocess
+
+    path = os.path.join(ROOT, "dynalm_amd", "lib", "libdqceil.so")
+    if not os.path.exists(path):
+        pytest.skip("libdqceil.so not built")
+    lib = C.CDLL(path)
+    lib.dqc_read_q4k.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    lib.dqc_mfma_rate.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.POINTER(C.c_double), C.c_void_p]
+    assert lib.dqc_read_q4k(None, None, 224, 16, 16, None, None) == 1
+    assert lib.dqc_read_q4k(1, 1, 224, 16, 3, 1, None) == 1  # waves must divide the blocks
+    assert lib.dqc_mfma_rate(256, 10, 2, 1, C.byref(C.c_double()), None) == 1  # unknown MFMA kind
+    out = subprocess.run(["nm", "-D", "--defined-only", dq.lib_path()], capture_output=True, text=True).stdout
+    assert "dqc_" not in out
+
+
 def test_sizes():
     # dtype_row_bytes (dynacore/src/tensor/dtype.cpp:24-54)
     assert dq.row_bytes(dq.Q4_K, 4096) == 16 * 144
