@@ -37,6 +37,7 @@ sys.path.insert(0, ROOT)
 METRIC = "Q4_K GEMV HBM GB/s (% peak) at M=1; Q4_K GEMM int8 TOPS (% peak) at M=512"
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E
 PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA
+PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 K, N = 4096, 14336        # config 3 gate/up, config 4
 Q4K_ROW = K // 256 * 144
 Q8K_ROW = K // 256 * 292
@@ -489,6 +490,21 @@ def main() -> None:
     ops = 2.0 * m * N * K
     tops = ops / (ms_gemm * 1e-3) / 1e12
 
+    # ---- the fp32 expand + GEMM class at the same shape (the default plan's choice for
+    # m > 8 dense fp32 rows): weights expanded in LDS, v_mfma_f32_32x32x2_f32
+    yf = torch.empty((m, N), dtype=torch.float32, device="cuda")
+
+    def f32_gemm(i: int, st: int) -> None:
+        dq.matmul_plan(weights[i % ng], None, xg, m, K, yf, N, None, st)
+
+    def f32_row_dot(i: int, st: int) -> None:
+        dq.matmul_act(weights[i % ng], dq.ACT_F32, xg, m, K, yf, N, None, st)
+
+    log(f"fp32 expand GEMM M={m}")
+    ms_f32 = time_graph(f32_gemm, 10, 2)
+    ms_f32_rows = time_graph(f32_row_dot, 3, 1)
+    tf32 = ops / (ms_f32 * 1e-3) / 1e12
+
     log("ceilings: plain read at the GEMV's launch shape, int8 MFMA rate")
     ceil = ceilings(args.steps, args.warmup)
     read_ceiling = ceil["33MB"]["gbs"]
@@ -550,6 +566,15 @@ def main() -> None:
                          "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4),
                          "traffic": traffic.get("gemm_m512")},
         },
+    }
+    result["f32_expand_gemm"] = {
+        "workload": f"config 4 prefill shape, fp32 activations: dq_matmul_plan (default plan -> kF32ExpandGemm), "
+                    f"Q4_K M={m} K={K} N={N}",
+        "ms_per_launch": round(ms_f32, 4),
+        "tflops": round(tf32, 2),
+        "ms_row_dot_gemv": round(ms_f32_rows, 4),
+        "roofline": {"kernel": "dq::k_gemm_f32<Q4_K>", "bound": "mfma", "achieved": round(tf32, 2),
+                     "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": round(tf32 / PEAK_FP32_MFMA_TFLOPS, 4)},
     }
     if ms_gated is not None:
         gbytes = 2 * Q4K_ROW * N + Q8K_ROW + 4 * N

@@ -370,6 +370,7 @@ class MatmulShape(C.Structure):
 # dq_kernel: dynacore MatmulKernelId values (kernel/matmul_registry.h:33-51)
 KERNEL_INT8_SUBSCALED, KERNEL_INT8_SUPERBLOCK, KERNEL_INT8_PER32 = 7, 8, 9
 KERNEL_INT16_ROWS, KERNEL_F32_EXPAND_GEMM, KERNEL_F32_ROW_DOT = 13, 14, 15
+F32_GEMM_MIN_ROWS = 16  # DQ_F32_GEMM_MIN_ROWS: the expand class on the matrix cores from here on
 KERNEL_NAMES = {7: "int8_subscaled", 8: "int8_superblock", 9: "int8_per32", 13: "int16_rows", 14: "f32_expand_gemm",
                 15: "f32_row_dot"}
 

@@ -397,6 +397,16 @@ int matmul_sel_impl(const dq_weight* w, const dq_selection& sel, const float* x,
     case DQ_KERNEL_INT8_PER32:  // per-32: dq_matmul's routes for Q8_0 / Q4_0
       if (t == DQ_Q8_0 || t == DQ_Q4_0) return matmul_impl(w, x, m, x_stride, y, y_stride, bias, s, r);
       break;
+    case DQ_KERNEL_F32_EXPAND_GEMM:  // expand + GEMM on the matrix cores (cpu_device.cpp:1114-1152)
+      if (m >= kF32GemmMinRows) {
+        const int64_t xs = m > 1 ? x_stride : w->dev.k;
+        if ((127 * xs + w->dev.k) * 4 >= ((int64_t)1 << 32)) {  // one tile's 128 rows, 32-bit offsets
+          return fail(DQ_UNSUPPORTED, "128 activation rows of stride %lld exceed 4 GiB", (long long)xs);
+        }
+        DQ_HIP(launch_gemm_f32(w->dev, x, xs, m, 0, w->dev.n, y, y_stride, bias, s), "fp32 gemm launch");
+        return DQ_OK;
+      }
+      break;
     default:
       break;
   }

@@ -76,6 +76,12 @@ hipError_t launch_units(const WeightDev& w, int af, const uint8_t* acts, int64_t
 hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
                        float* y, int64_t ys, const float* bias, hipStream_t s);
 bool gemm_supported(int dtype, int af);
+// The expand-class fp32 GEMM (dq_gemm_f32.hip): weight tiles expanded to fp32 in LDS
+// and contracted with the fp32 rows x (stride xs floats) on the matrix cores; any of
+// the four weight types. Below kF32GemmMinRows rows the fp32 GEMV passes are faster.
+hipError_t launch_gemm_f32(const WeightDev& w, const float* x, int64_t xs, int64_t m, int64_t n0, int64_t n1, float* y,
+                           int64_t ys, const float* bias, hipStream_t s);
+constexpr int64_t kF32GemmMinRows = DQ_F32_GEMM_MIN_ROWS;
 // The 32-value block GEMM (Q8_0 / Q4_0 x per-32 ActBlockQ8) that launch_gemm dispatches to.
 hipError_t launch_gemm_b32(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0,
                            int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s);

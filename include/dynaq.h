@@ -280,6 +280,13 @@ typedef enum dq_kernel {
   DQ_KERNEL_F32_ROW_DOT = 15,     /* kF32RowDot: fp32 activations (reference class) */
 } dq_kernel;
 
+/* DQ_KERNEL_F32_EXPAND_GEMM runs on the matrix cores from this many rows on: weight
+ * tiles expanded to fp32 as the reference's x86 expansion does (one fma per value),
+ * contracted with the fp32 rows on v_mfma_f32 (sums in the matrix cores' order, within
+ * 1e-5 of sum |x_k w_k|; a row's outputs do not depend on the other rows). Fewer rows
+ * run the fp32 row-dot GEMV, the same class in vec_dot order. */
+#define DQ_F32_GEMM_MIN_ROWS 16
+
 /* The matmul knobs of KernelPlan that choose among these kernels, with the
  * reference's meaning and names (kernel_plan.h:34-92); matmul_disabled is a mask
  * of (1u << dq_kernel), as KernelPlan::matmul_disabled (kernel_plan.h:144-148). */

@@ -220,6 +220,50 @@ int dqo_dequantize(int dtype, const void* blocks, float* y, int64_t n) {
   return 0;
 }
 
+/* kernels_avx2.cpp:370-466: store_scaled(q, n, d, mn) writes fma(q, d, mn) for each
+ * code; Q4_K passes (d * sc_j, -dmin * m_j) per 32 values (low nibbles of 32 qs bytes,
+ * then their high nibbles), Q6_K (d * sc_g, 0) per 16, Q8_0 / Q4_0 (d, 0) per block. */
+int dqo_expand_x86(int dtype, const void* blocks, float* y, int64_t n) {
+  const int64_t be = dqo_block_elems(dtype), bb = dqo_block_bytes(dtype);
+  if (be <= 0 || n % be != 0 || dtype == DQO_Q8_K) return -1;
+  const uint8_t* b = (const uint8_t*)blocks;
+  int8_t q[256];
+  for (int64_t i = 0; i < n / be; ++i, b += bb, y += be) {
+    switch (dtype) {
+      case DQO_Q8_0: { /* :375-378 */
+        const float d = dqo_fp16_to_fp32(rd16(b));
+        for (int j = 0; j < 32; ++j) y[j] = fmaf((float)(int8_t)b[2 + j], d, 0.0f);
+        break;
+      }
+      case DQO_Q4_0: { /* :380-391 */
+        const float d = dqo_fp16_to_fp32(rd16(b));
+        q40_codes(b, q);
+        for (int j = 0; j < 32; ++j) y[j] = fmaf((float)q[j], d, 0.0f);
+        break;
+      }
+      case DQO_Q4_K: { /* :420-438 */
+        const float d = dqo_fp16_to_fp32(rd16(b)), dmin = dqo_fp16_to_fp32(rd16(b + 2));
+        q4k_codes(b, q);
+        for (int j = 0; j < 8; ++j) {
+          uint8_t sc, mn;
+          dqo_scale_min_k4(j, b + 4, &sc, &mn);
+          const float d1 = d * (float)sc, m1 = -dmin * (float)mn;
+          for (int t = 0; t < 32; ++t) y[32 * j + t] = fmaf((float)q[32 * j + t], d1, m1);
+        }
+        break;
+      }
+      case DQO_Q6_K: { /* :440-466 */
+        const float d = dqo_fp16_to_fp32(rd16(b + 208));
+        q6k_codes(b, q);
+        for (int e = 0; e < 256; ++e) y[e] = fmaf((float)q[e], d * (float)(int8_t)b[192 + e / 16], 0.0f);
+        break;
+      }
+      default: return -1;
+    }
+  }
+  return 0;
+}
+
 int dqo_dequantize_act(int fmt, const void* a, float* y, int64_t n) {
   const int64_t be = dqo_act_block_elems(fmt), bb = act_block_bytes(fmt);
   if (be <= 0 || n % be != 0) return -1;

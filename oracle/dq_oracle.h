@@ -82,6 +82,10 @@ void dqo_scale_min_k4(int j, const uint8_t* q, uint8_t* sc, uint8_t* m);
 
 /* Dequantize n values (a whole number of blocks). Returns 0, or -1 on a bad type / size. */
 int dqo_dequantize(int dtype, const void* blocks, float* y, int64_t n);
+/* The x86 expansion of the fp32 expand + GEMM class (dynacore/cpu/avx2/kernels_avx2.cpp:
+ * 370-466): every value one fma(q, scale, offset) of the block's scale products.
+ * Returns 0, or -1 on a bad type / size. */
+int dqo_expand_x86(int dtype, const void* blocks, float* y, int64_t n);
 /* Dequantize a quantized activation row (x ~= d * q). */
 int dqo_dequantize_act(int fmt, const void* a, float* y, int64_t n);
 

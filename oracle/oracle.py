@@ -44,6 +44,7 @@ def _load_oracle():
         "dqo_fp32_to_fp16_n": (None, [_P, _P, _I64]),
         "dqo_scale_min_k4": (None, [C.c_int, _P, _P, _P]),
         "dqo_dequantize": (C.c_int, [C.c_int, _P, _P, _I64]),
+        "dqo_expand_x86": (C.c_int, [C.c_int, _P, _P, _I64]),
         "dqo_dequantize_act": (C.c_int, [C.c_int, _P, _P, _I64]),
         "dqo_quantize_act": (C.c_int, [C.c_int, _P, _P, _I64]),
         "dqo_quantize_act_rows": (C.c_int, [C.c_int, _P, _I64, _I64, _I64, _P]),
@@ -143,6 +144,16 @@ def dequantize(dtype: int, blocks: np.ndarray, k: int) -> np.ndarray:
     out = np.empty((rows, k), np.float32)
     for r in range(rows):
         _check(lib().dqo_dequantize(dtype, _ptr(blocks[r]), _ptr(out[r]), k), "dequantize")
+    return out
+
+
+def expand_x86(dtype: int, blocks: np.ndarray, k: int) -> np.ndarray:
+    """The fp32 expand + GEMM class's weight expansion (one fma per value, the
+    reference's x86 dequant), [rows, k]."""
+    blocks = np.ascontiguousarray(np.atleast_2d(blocks), dtype=np.uint8)
+    out = np.empty((blocks.shape[0], k), np.float32)
+    for r in range(blocks.shape[0]):
+        _check(lib().dqo_expand_x86(dtype, _ptr(blocks[r]), _ptr(out[r]), k), "expand_x86")
     return out
 
 
@@ -265,6 +276,8 @@ def ref():
             "ref_vec_dot": (C.c_int, [C.c_int, C.c_int, _P, _P, _I64, _P]),
             "ref_select_matmul": (C.c_int, [_I64, _I64, _I64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                             C.c_int, C.c_int, C.c_uint32, C.POINTER(C.c_int)]),
+            "ref_expand_x86": (C.c_int, [C.c_int, _P, _P, _I64]),
+            "ref_expand_gemm": (C.c_int, [C.c_int, _P, _I64, _I64, _P, _I64, _I64, _P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(r, name)
@@ -306,6 +319,30 @@ def ref_dequantize(dtype: int, blocks: np.ndarray, k: int) -> np.ndarray:
     out = np.empty(k, np.float32)
     _check(r.ref_dequantize(dtype, _ptr(blocks), _ptr(out), k), "ref_dequantize")
     return out
+
+
+def ref_expand_x86(dtype: int, rows: np.ndarray, k: int) -> np.ndarray:
+    """The reference's x86 expansion of weight rows to fp32 (the AVX2 dequant that
+    kF32ExpandGemm uses), [n, k]."""
+    r = ref()
+    rows = np.ascontiguousarray(np.atleast_2d(rows), dtype=np.uint8)
+    out = np.empty((rows.shape[0], k), np.float32)
+    for i in range(rows.shape[0]):
+        _check(r.ref_expand_x86(dtype, _ptr(rows[i]), _ptr(out[i]), k), "ref_expand_x86")
+    return out
+
+
+def ref_expand_gemm(dtype: int, rows: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """The reference's kF32ExpandGemm on one thread: y [m, n] = x [m, k] . expand(rows)^T
+    in its panel / gemm_panel order."""
+    r = ref()
+    rows = np.ascontiguousarray(np.atleast_2d(rows), dtype=np.uint8)
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    m, k = x.shape
+    y = np.empty((m, rows.shape[0]), np.float32)
+    _check(r.ref_expand_gemm(dtype, _ptr(rows), rows.shape[1], rows.shape[0], _ptr(x), m, k, _ptr(y)),
+           "ref_expand_gemm")
+    return y
 
 
 def ref_dot_rows(kind: int, dtype: int, w_row: np.ndarray, acts: np.ndarray, k: int) -> np.ndarray:

@@ -273,4 +273,32 @@ int64_t ref_bench_gemv(int kind, int dtype, const void* const* w_copies, int nco
 // reference's SiLU (dynacore/cpu/cpu_device.cpp:117-123).
 float ref_exp_nonpos(float x) { return dynacore::exp_nonpos(x); }
 
+// The x86 expansion of kF32ExpandGemm: the AVX2 table's dequant for the type
+// (kernels_avx2.cpp:370-466, installed at :1925-1933). Returns -1 without AVX2.
+int ref_expand_x86(int dtype, const void* blocks, float* y, int64_t n) {
+  if (!valid_type(dtype) || !cpu_info().features.avx2) return -1;
+  const DequantFn f = avx2_table().dequant_for(static_cast<DType>(dtype));
+  if (f == nullptr || n % dtype_block_elems(static_cast<DType>(dtype)) != 0) return -1;
+  f(blocks, y, n);
+  return 0;
+}
+
+// kF32ExpandGemm on one thread (cpu_device.cpp:1114-1152 with gemm_k_block = 0):
+// panels of 4 weight rows expanded by the AVX2 dequant, then the AVX2 gemm_panel
+// against all m activation rows (x: m rows of stride k). y: m x n, stride n.
+int ref_expand_gemm(int dtype, const void* w, int64_t w_row_bytes, int64_t n, const float* x, int64_t m, int64_t k,
+                    float* y) {
+  if (!valid_type(dtype) || !cpu_info().features.avx2) return -1;
+  const CpuKernels& kt = avx2_table();
+  const DequantFn f = kt.dequant_for(static_cast<DType>(dtype));
+  if (f == nullptr || kt.gemm_panel == nullptr) return -1;
+  std::vector<float> panel(static_cast<size_t>(4 * k));
+  for (int64_t j0 = 0; j0 < n; j0 += 4) {
+    const int nr = static_cast<int>(std::min<int64_t>(4, n - j0));
+    for (int r = 0; r < nr; ++r) f(static_cast<const uint8_t*>(w) + (j0 + r) * w_row_bytes, panel.data() + r * k, k);
+    kt.gemm_panel(panel.data(), nr, x, k, m, k, y + j0, n, false);
+  }
+  return 0;
+}
+
 }  // extern "C"

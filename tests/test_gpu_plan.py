@@ -59,11 +59,13 @@ def test_default_plan(cuda, t, m):
     sel = dq.select(m, n, k, t)
     y = run_plan(w, None, x)
     # the same bits as the selected contract's own path
+    mfma_f32 = sel.kernel == dq.KERNEL_F32_EXPAND_GEMM and m >= dq.F32_GEMM_MIN_ROWS
     if sel.kernel == dq.KERNEL_INT8_PER32 and t in (O.Q8_0, O.Q4_0):
         same = host(T.matmul(w, dev(x)))
-    else:
+    elif not mfma_f32:  # the matrix-core GEMM sums in its own order (tests/test_gpu_f32_gemm.py)
         same = host(T.matmul_act(w, sel.act, dev(x)))
-    assert np.array_equal(y.view(np.uint32), same.view(np.uint32)), dq.KERNEL_NAMES[sel.kernel]
+    if not mfma_f32:
+        assert np.array_equal(y.view(np.uint32), same.view(np.uint32)), dq.KERNEL_NAMES[sel.kernel]
     want = O.matmul(t, sel.act, rows, O.quantize_act(sel.act, x), k)
     if sel.act == O.ACT_SX:
         assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
@@ -71,7 +73,7 @@ def test_default_plan(cuda, t, m):
         ok, worst = close(y, want)
         assert ok, f"{dq.KERNEL_NAMES[sel.kernel]}: worst error ratio {worst:.3g}"
     else:
-        assert within_terms(y, want, t, sel.act, rows, x, k), dq.KERNEL_NAMES[sel.kernel]
+        assert within_terms(y, want, t, sel.act, rows, x, k, rel=1e-5 if mfma_f32 else 2e-6), dq.KERNEL_NAMES[sel.kernel]
 
 
 @pytest.mark.parametrize("t", TYPES, ids=lambda t: O.TYPE_NAMES[t])
