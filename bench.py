@@ -15,9 +15,10 @@ Both `roofline` objects use per-kernel durations from HIP events around one repl
 of a HIP graph that holds exactly K back-to-back launches of that kernel alone (the
 Python launch loop costs ~5 us per call, close to the kernel itself; its timing is
 reported beside). `cpu_baseline` times the
-kernel dynacore selects on x86 for this call (Q4_K x sub-scaled int8,
-dot_rows_n_sx_q4_K, dynacore/src/kernel/matmul_registry.cpp:139-165) compiled from
-the reference sources (oracle/_ref) on the host cores, on a bounded sample.
+call dynacore makes on x86 for this step (Q4_K x sub-scaled int8: quantize_act_sx and
+dot_q8_sx_rows_n on its ThreadPool, dynacore/cpu/cpu_device.cpp:941-960,
+dynacore/src/kernel/matmul_registry.cpp:139-165) compiled from the reference sources
+(oracle/_ref) on the host's physical cores, on a bounded sample.
 Inputs are synthetic: random valid Q4_K blocks (fp16 d, dmin in U(0.002, 0.02)) and
 N(0, 1) activations; timing does not depend on the values.
 """
@@ -103,52 +104,107 @@ def time_graph(fn, iters: int, warmup: int) -> float:
     return ms
 
 
-def cpu_baseline(w_host: np.ndarray, copies: int, budget_s: float) -> dict:
-    """dynacore's x86 decode kernel for this call, timed on the host cores."""
+def host_cpu() -> dict:
+    """The host CPU as bench.py reports it: model, ISA flags of interest, cores."""
+    info = {"cpu": "unknown", "isa": []}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and info["cpu"] == "unknown":
+                    info["cpu"] = line.split(":", 1)[1].strip()
+                elif line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    info["isa"] = [f for f in ("avx2", "fma", "f16c", "avx_vnni", "avx512f", "avx512_vnni", "amx_int8")
+                                   if f in flags]
+                    break
+    except OSError:
+        pass
+    return info
+
+
+def llc_of_cpus(cpus) -> tuple[int, int]:
+    """(bytes of one last-level cache, number of distinct last-level caches) over the
+    given CPUs, from sysfs (the highest cache index that is not an instruction cache)."""
+    base = "/sys/devices/system/cpu"
+    size, seen = 0, set()
+    for c in sorted(cpus):
+        d = f"{base}/cpu{c}/cache"
+        try:
+            idx = sorted(int(e[5:]) for e in os.listdir(d) if e.startswith("index"))
+        except OSError:
+            continue
+        for i in reversed(idx):
+            try:
+                with open(f"{d}/index{i}/type") as f:
+                    if f.read().strip() == "Instruction":
+                        continue
+                with open(f"{d}/index{i}/size") as f:
+                    txt = f.read().strip()
+                with open(f"{d}/index{i}/shared_cpu_list") as f:
+                    shared = f.read().strip()
+            except OSError:
+                continue
+            mult = {"K": 1 << 10, "M": 1 << 20, "G": 1 << 30}.get(txt[-1:], 1)
+            size = max(size, int(txt.rstrip("KMG")) * mult)
+            seen.add(shared)
+            break
+    return size, len(seen)
+
+
+def cpu_baseline(w_host: np.ndarray, budget_s: float) -> dict:
+    """dynacore's x86 decode call for this step, timed on the host cores: the
+    reference's own CpuDevice decode path for the sub-scaled int8 class (its x86
+    default for M=1, quantize_act_sx included in every call) on its own ThreadPool,
+    created once, over the weight rows with its grain (oracle/_ref, ref_bench_decode_sx)."""
     from oracle import oracle as O
 
     x = O.normal(7, K)
     nbytes = Q4K_ROW * N + K // 256 * 320 + 4 * N
-    cores = min(16, os.cpu_count() or 1)
-    cpu = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    host = host_cpu()
     r = O.ref()
     if r is not None and r.ref_has_avx2():
         import ctypes as C
 
-        acts = O.ref_quantize("sx", x)
+        phys, logical = r.ref_physical_cores(), r.ref_logical_cores()
+        try:
+            cpus = os.sched_getaffinity(0)
+        except AttributeError:
+            cpus = set(range(os.cpu_count() or 1))
+        share = len(cpus)
+        threads = max(1, min(phys, share, 16))  # the GPU box's CPU share is 16
+        llc, n_llc = llc_of_cpus(cpus)
+        if llc == 0:
+            llc, n_llc = int(r.ref_llc_bytes()), 1
+        # rotate over copies totalling at least twice all the last-level caches the threads can use
+        copies = int(min(16, max(2, -(-2 * max(llc * n_llc, 1) // w_host.nbytes) + 1)))
         ws = [w_host] + [w_host.copy() for _ in range(copies - 1)]
         ptrs = (C.c_void_p * copies)(*[w.ctypes.data for w in ws])
         y = np.empty(N, np.float32)
-        ns = r.ref_bench_gemv(3, O.Q4_K, ptrs, copies, Q4K_ROW, N, acts.ctypes.data, acts.size, 1, K, y.ctypes.data,
-                              cores, 2)
-        per = ns / 2 / 1e9
+        chunks = 32  # KernelPlan::matmul_chunks_per_thread (kernel_plan.h:40)
+
+        def run(th: int, iters: int) -> float:
+            ns = r.ref_bench_decode_sx(O.Q4_K, ptrs, copies, Q4K_ROW, N, x.ctypes.data, 1, K, y.ctypes.data, th,
+                                       chunks, iters)
+            assert ns > 0, f"ref_bench_decode_sx: {ns}"
+            return ns / iters / 1e9
+
+        per = run(threads, 2)
         iters = max(4, int(budget_s / max(per, 1e-6)))
-        ns = r.ref_bench_gemv(3, O.Q4_K, ptrs, copies, Q4K_ROW, N, acts.ctypes.data, acts.size, 1, K, y.ctypes.data,
-                              cores, iters)
-        sec = ns / iters / 1e9
-        # one thread as well (the scalar-core rate), on a shorter sample
-        ns1 = r.ref_bench_gemv(3, O.Q4_K, ptrs, copies, Q4K_ROW, N, acts.ctypes.data, acts.size, 1, K, y.ctypes.data,
-                               1, 1)
-        iters1 = max(2, int(0.25 * budget_s / max(ns1 / 1e9, 1e-6)))
-        ns1 = r.ref_bench_gemv(3, O.Q4_K, ptrs, copies, Q4K_ROW, N, acts.ctypes.data, acts.size, 1, K, y.ctypes.data,
-                               1, iters1)
-        sec1 = ns1 / iters1 / 1e9
-        return {"value": round(nbytes / sec / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "reference",
+        sec = run(threads, iters)
+        sec1 = run(1, 1)
+        iters1 = max(2, int(0.25 * budget_s / max(sec1, 1e-6)))
+        sec1 = run(1, iters1)
+        return {"value": round(nbytes / sec / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "reference",
                 "ms_per_call": round(sec * 1e3, 4), "tokens_per_s": round(1.0 / sec, 1),
                 "one_thread": {"value": round(nbytes / sec1 / 1e9, 2), "ms_per_call": round(sec1 * 1e3, 4),
                                "calls": iters1},
-                "sample": f"{iters} calls of the full K=4096 N=14336 M=1 Q4_K GEMV, dynacore AVX2 "
-                          f"dot_rows_n_sx_q4_K (sub-scaled int8 activations, its x86 default), {cores} threads "
-                          f"over 16-row units, {copies} rotated weight copies",
-                "cpu": cpu, "isa": "avx2+fma+f16c"}
+                "sample": f"{iters} calls of the full K=4096 N=14336 M=1 Q4_K decode matmul as dynacore's CpuDevice "
+                          f"runs it on x86 (quantize_act_sx + dot_q8_sx_rows_n, kInt8Subscaled) on its ThreadPool of "
+                          f"{threads} threads (grain_for over rows, {chunks} chunks per thread), {copies} rotated "
+                          f"weight copies ({copies * w_host.nbytes >> 20} MiB; {n_llc} last-level caches of "
+                          f"{llc >> 20} MiB over the process's CPUs)",
+                "cpu": host["cpu"], "isa": host["isa"], "physical_cores": phys, "logical_cores": logical,
+                "cpu_share": share, "llc_bytes": llc, "llc_count": n_llc, "weight_copies": copies}
     # scalar oracle restatement on a bounded sample of rows, scaled to N
     a = O.quantize_act(O.ACT_SX, x[None])
     rows = 256
@@ -157,7 +213,8 @@ def cpu_baseline(w_host: np.ndarray, copies: int, budget_s: float) -> dict:
     sec = (time.perf_counter() - t0) * N / rows
     return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "ms_per_call": round(sec * 1e3, 3), "tokens_per_s": round(1.0 / sec, 2),
-            "sample": f"{rows} of {N} rows of the Q4_K x sub-scaled GEMV (scalar oracle), scaled to N", "cpu": cpu}
+            "sample": f"{rows} of {N} rows of the Q4_K x sub-scaled GEMV (scalar oracle), scaled to N",
+            "cpu": host["cpu"], "isa": host["isa"]}
 
 
 # Config 5: Qwen2.5-1.5B-shaped decode step, M = 16: per layer (name, dtype, n, k)
@@ -595,7 +652,7 @@ def main() -> None:
         result["decode_stack_m16"] = decode_stack(args.stack_steps, stream)
     if not args.no_cpu:
         log("CPU baseline")
-        result["cpu_baseline"] = cpu_baseline(w_host, 4, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(w_host, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 

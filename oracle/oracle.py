@@ -267,8 +267,6 @@ def ref():
             "ref_quantize_act_sx": (C.c_int, [_P, _P, _I64]),
             "ref_dot_rows": (C.c_int, [C.c_int, C.c_int, _P, _P, _I64, C.c_int, _I64, _P]),
             "ref_dot_rows_n": (C.c_int, [C.c_int, C.c_int, _P, _I64, _I64, _I64, _P, _I64, C.c_int, _I64, _P, _I64, _P]),
-            "ref_bench_gemv": (_I64, [C.c_int, C.c_int, C.POINTER(_P), C.c_int, _I64, _I64, _P, _I64, C.c_int, _I64, _P,
-                                      C.c_int, C.c_int]),
             "ref_exp_nonpos": (C.c_float, [C.c_float]),
             "ref_quantize_act16": (C.c_int, [_P, _P, _I64]),
             "ref_split_act16": (C.c_int, [_P, _P, _I64]),
@@ -277,6 +275,9 @@ def ref():
             "ref_select_matmul": (C.c_int, [_I64, _I64, _I64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                             C.c_int, C.c_int, C.c_uint32, C.POINTER(C.c_int)]),
             "ref_expand_x86": (C.c_int, [C.c_int, _P, _P, _I64]),
+            "ref_bench_decode_sx": (_I64, [C.c_int, C.POINTER(_P), C.c_int, _I64, _I64, _P, C.c_int, _I64, _P,
+                                           C.c_int, C.c_int, C.c_int]),
+            "ref_llc_bytes": (_I64, []),
             "ref_expand_gemm": (C.c_int, [C.c_int, _P, _I64, _I64, _P, _I64, _I64, _P]),
         }
         for name, (res, args) in sig.items():

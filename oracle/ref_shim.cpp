@@ -13,19 +13,22 @@
 //   dynacore/cpu/generic/kernels_generic.cpp:67-150         vec_dot_* (fp32 activations)
 //   dynacore/include/dynacore/base/fast_exp.h:16-35         exp_nonpos (SiLU)
 //   dynacore/src/kernel/matmul_registry.cpp:287-429         select_matmul (kernel choice)
+//   dynacore/cpu/avx2/kernels_avx2.cpp:146-230,370-466      gemm_panel, dequant_* (fp32 expand + GEMM)
+//   dynacore/src/execution/thread_pool.cpp                  ThreadPool (the timed decode call)
 // Used to pin the C oracle (tests) and, on the GPU box, as the timed CPU
 // baseline ("reference" kind) of bench.py.
 
 #include <algorithm>
-#include <atomic>
 #include <chrono>
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
-#include <thread>
+#include <string>
 #include <vector>
 
 #include "dynacore/base/fast_exp.h"
 #include "dynacore/cpu/cpu_kernels.h"
+#include "dynacore/execution/thread_pool.h"
 #include "dynacore/hardware/cpu_info.h"
 #include "dynacore/kernel/kernel_plan.h"
 #include "dynacore/kernel/matmul_registry.h"
@@ -230,43 +233,71 @@ int ref_dot_rows_n(int kind, int dtype, const void* w, int64_t w_row_bytes, int6
   return 0;
 }
 
-// Timed CPU baseline: `threads` std::threads split the N weight rows into
-// 16-row units (as CpuDevice's decode partition, dynacore/cpu/cpu_device.cpp:925-934),
-// each running the AVX2 multi-row kernel of `kind` over its rows; the weight
-// copies in `w_copies` are visited in rotation so successive calls read cold
-// memory (dynalm/benchmarks/bench_decode_matmul.cpp:11-14). Runs `iters` calls
-// after one warm-up call and returns the total nanoseconds of the timed calls.
-int64_t ref_bench_gemv(int kind, int dtype, const void* const* w_copies, int ncopies, int64_t w_row_bytes, int64_t n,
-                       const void* acts, int64_t act_row_bytes, int m, int64_t k, float* y, int threads, int iters) {
-  if (!valid_type(dtype) || m < 1 || m > kDotRowsNMax || ncopies < 1 || threads < 1 || iters < 1) return -1;
+// CpuDevice::matmul's decode call for the sub-scaled int8 class (kInt8Subscaled,
+// dynacore/cpu/cpu_device.cpp:941-960) timed as the reference runs it: one
+// ThreadPool of `threads` (the calling thread included) created before the timed
+// calls and reused by all of them (src/execution/thread_pool.cpp:31-45); each call
+// quantizes the m fp32 rows with quantize_act_sx, then parallel_for over the n weight
+// rows with grain_for(n, threads, 4, chunks_per_thread) (cpu_device.cpp:101-103),
+// each chunk one dot_q8_sx_rows_n call (int8_rows' dot_n branch, :410-420). The
+// weight copies in `w_copies` are visited in rotation. Runs `iters` calls after one
+// warm-up call and returns the nanoseconds of the timed calls.
+int64_t ref_bench_decode_sx(int dtype, const void* const* w_copies, int ncopies, int64_t w_row_bytes, int64_t n,
+                            const float* x, int m, int64_t k, float* y, int threads, int chunks_per_thread, int iters) {
+  if ((dtype != 14 && dtype != 16) || m < 1 || m > kDotRowsNMax || ncopies < 1 || threads < 1 || iters < 1 ||
+      k % 256 != 0 || chunks_per_thread < 1) {
+    return -1;
+  }
   const CpuKernels& t = avx2_table();
-  const size_t ti = static_cast<size_t>(dtype);
-  DotQ8RowsNFn fn = kind == 1 ? t.dot_q8_rows_n[ti] : kind == 3 ? t.dot_q8_sx_rows_n[ti] : nullptr;
-  if (!fn) return -2;
-  const auto p = row_ptrs(acts, act_row_bytes, m);
-  const int64_t units = (n + 15) / 16;
-  auto run = [&](const void* w) {
-    std::atomic<int64_t> next{0};
-    auto worker = [&] {
-      std::vector<float*> yp(static_cast<size_t>(m));
-      for (;;) {
-        const int64_t u = next.fetch_add(4);
-        if (u >= units) break;
-        const int64_t n0 = u * 16, n1 = std::min(n, (u + 4) * 16);
-        for (int r = 0; r < m; ++r) yp[static_cast<size_t>(r)] = y + r * n + n0;
-        fn(w, w_row_bytes, n0, n1, p.data(), m, k, yp.data(), nullptr);
+  DotQ8RowsNFn fn = t.dot_q8_sx_rows_n[static_cast<size_t>(dtype)];
+  if (!fn || !t.quantize_act_sx) return -2;
+  const int64_t nb = k / kActQ8Block;
+  std::vector<ActBlockQ8> act(static_cast<size_t>(m * nb));
+  ThreadPool pool(threads);
+  const size_t grain = std::max<size_t>(4, static_cast<size_t>(n) / (static_cast<size_t>(pool.size()) *
+                                                                     static_cast<size_t>(chunks_per_thread)));
+  auto call = [&](const void* w) {
+    for (int r = 0; r < m; ++r) t.quantize_act_sx(x + r * k, act.data() + r * nb, k);
+    pool.parallel_for(static_cast<size_t>(n), grain, [&](size_t begin, size_t end) {
+      const ActBlockQ8* xn[kDotRowsNMax];
+      float* yr[kDotRowsNMax];
+      for (int r = 0; r < m; ++r) {
+        xn[r] = act.data() + r * nb;
+        yr[r] = y + r * n + static_cast<int64_t>(begin);
       }
-    };
-    std::vector<std::thread> pool;
-    for (int i = 1; i < threads; ++i) pool.emplace_back(worker);
-    worker();
-    for (auto& th : pool) th.join();
+      fn(w, w_row_bytes, static_cast<int64_t>(begin), static_cast<int64_t>(end), xn, m, k, yr, nullptr);
+    });
   };
-  run(w_copies[0]);
+  call(w_copies[0]);
   const auto t0 = std::chrono::steady_clock::now();
-  for (int it = 0; it < iters; ++it) run(w_copies[(it + 1) % ncopies]);
+  for (int it = 0; it < iters; ++it) call(w_copies[(it + 1) % ncopies]);
   const auto t1 = std::chrono::steady_clock::now();
   return std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
+}
+
+// The host's last-level cache in bytes (sysfs, the largest unified or data cache of
+// cpu0), or 0 when sysfs does not say.
+int64_t ref_llc_bytes(void) {
+  int64_t best = 0;
+  for (int i = 0; i < 16; ++i) {
+    const std::string dir = "/sys/devices/system/cpu/cpu0/cache/index" + std::to_string(i) + "/";
+    FILE* ft = std::fopen((dir + "type").c_str(), "r");
+    if (ft == nullptr) break;
+    char type[32] = {0};
+    const int got = std::fscanf(ft, "%31s", type);
+    std::fclose(ft);
+    if (got != 1 || std::string(type) == "Instruction") continue;
+    FILE* fs = std::fopen((dir + "size").c_str(), "r");
+    if (fs == nullptr) continue;
+    long long v = 0;
+    char unit = 0;
+    const int gs = std::fscanf(fs, "%lld%c", &v, &unit);
+    std::fclose(fs);
+    if (gs < 1) continue;
+    const int64_t bytes = unit == 'K' ? v << 10 : unit == 'M' ? v << 20 : unit == 'G' ? v << 30 : v;
+    best = std::max(best, bytes);
+  }
+  return best;
 }
 
 // e^x for x <= 0 (dynacore/include/dynacore/base/fast_exp.h:16-35), the exp of the

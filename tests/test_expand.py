@@ -117,3 +117,36 @@ def test_reference_expand_gemm_is_within_the_class_bound(ev, rv, t):
     rw, gx = ev[f"rw_{name}"], ev[f"gx_{name}"]
     exact, mag = _exact(t, rw, gx, gx.shape[1])
     assert np.all(np.abs(ev[f"expgemm_rw_{name}"] - exact) <= 1e-6 * mag)
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (needs the reference sources)")
+def test_cpu_baseline_call_computes_the_decode_step():
+    """bench.py's CPU baseline (ref_bench_decode_sx: quantize_act_sx + the sub-scaled row
+    kernel on the reference's ThreadPool) writes the decode step's outputs, on 1 and 3
+    threads: bit-equal to the same reference kernel called once over all rows (so the
+    pool's partition covers every row once), and within the sub-scaled class's fp32
+    reordering bound of the oracle."""
+    import ctypes as C
+
+    r = O.ref()
+    if not r.ref_has_avx2():
+        pytest.skip("no AVX2 on this host")
+    k, n = 1024, 200
+    rng = np.random.default_rng(77)
+    rows = rng.integers(0, 256, (n, k // 256, 144), dtype=np.uint8)
+    rows[:, :, 0:4] = rng.uniform(0.002, 0.02, (n, k // 256, 2)).astype(np.float16).view(np.uint8).reshape(n, -1, 4)
+    rows = np.ascontiguousarray(rows.reshape(n, -1))
+    x = O.normal(78, k)
+    a = O.ref_quantize("sx", x)
+    whole = np.empty(n, np.float32)
+    assert r.ref_dot_rows_n(3, O.Q4_K, rows.ctypes.data, rows.shape[1], 0, n, a.ctypes.data, a.size, 1, k,
+                            whole.ctypes.data, n, None) == 0
+    oracle = O.matmul(O.Q4_K, O.ACT_SX, rows, a.reshape(1, -1), k)[0]
+    ptrs = (C.c_void_p * 1)(rows.ctypes.data)
+    for threads in (1, 3):
+        y = np.full(n, np.nan, np.float32)
+        assert r.ref_bench_decode_sx(O.Q4_K, ptrs, 1, rows.shape[1], n, x.ctypes.data, 1, k, y.ctypes.data, threads,
+                                     32, 1) > 0
+        assert np.array_equal(y.view(np.uint32), whole.view(np.uint32))
+        assert np.max(np.abs(y - oracle)) <= 1e-5 * np.abs(oracle).max()
+    assert r.ref_llc_bytes() >= 0
