@@ -10,12 +10,9 @@
 #pragma once
 
 #include "dq_device.h"
+#include "dq_internal.h"
 
 namespace dq {
-
-enum { kActSilu = 0, kActGelu = 1, kActGeluTanh = 2 };
-
-__host__ __device__ inline bool act_ok(int act) { return act == kActSilu || act == kActGelu || act == kActGeluTanh; }
 
 // e^x for x <= 0 (dynacore/include/dynacore/base/fast_exp.h:16-35): comparison
 // clamp to [-87, 88] (NaN goes to -87), n = round(x / ln 2) by the 1.5 * 2^23

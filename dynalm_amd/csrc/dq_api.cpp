@@ -17,7 +17,6 @@
 #include <vector>
 
 #include "../../include/dynaq.h"
-#include "dq_act.h"
 #include "dq_internal.h"
 
 namespace {
@@ -186,11 +185,14 @@ int upload_impl(int dtype, const void* rows, bool host, int64_t n, int64_t k, in
   }
   if (e == hipSuccess) e = dq::launch_repack(dtype, src, row_bytes, n, d.nblk, d.plane, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
-  if (staging != nullptr) hipFree(staging);
+  if (staging != nullptr) {
+    const hipError_t ef = hipFree(staging);
+    if (e == hipSuccess) e = ef;
+  }
   if (e != hipSuccess) {
     rc = hip_fail(e, "weight upload");
     for (int p = 0; p < dq::kMaxPlanes; ++p)
-      if (d.plane[p]) hipFree(d.plane[p]);
+      if (d.plane[p]) (void)hipFree(d.plane[p]);  // already failing: the first error is reported
     delete w;
     return rc;
   }
@@ -474,17 +476,23 @@ int dq_weight_download(const dq_weight* w, void* host_rows, int64_t row_bytes, v
   }
   if (e == hipSuccess) e = hipMemcpyAsync(host_rows, staging, (size_t)(d.n * row_bytes), hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
-  hipFree(staging);
+  const hipError_t ef = hipFree(staging);
+  if (e == hipSuccess) e = ef;
   if (e != hipSuccess) return hip_fail(e, "weight download");
   return DQ_OK;
 }
 
 int dq_weight_free(dq_weight* w) {
   if (w == nullptr) return DQ_OK;
+  hipError_t e = hipSuccess;  // every plane is released; the first failure is reported
   for (int p = 0; p < dq::kMaxPlanes; ++p) {
-    if (w->dev.plane[p] != nullptr) hipFree(w->dev.plane[p]);
+    if (w->dev.plane[p] != nullptr) {
+      const hipError_t ef = hipFree(w->dev.plane[p]);
+      if (e == hipSuccess) e = ef;
+    }
   }
   delete w;
+  if (e != hipSuccess) return hip_fail(e, "weight free");
   return DQ_OK;
 }
 

@@ -143,6 +143,11 @@ struct Region {
   size_t bytes = 0;
 };
 
+// The activations of the gated projection (dynacore Activation, device/ops.h:14);
+// their device code is in dq_act.h.
+enum { kActSilu = 0, kActGelu = 1, kActGeluTanh = 2 };
+inline bool act_ok(int act) { return act == kActSilu || act == kActGelu || act == kActGeluTanh; }
+
 }  // namespace dq
 
 // The library's weight handle (include/dynaq.h).
