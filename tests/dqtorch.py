@@ -1,4 +1,4 @@
-"""Torch-tensor conveniences over the C ABI (device memory and streams only).
+"""Test conveniences: torch tensors in and out of the C ABI's ctypes wrappers.
 
 PyTorch supplies device buffers and the current HIP stream; every computation
 runs in libdynaq.so's kernels.

@@ -48,7 +48,7 @@ def _torch():
 def _dq_matmul(t, rows, k, x, bias, plan=None):
     """dq_matmul_plan on device copies of the same rows (the path run() wraps)."""
     torch = _torch()
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     w = dq.Weight.upload(t, rows, k)
     if x.strides[0] != 4 * k:
@@ -165,7 +165,7 @@ def test_set_plan_selects_the_contract(cuda):
     activations; the all-integer plan reproduces dq_matmul (the super-block class)
     bit for bit; NULL restores the defaults (sub-scaled)."""
     torch = _torch()
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n, m = 1536, 256, 4
     rows = gguf_weights(O.Q6_K, n, k, 2000, outlier_frac=0.01)

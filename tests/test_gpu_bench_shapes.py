@@ -47,7 +47,7 @@ def test_gemm_q4k_bench_shape(cuda, m):
     the third super-block on), one round of 224 workgroups at M=512 and 3.5 rounds at
     M=2048. dq_gemm == dq_gemv bit for bit on every output; 128 sampled columns ==
     the oracle bit for bit; dq_matmul (quantize + GEMM) == quantize then dq_gemm."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 4096, 14336
     w_rows = weight_rows(O.Q4_K, n, k, 4000 + m, edge=True)
@@ -72,7 +72,7 @@ def test_gemm_q6k_many_superblocks(cuda, m, n, k):
     """The Q6_K large GEMM over several super-blocks: <4, 2, 4> at N=14336 (4 super-blocks)
     and <2, 2, 2> at the FFN-down shape the bench times (K=14336, N=4096: 56 super-blocks).
     Bit-identical to the GEMV on every output and to the oracle on sampled columns."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     w_rows = weight_rows(O.Q6_K, n, k, 4100 + k, edge=True)
     x = activations(m, k, 4101 + k)
@@ -92,7 +92,7 @@ def test_gated_skinny_config5_shape(cuda):
     super-blocks (12 counting gate and up) on 256 CUs select the 4-wave gated skinny launch
     after one quantize launch. Every output against the oracle's act(g) * u (SiLU: bit-exact),
     and bit-identical to act_mul over two dq_matmul calls."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     n, k, m = 8960, 1536, 16
     rg = gguf_weights(O.Q4_K, n, k, 4200)
@@ -119,7 +119,7 @@ def test_fused_decode_long_rows(cuda, t, n, m):
     M = 1 run the early-activation GEMV (3-4 super-blocks per wave). Bit-identical to the
     standalone quantizer followed by dq_gemv; sampled rows against the oracle (bit-exact for
     Q8_K, within the fp32 bar for per-32)."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k = 14336
     w_rows = gguf_weights(t, n, k, 4300 + t + n)
@@ -147,7 +147,7 @@ def test_row_range_matches_full_call(cuda, t, fmt, k):
     """qmm.h:35-36: the caller partitions [n0, n1) and a row's result does not depend on the
     partition. N = 4096 is 64 row groups (the full call splits K); the halves and a ragged
     range have fewer groups, yet each row's bits equal the full call's."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     n, m = 4096, 3
     w_rows = gguf_weights(t, n, k, 4400 + t + k)

@@ -40,7 +40,7 @@ def host(t):
 
 def run(w, xd, bias=None):
     """dq_matmul_plan with the default plan on the rows of xd (a 2-D device view)."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     m = xd.shape[0]
     y = torch.empty((m, w.n), device="cuda")

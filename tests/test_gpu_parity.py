@@ -32,7 +32,7 @@ def host(t) -> np.ndarray:
 
 
 def quant_gpu(fmt, x: np.ndarray, stride_pad: int = 0) -> np.ndarray:
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     m, k = x.shape
     xp = np.zeros((m, k + stride_pad), np.float32)
@@ -99,7 +99,7 @@ def test_upload_round_trip(cuda, t, n):
 
 @pytest.mark.parametrize("pair", PAIRS, ids=pair_id)
 def test_integer_partials_bit_exact(cuda, pair):
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     t, fmt = pair
     k, n, m = 1024, 24, 3
@@ -122,7 +122,7 @@ def test_integer_partials_bit_exact(cuda, pair):
 def test_gemv_parity(cuda, pair, m):
     """BASELINE-distribution inputs (N(0, 0.02) weights with 1% outliers at 8 sigma,
     N(0, 1) activations): the north-star bar, 1e-4 relative / 1e-5 absolute."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     t, fmt = pair
     k, n = 2048, 72
@@ -147,7 +147,7 @@ def test_gemv_stress(cuda, pair, m):
     oracle's own generic order misses the exact value by more): the bar is the reference's,
     |y - y_exact| <= 1e-5 * sum |w_i x_i| (test_int_kernels.cpp:131-147), and Q8_K pairs stay
     bit-identical to the oracle."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     t, fmt = pair
     k, n = 2048, 72
@@ -167,7 +167,7 @@ def test_gemv_stress(cuda, pair, m):
 @pytest.mark.parametrize("pair", [(O.Q4_K, O.ACT_Q8_K), (O.Q8_0, O.ACT_PER32)], ids=pair_id)
 def test_gemv_row_range(cuda, pair):
     """Rows [n0, n1) only: untouched outside, identical inside (qmm.h:35-36 ranges)."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     t, fmt = pair
     k, n = 1024, 50
@@ -187,7 +187,7 @@ def test_gemv_row_range(cuda, pair):
 
 @pytest.mark.parametrize("m", [1, 64, 300])
 def test_gemm_q4k_parity(cuda, m):
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 1024, 136
     w_rows = weight_rows(O.Q4_K, n, k, 40 + m, edge=True)
@@ -202,7 +202,7 @@ def test_gemm_q4k_parity(cuda, m):
 
 
 def test_gemm_row_range_and_tails(cuda):
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n, m = 512, 203, 257
     w_rows = weight_rows(O.Q4_K, n, k, 5)
@@ -231,7 +231,7 @@ def test_gemm_big_tile(cuda, m, n0, n1):
     output bit-identical to the skinny / M=1 GEMV path on the same Q8_K rows, sampled
     rows bit-identical to the oracle; a partial second activation tile (m=300) and a
     row range that cuts both end tiles."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 512, 14336
     w_rows = weight_rows(O.Q4_K, n, k, 77 + m, edge=True)
@@ -255,7 +255,7 @@ def test_gemm_extreme_codes(cuda):
     16-value group of -128 codes (a valid ggml Q8_K code, bsum -2048: exact in fp16),
     saturated 6-bit scales and mins. S and the mins term reach their largest
     magnitudes; outputs stay bit-identical to the oracle and the GEMV."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 512, 14336
     w_rows = weight_rows(O.Q4_K, n, k, 91, edge=True)
@@ -283,7 +283,7 @@ def test_gemm_extreme_codes(cuda):
 @pytest.mark.parametrize("m", [1, 7, 40])
 def test_matmul_end_to_end(cuda, t, m):
     """Device::matmul semantics: fp32 x in, fp32 y out, quantization on the GPU."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 1024, 64
     w_rows = gguf_weights(t, n, k, 60 + t, outlier_frac=0.01)
@@ -301,7 +301,7 @@ def test_matmul_end_to_end(cuda, t, m):
 def test_fused_decode_equals_quantize_then_gemv(cuda, t, m):
     """dq_matmul's decode path quantizes inside the GEMV: bit-identical to the
     standalone quantizer followed by dq_gemv on the same rows."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 2048, 130
     w_rows = gguf_weights(t, n, k, 70 + t)
@@ -319,7 +319,7 @@ def test_fused_decode_equals_quantize_then_gemv(cuda, t, m):
 def test_q4k_full_size_decode_and_prefill(cuda):
     """Config 3/4 shape (K=4096, N=14336): sampled rows against the oracle, and the
     GEMV and the MFMA GEMM bit-identical on the same inputs at full size."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 4096, 14336
     w_rows = gguf_weights(O.Q4_K, n, k, 2024, outlier_frac=0.01)
@@ -338,7 +338,7 @@ def test_q4k_full_size_decode_and_prefill(cuda):
 
 def test_q6k_full_size_down(cuda):
     """Config 3's down projection (Q6_K, K=14336, N=4096): sampled rows."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 14336, 4096
     w_rows = gguf_weights(O.Q6_K, n, k, 77, outlier_frac=0.01)
@@ -354,7 +354,7 @@ def test_q4k_full_size_properties(cuda):
     """Size-independent checks at config 3's full gate shape: the device copy unpacks to
     the uploaded bytes; each row of an M=4 pass equals its own M=1 call; two row-range
     calls reproduce the full call; the fused decode path equals quantize + GEMV."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 4096, 14336
     w_rows = weight_rows(O.Q4_K, n, k, 31)
@@ -376,7 +376,7 @@ def test_q4k_full_size_properties(cuda):
 def test_config1_q8_0_gemv_4096(cuda):
     """Config 1: Q8_0 4096x4096 weights from N(0, 0.02) (GGUF Q8_0 quantizer), one
     N(0, 1) row, both activation contracts (dynacore per-32 and GGUF Q8_0)."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k = n = 4096
     w_rows = gguf_weights(O.Q8_0, n, k, 101)
@@ -396,7 +396,7 @@ def test_config1_q8_0_gemv_4096(cuda):
 def test_config2_q4_0_gate_shape(cuda, m):
     """Config 2: Q4_0 at K=4096, N=14336, M in {1, 4, 8}; sampled rows against the
     oracle, through dq_matmul (per-32 activations quantized in the kernel)."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 4096, 14336
     w_rows = gguf_weights(O.Q4_0, n, k, 200 + m)
@@ -419,7 +419,7 @@ QWEN_SHAPES = [  # (name, dtype, n, k) of one Qwen2.5-1.5B layer and the lm_head
 def test_config5_qwen_layer_m16(cuda, shape):
     """Config 5: the decode-step matmuls of a Qwen2.5-1.5B layer at M=16 through
     dq_matmul (Q8_K activations, GEMV passes): bit-identical to the oracle."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     _, t, n, k = shape
     w_rows = gguf_weights(t, n, k, 300 + n + k)
@@ -432,7 +432,7 @@ def test_config5_qwen_layer_m16(cuda, shape):
 
 def test_config5_lm_head_m16(cuda):
     """Config 5's lm_head: Q6_K 151936 x 1536 at M=16; sampled rows bit-identical."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 1536, 151936
     w_rows = weight_rows(O.Q6_K, n, k, 400)
@@ -470,7 +470,7 @@ def test_matmul_many_groups_equal_single_matmuls(cuda):
     Q/K/V-style jobs sharing one x (Q4_K, Q4_K, Q6_K; one with bias), a gate/up pair
     on another x with another k, and jobs that take other paths (m = 1, m = 40) in one
     call: every y bit-identical to its own dq_matmul and to the oracle."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     m, k1, k2 = 16, 1536, 512
     x1, x2 = activations(m, k1, 80), activations(m, k2, 81)
@@ -515,7 +515,7 @@ def test_skinny_activation_tiles_and_passes(cuda, t, m):
     tiles (rows past m read zeros); more rows run passes of 64 (a last single row on
     the M = 1 GEMV): dq_gemv on pre-quantized rows and dq_matmul (Q6_K at any m,
     Q4_K up to 64 rows) bit-identical to the oracle."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 1280, 80
     w_rows = gguf_weights(t, n, k, 120 + m, outlier_frac=0.01)
@@ -540,7 +540,7 @@ def test_skinny_long_rows_bit_exact(cuda, t, m, n, k):
     projection's shape: 96 tiles of 35 super-blocks; 3 tiles of 56): bit-identical to
     the oracle, with a bias, and with an output row range that leaves the other rows
     untouched."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     seed = 1300 + m + t
     w_rows = gguf_weights(t, n, k, seed, outlier_frac=0.01)
@@ -597,7 +597,7 @@ def _act_inputs(m: int, n: int, seed: int) -> tuple[np.ndarray, np.ndarray]:
 @pytest.mark.parametrize("m,n,pad", [(1, 4096, 0), (5, 1000, 0), (7, 1024, 12), (300, 96, 4)])
 def test_act_mul_parity(cuda, act, m, n, pad):
     """Device::act_mul (dynacore/cpu/cpu_device.cpp:1912-1930): vector and scalar paths, strided rows."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     g, u = _act_inputs(m, n, 10 * m + n)
     gd = torch.zeros((m, n + pad), device="cuda")
@@ -627,7 +627,7 @@ def test_matmul_gated_parity(cuda, act, t, m):
     """Device::matmul_gated (dynacore/include/dynacore/device/device.h:188-199): the fused M = 1 GEMV
     (m = 1), the fused skinny kernel (m <= 16) and the unfused sequence (m > 16) against the oracle's
     act(x . Wg^T) * (x . Wu^T); and bit-identical to act_mul over two dq_matmul calls on the GPU."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     n, k = 200, 1280
     rg, ru, wg, wu = _gated_case(t, t, n, k, 300 + m)
@@ -646,7 +646,7 @@ def test_matmul_gated_parity(cuda, act, t, m):
 def test_matmul_gated_mixed_types_and_scratch(cuda, m):
     """Gate and up of different types (Q4_K / Q6_K: the unfused sequence), strided x and out, and
     caller-given scratch of a wider stride; Q8_0 weights (per-32 activations) as well."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     n, k = 136, 768
     rg, ru, wg, wu = _gated_case(O.Q4_K, O.Q6_K, n, k, 400 + m)
@@ -675,7 +675,7 @@ def test_matmul_gated_mixed_types_and_scratch(cuda, m):
 def test_matmul_gated_full_size_m1(cuda):
     """BASELINE's shape as a gate / up pair (Q4_K, K = 4096, N = 14336, M = 1): bit-identical to
     act_mul over the two single matmuls, and to the oracle on sampled rows."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     n, k = 14336, 4096
     rg, ru, wg, wu = _gated_case(O.Q4_K, O.Q4_K, n, k, 500)
@@ -692,7 +692,7 @@ def test_matmul_gated_full_size_m1(cuda):
 
 
 def test_matmul_gated_rejects(cuda):
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k = 512
     wg = dq.Weight.upload(O.Q4_K, gguf_weights(O.Q4_K, 64, k, 5), k)
@@ -714,7 +714,7 @@ def test_matmul_gated_rejects(cuda):
 def test_gguf_upload_round_trip(cuda, tmp_path):
     """Weights uploaded from a GGUF file (one file and a 3-part split model) download back to the
     file's bytes, and multiply bit-identically to the same rows uploaded from memory."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
     from gguf_writer import GGML_Q4_0, GGML_Q4_K, GGML_Q6_K, GGML_Q8_0, GgufWriter, split_names
 
     specs = {"q4k": (GGML_Q4_K, O.Q4_K, 96, 512), "q6k": (GGML_Q6_K, O.Q6_K, 64, 768),
@@ -778,7 +778,7 @@ def test_quantize_sx_matches_reference_golden(cuda):
 @pytest.mark.parametrize("m", [1, 3, 8, 11])
 def test_gemv_sx_parity(cuda, t, m):
     """Sub-scaled GEMV: bit-identical to the oracle's canonical order; integer unit partials exact."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 1280, 200
     rows = gguf_weights(t, n, k, 1200 + m, outlier_frac=0.01)
@@ -800,7 +800,7 @@ def test_gemv_sx_parity(cuda, t, m):
 def test_gemv_sx_vs_reference_avx2(cuda, t):
     """Against the reference's own sub-scaled AVX2 kernel (golden sxdot_*, the contract dynacore runs
     by default on x86): fp32 reorderings only."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     gold = _gold()
     name = O.TYPE_NAMES[t]
@@ -812,7 +812,7 @@ def test_gemv_sx_vs_reference_avx2(cuda, t):
 
 def test_gemv_sx_s_beyond_int32(cuda):
     """Constant inputs and extreme Q4_K weights push S = sum sc m P past 2^31; the GPU keeps it exact."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k = 512
     blk = np.zeros(144, np.uint8)
@@ -873,7 +873,7 @@ Q16_TYPES = [O.Q8_0, O.Q4_K, O.Q6_K]
 def test_gemv_q16_parity(cuda, t, m):
     """int16 GEMV: within the reference's bound of the exact product and of the oracle;
     integer unit partials bit-exact; dq_matmul_act (GPU quantization) gives the same bits."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 1280, 200
     rows = weight_rows(t, n, k, 1400 + m, edge=True)
@@ -932,7 +932,7 @@ def _q16_exact_case(t: int, n: int, k: int, seed: int) -> tuple[np.ndarray, np.n
 
 @pytest.mark.parametrize("t", Q16_TYPES, ids=lambda t: O.TYPE_NAMES[t])
 def test_gemv_q16_exact_integers(cuda, t):
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 256, 256
     rows, a = _q16_exact_case(t, n, k, 1500 + t)
@@ -948,7 +948,7 @@ def test_gemv_q16_exact_integers(cuda, t):
 @pytest.mark.parametrize("t", Q16_TYPES, ids=lambda t: O.TYPE_NAMES[t])
 def test_gemv_q16_vs_reference_avx2(cuda, t):
     """Against the reference's AVX2 dot_rows16_* (golden q16dot_*): fp32 order only."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     gold = _gold()
     name = O.TYPE_NAMES[t]
@@ -964,7 +964,7 @@ def test_gemv_q16_vs_reference_avx2(cuda, t):
 def test_gemv_q16_ffn_down_size(cuda, t):
     """The int16 contract's matmul: the FFN down projection, K = 14336 (config 4's
     intermediate size), 5 rows (a 4-row pass and a 1-row pass), 320 sampled outputs."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 14336, 320
     rows = gguf_weights(t, n, k, 1600 + t, outlier_frac=0.01)
@@ -994,7 +994,7 @@ def test_gemv_f32_parity(cuda, t, m):
     added per wave slice and slices in order, so only the cross-slice additions differ
     from the oracle's (the reference generic order): within 2e-6 of the sum of |terms| of
     the oracle and 1e-5 of the exact product; dq_act_quantize copies the rows."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 1280, 200
     rows = weight_rows(t, n, k, 1950 + m, edge=True)
@@ -1019,7 +1019,7 @@ def test_gemv_f32_parity(cuda, t, m):
 @pytest.mark.parametrize("t", list(O.TYPE_NAMES)[:4], ids=lambda t: O.TYPE_NAMES[t])
 def test_gemv_f32_vs_reference_golden(cuda, t):
     """Against the reference's own generic vec_dot outputs (golden vecdot_*)."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     gold = _gold()
     name = O.TYPE_NAMES[t]
@@ -1035,7 +1035,7 @@ def test_gemv_f32_vs_reference_golden(cuda, t):
 def test_gemv_f32_large_k_passes(cuda, t):
     """K = 14336 (the FFN down projection): the staged fp32 rows fill the LDS at 2 rows, so
     5 rows run in passes of 2, 2 and 1."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 14336, 256
     rows = gguf_weights(t, n, k, 1980 + t, outlier_frac=0.01)
@@ -1062,7 +1062,7 @@ def test_gemv_split_k(cuda, pair, m):
     workgroups and add the parts in split order in a second launch. Within 2e-6 of the
     sum of |terms| of the oracle; the same bits on a second run and on a row range
     (the same split)."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     t, fmt = pair
     k, n = (8192 if fmt in (O.ACT_PER32, O.ACT_Q8_0) else 4096), 256
@@ -1097,7 +1097,7 @@ def test_gemm_b32_bit_exact(cuda, t, m, n, k):
     every output (kernels_generic.cpp:216-239): bit-identical to the oracle, edge weight
     blocks and partial tiles (rows, weight rows and a 3-block K) included; through
     dq_matmul (quantize + GEMM from 32 rows, the GEMV below) with a bias."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     rows = weight_rows(t, n, k, 2100 + m + t, edge=True)
     x = activations(m, k, 2110 + m)
@@ -1118,7 +1118,7 @@ def test_gemm_b32_bit_exact(cuda, t, m, n, k):
 def test_gemm_b32_row_range_and_saturated_codes(cuda):
     """A row range (unaligned ends) leaves the other outputs untouched; +-127 activations
     against -128 / +127 Q8_0 codes (the largest block sums) stay exact."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n, m = 512, 192, 70
     rows = weight_rows(O.Q8_0, n, k, 2130, edge=True).reshape(n, -1, 34)
@@ -1144,7 +1144,7 @@ def test_gemm_q6k_bit_exact(cuda, m, n, k):
     operands 64 wh + wl, S = 64 sum(wh a) + sum(wl a) per super-block, combined in the
     canonical order u = d (float)S, acc = fma(da, u, acc): bit-identical to the oracle and
     to the GEMV (edge blocks: saturated and negative scales, d = 0)."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     rows = weight_rows(O.Q6_K, n, k, 2200 + m, edge=True)
     x = activations(m, k, 2210 + m)
@@ -1162,7 +1162,7 @@ def test_gemm_q6k_extreme_codes_and_route(cuda):
     """Saturated operands (codes 0 and 63, scales -128 and 127, activations +-127 and
     -128-free Q8_K rows) stay exact; dq_matmul sends 40 rows at K = 14336 (whose super-
     blocks do not fit the skinny kernel's LDS) to the GEMM, and 70 rows at any K."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n, m = 512, 192, 80
     rows = weight_rows(O.Q6_K, n, k, 2230, edge=True).reshape(n, -1, 210)

@@ -39,7 +39,7 @@ def within_terms(y, want, t, fmt, rows, x, k, rel=2e-6):
 
 
 def run_plan(w, plan, x, bias=None):
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     xd = dev(x) if isinstance(x, np.ndarray) else x
     y = torch.empty((xd.shape[0], w.n), device="cuda")
@@ -50,7 +50,7 @@ def run_plan(w, plan, x, bias=None):
 @pytest.mark.parametrize("t", TYPES, ids=lambda t: O.TYPE_NAMES[t])
 @pytest.mark.parametrize("m", [1, 3, 4, 5, 8, 9, 40])
 def test_default_plan(cuda, t, m):
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 1536, 200
     rows = gguf_weights(t, n, k, 2200 + t + m, outlier_frac=0.01)
@@ -79,7 +79,7 @@ def test_default_plan(cuda, t, m):
 @pytest.mark.parametrize("t", TYPES, ids=lambda t: O.TYPE_NAMES[t])
 @pytest.mark.parametrize("m", [1, 5, 40, 300])
 def test_all_int8_plan_is_dq_matmul(cuda, t, m):
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n = 1024, 256
     rows = gguf_weights(t, n, k, 2300 + t + m)
@@ -91,7 +91,7 @@ def test_all_int8_plan_is_dq_matmul(cuda, t, m):
 @pytest.mark.parametrize("t", [O.Q6_K, O.Q4_K, O.Q8_0], ids=lambda t: O.TYPE_NAMES[t])
 def test_ffn_down_plan_int16(cuda, t):
     """The down projection's plan: int16 activations up to 8 rows at K = 14336."""
-    from dynalm_amd import torch_ops as T
+    import dqtorch as T
 
     k, n, m = 14336, 256, 6
     rows = gguf_weights(t, n, k, 2400 + t)
