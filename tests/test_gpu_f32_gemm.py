@@ -141,3 +141,20 @@ def test_bench_shape(cuda):
     cols.sort()
     exact, mag = bound(O.Q4_K, rows[cols], x, k)
     assert np.all(np.abs(y[:, cols] - exact) <= REL * mag)
+
+
+@pytest.mark.parametrize("t", TYPES, ids=lambda t: O.TYPE_NAMES[t])
+def test_wide_tiles(cuda, t):
+    """A shape whose grid takes the 224-row weight tiles (M = 300, N = 14000: 189 tiles of
+    224 rows against 330 of 128), the last tile running past the weight's padded rows:
+    every output against the exact product, and the first 16 rows bit-equal alone."""
+    k = 256 if t in (O.Q4_K, O.Q6_K) else 96
+    n, m = 14000, 300
+    rows = gguf_weights(t, n, k, 3700 + t)
+    x = activations(m, k, 3701)
+    w = dq.Weight.upload(t, rows, k)
+    xd = dev(x)
+    y = run(w, xd)
+    exact, mag = bound(t, rows, x, k)
+    assert np.all(np.abs(y - exact) <= REL * mag + 1e-30)
+    assert np.array_equal(y[:16].view(np.uint32), run(w, xd[:16]).view(np.uint32))
