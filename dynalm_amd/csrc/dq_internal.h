@@ -76,6 +76,12 @@ hipError_t launch_units(const WeightDev& w, int af, const uint8_t* acts, int64_t
 hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
                        float* y, int64_t ys, const float* bias, hipStream_t s);
 bool gemm_supported(int dtype, int af);
+// The streamed Q4_K x Q8_K GEMM (dq_gemm_stream.hip): 128 x 256 tiles, 8 waves each
+// owning one 32-row weight tile, K in half super-blocks. gemm_stream_ok says whether
+// the shape fits its 32-bit buffer offsets.
+hipError_t launch_gemm_stream(const WeightDev& w, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
+                              float* y, int64_t ys, const float* bias, hipStream_t s);
+bool gemm_stream_ok(const WeightDev& w, int64_t m, int64_t n0, int64_t n1, int64_t arb);
 // The expand-class fp32 GEMM (dq_gemm_f32.hip): weight tiles expanded to fp32 in LDS
 // and contracted with the fp32 rows x (stride xs floats) on the matrix cores; any of
 // the four weight types. Below kF32GemmMinRows rows the fp32 GEMV passes are faster.
