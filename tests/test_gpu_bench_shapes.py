@@ -1,9 +1,9 @@
 """GPU parity at the exact shapes bench.py times, and on the launch variants only those
 shapes select.
 
-- The large GEMM kernels over many super-blocks: Q4_K K=4096 N=14336 at M=512 (the
-  256 x 128 tile, one round of workgroups) and M=2048 (3.5 rounds), Q6_K over 4 and
-  56 super-blocks. Every output bit-identical to the GEMV on the same Q8_K rows,
+- The large GEMM kernels over many super-blocks: Q4_K K=4096 N=14336 at M=512 and
+  M=2048 (the streamed 128 x 256 kernel: one round of 224 workgroups, and 3.5 rounds),
+  Q6_K over 4 and 56 super-blocks (the 256 x 128 tile). Every output bit-identical to the GEMV on the same Q8_K rows,
   sampled columns bit-identical to the oracle.
 - The 4-wave gated skinny launch at config 5's gate/up shape (Q4_K 8960 x 1536, M=16).
 - dq_matmul's fused decode path at K = 14336 (split-K for the per-32 formats, the
@@ -42,10 +42,9 @@ def bits(a: np.ndarray) -> np.ndarray:
 
 @pytest.mark.parametrize("m", [512, 2048])
 def test_gemm_q4k_bench_shape(cuda, m):
-    """Config 4 (K=4096, N=14336) at the bench's M: k_gemm_q4k_big<Q4_K, 4, 2, 4> over 16
-    super-blocks (the direct-to-LDS loads of super-block b + 1 into buffers just read, from
-    the third super-block on), one round of 224 workgroups at M=512 and 3.5 rounds at
-    M=2048. dq_gemm == dq_gemv bit for bit on every output; 128 sampled columns ==
+    """Config 4 (K=4096, N=14336) at the bench's M: k_gemm_q4k_stream over 16 super-blocks
+    (32 half-super-block positions through its ring of four LDS buffers), one round of
+    224 workgroups at M=512 and 3.5 rounds at M=2048. dq_gemm == dq_gemv bit for bit on every output; 128 sampled columns ==
     the oracle bit for bit; dq_matmul (quantize + GEMM) == quantize then dq_gemm."""
     import dqtorch as T
 
