@@ -619,7 +619,7 @@ def main() -> None:
             "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2),
             "pct_of_mfma_ceiling": round(100 * tops / mfma_ceiling, 2),
             "tokens_per_s": round(m / (ms_gemm * 1e-3), 1),
-            "roofline": {"kernel": "dq::k_gemm_q4k_big<4, 2, 4>", "bound": "mfma", "achieved": round(tops, 2),
+            "roofline": {"kernel": "dq::k_gemm_q4k_stream", "bound": "mfma", "achieved": round(tops, 2),
                          "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4),
                          "traffic": traffic.get("gemm_m512")},
         },
