@@ -30,4 +30,21 @@ DQ_DEV u32 sel_subblocks(int hi) { return hi ? 0x07050301u : 0x06040200u; }
 DQ_DEV u32 sel_u16x2(int s) { return 0x0C000C00u | ((u32)s << 16) | (u32)s; }
 DQ_DEV u32 sel_x4(int s) { return (u32)s * 0x01010101u; }
 
+// Q6_K: w = sc_u (q - 32) (|w| <= 4096) of four codes (bytes of q, 0..63) with the
+// unit scale sc (-128..127), split exactly into int8 operands w = 64 wh + wl with
+// wh = floor(w / 64) in -64..64 and wl in 0..63; 16-bit lane arithmetic, two codes per
+// operation.
+DQ_DEV void q6_split(u32 q, int sc, u32& H, u32& L) {
+  typedef short s2 __attribute__((ext_vector_type(2)));
+  const s2 e = __builtin_bit_cast(s2, __builtin_amdgcn_perm(0u, q, 0x0C010C00u));  // codes 0, 1
+  const s2 o = __builtin_bit_cast(s2, __builtin_amdgcn_perm(0u, q, 0x0C030C02u));  // codes 2, 3
+  const s2 k = {(short)sc, (short)sc}, c = {(short)(-32 * sc), (short)(-32 * sc)};
+  const s2 we = e * k + c, wo = o * k + c;
+  const s2 he = we >> (short)6, ho = wo >> (short)6;
+  const s2 m63 = {63, 63};
+  const s2 le = we & m63, lo = wo & m63;
+  H = __builtin_amdgcn_perm(__builtin_bit_cast(u32, ho), __builtin_bit_cast(u32, he), 0x06040200u);
+  L = __builtin_amdgcn_perm(__builtin_bit_cast(u32, lo), __builtin_bit_cast(u32, le), 0x06040200u);
+}
+
 }  // namespace dq

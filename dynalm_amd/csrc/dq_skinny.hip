@@ -16,10 +16,9 @@
 // (0..945) does not fit int8, so sc = 8 sh + sl and the B operands are sh*q and
 // sl*q (bytes <= 105, one packed 16-bit multiply per 4 nibbles); a third operand
 // holds m_j at every position of sub-block j, so its MFMA sum is exactly Mn.
-// Q6_K: in K-step s lane group g of B holds sub-block 4s + g; one MFMA per
-// sub-block with the A operand masked to that lane group gives P_u, and one with
-// sc_u at every position of sub-block u gives the -32 correction
-// (dequantize_q6_K layout, quant_formats.cpp:192-216).
+// Q6_K: in K-step s lane group g of B holds sub-block 4s + g (one scale), so the
+// effective weight w = sc_u (q - 32) splits exactly into int8 operands w = 64 wh + wl
+// and two MFMA chains give S (dequantize_q6_K layout, quant_formats.cpp:192-216).
 //
 // Workgroup: 4 or 8 waves over 16 * CT weight rows (CT MFMA column tiles) and all
 // super-blocks, wave w taking a contiguous slice of super-blocks. CT = 4 (a whole
@@ -250,42 +249,40 @@ DQ_DEV void tterms(const WSB<kQ4_K, CT>& w, int ct, const ActSB<MT>& A, int lg, 
 
 template <int CT, int MT>
 DQ_DEV void tterms(const WSB<kQ6_K, CT>& w, int ct, const ActSB<MT>& A, int lg, float t[MT][4]) {
-  const v4u zero = {0u, 0u, 0u, 0u};
-  v4i_t S[MT], C[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    S[mt] = v4i_t{0, 0, 0, 0};
-    C[mt] = v4i_t{0, 0, 0, 0};
-  }
+  // lane group g at K-step s holds sub-block u = 4s + g (one scale): w = sc_u (q - 32)
+  // split exactly into int8 operands w = 64 wh + wl (q6_split), two MFMA chains give
+  // S = 64 sum(wh a) + sum(wl a) = sum_u sc_u sum((q - 32) a), and t = d (float)S
+  v4i_t H[MT], L[MT];
+  const int sh = 2 * (lg >> 1);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    // codes of sub-block 4s + g: quarter 2(s&1) + g/2 of half s/2
+    // codes of sub-block 4s + g: the low (even s) or high nibbles of ql chunk g + 4(s>>1)
+    // with their top two bits from qh chunk 2(s>>1) + (g&1), bit pair g/2 (+2 for odd s)
     const v4u lo = (s >> 1) ? w.l1[ct] : w.l0[ct], hb = (s >> 1) ? w.h1[ct] : w.h0[ct];
-    const u32 qsh = 2u * (u32)(2 * (s & 1) + (lg >> 1));
+    const u32 qsh = (u32)(sh + 4 * (s & 1));
     const v4u q = ((lo >> (u32)(4 * (s & 1))) & 0x0F0F0F0Fu) | (((hb >> qsh) & 0x03030303u) << 4);
-    // scales of sub-blocks 4s .. 4s + 3 (signed bytes of scale dword s)
     const u32 sw = s == 0 ? w.sc[ct].x : s == 1 ? w.sc[ct].y : s == 2 ? w.sc[ct].z : w.sc[ct].w;
-    const u32 mine = (u32)sbfe(sw, 8 * lg, 8) & 0xFFu;  // this lane group's scale
-    const u32 sc4 = mine * 0x01010101u;
+    const int sc = sbfe(sw, 8 * lg, 8);
+    v4u bh, bl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u32 h, l;
+      q6_split(q[i], sc, h, l);
+      bh[i] = h;
+      bl[i] = l;
+    }
     const v4i_t z = {0, 0, 0, 0};
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      C[mt] = mfma(A.a[mt][s], v4u{sc4, sc4, sc4, sc4}, C[mt]);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const v4u au = lg == u ? A.a[mt][s] : zero;
-        const v4i_t P = mfma(au, q, z);
-        const int scu = sbfe(sw, 8 * u, 8);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) S[mt][e] += scu * __builtin_amdgcn_sbfe(P[e], 0, 24);
-      }
+      H[mt] = mfma(A.a[mt][s], bh, s == 0 ? z : H[mt]);
+      L[mt] = mfma(A.a[mt][s], bl, s == 0 ? z : L[mt]);
     }
   }
   const float d = h2f(w.dw[ct]);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) t[mt][e] = d * (float)(S[mt][e] - 32 * C[mt][e]);
+    for (int e = 0; e < 4; ++e) t[mt][e] = d * (float)((H[mt][e] << 6) + L[mt][e]);
 }
 
 template <int WT, int CT>
@@ -316,7 +313,7 @@ struct WRes<kQ6_K, CT> {
 // flight during the compute (activation loads of b are issued before the weight
 // loads of b + 1, so waiting for them does not wait for the prefetch: loads retire
 // in order).
-template <int WT, int CT, int MT, bool kFused>
+template <int WT, int CT, int MT, bool kFused, int D>
 DQ_DEV void skinny_wave(const SkinnyJob& J, const uint8_t* const* p, int nblk, int64_t G, int r0, bool ok, int b0,
                         int b1, float* tt, float* dal, int li, int lg) {
   constexpr int NC = 16 * CT, NR = 16 * MT;
@@ -350,7 +347,31 @@ DQ_DEV void skinny_wave(const SkinnyJob& J, const uint8_t* const* p, int nblk, i
     }
   };
   if (b0 >= b1) return;
-  if constexpr (CT == 1) {
+  if constexpr (CT == 1 && D > 1) {
+    static_assert(D % 2 == 0, "the activation double buffer alternates with the slot index");
+    // D super-blocks of weights in flight: slot i holds super-block b0 + i (mod D) and
+    // is refilled with b + D after b's t-terms. Each step issues the activations of
+    // b + 1 before it waits for b, and the refills come after: loads retire in order,
+    // so waiting for b's activations never waits for a refill.
+    WSB<WT, CT> w[D];
+#pragma unroll
+    for (int i = 0; i < D; ++i)
+      if (b0 + i < b1) res.load(w[i], b0 + i, r0, li, lg);
+    ActSB<MT> A[2];
+    act(b0, A[0]);
+#pragma unroll 1
+    for (int bb = b0; bb < b1; bb += D) {
+#pragma unroll
+      for (int i = 0; i < D; ++i) {
+        const int b = bb + i;
+        if (b < b1) {
+          if (b + 1 < b1) act(b + 1, A[(i + 1) & 1]);
+          emit(w[i], A[i & 1], b);
+          if (b + D < b1) res.load(w[i], b + D, r0, li, lg);
+        }
+      }
+    }
+  } else if constexpr (CT == 1) {
     WSB<WT, CT> cur;
     res.load(cur, b0, r0, li, lg);
     for (int b = b0; b < b1; ++b) {
@@ -376,8 +397,10 @@ DQ_DEV void skinny_wave(const SkinnyJob& J, const uint8_t* const* p, int nblk, i
   }
 }
 
-// W waves per workgroup (4 or 8; launch_group picks it from the launch's shape).
-template <int CT, int MT, bool kFused, bool kGated, int W>
+// W waves per workgroup (4 or 8; launch_group picks it from the launch's shape); D
+// super-blocks of weights in flight per wave (launch_group picks 4 for one round of
+// workgroups with several super-blocks per wave).
+template <int CT, int MT, bool kFused, bool kGated, int W, int D = 1>
 __global__ __launch_bounds__(W * 64) void k_skinny(SkinnyGroup g) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int NC = 16 * CT, NR = 16 * MT;
@@ -405,9 +428,9 @@ __global__ __launch_bounds__(W * 64) void k_skinny(SkinnyGroup g) {
   float* tw = half ? tu : tt;
   float* dw = dal + half * nblk * NR;
   if (J.dtype == kQ6_K) {
-    skinny_wave<kQ6_K, CT, MT, kFused>(J, planes, nblk, G, r0, ok, b0, b1, tw, dw, li, lg);
+    skinny_wave<kQ6_K, CT, MT, kFused, D>(J, planes, nblk, G, r0, ok, b0, b1, tw, dw, li, lg);
   } else {
-    skinny_wave<kQ4_K, CT, MT, kFused>(J, planes, nblk, G, r0, ok, b0, b1, tw, dw, li, lg);
+    skinny_wave<kQ4_K, CT, MT, kFused, D>(J, planes, nblk, G, r0, ok, b0, b1, tw, dw, li, lg);
   }
   __syncthreads();
   // the in-order chains of the tile's NR x NC outputs, shared by all waves
@@ -436,16 +459,16 @@ size_t skinny_lds(int64_t nblk, int ct, int mt, bool gated = false) {
 }
 constexpr size_t kSkinnyMaxLds = 160 * 1024;
 
-template <int CT, int MT, bool kFused, bool kGated = false, int W = kSkinnyWaves>
+template <int CT, int MT, bool kFused, bool kGated = false, int W = kSkinnyWaves, int D = 1>
 hipError_t skinny_launch(const SkinnyGroup& g, int wgs, hipStream_t s) {
   const size_t lds = skinny_lds(g.nblk, CT, MT, kGated);
   if (lds > kSkinnyMaxLds) return hipErrorInvalidValue;
   if (lds > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_skinny<CT, MT, kFused, kGated, W>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_skinny<CT, MT, kFused, kGated, W, D>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((k_skinny<CT, MT, kFused, kGated, W>), dim3((unsigned)wgs), dim3(W * 64), lds, s, g);
+  hipLaunchKernelGGL((k_skinny<CT, MT, kFused, kGated, W, D>), dim3((unsigned)wgs), dim3(W * 64), lds, s, g);
   return hipGetLastError();
 }
 
@@ -503,7 +526,12 @@ hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t*
   if (ct == 4) return fused ? skinny_launch<4, 1, true, false, 4>(g, (int)wgs, s)
                             : skinny_launch<4, 1, false, false, 4>(g, (int)wgs, s);
   if (fused) return skinny_launch<1, 1, true>(g, (int)wgs, s);
-  return four ? skinny_launch<1, 1, false, false, 4>(g, (int)wgs, s) : skinny_launch<1, 1, false>(g, (int)wgs, s);
+  if (four) return skinny_launch<1, 1, false, false, 4>(g, (int)wgs, s);
+  // One round of 8-wave workgroups with at least 3 super-blocks per wave (a long-K
+  // matmul such as an FFN down projection): the waves' dependent load steps, not the
+  // bytes, set the time, so 4 super-blocks of weights stay in flight per wave.
+  if (wgs <= cus && g.nblk >= 3 * kSkinnyWaves) return skinny_launch<1, 1, false, false, kSkinnyWaves, 4>(g, (int)wgs, s);
+  return skinny_launch<1, 1, false>(g, (int)wgs, s);
 }
 
 }  // namespace
