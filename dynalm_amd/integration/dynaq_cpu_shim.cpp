@@ -20,33 +20,9 @@
 
 #include "dynacore/cpu/cpu_device.h"
 #include "dynaq.h"
+#include "dynaq_convert.h"
 
 namespace dynaq_shim {
-
-// KernelPlan's matmul knobs (kernel_plan.h:34-148) as a dq_plan. MatmulKernelId bits
-// are dq_kernel bits, so matmul_disabled carries over.
-dq_plan to_dq_plan(const dynacore::KernelPlan& p) {
-  dq_plan q;
-  q.expand_min_rows = p.expand_min_rows;
-  q.int8_decode_max_rows = p.int8_decode_max_rows;
-  q.int16_decode_max_rows = p.int16_decode_max_rows;
-  q.int8_superblock_min_rows = p.int8_superblock_min_rows;
-  q.int8_superblock_max_rows = p.int8_superblock_max_rows;
-  q.int8_subscale_min_rows = p.int8_subscale_min_rows;
-  q.matmul_disabled = p.matmul_disabled;
-  return q;
-}
-
-// DType values are dq_dtype values for the four weight types.
-int dq_type(dynacore::DType t) {
-  switch (t) {
-    case dynacore::DType::kQ4_0: return DQ_Q4_0;
-    case dynacore::DType::kQ8_0: return DQ_Q8_0;
-    case dynacore::DType::kQ4_K: return DQ_Q4_K;
-    case dynacore::DType::kQ6_K: return DQ_Q6_K;
-    default: return -1;
-  }
-}
 
 // Registers GPU `gpu` as `dev`'s external matmul kernel for calls of at least min_rows
 // rows, keeping up to `limit` bytes of weight copies in HBM (0: all). Call before

@@ -30,3 +30,27 @@ def test_shim_compiles_against_reference_headers(tmp_path):
     for name in ("dq_external_create", "dq_external_set_plan", "dq_external_run", "dq_external_eligible"):
         assert f"U {name}" in syms, name
     assert "dynaq_shim::register_dynaq" in syms
+
+
+DEVICE = os.path.join(ROOT, "dynalm_amd", "integration", "dynaq_gpu_device.cpp")
+HIP_INC = "/opt/rocm/include"
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_INC) or shutil.which("g++") is None or not os.path.isdir(HIP_INC),
+                    reason="needs the reference's headers, g++ and the HIP headers")
+def test_gpu_device_compiles_against_reference_headers(tmp_path):
+    """dynaq_gpu_device.cpp: a dynacore::Device subclass (every pure virtual of device.h:70-219
+    overridden, or the class would be abstract and create() would not compile), against
+    device.h, tensor.h, storage.h and status.h with include/dynaq.h and the HIP runtime API."""
+    obj = tmp_path / "device.o"
+    cmd = ["g++", "-std=c++20", "-O1", "-Wall", "-Werror", "-c", DEVICE, "-o", str(obj), "-D__HIP_PLATFORM_AMD__",
+           "-DENGINE_HAS_AVX2=1", "-DENGINE_HAS_AVX512=0", "-DENGINE_HAS_AMX=0", "-DENGINE_HAS_NEON=0",
+           f"-I{REF_INC}", f"-I{os.path.join(ROOT, 'include')}", f"-I{HIP_INC}"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-3000:]
+    syms = subprocess.run(["nm", "-C", str(obj)], capture_output=True, text=True).stdout
+    for name in ("dq_weight_upload", "dq_weight_free", "dq_matmul_plan", "dq_matmul_many", "dq_matmul_gated",
+                 "dq_act_mul", "dq_select", "dq_plan_defaults"):
+        assert f"U {name}" in syms, name
+    assert "vtable for dynaq_shim::DynaqGpuDevice" in syms
+    assert "dynaq_shim::DynaqGpuDevice::create" in syms
