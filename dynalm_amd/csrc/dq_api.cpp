@@ -535,14 +535,15 @@ int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
   if (int rc = check_acts(w, fmt, acts, m); rc != DQ_OK) return rc;
   if (int rc = check_out(w, m, n0, n1, y, y_stride); rc != DQ_OK) return rc;
   if (m == 0 || n0 == n1) return DQ_OK;
-  if (m >= 2 && dq::gemv_mma_supported(w->dev.dtype, fmt, 2) &&
-      dq::gemv_mma_lds_ok(w->dev.nblk, m < dq::kSkinnyMaxRows ? m : dq::kSkinnyMaxRows)) {
-    // K-quants x Q8_K: the skinny MFMA GEMV in passes of up to 64 rows (a last
-    // single row goes to the M = 1 GEMV)
+  const int64_t pass = fmt == DQ_ACT_SX ? dq::kSkinnySxMaxRows : dq::kSkinnyMaxRows;
+  if (m >= 2 && dq::gemv_mma_supported(w->dev.dtype, fmt, 2) && dq::gemv_mma_lds_ok(w->dev.nblk, m < pass ? m : pass) &&
+      (fmt != DQ_ACT_SX || dq::skinny_sx_pays(w->dev, m < pass ? m : pass, n0, n1))) {
+    // K-quants x Q8_K / sub-scaled: the skinny MFMA GEMV in passes of up to 64 (16)
+    // rows (a last single row goes to the M = 1 GEMV)
     const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
     const uint8_t* a = static_cast<const uint8_t*>(acts);
-    for (int64_t r0 = 0; r0 < m; r0 += dq::kSkinnyMaxRows) {
-      const int64_t rows = m - r0 < dq::kSkinnyMaxRows ? m - r0 : dq::kSkinnyMaxRows;
+    for (int64_t r0 = 0; r0 < m; r0 += pass) {
+      const int64_t rows = m - r0 < pass ? m - r0 : pass;
       if (rows == 1) {
         DQ_HIP(dq::launch_gemv(w->dev, fmt, a + r0 * arb, arb, 1, n0, n1, y + r0 * y_stride, y_stride, bias, nullptr,
                                as_stream(stream)),

@@ -92,11 +92,16 @@ constexpr int64_t kF32GemmMinRows = DQ_F32_GEMM_MIN_ROWS;
 hipError_t launch_gemm_b32(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0,
                            int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s);
 bool gemm_b32_supported(int dtype, int af);
-// Skinny MFMA GEMV (Q4_K / Q6_K x Q8_K, 2 <= m <= kSkinnyMaxRows) on pre-quantized
-// Q8_K rows; hipErrorInvalidValue otherwise.
+// Skinny MFMA GEMV on pre-quantized rows: Q4_K / Q6_K x Q8_K for 2 <= m <=
+// kSkinnyMaxRows, and x sub-scaled (DQ_ACT_SX) for 2 <= m <= kSkinnySxMaxRows;
+// hipErrorInvalidValue otherwise.
 hipError_t launch_gemv_mma(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0,
                            int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s);
 constexpr int64_t kSkinnyMaxRows = 64;
+constexpr int64_t kSkinnySxMaxRows = 16;
+// Whether m sub-scaled rows over rows [n0, n1) of w run faster on the skinny MFMA GEMV
+// than on the VALU GEMV (the launch shapes where it was measured faster).
+bool skinny_sx_pays(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
 bool gemv_mma_supported(int dtype, int af, int64_t m);
 // Whether the skinny kernel's LDS holds the t-terms of nblk super-blocks for m rows
 // (gated: of two weights).

@@ -52,6 +52,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "dq_act.h"
 #include "dq_device.h"
 #include "dq_internal.h"
@@ -160,6 +162,33 @@ DQ_DEV void load_codes(const ActSrc<false>& src, int b, int li, int lg, ActSB<MT
 #pragma unroll
     for (int s = 0; s < 4; ++s) o.a[mt][s] = ld16(src.r, base + 4 + 64 * s + 16 * lg);
     o.da[mt] = as_f(ld4(src.r, base));
+  }
+}
+
+// Sub-scaled activations (ActSuperQ8, 320 bytes per super-block: codes, u @256, the
+// sub-block multipliers m_b as int16 @260; kernels_avx2.cpp:1077-1096): the codes as
+// in ActSB, u of row 16 mt + li in da (the chain's per-super-block factor), and the
+// eight m_b of each of this lane's output rows 16 mt + 4 lg + e (dword s holds
+// m_{2s} | m_{2s+1} << 16).
+template <int MT>
+struct ActSBX {
+  v4u a[MT][4];
+  float da[MT];
+  v4u mb[MT][4];
+};
+
+template <int MT>
+DQ_DEV void load_codes_sx(const ActSrc<false>& src, int b, int li, int lg, ActSBX<MT>& o) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const u32 base = (u32)((16 * mt + li) * src.stride + (int64_t)b * 320);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) o.a[mt][s] = ld16(src.r, base + 64 * s + 16 * lg);
+    o.da[mt] = as_f(ld4(src.r, base + 256));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o.mb[mt][e] = ld16(src.r, (u32)((16 * mt + 4 * lg + e) * src.stride + (int64_t)b * 320 + 260));
+    }
   }
 }
 
@@ -285,6 +314,124 @@ DQ_DEV void tterms(const WSB<kQ6_K, CT>& w, int ct, const ActSB<MT>& A, int lg, 
     for (int e = 0; e < 4; ++e) t[mt][e] = d * (float)((H[mt][e] << 6) + L[mt][e]);
 }
 
+// Sub-scaled activations (kernels_avx2.cpp:1117-1216): the super-block integers carry
+// the activation multiplier of each 32-value sub-block b, S = sum_b m_b S_b, which
+// differs per activation row, so it cannot ride in the weight operand. K-step s
+// spans sub-blocks 2 s (lane groups 0, 1) and 2 s + 1 (lane groups 2, 3): each chain
+// runs twice per step on the activation operand with the other half's lanes zeroed,
+// and the exact products m_b S_b (below 2^31 each) are added into a 64-bit S. Then
+// the canonical order of the Q8_K pair: t = d (float)S (Q4_K: t = fma(-dmin, Mn, t)
+// with Mn = sum_b m_b m_j (code sum of sub-block b)), the chain multiplies by u.
+DQ_DEV void halves(v4u a, int lg, v4u& a0, v4u& a1) {
+  const u32 keep0 = lg < 2 ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a0[i] = a[i] & keep0;
+    a1[i] = a[i] & ~keep0;
+  }
+}
+DQ_DEV int mb_lo(v4u mb, int s) { return (int)((s == 0 ? mb.x : s == 1 ? mb.y : s == 2 ? mb.z : mb.w) & 0xFFFFu); }
+DQ_DEV int mb_hi(v4u mb, int s) { return (int)((s == 0 ? mb.x : s == 1 ? mb.y : s == 2 ? mb.z : mb.w) >> 16); }
+
+template <int CT, int MT>
+DQ_DEV void tterms(const WSB<kQ4_K, CT>& w, int ct, const ActSBX<MT>& A, int lg, float t[MT][4]) {
+  const int hi = lg >> 1;
+  const u32 shift = 4u * (u32)hi, flip = hi ? 0x08080808u : 0u;  // high nibbles are stored XOR 8
+  const v4u hd = w.hd[ct];
+  const u32 sc_lo = hd.y & 0x3F3F3F3Fu, mn_lo = hd.z & 0x3F3F3F3Fu;
+  const u32 sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+  const u32 mn_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+  const u32 sc = __builtin_amdgcn_perm(sc_hi, sc_lo, sel_subblocks(hi));
+  const u32 KH = (sc >> 3) & 0x07070707u, KL = sc & 0x07070707u;
+  const u32 MN = __builtin_amdgcn_perm(mn_hi, mn_lo, sel_subblocks(hi));
+  int64_t S[MT][4];
+  int Mn[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      S[mt][e] = 0;
+      Mn[mt][e] = 0;
+    }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const v4u qb = ((w.q[ct][s] >> shift) & 0x0F0F0F0Fu) ^ flip;
+    const u32 kh = __builtin_amdgcn_perm(0u, KH, sel_u16x2(s));
+    const u32 kl = __builtin_amdgcn_perm(0u, KL, sel_u16x2(s));
+    const u32 mm4 = __builtin_amdgcn_perm(0u, MN, sel_x4(s));
+    const v4u H = {mul_bytes(qb.x, kh), mul_bytes(qb.y, kh), mul_bytes(qb.z, kh), mul_bytes(qb.w, kh)};
+    const v4u Lo = {mul_bytes(qb.x, kl), mul_bytes(qb.y, kl), mul_bytes(qb.z, kl), mul_bytes(qb.w, kl)};
+    const v4u Mp = {mm4, mm4, mm4, mm4};
+    const v4i_t z = {0, 0, 0, 0};
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      v4u a0, a1;
+      halves(A.a[mt][s], lg, a0, a1);
+      const v4i_t h0 = mfma(a0, H, z), l0 = mfma(a0, Lo, z), m0 = mfma(a0, Mp, z);
+      const v4i_t h1 = mfma(a1, H, z), l1 = mfma(a1, Lo, z), m1 = mfma(a1, Mp, z);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int f0 = mb_lo(A.mb[mt][e], s), f1 = mb_hi(A.mb[mt][e], s);
+        S[mt][e] += (int64_t)(((h0[e] << 3) + l0[e]) * f0) + (int64_t)(((h1[e] << 3) + l1[e]) * f1);
+        Mn[mt][e] += m0[e] * f0 + m1[e] * f1;
+      }
+    }
+  }
+  const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float u = d * (float)S[mt][e];
+      t[mt][e] = fmaf(-dmin, (float)Mn[mt][e], u);
+    }
+}
+
+template <int CT, int MT>
+DQ_DEV void tterms(const WSB<kQ6_K, CT>& w, int ct, const ActSBX<MT>& A, int lg, float t[MT][4]) {
+  int64_t S[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) S[mt][e] = 0;
+  const int sh = 2 * (lg >> 1);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const v4u lo = (s >> 1) ? w.l1[ct] : w.l0[ct], hb = (s >> 1) ? w.h1[ct] : w.h0[ct];
+    const u32 qsh = (u32)(sh + 4 * (s & 1));
+    const v4u q = ((lo >> (u32)(4 * (s & 1))) & 0x0F0F0F0Fu) | (((hb >> qsh) & 0x03030303u) << 4);
+    const u32 sw = s == 0 ? w.sc[ct].x : s == 1 ? w.sc[ct].y : s == 2 ? w.sc[ct].z : w.sc[ct].w;
+    const int sc = sbfe(sw, 8 * lg, 8);
+    v4u bh, bl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u32 h, l;
+      q6_split(q[i], sc, h, l);
+      bh[i] = h;
+      bl[i] = l;
+    }
+    const v4i_t z = {0, 0, 0, 0};
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      v4u a0, a1;
+      halves(A.a[mt][s], lg, a0, a1);
+      const v4i_t h0 = mfma(a0, bh, z), l0 = mfma(a0, bl, z);
+      const v4i_t h1 = mfma(a1, bh, z), l1 = mfma(a1, bl, z);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // |64 H + L| <= 32 * 128 * 32 * 127 per half step, times m_b <= 128: below 2^31
+        const int f0 = mb_lo(A.mb[mt][e], s), f1 = mb_hi(A.mb[mt][e], s);
+        S[mt][e] += (int64_t)(((h0[e] << 6) + l0[e]) * f0) + (int64_t)(((h1[e] << 6) + l1[e]) * f1);
+      }
+    }
+  }
+  const float d = h2f(w.dw[ct]);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[mt][e] = d * (float)S[mt][e];
+}
+
 template <int WT, int CT>
 struct WRes;
 template <int CT>
@@ -313,15 +460,17 @@ struct WRes<kQ6_K, CT> {
 // flight during the compute (activation loads of b are issued before the weight
 // loads of b + 1, so waiting for them does not wait for the prefetch: loads retire
 // in order).
-template <int WT, int CT, int MT, bool kFused, int D>
+template <int WT, int CT, int MT, bool kFused, int D, bool kSx>
 DQ_DEV void skinny_wave(const SkinnyJob& J, const uint8_t* const* p, int nblk, int64_t G, int r0, bool ok, int b0,
                         int b1, float* tt, float* dal, int li, int lg) {
   constexpr int NC = 16 * CT, NR = 16 * MT;
+  static_assert(!kSx || !kFused, "sub-scaled rows arrive quantized");
+  using Act = std::conditional_t<kSx, ActSBX<MT>, ActSB<MT>>;
   WRes<WT, CT> res;
   res.init(p, G, nblk, ok);
   ActSrc<kFused> src;
   src.init(J);
-  auto emit = [&](const WSB<WT, CT>& w, const ActSB<MT>& A, int b) {
+  auto emit = [&](const WSB<WT, CT>& w, const Act& A, int b) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       float t[MT][4];
@@ -336,8 +485,10 @@ DQ_DEV void skinny_wave(const SkinnyJob& J, const uint8_t* const* p, int nblk, i
       for (int mt = 0; mt < MT; ++mt) dal[b * NR + 16 * mt + li] = A.da[mt];
     }
   };
-  auto act = [&](int b, ActSB<MT>& A) {
-    if constexpr (kFused) {
+  auto act = [&](int b, Act& A) {
+    if constexpr (kSx) {
+      load_codes_sx<MT>(src, b, li, lg, A);
+    } else if constexpr (kFused) {
       static_assert(MT == 1, "in-kernel quantization covers one activation tile");
       XSB x;
       load_x(src, b, li, lg, x);
@@ -357,7 +508,7 @@ DQ_DEV void skinny_wave(const SkinnyJob& J, const uint8_t* const* p, int nblk, i
 #pragma unroll
     for (int i = 0; i < D; ++i)
       if (b0 + i < b1) res.load(w[i], b0 + i, r0, li, lg);
-    ActSB<MT> A[2];
+    Act A[2];
     act(b0, A[0]);
 #pragma unroll 1
     for (int bb = b0; bb < b1; bb += D) {
@@ -375,7 +526,7 @@ DQ_DEV void skinny_wave(const SkinnyJob& J, const uint8_t* const* p, int nblk, i
     WSB<WT, CT> cur;
     res.load(cur, b0, r0, li, lg);
     for (int b = b0; b < b1; ++b) {
-      ActSB<MT> A;
+      Act A;
       act(b, A);
       WSB<WT, CT> nxt;
       res.load(nxt, b + 1 < b1 ? b + 1 : b, r0, li, lg);
@@ -390,7 +541,7 @@ DQ_DEV void skinny_wave(const SkinnyJob& J, const uint8_t* const* p, int nblk, i
       WSB<WT, CT> w;
       res.load(w, b, r0, li, lg);
       __builtin_amdgcn_sched_barrier(0);
-      ActSB<MT> A;
+      Act A;
       act(b, A);
       emit(w, A, b);
     }
@@ -400,7 +551,7 @@ DQ_DEV void skinny_wave(const SkinnyJob& J, const uint8_t* const* p, int nblk, i
 // W waves per workgroup (4 or 8; launch_group picks it from the launch's shape); D
 // super-blocks of weights in flight per wave (launch_group picks 4 for one round of
 // workgroups with several super-blocks per wave).
-template <int CT, int MT, bool kFused, bool kGated, int W, int D = 1>
+template <int CT, int MT, bool kFused, bool kGated, int W, int D = 1, bool kSx = false>
 __global__ __launch_bounds__(W * 64) void k_skinny(SkinnyGroup g) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int NC = 16 * CT, NR = 16 * MT;
@@ -428,9 +579,9 @@ __global__ __launch_bounds__(W * 64) void k_skinny(SkinnyGroup g) {
   float* tw = half ? tu : tt;
   float* dw = dal + half * nblk * NR;
   if (J.dtype == kQ6_K) {
-    skinny_wave<kQ6_K, CT, MT, kFused, D>(J, planes, nblk, G, r0, ok, b0, b1, tw, dw, li, lg);
+    skinny_wave<kQ6_K, CT, MT, kFused, D, kSx>(J, planes, nblk, G, r0, ok, b0, b1, tw, dw, li, lg);
   } else {
-    skinny_wave<kQ4_K, CT, MT, kFused, D>(J, planes, nblk, G, r0, ok, b0, b1, tw, dw, li, lg);
+    skinny_wave<kQ4_K, CT, MT, kFused, D, kSx>(J, planes, nblk, G, r0, ok, b0, b1, tw, dw, li, lg);
   }
   __syncthreads();
   // the in-order chains of the tile's NR x NC outputs, shared by all waves
@@ -459,16 +610,17 @@ size_t skinny_lds(int64_t nblk, int ct, int mt, bool gated = false) {
 }
 constexpr size_t kSkinnyMaxLds = 160 * 1024;
 
-template <int CT, int MT, bool kFused, bool kGated = false, int W = kSkinnyWaves, int D = 1>
+template <int CT, int MT, bool kFused, bool kGated = false, int W = kSkinnyWaves, int D = 1, bool kSx = false>
 hipError_t skinny_launch(const SkinnyGroup& g, int wgs, hipStream_t s) {
   const size_t lds = skinny_lds(g.nblk, CT, MT, kGated);
   if (lds > kSkinnyMaxLds) return hipErrorInvalidValue;
   if (lds > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_skinny<CT, MT, kFused, kGated, W, D>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const hipError_t e =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&k_skinny<CT, MT, kFused, kGated, W, D, kSx>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((k_skinny<CT, MT, kFused, kGated, W, D>), dim3((unsigned)wgs), dim3(W * 64), lds, s, g);
+  hipLaunchKernelGGL((k_skinny<CT, MT, kFused, kGated, W, D, kSx>), dim3((unsigned)wgs), dim3(W * 64), lds, s, g);
   return hipGetLastError();
 }
 
@@ -494,7 +646,7 @@ int skinny_ct(int64_t wgs16, int64_t nblk, int cus, int mt) {
 }
 
 hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t* last_row, bool fused, bool gated,
-                        int cus, hipStream_t s) {
+                        int cus, hipStream_t s, bool sx = false) {
   int mmax = 0;
   int64_t wgs16 = 0;
   for (int i = 0; i < g.count; ++i) {
@@ -502,7 +654,8 @@ hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t*
     mmax = g.job[i].m > mmax ? g.job[i].m : mmax;
   }
   const int mt = mmax > 16 ? 4 : 1;
-  if (mt == 4 && fused) return hipErrorInvalidValue;
+  if (mt == 4 && (fused || sx)) return hipErrorInvalidValue;
+  if (sx && (fused || gated)) return hipErrorInvalidValue;
   const int ct = gated ? 1 : skinny_ct(wgs16, g.nblk, cus, mt);
   const int nc = 16 * ct;
   int64_t wgs = 0;
@@ -522,6 +675,15 @@ hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t*
     if (fused) return skinny_launch<1, 1, true, true>(g, (int)wgs, s);
     return four ? skinny_launch<1, 1, false, true, 4>(g, (int)wgs, s) : skinny_launch<1, 1, false, true>(g, (int)wgs, s);
   }
+  if (sx) {
+    // sub-scaled rows (up to 16): the launch shapes of the Q8_K rows below
+    if (ct == 4) return skinny_launch<4, 1, false, false, 4, 1, true>(g, (int)wgs, s);
+    if (four) return skinny_launch<1, 1, false, false, 4, 1, true>(g, (int)wgs, s);
+    if (wgs <= cus && g.nblk >= 3 * kSkinnyWaves) {  // 2 in flight: the m_b words take the registers of 2 more
+      return skinny_launch<1, 1, false, false, kSkinnyWaves, 2, true>(g, (int)wgs, s);
+    }
+    return skinny_launch<1, 1, false, false, kSkinnyWaves, 1, true>(g, (int)wgs, s);
+  }
   if (mt == 4) return skinny_launch<1, 4, false>(g, (int)wgs, s);
   if (ct == 4) return fused ? skinny_launch<4, 1, true, false, 4>(g, (int)wgs, s)
                             : skinny_launch<4, 1, false, false, 4>(g, (int)wgs, s);
@@ -537,7 +699,22 @@ hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t*
 }  // namespace
 
 bool gemv_mma_supported(int dtype, int af, int64_t m) {
-  return (dtype == kQ4_K || dtype == kQ6_K) && af == kActQ8_K && m >= 2 && m <= kSkinnyMaxRows;
+  if (dtype != kQ4_K && dtype != kQ6_K) return false;
+  if (af == kActQ8_K) return m >= 2 && m <= kSkinnyMaxRows;
+  return af == kActSX && m >= 2 && m <= kSkinnySxMaxRows;
+}
+
+// Sub-scaled rows: the MFMA GEMV costs the same from 2 to 16 rows, the VALU GEMV grows
+// with the rows but is cheaper for a few rows of a launch with many 16-row tiles.
+// Measured (graph replay, rotated weights; skinny vs VALU GEMV at m = 2 / 4 / 8):
+// Q4_K 8960 x 1536 11.8 / 11.9 / 12.3 vs 8.2 / 10.6 / 15.3 us; Q4_K 14336 x 4096
+// 23.2 / 23.3 / 23.6 vs 13.2 / 17.5 / 25.0; Q6_K 151936 x 1536 (64-row tiles) 128 / 128 /
+// 130 vs 71 / 100 / 156; one round of tiles (Q4_K 1536 x 1536, 4096 x 14336; Q6_K
+// 1536 x 8960, 4096 x 14336) 6.5 / 20.8 / 16.1 / 24.5 vs 7.3 / 23.6 / 23.8 / 34.1 at m = 2.
+bool skinny_sx_pays(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {
+  const int64_t tiles = (n1 + 15) / 16 - n0 / 16;
+  const int64_t cus = w.cus > 0 ? w.cus : 256;
+  return m >= 8 || tiles <= cus || (w.dtype == kQ6_K && tiles < 16 * cus);
 }
 
 bool gemv_mma_lds_ok(int64_t nblk, int64_t m, bool gated) {
@@ -566,7 +743,7 @@ hipError_t launch_gemv_mma(const WeightDev& w, int af, const uint8_t* acts, int6
   g.job[0].arb = arb;
   g.count = 1;
   g.nblk = (int)w.nblk;
-  return launch_group(g, &n0, &n1, false, false, w.cus, s);
+  return launch_group(g, &n0, &n1, false, false, w.cus, s, af == kActSX);
 }
 
 hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s) {
