@@ -10,15 +10,19 @@
 // code sum of the activation block.
 //
 // Workgroup: 4 waves over a 64 x 64 tile (activation rows x one 64-row weight group),
-// each wave 32 x 32 (2 x 2 MFMA tiles), one LDS stage of 8 blocks at a time: with 41 KB
-// three workgroups share a CU and hide each other's loads (measured: a double-buffered
-// stage, one workgroup per CU, was 1.4-1.8x slower at M = 512). Per stage the weight codes (the
+// each wave 32 x 32 (2 x 2 MFMA tiles), two LDS stages of 4 blocks (44 KB: three
+// workgroups per CU): the direct-to-LDS loads of the next stage are in flight while one
+// is computed, across an LDS-only barrier (a full __syncthreads would wait for them; a
+// third stage, two workgroups per CU, measured slower). Per stage the weight codes (the
 // plane layout: per block and 16-byte chunk 64 rows x 16 B, 1 KB contiguous), their fp16
-// scales and the 320 activation bytes of each of the 64 rows reach LDS by direct-to-LDS
-// buffer loads (rows and blocks past the ends read as zeros); the activation scales and
-// sums are then gathered into [block][row] arrays so that a lane reads the four rows of
-// its MFMA result with one 16-byte read. The epilogue (4 VALU per output and block) is
-// the bound; the MFMA work is an eighth of it.
+// scales and the 160 activation bytes of each of the 64 rows reach LDS by direct-to-LDS
+// buffer loads (rows and blocks past the ends read as zeros); the activation scales, the
+// Q4_0 offsets -8 sum(a_i) and the weight scales as floats are then gathered into
+// [block][row] arrays so that a lane reads the four rows of its MFMA result with one
+// 16-byte read. The MFMAs write VGPRs (a budget of at most 256 registers, at least two
+// waves per SIMD, selects that form: no accumulation registers to read back), the Q4_0 offset is the MFMA's initial accumulator, and the four
+// products of the next block are in flight during each block's epilogue (4 VALU per output
+// and block, the bound; the MFMA work is an eighth of it).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -32,26 +36,31 @@ namespace {
 
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kKB = 8;                      // blocks per stage
+constexpr int kKB = 4;                      // blocks per stage
 constexpr int kARow = kKB * 40;             // staged activation bytes per row
 constexpr int kA = 0;                       // [64 rows][kKB * 40 B] activation blocks as stored
 constexpr int kB = kA + 64 * kARow;         // [kKB][2 chunks][64 rows][16 B] weight codes
 constexpr int kD = kB + kKB * 2 * 64 * 16;  // [kKB][64 rows] fp16 weight scales
 constexpr int kDA = kD + kKB * 64 * 2;      // [kKB][64 rows] activation scales (float)
-constexpr int kSA = kDA + kKB * 64 * 4;     // [kKB][64 rows] activation code sums (int)
-constexpr int kStage = kSA + kKB * 64 * 4;
-constexpr int kLds = kStage;  // single-buffered: 41 KB, three workgroups per CU overlap each other
+constexpr int kSA = kDA + kKB * 64 * 4;     // [kKB][64 rows] Q4_0: -8 x activation code sums (int)
+constexpr int kDW = kSA + kKB * 64 * 4;     // [kKB][64 rows] weight scales as float
+constexpr int kStage = kDW + kKB * 64 * 4;
+constexpr int kLds = 2 * kStage;  // two stages: 44 KB, three workgroups per CU
 
 DQ_DEV void ld_lds16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_dst, u32 voff, u32 soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_dst, 16, voff, soff, 0, 0);
 }
+
+// a workgroup barrier after this wave's LDS reads and writes: later direct-to-LDS loads stay
+// in flight across it (__syncthreads would wait for them)
+DQ_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 DQ_DEV v4i_t mfma32(v2u a, v2u b, v4i_t c) {
   return __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), c, 0, 0, 0);
 }
 
 template <int WT>
-__global__ __launch_bounds__(256) void k_gemm_b32(const uint8_t* __restrict__ qs_plane, const uint8_t* __restrict__ d_plane,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_b32(const uint8_t* __restrict__ qs_plane, const uint8_t* __restrict__ d_plane,
                                                   int nblk, int64_t g0, int64_t n0, int64_t n1,
                                                   const uint8_t* __restrict__ acts, int64_t arb, int64_t m,
                                                   float* __restrict__ y, int64_t ys, const float* __restrict__ bias,
@@ -86,81 +95,113 @@ __global__ __launch_bounds__(256) void k_gemm_b32(const uint8_t* __restrict__ qs
   // staging of blocks [b, b + kKB) into buffer buf: direct-to-LDS loads only
   auto issue = [&](int b, int buf) {
     uint8_t* base = lds + buf * kStage;
-    // activations: piece p (16 B) of the 64 x kARow region is row p / 20, byte 16 (p % 20)
+    // activations: piece p (16 B) of the 64 x kARow region is row p / kAP, byte 16 (p % kAP);
+    // 1 KB instruction i goes to wave i % 4
+    constexpr int kAP = kARow / 16, kAI = 64 * kAP / 64;
 #pragma unroll
-    for (int i = 0; i < 5; ++i) {
-      const int p = (wave * 5 + i) * 64 + lane, row = p / 20;
-      ld_lds16(ra, base + kA + (wave * 5 + i) * 1024, (u32)(row * arb + 16 * (p % 20)), (u32)(b * 40));
+    for (int ii = 0; ii < (kAI + 3) / 4; ++ii) {
+      const int i = wave + 4 * ii;
+      if (i < kAI) {
+        const int p = i * 64 + lane, row = p / kAP;
+        ld_lds16(ra, base + kA + i * 1024, (u32)(row * arb + 16 * (p % kAP)), (u32)(b * 40));
+      }
     }
     // weight codes: one 1 KB instruction per (block, chunk)
 #pragma unroll
-    for (int i = 0; i < 4 * kC / 2; ++i) {
-      const int q = wave * (4 * kC / 2) + i;  // (block, chunk) = (q / kC, q % kC)
+    for (int i = 0; i < kKB * kC / 4; ++i) {
+      const int q = wave * (kKB * kC / 4) + i;  // (block, chunk) = (q / kC, q % kC)
       ld_lds16(rq, base + kB + q * 1024, (u32)(lane * 16), (u32)((b * kC + q) * 1024));
     }
-    if (wave == 0) ld_lds16(rd, base + kD, (u32)(lane * 16), (u32)(b * 128));
+    // fp16 weight scales: kKB x 128 B (wave 3: it issues the fewest activation loads)
+    if (wave == 3 && lane < kKB * 8) ld_lds16(rd, base + kD, (u32)(lane * 16), (u32)(b * 128));
   };
-  // the activation scales and code sums of a landed stage as [block][row]
+  // the activation scales, code sums and weight scales of a landed stage as [block][row]
   auto gather = [&](int buf) {
     uint8_t* base = lds + buf * kStage;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kKB / 4; ++i) {
       const int idx = t + 256 * i, j = idx >> 6, row = idx & 63;
       const v2u ds = *reinterpret_cast<const v2u*>(base + kA + row * kARow + j * 40);
       *reinterpret_cast<u32*>(base + kDA + idx * 4) = ds.x;
-      *reinterpret_cast<u32*>(base + kSA + idx * 4) = ds.y;
+      if (WT == kQ4_0) *reinterpret_cast<int*>(base + kSA + idx * 4) = -8 * (int)ds.y;
+      *reinterpret_cast<float*>(base + kDW + idx * 4) = h2f(*reinterpret_cast<const uint16_t*>(base + kD + idx * 2));
+    }
+  };
+  // P_b of this wave's 2 x 2 MFMA tiles for block j of the landed stage; Q4_0 starts the
+  // integer accumulator at -8 x the activation code sum of the row
+  auto products = [&](const uint8_t* base, int j, v4i_t (&p)[2][2]) {
+    v2u af[2], bf[2];
+    v4i_t c[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int row = 32 * wm + 16 * rt + li;
+      af[rt] = *reinterpret_cast<const v2u*>(base + kA + row * kARow + j * 40 + 8 + 8 * lg);
+      c[rt] = WT == kQ4_0 ? *reinterpret_cast<const v4i_t*>(base + kSA + (j * 64 + 32 * wm + 16 * rt + 4 * lg) * 4)
+                          : v4i_t{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int col = 32 * wn + 16 * ct + li;
+      if (WT == kQ8_0) {
+        bf[ct] = *reinterpret_cast<const v2u*>(base + kB + ((j * 2 + (lg >> 1)) * 64 + col) * 16 + 8 * (lg & 1));
+      } else {
+        // values 0..15 are the low nibbles of bytes 0..15, 16..31 the high ones
+        const v2u raw = *reinterpret_cast<const v2u*>(base + kB + (j * 64 + col) * 16 + 8 * (lg & 1));
+        const u32 sh = (lg >> 1) * 4;
+        bf[ct] = v2u{(raw.x >> sh) & 0x0F0F0F0Fu, (raw.y >> sh) & 0x0F0F0F0Fu};
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) p[rt][ct] = mfma32(af[rt], bf[ct], c[rt]);
+  };
+  // acc = acc + (dw * da) * (float)P_b, in block order
+  auto epilogue = [&](const uint8_t* base, int j, const v4i_t (&p)[2][2]) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int r0 = 32 * wm + 16 * rt + 4 * lg;  // rows r0 .. r0 + 3 of this lane's results
+      const f4_t da = *reinterpret_cast<const f4_t*>(base + kDA + (j * 64 + r0) * 4);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const float dw = *reinterpret_cast<const float*>(base + kDW + (j * 64 + 32 * wn + 16 * ct + li) * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float t1 = dw * da[e];
+          const float t2 = t1 * (float)p[rt][ct][e];
+          acc[rt][ct][e] = acc[rt][ct][e] + t2;
+        }
+      }
     }
   };
 
-  for (int b = 0, buf = 0; b < nblk; b += kKB) {
-    issue(b, buf);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+  // two stages: the loads of the next stage are in flight while this one is computed
+  issue(0, 0);
+  for (int b = 0, buf = 0; b < nblk; b += kKB, buf ^= 1) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the stage have landed
+    lds_barrier();                  // everyone's have, and the other stage's compute is done
+    if (b + kKB < nblk) issue(b + kKB, buf ^ 1);
     gather(buf);
-    __syncthreads();
+    lds_barrier();
     const uint8_t* base = lds + buf * kStage;
-    const int nj = nblk - b < kKB ? nblk - b : kKB;
-    for (int j = 0; j < nj; ++j) {
-      v2u af[2], bf[2];
+    if (nblk - b >= kKB) {
+      // a full stage: the products of the next block are in flight during each epilogue
+      v4i_t p[2][2], q[2][2];
+      products(base, 0, p);
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        const int row = 32 * wm + 16 * rt + li;
-        af[rt] = *reinterpret_cast<const v2u*>(base + kA + row * kARow + j * 40 + 8 + 8 * lg);
+      for (int j = 0; j < kKB; j += 2) {
+        products(base, j + 1, q);
+        epilogue(base, j, p);
+        if (j + 2 < kKB) products(base, j + 2, p);
+        epilogue(base, j + 1, q);
       }
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const int col = 32 * wn + 16 * ct + li;
-        if (WT == kQ8_0) {
-          bf[ct] = *reinterpret_cast<const v2u*>(base + kB + ((j * 2 + (lg >> 1)) * 64 + col) * 16 + 8 * (lg & 1));
-        } else {
-          // values 0..15 are the low nibbles of bytes 0..15, 16..31 the high ones
-          const v2u raw = *reinterpret_cast<const v2u*>(base + kB + (j * 64 + col) * 16 + 8 * (lg & 1));
-          bf[ct] = lg < 2 ? v2u{raw.x & 0x0F0F0F0Fu, raw.y & 0x0F0F0F0Fu}
-                          : v2u{(raw.x >> 4) & 0x0F0F0F0Fu, (raw.y >> 4) & 0x0F0F0F0Fu};
-        }
-      }
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        const int r0 = 32 * wm + 16 * rt + 4 * lg;  // rows r0 .. r0 + 3 of this lane's results
-        const f4_t da = *reinterpret_cast<const f4_t*>(base + kDA + (j * 64 + r0) * 4);
-        v4i_t sa = {0, 0, 0, 0};
-        if (WT == kQ4_0) sa = *reinterpret_cast<const v4i_t*>(base + kSA + (j * 64 + r0) * 4);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          const int col = 32 * wn + 16 * ct + li;
-          const float dw = h2f(*reinterpret_cast<const uint16_t*>(base + kD + (j * 64 + col) * 2));
-          const v4i_t p = mfma32(af[rt], bf[ct], v4i_t{0, 0, 0, 0});
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int pe = WT == kQ4_0 ? p[e] - 8 * sa[e] : p[e];
-            const float t1 = dw * da[e];
-            const float t2 = t1 * (float)pe;
-            acc[rt][ct][e] = acc[rt][ct][e] + t2;
-          }
-        }
+    } else {
+      for (int j = 0; j < nblk - b; ++j) {
+        v4i_t p[2][2];
+        products(base, j, p);
+        epilogue(base, j, p);
       }
     }
-    __syncthreads();  // the stage is free for the next loads
   }
 
   // ---- store

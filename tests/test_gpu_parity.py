@@ -1091,11 +1091,12 @@ def test_gemv_split_k(cuda, pair, m):
 
 
 @pytest.mark.parametrize("t", [O.Q8_0, O.Q4_0], ids=lambda t: O.TYPE_NAMES[t])
-@pytest.mark.parametrize("m,n,k", [(17, 200, 1280), (64, 256, 4096), (130, 320, 512), (300, 64, 96)])
+@pytest.mark.parametrize("m,n,k", [(17, 200, 1280), (64, 256, 4096), (130, 320, 512), (300, 64, 96), (40, 96, 640)])
 def test_gemm_b32_bit_exact(cuda, t, m, n, k):
     """The block GEMM runs the generic per-block sequence acc = acc + (dw*da)*(float)P_b for
     every output (kernels_generic.cpp:216-239): bit-identical to the oracle, edge weight
-    blocks and partial tiles (rows, weight rows and a 3-block K) included; through
+    blocks and partial tiles (rows, weight rows, a 3-block K and a 20-block K: two full
+    8-block stages and a partial one) included; through
     dq_matmul (quantize + GEMM from 32 rows, the GEMV below) with a bias."""
     import dqtorch as T
 
