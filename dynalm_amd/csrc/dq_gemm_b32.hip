@@ -18,11 +18,13 @@
 // scales and the 160 activation bytes of each of the 64 rows reach LDS by direct-to-LDS
 // buffer loads (rows and blocks past the ends read as zeros); the activation scales, the
 // Q4_0 offsets -8 sum(a_i) and the weight scales as floats are then gathered into
-// [block][row] arrays so that a lane reads the four rows of its MFMA result with one
-// 16-byte read. The MFMAs write VGPRs (a budget of at most 256 registers, at least two
-// waves per SIMD, selects that form: no accumulation registers to read back), the Q4_0 offset is the MFMA's initial accumulator, and the four
-// products of the next block are in flight during each block's epilogue (4 VALU per output
-// and block, the bound; the MFMA work is an eighth of it).
+// [block][row] arrays (a lane reads the offsets of its four result rows with one 16-byte
+// read, and one scale of each kind for the outer products below). The MFMAs write VGPRs (a budget of at most 256 registers, at least two
+// waves per SIMD, selects that form: no accumulation registers to read back), the Q4_0
+// offset is the MFMA's initial accumulator, the scale products dw * da of a block come
+// from one fp32 MFMA of four K = 1 outer products (each a single rounded product, as
+// the VALU's; subnormal products included), and the products of the next block are in
+// flight during each block's epilogue (3 VALU per output and block: cvt, multiply, add).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -57,6 +59,16 @@ DQ_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" :::
 
 DQ_DEV v4i_t mfma32(v2u a, v2u b, v4i_t c) {
   return __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), c, 0, 0, 0);
+}
+
+typedef float f16v_t __attribute__((ext_vector_type(16)));
+
+// Four 16 x 16 outer products in one instruction (K = 1, four blocks): lane group g
+// gives column vector a (its 16 lanes' values) and row vector b of block g; registers
+// 4 g' .. 4 g' + 3 of every lane hold block g' at rows 4 lg + e, column li, the layout
+// of the 16 x 16 integer products. Each output is one product a_i b_j rounded once.
+DQ_DEV f16v_t outer4(float a, float b) {
+  return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, f16v_t{}, 0, 0, 0);
 }
 
 template <int WT>
@@ -127,9 +139,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
       *reinterpret_cast<float*>(base + kDW + idx * 4) = h2f(*reinterpret_cast<const uint16_t*>(base + kD + idx * 2));
     }
   };
-  // P_b of this wave's 2 x 2 MFMA tiles for block j of the landed stage; Q4_0 starts the
-  // integer accumulator at -8 x the activation code sum of the row
-  auto products = [&](const uint8_t* base, int j, v4i_t (&p)[2][2]) {
+  // For block j of the landed stage and this wave's 2 x 2 MFMA tiles: P_b (Q4_0 starts
+  // the integer accumulator at -8 x the activation code sum of the row), and the scale
+  // products dw * da as four outer products, tile (rt, ct) = (g >> 1, g & 1) from lane
+  // group g.
+  struct Prod {
+    v4i_t p[2][2];
+    f16v_t s;
+  };
+  auto products = [&](const uint8_t* base, int j, Prod& pr) {
+    const float sa = *reinterpret_cast<const float*>(base + kDA + (j * 64 + 32 * wm + 16 * (lg >> 1) + li) * 4);
+    const float sw = *reinterpret_cast<const float*>(base + kDW + (j * 64 + 32 * wn + 16 * (lg & 1) + li) * 4);
     v2u af[2], bf[2];
     v4i_t c[2];
 #pragma unroll
@@ -154,25 +174,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) p[rt][ct] = mfma32(af[rt], bf[ct], c[rt]);
+      for (int ct = 0; ct < 2; ++ct) pr.p[rt][ct] = mfma32(af[rt], bf[ct], c[rt]);
+    pr.s = outer4(sa, sw);
   };
   // acc = acc + (dw * da) * (float)P_b, in block order
-  auto epilogue = [&](const uint8_t* base, int j, const v4i_t (&p)[2][2]) {
+  auto epilogue = [&](const Prod& pr) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const int r0 = 32 * wm + 16 * rt + 4 * lg;  // rows r0 .. r0 + 3 of this lane's results
-      const f4_t da = *reinterpret_cast<const f4_t*>(base + kDA + (j * 64 + r0) * 4);
+    for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const float dw = *reinterpret_cast<const float*>(base + kDW + (j * 64 + 32 * wn + 16 * ct + li) * 4);
+      for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float t1 = dw * da[e];
-          const float t2 = t1 * (float)p[rt][ct][e];
+          const float t1 = pr.s[4 * (2 * rt + ct) + e];
+          const float t2 = t1 * (float)pr.p[rt][ct][e];
           acc[rt][ct][e] = acc[rt][ct][e] + t2;
         }
-      }
-    }
   };
 
   // two stages: the loads of the next stage are in flight while this one is computed
@@ -186,20 +202,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const uint8_t* base = lds + buf * kStage;
     if (nblk - b >= kKB) {
       // a full stage: the products of the next block are in flight during each epilogue
-      v4i_t p[2][2], q[2][2];
+      Prod p, q;
       products(base, 0, p);
 #pragma unroll
       for (int j = 0; j < kKB; j += 2) {
         products(base, j + 1, q);
-        epilogue(base, j, p);
+        epilogue(p);
         if (j + 2 < kKB) products(base, j + 2, p);
-        epilogue(base, j + 1, q);
+        epilogue(q);
       }
     } else {
       for (int j = 0; j < nblk - b; ++j) {
-        v4i_t p[2][2];
+        Prod p;
         products(base, j, p);
-        epilogue(base, j, p);
+        epilogue(p);
       }
     }
   }

@@ -1116,6 +1116,35 @@ def test_gemm_b32_bit_exact(cuda, t, m, n, k):
         assert ok, worst
 
 
+@pytest.mark.parametrize("t", [O.Q8_0, O.Q4_0], ids=lambda t: O.TYPE_NAMES[t])
+def test_gemm_b32_subnormal_scale_products(cuda, t):
+    """fp16 weight scales down to the smallest subnormal (2^-24) against activation rows of
+    magnitude 1e-33: dw * da falls below the smallest normal float (subnormal or zero products),
+    and the GEMM still equals the oracle's float32 order bit for bit."""
+    import dqtorch as T
+
+    n, k, m = 128, 256, 40
+    bb = 34 if t == O.Q8_0 else 18
+    rows = weight_rows(t, n, k, 2140 + t, edge=True).reshape(n, -1, bb)
+    d = np.array([0x0001, 0x0003, 0x03FF, 0x0400, 0x3C00], np.uint16)  # subnormals, min normal, 1.0
+    d_rows = np.repeat(d[np.arange(n) % len(d)][:, None], k // 32, axis=1)  # one scale per weight row
+    d_rows[n // 2:, ::2] = 0x3C00                                            # and mixed rows
+    rows[:, :, 0:2] = d_rows.view(np.uint8).reshape(n, -1, 2)
+    rows = rows.reshape(n, -1)
+    x = activations(m, k, 2141)
+    x[: m // 2] *= np.float32(1e-33)
+    a = O.quantize_act(O.ACT_PER32, x)
+    w = dq.Weight.upload(t, rows, k)
+    y = host(T.gemm(w, O.ACT_PER32, dev(a)))
+    want = O.matmul(t, O.ACT_PER32, rows, a, k)
+    # outputs whose every scale product is subnormal: a kernel flushing them would give zeros
+    dw = np.float32(np.float16(d.view(np.float16)[0]))                   # 2^-24
+    da = a.reshape(m, -1, 40)[:, :, :4].copy().view(np.float32)[..., 0]  # [m][blocks]
+    assert np.all(dw * da[: m // 2] < np.finfo(np.float32).tiny)
+    assert np.count_nonzero(want[: m // 2, 0: n // 2: len(d)]) > 0
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
 def test_gemm_b32_row_range_and_saturated_codes(cuda):
     """A row range (unaligned ends) leaves the other outputs untouched; +-127 activations
     against -128 / +127 Q8_0 codes (the largest block sums) stay exact."""
