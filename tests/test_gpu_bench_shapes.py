@@ -5,6 +5,7 @@ shapes select.
   M=2048 (the streamed 128 x 256 kernel: one round of 224 workgroups, and 3.5 rounds),
   Q6_K over 4 and 56 super-blocks (the 256 x 128 tile). Every output bit-identical to the GEMV on the same Q8_K rows,
   sampled columns bit-identical to the oracle.
+- The per-32 GEMM (Q8_0 4096 x 4096, Q4_0 K=4096 N=14336) at M=512.
 - The 4-wave gated skinny launch at config 5's gate/up shape (Q4_K 8960 x 1536, M=16).
 - dq_matmul's fused decode path at K = 14336 (split-K for the per-32 formats, the
   early-activation GEMV for the K-quants), equal to quantize + dq_gemv bit for bit.
@@ -61,6 +62,30 @@ def test_gemm_q4k_bench_shape(cuda, m):
     assert np.array_equal(bits(yg), bits(yv)), "GEMM differs from the GEMV"
     cols = np.random.default_rng(m).choice(n, 128, replace=False)
     want = O.matmul(O.Q4_K, O.ACT_Q8_K, w_rows[cols], a, k)
+    assert np.array_equal(bits(yg[:, cols]), bits(want)), "GEMM differs from the oracle"
+    ym = host(T.matmul(w, xd))
+    assert np.array_equal(bits(ym), bits(yg)), "dq_matmul differs from quantize + dq_gemm"
+
+
+@pytest.mark.parametrize("t,n,k", [(O.Q8_0, 4096, 4096), (O.Q4_0, 14336, 4096)], ids=["q8_0", "q4_0"])
+def test_gemm_b32_bench_shape(cuda, t, n, k):
+    """The per-32 GEMM at the shapes the bench times (M=512): k_gemm_b32 over 128 blocks, 32
+    stages through its two LDS stage buffers, 512 / 1,792 workgroups (one round / 2.3 rounds
+    of three per CU). 128 sampled columns == the oracle bit for bit; dq_matmul (quantize +
+    GEMM) == quantize then dq_gemm on every output."""
+    import dqtorch as T
+
+    m = 512
+    w_rows = weight_rows(t, n, k, 4500 + t, edge=True)
+    x = activations(m, k, 4501)
+    w = dq.Weight.upload(t, w_rows, k)
+    xd = dev(x)
+    ad = T.quantize(O.ACT_PER32, xd)
+    a = host(ad)
+    assert np.array_equal(a, O.quantize_act(O.ACT_PER32, x))
+    yg = host(T.gemm(w, O.ACT_PER32, ad))
+    cols = np.unique(np.concatenate([np.random.default_rng(t).choice(n, 128, replace=False), [0, n - 1]]))
+    want = O.matmul(t, O.ACT_PER32, w_rows[cols], a, k)
     assert np.array_equal(bits(yg[:, cols]), bits(want)), "GEMM differs from the oracle"
     ym = host(T.matmul(w, xd))
     assert np.array_equal(bits(ym), bits(yg)), "dq_matmul differs from quantize + dq_gemm"
