@@ -229,17 +229,18 @@ int check_out(const dq_weight* w, int64_t m, int64_t n0, int64_t n1, float* y, i
 // for 24..64 rows at K=4096, N=14336), LDS for the weight's super-blocks, and fp32
 // rows addressable with 32-bit offsets.
 // Whether dq_matmul / dq_matmul_act run m rows of this pair on a GEMM: above
-// DQ_GEMV_MAX_ROWS for Q4_K x Q8_K; from 20 rows for the 32-value block GEMM (Q8_0 /
-// Q4_0 x per-32; measured at K = 4096, N = 4096 / 14336: the GEMM 37-39 / 42-43 us for
-// 8..32 rows, the GEMV passes 31.6 / 33.3 us at 16 rows, 39.0 / 40.4 at 17, 47.0 / 49.3
-// at 24, 62.5 / 65.7 at 32); Q6_K x Q8_K above 64 rows, and above
+// DQ_GEMV_MAX_ROWS for Q4_K x Q8_K; from 13 rows for the 32-value block GEMM (Q8_0 /
+// Q4_0 x per-32; dq_matmul measured at K = 4096, N = 4096 / 14336, quantization
+// included: GEMV passes 27.9 / 30.9 us at 12 rows, 35.7 / 36.6 at 13, 41.5 / 43.8 at
+// 18; quantize + GEMM 26.9 / 32.7 at 13, 27.0 / 32.4 at 18; at K = 14336 the two are
+// equal at 13 rows, 81.7 vs 82.8 us); Q6_K x Q8_K above 64 rows, and above
 // 16 where the skinny GEMV's LDS does not hold the row's super-blocks (K = 14336:
 // 110 us against 171-611 us for 17..64 rows) or the weight has 4096 rows or more (the
 // GEMM's grid fills the CUs: 35 vs 45 us at K = 4096, N = 14336; with N = 1536 it
 // loses, 70 vs 23 us).
 bool use_gemm(const dq::WeightDev& w, int fmt, int64_t m) {
   if (!dq::gemm_supported(w.dtype, fmt)) return false;
-  if (w.dtype == DQ_Q8_0 || w.dtype == DQ_Q4_0) return m >= 20;
+  if (w.dtype == DQ_Q8_0 || w.dtype == DQ_Q4_0) return m >= 13;
   if (w.dtype == DQ_Q6_K) {
     return m > dq::kSkinnyMaxRows ||
            (m > DQ_GEMV_MAX_ROWS && (!dq::gemv_mma_lds_ok(w.nblk, m) || w.n >= 4096));

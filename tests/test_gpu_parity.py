@@ -1092,14 +1092,14 @@ def test_gemv_split_k(cuda, pair, m):
 
 @pytest.mark.parametrize("t", [O.Q8_0, O.Q4_0], ids=lambda t: O.TYPE_NAMES[t])
 @pytest.mark.parametrize("m,n,k", [(17, 200, 1280), (64, 256, 4096), (130, 320, 512), (300, 64, 96), (40, 96, 640),
-                                   (33, 72, 128), (65, 130, 160), (20, 96, 512), (19, 96, 512)])
+                                   (33, 72, 128), (65, 130, 160), (13, 96, 512), (12, 96, 512)])
 def test_gemm_b32_bit_exact(cuda, t, m, n, k):
     """The block GEMM runs the generic per-block sequence acc = acc + (dw*da)*(float)P_b for
     every output (kernels_generic.cpp:216-239): bit-identical to the oracle, edge weight
     blocks and partial tiles (rows, weight rows; K of 3 blocks: a partial stage only; 4: one
     full 4-block stage; 5: a full stage and a 1-block one; 20: five stages, the two LDS
     buffers alternating) included; through
-    dq_matmul (quantize + GEMM from 20 rows, the GEMV below) with a bias."""
+    dq_matmul (quantize + GEMM from 13 rows, the GEMV below) with a bias."""
     import dqtorch as T
 
     rows = weight_rows(t, n, k, 2100 + m + t, edge=True)
@@ -1111,11 +1111,36 @@ def test_gemm_b32_bit_exact(cuda, t, m, n, k):
     assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
     bias = O.normal(2120 + m, n)
     ym = host(T.matmul(w, dev(x), dev(bias)))
-    if m >= 20:
+    if m >= 13:
         assert np.array_equal(ym.view(np.uint32), (want + bias).view(np.uint32))
     else:
         ok, worst = close(ym, want + bias)
         assert ok, worst
+
+
+@pytest.mark.parametrize("t", [O.Q8_0, O.Q4_0], ids=lambda t: O.TYPE_NAMES[t])
+@pytest.mark.parametrize("m,n,k", [(256, 8192, 128), (300, 16384, 96), (20, 33024, 64), (100, 8000, 96),
+                                   (24, 1000, 160)],
+                         ids=["tile64", "tile64-partial", "tile32-wide", "tile32-rows", "tile32-small"])
+def test_gemm_b32_tile_shapes(cuda, t, m, n, k):
+    """Both tiles of the block GEMM, picked by the launch's shape on 256 CUs: 64 x 64 where
+    those tiles are at least 7/4 of the CUs (128 row groups x 4 activation tiles; 256 x 5,
+    the last tile 44 rows), else 32 x 32 (m <= 32 over 516 row groups; 125 groups x 2 64-row
+    tiles, too few, so 4 x 32 rows; 16 groups). The tail stages of K = 64 / 96 / 160
+    included; bit-identical to the oracle, and a cut row range leaves the rest untouched."""
+    import dqtorch as T
+
+    rows = weight_rows(t, n, k, 2150 + m + t, edge=True)
+    x = activations(m, k, 2151 + m)
+    a = O.quantize_act(O.ACT_PER32, x)
+    w = dq.Weight.upload(t, rows, k)
+    y = host(T.gemm(w, O.ACT_PER32, dev(a)))
+    want = O.matmul(t, O.ACT_PER32, rows, a, k)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+    n0, n1 = 40, n - 23
+    yr = host(T.gemm(w, O.ACT_PER32, dev(a), n0=n0, n1=n1))
+    assert np.array_equal(yr[:, n0:n1].view(np.uint32), want[:, n0:n1].view(np.uint32))
+    assert not yr[:, :n0].any() and not yr[:, n1:].any()
 
 
 @pytest.mark.parametrize("t", [O.Q8_0, O.Q4_0], ids=lambda t: O.TYPE_NAMES[t])
