@@ -201,6 +201,28 @@ def test_gemm_q4k_parity(cuda, m):
     assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,n,k", [(40, 1000, 256), (40, 1000, 512), (100, 1000, 768), (64, 14336, 4096),
+                                   (128, 14336, 4096), (20, 4096, 14336)])
+def test_gemm_q4k_small_m_superblocks(cuda, m, n, k):
+    """The 4-wave GEMM for 17..128 rows (two LDS buffers, the loads of super-block b + 1
+    issued as b starts) over one super-block (nothing to prefetch), two and three, the
+    bench's M=64 / 128 shapes and a long row (56 super-blocks, 64 row groups). Every output
+    bit-identical to the GEMV on the same Q8_K rows; sampled columns to the oracle."""
+    import dqtorch as T
+
+    w_rows = weight_rows(O.Q4_K, n, k, 60 + m + k, edge=True)
+    x = activations(m, k, 61 + m)
+    a = O.quantize_act(O.ACT_Q8_K, x)
+    w = dq.Weight.upload(O.Q4_K, w_rows, k)
+    ad = dev(a)
+    yg = host(T.gemm(w, O.ACT_Q8_K, ad))
+    yv = host(T.gemv(w, O.ACT_Q8_K, ad))
+    assert np.array_equal(yg.view(np.uint32), yv.view(np.uint32))
+    cols = np.unique(np.concatenate([np.random.default_rng(m + k).choice(n, min(n, 96), replace=False), [0, n - 1]]))
+    want = O.matmul(O.Q4_K, O.ACT_Q8_K, w_rows[cols], a, k)
+    assert np.array_equal(yg[:, cols].view(np.uint32), want.view(np.uint32))
+
+
 def test_gemm_row_range_and_tails(cuda):
     import dqtorch as T
 
