@@ -22,9 +22,11 @@
 // is an integer below 2^24, so the fp32 result is exactly (float)Mn.
 //
 // Two kernel families, both with 16 x 16 output tiles per MFMA and one wave owning
-// 64 activation rows x 16*NT weight rows:
-// - k_gemm_q4k<WM, NT> (up to 128 rows): 4 waves, one per SIMD. Per super-block a
-//   wave holds its 64 rows' activation operands (16 KB) in registers and walks its
+// 16 MTW (64 unless stated) activation rows x 16*NT weight rows:
+// - k_gemm_q4k<WM, NT, MTW> (up to 128 rows): 4 waves, one per SIMD, WM along the
+//   activation rows (MTW = 1, 2 or 4 activation tiles each: shorter waves and more
+//   workgroups for small launches). Per super-block a wave holds its rows' activation
+//   operands (4 KB per tile) in registers and walks its
 //   NT weight tiles; for each it unpacks the nibbles, scales and mins of 16 weight
 //   rows itself (three stages: LDS reads of tile nt + 2, unpacking of nt + 1, MFMAs
 //   of nt). Activation codes (swizzled), nibbles and headers reach LDS by
@@ -69,11 +71,12 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;  // 4 waves, one per SIMD
 
-// LDS layout of one super-block's operands (bytes); two such buffers.
-template <int WM, int NT>
+// LDS layout of one super-block's operands (bytes); two such buffers. WM waves along the
+// activation rows, each owning MTW 16-row activation tiles.
+template <int WM, int NT, int MTW = 4>
 struct Cfg {
   static constexpr int kWN = 4 / WM;               // waves along the weight rows
-  static constexpr int kBM = 64 * WM;              // activation rows per workgroup
+  static constexpr int kBM = 16 * MTW * WM;        // activation rows per workgroup
   static constexpr int kBN = kWN * 16 * NT;        // weight rows per workgroup
   static constexpr int kWB = (kBN + 63) / 64;      // 64-row load blocks of weight rows
   static constexpr int kWRows = 64 * kWB;
@@ -200,16 +203,17 @@ DQ_DEV PrepB prep_tile_q6(v4u scw, v4u w0, v4u w1, v4u h0, v4u h1, int lg) {
 
 }  // namespace
 
-template <int WM, int NT>
+template <int WM, int NT, int MTW>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_q4k(
     const uint8_t* __restrict__ qs_plane, const uint8_t* __restrict__ hdr_plane, int nb, int64_t n_pad, int64_t nt0,
     int64_t n0, int64_t n1, const uint8_t* __restrict__ acts, int64_t arb, int64_t m, float* __restrict__ y, int64_t ys,
     const float* __restrict__ bias, int tiles_n, int tiles_m) {
-  using C = Cfg<WM, NT>;
+  using C = Cfg<WM, NT, MTW>;
   extern __shared__ __align__(16) uint8_t lds[];
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave % WM, wn = wave / WM;
+  const int wr = 16 * MTW * wm;  // the wave's first activation row in the tile
   const int li = lane & 15, lg = lane >> 4;
 
   // Tile order: workgroup i runs on XCD i % 8; consecutive logical tiles (the
@@ -277,8 +281,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     }
     // activation scales
 #pragma unroll
-    for (int k = 0; k < C::kBM / 64; ++k) {
-      if (wave == 3 - k) ld_lds4(ra, Lb + C::kDA + 256 * k, (u32)((64 * k + lane) * arb), (u32)(b * 292));
+    for (int k = 0; k < (C::kBM + 63) / 64; ++k) {
+      if (wave == 3 - k && 64 * k + lane < C::kBM) {
+        ld_lds4(ra, Lb + C::kDA + 256 * k, (u32)((64 * k + lane) * arb), (u32)(b * 292));
+      }
     }
   };
   auto bs_load = [&](int b) -> v4u { return bs_role ? ld16(ra, bs_off + (u32)(b * 292)) : v4u{0, 0, 0, 0}; };
@@ -288,12 +294,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 
   // ---- per-lane LDS read offsets
   const int qlg = 4 * (lg >> 1) + (lg & 1);
-  const int arow = 64 * wm + li;
+  const int arow = wr + li;
   int a_rd[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) a_rd[s] = C::kA + arow * 256 + 16 * ((qlg ^ li) ^ (8 * (s >> 1) + 2 * (s & 1)));
   const int bs_rd = C::kBS + arow * 32 + 8 * lg;
-  const int da_rd = C::kDA + (64 * wm + 4 * lg) * 4;
+  const int da_rd = C::kDA + (wr + 4 * lg) * 4;
   const int wrow = 16 * NT * wn + li;
   const int w_rd = C::kW + (lg * C::kWRows + wrow) * 16;
   const int h_rd = C::kH + wrow * 16;
@@ -307,11 +313,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   };
   auto prep_b = [&](const RawB& r) -> PrepB { return prep_tile(r, sel_sc, sel_mn); };
 
-  f4_t acc[NT][4];
+  f4_t acc[NT][MTW];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) acc[nt][mt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int mt = 0; mt < MTW; ++mt) acc[nt][mt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   // ---- prologue: super-block 0 into buffer 0
   {
@@ -334,11 +340,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     }
 
     // this super-block's activation operands
-    v4u a[4][4];
-    h4_t am[4];
-    f4_t da[4];
+    v4u a[MTW][4];
+    h4_t am[MTW];
+    f4_t da[MTW];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MTW; ++mt) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) a[mt][s] = lds_ld16(Lc, a_rd[s] + mt * 16 * 256);
       am[mt] = __builtin_bit_cast(h4_t, lds_ld8(Lc, bs_rd + mt * 16 * 32));
@@ -358,10 +364,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     for (int nt = 0; nt < NT; ++nt) {
       if (nt + 2 < NT) raw[nt + 2] = load_b(Lc, nt + 2);
       if (nt + 1 < NT) pb[nt + 1] = prep_b(raw[nt + 1]);
-      v4i_t tH[4], tL[4];
-      f4_t tM[4];
+      v4i_t tH[MTW], tL[MTW];
+      f4_t tM[MTW];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < MTW; ++mt) {
         const v4i_t z = {0, 0, 0, 0};
         tH[mt] = mfma(a[mt][0], pb[nt].H[0], z);
         tL[mt] = mfma(a[mt][0], pb[nt].L[0], z);
@@ -373,7 +379,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         tM[mt] = mfma_h(am[mt], pb[nt].mb, f4_t{0.0f, 0.0f, 0.0f, 0.0f});
       }
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < MTW; ++mt) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int S = tL[mt][e] + (tH[mt][e] << 3);
@@ -400,10 +406,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     if (n < n0 || n >= n1) continue;
     const float bn_ = bias ? bias[n] : 0.0f;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MTW; ++mt) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int64_t mm = mbase + 64 * wm + 16 * mt + 4 * lg + e;
+        const int64_t mm = mbase + wr + 16 * mt + 4 * lg + e;
         if (mm < m) y[mm * ys + n] = bias ? acc[nt][mt][e] + bn_ : acc[nt][mt][e];
       }
     }
@@ -733,15 +739,15 @@ bool gemm_supported(int dtype, int af) {
 
 namespace {
 
-template <int WM, int NT>
+template <int WM, int NT, int MTW = 4>
 hipError_t launch_cfg(const WeightDev& w, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
                       float* y, int64_t ys, const float* bias, hipStream_t s) {
-  using C = Cfg<WM, NT>;
+  using C = Cfg<WM, NT, MTW>;
   static_assert(C::kLds <= 160 * 1024, "LDS");
   static bool attr_set[64] = {};
   const int dev = w.device < 64 ? w.device : 63;
   if (!attr_set[dev]) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_q4k<WM, NT>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_q4k<WM, NT, MTW>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds);
     if (e != hipSuccess) return e;
     attr_set[dev] = true;
@@ -754,7 +760,7 @@ hipError_t launch_cfg(const WeightDev& w, const uint8_t* acts, int64_t arb, int6
       tiles_n * tiles_m >= (1ll << 31)) {
     return hipErrorInvalidValue;
   }
-  hipLaunchKernelGGL((k_gemm_q4k<WM, NT>), dim3((unsigned)(tiles_n * tiles_m)), dim3(kThreads), C::kLds, s,
+  hipLaunchKernelGGL((k_gemm_q4k<WM, NT, MTW>), dim3((unsigned)(tiles_n * tiles_m)), dim3(kThreads), C::kLds, s,
                      w.plane[0], w.plane[1], (int)w.nblk, w.n_pad, nt0, n0, n1, acts, arb, m, y, ys, bias,
                      (int)tiles_n, (int)tiles_m);
   return hipGetLastError();
@@ -811,20 +817,34 @@ hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t 
     if (wgs * 8 >= (int64_t)cus * 7) return launch_big<kQ4_K, 4, 2, 4>(w, acts, arb, m, n0, n1, y, ys, bias, s);
     return launch_big<kQ4_K, 2, 2, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s);
   }
-  // up to 128 rows: the 4-wave kernel with 64 or 128 activation rows; the weight-tile
-  // width is picked by rounds of workgroups over the CUs times the per-wave work
-  // (NT weight tiles plus a fixed share)
-  const int wm = m > 64 ? 2 : 1;
-  const int64_t tm = (m + 64 * wm - 1) / (64 * wm);
-  const int64_t bn2 = (4 / wm) * 32, bn1 = (4 / wm) * 16;
-  const int64_t cost2 = ((rows + bn2 - 1) / bn2 * tm + cus - 1) / cus * 3;
-  const int64_t cost1 = ((rows + bn1 - 1) / bn1 * tm + cus - 1) / cus * 2;
-  if (wm == 2) {
-    return cost2 <= cost1 ? launch_cfg<2, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s)
-                          : launch_cfg<2, 1>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+  // up to 128 rows: the 4-wave kernel in the shape (waves along the activation rows, weight
+  // tiles per wave, activation tiles per wave) whose rounds of workgroups over the CUs
+  // times its measured time per super-block (1 workgroup per CU; K = 4096 and 14336,
+  // N = 4096 and 14336) is least: 32 x 32 tiles 0.68 us, 32 x 64 (two activation tiles
+  // per wave) 0.93, 64 x 64 1.38, 128 x 64 2.53.
+  struct Shape {
+    int wm, nt, mtw, us100;
+  };
+  constexpr Shape kShapes[] = {{2, 1, 1, 68}, {1, 1, 2, 93}, {1, 1, 4, 138}, {2, 2, 4, 253}};
+  const int64_t ntn = n1 - (n0 / kRowGroup) * kRowGroup;
+  int best = 0;
+  int64_t best_cost = -1;
+  for (int i = 0; i < 4; ++i) {
+    const Shape& c = kShapes[i];
+    const int64_t bm = 16 * c.mtw * c.wm, bn = (4 / c.wm) * 16 * c.nt;
+    const int64_t wgs = (ntn + bn - 1) / bn * ((m + bm - 1) / bm);
+    const int64_t cost = (wgs + cus - 1) / cus * c.us100;
+    if (best_cost < 0 || cost < best_cost) {
+      best = i;
+      best_cost = cost;
+    }
   }
-  return cost2 <= cost1 ? launch_cfg<1, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s)
-                        : launch_cfg<1, 1>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+  switch (best) {
+    case 0: return launch_cfg<2, 1, 1>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+    case 1: return launch_cfg<1, 1, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+    case 2: return launch_cfg<1, 1, 4>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+    default: return launch_cfg<2, 2, 4>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+  }
 }
 
 }  // namespace dq

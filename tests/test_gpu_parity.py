@@ -202,12 +202,16 @@ def test_gemm_q4k_parity(cuda, m):
 
 
 @pytest.mark.parametrize("m,n,k", [(40, 1000, 256), (40, 1000, 512), (100, 1000, 768), (64, 14336, 4096),
-                                   (128, 14336, 4096), (20, 4096, 14336)])
+                                   (128, 14336, 4096), (20, 4096, 14336), (24, 14336, 512), (96, 4096, 1024),
+                                   (17, 200, 512)])
 def test_gemm_q4k_small_m_superblocks(cuda, m, n, k):
     """The 4-wave GEMM for 17..128 rows (two LDS buffers, the loads of super-block b + 1
-    issued as b starts) over one super-block (nothing to prefetch), two and three, the
-    bench's M=64 / 128 shapes and a long row (56 super-blocks, 64 row groups). Every output
-    bit-identical to the GEMV on the same Q8_K rows; sampled columns to the oracle."""
+    issued as b starts) in each of its shapes, picked by the launch on 256 CUs: 32 x 32
+    tiles (1,000 and 4,096 weight rows), 32 x 64 (24 rows of 14,336; 96 rows of 4,096),
+    64 x 64 (64 rows of 14,336) and 128 x 64 (128 rows of 14,336); over one super-block
+    (nothing to prefetch), two and three, the bench's M=64 / 128 shapes, a long row (56
+    super-blocks) and a partial weight tile (200 rows). Every output bit-identical to the
+    GEMV on the same Q8_K rows; sampled columns to the oracle."""
     import dqtorch as T
 
     w_rows = weight_rows(O.Q4_K, n, k, 60 + m + k, edge=True)
