@@ -229,7 +229,10 @@ int check_out(const dq_weight* w, int64_t m, int64_t n0, int64_t n1, float* y, i
 // for 24..64 rows at K=4096, N=14336), LDS for the weight's super-blocks, and fp32
 // rows addressable with 32-bit offsets.
 // Whether dq_matmul / dq_matmul_act run m rows of this pair on a GEMM: above
-// DQ_GEMV_MAX_ROWS for Q4_K x Q8_K; from 13 rows for the 32-value block GEMM (Q8_0 /
+// DQ_GEMV_MAX_ROWS for Q4_K x Q8_K, except up to 48 rows of weights with at most 4096
+// rows where the skinny GEMV's LDS holds the row (its 64-row tiles beat the GEMM's few
+// workgroups there: 9.4-11.1 vs 11.8-12.2 us at K = N = 4096, 19.0-20.3 vs 22.7-23.1 at
+// K = 8960, N = 1536; at N = 14336 the GEMM wins, 16.1 vs 25.2 us at 17 rows); from 13 rows for the 32-value block GEMM (Q8_0 /
 // Q4_0 x per-32; dq_matmul measured at K = 4096, N = 4096 / 14336, quantization
 // included: GEMV passes 27.9 / 30.9 us at 12 rows, 35.7 / 36.6 at 13, 41.5 / 43.8 at
 // 18; quantize + GEMM 26.9 / 32.7 at 13, 27.0 / 32.4 at 18; at K = 14336 the two are
@@ -245,6 +248,7 @@ bool use_gemm(const dq::WeightDev& w, int fmt, int64_t m) {
     return m > dq::kSkinnyMaxRows ||
            (m > DQ_GEMV_MAX_ROWS && (!dq::gemv_mma_lds_ok(w.nblk, m) || w.n >= 4096));
   }
+  if (m > DQ_GEMV_MAX_ROWS && m <= 48 && w.n <= 4096 && dq::gemv_mma_lds_ok(w.nblk, m)) return false;
   return m > DQ_GEMV_MAX_ROWS;
 }
 

@@ -227,6 +227,28 @@ def test_gemm_q4k_small_m_superblocks(cuda, m, n, k):
     assert np.array_equal(yg[:, cols].view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,n,k", [(24, 1536, 8960), (40, 4096, 4096), (48, 2048, 1024), (49, 2048, 1024),
+                                   (24, 14336, 1024)])
+def test_matmul_q4k_route_17_to_48_rows(cuda, m, n, k):
+    """dq_matmul for 17..48 rows of Q4_K: the skinny GEMV (64-row tiles, quantize launch)
+    on weights of at most 4096 rows, the GEMM above 48 rows and on wider weights. Both
+    compute the canonical order, so every route gives the bits of quantize + dq_gemm;
+    sampled columns equal the oracle."""
+    import dqtorch as T
+
+    w_rows = weight_rows(O.Q4_K, n, k, 70 + m + k, edge=True)
+    x = activations(m, k, 71 + m)
+    w = dq.Weight.upload(O.Q4_K, w_rows, k)
+    xd = dev(x)
+    ym = host(T.matmul(w, xd))
+    ad = T.quantize(O.ACT_Q8_K, xd)
+    yg = host(T.gemm(w, O.ACT_Q8_K, ad))
+    assert np.array_equal(ym.view(np.uint32), yg.view(np.uint32))
+    cols = np.unique(np.concatenate([np.random.default_rng(m).choice(n, 64, replace=False), [0, n - 1]]))
+    want = O.matmul(O.Q4_K, O.ACT_Q8_K, w_rows[cols], O.quantize_act(O.ACT_Q8_K, x), k)
+    assert np.array_equal(ym[:, cols].view(np.uint32), want.view(np.uint32))
+
+
 def test_gemm_row_range_and_tails(cuda):
     import dqtorch as T
 
