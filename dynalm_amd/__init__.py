@@ -64,6 +64,14 @@ _I64 = C.c_int64
 _I = C.c_int
 
 # Every symbol include/dynaq.h declares, with its ctypes signature.
+class QmmActs(C.Structure):
+    """dq_qmm_acts: qmm::Acts (dynacore/include/dynacore/cpu/qmm.h:71-79), device pointers."""
+    _fields_ = [("mode", C.c_int32), ("paired", C.c_int32), ("m", C.c_int64), ("k", C.c_int64),
+                ("hi", C.c_void_p), ("lo", C.c_void_p), ("d", C.c_void_p), ("c", C.c_void_p)]
+
+
+QMM_INT8, QMM_INT16 = 0, 1  # dq_qmm_mode (qmm::ActMode)
+
 EXPORTS = {
     "dq_version": (C.c_char_p, []),
     "dq_last_error": (C.c_char_p, []),
@@ -76,6 +84,9 @@ EXPORTS = {
     "dq_weight_free": (_I, [_P]),
     "dq_weight_info": (_I, [_P, C.POINTER(_I), C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64)]),
     "dq_act_quantize": (_I, [_I, _P, _I64, _I64, _I64, _P, _P]),
+    "dq_qmm_act_bytes": (_I64, [_I, _I64, _I64, _I]),
+    "dq_qmm_act_prepare": (_I, [_P, _I64, _I, _I64, _I64, _I, C.POINTER(QmmActs), _P]),
+    "dq_qmm_quantize_rows": (_I, [_P, _I64, _I64, _I64, C.POINTER(QmmActs), _P]),
     "dq_gemv": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "dq_gemm": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "dq_matmul": (_I, [_P, _P, _I64, _I64, _P, _I64, _P, _P]),
@@ -211,6 +222,26 @@ class Weight:
 
 def act_quantize(fmt: int, x, m: int, k: int, x_stride: int, out, stream: int = 0) -> None:
     _check(lib().dq_act_quantize(fmt, _ptr(x), m, k, x_stride, _ptr(out), stream))
+
+
+def qmm_act_bytes(mode: int, m: int, k: int, paired: bool) -> int:
+    """Bytes of qmm's activation buffer for the shape (ActBuffer::prepare's layout)."""
+    n = lib().dq_qmm_act_bytes(mode, m, k, int(paired))
+    if n < 0:
+        raise DqError(3, f"qmm acts: mode {mode}, m {m}, k {k}")
+    return n
+
+
+def qmm_act_prepare(base, nbytes: int, mode: int, m: int, k: int, paired: bool, stream: int = 0) -> QmmActs:
+    """ActBuffer::prepare (qmm_reference.cpp:440-469) on a device buffer of nbytes."""
+    a = QmmActs()
+    _check(lib().dq_qmm_act_prepare(_ptr(base), nbytes, mode, m, k, int(paired), C.byref(a), stream))
+    return a
+
+
+def qmm_quantize_rows(x, x_stride: int, r0: int, r1: int, acts: QmmActs, stream: int = 0) -> None:
+    """ActBuffer::quantize_rows (qmm_reference.cpp:472-488): rows [r0, r1) of x."""
+    _check(lib().dq_qmm_quantize_rows(_ptr(x), x_stride, r0, r1, C.byref(acts), stream))
 
 
 def gemv(w: Weight, fmt: int, acts, m: int, n0: int, n1: int, y, y_stride: int, bias=None, stream: int = 0) -> None:

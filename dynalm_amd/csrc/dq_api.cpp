@@ -536,6 +536,65 @@ int dq_act_quantize(int fmt, const float* x, int64_t m, int64_t k, int64_t x_str
   return DQ_OK;
 }
 
+static int64_t qmm_align64(int64_t v) { return (v + 63) / 64 * 64; }
+
+int64_t dq_qmm_act_bytes(int mode, int64_t m, int64_t k, int paired) {
+  if ((mode != DQ_QMM_INT8 && mode != DQ_QMM_INT16) || m < 0 || k <= 0 || k % 32 != 0) return -1;
+  if (m > ((int64_t)1 << 24) || k > ((int64_t)1 << 30)) return -1;
+  const int64_t m_pad = paired ? (m + 1) / 2 * 2 : m;
+  const int64_t code = qmm_align64(m_pad * k), scale = qmm_align64(m_pad * (k / 32) * 4);
+  return code * (mode == DQ_QMM_INT16 ? 2 : 1) + 2 * scale;
+}
+
+int dq_qmm_act_prepare(void* base, int64_t bytes, int mode, int64_t m, int64_t k, int paired, dq_qmm_acts* out,
+                       void* stream) {
+  const int64_t need = dq_qmm_act_bytes(mode, m, k, paired);
+  if (need < 0) return fail(DQ_INVALID_ARGUMENT, "qmm acts: mode %d, m %lld, k %lld (k must be a positive multiple of 32)",
+                            mode, (long long)m, (long long)k);
+  if (base == nullptr || out == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
+  if (reinterpret_cast<uintptr_t>(base) % 64 != 0) return fail(DQ_INVALID_ARGUMENT, "qmm acts buffer must be 64-byte aligned");
+  if (bytes < need) return fail(DQ_INVALID_ARGUMENT, "qmm acts buffer of %lld bytes < %lld", (long long)bytes, (long long)need);
+  const int64_t m_pad = paired ? (m + 1) / 2 * 2 : m;
+  const int64_t code = qmm_align64(m_pad * k), lo_bytes = mode == DQ_QMM_INT16 ? code : 0;
+  const int64_t scale = qmm_align64(m_pad * (k / 32) * 4);
+  uint8_t* p = static_cast<uint8_t*>(base);
+  out->mode = mode;
+  out->paired = paired ? 1 : 0;
+  out->m = m;
+  out->k = k;
+  out->hi = reinterpret_cast<int8_t*>(p);
+  out->lo = mode == DQ_QMM_INT16 ? p + code : nullptr;
+  out->d = reinterpret_cast<float*>(p + code + lo_bytes);
+  out->c = reinterpret_cast<float*>(p + code + lo_bytes + scale);
+  if (paired && (m & 1)) {
+    DQ_HIP(dq::launch_qmm_pad(m, k, out->hi, out->lo, out->d, out->c, as_stream(stream)), "qmm pad launch");
+  }
+  return DQ_OK;
+}
+
+int dq_qmm_quantize_rows(const float* x, int64_t x_stride, int64_t r0, int64_t r1, const dq_qmm_acts* a, void* stream) {
+  if (a == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
+  if (dq_qmm_act_bytes(a->mode, a->m, a->k, a->paired) < 0 || a->hi == nullptr || a->d == nullptr || a->c == nullptr ||
+      (a->mode == DQ_QMM_INT16) != (a->lo != nullptr)) {
+    return fail(DQ_INVALID_ARGUMENT, "qmm acts not prepared");
+  }
+  if (r0 < 0 || r1 < r0 || r1 > a->m) {
+    return fail(DQ_INVALID_ARGUMENT, "rows [%lld, %lld) outside [0, %lld)", (long long)r0, (long long)r1, (long long)a->m);
+  }
+  if (r0 == r1) return DQ_OK;
+  if (x == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
+  if (r1 > 1 && x_stride < a->k) {
+    return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)a->k);
+  }
+  if (reinterpret_cast<uintptr_t>(a->hi) % 4 != 0 || (a->lo && reinterpret_cast<uintptr_t>(a->lo) % 4 != 0)) {
+    return fail(DQ_INVALID_ARGUMENT, "qmm acts codes must be 4-byte aligned");
+  }
+  DQ_HIP(dq::launch_qmm_quantize(x, x_stride, r0, r1, a->k, a->mode == DQ_QMM_INT16, a->paired != 0, a->hi, a->lo, a->d,
+                                 a->c, as_stream(stream)),
+         "qmm quantize launch");
+  return DQ_OK;
+}
+
 int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0, int64_t n1, float* y,
             int64_t y_stride, const float* bias, void* stream) {
   if (int rc = check_acts(w, fmt, acts, m); rc != DQ_OK) return rc;

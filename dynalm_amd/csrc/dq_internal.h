@@ -51,6 +51,12 @@ struct Workspace {
 
 hipError_t launch_quantize(int af, const float* x, int64_t m, int64_t k, int64_t x_stride, uint8_t* out, int64_t orb,
                            hipStream_t s);
+// qmm's activation buffer (dynacore/include/dynacore/cpu/qmm.h:57-86): rows [r0, r1) of x
+// into the row or pair layout, int8 or int16 codes; and the zero pad row of a paired
+// buffer of odd m.
+hipError_t launch_qmm_quantize(const float* x, int64_t x_stride, int64_t r0, int64_t r1, int64_t k, bool i16,
+                               bool paired, int8_t* hi, uint8_t* lo, float* d, float* c, hipStream_t s);
+hipError_t launch_qmm_pad(int64_t m, int64_t k, int8_t* hi, uint8_t* lo, float* d, float* c, hipStream_t s);
 hipError_t launch_repack(int t, const uint8_t* src, int64_t row_stride, int64_t n, int64_t nblk, uint8_t* const* planes,
                          hipStream_t s);
 hipError_t launch_unpack(int t, uint8_t* dst, int64_t row_stride, int64_t n, int64_t nblk, uint8_t* const* planes,

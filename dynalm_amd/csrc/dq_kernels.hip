@@ -256,6 +256,103 @@ hipError_t launch_quantize(int af, const float* x, int64_t m, int64_t k, int64_t
   return hipGetLastError();
 }
 
+// qmm's activation buffer (dynacore/include/dynacore/cpu/qmm.h:57-86), written by
+// quantize_row_ref (dynacore/cpu/qmm/qmm_reference.cpp:25-51) as ActBuffer::quantize_rows
+// lays it out (qmm_reference.cpp:472-488): per 32-value block d = amax / qmax
+// (qmax 127, or 32767 for the int16 mode), codes RNE of the clamped x * (1 / d), and
+// c = d * (float)(code sum). Code i of a block goes to chunk 4 b + i / 8, byte i % 8,
+// chunks cs bytes apart (row layout: 8, row r at hi + r k; pair layout: 16, row r at
+// hi + (r / 2) 2 k + 8 (r & 1)); scales ds floats apart (1, or 2 interleaving a pair).
+// The int16 mode stores q = 256 hi + lo (hi the arithmetic shift, lo the low byte).
+// Thread (row, block, quad): four values, the block's amax and sum across its 8 lanes.
+template <bool kI16>
+__global__ __launch_bounds__(256) void k_qmm_quant(const float* __restrict__ x, int64_t x_stride, int64_t r0,
+                                                   int64_t rows, int64_t k, int paired, int8_t* __restrict__ hi,
+                                                   uint8_t* __restrict__ lo, float* __restrict__ d,
+                                                   float* __restrict__ c) {
+  const int64_t kb = k / 32;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const bool live = t < rows * kb * 8;  // dead lanes still take part in the shuffles
+  const int64_t tt = live ? t : 0;
+  const int64_t r = r0 + tt / (kb * 8);
+  const int64_t b = (tt / 8) % kb;
+  const int q4 = (int)(tt & 7);
+  const float* xp = x + r * x_stride + b * 32 + 4 * q4;
+  const float v[4] = {xp[0], xp[1], xp[2], xp[3]};
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  amax = fmaxf(amax, __shfl_xor(amax, 4));
+  constexpr float qmax = kI16 ? 32767.0f : 127.0f;
+  const float db = amax / qmax;
+  const float id = db > 0 ? 1.0f / db : 0.0f;
+  int sum = 0;
+  u32 whi = 0, wlo = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float s = v[e] * id;
+    s = s > -qmax ? (s < qmax ? s : qmax) : -qmax;  // NaN -> -qmax, as the reference's clamp
+    const int q = (int)__builtin_rintf(s);
+    sum += q;
+    if (kI16) {
+      whi |= ((u32)(q >> 8) & 0xFFu) << (8 * e);
+      wlo |= ((u32)q & 0xFFu) << (8 * e);
+    } else {
+      whi |= ((u32)q & 0xFFu) << (8 * e);
+    }
+  }
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  sum += __shfl_xor(sum, 4);
+  if (!live) return;
+  const int64_t rowoff = paired ? (r / 2) * 2 * k + 8 * (r & 1) : r * k;
+  const int64_t cs = paired ? 16 : 8;
+  const int64_t at = rowoff + (4 * b + q4 / 2) * cs + 4 * (q4 & 1);
+  *reinterpret_cast<u32*>(hi + at) = whi;
+  if (kI16) *reinterpret_cast<u32*>(lo + at) = wlo;
+  if (q4 == 0) {
+    const int64_t so = paired ? ((r / 2) * kb + b) * 2 + (r & 1) : r * kb + b;
+    d[so] = db;
+    c[so] = db * (float)sum;
+  }
+}
+
+// The pad row of a paired buffer with odd m (row m of the last pair): zero codes and
+// scales, as ActBuffer::prepare writes them (qmm_reference.cpp:455-469).
+__global__ __launch_bounds__(256) void k_qmm_pad(int64_t m, int64_t k, int8_t* __restrict__ hi,
+                                                 uint8_t* __restrict__ lo, float* __restrict__ d,
+                                                 float* __restrict__ c) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t kb = k / 32, base = (m / 2) * 2 * k;
+  if (t < k / 8) {
+    *reinterpret_cast<uint2*>(hi + base + t * 16 + 8) = uint2{0u, 0u};
+    if (lo) *reinterpret_cast<uint2*>(lo + base + t * 16 + 8) = uint2{0u, 0u};
+  }
+  if (t < kb) {
+    const int64_t so = ((m / 2) * kb + t) * 2 + 1;
+    d[so] = 0.0f;
+    c[so] = 0.0f;
+  }
+}
+
+hipError_t launch_qmm_quantize(const float* x, int64_t x_stride, int64_t r0, int64_t r1, int64_t k, bool i16,
+                               bool paired, int8_t* hi, uint8_t* lo, float* d, float* c, hipStream_t s) {
+  const int64_t rows = r1 - r0;
+  if (rows <= 0 || k <= 0) return hipSuccess;
+  const dim3 g = grid1(rows * (k / 32) * 8, 256);
+  if (i16) {
+    hipLaunchKernelGGL(k_qmm_quant<true>, g, dim3(256), 0, s, x, x_stride, r0, rows, k, paired ? 1 : 0, hi, lo, d, c);
+  } else {
+    hipLaunchKernelGGL(k_qmm_quant<false>, g, dim3(256), 0, s, x, x_stride, r0, rows, k, paired ? 1 : 0, hi, lo, d, c);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_qmm_pad(int64_t m, int64_t k, int8_t* hi, uint8_t* lo, float* d, float* c, hipStream_t s) {
+  hipLaunchKernelGGL(k_qmm_pad, grid1(k / 8, 256), dim3(256), 0, s, m, k, hi, lo, d, c);
+  return hipGetLastError();
+}
+
 hipError_t launch_repack(int t, const uint8_t* src, int64_t row_stride, int64_t n, int64_t nblk, uint8_t* const* planes,
                          hipStream_t s) {
   Planes pl{};

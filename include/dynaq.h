@@ -146,6 +146,40 @@ DQ_API int dq_weight_info(const dq_weight* w, int* dtype, int64_t* n, int64_t* k
  * (dynacore/include/dynacore/cpu/qmm.h:122-123); bit-identical results. */
 DQ_API int dq_act_quantize(int fmt, const float* x, int64_t m, int64_t k, int64_t x_stride, void* out, void* stream);
 
+/* qmm's activation buffer: m rows of k values (k % 32 == 0) quantized per 32-value
+ * block to int8 or int16 codes with d = amax / qmax and c = d * (code sum), in the row
+ * layout (gemv) or the pair-interleaved layout (gemm; rows 2p and 2p + 1 in 8-byte
+ * chunks, scales interleaved). Replaces qmm::ActBuffer (dynacore/include/dynacore/cpu/
+ * qmm.h:57-93) and its tier's quantize_row (qmm.h:122-123; the reference tier,
+ * dynacore/cpu/qmm/qmm_reference.cpp:25-51); bit-identical bytes. */
+typedef enum dq_qmm_mode { /* qmm::ActMode (qmm.h:46) */
+  DQ_QMM_INT8 = 0,
+  DQ_QMM_INT16 = 1 /* q = 256 * hi + lo */
+} dq_qmm_mode;
+/* qmm::Acts (qmm.h:71-79); the pointers are device memory inside one buffer. */
+typedef struct dq_qmm_acts {
+  int32_t mode;
+  int32_t paired;
+  int64_t m, k;
+  int8_t* hi;
+  uint8_t* lo; /* DQ_QMM_INT16 only, else NULL */
+  float* d;
+  float* c;
+} dq_qmm_acts;
+/* Bytes ActBuffer::prepare lays out for the shape (qmm_reference.cpp:440-454): codes,
+ * low bytes (int16), d and c, each region rounded up to 64 bytes; -1 if invalid. */
+DQ_API int64_t dq_qmm_act_bytes(int mode, int64_t m, int64_t k, int paired);
+/* ActBuffer::prepare on a caller's device buffer (64-byte aligned, at least
+ * dq_qmm_act_bytes): fills *out and, for a paired buffer of odd m, zeroes the pad
+ * row's codes and scales on `stream` (qmm_reference.cpp:455-469). */
+DQ_API int dq_qmm_act_prepare(void* base, int64_t bytes, int mode, int64_t m, int64_t k, int paired,
+                              dq_qmm_acts* out, void* stream);
+/* ActBuffer::quantize_rows (qmm_reference.cpp:472-488): rows [r0, r1) of x (row r at
+ * x + r * x_stride floats, device memory) into a prepared buffer. Disjoint row
+ * ranges may be quantized by separate calls. */
+DQ_API int dq_qmm_quantize_rows(const float* x, int64_t x_stride, int64_t r0, int64_t r1, const dq_qmm_acts* a,
+                                void* stream);
+
 /* y[r * y_stride + i] = dot(weight row i, activation row r) + (bias ? bias[i] : 0)
  * for r < m and i in [n0, n1). `acts`: m rows in format fmt, as dq_act_quantize
  * writes them. Replaces qmm::Kernels::gemv (dynacore/include/dynacore/cpu/qmm.h:125-126)

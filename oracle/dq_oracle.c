@@ -1004,3 +1004,69 @@ int dqo_activation(int act, const float* x, float* y, int64_t n) {
   for (int64_t i = 0; i < n; ++i) y[i] = act1(act, x[i]);
   return 0;
 }
+
+/* ------------------------------------------------- qmm activation buffer */
+
+/* One row of qmm activations: quantize_row_ref, dynacore/cpu/qmm/qmm_reference.cpp:25-51.
+   Per 32-value block: amax (NaN ignored, as std::max(amax, |x|) keeps amax), d = amax / qmax,
+   id = 1 / d (0 for d == 0), code = nearbyint(clamp(x * id, -qmax, qmax)) with NaN going to
+   -qmax, c = d * (float)(code sum). Code i of block b at chunk 4 b + i / 8, byte i % 8,
+   chunks cs bytes apart; int16 stores q >> 8 in hi and q & 0xFF in lo. */
+static void qmm_row(const float* x, int64_t k, int mode, int8_t* hi, uint8_t* lo, int64_t cs, float* d, float* c,
+                    int64_t ds) {
+  const float qmax = mode == 0 ? 127.0f : 32767.0f;
+  for (int64_t b = 0; b < k / 32; ++b, x += 32) {
+    float amax = 0.0f;
+    for (int i = 0; i < 32; ++i) {
+      const float a = fabsf(x[i]);
+      if (amax < a) amax = a;
+    }
+    const float db = amax / qmax;
+    const float id = db > 0 ? 1.0f / db : 0.0f;
+    int32_t sum = 0;
+    for (int i = 0; i < 32; ++i) {
+      float v = x[i] * id;
+      v = v > -qmax ? (v < qmax ? v : qmax) : -qmax;
+      const int32_t q = (int32_t)nearbyintf(v);
+      sum += q;
+      const int64_t at = (b * 4 + i / 8) * cs + i % 8;
+      if (mode == 0) {
+        hi[at] = (int8_t)q;
+      } else {
+        hi[at] = (int8_t)(q >> 8);
+        lo[at] = (uint8_t)(q & 0xFF);
+      }
+    }
+    d[b * ds] = db;
+    c[b * ds] = db * (float)sum;
+  }
+}
+
+/* All m rows into the layout of ActBuffer::prepare / quantize_rows (qmm_reference.cpp:440-488;
+   dynacore/include/dynacore/cpu/qmm.h:57-70): row layout codes at hi + r k, scales at r kb;
+   pair layout (paired != 0) rows 2p, 2p + 1 interleaved in 8-byte chunks at hi + p 2k + 16 j
+   (+ 8 for the odd row), scales at (p kb + b) 2 + (r & 1), an odd m padded with a zero row.
+   hi / lo hold m_pad k bytes, d / c m_pad k / 32 floats (m_pad = m rounded up to even when
+   paired). Returns -1 on a bad shape. */
+int dqo_qmm_quantize(const float* x, int64_t x_stride, int64_t m, int64_t k, int mode, int paired, int8_t* hi,
+                     uint8_t* lo, float* d, float* c) {
+  if ((mode != 0 && mode != 1) || m < 0 || k <= 0 || k % 32 != 0 || (mode == 1 && lo == NULL)) return -1;
+  const int64_t kb = k / 32;
+  for (int64_t r = 0; r < m; ++r) {
+    const float* xr = x + r * x_stride;
+    if (paired) {
+      const int64_t off = (r / 2) * 2 * k + (r & 1) * 8, so = (r / 2) * kb * 2 + (r & 1);
+      qmm_row(xr, k, mode, hi + off, mode ? lo + off : NULL, 16, d + so, c + so, 2);
+    } else {
+      qmm_row(xr, k, mode, hi + r * k, mode ? lo + r * k : NULL, 8, d + r * kb, c + r * kb, 1);
+    }
+  }
+  if (paired && (m & 1)) {
+    for (int64_t j = 0; j < k / 8; ++j) {
+      memset(hi + (m / 2) * 2 * k + j * 16 + 8, 0, 8);
+      if (mode) memset(lo + (m / 2) * 2 * k + j * 16 + 8, 0, 8);
+    }
+    for (int64_t b = 0; b < kb; ++b) d[((m / 2) * kb + b) * 2 + 1] = c[((m / 2) * kb + b) * 2 + 1] = 0.0f;
+  }
+  return 0;
+}

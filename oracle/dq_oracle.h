@@ -93,6 +93,10 @@ int dqo_dequantize_act(int fmt, const void* a, float* y, int64_t n);
 int dqo_quantize_act(int fmt, const float* x, void* out, int64_t n);
 /* Quantize m rows (row stride x_stride floats) into consecutive quantized rows. */
 int dqo_quantize_act_rows(int fmt, const float* x, int64_t m, int64_t n, int64_t x_stride, void* out);
+/* qmm's activation buffer (dynacore/cpu/qmm/qmm_reference.cpp:25-51,440-488): m rows, int8
+   (mode 0) or int16 (mode 1) codes, row or pair layout, d and c = d * code sum per block. */
+int dqo_qmm_quantize(const float* x, int64_t x_stride, int64_t m, int64_t k, int mode, int paired, int8_t* hi,
+                     uint8_t* lo, float* d, float* c);
 
 /* Encode one fp32 row of n values as GGUF blocks of dtype (Q8_0: the reference
  * quantize_q8_0; Q4_0 / Q4_K / Q6_K: this file's own deterministic encoders). */

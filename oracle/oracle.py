@@ -48,6 +48,7 @@ def _load_oracle():
         "dqo_dequantize_act": (C.c_int, [C.c_int, _P, _P, _I64]),
         "dqo_quantize_act": (C.c_int, [C.c_int, _P, _P, _I64]),
         "dqo_quantize_act_rows": (C.c_int, [C.c_int, _P, _I64, _I64, _I64, _P]),
+        "dqo_qmm_quantize": (C.c_int, [_P, _I64, _I64, _I64, C.c_int, C.c_int, _P, _P, _P, _P]),
         "dqo_encode_weight": (C.c_int, [C.c_int, _P, _P, _I64]),
         "dqo_encode_weight_rows": (C.c_int, [C.c_int, _P, _I64, _I64, _P]),
         "dqo_partials_count": (C.c_int, [C.c_int, C.c_int, _I64, C.POINTER(_I64), C.POINTER(_I64)]),
@@ -275,6 +276,7 @@ def ref():
             "ref_select_matmul": (C.c_int, [_I64, _I64, _I64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                             C.c_int, C.c_int, C.c_uint32, C.POINTER(C.c_int)]),
             "ref_expand_x86": (C.c_int, [C.c_int, _P, _P, _I64]),
+            "ref_qmm_quantize": (C.c_int, [_P, _I64, _I64, _I64, C.c_int, C.c_int, _P, _P, _P, _P]),
             "ref_bench_decode_sx": (_I64, [C.c_int, C.POINTER(_P), C.c_int, _I64, _I64, _P, C.c_int, _I64, _P,
                                            C.c_int, C.c_int, C.c_int]),
             "ref_llc_bytes": (_I64, []),
@@ -386,3 +388,33 @@ def ref_vec_dot(tier: int, dtype: int, w_row: np.ndarray, x: np.ndarray, k: int)
     out = np.empty(1, np.float32)
     _check(r.ref_vec_dot(tier, dtype, _ptr(w_row), _ptr(x), k, _ptr(out)), "ref_vec_dot")
     return float(out[0])
+
+
+def _qmm_out(m: int, k: int, mode: int, paired: bool):
+    m_pad = (m + 1) // 2 * 2 if paired else m
+    hi = np.zeros(m_pad * k, np.int8)
+    lo = np.zeros(m_pad * k, np.uint8) if mode == 1 else None
+    d = np.zeros(m_pad * (k // 32), np.float32)
+    c = np.zeros(m_pad * (k // 32), np.float32)
+    return hi, lo, d, c
+
+
+def qmm_quantize(x: np.ndarray, mode: int, paired: bool):
+    """qmm's activation buffer for the rows of x (dynacore/cpu/qmm/qmm_reference.cpp:25-51,
+    440-488): (hi, lo or None, d, c) as flat arrays in the row or pair layout."""
+    x = np.ascontiguousarray(x, np.float32)
+    m, k = x.shape
+    hi, lo, d, c = _qmm_out(m, k, mode, paired)
+    _check(lib().dqo_qmm_quantize(_ptr(x), k, m, k, mode, int(paired), _ptr(hi), _ptr(lo) if lo is not None else None,
+                                  _ptr(d), _ptr(c)), "qmm_quantize")
+    return hi, lo, d, c
+
+
+def ref_qmm_quantize(x: np.ndarray, mode: int, paired: bool):
+    """The same buffer from the reference's own ActBuffer and reference tier (oracle/_ref)."""
+    x = np.ascontiguousarray(x, np.float32)
+    m, k = x.shape
+    hi, lo, d, c = _qmm_out(m, k, mode, paired)
+    _check(ref().ref_qmm_quantize(_ptr(x), k, m, k, mode, int(paired), _ptr(hi), _ptr(lo) if lo is not None else None,
+                                  _ptr(d), _ptr(c)), "ref_qmm_quantize")
+    return hi, lo, d, c

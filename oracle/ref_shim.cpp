@@ -28,6 +28,7 @@
 
 #include "dynacore/base/fast_exp.h"
 #include "dynacore/cpu/cpu_kernels.h"
+#include "dynacore/cpu/qmm.h"
 #include "dynacore/execution/thread_pool.h"
 #include "dynacore/hardware/cpu_info.h"
 #include "dynacore/kernel/kernel_plan.h"
@@ -329,6 +330,25 @@ int ref_expand_gemm(int dtype, const void* w, int64_t w_row_bytes, int64_t n, co
     for (int r = 0; r < nr; ++r) f(static_cast<const uint8_t*>(w) + (j0 + r) * w_row_bytes, panel.data() + r * k, k);
     kt.gemm_panel(panel.data(), nr, x, k, m, k, y + j0, n, false);
   }
+  return 0;
+}
+
+// qmm's ActBuffer as the reference lays it out and fills it with its reference tier
+// (dynacore/cpu/qmm/qmm_reference.cpp:25-51,440-488), copied out: hi / lo m_pad * k bytes,
+// d / c m_pad * k / 32 floats (m_pad = m rounded up to even for the pair layout).
+int ref_qmm_quantize(const float* x, int64_t x_stride, int64_t m, int64_t k, int mode, int paired, int8_t* hi,
+                     uint8_t* lo, float* d, float* c) {
+  if ((mode != 0 && mode != 1) || m < 0 || k <= 0 || k % 32 != 0) return -1;
+  const auto am = mode == 0 ? dynacore::qmm::ActMode::kInt8 : dynacore::qmm::ActMode::kInt16;
+  dynacore::qmm::ActBuffer buf;
+  buf.prepare(am, m, k, paired != 0);
+  buf.quantize_rows(x, x_stride, 0, m, dynacore::qmm::reference_kernels());
+  const dynacore::qmm::Acts& a = buf.acts();
+  const int64_t m_pad = paired ? (m + 1) / 2 * 2 : m;
+  std::memcpy(hi, a.hi, static_cast<size_t>(m_pad * k));
+  if (mode == 1) std::memcpy(lo, a.lo, static_cast<size_t>(m_pad * k));
+  std::memcpy(d, a.d, static_cast<size_t>(m_pad * (k / 32)) * sizeof(float));
+  std::memcpy(c, a.c, static_cast<size_t>(m_pad * (k / 32)) * sizeof(float));
   return 0;
 }
 

@@ -139,3 +139,29 @@ def test_gated_validation_without_gpu():
     assert lib.dq_matmul_gated(7, None, 1, 0, None, None, None, 0, None, None, 0, None) == 1
     assert lib.dq_matmul_gated(dq.SILU, None, 1, 0, None, None, None, 0, None, None, 0, None) == 1
     assert b"null weight" in lib.dq_last_error()
+
+
+def test_qmm_buffer_layout_and_validation_without_gpu():
+    """ActBuffer::prepare's layout (qmm_reference.cpp:440-454): codes, low bytes (int16), d and
+    c, each rounded up to 64 bytes, pairs padded to an even row count; bad shapes, buffers and
+    row ranges are rejected before any GPU call."""
+    import ctypes as C
+
+    assert dq.qmm_act_bytes(dq.QMM_INT8, 3, 64, False) == 192 + 2 * 64
+    assert dq.qmm_act_bytes(dq.QMM_INT8, 3, 64, True) == 256 + 2 * 64
+    assert dq.qmm_act_bytes(dq.QMM_INT16, 2, 4096, True) == 2 * 8192 + 2 * 1024
+    for bad in [(2, 1, 32, 0), (0, 1, 48, 0), (0, -1, 32, 0), (0, 1, 0, 0)]:
+        assert dq.lib().dq_qmm_act_bytes(*bad) == -1
+    a = dq.qmm_act_prepare(1 << 20, dq.qmm_act_bytes(dq.QMM_INT16, 4, 256, True), dq.QMM_INT16, 4, 256, True)
+    assert (a.hi, a.lo, a.d, a.c) == (1 << 20, (1 << 20) + 1024, (1 << 20) + 2048, (1 << 20) + 2048 + 128)
+    with pytest.raises(dq.DqError):
+        dq.qmm_act_prepare((1 << 20) + 32, 1 << 16, dq.QMM_INT8, 4, 256, False)  # misaligned
+    with pytest.raises(dq.DqError):
+        dq.qmm_act_prepare(1 << 20, 100, dq.QMM_INT8, 4, 256, False)  # too small
+    with pytest.raises(dq.DqError):
+        dq.qmm_quantize_rows(1 << 24, 256, 2, 5, a)  # rows past m
+    with pytest.raises(dq.DqError):
+        dq.qmm_quantize_rows(1 << 24, 128, 0, 2, a)  # x_stride < k
+    with pytest.raises(dq.DqError):
+        dq.qmm_quantize_rows(1 << 24, 256, 0, 2, dq.QmmActs())  # not prepared
+    assert dq.lib().dq_qmm_quantize_rows(None, 256, 1, 1, C.byref(a), None) == 0  # empty range: no launch

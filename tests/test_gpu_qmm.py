@@ -1,0 +1,88 @@
+"""qmm's activation buffer on the GPU (dq_qmm_act_prepare / dq_qmm_quantize_rows) against
+the oracle's restatement of ActBuffer + quantize_row_ref (dynacore/cpu/qmm/qmm_reference.cpp:
+25-51,440-488), byte for byte; the oracle is pinned to the reference build in test_oracle.py.
+Cases follow dynacore/tests/test_qmm.cpp's: both modes and layouts, odd m (pad row), split
+row ranges, strided rows, and NaN / Inf / zero / tie inputs."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import dynalm_amd as dq
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def rows(m: int, k: int, seed: int) -> np.ndarray:
+    x = (np.random.default_rng(seed).standard_normal((m, k)) * 3).astype(np.float32)
+    x[0, 3] = np.nan
+    x[m - 1, min(40, k - 1)] = np.inf
+    if k >= 128:
+        x[0, 64:96] = 0.0
+        x[0, 96:128] = -0.0
+        x[m - 1, 0] = -np.inf
+    if k >= 64:
+        x[m - 1, 32] = 127.0
+        x[m - 1, 33:64] = np.float32(0.5) + np.arange(31, dtype=np.float32)
+    return x
+
+
+def run_gpu(x: np.ndarray, mode: int, paired: bool, x_stride: int | None = None, splits=()):
+    """Quantize the rows of x on the GPU (over the row ranges cut at `splits`); return the
+    buffer's regions as the oracle returns them."""
+    m, k = x.shape
+    xs = x_stride or k
+    xp = np.zeros((m, xs), np.float32)
+    xp[:, :k] = x
+    xd = torch.from_numpy(xp).cuda()
+    nbytes = dq.qmm_act_bytes(mode, m, k, paired)
+    buf = torch.full((nbytes,), 0xAB, dtype=torch.uint8, device="cuda")  # stale contents
+    st = torch.cuda.current_stream().cuda_stream
+    a = dq.qmm_act_prepare(buf, nbytes, mode, m, k, paired, st)
+    cuts = [0, *splits, m]
+    for r0, r1 in zip(cuts[:-1], cuts[1:]):
+        dq.qmm_quantize_rows(xd, xs, r0, r1, a, st)
+    torch.cuda.synchronize()
+    h = buf.cpu().numpy()
+    base = buf.data_ptr()
+    m_pad = (m + 1) // 2 * 2 if paired else m
+    ncode, nsc = m_pad * k, m_pad * (k // 32)
+    hi = h[a.hi - base:a.hi - base + ncode].view(np.int8)
+    lo = h[a.lo - base:a.lo - base + ncode] if mode == 1 else None
+    d = h[a.d - base:a.d - base + 4 * nsc].view(np.float32)
+    c = h[a.c - base:a.c - base + 4 * nsc].view(np.float32)
+    return hi, lo, d, c
+
+
+def same(got, want):
+    for g, w in zip(got, want):
+        assert (g is None) == (w is None)
+        if g is not None:
+            assert g.tobytes() == w.tobytes()
+
+
+@pytest.mark.parametrize("mode", [dq.QMM_INT8, dq.QMM_INT16])
+@pytest.mark.parametrize("paired", [False, True])
+@pytest.mark.parametrize("m,k", [(1, 32), (2, 256), (7, 1536), (16, 4096)])
+def test_qmm_quantize_bit_exact(cuda, mode, paired, m, k):
+    x = rows(m, k, 3 * m + k)
+    same(run_gpu(x, mode, paired), O.qmm_quantize(x, mode, paired))
+
+
+@pytest.mark.parametrize("mode", [dq.QMM_INT8, dq.QMM_INT16])
+@pytest.mark.parametrize("paired", [False, True])
+def test_qmm_quantize_split_rows_and_stride(cuda, mode, paired):
+    """Row ranges quantized by separate calls (odd cut points, so a pair is written by two
+    calls) and rows x_stride > k floats apart give the one-call bytes."""
+    x = rows(9, 512, 17)
+    want = O.qmm_quantize(x, mode, paired)
+    same(run_gpu(x, mode, paired, x_stride=544, splits=(3, 4, 7)), want)
+
+
+@pytest.mark.parametrize("mode", [dq.QMM_INT8, dq.QMM_INT16])
+def test_qmm_quantize_prefill_shape(cuda, mode):
+    """Config 4's prefill activations (512 rows of 4096) in the gemm's pair layout."""
+    x = np.random.default_rng(4).standard_normal((512, 4096)).astype(np.float32)
+    same(run_gpu(x, mode, True), O.qmm_quantize(x, mode, True))

@@ -611,3 +611,80 @@ def test_subscaled_s_exceeds_int32():
     y = O.matmul(O.Q4_K, O.ACT_SX, w, a, k)
     ref = float(O.dequantize_act(O.ACT_SX, a, k).astype(np.float64) @ O.dequantize(O.Q4_K, w[0], k).ravel())
     assert abs(float(y[0, 0]) - ref) <= 1e-6 * abs(ref)
+
+
+# ---------------------------------------------------------------- qmm activation buffer
+
+def _qmm_rows(m: int, k: int, seed: int) -> np.ndarray:
+    """Rows of N(0, 3) with the cases the reference's clamp and rounding decide: NaN, +-Inf,
+    all-zero and negative-zero blocks, half-way codes, a block whose amax is exactly qmax."""
+    x = (np.random.default_rng(seed).standard_normal((m, k)) * 3).astype(np.float32)
+    x[0, 3] = np.nan
+    x[m - 1, min(40, k - 1)] = np.inf
+    if k >= 128:
+        x[0, 64:96] = 0.0
+        x[0, 96:128] = -0.0
+        x[m - 1, 0] = -np.inf
+    if k >= 64:
+        x[m - 1, 32] = 127.0
+        x[m - 1, 33:64] = np.float32(0.5) + np.arange(31, dtype=np.float32)  # codes at exact .5 ties
+    return x
+
+
+@needs_ref
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("paired", [False, True])
+@pytest.mark.parametrize("m,k", [(1, 32), (2, 256), (3, 1536), (8, 4096)])
+def test_qmm_quantize_matches_reference(mode, paired, m, k):
+    """The oracle's qmm buffer is byte-identical to the reference's own ActBuffer filled by
+    its reference tier (dynacore/cpu/qmm/qmm_reference.cpp:25-51,440-488, built in oracle/_ref)."""
+    x = _qmm_rows(m, k, 11 * m + k)
+    got, want = O.qmm_quantize(x, mode, paired), O.ref_qmm_quantize(x, mode, paired)
+    for g, w in zip(got, want):
+        assert (g is None) == (w is None)
+        if g is not None:
+            assert g.tobytes() == w.tobytes()
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_qmm_quantize_layouts_and_scales(mode):
+    """Without the reference: the pair layout is the row layout interleaved in 8-byte chunks
+    (qmm.h:63-66), the pad row of an odd m is zero, c = d * (code sum) per block, codes stay
+    within +-qmax and a block's largest |x| maps to +-qmax."""
+    m, k = 5, 512
+    x = (np.random.default_rng(5).standard_normal((m, k)) * 2).astype(np.float32)
+    hi_r, lo_r, d_r, c_r = O.qmm_quantize(x, mode, False)
+    hi_p, lo_p, d_p, c_p = O.qmm_quantize(x, mode, True)
+    kb, qmax = k // 32, (127 if mode == 0 else 32767)
+    q = hi_r.astype(np.int32) if mode == 0 else hi_r.astype(np.int32) * 256 + lo_r.astype(np.int32)
+    q = q.reshape(m, k)
+    assert np.abs(q).max() <= qmax
+    sums = q.reshape(m, kb, 32).sum(axis=2)
+    np.testing.assert_array_equal(c_r.reshape(m, kb), (d_r.reshape(m, kb) * sums.astype(np.float32)).astype(np.float32))
+    big = np.abs(x.reshape(m, kb, 32)).argmax(axis=2)
+    assert (np.abs(np.take_along_axis(q.reshape(m, kb, 32), big[..., None], 2)) == qmax).all()
+    m_pad = m + 1
+    inter = np.zeros((m_pad // 2, k // 8, 2, 8), np.int8)
+    rows = np.zeros((m_pad, k), np.int8)
+    rows[:m] = hi_r.reshape(m, k)
+    inter[:, :, 0] = rows[0::2].reshape(m_pad // 2, k // 8, 8)
+    inter[:, :, 1] = rows[1::2].reshape(m_pad // 2, k // 8, 8)
+    assert hi_p.tobytes() == inter.tobytes()
+    dd = np.zeros((m_pad, kb), np.float32)
+    dd[:m] = d_r.reshape(m, kb)
+    np.testing.assert_array_equal(d_p.reshape(m_pad // 2, kb, 2), np.stack([dd[0::2], dd[1::2]], axis=2))
+
+
+def test_qmm_quantize_golden():
+    """The oracle against the committed reference buffers (tests/golden/make_qmm_golden.py):
+    both modes and layouts, 3 rows (a pad row when paired), NaN / Inf / zero / tie inputs."""
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "qmm_vectors.npz"))
+    for mode in (0, 1):
+        for paired in (0, 1):
+            key = f"m{mode}p{paired}"
+            hi, lo, d, c = O.qmm_quantize(g["x"], mode, bool(paired))
+            assert hi.tobytes() == g[f"{key}_hi"].tobytes()
+            assert d.tobytes() == g[f"{key}_d"].tobytes() and c.tobytes() == g[f"{key}_c"].tobytes()
+            assert (lo is None) == (mode == 0)
+            if lo is not None:
+                assert lo.tobytes() == g[f"{key}_lo"].tobytes()
