@@ -87,6 +87,8 @@ EXPORTS = {
     "dq_qmm_act_bytes": (_I64, [_I, _I64, _I64, _I]),
     "dq_qmm_act_prepare": (_I, [_P, _I64, _I, _I64, _I64, _I, C.POINTER(QmmActs), _P]),
     "dq_qmm_quantize_rows": (_I, [_P, _I64, _I64, _I64, C.POINTER(QmmActs), _P]),
+    "dq_qmm_gemv": (_I, [_P, _I64, _I64, C.POINTER(QmmActs), _I64, _I, _P, _I64, _P, _P]),
+    "dq_qmm_gemm": (_I, [_P, _I64, _I64, C.POINTER(QmmActs), _P, _I64, _P, _P]),
     "dq_gemv": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "dq_gemm": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "dq_matmul": (_I, [_P, _P, _I64, _I64, _P, _I64, _P, _P]),
@@ -242,6 +244,17 @@ def qmm_act_prepare(base, nbytes: int, mode: int, m: int, k: int, paired: bool, 
 def qmm_quantize_rows(x, x_stride: int, r0: int, r1: int, acts: QmmActs, stream: int = 0) -> None:
     """ActBuffer::quantize_rows (qmm_reference.cpp:472-488): rows [r0, r1) of x."""
     _check(lib().dq_qmm_quantize_rows(_ptr(x), x_stride, r0, r1, C.byref(acts), stream))
+
+
+def qmm_gemv(w: Weight, n0: int, n1: int, acts: QmmActs, r0: int, rows: int, y, y_stride: int, bias=None,
+             stream: int = 0) -> None:
+    """qmm::Kernels::gemv on a qmm activation buffer (rows [r0, r0 + rows))."""
+    _check(lib().dq_qmm_gemv(w.handle, n0, n1, C.byref(acts), r0, rows, _ptr(y), y_stride, _ptr(bias), stream))
+
+
+def qmm_gemm(w: Weight, n0: int, n1: int, acts: QmmActs, y, y_stride: int, bias=None, stream: int = 0) -> None:
+    """qmm::Kernels::gemm on a qmm activation buffer (every row)."""
+    _check(lib().dq_qmm_gemm(w.handle, n0, n1, C.byref(acts), _ptr(y), y_stride, _ptr(bias), stream))
 
 
 def gemv(w: Weight, fmt: int, acts, m: int, n0: int, n1: int, y, y_stride: int, bias=None, stream: int = 0) -> None:

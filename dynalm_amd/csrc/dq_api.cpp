@@ -536,6 +536,18 @@ int dq_act_quantize(int fmt, const float* x, int64_t m, int64_t k, int64_t x_str
   return DQ_OK;
 }
 
+static int qmm_acts_ok(const dq_qmm_acts* a) {
+  if (a == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
+  if (dq_qmm_act_bytes(a->mode, a->m, a->k, a->paired) < 0 || a->hi == nullptr || a->d == nullptr || a->c == nullptr ||
+      (a->mode == DQ_QMM_INT16) != (a->lo != nullptr)) {
+    return fail(DQ_INVALID_ARGUMENT, "qmm acts not prepared");
+  }
+  if (reinterpret_cast<uintptr_t>(a->hi) % 4 != 0 || (a->lo && reinterpret_cast<uintptr_t>(a->lo) % 4 != 0)) {
+    return fail(DQ_INVALID_ARGUMENT, "qmm acts codes must be 4-byte aligned");
+  }
+  return DQ_OK;
+}
+
 static int64_t qmm_align64(int64_t v) { return (v + 63) / 64 * 64; }
 
 int64_t dq_qmm_act_bytes(int mode, int64_t m, int64_t k, int paired) {
@@ -573,11 +585,7 @@ int dq_qmm_act_prepare(void* base, int64_t bytes, int mode, int64_t m, int64_t k
 }
 
 int dq_qmm_quantize_rows(const float* x, int64_t x_stride, int64_t r0, int64_t r1, const dq_qmm_acts* a, void* stream) {
-  if (a == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
-  if (dq_qmm_act_bytes(a->mode, a->m, a->k, a->paired) < 0 || a->hi == nullptr || a->d == nullptr || a->c == nullptr ||
-      (a->mode == DQ_QMM_INT16) != (a->lo != nullptr)) {
-    return fail(DQ_INVALID_ARGUMENT, "qmm acts not prepared");
-  }
+  if (int rc = qmm_acts_ok(a); rc != DQ_OK) return rc;
   if (r0 < 0 || r1 < r0 || r1 > a->m) {
     return fail(DQ_INVALID_ARGUMENT, "rows [%lld, %lld) outside [0, %lld)", (long long)r0, (long long)r1, (long long)a->m);
   }
@@ -586,13 +594,49 @@ int dq_qmm_quantize_rows(const float* x, int64_t x_stride, int64_t r0, int64_t r
   if (r1 > 1 && x_stride < a->k) {
     return fail(DQ_INVALID_ARGUMENT, "x_stride %lld < k %lld", (long long)x_stride, (long long)a->k);
   }
-  if (reinterpret_cast<uintptr_t>(a->hi) % 4 != 0 || (a->lo && reinterpret_cast<uintptr_t>(a->lo) % 4 != 0)) {
-    return fail(DQ_INVALID_ARGUMENT, "qmm acts codes must be 4-byte aligned");
-  }
   DQ_HIP(dq::launch_qmm_quantize(x, x_stride, r0, r1, a->k, a->mode == DQ_QMM_INT16, a->paired != 0, a->hi, a->lo, a->d,
                                  a->c, as_stream(stream)),
          "qmm quantize launch");
   return DQ_OK;
+}
+
+// qmm's gemv / gemm on a qmm activation buffer: its rows converted once to the per-32
+// (int8) or int16 block format in the per-device scratch, then the library's GEMV
+// passes or GEMM for that format. y row r0 + r for buffer row r0 + r.
+static int qmm_matmul(const dq_weight* w, const dq_qmm_acts* a, int64_t r0, int64_t rows, int64_t n0, int64_t n1,
+                      float* y, int64_t y_stride, const float* bias, void* stream, bool gemm) {
+  if (int rc = qmm_acts_ok(a); rc != DQ_OK) return rc;
+  if (w == nullptr) return fail(DQ_INVALID_ARGUMENT, "null weight");
+  if (a->k != w->dev.k) return fail(DQ_INVALID_ARGUMENT, "acts k %lld != weight k %lld", (long long)a->k, (long long)w->dev.k);
+  if (r0 < 0 || rows < 0 || r0 + rows > a->m) {
+    return fail(DQ_INVALID_ARGUMENT, "rows [%lld, %lld) outside [0, %lld)", (long long)r0, (long long)(r0 + rows),
+                (long long)a->m);
+  }
+  const int fmt = a->mode == DQ_QMM_INT16 ? DQ_ACT_Q16 : DQ_ACT_PER32;
+  if (int rc = check_acts(w, fmt, a->hi, rows); rc != DQ_OK) return rc;
+  if (int rc = check_out(w, rows, n0, n1, y + r0 * y_stride, y_stride); rc != DQ_OK) return rc;
+  if (rows == 0 || n0 == n1) return DQ_OK;
+  const int64_t orb = dq_act_row_bytes(fmt, a->k);
+  void* buf = nullptr;
+  if (int rc = scratch_get(w->dev.device, (size_t)(rows * orb), &buf); rc != DQ_OK) return rc;
+  DQ_HIP(dq::launch_qmm_to_blocks(a->hi, a->lo, a->d, a->k, a->mode == DQ_QMM_INT16, a->paired != 0, r0, rows,
+                                  static_cast<uint8_t*>(buf), orb, as_stream(stream)),
+         "qmm conversion launch");
+  if (gemm && dq::gemm_supported(w->dev.dtype, fmt)) {
+    return dq_gemm(w, fmt, buf, rows, n0, n1, y + r0 * y_stride, y_stride, bias, stream);
+  }
+  return dq_gemv(w, fmt, buf, rows, n0, n1, y + r0 * y_stride, y_stride, bias, stream);
+}
+
+int dq_qmm_gemv(const dq_weight* w, int64_t n0, int64_t n1, const dq_qmm_acts* a, int64_t r0, int rows, float* y,
+                int64_t y_stride, const float* bias, void* stream) {
+  return qmm_matmul(w, a, r0, rows, n0, n1, y, y_stride, bias, stream, false);
+}
+
+int dq_qmm_gemm(const dq_weight* w, int64_t n0, int64_t n1, const dq_qmm_acts* a, float* y, int64_t y_stride,
+                const float* bias, void* stream) {
+  if (int rc = qmm_acts_ok(a); rc != DQ_OK) return rc;
+  return qmm_matmul(w, a, 0, a->m, n0, n1, y, y_stride, bias, stream, true);
 }
 
 int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0, int64_t n1, float* y,

@@ -57,6 +57,10 @@ hipError_t launch_quantize(int af, const float* x, int64_t m, int64_t k, int64_t
 hipError_t launch_qmm_quantize(const float* x, int64_t x_stride, int64_t r0, int64_t r1, int64_t k, bool i16,
                                bool paired, int8_t* hi, uint8_t* lo, float* d, float* c, hipStream_t s);
 hipError_t launch_qmm_pad(int64_t m, int64_t k, int8_t* hi, uint8_t* lo, float* d, float* c, hipStream_t s);
+// Rows [r0, r0 + rows) of a qmm activation buffer as per-32 ActBlockQ8 (int8) or
+// ActBlockQ16 (int16) rows of orb bytes.
+hipError_t launch_qmm_to_blocks(const int8_t* hi, const uint8_t* lo, const float* d, int64_t k, bool i16, bool paired,
+                                int64_t r0, int64_t rows, uint8_t* out, int64_t orb, hipStream_t s);
 hipError_t launch_repack(int t, const uint8_t* src, int64_t row_stride, int64_t n, int64_t nblk, uint8_t* const* planes,
                          hipStream_t s);
 hipError_t launch_unpack(int t, uint8_t* dst, int64_t row_stride, int64_t n, int64_t nblk, uint8_t* const* planes,

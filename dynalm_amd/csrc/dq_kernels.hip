@@ -353,6 +353,64 @@ hipError_t launch_qmm_pad(int64_t m, int64_t k, int8_t* hi, uint8_t* lo, float* 
   return hipGetLastError();
 }
 
+// Rows [r0, r0 + rows) of a qmm activation buffer as the library's per-32 activation
+// blocks, for qmm's gemv / gemm tables: ActBlockQ8 {d, sum, q[32]} (int8 mode) or
+// ActBlockQ16 {d, sum, int16 q[32]} (int16 mode, q = 256 hi + lo;
+// dynacore/include/dynacore/cpu/cpu_kernels.h:31-36,77-82). Both quantizers have the
+// same arithmetic (d = amax / qmax, RNE, clamp), so the codes and d carry over and sum
+// is the exact code sum (c = d * sum is not needed). Thread (row, block, quad).
+template <bool kI16>
+__global__ __launch_bounds__(256) void k_qmm_to_blocks(const int8_t* __restrict__ hi, const uint8_t* __restrict__ lo,
+                                                       const float* __restrict__ d, int64_t k, int paired, int64_t r0,
+                                                       int64_t rows, uint8_t* __restrict__ out, int64_t orb) {
+  const int64_t kb = k / 32;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const bool live = t < rows * kb * 8;
+  const int64_t tt = live ? t : 0;
+  const int64_t rr = tt / (kb * 8), r = r0 + rr;
+  const int64_t b = (tt / 8) % kb;
+  const int q4 = (int)(tt & 7);
+  const int64_t rowoff = paired ? (r / 2) * 2 * k + 8 * (r & 1) : r * k;
+  const int64_t at = rowoff + (4 * b + q4 / 2) * (paired ? 16 : 8) + 4 * (q4 & 1);
+  const u32 wh = *reinterpret_cast<const u32*>(hi + at);
+  const u32 wl = kI16 ? *reinterpret_cast<const u32*>(lo + at) : 0u;
+  int q[4], sum = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int h = (int)(int8_t)(wh >> (8 * e));
+    q[e] = kI16 ? 256 * h + (int)((wl >> (8 * e)) & 0xFFu) : h;
+    sum += q[e];
+  }
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  sum += __shfl_xor(sum, 4);
+  if (!live) return;
+  uint8_t* blk = out + rr * orb + b * (kI16 ? 72 : 40);
+  if (kI16) {
+    *reinterpret_cast<uint2*>(blk + 8 + 8 * q4) =
+        uint2{((u32)q[0] & 0xFFFFu) | ((u32)q[1] << 16), ((u32)q[2] & 0xFFFFu) | ((u32)q[3] << 16)};
+  } else {
+    *reinterpret_cast<u32*>(blk + 8 + 4 * q4) = wh;
+  }
+  if (q4 == 0) {
+    const int64_t so = paired ? ((r / 2) * kb + b) * 2 + (r & 1) : r * kb + b;
+    *reinterpret_cast<float*>(blk) = d[so];
+    *reinterpret_cast<int*>(blk + 4) = sum;
+  }
+}
+
+hipError_t launch_qmm_to_blocks(const int8_t* hi, const uint8_t* lo, const float* d, int64_t k, bool i16, bool paired,
+                                int64_t r0, int64_t rows, uint8_t* out, int64_t orb, hipStream_t s) {
+  if (rows <= 0 || k <= 0) return hipSuccess;
+  const dim3 g = grid1(rows * (k / 32) * 8, 256);
+  if (i16) {
+    hipLaunchKernelGGL(k_qmm_to_blocks<true>, g, dim3(256), 0, s, hi, lo, d, k, paired ? 1 : 0, r0, rows, out, orb);
+  } else {
+    hipLaunchKernelGGL(k_qmm_to_blocks<false>, g, dim3(256), 0, s, hi, lo, d, k, paired ? 1 : 0, r0, rows, out, orb);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_repack(int t, const uint8_t* src, int64_t row_stride, int64_t n, int64_t nblk, uint8_t* const* planes,
                          hipStream_t s) {
   Planes pl{};

@@ -179,6 +179,19 @@ DQ_API int dq_qmm_act_prepare(void* base, int64_t bytes, int mode, int64_t m, in
  * ranges may be quantized by separate calls. */
 DQ_API int dq_qmm_quantize_rows(const float* x, int64_t x_stride, int64_t r0, int64_t r1, const dq_qmm_acts* a,
                                 void* stream);
+/* qmm::Kernels::gemv (dynacore/include/dynacore/cpu/qmm.h:125-126): y[(r0 + r) * y_stride + n]
+ * for r < rows and n in [n0, n1), from rows [r0, r0 + rows) of a qmm buffer in either
+ * layout, + bias. The codes and d equal the per-32 (int8) / int16 block formats' (same
+ * quantizer arithmetic), so this is dq_gemv on DQ_ACT_PER32 / DQ_ACT_Q16 rows: bit-identical
+ * to it, within the fp32 tolerance of qmm's own order (qmm_reference.cpp:68-114). No
+ * kGemvMaxRows limit. */
+DQ_API int dq_qmm_gemv(const dq_weight* w, int64_t n0, int64_t n1, const dq_qmm_acts* a, int64_t r0, int rows,
+                       float* y, int64_t y_stride, const float* bias, void* stream);
+/* qmm::Kernels::gemm (qmm.h:128-129): every row of the buffer (the reference expects the
+ * pair layout; both are accepted), on the MFMA GEMM where the format has one (Q8_0 / Q4_0
+ * per-32), else the GEMV passes. The gemm scratch is the library's. */
+DQ_API int dq_qmm_gemm(const dq_weight* w, int64_t n0, int64_t n1, const dq_qmm_acts* a, float* y, int64_t y_stride,
+                       const float* bias, void* stream);
 
 /* y[r * y_stride + i] = dot(weight row i, activation row r) + (bias ? bias[i] : 0)
  * for r < m and i in [n0, n1). `acts`: m rows in format fmt, as dq_act_quantize

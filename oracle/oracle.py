@@ -277,6 +277,7 @@ def ref():
                                             C.c_int, C.c_int, C.c_uint32, C.POINTER(C.c_int)]),
             "ref_expand_x86": (C.c_int, [C.c_int, _P, _P, _I64]),
             "ref_qmm_quantize": (C.c_int, [_P, _I64, _I64, _I64, C.c_int, C.c_int, _P, _P, _P, _P]),
+            "ref_qmm_gemv": (C.c_int, [C.c_int, _P, _I64, _I64, _P, _I64, _I64, C.c_int, C.c_int, _P]),
             "ref_bench_decode_sx": (_I64, [C.c_int, C.POINTER(_P), C.c_int, _I64, _I64, _P, C.c_int, _I64, _P,
                                            C.c_int, C.c_int, C.c_int]),
             "ref_llc_bytes": (_I64, []),
@@ -418,3 +419,15 @@ def ref_qmm_quantize(x: np.ndarray, mode: int, paired: bool):
     _check(ref().ref_qmm_quantize(_ptr(x), k, m, k, mode, int(paired), _ptr(hi), _ptr(lo) if lo is not None else None,
                                   _ptr(d), _ptr(c)), "ref_qmm_quantize")
     return hi, lo, d, c
+
+
+def ref_qmm_gemv(dtype: int, w_rows: np.ndarray, x: np.ndarray, mode: int, paired: bool) -> np.ndarray:
+    """qmm's reference-tier gemv on x quantized into an ActBuffer (oracle/_ref): m x n fp32."""
+    x = np.ascontiguousarray(x, np.float32)
+    w_rows = np.ascontiguousarray(w_rows)
+    m, k = x.shape
+    n = w_rows.shape[0]
+    y = np.zeros((m, n), np.float32)
+    _check(ref().ref_qmm_gemv(dtype, _ptr(w_rows), w_rows.shape[1], n, _ptr(x), m, k, mode, int(paired), _ptr(y)),
+           "ref_qmm_gemv")
+    return y

@@ -352,4 +352,22 @@ int ref_qmm_quantize(const float* x, int64_t x_stride, int64_t m, int64_t k, int
   return 0;
 }
 
+// qmm's reference-tier gemv (dynacore/cpu/qmm/qmm_reference.cpp:68-114) over all m rows of x,
+// quantized into an ActBuffer of the given mode and layout; calls of at most kGemvMaxRows rows
+// (qmm.h:125-126). w: n GGUF rows of w_row_bytes; y: m x n, stride n.
+int ref_qmm_gemv(int dtype, const void* w, int64_t w_row_bytes, int64_t n, const float* x, int64_t m, int64_t k, int mode,
+                 int paired, float* y) {
+  if (!valid_type(dtype) || (mode != 0 && mode != 1) || m <= 0 || k <= 0 || k % 32 != 0) return -1;
+  if (!dynacore::qmm::supports(static_cast<DType>(dtype))) return -1;
+  dynacore::qmm::ActBuffer buf;
+  buf.prepare(mode == 0 ? dynacore::qmm::ActMode::kInt8 : dynacore::qmm::ActMode::kInt16, m, k, paired != 0);
+  const dynacore::qmm::Kernels& kern = dynacore::qmm::reference_kernels();
+  buf.quantize_rows(x, k, 0, m, kern);
+  for (int64_t r0 = 0; r0 < m; r0 += dynacore::qmm::kGemvMaxRows) {
+    const int rows = static_cast<int>(std::min<int64_t>(dynacore::qmm::kGemvMaxRows, m - r0));
+    kern.gemv(static_cast<DType>(dtype), w, w_row_bytes, 0, n, buf.acts(), r0, rows, y, n, nullptr);
+  }
+  return 0;
+}
+
 }  // extern "C"

@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 
 import dynalm_amd as dq
+from dqtest import TYPES, activations, close, gguf_weights
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -86,3 +87,71 @@ def test_qmm_quantize_prefill_shape(cuda, mode):
     """Config 4's prefill activations (512 rows of 4096) in the gemm's pair layout."""
     x = np.random.default_rng(4).standard_normal((512, 4096)).astype(np.float32)
     same(run_gpu(x, mode, True), O.qmm_quantize(x, mode, True))
+
+
+def prepared(x: np.ndarray, mode: int, paired: bool):
+    m, k = x.shape
+    nbytes = dq.qmm_act_bytes(mode, m, k, paired)
+    buf = torch.empty((nbytes,), dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    a = dq.qmm_act_prepare(buf, nbytes, mode, m, k, paired, st)
+    xd = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    dq.qmm_quantize_rows(xd, k, 0, m, a, st)
+    return buf, xd, a
+
+
+def supported(t: int, mode: int) -> bool:
+    return mode == dq.QMM_INT8 or t != O.Q4_0  # no int16 kernel for Q4_0 weights
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("mode", [dq.QMM_INT8, dq.QMM_INT16])
+@pytest.mark.parametrize("paired", [False, True])
+def test_qmm_gemv(cuda, t, mode, paired):
+    """qmm::Kernels::gemv on the qmm buffer: rows [r0, r0 + rows) of either layout equal
+    dq_gemv on the same rows quantized to the per-32 / int16 block format bit for bit, and
+    qmm's reference gemv (its own fp32 order) within the north-star tolerance."""
+    import dqtorch as T
+
+    if not supported(t, mode):
+        pytest.skip("int16 activations have no Q4_0 kernel")
+    m, k, n, r0, rows = 7, 1024, 96, 2, 5
+    w_rows = gguf_weights(t, n, k, 31 + t, outlier_frac=0.01)
+    x = activations(m, k, 7 * t + mode, outliers=False)
+    w = dq.Weight.upload(t, w_rows, k)
+    buf, xd, a = prepared(x, mode, paired)
+    bias = torch.from_numpy(np.linspace(-1, 1, n, dtype=np.float32)).cuda()
+    y = torch.full((m, n), 7.0, device="cuda")
+    dq.qmm_gemv(w, 0, n, a, r0, rows, y, n, bias, torch.cuda.current_stream().cuda_stream)
+    fmt = O.ACT_PER32 if mode == dq.QMM_INT8 else O.ACT_Q16
+    acts = T.quantize(fmt, xd)
+    want = T.gemv(w, fmt, acts, bias=bias)
+    got = y.cpu().numpy()
+    assert np.array_equal(got[r0:r0 + rows].view(np.uint32), want.cpu().numpy()[r0:r0 + rows].view(np.uint32))
+    assert (got[:r0] == 7.0).all() and (got[r0 + rows:] == 7.0).all()
+    if O.ref_available():
+        ref = O.ref_qmm_gemv(t, w_rows, x, mode, paired) + np.linspace(-1, 1, n, dtype=np.float32)
+        ok, worst = close(got[r0:r0 + rows], ref[r0:r0 + rows])
+        assert ok, f"worst error ratio {worst:.3g}"
+    w.free()
+
+
+@pytest.mark.parametrize("t", [O.Q8_0, O.Q4_0, O.Q4_K])
+def test_qmm_gemm(cuda, t):
+    """qmm::Kernels::gemm on a paired buffer of odd m: every row equals dq_gemm (Q8_0 / Q4_0
+    on the per-32 MFMA GEMM) or dq_gemv (Q4_K) on the per-32 rows bit for bit."""
+    import dqtorch as T
+
+    m, k, n = 67, 2048, 256
+    w_rows = gguf_weights(t, n, k, 77 + t, outlier_frac=0.01)
+    x = activations(m, k, 5 + t, outliers=False)
+    w = dq.Weight.upload(t, w_rows, k)
+    buf, xd, a = prepared(x, dq.QMM_INT8, True)
+    y = torch.zeros((m, n), device="cuda")
+    dq.qmm_gemm(w, 0, n, a, y, n, None, torch.cuda.current_stream().cuda_stream)
+    acts = T.quantize(O.ACT_PER32, xd)
+    want = T.gemm(w, O.ACT_PER32, acts) if t != O.Q4_K else T.gemv(w, O.ACT_PER32, acts)
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), want.cpu().numpy().view(np.uint32))
+    ok, worst = close(y.cpu().numpy(), O.matmul(t, O.ACT_PER32, w_rows, O.quantize_act(O.ACT_PER32, x), k))
+    assert ok, f"worst error ratio {worst:.3g}"
+    w.free()
