@@ -445,6 +445,33 @@ def measured_traffic() -> dict:
     return out
 
 
+def output_checks(w, x, acts, xg, ag, m: int, stream: int) -> dict:
+    """Bit-equality of the timed paths with independent kernels on the same inputs."""
+    import torch
+
+    import dynalm_amd as dq
+
+    y_fused = torch.empty((1, N), device="cuda")
+    y_gemv = torch.empty((1, N), device="cuda")
+    dq.matmul(w, x, 1, K, y_fused, N, None, stream)
+    dq.act_quantize(dq.ACT_Q8_K, x, 1, K, K, acts, stream)
+    dq.gemv(w, dq.ACT_Q8_K, acts, 1, 0, N, y_gemv, N, None, stream)
+    yg = torch.empty((m, N), device="cuda")
+    dq.gemm(w, dq.ACT_Q8_K, ag, m, 0, N, yg, N, None, stream)
+    idx = torch.linspace(0, m - 1, 16, device="cuda").round().long()
+    a16 = ag[idx].contiguous()
+    y16 = torch.empty((16, N), device="cuda")
+    dq.gemv(w, dq.ACT_Q8_K, a16, 16, 0, N, y16, N, None, stream)
+    y1 = torch.empty((1, N), device="cuda")
+    dq.gemv(w, dq.ACT_Q8_K, a16[:1], 1, 0, N, y1, N, None, stream)
+    torch.cuda.synchronize()
+    bits = lambda t: t.view(torch.int32)
+    return {"fused_step_eq_gemv": bool(torch.equal(bits(y_fused), bits(y_gemv))),
+            "gemm_rows_eq_skinny_gemv": bool(torch.equal(bits(yg[idx]), bits(y16))),
+            "gemm_row_eq_gemv": bool(torch.equal(bits(yg[idx[:1]]), bits(y1))),
+            "rows_checked": [int(i) for i in idx.tolist()]}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -546,6 +573,13 @@ def main() -> None:
     ms_gemm = time_graph(gemm, args.gemm_iters, 3)
     ops = 2.0 * m * N * K
     tops = ops / (ms_gemm * 1e-3) / 1e12
+
+    # ---- the timed kernels' outputs, checked against independent kernels that compute the
+    # same integers and fp32 steps (no oracle here): the fused M = 1 step against the GEMV on
+    # separately quantized rows, and sampled GEMM rows against the M = 1 GEMV and the skinny
+    # MFMA GEMV on those rows; every pair must agree bit for bit
+    checks = output_checks(weights[0], x, acts, xg, ag, m, stream)
+    log(f"output checks: {checks}")
 
     # ---- the fp32 expand + GEMM class at the same shape (the default plan's choice for
     # m > 8 dense fp32 rows): weights expanded in LDS, v_mfma_f32_32x32x2_f32
@@ -653,7 +687,10 @@ def main() -> None:
     if not args.no_cpu:
         log("CPU baseline")
         result["cpu_baseline"] = cpu_baseline(w_host, args.cpu_seconds)
+    result["output_checks"] = checks
     print(json.dumps(result), flush=True)
+    if not all(v for key, v in checks.items() if key != "rows_checked"):
+        raise SystemExit("output check failed: the timed kernels disagree with the GEMV on the same inputs")
 
 
 if __name__ == "__main__":
