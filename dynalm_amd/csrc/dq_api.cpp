@@ -117,6 +117,47 @@ int scratch_get(int device, size_t need, void** out) { return scratch_get(g_scra
 
 constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
+// Per-(device, stream) workspaces of the public entry points whose kernels need device
+// memory beyond their arguments (dq_gemm's f16 activation operands). Each stream has
+// its own buffer, so calls on different streams do not share one; the pool lock is
+// held until the caller has enqueued the launches that use the buffer, so a call on
+// the same stream from another thread cannot grow (free) it before they are queued,
+// and launches on one stream run in order. Growing synchronizes that stream first.
+struct StreamWs {
+  int device;
+  void* stream;
+  void* p;
+  size_t bytes;
+};
+std::mutex g_sws_mu;
+std::vector<StreamWs> g_sws;
+
+template <class F>
+int with_stream_ws(int device, void* stream, size_t need, F&& fn) {
+  std::lock_guard<std::mutex> lock(g_sws_mu);
+  StreamWs* e = nullptr;
+  for (StreamWs& x : g_sws)
+    if (x.device == device && x.stream == stream) e = &x;
+  if (e == nullptr) {
+    g_sws.push_back(StreamWs{device, stream, nullptr, 0});
+    e = &g_sws.back();
+  }
+  if (e->bytes < need) {
+    dq::DeviceScope ds(device);
+    DQ_HIP(ds.err, "hipSetDevice");
+    if (e->p != nullptr) {
+      DQ_HIP(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+      DQ_HIP(hipFree(e->p), "hipFree");
+      e->p = nullptr;
+      e->bytes = 0;
+    }
+    const size_t sz = need < (1u << 20) ? (1u << 20) : need;
+    DQ_HIP(hipMalloc(&e->p, sz), "hipMalloc(stream workspace)");
+    e->bytes = sz;
+  }
+  return fn(static_cast<uint8_t*>(e->p));
+}
+
 // The quantized-activation buffer of one matmul: the start of the caller's region,
 // or the per-device pool.
 int acts_buffer(int device, size_t need, const dq::Region& r, void** out) {
@@ -328,8 +369,22 @@ namespace dq {
 size_t matmul_scratch_bytes(const dq_weight* w, int fmt, int64_t m) {
   const int f = fmt < 0 ? dq_act_format_for(w->dev.dtype) : fmt;
   if (f == DQ_ACT_F32) return gemv_split_bytes(w->dev, f, m < 8 ? m : 8);  // the rows are read in place
-  const size_t acts = round256((size_t)(m * dq_act_row_bytes(f, w->dev.k)));
+  size_t acts = round256((size_t)(m * dq_act_row_bytes(f, w->dev.k)));
+  if (f == DQ_ACT_Q8_K && gemm_h16_pays(w->dev, m, 0, w->dev.n)) acts = round256((size_t)act16_bytes(m, w->dev.k));
   return acts + gemv_split_bytes(w->dev, f, m < 8 ? m : 8);
+}
+
+// Q4_K prefill on the f16 GEMM: quantize straight into its operand layout (in the
+// region when one is given), then the GEMM.
+static int gemm_h16_from_x(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, float* y,
+                           int64_t y_stride, const float* bias, hipStream_t s, const Region& r) {
+  void* a16 = nullptr;
+  if (int rc = acts_buffer(w->dev.device, (size_t)act16_bytes(m, w->dev.k), r, &a16); rc != DQ_OK) return rc;
+  DQ_HIP(launch_act16_quant(x, m > 1 ? x_stride : w->dev.k, m, w->dev.k, static_cast<uint8_t*>(a16), s),
+         "act16 quantize launch");
+  DQ_HIP(launch_gemm_h16(w->dev, static_cast<const uint8_t*>(a16), m, 0, w->dev.n, y, y_stride, bias, s),
+         "gemm launch");
+  return DQ_OK;
 }
 
 int matmul_impl(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, float* y, int64_t y_stride,
@@ -358,6 +413,9 @@ int matmul_impl(const dq_weight* w, const float* x, int64_t m, int64_t x_stride,
     DQ_HIP(launch_gemv_fused(w->dev, x, x_stride, m, y, y_stride, bias, s, r.base ? &ws : nullptr), "gemv launch");
     return DQ_OK;
   }
+  if (fmt == DQ_ACT_Q8_K && gemm_h16_pays(w->dev, m, 0, w->dev.n)) {
+    return gemm_h16_from_x(w, x, m, x_stride, y, y_stride, bias, s, r);
+  }
   void* acts = nullptr;
   if (int rc = acts_buffer(w->dev.device, (size_t)(m * arb), r, &acts); rc != DQ_OK) return rc;
   if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, x_stride, acts, stream); rc != DQ_OK) return rc;
@@ -377,6 +435,9 @@ int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int6
                        nullptr, s, r.base ? &ws : nullptr),
            "gemv launch");
     return DQ_OK;
+  }
+  if (fmt == DQ_ACT_Q8_K && use_gemm(w->dev, fmt, m) && gemm_h16_pays(w->dev, m, 0, w->dev.n)) {
+    return gemm_h16_from_x(w, x, m, x_stride, y, y_stride, bias, s, r);
   }
   void* acts = nullptr;
   if (int rc = acts_buffer(w->dev.device, (size_t)(m * arb), r, &acts); rc != DQ_OK) return rc;
@@ -679,6 +740,16 @@ int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
     return fail(DQ_UNSUPPORTED, "no GEMM kernel for weight type %d with activation format %d", w->dev.dtype, fmt);
   }
   if (m == 0 || n0 == n1) return DQ_OK;
+  if (fmt == DQ_ACT_Q8_K && dq::gemm_h16_pays(w->dev, m, n0, n1)) {
+    // Q4_K: the codes as f16 operands (one conversion launch), then the f16 GEMM
+    const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
+    return with_stream_ws(w->dev.device, stream, (size_t)dq::act16_bytes(m, w->dev.k), [&](uint8_t* ws) -> int {
+      DQ_HIP(dq::launch_act16_from_q8k(static_cast<const uint8_t*>(acts), arb, m, w->dev.k, ws, as_stream(stream)),
+             "act16 conversion launch");
+      DQ_HIP(dq::launch_gemm_h16(w->dev, ws, m, n0, n1, y, y_stride, bias, as_stream(stream)), "gemm launch");
+      return DQ_OK;
+    });
+  }
   if ((m + 127) / 128 > 65535) return fail(DQ_UNSUPPORTED, "m too large");
   DQ_HIP(dq::launch_gemm(w->dev, fmt, static_cast<const uint8_t*>(acts), dq_act_row_bytes(fmt, w->dev.k), m, n0, n1, y,
                          y_stride, bias, as_stream(stream)),

@@ -809,11 +809,6 @@ hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t 
       if (wgs * 8 >= (int64_t)cus * 7) return launch_big<kQ6_K, 4, 2, 4>(w, acts, arb, m, n0, n1, y, ys, bias, s);
       return launch_big<kQ6_K, 2, 2, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s);
     }
-    // the streamed kernel (128 x 256 tiles) where its grid reaches 5/8 of the CUs
-    // (measured: faster there, slower on smaller grids)
-    const int64_t swgs = (rows + 255) / 256 * ((m + 127) / 128);
-    if (swgs * 8 >= (int64_t)cus * 5 && gemm_stream_ok(w, m, n0, n1, arb))
-      return launch_gemm_stream(w, acts, arb, m, n0, n1, y, ys, bias, s);
     if (wgs * 8 >= (int64_t)cus * 7) return launch_big<kQ4_K, 4, 2, 4>(w, acts, arb, m, n0, n1, y, ys, bias, s);
     return launch_big<kQ4_K, 2, 2, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s);
   }

@@ -86,12 +86,17 @@ hipError_t launch_units(const WeightDev& w, int af, const uint8_t* acts, int64_t
 hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
                        float* y, int64_t ys, const float* bias, hipStream_t s);
 bool gemm_supported(int dtype, int af);
-// The streamed Q4_K x Q8_K GEMM (dq_gemm_stream.hip): 128 x 256 tiles, 8 waves each
-// owning one 32-row weight tile, K in half super-blocks. gemm_stream_ok says whether
-// the shape fits its 32-bit buffer offsets.
-hipError_t launch_gemm_stream(const WeightDev& w, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0, int64_t n1,
-                              float* y, int64_t ys, const float* bias, hipStream_t s);
-bool gemm_stream_ok(const WeightDev& w, int64_t m, int64_t n0, int64_t n1, int64_t arb);
+// The Q4_K x Q8_K GEMM on the f16 matrix cores (dq_gemm_h16.hip): 128 x 256 tiles,
+// activation codes as f16 in the "act16" layout of act16_bytes(m, k) bytes, written
+// from Q8_K rows (launch_act16_from_q8k) or from fp32 rows with the Q8_K quantizer's
+// arithmetic (launch_act16_quant). gemm_h16_pays: the shapes it is used for (its grid
+// fills at least 5/8 of the CUs, and the offsets fit 32 bits).
+int64_t act16_bytes(int64_t m, int64_t k);
+bool gemm_h16_pays(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
+hipError_t launch_act16_from_q8k(const uint8_t* acts, int64_t arb, int64_t m, int64_t k, uint8_t* out, hipStream_t s);
+hipError_t launch_act16_quant(const float* x, int64_t x_stride, int64_t m, int64_t k, uint8_t* out, hipStream_t s);
+hipError_t launch_gemm_h16(const WeightDev& w, const uint8_t* act16, int64_t m, int64_t n0, int64_t n1, float* y,
+                           int64_t ys, const float* bias, hipStream_t s);
 // The expand-class fp32 GEMM (dq_gemm_f32.hip): weight tiles expanded to fp32 in LDS
 // and contracted with the fp32 rows x (stride xs floats) on the matrix cores; any of
 // the four weight types. Below kF32GemmMinRows rows the fp32 GEMV passes are faster.

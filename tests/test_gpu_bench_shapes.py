@@ -2,7 +2,7 @@
 shapes select.
 
 - The large GEMM kernels over many super-blocks: Q4_K K=4096 N=14336 at M=512 and
-  M=2048 (the streamed 128 x 256 kernel: one round of 224 workgroups, and 3.5 rounds),
+  M=2048 (the f16 128 x 256 kernel: one round of 224 workgroups, and 3.5 rounds),
   Q6_K over 4 and 56 super-blocks (the 256 x 128 tile). Every output bit-identical to the GEMV on the same Q8_K rows,
   sampled columns bit-identical to the oracle.
 - The per-32 GEMM (Q8_0 4096 x 4096, Q4_0 K=4096 N=14336) at M=512.
@@ -43,9 +43,9 @@ def bits(a: np.ndarray) -> np.ndarray:
 
 @pytest.mark.parametrize("m", [512, 2048])
 def test_gemm_q4k_bench_shape(cuda, m):
-    """Config 4 (K=4096, N=14336) at the bench's M: k_gemm_q4k_stream over 16 super-blocks
-    (32 half-super-block positions through its ring of four LDS buffers), one round of
-    224 workgroups at M=512 and 3.5 rounds at M=2048. dq_gemm == dq_gemv bit for bit on every output; 128 sampled columns ==
+    """Config 4 (K=4096, N=14336) at the bench's M: k_gemm_q4k_h16 over 16 super-blocks
+    (through its ring of two LDS operand buffers), one round of 224 workgroups at M=512
+    and 3.5 rounds at M=2048. dq_gemm == dq_gemv bit for bit on every output; 128 sampled columns ==
     the oracle bit for bit; dq_matmul (quantize + GEMM) == quantize then dq_gemm."""
     import dqtorch as T
 
