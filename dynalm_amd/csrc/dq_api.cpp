@@ -70,7 +70,7 @@ bool act_fmt_ok(int f) {
 // dynacore/cpu/avx2/kernels_avx2.cpp:1957-1960).
 bool pair_ok(int t, int f) {
   if (f == DQ_ACT_F32) return true;  // every weight type has an fp32 row kernel (vec_dot_*)
-  if (f == DQ_ACT_Q16) return t == DQ_Q8_0 || t == DQ_Q4_K || t == DQ_Q6_K;
+  if (f == DQ_ACT_Q16) return true;  // the int16 GEMV takes every weight type
   if (t == DQ_Q8_0 || t == DQ_Q4_0) return f == DQ_ACT_PER32 || f == DQ_ACT_Q8_0;
   return f == DQ_ACT_Q8_K || f == DQ_ACT_SX || f == DQ_ACT_PER32;
 }

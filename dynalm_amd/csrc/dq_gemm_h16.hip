@@ -281,6 +281,9 @@ __global__ __launch_bounds__(kHThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   // nibbles. Issuing the operands in one burst instead stalls the waves at the
   // interval start (in-order issue behind the queued loads).
   auto mfma_sb = [&](int s) {
+    // the MFMA phase outranks the other wave's epilogue: a dense fp32 VALU stream from
+    // one wave otherwise delays the other's MFMA issue (measured: 4% per launch)
+    __builtin_amdgcn_s_setprio(2);
     const bool next = s + 1 < nb;
     hdr_n = ld_hdr(s + 1);
     const uint8_t* P = lds + __builtin_amdgcn_readfirstlane((s & 1) * kHPos);
@@ -323,6 +326,7 @@ __global__ __launch_bounds__(kHThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   };
   // The canonical epilogue of super-block s's four tiles, header he.
   auto epi_sb = [&](int s, const v4u& he) {
+    __builtin_amdgcn_s_setprio(0);
     const uint8_t* SB = lds + kHSbBase + __builtin_amdgcn_readfirstlane((s & 1) * kHSb);
     const float d24 = h2f(he.x) * 16777216.0f, ndm24 = -h2f(he.x >> 16) * 16777216.0f;
     // Mn's B operand: m_j of sub-blocks 4 hh .. 4 hh + 3, each for two bsum groups, raw bits

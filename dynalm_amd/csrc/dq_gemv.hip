@@ -546,16 +546,29 @@ DQ_DEV void compute32(const Chunk32<WT, U>& ch, int bb, const uint8_t* st, Out<M
 #pragma unroll
     for (int mm = 0; mm < M; ++mm) {
       if (AF == kActQ16) {
-        // int16 activations, Q8_0 (kernels_avx2.cpp:1662-1676): the exact
-        // P = sum q a = 256 sum(q hi) + sum(q (lo - 128)) + 128 sum(q); acc += (float)P (dw da)
         const uint8_t* ab = st + (mm * o.nblk + b) * kStage16;
-        const v4u q0 = ch.q[u][0], q1 = ch.q[u][Chunk32<WT, U>::kC - 1];
-        const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
-        const v4u flip = {0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
-        const int ph = sdot16(q1, lds16(ab + 32), sdot16(q0, lds16(ab + 16), 0));
-        const int pl = sdot16(q1, lds16(ab + 64) ^ flip, sdot16(q0, lds16(ab + 48) ^ flip, 0));
-        const int sq = sdot16(q1, ones, sdot16(q0, ones, 0));
-        const int P = ph * 256 + pl + 128 * sq;
+        int P;
+        if (WT == kQ8_0) {
+          // int16 activations, Q8_0 (kernels_avx2.cpp:1662-1676): the exact
+          // P = sum q a = 256 sum(q hi) + sum(q (lo - 128)) + 128 sum(q)
+          const v4u q0 = ch.q[u][0], q1 = ch.q[u][Chunk32<WT, U>::kC - 1];
+          const v4u ones = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
+          const v4u flip = {0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
+          const int ph = sdot16(q1, lds16(ab + 32), sdot16(q0, lds16(ab + 16), 0));
+          const int pl = sdot16(q1, lds16(ab + 64) ^ flip, sdot16(q0, lds16(ab + 48) ^ flip, 0));
+          const int sq = sdot16(q1, ones, sdot16(q0, ones, 0));
+          P = ph * 256 + pl + 128 * sq;
+        } else {
+          // int16 activations, Q4_0 (qmm's dot_row_ref, qmm_reference.cpp:68-93, codes
+          // nibble - 8 as qmm_unpack.h:61-75 unpacks them): low nibbles are values 0..15,
+          // high nibbles 16..31; the exact P = 256 sum(nib hi) + sum(nib lo) - 8 sum(a)
+          // (|sum nib a| <= 15 * 32768 * 32 < 2^31)
+          const v4u q0 = ch.q[u][0] & 0x0F0F0F0Fu, q1 = (ch.q[u][0] >> 4) & 0x0F0F0F0Fu;
+          const int ph = sdot16(q1, lds16(ab + 32), sdot16(q0, lds16(ab + 16), 0));
+          const int pl = (int)udot16(q1, lds16(ab + 64), udot16(q0, lds16(ab + 48), 0u));
+          P = ph * 256 + pl - 8 * (int)lds4(ab + 4);
+        }
+        // acc += (float)P (dw da): the reference's (dw da) P for both formats
         o.acc[mm] = o.acc[mm] + (float)P * (dw * as_f(lds4(ab)));
         continue;
       }
@@ -1295,6 +1308,7 @@ static hipError_t gemv_pass(const WeightDev& w, int af, const uint8_t* acts, int
       return af == kActPer32 ? gemv_waves<kQ8_0, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s)
                              : gemv_waves<kQ8_0, kActQ8_0, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
     default:
+      if (af == kActQ16) return gemv_waves<kQ4_0, kActQ16, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
       if (af == kActF32) return gemv_waves<kQ4_0, kActF32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
       return af == kActPer32 ? gemv_waves<kQ4_0, kActPer32, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s)
                              : gemv_waves<kQ4_0, kActQ8_0, M, false>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, ws, s);

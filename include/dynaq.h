@@ -89,8 +89,10 @@ typedef enum dq_dtype {
  *                 channels (the FFN down projection). d = amax32/32767, codes round half to
  *                 even (saturated to int16), sum = the sum of the codes
  *                 (dynacore/include/dynacore/cpu/cpu_kernels.h:72-82,
- *                  dynacore/cpu/avx2/kernels_avx2.cpp:1631-1652). With Q8_0, Q4_K and Q6_K;
- *                 the kernels form each 32-value (Q6_K: 16-value) integer dot exactly;
+ *                  dynacore/cpu/avx2/kernels_avx2.cpp:1631-1652). With every weight type
+ *                 (Q4_0 as qmm's int16 mode runs it, qmm_reference.cpp:68-93; the reference's
+ *                 AVX2 int16 kernels cover Q8_0, Q4_K and Q6_K); the kernels form each
+ *                 32-value (Q6_K: 16-value) integer dot exactly;
  *   DQ_ACT_F32    no quantization: fp32 rows of k floats (4k bytes), dynacore's kF32
  *                 contract (f32_row_dot, the reference-accuracy fallback and x86 prefill
  *                 default, dynacore/src/kernel/matmul_registry.cpp:51-54) with the arithmetic

@@ -586,7 +586,7 @@ int dqo_encode_weight_rows(int dtype, const float* x, int64_t rows, int64_t n, v
 
 static int pair_ok(int wtype, int fmt) {
   if (fmt == DQO_ACT_F32) return 0; /* no integer partials; the dots have their own path */
-  if (fmt == DQO_ACT_Q16) return wtype == DQO_Q8_0 || wtype == DQO_Q4_K || wtype == DQO_Q6_K;
+  if (fmt == DQO_ACT_Q16) return wtype == DQO_Q8_0 || wtype == DQO_Q4_0 || wtype == DQO_Q4_K || wtype == DQO_Q6_K;
   switch (wtype) {
     case DQO_Q8_0: case DQO_Q4_0: return fmt == DQO_ACT_PER32 || fmt == DQO_ACT_Q8_0;
     case DQO_Q4_K: case DQO_Q6_K: return fmt == DQO_ACT_PER32 || fmt == DQO_ACT_Q8_K || fmt == DQO_ACT_SX;
@@ -791,12 +791,25 @@ float dqo_dot(int wtype, int fmt, const void* wrow, const void* arow, int64_t k)
      * the integer sub-block scale, acc = fma((float)(sc*P), d*da, acc); Q4_K's mins
      * term cor += dmin*((m*da)*(float)sum) apart, returned as acc - cor. */
     float cor = 0.0f;
-    for (int64_t b = 0; b < (wtype == DQO_Q8_0 ? k / 32 : k / 256); ++b) {
+    const int b32 = wtype == DQO_Q8_0 || wtype == DQO_Q4_0;
+    for (int64_t b = 0; b < (b32 ? k / 32 : k / 256); ++b) {
       if (wtype == DQO_Q8_0) {
         int32_t p = 0;
         for (int t = 0; t < 32; ++t) p += (int32_t)(int8_t)w[b * 34 + 2 + t] * act_code(fmt, a, 32 * b + t);
         const float dw = dqo_fp16_to_fp32(rd16(w + b * 34));
         acc = fmaf((float)p, dw * rdf(a + b * 72), acc);
+        continue;
+      }
+      if (wtype == DQO_Q4_0) {
+        /* no AVX2 kernel: qmm's dot_row_ref (qmm_reference.cpp:68-93) with the codes
+         * qmm_unpack.h:61-75 unpacks, acc += (dw * da) * (float)P per block */
+        int8_t q[32];
+        weight_codes(wtype, w, b, q);
+        int32_t p = 0;
+        for (int t = 0; t < 32; ++t) p += (int32_t)q[t] * act_code(fmt, a, 32 * b + t);
+        const float t1 = dqo_fp16_to_fp32(rd16(w + b * 18)) * rdf(a + b * 72);
+        const float t2 = t1 * (float)p;
+        acc = acc + t2;
         continue;
       }
       const uint8_t* blk = w + b * (wtype == DQO_Q4_K ? 144 : 210);

@@ -79,8 +79,8 @@ def test_sizes():
     assert dq.partials_count(dq.Q4_K, dq.ACT_Q16, 4096) == (128, 0)
     assert dq.partials_count(dq.Q6_K, dq.ACT_Q16, 4096) == (256, 0)
     assert dq.partials_count(dq.Q8_0, dq.ACT_Q16, 4096) == (128, 0)
-    with pytest.raises(dq.DqError):
-        dq.partials_count(dq.Q4_0, dq.ACT_Q16, 256)  # no int16 kernel for Q4_0 in the reference either
+    # Q4_0: qmm's int16 mode runs every format (qmm_reference.cpp:68-93)
+    assert dq.partials_count(dq.Q4_0, dq.ACT_Q16, 4096) == (128, 0)
     # fp32 activations (the kF32 contract): the rows themselves, no integer partials
     assert dq.act_row_bytes(dq.ACT_F32, 4096) == 4096 * 4
     assert dq.act_row_bytes(dq.ACT_F32, 100) == -1

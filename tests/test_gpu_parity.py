@@ -913,7 +913,8 @@ def test_quantize_q16_matches_reference_golden(cuda):
     assert np.array_equal(quant_gpu(O.ACT_Q16, gold["q16_x"]), gold["act_q16"])
 
 
-Q16_TYPES = [O.Q8_0, O.Q4_K, O.Q6_K]
+Q16_TYPES = [O.Q8_0, O.Q4_0, O.Q4_K, O.Q6_K]
+Q16_AVX2 = [O.Q8_0, O.Q4_K, O.Q6_K]  # the types with a reference AVX2 int16 kernel (golden q16dot_*)
 
 
 @pytest.mark.parametrize("t", Q16_TYPES, ids=lambda t: O.TYPE_NAMES[t])
@@ -953,6 +954,9 @@ def _q16_exact_case(t: int, n: int, k: int, seed: int) -> tuple[np.ndarray, np.n
         blk = rows.reshape(n, -1, 34)
         blk[:, :, 0:2] = one
         blk[:, :, 2:] = rng.integers(-31, 32, blk[:, :, 2:].shape).astype(np.int8).view(np.uint8)
+    elif t == O.Q4_0:
+        blk = rows.reshape(n, -1, 18)
+        blk[:, :, 0:2] = one                              # codes: the random nibbles - 8
     elif t == O.Q4_K:
         blk = rows.reshape(n, -1, 144)
         blk[:, :, 0:2] = one
@@ -993,7 +997,7 @@ def test_gemv_q16_exact_integers(cuda, t):
     assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("t", Q16_TYPES, ids=lambda t: O.TYPE_NAMES[t])
+@pytest.mark.parametrize("t", Q16_AVX2, ids=lambda t: O.TYPE_NAMES[t])
 def test_gemv_q16_vs_reference_avx2(cuda, t):
     """Against the reference's AVX2 dot_rows16_* (golden q16dot_*): fp32 order only."""
     import dqtorch as T

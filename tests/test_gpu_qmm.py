@@ -100,10 +100,6 @@ def prepared(x: np.ndarray, mode: int, paired: bool):
     return buf, xd, a
 
 
-def supported(t: int, mode: int) -> bool:
-    return mode == dq.QMM_INT8 or t != O.Q4_0  # no int16 kernel for Q4_0 weights
-
-
 @pytest.mark.parametrize("t", TYPES)
 @pytest.mark.parametrize("mode", [dq.QMM_INT8, dq.QMM_INT16])
 @pytest.mark.parametrize("paired", [False, True])
@@ -113,8 +109,6 @@ def test_qmm_gemv(cuda, t, mode, paired):
     qmm's reference gemv (its own fp32 order) within the north-star tolerance."""
     import dqtorch as T
 
-    if not supported(t, mode):
-        pytest.skip("int16 activations have no Q4_0 kernel")
     m, k, n, r0, rows = 7, 1024, 96, 2, 5
     w_rows = gguf_weights(t, n, k, 31 + t, outlier_frac=0.01)
     x = activations(m, k, 7 * t + mode, outliers=False)

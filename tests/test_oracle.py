@@ -14,7 +14,7 @@ import os
 import numpy as np
 import pytest
 
-from dqtest import BLOCK, TYPES, activations, weight_rows
+from dqtest import BLOCK, TYPES, activations, gguf_weights, weight_rows
 from oracle import oracle as O
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_vectors.npz")
@@ -303,7 +303,7 @@ def _act_codes(fmt: int, a: np.ndarray, k: int) -> np.ndarray:
 PAIRS_ALL = [(O.Q8_0, O.ACT_PER32), (O.Q8_0, O.ACT_Q8_0), (O.Q4_0, O.ACT_PER32), (O.Q4_0, O.ACT_Q8_0),
              (O.Q4_K, O.ACT_PER32), (O.Q4_K, O.ACT_Q8_K), (O.Q4_K, O.ACT_SX),
              (O.Q6_K, O.ACT_PER32), (O.Q6_K, O.ACT_Q8_K), (O.Q6_K, O.ACT_SX),
-             (O.Q8_0, O.ACT_Q16), (O.Q4_K, O.ACT_Q16), (O.Q6_K, O.ACT_Q16)]
+             (O.Q8_0, O.ACT_Q16), (O.Q4_0, O.ACT_Q16), (O.Q4_K, O.ACT_Q16), (O.Q6_K, O.ACT_Q16)]
 
 
 @pytest.mark.parametrize("t,fmt", PAIRS_ALL, ids=lambda p: str(p))
@@ -673,6 +673,36 @@ def test_qmm_quantize_layouts_and_scales(mode):
     dd = np.zeros((m_pad, kb), np.float32)
     dd[:m] = d_r.reshape(m, kb)
     np.testing.assert_array_equal(d_p.reshape(m_pad // 2, kb, 2), np.stack([dd[0::2], dd[1::2]], axis=2))
+
+
+def _q16_rows_from_qmm(x: np.ndarray) -> np.ndarray:
+    """The rows of qmm's int16 buffer (row layout) as int16 activation blocks (float d,
+    int32 code sum, int16 codes[32]): the conversion dq_qmm_gemv makes on the GPU."""
+    hi, lo, d, _ = O.qmm_quantize(x, 1, False)
+    m, k = x.shape
+    kb = k // 32
+    codes = (hi.astype(np.int32).reshape(m, kb, 32) * 256 + lo.astype(np.int32).reshape(m, kb, 32)).astype(np.int16)
+    out = np.zeros((m, kb, 72), np.uint8)
+    out[:, :, 0:4] = np.ascontiguousarray(d, np.float32).reshape(m, kb, 1).view(np.uint8)
+    out[:, :, 4:8] = codes.astype(np.int32).sum(-1, dtype=np.int32).reshape(m, kb, 1).view(np.uint8)
+    out[:, :, 8:] = codes.view(np.uint8).reshape(m, kb, 64)
+    return out.reshape(m, -1)
+
+
+@needs_ref
+def test_q16_q4_0_matches_reference_qmm():
+    """Q4_0 x int16 has no AVX2 kernel in the reference; the oracle follows qmm's
+    dot_row_ref (dynacore/cpu/qmm/qmm_reference.cpp:68-93, codes from qmm_unpack.h:61-75):
+    on the reference's own int16 ActBuffer rows it equals the reference build's qmm gemv
+    bit for bit (one accumulator, blocks in order, (dw * da) * P)."""
+    m, k, n = 5, 1024, 40
+    w = gguf_weights(O.Q4_0, n, k, 2100, outlier_frac=0.01)
+    x = (np.random.default_rng(2101).standard_normal((m, k)) * 3).astype(np.float32)
+    x[:, 5::67] *= np.float32(90.0)
+    a16 = _q16_rows_from_qmm(x)
+    got = O.matmul(O.Q4_0, O.ACT_Q16, w, a16, k)
+    want = O.ref_qmm_gemv(O.Q4_0, w, x, 1, False)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 def test_qmm_quantize_golden():
