@@ -38,6 +38,7 @@ sys.path.insert(0, ROOT)
 METRIC = "Q4_K GEMV HBM GB/s (% peak) at M=1; Q4_K GEMM int8 TOPS (% peak) at M=512"
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E
 PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 K, N = 4096, 14336        # config 3 gate/up, config 4
 Q4K_ROW = K // 256 * 144
@@ -306,7 +307,9 @@ def prefill_sweep(ms: list[int], weights, gen) -> list[dict]:
         log(f"prefill sweep M={m} x{iters}")
         ms_call = time_graph(lambda i, st: dq.matmul(weights[i % ng], x, m, K, y, N, None, st), iters, 3)
         tops = 2.0 * m * N * K / (ms_call * 1e-3) / 1e12
-        out.append({"m": m, "kernel": "skinny MFMA GEMV" if m <= 16 else "MFMA GEMM",
+        cus = torch.cuda.get_device_properties(0).multi_processor_count
+        f16 = m > 128 and -(-m // 128) * -(-N // 256) * 8 >= 5 * cus  # the f16 GEMM's rule (gemm_h16_pays)
+        out.append({"m": m, "kernel": "skinny MFMA GEMV" if m <= 16 else "f16 MFMA GEMM" if f16 else "int8 MFMA GEMM",
                     "ms_per_call": round(ms_call, 4), "tops": round(tops, 1),
                     "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2), "tokens_per_s": round(m / (ms_call * 1e-3), 1)})
         del x, y
@@ -416,7 +419,7 @@ def ceilings(steps: int, warmup: int) -> dict:
     torch.cuda.empty_cache()
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     mfma = {"launch": f"{cus} workgroups x 8 waves (two per SIMD), 8 independent accumulators per wave"}
-    for label, kind, iters in (("16x16x64", 0, 4000), ("32x32x32", 1, 2000)):
+    for label, kind, iters in (("16x16x64", 0, 4000), ("32x32x32", 1, 2000), ("f16_32x32x16", 2, 2000)):
         buf = torch.empty(cus * 512, dtype=torch.int32, device="cuda")
         ops = C.c_double(0.0)
 
@@ -600,6 +603,7 @@ def main() -> None:
     ceil = ceilings(args.steps, args.warmup)
     read_ceiling = ceil["33MB"]["gbs"]
     mfma_ceiling = ceil["mfma"]["16x16x64"]["tops"]
+    f16_ceiling = ceil["mfma"]["f16_32x32x16"]["tops"]
 
     traffic = measured_traffic()
     result = {
@@ -629,6 +633,7 @@ def main() -> None:
         "read_ceiling_gbs": read_ceiling,
         "pct_of_read_ceiling": round(100 * value / read_ceiling, 2),
         "mfma_ceiling_tops": mfma_ceiling,
+        "f16_mfma_ceiling_tflops": f16_ceiling,
         "ceilings": ceil,
         "tokens_per_s": round(1e3 / ms_step, 1),
         "roofline": {
@@ -650,12 +655,13 @@ def main() -> None:
             "workload": f"config 4 prefill: Q4_K x Q8_K GEMM, M={m} K=4096 N=14336",
             "ms_per_launch": round(ms_gemm, 4),
             "tops": round(tops, 2),
-            "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2),
-            "pct_of_mfma_ceiling": round(100 * tops / mfma_ceiling, 2),
+            "matrix_core": "f16 (v_mfma_f32_32x32x16_f16 on exact integer operands)",
+            "pct_peak_f16": round(100 * tops / PEAK_F16_TFLOPS, 2),
+            "pct_of_f16_mfma_ceiling": round(100 * tops / f16_ceiling, 2),
             "tokens_per_s": round(m / (ms_gemm * 1e-3), 1),
-            "roofline": {"kernel": "dq::k_gemm_q4k_stream", "bound": "mfma", "achieved": round(tops, 2),
-                         "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4),
-                         "traffic": traffic.get("gemm_m512")},
+            "roofline": {"kernel": "dq::k_gemm_q4k_h16 (ms per dq_gemm call: + k_act16_from_q8k)", "bound": "mfma",
+                         "achieved": round(tops, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tops / PEAK_F16_TFLOPS, 4), "traffic": traffic.get("gemm_m512")},
         },
     }
     result["f32_expand_gemm"] = {

@@ -67,7 +67,8 @@ _I = C.c_int
 class QmmActs(C.Structure):
     """dq_qmm_acts: qmm::Acts (dynacore/include/dynacore/cpu/qmm.h:71-79), device pointers."""
     _fields_ = [("mode", C.c_int32), ("paired", C.c_int32), ("m", C.c_int64), ("k", C.c_int64),
-                ("hi", C.c_void_p), ("lo", C.c_void_p), ("d", C.c_void_p), ("c", C.c_void_p)]
+                ("hi", C.c_void_p), ("lo", C.c_void_p), ("d", C.c_void_p), ("c", C.c_void_p),
+                ("blocks", C.c_void_p)]
 
 
 QMM_INT8, QMM_INT16 = 0, 1  # dq_qmm_mode (qmm::ActMode)

@@ -600,23 +600,27 @@ int dq_act_quantize(int fmt, const float* x, int64_t m, int64_t k, int64_t x_str
 static int qmm_acts_ok(const dq_qmm_acts* a) {
   if (a == nullptr) return fail(DQ_INVALID_ARGUMENT, "null argument");
   if (dq_qmm_act_bytes(a->mode, a->m, a->k, a->paired) < 0 || a->hi == nullptr || a->d == nullptr || a->c == nullptr ||
-      (a->mode == DQ_QMM_INT16) != (a->lo != nullptr)) {
+      a->blocks == nullptr || (a->mode == DQ_QMM_INT16) != (a->lo != nullptr)) {
     return fail(DQ_INVALID_ARGUMENT, "qmm acts not prepared");
   }
-  if (reinterpret_cast<uintptr_t>(a->hi) % 4 != 0 || (a->lo && reinterpret_cast<uintptr_t>(a->lo) % 4 != 0)) {
-    return fail(DQ_INVALID_ARGUMENT, "qmm acts codes must be 4-byte aligned");
+  if (reinterpret_cast<uintptr_t>(a->hi) % 4 != 0 || (a->lo && reinterpret_cast<uintptr_t>(a->lo) % 4 != 0) ||
+      reinterpret_cast<uintptr_t>(a->blocks) % 16 != 0) {
+    return fail(DQ_INVALID_ARGUMENT, "qmm acts codes must be 4-byte aligned (blocks 16-byte)");
   }
   return DQ_OK;
 }
 
 static int64_t qmm_align64(int64_t v) { return (v + 63) / 64 * 64; }
+// The block format a qmm mode's rows convert to: per-32 (int8) or int16.
+static int qmm_fmt(int mode) { return mode == DQ_QMM_INT16 ? DQ_ACT_Q16 : DQ_ACT_PER32; }
 
 int64_t dq_qmm_act_bytes(int mode, int64_t m, int64_t k, int paired) {
   if ((mode != DQ_QMM_INT8 && mode != DQ_QMM_INT16) || m < 0 || k <= 0 || k % 32 != 0) return -1;
   if (m > ((int64_t)1 << 24) || k > ((int64_t)1 << 30)) return -1;
   const int64_t m_pad = paired ? (m + 1) / 2 * 2 : m;
   const int64_t code = qmm_align64(m_pad * k), scale = qmm_align64(m_pad * (k / 32) * 4);
-  return code * (mode == DQ_QMM_INT16 ? 2 : 1) + 2 * scale;
+  const int64_t blocks = qmm_align64(m * dq_act_row_bytes(qmm_fmt(mode), k));
+  return code * (mode == DQ_QMM_INT16 ? 2 : 1) + 2 * scale + blocks;
 }
 
 int dq_qmm_act_prepare(void* base, int64_t bytes, int mode, int64_t m, int64_t k, int paired, dq_qmm_acts* out,
@@ -639,6 +643,7 @@ int dq_qmm_act_prepare(void* base, int64_t bytes, int mode, int64_t m, int64_t k
   out->lo = mode == DQ_QMM_INT16 ? p + code : nullptr;
   out->d = reinterpret_cast<float*>(p + code + lo_bytes);
   out->c = reinterpret_cast<float*>(p + code + lo_bytes + scale);
+  out->blocks = p + code + lo_bytes + 2 * scale;
   if (paired && (m & 1)) {
     DQ_HIP(dq::launch_qmm_pad(m, k, out->hi, out->lo, out->d, out->c, as_stream(stream)), "qmm pad launch");
   }
@@ -658,12 +663,19 @@ int dq_qmm_quantize_rows(const float* x, int64_t x_stride, int64_t r0, int64_t r
   DQ_HIP(dq::launch_qmm_quantize(x, x_stride, r0, r1, a->k, a->mode == DQ_QMM_INT16, a->paired != 0, a->hi, a->lo, a->d,
                                  a->c, as_stream(stream)),
          "qmm quantize launch");
+  // the same rows in the block format gemv / gemm read, from the codes just written
+  const int64_t orb = dq_act_row_bytes(qmm_fmt(a->mode), a->k);
+  DQ_HIP(dq::launch_qmm_to_blocks(a->hi, a->lo, a->d, a->k, a->mode == DQ_QMM_INT16, a->paired != 0, r0, r1 - r0,
+                                  a->blocks + r0 * orb, orb, as_stream(stream)),
+         "qmm conversion launch");
   return DQ_OK;
 }
 
-// qmm's gemv / gemm on a qmm activation buffer: its rows converted once to the per-32
-// (int8) or int16 block format in the per-device scratch, then the library's GEMV
-// passes or GEMM for that format. y row r0 + r for buffer row r0 + r.
+// qmm's gemv / gemm on a qmm activation buffer: the library's GEMV passes or GEMM on
+// the buffer's rows in the per-32 (int8) or int16 block format, which
+// dq_qmm_quantize_rows wrote beside the codes. Reads only the caller's buffer (no
+// library state), so calls on disjoint [n0, n1) or row ranges may run concurrently.
+// y row r0 + r for buffer row r0 + r.
 static int qmm_matmul(const dq_weight* w, const dq_qmm_acts* a, int64_t r0, int64_t rows, int64_t n0, int64_t n1,
                       float* y, int64_t y_stride, const float* bias, void* stream, bool gemm) {
   if (int rc = qmm_acts_ok(a); rc != DQ_OK) return rc;
@@ -673,16 +685,13 @@ static int qmm_matmul(const dq_weight* w, const dq_qmm_acts* a, int64_t r0, int6
     return fail(DQ_INVALID_ARGUMENT, "rows [%lld, %lld) outside [0, %lld)", (long long)r0, (long long)(r0 + rows),
                 (long long)a->m);
   }
-  const int fmt = a->mode == DQ_QMM_INT16 ? DQ_ACT_Q16 : DQ_ACT_PER32;
-  if (int rc = check_acts(w, fmt, a->hi, rows); rc != DQ_OK) return rc;
-  if (int rc = check_out(w, rows, n0, n1, y + r0 * y_stride, y_stride); rc != DQ_OK) return rc;
-  if (rows == 0 || n0 == n1) return DQ_OK;
+  const int fmt = qmm_fmt(a->mode);
   const int64_t orb = dq_act_row_bytes(fmt, a->k);
-  void* buf = nullptr;
-  if (int rc = scratch_get(w->dev.device, (size_t)(rows * orb), &buf); rc != DQ_OK) return rc;
-  DQ_HIP(dq::launch_qmm_to_blocks(a->hi, a->lo, a->d, a->k, a->mode == DQ_QMM_INT16, a->paired != 0, r0, rows,
-                                  static_cast<uint8_t*>(buf), orb, as_stream(stream)),
-         "qmm conversion launch");
+  const uint8_t* buf = a->blocks + r0 * orb;
+  if (int rc = check_acts(w, fmt, buf, rows); rc != DQ_OK) return rc;
+  if (y == nullptr && rows > 0) return fail(DQ_INVALID_ARGUMENT, "null output");
+  if (int rc = check_out(w, rows, n0, n1, rows > 0 ? y + r0 * y_stride : y, y_stride); rc != DQ_OK) return rc;
+  if (rows == 0 || n0 == n1) return DQ_OK;
   if (gemm && dq::gemm_supported(w->dev.dtype, fmt)) {
     return dq_gemm(w, fmt, buf, rows, n0, n1, y + r0 * y_stride, y_stride, bias, stream);
   }

@@ -8,10 +8,10 @@
 //   plane and one 1 KB load of the header plane, at the GEMV's offsets), and one fp32
 //   store per row. Its time is what the GEMV would take if its arithmetic, LDS
 //   staging, barrier and in-order chain were free.
-// - dqc_mfma_rate: back-to-back int8 MFMAs (v_mfma_i32_16x16x64_i8 or
-//   v_mfma_i32_32x32x32_i8), eight independent accumulators per wave, two waves per
-//   SIMD on every CU: the int8 matrix rate the GEMM could reach at the clock the
-//   device runs under MFMA load.
+// - dqc_mfma_rate: back-to-back MFMAs (int8 v_mfma_i32_16x16x64_i8 or
+//   v_mfma_i32_32x32x32_i8, or f16 v_mfma_f32_32x32x16_f16), eight independent
+//   accumulators per wave, two waves per SIMD on every CU: the matrix rate a GEMM could
+//   reach at the clock the device runs under MFMA load.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -53,6 +53,30 @@ __global__ __launch_bounds__(1024) void k_read_q4k(const uint8_t* __restrict__ q
     for (int i = 1; i < nw; ++i) x ^= fold[i][r];
     out[G * 64 + r] = __builtin_bit_cast(float, x & 0x3FFFFFFFu);
   }
+}
+
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
+
+__global__ __launch_bounds__(512) void k_mfma_rate_f16(int iters, int* __restrict__ out) {
+  const int l = threadIdx.x & 63;
+  const v4u a = {(u32)(l * 0x00010001u), (u32)(l + 1), (u32)(l ^ 7), 3u};
+  const v4u b = {(u32)(l * 0x00030001u), 5u, (u32)(l + 9), (u32)(l * 3)};
+  v16f_t c[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c[j] = v16f_t{};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      c[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_t, a), __builtin_bit_cast(v8h_t, b), c[j], 0,
+                                                    0, 0);
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += c[j][e];
+  out[blockIdx.x * blockDim.x + threadIdx.x] = (int)s;
 }
 
 template <bool k32>
@@ -108,18 +132,20 @@ __attribute__((visibility("default"))) int dqc_read_q4k(const void* qs, const vo
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
-// workgroups of 8 waves, each wave iters x 8 MFMAs of the kind (0: 16x16x64, 1:
-// 32x32x32); out: workgroups * 512 ints. Returns the int8 operations of the launch
-// through ops (2 M N K per MFMA).
+// workgroups of 8 waves, each wave iters x 8 MFMAs of the kind (0: int8 16x16x64, 1:
+// int8 32x32x32, 2: f16 32x32x16); out: workgroups * 512 ints. Returns the operations
+// of the launch through ops (2 M N K per MFMA).
 __attribute__((visibility("default"))) int dqc_mfma_rate(int workgroups, int iters, int kind, int* out, double* ops,
                                                          void* stream) {
-  if (out == nullptr || ops == nullptr || workgroups <= 0 || iters <= 0 || (kind != 0 && kind != 1)) return 1;
+  if (out == nullptr || ops == nullptr || workgroups <= 0 || iters <= 0 || kind < 0 || kind > 2) return 1;
   if (kind == 0) {
     hipLaunchKernelGGL(k_mfma_rate<false>, dim3((unsigned)workgroups), dim3(512), 0, (hipStream_t)stream, iters, out);
-  } else {
+  } else if (kind == 1) {
     hipLaunchKernelGGL(k_mfma_rate<true>, dim3((unsigned)workgroups), dim3(512), 0, (hipStream_t)stream, iters, out);
+  } else {
+    hipLaunchKernelGGL(k_mfma_rate_f16, dim3((unsigned)workgroups), dim3(512), 0, (hipStream_t)stream, iters, out);
   }
-  *ops = (double)workgroups * 8 * iters * 8 * 2.0 * (kind == 0 ? 16.0 * 16 * 64 : 32.0 * 32 * 32);
+  *ops = (double)workgroups * 8 * iters * 8 * 2.0 * (kind == 0 ? 16.0 * 16 * 64 : kind == 1 ? 32.0 * 32 * 32 : 32.0 * 32 * 16);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

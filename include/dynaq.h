@@ -167,9 +167,11 @@ typedef struct dq_qmm_acts {
   uint8_t* lo; /* DQ_QMM_INT16 only, else NULL */
   float* d;
   float* c;
+  uint8_t* blocks; /* the m rows as DQ_ACT_PER32 (int8) / DQ_ACT_Q16 (int16) blocks, row layout */
 } dq_qmm_acts;
 /* Bytes ActBuffer::prepare lays out for the shape (qmm_reference.cpp:440-454): codes,
- * low bytes (int16), d and c, each region rounded up to 64 bytes; -1 if invalid. */
+ * low bytes (int16), d and c, each region rounded up to 64 bytes, then (past the
+ * reference's regions) the rows in the block format gemv / gemm read; -1 if invalid. */
 DQ_API int64_t dq_qmm_act_bytes(int mode, int64_t m, int64_t k, int paired);
 /* ActBuffer::prepare on a caller's device buffer (64-byte aligned, at least
  * dq_qmm_act_bytes): fills *out and, for a paired buffer of odd m, zeroes the pad
@@ -177,8 +179,9 @@ DQ_API int64_t dq_qmm_act_bytes(int mode, int64_t m, int64_t k, int paired);
 DQ_API int dq_qmm_act_prepare(void* base, int64_t bytes, int mode, int64_t m, int64_t k, int paired,
                               dq_qmm_acts* out, void* stream);
 /* ActBuffer::quantize_rows (qmm_reference.cpp:472-488): rows [r0, r1) of x (row r at
- * x + r * x_stride floats, device memory) into a prepared buffer. Disjoint row
- * ranges may be quantized by separate calls. */
+ * x + r * x_stride floats, device memory) into a prepared buffer: the codes, d and c,
+ * and the same rows in the blocks region. Disjoint row ranges may be quantized by
+ * separate calls. */
 DQ_API int dq_qmm_quantize_rows(const float* x, int64_t x_stride, int64_t r0, int64_t r1, const dq_qmm_acts* a,
                                 void* stream);
 /* qmm::Kernels::gemv (dynacore/include/dynacore/cpu/qmm.h:125-126): y[(r0 + r) * y_stride + n]
@@ -186,12 +189,13 @@ DQ_API int dq_qmm_quantize_rows(const float* x, int64_t x_stride, int64_t r0, in
  * layout, + bias. The codes and d equal the per-32 (int8) / int16 block formats' (same
  * quantizer arithmetic), so this is dq_gemv on DQ_ACT_PER32 / DQ_ACT_Q16 rows: bit-identical
  * to it, within the fp32 tolerance of qmm's own order (qmm_reference.cpp:68-114). No
- * kGemvMaxRows limit. */
+ * kGemvMaxRows limit. Reads the buffer's blocks region only (no library state, as the
+ * reference's pure functions): calls on disjoint [n0, n1) ranges may run concurrently. */
 DQ_API int dq_qmm_gemv(const dq_weight* w, int64_t n0, int64_t n1, const dq_qmm_acts* a, int64_t r0, int rows,
                        float* y, int64_t y_stride, const float* bias, void* stream);
 /* qmm::Kernels::gemm (qmm.h:128-129): every row of the buffer (the reference expects the
  * pair layout; both are accepted), on the MFMA GEMM where the format has one (Q8_0 / Q4_0
- * per-32), else the GEMV passes. The gemm scratch is the library's. */
+ * per-32), else the GEMV passes. Reads the blocks region, as dq_qmm_gemv. */
 DQ_API int dq_qmm_gemm(const dq_weight* w, int64_t n0, int64_t n1, const dq_qmm_acts* a, float* y, int64_t y_stride,
                        const float* bias, void* stream);
 

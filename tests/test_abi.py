@@ -49,7 +49,7 @@ def test_ceiling_probe_library_is_separate():
     lib.dqc_mfma_rate.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.POINTER(C.c_double), C.c_void_p]
     assert lib.dqc_read_q4k(None, None, 224, 16, 16, None, None) == 1
     assert lib.dqc_read_q4k(1, 1, 224, 16, 3, 1, None) == 1  # waves must divide the blocks
-    assert lib.dqc_mfma_rate(256, 10, 2, 1, C.byref(C.c_double()), None) == 1  # unknown MFMA kind
+    assert lib.dqc_mfma_rate(256, 10, 3, 1, C.byref(C.c_double()), None) == 1  # unknown MFMA kind
     out = subprocess.run(["nm", "-D", "--defined-only", dq.lib_path()], capture_output=True, text=True).stdout
     assert "dqc_" not in out
 
@@ -147,13 +147,15 @@ def test_qmm_buffer_layout_and_validation_without_gpu():
     row ranges are rejected before any GPU call."""
     import ctypes as C
 
-    assert dq.qmm_act_bytes(dq.QMM_INT8, 3, 64, False) == 192 + 2 * 64
-    assert dq.qmm_act_bytes(dq.QMM_INT8, 3, 64, True) == 256 + 2 * 64
-    assert dq.qmm_act_bytes(dq.QMM_INT16, 2, 4096, True) == 2 * 8192 + 2 * 1024
+    # + the rows as per-32 (40 B) / int16 (72 B) blocks per 32 values, rounded to 64
+    assert dq.qmm_act_bytes(dq.QMM_INT8, 3, 64, False) == 192 + 2 * 64 + 256
+    assert dq.qmm_act_bytes(dq.QMM_INT8, 3, 64, True) == 256 + 2 * 64 + 256
+    assert dq.qmm_act_bytes(dq.QMM_INT16, 2, 4096, True) == 2 * 8192 + 2 * 1024 + 2 * 128 * 72
     for bad in [(2, 1, 32, 0), (0, 1, 48, 0), (0, -1, 32, 0), (0, 1, 0, 0)]:
         assert dq.lib().dq_qmm_act_bytes(*bad) == -1
     a = dq.qmm_act_prepare(1 << 20, dq.qmm_act_bytes(dq.QMM_INT16, 4, 256, True), dq.QMM_INT16, 4, 256, True)
-    assert (a.hi, a.lo, a.d, a.c) == (1 << 20, (1 << 20) + 1024, (1 << 20) + 2048, (1 << 20) + 2048 + 128)
+    assert (a.hi, a.lo, a.d, a.c, a.blocks) == (1 << 20, (1 << 20) + 1024, (1 << 20) + 2048, (1 << 20) + 2048 + 128,
+                                                (1 << 20) + 2048 + 256)
     with pytest.raises(dq.DqError):
         dq.qmm_act_prepare((1 << 20) + 32, 1 << 16, dq.QMM_INT8, 4, 256, False)  # misaligned
     with pytest.raises(dq.DqError):
