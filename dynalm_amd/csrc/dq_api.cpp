@@ -285,6 +285,9 @@ int check_out(const dq_weight* w, int64_t m, int64_t n0, int64_t n1, float* y, i
 bool use_gemm(const dq::WeightDev& w, int fmt, int64_t m) {
   if (!dq::gemm_supported(w.dtype, fmt)) return false;
   if (w.dtype == DQ_Q8_0 || w.dtype == DQ_Q4_0) return m >= 13;
+  // Q4_K x per-32: the 128-row f16 GEMM against GEMV passes of 4 rows, which read the
+  // weights once per pass (the GEMM takes about as long as 10 passes at N = 14336)
+  if (fmt == DQ_ACT_PER32) return m > 64 && dq::gemm_p32_ok(w, m, 0, w.n);
   if (w.dtype == DQ_Q6_K) {
     return m > dq::kSkinnyMaxRows ||
            (m > DQ_GEMV_MAX_ROWS && (!dq::gemv_mma_lds_ok(w.nblk, m) || w.n >= 4096));
@@ -371,6 +374,9 @@ size_t matmul_scratch_bytes(const dq_weight* w, int fmt, int64_t m) {
   if (f == DQ_ACT_F32) return gemv_split_bytes(w->dev, f, m < 8 ? m : 8);  // the rows are read in place
   size_t acts = round256((size_t)(m * dq_act_row_bytes(f, w->dev.k)));
   if (f == DQ_ACT_Q8_K && gemm_h16_pays(w->dev, m, 0, w->dev.n)) acts = round256((size_t)act16_bytes(m, w->dev.k));
+  if (f == DQ_ACT_PER32 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, f, m)) {
+    acts += round256((size_t)act32_bytes(m, w->dev.k));  // the per-32 rows, then their act32 layout
+  }
   return acts + gemv_split_bytes(w->dev, f, m < 8 ? m : 8);
 }
 
@@ -438,6 +444,20 @@ int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int6
   }
   if (fmt == DQ_ACT_Q8_K && use_gemm(w->dev, fmt, m) && gemm_h16_pays(w->dev, m, 0, w->dev.n)) {
     return gemm_h16_from_x(w, x, m, x_stride, y, y_stride, bias, s, r);
+  }
+  if (fmt == DQ_ACT_PER32 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, fmt, m)) {
+    // Q4_K x per-32 prefill: per-32 rows, their f16 operand layout, the f16 GEMM (all
+    // in the region when one is given)
+    const size_t rows_bytes = round256((size_t)(m * arb));
+    void* buf = nullptr;
+    if (int rc = acts_buffer(w->dev.device, rows_bytes + (size_t)act32_bytes(m, w->dev.k), r, &buf); rc != DQ_OK) {
+      return rc;
+    }
+    uint8_t* a32 = static_cast<uint8_t*>(buf) + rows_bytes;
+    if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, buf, stream); rc != DQ_OK) return rc;
+    DQ_HIP(launch_act32_from_p32(static_cast<const uint8_t*>(buf), arb, m, w->dev.k, a32, s), "act32 conversion launch");
+    DQ_HIP(launch_gemm_p32(w->dev, a32, m, 0, w->dev.n, y, y_stride, bias, s), "gemm launch");
+    return DQ_OK;
   }
   void* acts = nullptr;
   if (int rc = acts_buffer(w->dev.device, (size_t)(m * arb), r, &acts); rc != DQ_OK) return rc;
@@ -692,7 +712,7 @@ static int qmm_matmul(const dq_weight* w, const dq_qmm_acts* a, int64_t r0, int6
   if (y == nullptr && rows > 0) return fail(DQ_INVALID_ARGUMENT, "null output");
   if (int rc = check_out(w, rows, n0, n1, rows > 0 ? y + r0 * y_stride : y, y_stride); rc != DQ_OK) return rc;
   if (rows == 0 || n0 == n1) return DQ_OK;
-  if (gemm && dq::gemm_supported(w->dev.dtype, fmt)) {
+  if (gemm && use_gemm(w->dev, fmt, rows)) {
     return dq_gemm(w, fmt, buf, rows, n0, n1, y + r0 * y_stride, y_stride, bias, stream);
   }
   return dq_gemv(w, fmt, buf, rows, n0, n1, y + r0 * y_stride, y_stride, bias, stream);
@@ -756,6 +776,17 @@ int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
       DQ_HIP(dq::launch_act16_from_q8k(static_cast<const uint8_t*>(acts), arb, m, w->dev.k, ws, as_stream(stream)),
              "act16 conversion launch");
       DQ_HIP(dq::launch_gemm_h16(w->dev, ws, m, n0, n1, y, y_stride, bias, as_stream(stream)), "gemm launch");
+      return DQ_OK;
+    });
+  }
+  if (fmt == DQ_ACT_PER32 && w->dev.dtype == DQ_Q4_K) {
+    // Q4_K x per-32: the codes as f16 operands (one conversion launch), then the f16 GEMM
+    if (!dq::gemm_p32_ok(w->dev, m, n0, n1)) return fail(DQ_UNSUPPORTED, "m too large");
+    const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
+    return with_stream_ws(w->dev.device, stream, (size_t)dq::act32_bytes(m, w->dev.k), [&](uint8_t* ws) -> int {
+      DQ_HIP(dq::launch_act32_from_p32(static_cast<const uint8_t*>(acts), arb, m, w->dev.k, ws, as_stream(stream)),
+             "act32 conversion launch");
+      DQ_HIP(dq::launch_gemm_p32(w->dev, ws, m, n0, n1, y, y_stride, bias, as_stream(stream)), "gemm launch");
       return DQ_OK;
     });
   }

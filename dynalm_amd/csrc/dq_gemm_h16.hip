@@ -58,6 +58,7 @@
 #include <stdint.h>
 
 #include "dq_device.h"
+#include "dq_f16mma.h"
 #include "dq_internal.h"
 #include "dq_mfma.h"
 #include "dq_quant.h"
@@ -65,9 +66,6 @@
 namespace dq {
 
 namespace {
-
-typedef float v16f_t __attribute__((ext_vector_type(16)));
-typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
 
 constexpr int kHM = 128, kHN = 256;  // activation rows x weight rows per workgroup
 constexpr int kHThreads = 512;       // 8 waves, two per SIMD
@@ -78,47 +76,6 @@ constexpr int kHBs = 0, kHDa = 4096, kHSb = 4608;
 constexpr int kHSbBase = 2 * kHPos;
 constexpr int kHLds = kHSbBase + 2 * kHSb;
 static_assert(kHLds <= 160 * 1024, "LDS");
-
-DQ_DEV v16f_t mfma_h(v4u a, v4u b, v16f_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h_t, a), __builtin_bit_cast(v8h_t, b), c, 0, 0,
-                                                0);
-}
-DQ_DEV v4u lds16(const uint8_t* p) { return *reinterpret_cast<const v4u*>(p); }
-
-// Direct-to-LDS buffer loads: lane l's 16 (4) bytes land at dst + 16 l (4 l).
-DQ_DEV void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* dst, u32 voff, u32 soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
-}
-DQ_DEV void dma4(__amdgpu_buffer_rsrc_t r, uint8_t* dst, u32 voff, u32 soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4, voff, soff, 0, 0);
-}
-
-// LDS reads that stay where they are written: ordered with the other volatile
-// accesses and the empty asm statements that pin the results computed before them.
-DQ_DEV v4u lds16v(const uint8_t* p) {
-  typedef const volatile __attribute__((address_space(3))) v4u lds_v4u;
-  return *(lds_v4u*)(p);
-}
-DQ_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-// Eight Q8_K codes (two dwords: values v .. v + 3 and v + 32 .. v + 35) as f16 in the
-// operand's half order {v, v + 2, v + 1, v + 3, v + 32, v + 34, v + 33, v + 35}.
-DQ_DEV v4u codes_f16(u32 c0, u32 c1) {
-  auto h = [](u32 w, int i) -> u32 {
-    return (u32)__builtin_bit_cast(uint16_t, (_Float16)(float)(int8_t)((w >> (8 * i)) & 0xFFu));
-  };
-  return v4u{h(c0, 0) | (h(c0, 2) << 16), h(c0, 1) | (h(c0, 3) << 16), h(c1, 0) | (h(c1, 2) << 16),
-             h(c1, 1) | (h(c1, 3) << 16)};
-}
-DQ_DEV u32 f16_pair(int a, int b) {
-  return (u32)__builtin_bit_cast(uint16_t, (_Float16)(float)a) |
-         ((u32)__builtin_bit_cast(uint16_t, (_Float16)(float)b) << 16);
-}
-
-template <int H>
-struct Pair {
-  static constexpr int h = H;
-};
 
 }  // namespace
 

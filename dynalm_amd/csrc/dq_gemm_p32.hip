@@ -1,0 +1,343 @@
+// dq_gemm_p32.hip -- prefill GEMM for Q4_K weights x per-32 activations (qmm's int8
+// contract: one scale d and one code sum per 32 values) on the f16 matrix cores, and
+// the activation layout it reads.
+//
+// Arithmetic. qmm's reference for Q4_K (dot_row_ref, qmm_reference.cpp:68-93, with
+// Fmt<kQ4_K>'s s32 = d sc_j and mn = dmin m_j, qmm_unpack.h) sums per sub-block j
+// (32 values) of every super-block
+//   acc += (d sc_j) da P_j - (dmin m_j) c_j,   P_j = sum_t q_t a_t,  c_j = da (code sum).
+// P_j, an integer below 2^24 in magnitude (15 * 128 * 32), runs on
+// v_mfma_f32_32x32x16_f16 with A = the int8 codes as f16 and B = the nibble q as the
+// raw 16-bit integer, which the matrix core reads as the f16 subnormal q * 2^-24: two
+// K-steps per sub-block into a fresh accumulator, which ends at exactly P_j * 2^-24.
+// Then per output and sub-block
+//   acc = fma(da * (d sc_j 2^24), P_j 2^-24, acc)               (two VALU operations)
+// and the mins term as fp32 matrix products on v_mfma_f32_32x32x2_f32, two
+// sub-blocks per instruction straight into the output accumulator:
+//   acc = acc + sum_j c_j (-dmin m_j).
+// Every product is exact or rounded once, but the summation order is not qmm's (nor
+// the per-32 GEMV's, kernels_generic.cpp:261-279): the outputs agree within the fp32
+// tolerance of a K-term dot product, not bit for bit.
+//
+// Work split. As the Q8_K f16 GEMM (dq_gemm_h16.hip): a workgroup owns 128 activation
+// rows x 256 weight rows with 8 waves, two per SIMD; wave w owns weight rows 32 w ..
+// 32 w + 31 against the four 32-row activation tiles, each lane one weight row whose
+// B operands it builds from nibbles it loads itself. Here K-steps 2 j and 2 j + 1
+// belong to sub-block j alone; after them the wave scales the sub-block's four tiles
+// into its accumulators (VALU) while the SIMD's other wave runs MFMAs. A super-block's
+// operands (128 rows x 256 codes as f16, 64 KB), activation scales and mins operands
+// (4 + 4 KB) go to LDS one interval ahead by direct-to-LDS loads spread over the
+// K-steps, into a ring of two; one barrier per super-block.
+//
+// Activation layout ("act32", k_act32_from_p32 from per-32 rows), for M_pad = m
+// rounded up to 128 rows (zero rows past m), T = M_pad / 32 row tiles, nb super-blocks:
+//   codes  [T][nb][k (16)][lane (64)][8 halves]  lane l: row 32 T + l % 32, half
+//          hh = l / 32; K-step k = 2 j + h holds values 32 j + 16 hh + 8 h + {0, 2, 1,
+//          3, 4, 6, 5, 7} of the super-block (sub-block j only)
+//   da     [T][nb][j (8)][32 rows] floats
+//   c      [T][nb][kk (4)][lane (64)] floats: c of row l % 32, sub-block 2 kk + l / 32
+// The K order is the one in which a lane's B operand comes out of two dwords of its
+// weight row's nibbles: values 32 j + t of sub-block j are the low (j even) or high
+// (j odd) nibbles of qs bytes 32 (j / 2) + t (quant_formats.cpp:150-167), so K-step
+// (j, h) of lane half hh reads bytes 8 h .. 8 h + 7 of qs chunk 2 (j / 2) + hh (16-byte
+// chunks; the plane stores the high nibbles XOR 8).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dq_device.h"
+#include "dq_f16mma.h"
+#include "dq_internal.h"
+#include "dq_mfma.h"
+
+namespace dq {
+
+namespace {
+
+constexpr int kPM = 128, kPN = 256;  // activation rows x weight rows per workgroup
+constexpr int kPThreads = 512;       // 8 waves, two per SIMD
+// Super-block buffer: operands [k (16)][t (4)][lane (64)][16 B], then the activation
+// scales [t (4)][j (8)][row (32)] and the mins operands [t (4)][kk (4)][lane (64)].
+constexpr int kPCodes = 65536, kPDa = kPCodes, kPC = kPDa + 4096;
+constexpr int kPBuf = kPC + 4096;
+constexpr int kPLds = 2 * kPBuf;
+static_assert(kPLds <= 160 * 1024, "LDS");
+
+DQ_DEV v16f_t mfma_f32_k2(float a, float b, v16f_t c) { return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0); }
+
+}  // namespace
+
+// ---------------------------------------------------------------- act32 writer
+
+// Per-32 rows (40 B per 32 values: float d, int32 code sum, int8 codes[32]) -> act32.
+// Workgroup (s, T): one 32-row tile's super-block s; rows past m are zeros.
+__global__ __launch_bounds__(256) void k_act32_from_p32(const uint8_t* __restrict__ acts, int64_t arb, int64_t m,
+                                                        int nb, int64_t m_pad, uint8_t* __restrict__ out) {
+  const int t = threadIdx.x;
+  const int s = blockIdx.x;
+  const int64_t T = blockIdx.y;
+  const int64_t codes_bytes = m_pad * nb * 512, da_bytes = m_pad / 32 * nb * 1024;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int u = t + 256 * e, k = u >> 6, l = u & 63, hh = l >> 5;
+    const int64_t row = 32 * T + (l & 31);
+    v4u o = {0u, 0u, 0u, 0u};
+    if (row < m) {
+      const uint8_t* q = acts + row * arb + (int64_t)(8 * s + (k >> 1)) * 40 + 8 + 16 * hh + 8 * (k & 1);
+      o = codes_f16(*reinterpret_cast<const u32*>(q), *reinterpret_cast<const u32*>(q + 4));
+    }
+    *reinterpret_cast<v4u*>(out + ((T * nb + s) * 16 + k) * 1024 + l * 16) = o;
+  }
+  {
+    // da: thread t = 32 j + r
+    const int j = t >> 5;
+    const int64_t row = 32 * T + (t & 31);
+    const float d = row < m ? *reinterpret_cast<const float*>(acts + row * arb + (int64_t)(8 * s + j) * 40) : 0.0f;
+    *reinterpret_cast<float*>(out + codes_bytes + (T * nb + s) * 1024 + t * 4) = d;
+  }
+  {
+    // c = d * (code sum): thread t = 64 kk + lane, sub-block 2 kk + lane / 32
+    const int l = t & 63, j = 2 * (t >> 6) + (l >> 5);
+    const int64_t row = 32 * T + (l & 31);
+    float c = 0.0f;
+    if (row < m) {
+      const uint8_t* b = acts + row * arb + (int64_t)(8 * s + j) * 40;
+      c = *reinterpret_cast<const float*>(b) * (float)*reinterpret_cast<const int32_t*>(b + 4);
+    }
+    *reinterpret_cast<float*>(out + codes_bytes + da_bytes + (T * nb + s) * 1024 + t * 4) = c;
+  }
+}
+
+// ---------------------------------------------------------------- the GEMM
+
+// One workgroup: activation rows [128 tm, + 128) x weight rows [nbase0 + 256 tn, + 256),
+// all super-blocks. Arguments as launch_gemm_p32.
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_q4k_p32(
+    const uint8_t* __restrict__ qs_plane, const uint8_t* __restrict__ hdr_plane, int nb, int64_t nbase0, int64_t n_pad,
+    int64_t n0, int64_t n1, const uint8_t* __restrict__ act32, int64_t m_pad, int64_t m, float* __restrict__ y,
+    int64_t ys, const float* __restrict__ bias, int tiles_m, int xcd_map) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int t = threadIdx.x, lane = t & 63;
+  const int li = lane & 31, hh = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+
+  // Workgroups with the same weight rows on one XCD (workgroups are dealt to the 8
+  // XCDs round-robin), so the activation tiles of a weight tile share its L2.
+  const int L = blockIdx.x;
+  int tn, tm;
+  if (xcd_map) {
+    tn = 8 * (L / (8 * tiles_m)) + (L & 7);
+    tm = (L >> 3) % tiles_m;
+  } else {
+    tn = L / tiles_m;
+    tm = L - tn * tiles_m;
+  }
+  tn = __builtin_amdgcn_readfirstlane(tn);
+  tm = __builtin_amdgcn_readfirstlane(tm);
+  const int64_t nbase = nbase0 + (int64_t)kPN * tn;
+  const int64_t mbase = (int64_t)tm * kPM;
+
+  const int64_t codes_bytes = m_pad * nb * 512, da_bytes = m_pad / 32 * nb * 1024;
+  const auto ra = rsrc(act32, (u32)(codes_bytes + 2 * da_bytes));
+  const auto rq = rsrc(qs_plane, (u32)(n_pad * nb * 128));
+  const auto rh = rsrc(hdr_plane, (u32)(n_pad * nb * 16));
+
+  // ---- this wave's loads. Operands of super-block s: blocks jb = 8 wave + i (i < 8) of
+  // the buffer, K-step jb / 4 of tile jb % 4; with piece 0 the activation scales
+  // (waves 0-3) or mins operands (waves 4-7) of tile wave % 4. The wave's weight row:
+  // 64-row group g0 + wave / 2, row 32 (wave & 1) + li; lane half hh loads qs chunks
+  // hh, 2 + hh, 4 + hh, 6 + hh of it and its header.
+  const u32 g0 = (u32)(nbase >> 6);
+  const u32 G = g0 + (u32)(wave >> 1), r64 = (u32)(32 * (wave & 1) + li);
+  const u32 vq = (G * (u32)nb * 8u + (u32)hh) * 1024u + r64 * 16u;  // + (s * 8 + 2 g) * 1024
+  const u32 vh = (G * (u32)nb * 64u + r64) * 16u;                  // + s * 1024
+
+  auto issue_piece = [&](int s, int i) {
+    uint8_t* P = lds + (s & 1) * kPBuf;
+    const int jb = 8 * wave + i;
+    const int64_t T = 4 * (int64_t)tm + (jb & 3);
+    dma16(ra, P + jb * 1024, (u32)(lane * 16), (u32)(((T * nb + s) * 16 + (jb >> 2)) * 1024));
+    if (i == 0) {
+      const int tt = wave & 3;
+      const int64_t Tb = 4 * (int64_t)tm + tt;
+      if (wave < 4) {
+        dma16(ra, P + kPDa + tt * 1024, (u32)(lane * 16), (u32)(codes_bytes + (Tb * nb + s) * 1024));
+      } else {
+        dma16(ra, P + kPC + tt * 1024, (u32)(lane * 16), (u32)(codes_bytes + da_bytes + (Tb * nb + s) * 1024));
+      }
+    }
+  };
+  // The nibbles of the current super-block: nib[g] = qs chunk 2 g + hh, read by the
+  // K-steps of sub-blocks 2 g and 2 g + 1 (K-steps 4 g .. 4 g + 3); the MFMA phase
+  // reloads nib[g] with the next super-block's after its last use. Super-blocks past
+  // the end reload the last one.
+  v4u nib[4], hdr, hdr_n;
+  auto ld_nib = [&](int s, int g) { return ld16(rq, vq + (u32)((s < nb ? s : nb - 1) * 8 + 2 * g) * 1024u); };
+  auto ld_hdr = [&](int s) { return ld16(rh, vh + (u32)(s < nb ? s : nb - 1) * 1024u); };
+
+  v16f_t acc[4], S[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    acc[mt] = v16f_t{};
+    S[mt] = v16f_t{};
+  }
+
+  // Super-block s: per sub-block j its two K-steps (four MFMA chains, one per
+  // activation tile) and then its scaling into the accumulators; the next super-block's
+  // loads spread over the K-steps; at the end the mins products.
+  auto run_sb = [&](int s) {
+    const bool next = s + 1 < nb;
+    hdr_n = ld_hdr(s + 1);
+    const uint8_t* P = lds + __builtin_amdgcn_readfirstlane((s & 1) * kPBuf);
+    // d sc_j 2^24 of this lane's weight row (get_scale_min_k4, quant_formats.h:62-70)
+    const float d24 = h2f(hdr.x) * 16777216.0f;
+    const u32 scA = hdr.y & 0x3F3F3F3Fu;
+    const u32 scB = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+    float ds[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ds[j] = d24 * (float)((j < 4 ? scA : scB) >> (8 * (j & 3)) & 0xFFu);
+    // B operand of K-step k = 2 j + h: 8 nibbles of two dwords, in the pair order
+    auto build = [&](int k) -> v4u {
+      const int j = k >> 1, h = k & 1;
+      u32 x0 = nib[j >> 1][2 * h], x1 = nib[j >> 1][2 * h + 1];
+      asm volatile("" : "+v"(x0), "+v"(x1));  // keeps this K-step's operand build here
+      if (j & 1) {
+        x0 ^= 0x80808080u;  // the plane's high nibbles XOR 8, undone
+        x1 ^= 0x80808080u;
+        return v4u{(x0 >> 4) & 0x000F000Fu, (x0 >> 12) & 0x000F000Fu, (x1 >> 4) & 0x000F000Fu,
+                   (x1 >> 12) & 0x000F000Fu};
+      }
+      return v4u{x0 & 0x000F000Fu, (x0 >> 8) & 0x000F000Fu, x1 & 0x000F000Fu, (x1 >> 8) & 0x000F000Fu};
+    };
+    v4u a[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) a[tt] = lds16(P + (tt * 64 + lane) * 16);
+    v4u b = build(0);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      __builtin_amdgcn_s_setprio(2);
+      v4u an[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        S[tt] = mfma_h(a[tt], b, (k & 1) == 0 ? v16f_t{} : S[tt]);
+        an[tt] = k < 15 ? lds16(P + ((4 * (k + 1) + tt) * 64 + lane) * 16) : a[tt];
+      }
+      if (k < 15) b = build(k + 1);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) a[tt] = an[tt];
+      if ((k & 1) == 0 && next) issue_piece(s + 1, k >> 1);
+      if ((k & 3) == 3) nib[k >> 2] = ld_nib(s + 1, k >> 2);
+      __builtin_amdgcn_sched_barrier(0);
+      if (k & 1) {
+        // sub-block j = k / 2 done: acc += (da ds_j) P_j over the four tiles; the
+        // activation scales of rows 32 tt + 8 q + 4 hh .. + 3 (results r = 4 q ..)
+        __builtin_amdgcn_s_setprio(0);
+        const int j = k >> 1;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          v4u da[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) da[q] = lds16v(P + kPDa + ((tt * 8 + j) * 32 + 8 * q + 4 * hh) * 4);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[tt][r] = fmaf(as_f(da[r >> 2][r & 3]) * ds[j], S[tt][r], acc[tt][r]);
+          asm volatile("" : "+v"(acc[tt]));  // the sub-block's results exist here, not after later MFMAs
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // the mins term: acc += c_j (-dmin m_j), sub-blocks 2 kk + hh (B: this lane's row)
+    const float ndm = -h2f(hdr.x >> 16);
+    const u32 mA = hdr.z & 0x3F3F3F3Fu;
+    const u32 mB = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      // lane half hh is K index hh of the pair (2 kk, 2 kk + 1)
+      const int j = 2 * kk + hh;
+      const u32 mj = (j < 4 ? mA : mB) >> (8 * (j & 3)) & 0xFFu;
+      const float bm = ndm * (float)mj;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const float cv = as_f(lds4v(P + kPC + ((tt * 4 + kk) * 64 + lane) * 4));
+        acc[tt] = mfma_f32_k2(cv, bm, acc[tt]);
+      }
+    }
+  };
+
+  // prologue: the first super-block's operands and weights
+#pragma unroll
+  for (int i = 0; i < 8; ++i) issue_piece(0, i);
+  hdr = ld_hdr(0);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) nib[g] = ld_nib(0, g);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  lds_barrier();
+#pragma unroll 1
+  for (int s = 0; s < nb; ++s) {
+    run_sb(s);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    hdr = hdr_n;
+  }
+
+  // ---- outputs (+ bias): rows 32 mt + 8 (r / 4) + 4 hh + r % 4, weight row nbase + 32 wave + li
+  const int64_t n = nbase + 32 * wave + li;
+  const int64_t mrows = m - mbase < kPM ? m - mbase : kPM;
+  if (n >= n0 && n < n1) {
+    const float bv = bias ? bias[n] : 0.0f;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 32 * mt + 8 * (r >> 2) + 4 * hh + (r & 3);
+        if (row < mrows) {
+          const float v = acc[mt][r];
+          y[(mbase + row) * ys + n] = bias ? v + bv : v;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- host
+
+int64_t act32_rows(int64_t m) { return (m + kPM - 1) / kPM * kPM; }
+
+int64_t act32_bytes(int64_t m, int64_t k) {
+  const int64_t mp = act32_rows(m), nb = k / 256;
+  return mp * nb * 512 + 2 * (mp / 32) * nb * 1024;
+}
+
+bool gemm_p32_ok(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {
+  if (w.dtype != kQ4_K || m <= 0 || n1 <= n0 || w.nblk <= 0) return false;
+  // 32-bit buffer offsets: the qs plane plus one tile's rows past its end, and act32;
+  // the writer's grid has one row of workgroups per 32 padded rows
+  if ((w.n_pad + 4 * kRowGroup) * w.nblk * 128 >= (1ll << 32)) return false;
+  if (act32_bytes(m, w.k) >= (1ll << 32) || act32_rows(m) / 32 > 65535) return false;
+  return true;
+}
+
+hipError_t launch_act32_from_p32(const uint8_t* acts, int64_t arb, int64_t m, int64_t k, uint8_t* out,
+                                 hipStream_t s) {
+  const int64_t mp = act32_rows(m);
+  if (mp / 32 > 65535 || k % 256 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_act32_from_p32, dim3((unsigned)(k / 256), (unsigned)(mp / 32)), dim3(256), 0, s, acts, arb, m,
+                     (int)(k / 256), mp, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_p32(const WeightDev& w, const uint8_t* act32, int64_t m, int64_t n0, int64_t n1, float* y,
+                           int64_t ys, const float* bias, hipStream_t s) {
+  if (!gemm_p32_ok(w, m, n0, n1)) return hipErrorInvalidValue;
+  const int64_t nbase0 = n0 / kRowGroup * kRowGroup;
+  const int64_t tiles_n = (n1 - nbase0 + kPN - 1) / kPN;
+  const int64_t tiles_m = (m + kPM - 1) / kPM;
+  const int xcd_map = tiles_n % 8 == 0 ? 1 : 0;
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_q4k_p32),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kPLds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_gemm_q4k_p32, dim3((unsigned)(tiles_n * tiles_m)), dim3(kPThreads), kPLds, s, w.plane[0],
+                     w.plane[1], (int)w.nblk, nbase0, w.n_pad, n0, n1, act32, act32_rows(m), m, y, ys, bias,
+                     (int)tiles_m, xcd_map);
+  return hipGetLastError();
+}
+
+}  // namespace dq

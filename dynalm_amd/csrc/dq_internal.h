@@ -97,6 +97,15 @@ hipError_t launch_act16_from_q8k(const uint8_t* acts, int64_t arb, int64_t m, in
 hipError_t launch_act16_quant(const float* x, int64_t x_stride, int64_t m, int64_t k, uint8_t* out, hipStream_t s);
 hipError_t launch_gemm_h16(const WeightDev& w, const uint8_t* act16, int64_t m, int64_t n0, int64_t n1, float* y,
                            int64_t ys, const float* bias, hipStream_t s);
+// The Q4_K x per-32 GEMM on the f16 matrix cores (dq_gemm_p32.hip), qmm's int8 gemm
+// contract: 128 x 256 tiles, codes as f16 in the "act32" layout of act32_bytes(m, k)
+// bytes written from per-32 rows (launch_act32_from_p32). gemm_p32_ok: Q4_K and the
+// offsets fit 32 bits.
+int64_t act32_bytes(int64_t m, int64_t k);
+bool gemm_p32_ok(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
+hipError_t launch_act32_from_p32(const uint8_t* acts, int64_t arb, int64_t m, int64_t k, uint8_t* out, hipStream_t s);
+hipError_t launch_gemm_p32(const WeightDev& w, const uint8_t* act32, int64_t m, int64_t n0, int64_t n1, float* y,
+                           int64_t ys, const float* bias, hipStream_t s);
 // The expand-class fp32 GEMM (dq_gemm_f32.hip): weight tiles expanded to fp32 in LDS
 // and contracted with the fp32 rows x (stride xs floats) on the matrix cores; any of
 // the four weight types. Below kF32GemmMinRows rows the fp32 GEMV passes are faster.
