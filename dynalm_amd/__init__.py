@@ -38,7 +38,7 @@ __all__ = [
     "act_quantize", "gemv", "gemm", "matmul", "matmul_many", "MatmulJob", "partials_count", "debug_partials",
     "SILU", "GELU", "GELU_TANH", "act_mul", "matmul_gated", "GgufFile", "GgufTensor", "EXPORTS",
     "MatmulShape", "External", "matmul_noalloc", "NOALLOC_SCRATCH_BYTES", "Plan", "Selection",
-    "plan_defaults", "plan_ffn_down", "select", "matmul_plan", "KERNEL_NAMES",
+    "plan_defaults", "plan_ffn_down", "select", "matmul_plan", "KERNEL_NAMES", "KERNEL_QMM_GEMM", "KERNEL_QMM_GEMV",
 ]
 
 Q4_0, Q8_0, Q4_K, Q6_K = 6, 10, 14, 16
@@ -413,11 +413,12 @@ class MatmulShape(C.Structure):
 
 
 # dq_kernel: dynacore MatmulKernelId values (kernel/matmul_registry.h:33-51)
+KERNEL_QMM_GEMM, KERNEL_QMM_GEMV = 1, 2
 KERNEL_INT8_SUBSCALED, KERNEL_INT8_SUPERBLOCK, KERNEL_INT8_PER32 = 7, 8, 9
 KERNEL_INT16_ROWS, KERNEL_F32_EXPAND_GEMM, KERNEL_F32_ROW_DOT = 13, 14, 15
 F32_GEMM_MIN_ROWS = 16  # DQ_F32_GEMM_MIN_ROWS: the expand class on the matrix cores from here on
-KERNEL_NAMES = {7: "int8_subscaled", 8: "int8_superblock", 9: "int8_per32", 13: "int16_rows", 14: "f32_expand_gemm",
-                15: "f32_row_dot"}
+KERNEL_NAMES = {1: "qmm_gemm", 2: "qmm_gemv", 7: "int8_subscaled", 8: "int8_superblock", 9: "int8_per32",
+                13: "int16_rows", 14: "f32_expand_gemm", 15: "f32_row_dot"}
 
 
 class Plan(C.Structure):
@@ -425,7 +426,7 @@ class Plan(C.Structure):
     _fields_ = [("expand_min_rows", C.c_int32), ("int8_decode_max_rows", C.c_int32),
                 ("int16_decode_max_rows", C.c_int32), ("int8_superblock_min_rows", C.c_int32),
                 ("int8_superblock_max_rows", C.c_int32), ("int8_subscale_min_rows", C.c_int32),
-                ("matmul_disabled", C.c_uint32)]
+                ("matmul_disabled", C.c_uint32), ("qmm", C.c_int32), ("qmm_gemm_min_rows", C.c_int32)]
 
     def as_dict(self) -> dict:
         return {f: getattr(self, f) for f, _ in self._fields_}

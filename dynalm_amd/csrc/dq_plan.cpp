@@ -6,9 +6,10 @@
 // The GPU offers what dynacore calls, in MatmulCaps (matmul_registry.h:103-123), an
 // int8-accelerated backend with the quantizers quantize_act / _sb / _sx / 16, per-32
 // row dots for all four weight types, super-block and sub-scaled dots for Q4_K and
-// Q6_K, and int16 dots for Q8_0, Q4_K and Q6_K (the AVX2 table's coverage,
-// dynacore/cpu/avx2/kernels_avx2.cpp:1903-1964). It has none of the kernels that read
-// dynacore's interleaved x8 copies, no qmm (ARM), no SME and no external kernels of
+// Q6_K, int16 row dots for all four weight types, and qmm (qmm.h's int8 and int16
+// contracts for every weight type, with a gemm kernel for Q8_0, Q4_0 and Q4_K). It has
+// none of the kernels that read dynacore's interleaved x8 copies, no SME and no
+// external kernels of
 // its own, so selection passes over those as the reference does when their caps are
 // absent. Host code only; no GPU is needed.
 #include <hip/hip_runtime.h>
@@ -25,6 +26,10 @@ bool allowed(const dq_plan& p, int id) { return (p.matmul_disabled & (1u << id))
 
 bool kquant(int t) { return t == DQ_Q4_K || t == DQ_Q6_K; }
 
+// MatmulCaps::qmm_gemm of this GPU: the weight types whose qmm int8 rows run on a GEMM
+// kernel (dq_gemm_b32.hip, dq_gemm_p32.hip).
+bool qmm_gemm(int t) { return t == DQ_Q8_0 || t == DQ_Q4_0 || t == DQ_Q4_K; }
+
 }  // namespace
 
 namespace dq {
@@ -38,12 +43,32 @@ dq_plan default_plan() {
   p.int8_superblock_max_rows = 8;  // kernel_plan.h:81
   p.int8_subscale_min_rows = 1;    // kernel_plan.h:92
   p.matmul_disabled = 0;           // kernel_plan.h:148
+  p.qmm = 1;                       // kernel_plan.h:156
+  p.qmm_gemm_min_rows = 9;         // kernel_plan.h:158
   return p;
 }
 
 dq_selection select(const dq_matmul_shape& s, const dq_plan& p) {
   const int64_t m = s.m, k = s.k;
   const int wt = s.dtype;
+  // Native qmm kernels (matmul_registry.cpp:313-340): the activation precision the op
+  // allows, int8 per-32 up to int8_decode_max_rows rows, else int16 up to
+  // int16_decode_max_rows; the gemm from qmm_gemm_min_rows rows where it exists, else
+  // the gemv. (No external kernels and no SME precede it here.)
+  if (p.qmm && k % 32 == 0) {
+    int act = DQ_ACT_F32;
+    if (p.int8_decode_max_rows > 0) {
+      act = m <= p.int8_decode_max_rows ? DQ_ACT_PER32 : DQ_ACT_F32;
+    } else if (p.int16_decode_max_rows > 0) {
+      act = m <= p.int16_decode_max_rows ? DQ_ACT_Q16 : DQ_ACT_F32;
+    }
+    if (act != DQ_ACT_F32) {
+      if (m >= p.qmm_gemm_min_rows && qmm_gemm(wt) && allowed(p, DQ_KERNEL_QMM_GEMM)) {
+        return dq_selection{DQ_KERNEL_QMM_GEMM, act};
+      }
+      if (allowed(p, DQ_KERNEL_QMM_GEMV)) return dq_selection{DQ_KERNEL_QMM_GEMV, act};
+    }
+  }
   // The int8 family (select_int8, matmul_registry.cpp:94-191).
   if (p.int8_decode_max_rows > 0 && k % 32 == 0) {
     const bool sb_rows = k % 256 == 0 && m <= std::max(p.int8_decode_max_rows, p.int8_superblock_max_rows);
@@ -64,8 +89,8 @@ dq_selection select(const dq_matmul_shape& s, const dq_plan& p) {
     }
   }
   // int16 prefill and int16 decode tiles read interleaved copies: absent here. The
-  // int16 row kernel (DD-076, matmul_registry.cpp:407-416).
-  if (m <= p.int16_decode_max_rows && wt != DQ_Q4_0 && k % 32 == 0 && allowed(p, DQ_KERNEL_INT16_ROWS)) {
+  // int16 row kernel (DD-076, matmul_registry.cpp:407-416), every weight type.
+  if (m <= p.int16_decode_max_rows && k % 32 == 0 && allowed(p, DQ_KERNEL_INT16_ROWS)) {
     return dq_selection{DQ_KERNEL_INT16_ROWS, DQ_ACT_Q16};
   }
   // fp32: expand + GEMM for dense batches, else the row kernel (matmul_registry.cpp:418-428).

@@ -21,6 +21,8 @@ inline dq_plan to_dq_plan(const dynacore::KernelPlan& p) {
   q.int8_superblock_max_rows = p.int8_superblock_max_rows;
   q.int8_subscale_min_rows = p.int8_subscale_min_rows;
   q.matmul_disabled = p.matmul_disabled;
+  q.qmm = p.qmm ? 1 : 0;
+  q.qmm_gemm_min_rows = p.qmm_gemm_min_rows;
   return q;
 }
 

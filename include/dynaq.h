@@ -324,12 +324,14 @@ typedef struct dq_matmul_shape {
 
 /* The kernels: dynacore::MatmulKernelId values (dynacore/include/dynacore/kernel/
  * matmul_registry.h:33-51) of the ones this library implements on the GPU; the
- * others (interleaved-copy, qmm, SME, external) do not exist here. */
+ * others (interleaved-copy, SME, external) do not exist here. */
 typedef enum dq_kernel {
+  DQ_KERNEL_QMM_GEMM = 1,         /* kQmmGemm: qmm's gemm, DQ_ACT_PER32 / DQ_ACT_Q16 (validated classes) */
+  DQ_KERNEL_QMM_GEMV = 2,         /* kQmmGemv: qmm's gemv, DQ_ACT_PER32 / DQ_ACT_Q16 */
   DQ_KERNEL_INT8_SUBSCALED = 7,   /* kInt8Subscaled: DQ_ACT_SX, K-quants (validated, DD-077) */
   DQ_KERNEL_INT8_SUPERBLOCK = 8,  /* kInt8Superblock: DQ_ACT_Q8_K, K-quants (fails DD-053: opt-in) */
   DQ_KERNEL_INT8_PER32 = 9,       /* kInt8Per32: DQ_ACT_PER32 (validated, DD-053) */
-  DQ_KERNEL_INT16_ROWS = 13,      /* kInt16Rows: DQ_ACT_Q16, Q8_0 / Q4_K / Q6_K (validated, DD-076) */
+  DQ_KERNEL_INT16_ROWS = 13,      /* kInt16Rows: DQ_ACT_Q16, every weight type (validated, DD-076) */
   DQ_KERNEL_F32_EXPAND_GEMM = 14, /* kF32ExpandGemm: fp32 activations, dense x (reference class) */
   DQ_KERNEL_F32_ROW_DOT = 15,     /* kF32RowDot: fp32 activations (reference class) */
 } dq_kernel;
@@ -342,8 +344,11 @@ typedef enum dq_kernel {
 #define DQ_F32_GEMM_MIN_ROWS 16
 
 /* The matmul knobs of KernelPlan that choose among these kernels, with the
- * reference's meaning and names (kernel_plan.h:34-92); matmul_disabled is a mask
- * of (1u << dq_kernel), as KernelPlan::matmul_disabled (kernel_plan.h:144-148). */
+ * reference's meaning and names (kernel_plan.h:34-92,156-160); matmul_disabled is a
+ * mask of (1u << dq_kernel), as KernelPlan::matmul_disabled (kernel_plan.h:144-148);
+ * qmm != 0 lets the native qmm kernels take every matmul whose op allows int8 (int16)
+ * activations, qmm_gemm_min_rows the rows from which qmm's gemm replaces its gemv. A
+ * plan with qmm 0 selects as on a backend without qmm (the reference's x86 tiers). */
 typedef struct dq_plan {
   int32_t expand_min_rows;
   int32_t int8_decode_max_rows;
@@ -352,6 +357,8 @@ typedef struct dq_plan {
   int32_t int8_superblock_max_rows;
   int32_t int8_subscale_min_rows;
   uint32_t matmul_disabled;
+  int32_t qmm;
+  int32_t qmm_gemm_min_rows;
 } dq_plan;
 
 /* A selection: the kernel and the activation format it quantizes x to (DQ_ACT_F32
@@ -363,7 +370,9 @@ typedef struct dq_selection {
 
 /* KernelPlan::defaults() without its environment overrides (kernel_plan.cpp:22-90):
  * expand 2, int8 decode 4 rows, int16 0, super-block off (min 0, max 8), sub-scaled
- * from 1 row, nothing disabled. */
+ * from 1 row, nothing disabled, qmm on with its gemm from 9 rows. (The engine raises
+ * int8_decode_max_rows to 2^30 on a backend whose qmm kernels are accelerated,
+ * dynalm/src/runtime/engine.cpp:365-375, as this one is.) */
 DQ_API int dq_plan_defaults(dq_plan* out);
 /* The plan the model uses for the FFN down projection (dynalm/src/model/
  * transformer.cpp:541-550, with int8_ffn_down off and int16_ffn_down on): no int8
@@ -371,14 +380,18 @@ DQ_API int dq_plan_defaults(dq_plan* out);
  * rows while int8 decode is on. */
 DQ_API int dq_plan_ffn_down(const dq_plan* base, dq_plan* out);
 /* select_matmul (dynacore/src/kernel/matmul_registry.cpp:287-429) over this
- * library's kernels; plan NULL: the defaults. A pure function; needs no GPU.
- * DQ_INVALID_ARGUMENT for shapes validate_matmul_shape rejects. */
+ * library's kernels, with the MatmulCaps of this GPU: qmm int8 and int16 activations
+ * for every weight type and a qmm gemm for Q8_0, Q4_0 and Q4_K; the int8 per-32,
+ * super-block and sub-scaled row dots; int16 row dots for every weight type; no
+ * interleaved copies, SME or external kernels. plan NULL: the defaults. A pure
+ * function; needs no GPU. DQ_INVALID_ARGUMENT for shapes validate_matmul_shape
+ * rejects. */
 DQ_API int dq_select(const dq_matmul_shape* s, const dq_plan* plan, dq_selection* out);
 /* y = x . w^T (+ bias) under the kernel dq_select picks for this call (plan NULL:
  * the defaults): Device::matmul with the step's KernelPlan (device.h:95,161).
  * dq_matmul is this call under the all-integer plan {int8_decode_max_rows and
  * int8_superblock_max_rows unbounded, int8_superblock_min_rows 1,
- * int8_subscale_min_rows 0}. */
+ * int8_subscale_min_rows 0, qmm 0}. */
 DQ_API int dq_matmul_plan(const dq_weight* w, const dq_plan* plan, const float* x, int64_t m, int64_t x_stride,
                           float* y, int64_t y_stride, const float* bias, void* stream);
 

@@ -59,7 +59,8 @@ extern "C" {
 // One Device call on GPU `gpu`: weights w1 (and w2) of type dq_dtype [n, k] from host rows of
 // row_bytes each, uploaded with Device::upload; x [m, k] fp32 (row stride x_stride floats)
 // copied into device memory from the host; the plan KernelPlan's member defaults (plan_kind 0:
-// KernelPlan::defaults() without its environment overrides) or the all-integer plan (1: super-block int8 at every m, as dq_matmul); then
+// KernelPlan::defaults() without its environment overrides) or the all-integer plan (1: super-block int8 at every m
+// without qmm, as dq_matmul); then
 //   op 0: matmul(x, w1, bias) -> y [m, n]
 //   op 1: matmul_many({x, w1, bias, y0}, {x, w2, null, y1}) -> y [2][m][n]
 //   op 2: matmul_gated(SiLU, x, w1, w2) -> y [m, n]
@@ -115,6 +116,7 @@ int dqdev_run(int gpu, int op, int plan_kind, int dq_dtype, const void* w1_rows,
     plan.int8_superblock_max_rows = 1 << 30;
     plan.int8_superblock_min_rows = 1;
     plan.int8_subscale_min_rows = 0;
+    plan.qmm = false;  // dq_matmul's plan selects without qmm
   }
   dev.set_kernel_plan(plan);
 

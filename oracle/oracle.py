@@ -274,7 +274,7 @@ def ref():
             "ref_dot_rows16": (C.c_int, [C.c_int, _P, _P, _I64, C.c_int, _I64, _P]),
             "ref_vec_dot": (C.c_int, [C.c_int, C.c_int, _P, _P, _I64, _P]),
             "ref_select_matmul": (C.c_int, [_I64, _I64, _I64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
-                                            C.c_int, C.c_int, C.c_uint32, C.POINTER(C.c_int)]),
+                                            C.c_int, C.c_int, C.c_uint32, C.c_int, C.c_int, C.POINTER(C.c_int)]),
             "ref_expand_x86": (C.c_int, [C.c_int, _P, _P, _I64]),
             "ref_qmm_quantize": (C.c_int, [_P, _I64, _I64, _I64, C.c_int, C.c_int, _P, _P, _P, _P]),
             "ref_qmm_gemv": (C.c_int, [C.c_int, _P, _I64, _I64, _P, _I64, _I64, C.c_int, C.c_int, _P]),

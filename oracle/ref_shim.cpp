@@ -75,14 +75,16 @@ extern "C" {
 int ref_has_avx2(void) { return cpu_info().features.avx2 ? 1 : 0; }
 
 // select_matmul under a KernelPlan whose matmul knobs are given (the rest at the
-// struct's defaults, no environment) and the MatmulCaps of an int8-accelerated
-// backend without interleaved copies, qmm, SME or external kernels whose kernel
-// table has: quantize_act / _sb / _sx / 16; per-32 row dots for Q4_0, Q8_0, Q4_K,
-// Q6_K; super-block and sub-scaled dots for Q4_K, Q6_K; int16 dots for Q8_0, Q4_K,
-// Q6_K. Returns the MatmulKernelId and writes the MatmulActFormat to *act.
+// struct's defaults, no environment) and the MatmulCaps of the GPU library's
+// backend: int8-accelerated, without interleaved copies, SME or external kernels;
+// kernel table: quantize_act / _sb / _sx / 16; per-32 row dots for Q4_0, Q8_0, Q4_K,
+// Q6_K; super-block and sub-scaled dots for Q4_K, Q6_K; int16 dots for all four;
+// qmm int8 and int16 for all four (k % 32 == 0) with a gemm for Q8_0, Q4_0, Q4_K.
+// Returns the MatmulKernelId and writes the MatmulActFormat to *act.
 int ref_select_matmul(int64_t m, int64_t n, int64_t k, int dtype, int x_dense, int expand_min_rows,
                       int int8_decode_max_rows, int int16_decode_max_rows, int int8_superblock_min_rows,
-                      int int8_superblock_max_rows, int int8_subscale_min_rows, uint32_t disabled, int* act) {
+                      int int8_superblock_max_rows, int int8_subscale_min_rows, uint32_t disabled, int qmm,
+                      int qmm_gemm_min_rows, int* act) {
   if (!valid_type(dtype) || dtype == 17) return -1;
   const DType wt = static_cast<DType>(dtype);
   MatmulShape s;
@@ -99,6 +101,8 @@ int ref_select_matmul(int64_t m, int64_t n, int64_t k, int dtype, int x_dense, i
   p.int8_superblock_max_rows = int8_superblock_max_rows;
   p.int8_subscale_min_rows = int8_subscale_min_rows;
   p.matmul_disabled = disabled;
+  p.qmm = qmm != 0;
+  p.qmm_gemm_min_rows = qmm_gemm_min_rows;
   const bool kq = wt == DType::kQ4_K || wt == DType::kQ6_K;
   MatmulCaps c;
   c.int8_accelerated = true;
@@ -106,7 +110,9 @@ int ref_select_matmul(int64_t m, int64_t n, int64_t k, int dtype, int x_dense, i
   c.dot_q8_rows = true;
   c.dot_q8_sb_rows = kq;
   c.dot_q8_sx_rows = kq;
-  c.dot_q16_rows = wt != DType::kQ4_0;
+  c.dot_q16_rows = true;
+  c.qmm_int8 = c.qmm_int16 = k % 32 == 0;
+  c.qmm_gemm = wt == DType::kQ8_0 || wt == DType::kQ4_0 || wt == DType::kQ4_K;
   const MatmulSelection sel = select_matmul(s, p, c);
   if (act != nullptr) *act = static_cast<int>(sel.act);
   return static_cast<int>(sel.id);

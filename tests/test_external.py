@@ -161,9 +161,10 @@ def test_min_rows_policy_and_rejected_calls(cuda):
 
 @pytest.mark.gpu
 def test_set_plan_selects_the_contract(cuda):
-    """Device::set_kernel_plan: the FFN down plan moves a Q6_K decode call to int16
-    activations; the all-integer plan reproduces dq_matmul (the super-block class)
-    bit for bit; NULL restores the defaults (sub-scaled)."""
+    """Device::set_kernel_plan: the defaults (qmm on: qmm's gemv on per-32 rows at 4
+    rows); without qmm the sub-scaled class; the FFN down plan moves a Q6_K decode call
+    to int16 activations; the all-integer plan reproduces dq_matmul (the super-block
+    class) bit for bit; NULL restores the defaults."""
     torch = _torch()
     import dqtorch as T
 
@@ -171,19 +172,30 @@ def test_set_plan_selects_the_contract(cuda):
     rows = gguf_weights(O.Q6_K, n, k, 2000, outlier_frac=0.01)
     x = activations(m, k, 2001)
     x[:, 5::61] *= np.float32(50.0)  # outlier channels, as the down projection's input has
+    wd = O.dequantize(O.Q6_K, rows, k).astype(np.float64).reshape(n, k)
+
+    def mag_of(fmt):
+        xa = O.dequantize_act(fmt, O.quantize_act(fmt, x), k).astype(np.float64)
+        return np.abs(xa) @ np.abs(wd).T
+
     ad = dq.External(0)
+    assert dq.select(m, n, k, dq.Q6_K).kernel == dq.KERNEL_QMM_GEMV
     y_def = ad.run(x, rows, dq.Q6_K, k)
     assert np.array_equal(y_def.view(np.uint32), _dq_matmul(O.Q6_K, rows, k, x, None).view(np.uint32))
-    assert np.array_equal(y_def.view(np.uint32),
+    want32 = O.matmul(O.Q6_K, O.ACT_PER32, rows, O.quantize_act(O.ACT_PER32, x), k)
+    assert np.all(np.abs(y_def - want32) <= 2e-6 * mag_of(O.ACT_PER32) + 1e-30)
+    noqmm = dq.plan_defaults()
+    noqmm.qmm = 0
+    ad.set_plan(noqmm)
+    y_sx = ad.run(x, rows, dq.Q6_K, k)
+    assert np.array_equal(y_sx.view(np.uint32),
                           O.matmul(O.Q6_K, O.ACT_SX, rows, O.quantize_act(O.ACT_SX, x), k).view(np.uint32))
     down = dq.plan_ffn_down()
     ad.set_plan(down)
     y16 = ad.run(x, rows, dq.Q6_K, k)
     assert np.array_equal(y16.view(np.uint32), _dq_matmul(O.Q6_K, rows, k, x, None, down).view(np.uint32))
     want16 = O.matmul(O.Q6_K, O.ACT_Q16, rows, O.quantize_act(O.ACT_Q16, x), k)
-    xa = O.dequantize_act(O.ACT_Q16, O.quantize_act(O.ACT_Q16, x), k).astype(np.float64)
-    mag = np.abs(xa) @ np.abs(O.dequantize(O.Q6_K, rows, k).astype(np.float64).reshape(n, k)).T
-    assert np.all(np.abs(y16 - want16) <= 2e-6 * mag + 1e-30)
+    assert np.all(np.abs(y16 - want16) <= 2e-6 * mag_of(O.ACT_Q16) + 1e-30)
     allint = dq.Plan(2, 1 << 30, 0, 1, 1 << 30, 0, 0)
     ad.set_plan(allint)
     yq = ad.run(x, rows, dq.Q6_K, k)

@@ -88,7 +88,7 @@ def test_all_int8_plan_is_dq_matmul(cuda, t, m):
     assert np.array_equal(run_plan(w, ALL_INT8, x).view(np.uint32), host(T.matmul(w, dev(x))).view(np.uint32))
 
 
-@pytest.mark.parametrize("t", [O.Q6_K, O.Q4_K, O.Q8_0], ids=lambda t: O.TYPE_NAMES[t])
+@pytest.mark.parametrize("t", [O.Q6_K, O.Q4_K, O.Q8_0, O.Q4_0], ids=lambda t: O.TYPE_NAMES[t])
 def test_ffn_down_plan_int16(cuda, t):
     """The down projection's plan: int16 activations up to 8 rows at K = 14336."""
     import dqtorch as T
@@ -103,6 +103,29 @@ def test_ffn_down_plan_int16(cuda, t):
     y = run_plan(w, down, x)
     assert np.array_equal(y.view(np.uint32), host(T.matmul_act(w, O.ACT_Q16, dev(x))).view(np.uint32))
     assert within_terms(y, O.matmul(t, O.ACT_Q16, rows, O.quantize_act(O.ACT_Q16, x), k), t, O.ACT_Q16, rows, x, k)
+
+
+@pytest.mark.parametrize("t,m", [(O.Q4_K, 300), (O.Q4_K, 40), (O.Q8_0, 130), (O.Q6_K, 70)],
+                         ids=["q4_K-300", "q4_K-40", "q8_0-130", "q6_K-70"])
+def test_engine_qmm_plan(cuda, t, m):
+    """The engine's plan on a backend with accelerated qmm (int8 rows unbounded,
+    dynalm/src/runtime/engine.cpp:365-375): qmm's gemm on per-32 rows from 9 rows where
+    the type has one (Q4_K: the f16 GEMM above 64 rows), else its gemv; the same bits as
+    the per-32 contract's own path, within tolerance of the oracle."""
+    import dqtorch as T
+
+    k, n = 1024, 512
+    rows = gguf_weights(t, n, k, 2600 + t + m, outlier_frac=0.01)
+    x = activations(m, k, 2601 + m, outliers=False)
+    w = dq.Weight.upload(t, rows, k)
+    eng = dq.plan_defaults()
+    eng.int8_decode_max_rows = 1 << 30
+    sel = dq.select(m, n, k, t, eng)
+    assert (sel.kernel, sel.act) == (dq.KERNEL_QMM_GEMV if t == O.Q6_K else dq.KERNEL_QMM_GEMM, O.ACT_PER32)
+    y = run_plan(w, eng, x)
+    assert np.array_equal(y.view(np.uint32), host(T.matmul_act(w, O.ACT_PER32, dev(x))).view(np.uint32))
+    ok, worst = close(y, O.matmul(t, O.ACT_PER32, rows, O.quantize_act(O.ACT_PER32, x), k))
+    assert ok, f"worst error ratio {worst:.3g}"
 
 
 def test_strided_rows_select_the_row_kernel(cuda):

@@ -132,8 +132,9 @@ def test_qmm_gemv(cuda, t, mode, paired):
 
 @pytest.mark.parametrize("t", [O.Q8_0, O.Q4_0, O.Q4_K])
 def test_qmm_gemm(cuda, t):
-    """qmm::Kernels::gemm on a paired buffer of odd m: every row equals dq_gemm (Q8_0 / Q4_0
-    on the per-32 MFMA GEMM) or dq_gemv (Q4_K) on the per-32 rows bit for bit."""
+    """qmm::Kernels::gemm on a paired buffer of odd m: every row equals dq_gemm on the
+    per-32 rows bit for bit (Q8_0 / Q4_0 on the per-32 int8 MFMA GEMM, Q4_K on the f16
+    GEMM, which takes more than 64 rows)."""
     import dqtorch as T
 
     m, k, n = 67, 2048, 256
@@ -144,7 +145,7 @@ def test_qmm_gemm(cuda, t):
     y = torch.zeros((m, n), device="cuda")
     dq.qmm_gemm(w, 0, n, a, y, n, None, torch.cuda.current_stream().cuda_stream)
     acts = T.quantize(O.ACT_PER32, xd)
-    want = T.gemm(w, O.ACT_PER32, acts) if t != O.Q4_K else T.gemv(w, O.ACT_PER32, acts)
+    want = T.gemm(w, O.ACT_PER32, acts)
     assert np.array_equal(y.cpu().numpy().view(np.uint32), want.cpu().numpy().view(np.uint32))
     ok, worst = close(y.cpu().numpy(), O.matmul(t, O.ACT_PER32, w_rows, O.quantize_act(O.ACT_PER32, x), k))
     assert ok, f"worst error ratio {worst:.3g}"
