@@ -599,6 +599,32 @@ def main() -> None:
     ms_f32_rows = time_graph(f32_row_dot, 3, 1)
     tf32 = ops / (ms_f32 * 1e-3) / 1e12
 
+    # ---- the default plans: KernelPlan::defaults() with this GPU's qmm caps. Prefill under
+    # the engine's plan on a backend with accelerated qmm (int8 rows unbounded,
+    # dynalm/src/runtime/engine.cpp:365-375): qmm's gemm on per-32 rows (per-32 quantize,
+    # f16 operand layout, k_gemm_q4k_p32). Decode (M = 1) under the defaults: qmm's gemv on
+    # per-32 rows; and without qmm, the x86 tiers' sub-scaled class (the CPU baseline's).
+    eng = dq.plan_defaults()
+    eng.int8_decode_max_rows = 1 << 30
+    noqmm = dq.plan_defaults()
+    noqmm.qmm = 0
+    sel_pre = dq.select(m, N, K, dq.Q4_K, eng)
+    sel_dec, sel_x86 = dq.select(1, N, K, dq.Q4_K), dq.select(1, N, K, dq.Q4_K, noqmm)
+
+    def prefill_plan(i: int, st: int) -> None:
+        dq.matmul_plan(weights[i % ng], eng, xg, m, K, yf, N, None, st)
+
+    def decode_plan(plan):
+        return lambda i, st: dq.matmul_plan(weights[i % nc], plan, x, 1, K, y, N, None, st)
+
+    log(f"default plans: prefill M={m} ({dq.KERNEL_NAMES[sel_pre.kernel]}), decode M=1 "
+        f"({dq.KERNEL_NAMES[sel_dec.kernel]}; without qmm {dq.KERNEL_NAMES[sel_x86.kernel]})")
+    ms_pre = time_graph(prefill_plan, 20, 3)
+    ms_dec = time_graph(decode_plan(None), args.steps, args.warmup)
+    ms_dec_x86 = time_graph(decode_plan(noqmm), args.steps, args.warmup)
+    tpre = ops / (ms_pre * 1e-3) / 1e12
+    dec_bytes = Q4K_ROW * N + 4 * K + 4 * N  # weights, the fp32 row, y
+
     log("ceilings: plain read at the GEMV's launch shape, int8 MFMA rate")
     ceil = ceilings(args.steps, args.warmup)
     read_ceiling = ceil["33MB"]["gbs"]
@@ -673,6 +699,29 @@ def main() -> None:
         "roofline": {"kernel": "dq::k_gemm_f32<Q4_K>", "bound": "mfma", "achieved": round(tf32, 2),
                      "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": round(tf32 / PEAK_FP32_MFMA_TFLOPS, 4)},
     }
+    result["prefill_default_plan"] = {
+        "workload": f"config 4 prefill, M={m} K={K} N={N} Q4_K: dq_matmul_plan under KernelPlan's defaults with "
+                    f"the engine's int8 row limit on a qmm-accelerated backend (unbounded) -> "
+                    f"{dq.KERNEL_NAMES[sel_pre.kernel]} on per-32 activations",
+        "ms_per_call": round(ms_pre, 4),
+        "tflops": round(tpre, 2),
+        "tokens_per_s": round(m / (ms_pre * 1e-3), 1),
+        "roofline": {"kernel": "dq::k_gemm_q4k_p32 (ms per call: + per-32 quantize + k_act32_from_p32)",
+                     "bound": "mfma", "achieved": round(tpre, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tpre / PEAK_F16_TFLOPS, 4)},
+    }
+    result["decode_default_plan"] = {
+        "workload": f"config 3 decode, M=1 K={K} N={N} Q4_K: dq_matmul_plan under KernelPlan's defaults "
+                    f"({dq.KERNEL_NAMES[sel_dec.kernel]}, per-32 activations: one quantize launch + the GEMV)",
+        "ms_per_call": round(ms_dec, 5),
+        "gbs": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 2),
+        "roofline": {"kernel": "dq::k_gemv<Q4_K, per-32, M=1> (ms per call: + quantize)", "bound": "hbm",
+                     "achieved": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(dec_bytes / (ms_dec * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+        "without_qmm": {"kernel": dq.KERNEL_NAMES[sel_x86.kernel], "ms_per_call": round(ms_dec_x86, 5),
+                        "gbs": round(dec_bytes / (ms_dec_x86 * 1e-3) / 1e9, 2),
+                        "note": "the class cpu_baseline times (the reference's x86 default)"},
+    }
     if ms_gated is not None:
         gbytes = 2 * Q4K_ROW * N + Q8K_ROW + 4 * N
         result["gated_m1"] = {
@@ -693,6 +742,9 @@ def main() -> None:
     if not args.no_cpu:
         log("CPU baseline")
         result["cpu_baseline"] = cpu_baseline(w_host, args.cpu_seconds)
+        cpu_ms = result["cpu_baseline"].get("ms_per_call")
+        if cpu_ms:
+            result["decode_default_plan"]["without_qmm"]["speedup_vs_cpu_baseline"] = round(cpu_ms / ms_dec_x86, 2)
     result["output_checks"] = checks
     print(json.dumps(result), flush=True)
     if not all(v for key, v in checks.items() if key != "rows_checked"):
