@@ -5,29 +5,33 @@
 // Arithmetic. qmm's reference for Q4_K (dot_row_ref, qmm_reference.cpp:68-93, with
 // Fmt<kQ4_K>'s s32 = d sc_j and mn = dmin m_j, qmm_unpack.h) sums per sub-block j
 // (32 values) of every super-block
-//   acc += (d sc_j) da P_j - (dmin m_j) c_j,   P_j = sum_t q_t a_t,  c_j = da (code sum).
-// P_j, an integer below 2^24 in magnitude (15 * 128 * 32), runs on
-// v_mfma_f32_32x32x16_f16 with A = the int8 codes as f16 and B = the nibble q as the
-// raw 16-bit integer, which the matrix core reads as the f16 subnormal q * 2^-24: two
-// K-steps per sub-block into a fresh accumulator, which ends at exactly P_j * 2^-24.
-// Then per output and sub-block
-//   acc = fma(da * (d sc_j 2^24), P_j 2^-24, acc)               (two VALU operations)
+//   acc += (d sc_j) da_j P_j - (dmin m_j) c_j,   P_j = sum_t q_t a_t,  c_j = da_j (code sum).
+// sc_j P_j, an integer below 2^24 in magnitude (63 * 15 * 128 * 32), runs on
+// v_mfma_f32_32x32x16_f16 with the weight operand sc_j q as the raw 16-bit integer
+// (at most 945, read by the matrix core as the f16 subnormal sc_j q 2^-24) and the
+// activation operand the int8 codes as f16: two K-steps per sub-block into a fresh
+// accumulator, which ends at exactly sc_j P_j 2^-24. Then
+//   per sub-block:    T = fma(da_j, sc_j P_j 2^-24, T)      (one VALU operation per output)
+//   per super-block:  acc = fma(d 2^24, T, acc)             (one per output), T = 0
 // and the mins term as fp32 matrix products on v_mfma_f32_32x32x2_f32, two
 // sub-blocks per instruction straight into the output accumulator:
-//   acc = acc + sum_j c_j (-dmin m_j).
-// Every product is exact or rounded once, but the summation order is not qmm's (nor
-// the per-32 GEMV's, kernels_generic.cpp:261-279): the outputs agree within the fp32
-// tolerance of a K-term dot product, not bit for bit.
+//   acc = acc + sum_j (-dmin m_j) c_j.
+// Every product is exact or rounded once, but d multiplies the super-block's sum
+// rather than each term, and the summation order is not qmm's (nor the per-32
+// GEMV's, kernels_generic.cpp:261-279): the outputs agree within the fp32 tolerance of
+// a K-term dot product, not bit for bit.
 //
-// Work split. As the Q8_K f16 GEMM (dq_gemm_h16.hip): a workgroup owns 128 activation
-// rows x 256 weight rows with 8 waves, two per SIMD; wave w owns weight rows 32 w ..
-// 32 w + 31 against the four 32-row activation tiles, each lane one weight row whose
-// B operands it builds from nibbles it loads itself. Here K-steps 2 j and 2 j + 1
-// belong to sub-block j alone; after them the wave scales the sub-block's four tiles
-// into its accumulators (VALU) while the SIMD's other wave runs MFMAs. A super-block's
-// operands (128 rows x 256 codes as f16, 64 KB), activation scales and mins operands
-// (4 + 4 KB) go to LDS one interval ahead by direct-to-LDS loads spread over the
-// K-steps, into a ring of two; one barrier per super-block.
+// Work split. A workgroup owns 128 activation rows x 256 weight rows with 8 waves, two
+// per SIMD; wave w owns weight rows 32 w .. 32 w + 31 against the four 32-row
+// activation tiles. The weight rows are the MFMA's A operand (lane l builds row l % 32's
+// operand from nibbles it loads itself, each serving four MFMAs), the activation rows
+// its B operand, so a lane's 16 results share one activation row and the
+// per-sub-block activation scale da_j is one register per tile, read ahead of the
+// sub-block. K-steps 2 j and 2 j + 1 belong to sub-block j alone; after them the wave
+// folds the sub-block into T (VALU) while the SIMD's other wave runs MFMAs. A
+// super-block's operands (128 rows x 256 codes as f16, 64 KB), activation scales and
+// mins operands (4 + 4 KB) go to LDS one interval ahead by direct-to-LDS loads spread
+// over the K-steps, into a ring of two; one barrier per super-block.
 //
 // Activation layout ("act32", k_act32_from_p32 from per-32 rows), for M_pad = m
 // rounded up to 128 rows (zero rows past m), T = M_pad / 32 row tiles, nb super-blocks:
@@ -174,7 +178,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   auto ld_nib = [&](int s, int g) { return ld16(rq, vq + (u32)((s < nb ? s : nb - 1) * 8 + 2 * g) * 1024u); };
   auto ld_hdr = [&](int s) { return ld16(rh, vh + (u32)(s < nb ? s : nb - 1) * 1024u); };
 
-  v16f_t acc[4], S[4];
+  v16f_t acc[4], S[4], T[4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
     acc[mt] = v16f_t{};
@@ -182,83 +186,90 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   }
 
   // Super-block s: per sub-block j its two K-steps (four MFMA chains, one per
-  // activation tile) and then its scaling into the accumulators; the next super-block's
-  // loads spread over the K-steps; at the end the mins products.
+  // activation tile) and then its fold into T; the next super-block's loads spread over
+  // the K-steps, and two of the mins products per sub-block; at the end T into acc.
   auto run_sb = [&](int s) {
     const bool next = s + 1 < nb;
     hdr_n = ld_hdr(s + 1);
     const uint8_t* P = lds + __builtin_amdgcn_readfirstlane((s & 1) * kPBuf);
-    // d sc_j 2^24 of this lane's weight row (get_scale_min_k4, quant_formats.h:62-70)
-    const float d24 = h2f(hdr.x) * 16777216.0f;
+    // this lane's weight row (get_scale_min_k4, quant_formats.h:62-70): sc_j as (sc, sc)
+    // 16-bit pairs, m_j, d and dmin
     const u32 scA = hdr.y & 0x3F3F3F3Fu;
     const u32 scB = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
-    float ds[8];
+    const u32 mA = hdr.z & 0x3F3F3F3Fu;
+    const u32 mB = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+    const float ndm = -h2f(hdr.x >> 16);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ds[j] = d24 * (float)((j < 4 ? scA : scB) >> (8 * (j & 3)) & 0xFFu);
-    // B operand of K-step k = 2 j + h: 8 nibbles of two dwords, in the pair order
+    for (int tt = 0; tt < 4; ++tt) T[tt] = v16f_t{};
+    // mins product kk of tile tt: A = -dmin m_j of this lane's row, B = c of the lane's
+    // activation row, K index hh: sub-block 2 kk + hh
+    auto mins = [&](int tt, int kk) {
+      const int j = 2 * kk + hh;
+      const float am = ndm * (float)((j < 4 ? mA : mB) >> (8 * (j & 3)) & 0xFFu);
+      const float cv = as_f(lds4v(P + kPC + ((tt * 4 + kk) * 64 + lane) * 4));
+      acc[tt] = mfma_f32_k2(am, cv, acc[tt]);
+    };
+    // weight operand of K-step k = 2 j + h: sc_j times 8 nibbles of two dwords, in the
+    // pair order
     auto build = [&](int k) -> v4u {
       const int j = k >> 1, h = k & 1;
       u32 x0 = nib[j >> 1][2 * h], x1 = nib[j >> 1][2 * h + 1];
       asm volatile("" : "+v"(x0), "+v"(x1));  // keeps this K-step's operand build here
+      const u32 sp = __builtin_amdgcn_perm(0u, j < 4 ? scA : scB, sel_u16x2(j & 3));
       if (j & 1) {
         x0 ^= 0x80808080u;  // the plane's high nibbles XOR 8, undone
         x1 ^= 0x80808080u;
-        return v4u{(x0 >> 4) & 0x000F000Fu, (x0 >> 12) & 0x000F000Fu, (x1 >> 4) & 0x000F000Fu,
-                   (x1 >> 12) & 0x000F000Fu};
+        return v4u{mul_bytes((x0 >> 4) & 0x000F000Fu, sp), mul_bytes((x0 >> 12) & 0x000F000Fu, sp),
+                   mul_bytes((x1 >> 4) & 0x000F000Fu, sp), mul_bytes((x1 >> 12) & 0x000F000Fu, sp)};
       }
-      return v4u{x0 & 0x000F000Fu, (x0 >> 8) & 0x000F000Fu, x1 & 0x000F000Fu, (x1 >> 8) & 0x000F000Fu};
+      return v4u{mul_bytes(x0 & 0x000F000Fu, sp), mul_bytes((x0 >> 8) & 0x000F000Fu, sp),
+                 mul_bytes(x1 & 0x000F000Fu, sp), mul_bytes((x1 >> 8) & 0x000F000Fu, sp)};
     };
-    v4u a[4];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) a[tt] = lds16(P + (tt * 64 + lane) * 16);
-    v4u b = build(0);
+    // da_j of this lane's activation row in tile tt
+    auto ld_da = [&](int tt, int j) { return as_f(lds4v(P + kPDa + ((tt * 8 + j) * 32 + li) * 4)); };
+    float da[4];
+    v4u w = build(0);
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       __builtin_amdgcn_s_setprio(2);
-      v4u an[4];
+      if ((k & 1) == 0) {
+        // the sub-block's activation scales, used after its two K-steps; two of the
+        // super-block's 16 mins products: tile j / 2, pair 2 (j & 1) + 0, 1
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) da[tt] = ld_da(tt, k >> 1);
+        mins(k >> 2, 2 * ((k >> 1) & 1));
+        mins(k >> 2, 2 * ((k >> 1) & 1) + 1);
+      }
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
-        S[tt] = mfma_h(a[tt], b, (k & 1) == 0 ? v16f_t{} : S[tt]);
-        an[tt] = k < 15 ? lds16(P + ((4 * (k + 1) + tt) * 64 + lane) * 16) : a[tt];
+        const v4u a = lds16(P + ((4 * k + tt) * 64 + lane) * 16);
+        S[tt] = mfma_h(w, a, (k & 1) == 0 ? v16f_t{} : S[tt]);
       }
-      if (k < 15) b = build(k + 1);
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) a[tt] = an[tt];
+      if (k < 15) w = build(k + 1);
       if ((k & 1) == 0 && next) issue_piece(s + 1, k >> 1);
       if ((k & 3) == 3) nib[k >> 2] = ld_nib(s + 1, k >> 2);
       __builtin_amdgcn_sched_barrier(0);
       if (k & 1) {
-        // sub-block j = k / 2 done: acc += (da ds_j) P_j over the four tiles; the
-        // activation scales of rows 32 tt + 8 q + 4 hh .. + 3 (results r = 4 q ..)
+        // sub-block j = k / 2 done: T += da_j sc_j P_j over the four tiles
         __builtin_amdgcn_s_setprio(0);
-        const int j = k >> 1;
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
-          v4u da[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) da[q] = lds16v(P + kPDa + ((tt * 8 + j) * 32 + 8 * q + 4 * hh) * 4);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[tt][r] = fmaf(as_f(da[r >> 2][r & 3]) * ds[j], S[tt][r], acc[tt][r]);
-          asm volatile("" : "+v"(acc[tt]));  // the sub-block's results exist here, not after later MFMAs
+          for (int r = 0; r < 16; ++r) T[tt][r] = fmaf(da[tt], S[tt][r], T[tt][r]);
+          asm volatile("" : "+v"(T[tt]));  // the sub-block's results exist here, not after later MFMAs
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // the mins term: acc += c_j (-dmin m_j), sub-blocks 2 kk + hh (B: this lane's row)
-    const float ndm = -h2f(hdr.x >> 16);
-    const u32 mA = hdr.z & 0x3F3F3F3Fu;
-    const u32 mB = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+    // acc += d 2^24 T: d of the lane's 16 result rows 8 (r / 4) + 4 hh + r % 4, which lanes
+    // 0-31 hold (one weight row each)
+    const float d24 = h2f(hdr.x) * 16777216.0f;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      // lane half hh is K index hh of the pair (2 kk, 2 kk + 1)
-      const int j = 2 * kk + hh;
-      const u32 mj = (j < 4 ? mA : mB) >> (8 * (j & 3)) & 0xFFu;
-      const float bm = ndm * (float)mj;
+    for (int r = 0; r < 16; ++r) {
+      const int src = 8 * (r >> 2) + 4 * hh + (r & 3);
+      const float dr = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * src, __builtin_bit_cast(int, d24)));
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const float cv = as_f(lds4v(P + kPC + ((tt * 4 + kk) * 64 + lane) * 4));
-        acc[tt] = mfma_f32_k2(cv, bm, acc[tt]);
-      }
+      for (int tt = 0; tt < 4; ++tt) acc[tt][r] = fmaf(dr, T[tt][r], acc[tt][r]);
     }
   };
 
@@ -278,19 +289,23 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     hdr = hdr_n;
   }
 
-  // ---- outputs (+ bias): rows 32 mt + 8 (r / 4) + 4 hh + r % 4, weight row nbase + 32 wave + li
-  const int64_t n = nbase + 32 * wave + li;
+  // ---- outputs (+ bias): activation row 32 mt + li, weight rows nbase + 32 wave +
+  // 8 (r / 4) + 4 hh + r % 4 (four consecutive rows per r / 4)
   const int64_t mrows = m - mbase < kPM ? m - mbase : kPM;
-  if (n >= n0 && n < n1) {
-    const float bv = bias ? bias[n] : 0.0f;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+  for (int mt = 0; mt < 4; ++mt) {
+    const int row = 32 * mt + li;
+    if (row >= mrows) continue;
+    float* yr = y + (mbase + row) * ys;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = 32 * mt + 8 * (r >> 2) + 4 * hh + (r & 3);
-        if (row < mrows) {
-          const float v = acc[mt][r];
-          y[(mbase + row) * ys + n] = bias ? v + bv : v;
+    for (int q = 0; q < 4; ++q) {
+      const int64_t nq = nbase + 32 * wave + 8 * q + 4 * hh;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t n = nq + e;
+        if (n >= n0 && n < n1) {
+          const float v = acc[mt][4 * q + e];
+          yr[n] = bias ? v + bias[n] : v;
         }
       }
     }
