@@ -358,7 +358,8 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_m1_gemm_m512_traffic.md"
 
 def pmc_leg(weights, x, acts, y, stream) -> None:
     """Launches for the counter passes: the copy kernel first (COPY_BYTES read and
-    written, the calibration of FETCH_SIZE / WRITE_SIZE), then the measured kernels."""
+    written, the calibration of FETCH_SIZE / WRITE_SIZE), then the measured kernels: the
+    fused and plain M=1 GEMVs, the M=512 Q8_K GEMM and the M=512 default-plan prefill."""
     import torch
 
     import dynalm_amd as dq
@@ -380,6 +381,11 @@ def pmc_leg(weights, x, acts, y, stream) -> None:
     dq.act_quantize(dq.ACT_Q8_K, xg, m, K, K, ag, stream)
     for i in range(4):
         dq.gemm(weights[i % nc], dq.ACT_Q8_K, ag, m, 0, N, yg, N, None, stream)
+    # the default-plan prefill: per-32 quantize, k_act32_from_p32, k_gemm_q4k_p32
+    eng = dq.plan_defaults()
+    eng.int8_decode_max_rows = 1 << 30
+    for i in range(4):
+        dq.matmul_plan(weights[i % nc], eng, xg, m, K, yg, N, None, stream)
     torch.cuda.synchronize()
     log("pmc leg done")
 
@@ -708,7 +714,7 @@ def main() -> None:
         "tokens_per_s": round(m / (ms_pre * 1e-3), 1),
         "roofline": {"kernel": "dq::k_gemm_q4k_p32 (ms per call: + per-32 quantize + k_act32_from_p32)",
                      "bound": "mfma", "achieved": round(tpre, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tpre / PEAK_F16_TFLOPS, 4)},
+                     "frac": round(tpre / PEAK_F16_TFLOPS, 4), "traffic": traffic.get("prefill_default_m512")},
     }
     result["decode_default_plan"] = {
         "workload": f"config 3 decode, M=1 K={K} N={N} Q4_K: dq_matmul_plan under KernelPlan's defaults "
