@@ -395,7 +395,9 @@ def ceilings(steps: int, warmup: int) -> dict:
     libdqceil.so (dynalm_amd/csrc/dq_ceiling.hip): the decode GEMV's loads alone
     (same grid, same per-wave runs and offsets, no arithmetic) over 33 MB and over
     132 MB (four times K at the same launch shape), rotated over copies totalling
-    528 MB as the GEMV is; and back-to-back int8 MFMAs on every SIMD."""
+    528 MB as the GEMV is; the plain read of the same 33 MB at ten launch shapes (the
+    best one is the read ceiling the GEMV's launch shape gives up against); and
+    back-to-back int8 MFMAs on every SIMD."""
     import ctypes as C
 
     import torch
@@ -422,6 +424,27 @@ def ceilings(steps: int, warmup: int) -> dict:
         out[label] = {"bytes": nbytes, "blocks_per_wave": nblk // waves, "copies": copies,
                       "ms_per_launch": round(ms, 5), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
         del qs, hd, y
+    torch.cuda.empty_cache()
+    # the plain read of the GEMV's weight bytes at ten launch shapes (16 rotated copies, as
+    # the GEMV): the best one-launch read of them, the GEMV's shape first
+    lib.dqc_read_flat.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    wbytes = Q4K_ROW * N
+    flat = [torch.full((wbytes,), 1, dtype=torch.uint8, device="cuda") for _ in range(16)]
+    sink = torch.empty(8192, dtype=torch.int32, device="cuda")
+    sweep = {}
+    for wgs, waves in ((N // 64, 16), (256, 16), (448, 8), (512, 8), (896, 4), (1024, 4), (1792, 2), (2048, 2),
+                       (3584, 1), (4096, 1)):
+        def flat_read(i: int, st: int, wgs=wgs, waves=waves) -> None:
+            rc = lib.dqc_read_flat(flat[i % 16].data_ptr(), wbytes, wgs, waves, sink.data_ptr(), st)
+            assert rc == 0, f"dqc_read_flat: {rc}"
+
+        ms = time_graph(flat_read, steps, warmup)
+        sweep[f"{wgs}x{waves}"] = {"ms_per_launch": round(ms, 5), "gbs": round(wbytes / (ms * 1e-3) / 1e9, 1)}
+    best = max(sweep, key=lambda key: sweep[key]["gbs"])
+    out["read_shape_sweep"] = {"bytes": wbytes, "kernel": "dqc_read_flat: one contiguous piece per wave, "
+                               "nontemporal dwordx4, up to 8 KB in flight per wave", "shapes": sweep,
+                               "best": best, "best_gbs": sweep[best]["gbs"]}
+    del flat, sink
     torch.cuda.empty_cache()
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     mfma = {"launch": f"{cus} workgroups x 8 waves (two per SIMD), 8 independent accumulators per wave"}
@@ -545,7 +568,7 @@ def main() -> None:
     ms_gemv = time_graph(gemv_only, args.steps, args.warmup)
     bytes_step = Q4K_ROW * N + Q8K_ROW + 4 * N
     value = bytes_step / (ms_step * 1e-3) / 1e9
-    # the step is one kernel (k_gemv<Q4_K, Q8_K, M=1, fused quantization>): its launch time is ms_step
+    # the step is one kernel (k_gemv_slab<16, fused>: Q4_K x Q8_K, M=1): its launch time is ms_step
     achieved = value
 
     # ---- the gated pair at the step's shape: act(x . Wg^T) * (x . Wu^T), one launch
@@ -664,12 +687,14 @@ def main() -> None:
         "pct_peak_hbm": round(100 * value / PEAK_HBM_GBS, 2),
         "read_ceiling_gbs": read_ceiling,
         "pct_of_read_ceiling": round(100 * value / read_ceiling, 2),
+        "best_read_gbs": ceil["read_shape_sweep"]["best_gbs"],
+        "pct_of_best_read": round(100 * value / ceil["read_shape_sweep"]["best_gbs"], 2),
         "mfma_ceiling_tops": mfma_ceiling,
         "f16_mfma_ceiling_tflops": f16_ceiling,
         "ceilings": ceil,
         "tokens_per_s": round(1e3 / ms_step, 1),
         "roofline": {
-            "kernel": "dq::k_gemv<Q4_K, Q8_K, M=1, fused quantization>",
+            "kernel": "dq::k_gemv_slab<16, true> (Q4_K x Q8_K, M=1, fused quantization, 56-row workgroups)",
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": PEAK_HBM_GBS,
@@ -679,7 +704,7 @@ def main() -> None:
             "ms_per_launch": round(ms_step, 5),
         },
         "gemv_prequantized": {
-            "kernel": "dq::k_gemv<Q4_K, Q8_K, M=1> (activations quantized by a separate launch)",
+            "kernel": "dq::k_gemv_slab<16, false> (Q4_K x Q8_K, M=1; activations quantized by a separate launch)",
             "ms_per_launch": round(ms_gemv, 5),
             "gbs": round(bytes_step / (ms_gemv * 1e-3) / 1e9, 2),
         },

@@ -12,6 +12,8 @@
 //   v_mfma_i32_32x32x32_i8, or f16 v_mfma_f32_32x32x16_f16), eight independent
 //   accumulators per wave, two waves per SIMD on every CU: the matrix rate a GEMM could
 //   reach at the clock the device runs under MFMA load.
+// - dqc_read_flat: a plain read of the same bytes at any launch shape, for the bench's
+//   launch-shape sweep (the best one-launch read of them).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -53,6 +55,30 @@ __global__ __launch_bounds__(1024) void k_read_q4k(const uint8_t* __restrict__ q
     for (int i = 1; i < nw; ++i) x ^= fold[i][r];
     out[G * 64 + r] = __builtin_bit_cast(float, x & 0x3FFFFFFFu);
   }
+}
+
+// A plain read of `bytes` at a given launch shape: workgroups of `waves` waves, wave v of
+// the grid reading the contiguous piece [v * per, (v + 1) * per) (per a multiple of 1 KB)
+// with nontemporal 16-byte loads, up to eight 1 KB loads in flight per wave, one value per
+// wave written; pieces past the end read zeros (the buffer's range check). The bench's
+// launch-shape sweep: the best one-launch read of the decode GEMV's bytes.
+__global__ __launch_bounds__(1024) void k_read_flat(const uint8_t* __restrict__ p, u32 per, u32 bytes,
+                                                   u32* __restrict__ out) {
+  const int r = threadIdx.x & 63;
+  const int64_t v = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t base = v * per;
+  const auto rs = dq::rsrc(p, bytes);
+  u32 x = 0;
+  for (u32 o = 0; o < per; o += 8 * 1024) {
+    v4u q[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      q[c] = o + c * 1024 < per ? dq::ld16nt(rs, (u32)(base + o + c * 1024 + r * 16)) : v4u{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) x ^= q[c].x ^ q[c].y ^ q[c].z ^ q[c].w;
+  }
+  if (r == 0) out[v] = x;
 }
 
 typedef float v16f_t __attribute__((ext_vector_type(16)));
@@ -118,6 +144,21 @@ __global__ __launch_bounds__(512) void k_mfma_rate(int iters, int* __restrict__ 
 }  // namespace
 
 extern "C" {
+
+// bytes (a multiple of 1 KB) read by wgs workgroups of waves waves, each wave a contiguous
+// piece of whole KB; out: one u32 per wave.
+__attribute__((visibility("default"))) int dqc_read_flat(const void* p, int64_t bytes, int wgs, int waves, void* out,
+                                                         void* stream) {
+  const int64_t nw = (int64_t)wgs * waves;
+  if (p == nullptr || out == nullptr || wgs <= 0 || waves <= 0 || waves > 16 || bytes <= 0 || bytes % 1024 != 0 ||
+      bytes + nw * 1024 >= (1ll << 32)) {
+    return 1;
+  }
+  const int64_t per = (bytes / 1024 + nw - 1) / nw * 1024;
+  hipLaunchKernelGGL(k_read_flat, dim3((unsigned)wgs), dim3(64 * waves), 0, (hipStream_t)stream,
+                     (const uint8_t*)p, (u32)per, (u32)bytes, (u32*)out);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
 
 // groups row groups of nblk super-blocks (planes of groups * nblk * 8192 and
 // * 1024 bytes); waves * bpw == nblk; out: groups * 64 floats.

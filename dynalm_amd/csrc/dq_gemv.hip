@@ -1085,6 +1085,93 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
   }
 }
 
+// ---- the one-row Q4_K x Q8_K decode on every CU. k_gemv runs one workgroup per
+// 64-row group, so a weight of fewer groups than CUs (config 3: 224 groups on 256
+// CUs) leaves CUs idle, and with them their share of the loads in flight.
+// k_gemv_slab runs workgroups of kSlabRows = 56 rows over the whole row, one wave per
+// super-block (K = 256 NB): lane l < 56 holds row 56 g + l of workgroup g, so each
+// vector load of a wave is one contiguous run of 896 bytes (two runs where the rows
+// cross a 64-row group); lanes 56..63 read nothing (past the buffer bound) and
+// store nothing. Each wave stages only its own super-block, as k_gemv's waves do.
+// The compute step is k_gemv's (the same t-term per row and super-block) and the
+// chain over the super-blocks runs in the same order, so the outputs are bit-equal
+// to k_gemv's.
+constexpr int kSlabRows = 56;
+
+template <int NB, bool kFuse>
+__global__ __launch_bounds__(NB * 64) void k_gemv_slab(const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
+                                                       int64_t groups, int64_t n0, int64_t n1,
+                                                       const uint8_t* __restrict__ acts, const float* __restrict__ x,
+                                                       float* __restrict__ y, const float* __restrict__ bias,
+                                                       int32_t* __restrict__ dbg, int64_t dbg_n) {
+  __shared__ __align__(16) uint8_t st[NB * kStageQ8K + kDummyBytes];
+  __shared__ __align__(16) float rec[NB * 64 + NB];  // t-terms [b][row], then da [b]
+  const int l = threadIdx.x & 63, b = wave_id();
+  const int64_t g0 = n0 / kRowGroup;
+  const bool live = l < kSlabRows;
+  const int64_t n = g0 * kRowGroup + (int64_t)blockIdx.x * kSlabRows + (live ? l : 0);
+  const int r = (int)(n % kRowGroup);
+  // the planes from row group g0 on; rows past the last group read zeros, and so do
+  // lanes 56..63 (block index past the resources)
+  Rsrcs rs;
+  rs.r0 = rsrc(p0 + g0 * NB * 64 * 128, (u32)((groups - g0) * NB * 64 * 128));
+  rs.r1 = rsrc(p1 + g0 * NB * 64 * 16, (u32)((groups - g0) * NB * 64 * 16));
+  rs.r2 = rs.r0;
+  rs.r3 = rs.r0;
+  const int bi = live ? (int)((n / kRowGroup - g0) * NB + b) : (int)((groups - g0) * NB);
+
+  // activation loads first, then the weight loads (k_gemv's early path)
+  float xv[4];
+  ActRegs<kActQ8_K, 1> ar;
+  if constexpr (kFuse) {
+    load4f(rsrc(x, (u32)(NB * 256 * 4)), (u32)((b * 256 + 4 * l) * 4), xv);
+  } else {
+    ar.issue(acts, (int64_t)NB * 292, b, b + 1, 1, l);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  Chunk<kQ4_K, 1> c;
+  c.load(rs, bi, bi + 1, bi + 1, r);
+  __builtin_amdgcn_sched_barrier(0);
+  uint8_t* ob = st + b * kStageQ8K;
+  if constexpr (kFuse) {
+    float d;
+    int bsum;
+    const u32 packed = q8k_quant(xv, d, bsum);
+    const int s32 = bsum + dpp<kHalfMirror>(bsum);
+    *reinterpret_cast<u32*>(ob + 16 + 4 * l) = packed;
+    if ((l & 3) == 0) *reinterpret_cast<int16_t*>(ob + 272 + 2 * (l >> 2)) = (int16_t)bsum;
+    if ((l & 7) == 0) stage_subsum(ob, l >> 3, s32);
+    if (l == 0) *reinterpret_cast<float*>(ob) = d;
+  } else {
+    ar.commit((int64_t)NB * 292, NB, b, b + 1, 1, l, st, st + NB * kStageQ8K);
+  }
+  wave_lds_sync();
+
+  Out<1> o;
+  o.rec = rec;
+  o.dav = rec + NB * 64;
+  o.dbg = dbg;
+  o.dbg_n = dbg_n;
+  o.n = live ? n : dbg_n;  // lanes 56..63 write no partials
+  o.nblk = NB;
+  o.r = l;
+  o.acc[0] = o.cor[0] = 0.0f;
+  compute<kActQ8_K, 1, 1>(c, b, st, o);
+  __syncthreads();
+  if (b != 0 || !live) return;
+  // k_gemv's chain: acc = fma(da_b, t_b, acc), b in order
+  float t[NB], dv[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    t[i] = rec[i * 64 + l];
+    dv[i] = rec[NB * 64 + i];
+  }
+  float v = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) v = fmaf(dv[i], t[i], v);
+  if (n >= n0 && n < n1) y[n] = bias ? v + bias[n] : v;
+}
+
 // Completes split-K rows (one 64-lane workgroup per row group, lane r = row): the
 // sum of the splits' row sums in split order, plus the bias.
 template <int M>
@@ -1243,6 +1330,22 @@ static hipError_t gemv_early(const WeightDev& w, const uint8_t* acts, int64_t ar
   return gemv_launch<WT, AF, M, kFuse, W, 0, kSplit>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, sp, s);
 }
 
+template <bool kFuse>
+static hipError_t gemv_slab(const WeightDev& w, const uint8_t* acts, const float* x, int64_t n0, int64_t n1, float* y,
+                            const float* bias, int32_t* dbg, hipStream_t s) {
+  const int64_t g0 = n0 / kRowGroup, g1 = (n1 + kRowGroup - 1) / kRowGroup;
+  const unsigned grid = (unsigned)(((g1 - g0) * kRowGroup + kSlabRows - 1) / kSlabRows);
+  const int64_t groups = w.n_pad / kRowGroup;
+  if (w.nblk == 16) {
+    hipLaunchKernelGGL((k_gemv_slab<16, kFuse>), dim3(grid), dim3(16 * 64), 0, s, w.plane[0], w.plane[1], groups, n0,
+                       n1, acts, x, y, bias, dbg, w.n);
+  } else {
+    hipLaunchKernelGGL((k_gemv_slab<8, kFuse>), dim3(grid), dim3(8 * 64), 0, s, w.plane[0], w.plane[1], groups, n0, n1,
+                       acts, x, y, bias, dbg, w.n);
+  }
+  return hipGetLastError();
+}
+
 template <int WT, int AF, int M, bool kFuse>
 static hipError_t gemv_waves(const WeightDev& w, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
                              int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
@@ -1252,6 +1355,12 @@ static hipError_t gemv_waves(const WeightDev& w, const uint8_t* acts, int64_t ar
   // row groups, not from [n0, n1): a row's slices, and so its fp32 sum order, do not
   // depend on how the caller partitions the rows (qmm.h:35-36).
   const int64_t groups = w.n_pad / kRowGroup;
+  if constexpr (WT == kQ4_K && AF == kActQ8_K && M == 1) {
+    // fewer row groups than CUs: 56-row workgroups spread the row over more CUs
+    if ((w.nblk == 8 || w.nblk == 16) && groups * kRowGroup <= (int64_t)kSlabRows * w.cus) {
+      return gemv_slab<kFuse>(w, acts, x, n0, n1, y, bias, dbg, s);
+    }
+  }
   const int splits = gemv_splits(w, AF);
   if constexpr (AF != kActQ8_K && AF != kActSX) {
     if (splits > 1) {

@@ -38,7 +38,7 @@ def test_exports_are_the_only_public_symbols():
 
 def test_ceiling_probe_library_is_separate():
     """bench.py's ceiling probes live in their own library: it loads and exports its
-    two entry points and rejects bad launches on the host; libdynaq exports none of them."""
+    entry points and rejects bad launches on the host; libdynaq exports none of them."""
     import subprocess
 
     path = os.path.join(ROOT, "dynalm_amd", "lib", "libdqceil.so")
@@ -50,6 +50,10 @@ def test_ceiling_probe_library_is_separate():
     assert lib.dqc_read_q4k(None, None, 224, 16, 16, None, None) == 1
     assert lib.dqc_read_q4k(1, 1, 224, 16, 3, 1, None) == 1  # waves must divide the blocks
     assert lib.dqc_mfma_rate(256, 10, 3, 1, C.byref(C.c_double()), None) == 1  # unknown MFMA kind
+    lib.dqc_read_flat.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    assert lib.dqc_read_flat(None, 1 << 20, 224, 16, 1, None) == 1
+    assert lib.dqc_read_flat(1, 1000, 224, 16, 1, None) == 1  # whole KB only
+    assert lib.dqc_read_flat(1, 1 << 20, 224, 17, 1, None) == 1  # at most 16 waves
     out = subprocess.run(["nm", "-D", "--defined-only", dq.lib_path()], capture_output=True, text=True).stdout
     assert "dqc_" not in out
 
