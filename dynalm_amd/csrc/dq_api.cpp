@@ -323,6 +323,7 @@ int run_skinny(std::vector<dq::GemvJob>& jobs, int device, hipStream_t s, const 
     }
     int64_t mmax = 0;
     for (const dq::GemvJob& j : batch) mmax = j.m > mmax ? j.m : mmax;
+    size_t used = 0;  // bytes of the caller's region holding quantized rows
     if (mmax > 16 || dq::skinny_units(batch.data(), (int)batch.size()) > dq::kSkinnyFuseMaxUnits) {
       // one Q8_K copy per distinct input (x, m, k, stride), as CpuDevice shares one
       // buffer between jobs that read the same activations (cpu_device.cpp:561-599)
@@ -348,6 +349,7 @@ int run_skinny(std::vector<dq::GemvJob>& jobs, int device, hipStream_t s, const 
       }
       void* scratch = nullptr;
       if (int rc = acts_buffer(device, bytes, r, &scratch); rc != DQ_OK) return rc;
+      used = bytes;
       uint8_t* base = static_cast<uint8_t*>(scratch);
       for (size_t i = 0; i < batch.size(); ++i) {
         dq::GemvJob& j = batch[i];
@@ -360,7 +362,24 @@ int run_skinny(std::vector<dq::GemvJob>& jobs, int device, hipStream_t s, const 
         j.xs = 0;
       }
     }
-    DQ_HIP(dq::launch_gemv_mma_many(batch.data(), (int)batch.size(), s), "grouped gemv launch");
+    const int64_t tb = batch.size() == 1 && batch[0].x == nullptr && batch[0].wu == nullptr
+                           ? dq::skinny_split_bytes(*batch[0].w, DQ_ACT_Q8_K, batch[0].m, 0, batch[0].w->n)
+                           : 0;
+    if (tb > 0 && r.base == nullptr) {
+      // one long-row matmul on few tiles: the split launch's t-terms in this stream's workspace
+      const int rc = with_stream_ws(device, static_cast<void*>(s), (size_t)tb, [&](uint8_t* p) -> int {
+        const dq::Workspace ws{p, (size_t)tb};
+        DQ_HIP(dq::launch_gemv_mma_many(batch.data(), 1, s, &ws), "grouped gemv launch");
+        return DQ_OK;
+      });
+      if (rc != DQ_OK) return rc;
+    } else if (tb > 0) {
+      // the caller's region after the quantized rows (too small: the unsplit launch)
+      const dq::Workspace ws = split_ws(r, used);
+      DQ_HIP(dq::launch_gemv_mma_many(batch.data(), 1, s, &ws), "grouped gemv launch");
+    } else {
+      DQ_HIP(dq::launch_gemv_mma_many(batch.data(), (int)batch.size(), s), "grouped gemv launch");
+    }
   }
   return DQ_OK;
 }
@@ -747,6 +766,16 @@ int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
         DQ_HIP(dq::launch_gemv(w->dev, fmt, a + r0 * arb, arb, 1, n0, n1, y + r0 * y_stride, y_stride, bias, nullptr,
                                as_stream(stream)),
                "gemv launch");
+      } else if (const int64_t tb = dq::skinny_split_bytes(w->dev, fmt, rows, n0, n1); tb > 0) {
+        // long rows on few tiles: the split launch's t-terms in this stream's workspace
+        const int rc = with_stream_ws(w->dev.device, stream, (size_t)tb, [&](uint8_t* p) -> int {
+          const dq::Workspace ws{p, (size_t)tb};
+          DQ_HIP(dq::launch_gemv_mma(w->dev, fmt, a + r0 * arb, arb, rows, n0, n1, y + r0 * y_stride, y_stride, bias,
+                                     as_stream(stream), &ws),
+                 "gemv launch");
+          return DQ_OK;
+        });
+        if (rc != DQ_OK) return rc;
       } else {
         DQ_HIP(dq::launch_gemv_mma(w->dev, fmt, a + r0 * arb, arb, rows, n0, n1, y + r0 * y_stride, y_stride, bias,
                                    as_stream(stream)),

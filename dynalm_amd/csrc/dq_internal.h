@@ -118,9 +118,14 @@ hipError_t launch_gemm_b32(const WeightDev& w, int af, const uint8_t* acts, int6
 bool gemm_b32_supported(int dtype, int af);
 // Skinny MFMA GEMV on pre-quantized rows: Q4_K / Q6_K x Q8_K for 2 <= m <=
 // kSkinnyMaxRows, and x sub-scaled (DQ_ACT_SX) for 2 <= m <= kSkinnySxMaxRows;
-// hipErrorInvalidValue otherwise.
+// hipErrorInvalidValue otherwise. ws (may be null): room for the t-terms of the split
+// launch that long Q6_K rows on few 16-row tiles take at m <= 16 (skinny_split_bytes;
+// without it they run unsplit, same results).
 hipError_t launch_gemv_mma(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0,
-                           int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s);
+                           int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s,
+                           const Workspace* ws = nullptr);
+// Bytes of that split launch's t-terms for these rows (0: the launch is not split).
+int64_t skinny_split_bytes(const WeightDev& w, int af, int64_t m, int64_t n0, int64_t n1);
 constexpr int64_t kSkinnyMaxRows = 64;
 constexpr int64_t kSkinnySxMaxRows = 16;
 // Whether m sub-scaled rows over rows [n0, n1) of w run faster on the skinny MFMA GEMV
@@ -150,7 +155,7 @@ struct GemvJob {
 // Grouped skinny MFMA GEMV: jobs of one K (same nblk) and one input kind (all
 // fused or none), Q4_K / Q6_K, 2 <= m <= 64 (fused: m <= 16), in launches of up to
 // 8 jobs; hipErrorInvalidValue for any other job.
-hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s);
+hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s, const Workspace* ws = nullptr);
 // Work of one grouped launch of these jobs (<= 8, one nblk) in wave-sized units
 // (workgroups x super-blocks): each unit of a launch on fp32 rows quantizes 16
 // activation rows of one super-block again, so the caller quantizes once instead

@@ -605,6 +605,80 @@ __global__ __launch_bounds__(W * 64) void k_skinny(SkinnyGroup g) {
   }
 }
 
+// ---- long Q6_K rows on few 16-row tiles (an FFN down projection at up to 16
+// activation rows: Q6_K 1536 x 8960 is 96 tiles of 35 super-blocks). k_skinny runs
+// one workgroup per tile there, so 96 CUs each stream ~280 KB (weights and the
+// tile's activation super-blocks), and a CU streams at most ~20 KB per microsecond
+// on this GPU. k_skinny_split spreads the row over ~all CUs: a workgroup takes one
+// 64-row group and a slice of kSplitWaves super-blocks, one wave per super-block with
+// k_skinny's CT = 4 step (each activation super-block is read once per 64 weight
+// rows, a quarter of the 16-row tiles' activation traffic), and stores the t-terms
+// in T[group][b][16 activation rows][64 weight rows]. k_skinny_chain then runs the
+// in-order chains acc = fma(d_b, t_b, acc) with d from the Q8_K rows. Same t-terms,
+// same chains: bit-equal to k_skinny.
+constexpr int kSplitWaves = 4;
+
+template <int WT>
+DQ_DEV void split_wave(const SkinnyJob& J, int nblk, int64_t G, int b, float* tb, int li, int lg) {
+  WRes<WT, 4> res;
+  res.init(J.p, G, nblk, true);
+  WSB<WT, 4> w;
+  res.load(w, b, 0, li, lg);
+  __builtin_amdgcn_sched_barrier(0);  // the weight loads first (the longer latency)
+  ActSrc<false> src;
+  src.init(J);
+  ActSB<1> A;
+  load_codes<1>(src, b, li, lg, A);
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    float t[1][4];
+    tterms<4, 1>(w, ct, A, lg, t);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tb[(4 * lg + e) * 64 + 16 * ct + li] = t[0][e];
+  }
+}
+
+__global__ __launch_bounds__(kSplitWaves * 64) void k_skinny_split(SkinnyJob J, int nblk, int slices, int64_t g0,
+                                                                   float* __restrict__ T) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
+  const int64_t gi = blockIdx.x / slices;
+  const int b = (int)(blockIdx.x % slices) * kSplitWaves + wave;
+  if (b >= nblk) return;
+  float* tb = T + (gi * nblk + b) * 16 * 64;
+  if (J.dtype == kQ6_K) {
+    split_wave<kQ6_K>(J, nblk, g0 + gi, b, tb, l & 15, l >> 4);
+  } else {
+    split_wave<kQ4_K>(J, nblk, g0 + gi, b, tb, l & 15, l >> 4);
+  }
+}
+
+// The chains of k_skinny_split's t-terms: one wave per (64-row group g0 + blockIdx.x,
+// activation row blockIdx.y), lane r = weight row (one-wave workgroups spread the
+// t-term reads over all CUs). Every load of a chain (nblk <= NB t-terms and d values)
+// is issued before its first FMA, so the chain waits on one round trip.
+template <int NB>
+__global__ __launch_bounds__(64) void k_skinny_chain(const float* __restrict__ T, const uint8_t* __restrict__ acts,
+                                                     int64_t arb, int m, int nblk, int64_t g0, int64_t n0, int64_t n1,
+                                                     float* __restrict__ y, int64_t ys, const float* __restrict__ bias) {
+  const int r = threadIdx.x, mm = (int)blockIdx.y;
+  const int64_t n = (g0 + blockIdx.x) * kRowGroup + r;
+  const float* tp = T + ((int64_t)blockIdx.x * nblk * 16 + mm) * 64 + r;
+  const uint8_t* ap = acts + mm * arb;
+  float t[NB], d[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int bc = b < nblk ? b : nblk - 1;  // past the row: a repeat, not used
+    t[b] = tp[bc * 16 * 64];
+    d[b] = *reinterpret_cast<const float*>(ap + bc * 292);
+  }
+  float v = 0.0f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (b < nblk) v = fmaf(d[b], t[b], v);
+  }
+  if (n >= n0 && n < n1) y[mm * ys + n] = bias ? v + bias[n] : v;
+}
+
 size_t skinny_lds(int64_t nblk, int ct, int mt, bool gated = false) {
   return (size_t)nblk * (16 * mt * (16 * ct + 1)) * (gated ? 2 : 1) * sizeof(float);
 }
@@ -645,8 +719,15 @@ int skinny_ct(int64_t wgs16, int64_t nblk, int cus, int mt) {
   return mt == 1 && wgs16 >= 16 * (int64_t)cus && skinny_lds(nblk, 4, 1) <= kSkinnyMaxLds ? 4 : 1;
 }
 
+// Bytes of k_skinny_split's t-terms for rows [n0, n1) of nblk super-blocks.
+int64_t split_t_bytes(int64_t n0, int64_t n1, int64_t nblk) {
+  return ((n1 + kRowGroup - 1) / kRowGroup - n0 / kRowGroup) * nblk * 16 * 64 * (int64_t)sizeof(float);
+}
+
+// ws: room for the split launch's t-terms (none: launches of one long-row job on few
+// tiles run k_skinny with 4 super-blocks of weights in flight per wave instead).
 hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t* last_row, bool fused, bool gated,
-                        int cus, hipStream_t s, bool sx = false) {
+                        int cus, hipStream_t s, bool sx = false, const Workspace* ws = nullptr) {
   int mmax = 0;
   int64_t wgs16 = 0;
   for (int i = 0; i < g.count; ++i) {
@@ -692,7 +773,30 @@ hipError_t launch_group(SkinnyGroup& g, const int64_t* first_row, const int64_t*
   // One round of 8-wave workgroups with at least 3 super-blocks per wave (a long-K
   // matmul such as an FFN down projection): the waves' dependent load steps, not the
   // bytes, set the time, so 4 super-blocks of weights stay in flight per wave.
-  if (wgs <= cus && g.nblk >= 3 * kSkinnyWaves) return skinny_launch<1, 1, false, false, kSkinnyWaves, 4>(g, (int)wgs, s);
+  if (wgs <= cus && g.nblk >= 3 * kSkinnyWaves) {
+    if (g.count == 1 && g.job[0].dtype == kQ6_K && g.nblk >= 32 && g.nblk <= 64 && 2 * wgs <= cus && ws != nullptr &&
+        ws->bytes >= (size_t)split_t_bytes(first_row[0], last_row[0], g.nblk)) {
+      // one matmul: the t-terms of 64-row groups x super-block slices, then the chains
+      const SkinnyJob& J = g.job[0];
+      const int64_t g0 = first_row[0] / kRowGroup, g1 = (last_row[0] + kRowGroup - 1) / kRowGroup;
+      const int slices = (g.nblk + kSplitWaves - 1) / kSplitWaves;
+      float* T = reinterpret_cast<float*>(ws->p);
+      hipLaunchKernelGGL(k_skinny_split, dim3((unsigned)((g1 - g0) * slices)), dim3(kSplitWaves * 64), 0, s, J, g.nblk,
+                         slices, g0, T);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      const dim3 grid((unsigned)(g1 - g0), (unsigned)J.m);
+      if (g.nblk <= 40) {
+        hipLaunchKernelGGL(k_skinny_chain<40>, grid, dim3(64), 0, s, T, J.acts, J.arb, J.m, g.nblk, g0, J.n0, J.n1,
+                           J.y, J.ys, J.bias);
+      } else {
+        hipLaunchKernelGGL(k_skinny_chain<64>, grid, dim3(64), 0, s, T, J.acts, J.arb, J.m, g.nblk, g0, J.n0, J.n1,
+                           J.y, J.ys, J.bias);
+      }
+      return hipGetLastError();
+    }
+    return skinny_launch<1, 1, false, false, kSkinnyWaves, 4>(g, (int)wgs, s);
+  }
   return skinny_launch<1, 1, false>(g, (int)wgs, s);
 }
 
@@ -733,8 +837,22 @@ int64_t skinny_units(const GemvJob* jobs, int count) {
   return wgs * jobs[0].w->nblk;
 }
 
+// The split route pays for Q6_K rows of at least 32 super-blocks on at most half as
+// many 16-row tiles as CUs. Measured (graph replay, M = 2 / 8 / 16, split vs k_skinny):
+// Q6_K 1536 x 8960 9.3 / 9.4 / 9.9 vs 10.7 / 10.8 / 11.5 us; with every CU holding a
+// tile it loses (Q6_K 4096 x 14336: 20.7 / 21.7 / 25.2 vs 16.0 / 16.2 / 17.7), and so it
+// does for Q4_K's lighter super-blocks (1536 x 6144: 7.6 / 7.8 / 8.0 vs 6.1 / 6.2 / 6.8).
+int64_t skinny_split_bytes(const WeightDev& w, int af, int64_t m, int64_t n0, int64_t n1) {
+  const int64_t tiles = (n1 + 15) / 16 - n0 / 16;
+  if (af != kActQ8_K || w.dtype != kQ6_K || m < 2 || m > 16 || n1 <= n0 || 2 * tiles > w.cus || w.nblk < 32 ||
+      w.nblk > 64) {
+    return 0;
+  }
+  return split_t_bytes(n0, n1, w.nblk);
+}
+
 hipError_t launch_gemv_mma(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t n0,
-                           int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s) {
+                           int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s, const Workspace* ws) {
   if (!gemv_mma_supported(w.dtype, af, m)) return hipErrorInvalidValue;
   if (n1 <= n0) return hipSuccess;
   SkinnyGroup g;
@@ -743,10 +861,10 @@ hipError_t launch_gemv_mma(const WeightDev& w, int af, const uint8_t* acts, int6
   g.job[0].arb = arb;
   g.count = 1;
   g.nblk = (int)w.nblk;
-  return launch_group(g, &n0, &n1, false, false, w.cus, s, af == kActSX);
+  return launch_group(g, &n0, &n1, false, false, w.cus, s, af == kActSX, ws);
 }
 
-hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s) {
+hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s, const Workspace* ws) {
   for (int i0 = 0; i0 < count; i0 += kSkinnyMaxJobs) {
     SkinnyGroup g;
     g.count = count - i0 < kSkinnyMaxJobs ? count - i0 : kSkinnyMaxJobs;
@@ -775,7 +893,7 @@ hipError_t launch_gemv_mma_many(const GemvJob* jobs, int count, hipStream_t s) {
       first[i] = 0;
       last[i] = q.w->n;
     }
-    const hipError_t e = launch_group(g, first, last, fused, gated, jobs[i0].w->cus, s);
+    const hipError_t e = launch_group(g, first, last, fused, gated, jobs[i0].w->cus, s, false, ws);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
