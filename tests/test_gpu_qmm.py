@@ -150,3 +150,61 @@ def test_qmm_gemm(cuda, t):
     ok, worst = close(y.cpu().numpy(), O.matmul(t, O.ACT_PER32, w_rows, O.quantize_act(O.ACT_PER32, x), k))
     assert ok, f"worst error ratio {worst:.3g}"
     w.free()
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("mode", [dq.QMM_INT8, dq.QMM_INT16])
+def test_qmm_gemv_unaligned_ranges(cuda, t, mode):
+    """Callers split [n0, n1) across threads (qmm.h:35-36): three pieces that start and
+    end inside 64-row groups give the one-call bits, and a single piece leaves every
+    output outside it untouched."""
+    m, k, n = 5, 1024, 200
+    w_rows = gguf_weights(t, n, k, 91 + t, outlier_frac=0.01)
+    x = activations(m, k, 92 + mode, outliers=False)
+    w = dq.Weight.upload(t, w_rows, k)
+    buf, xd, a = prepared(x, mode, True)
+    st = torch.cuda.current_stream().cuda_stream
+    full = torch.full((m, n), 7.0, device="cuda")
+    dq.qmm_gemv(w, 0, n, a, 0, m, full, n, None, st)
+    part = torch.full((m, n), 7.0, device="cuda")
+    for n0, n1 in ((0, 37), (37, 150), (150, n)):
+        dq.qmm_gemv(w, n0, n1, a, 0, m, part, n, None, st)
+    assert np.array_equal(part.cpu().numpy().view(np.uint32), full.cpu().numpy().view(np.uint32))
+    one = torch.full((m, n), 7.0, device="cuda")
+    dq.qmm_gemv(w, 37, 150, a, 1, 3, one, n, None, st)
+    got, ref = one.cpu().numpy(), full.cpu().numpy()
+    assert np.array_equal(got[1:4, 37:150].view(np.uint32), ref[1:4, 37:150].view(np.uint32))
+    inside = np.zeros_like(got, dtype=bool)
+    inside[1:4, 37:150] = True
+    assert (got[~inside] == 7.0).all()
+    w.free()
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("mode", [dq.QMM_INT8, dq.QMM_INT16])
+def test_qmm_gemm_modes_and_ranges(cuda, t, mode):
+    """qmm::Kernels::gemm in both modes on every format (int16, Q6_K and small row
+    counts run the GEMV passes; Q8_0 / Q4_0 / Q4_K in int8 mode the GEMMs): within the
+    north-star tolerance of qmm's reference gemv, and three unaligned [n0, n1) pieces
+    give the one-call bits."""
+    m, k, n = 67, 1024, 200
+    w_rows = gguf_weights(t, n, k, 95 + t, outlier_frac=0.01)
+    x = activations(m, k, 96 + mode, outliers=False)
+    w = dq.Weight.upload(t, w_rows, k)
+    buf, xd, a = prepared(x, mode, True)
+    st = torch.cuda.current_stream().cuda_stream
+    full = torch.full((m, n), 7.0, device="cuda")
+    dq.qmm_gemm(w, 0, n, a, full, n, None, st)
+    part = torch.full((m, n), 7.0, device="cuda")
+    for n0, n1 in ((0, 37), (37, 150), (150, n)):
+        dq.qmm_gemm(w, n0, n1, a, part, n, None, st)
+    got = full.cpu().numpy()
+    assert np.array_equal(part.cpu().numpy().view(np.uint32), got.view(np.uint32))
+    if O.ref_available():
+        ok, worst = close(got, O.ref_qmm_gemv(t, w_rows, x, mode, True))
+        assert ok, f"worst error ratio {worst:.3g}"
+    else:
+        fmt = O.ACT_PER32 if mode == dq.QMM_INT8 else O.ACT_Q16
+        ok, worst = close(got, O.matmul(t, fmt, w_rows, O.quantize_act(fmt, x), k))
+        assert ok, f"worst error ratio {worst:.3g}"
+    w.free()
