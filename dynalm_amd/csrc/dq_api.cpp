@@ -117,6 +117,12 @@ int scratch_get(int device, size_t need, void** out) { return scratch_get(g_scra
 
 constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
+// Rows from which Q4_K x int16 runs the f16 GEMM (dq_gemm_q16.hip) instead of the
+// int16 GEMV's passes of up to 4 rows, each of which reads the weight once. Measured
+// at K = 4096, N = 14336 (graph replay; GEMM vs passes): 16 rows 76 vs 59 us, 32 rows
+// 77 vs 117, 64 rows 81 vs 229, 128 rows 83 vs 448; 512 rows 176 us on the GEMM.
+constexpr int64_t kQ16GemmMinRows = 20;
+
 // Per-(device, stream) workspaces of the public entry points whose kernels need device
 // memory beyond their arguments (dq_gemm's f16 activation operands). Each stream has
 // its own buffer, so calls on different streams do not share one; the pool lock is
@@ -288,6 +294,8 @@ bool use_gemm(const dq::WeightDev& w, int fmt, int64_t m) {
   // Q4_K x per-32: the 128-row f16 GEMM against GEMV passes of 4 rows, which read the
   // weights once per pass (the GEMM takes about as long as 10 passes at N = 14336)
   if (fmt == DQ_ACT_PER32) return m > 64 && dq::gemm_p32_ok(w, m, 0, w.n);
+  // Q4_K x int16: the 64-row f16 GEMM against GEMV passes of 4 rows
+  if (fmt == DQ_ACT_Q16) return m >= kQ16GemmMinRows && dq::gemm_q16_ok(w, m, 0, w.n);
   if (w.dtype == DQ_Q6_K) {
     return m > dq::kSkinnyMaxRows ||
            (m > DQ_GEMV_MAX_ROWS && (!dq::gemv_mma_lds_ok(w.nblk, m) || w.n >= 4096));
@@ -396,6 +404,9 @@ size_t matmul_scratch_bytes(const dq_weight* w, int fmt, int64_t m) {
   if (f == DQ_ACT_PER32 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, f, m)) {
     acts += round256((size_t)act32_bytes(m, w->dev.k));  // the per-32 rows, then their act32 layout
   }
+  if (f == DQ_ACT_Q16 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, f, m)) {
+    acts += round256((size_t)act16i_bytes(m, w->dev.k));  // the int16 rows, then their act16i layout
+  }
   return acts + gemv_split_bytes(w->dev, f, m < 8 ? m : 8);
 }
 
@@ -476,6 +487,20 @@ int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int6
     if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, buf, stream); rc != DQ_OK) return rc;
     DQ_HIP(launch_act32_from_p32(static_cast<const uint8_t*>(buf), arb, m, w->dev.k, a32, s), "act32 conversion launch");
     DQ_HIP(launch_gemm_p32(w->dev, a32, m, 0, w->dev.n, y, y_stride, bias, s), "gemm launch");
+    return DQ_OK;
+  }
+  if (fmt == DQ_ACT_Q16 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, fmt, m)) {
+    // Q4_K x int16 prefill: int16 rows, their lo / 256 hi f16 layout, the f16 GEMM
+    const size_t rows_bytes = round256((size_t)(m * arb));
+    void* buf = nullptr;
+    if (int rc = acts_buffer(w->dev.device, rows_bytes + (size_t)act16i_bytes(m, w->dev.k), r, &buf); rc != DQ_OK) {
+      return rc;
+    }
+    uint8_t* a16 = static_cast<uint8_t*>(buf) + rows_bytes;
+    if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, buf, stream); rc != DQ_OK) return rc;
+    DQ_HIP(launch_act16i_from_q16(static_cast<const uint8_t*>(buf), arb, m, w->dev.k, a16, s),
+           "act16i conversion launch");
+    DQ_HIP(launch_gemm_q16(w->dev, a16, m, 0, w->dev.n, y, y_stride, bias, s), "gemm launch");
     return DQ_OK;
   }
   void* acts = nullptr;
@@ -816,6 +841,17 @@ int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
       DQ_HIP(dq::launch_act32_from_p32(static_cast<const uint8_t*>(acts), arb, m, w->dev.k, ws, as_stream(stream)),
              "act32 conversion launch");
       DQ_HIP(dq::launch_gemm_p32(w->dev, ws, m, n0, n1, y, y_stride, bias, as_stream(stream)), "gemm launch");
+      return DQ_OK;
+    });
+  }
+  if (fmt == DQ_ACT_Q16) {
+    // Q4_K x int16: lo / 256 hi as f16 operands (one conversion launch), then the f16 GEMM
+    if (!dq::gemm_q16_ok(w->dev, m, n0, n1)) return fail(DQ_UNSUPPORTED, "m too large");
+    const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
+    return with_stream_ws(w->dev.device, stream, (size_t)dq::act16i_bytes(m, w->dev.k), [&](uint8_t* ws) -> int {
+      DQ_HIP(dq::launch_act16i_from_q16(static_cast<const uint8_t*>(acts), arb, m, w->dev.k, ws, as_stream(stream)),
+             "act16i conversion launch");
+      DQ_HIP(dq::launch_gemm_q16(w->dev, ws, m, n0, n1, y, y_stride, bias, as_stream(stream)), "gemm launch");
       return DQ_OK;
     });
   }

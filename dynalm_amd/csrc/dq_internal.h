@@ -106,6 +106,16 @@ bool gemm_p32_ok(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
 hipError_t launch_act32_from_p32(const uint8_t* acts, int64_t arb, int64_t m, int64_t k, uint8_t* out, hipStream_t s);
 hipError_t launch_gemm_p32(const WeightDev& w, const uint8_t* act32, int64_t m, int64_t n0, int64_t n1, float* y,
                            int64_t ys, const float* bias, hipStream_t s);
+// The Q4_K x int16 GEMM on the f16 matrix cores (dq_gemm_q16.hip), the int16 contract
+// (ActBlockQ16 rows, qmm's int16 mode): 64 x 256 tiles, codes split into lo and 256 hi
+// as f16 in the "act16i" layout of act16i_bytes(m, k) bytes written from ActBlockQ16
+// rows (launch_act16i_from_q16). gemm_q16_ok: Q4_K and the 32-bit offset limits.
+int64_t act16i_bytes(int64_t m, int64_t k);
+bool gemm_q16_ok(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
+hipError_t launch_act16i_from_q16(const uint8_t* acts, int64_t arb, int64_t m, int64_t k, uint8_t* out,
+                                  hipStream_t s);
+hipError_t launch_gemm_q16(const WeightDev& w, const uint8_t* act, int64_t m, int64_t n0, int64_t n1, float* y,
+                           int64_t ys, const float* bias, hipStream_t s);
 // The expand-class fp32 GEMM (dq_gemm_f32.hip): weight tiles expanded to fp32 in LDS
 // and contracted with the fp32 rows x (stride xs floats) on the matrix cores; any of
 // the four weight types. Below kF32GemmMinRows rows the fp32 GEMV passes are faster.
