@@ -649,6 +649,14 @@ def main() -> None:
     log(f"default plans: prefill M={m} ({dq.KERNEL_NAMES[sel_pre.kernel]}), decode M=1 "
         f"({dq.KERNEL_NAMES[sel_dec.kernel]}; without qmm {dq.KERNEL_NAMES[sel_x86.kernel]})")
     ms_pre = time_graph(prefill_plan, 20, 3)
+
+    # ---- int16 prefill: the int16 contract (ActBlockQ16 rows) at config 4's shape,
+    # quantize + lo / 256 hi operand layout + k_gemm_q4k_q16 on the f16 matrix cores
+    def int16_prefill(i: int, st: int) -> None:
+        dq.matmul_act(weights[i % ng], dq.ACT_Q16, xg, m, K, yf, N, None, st)
+
+    log(f"int16 prefill M={m}")
+    ms_q16 = time_graph(int16_prefill, 20, 3)
     ms_dec = time_graph(decode_plan(None), args.steps, args.warmup)
     ms_dec_x86 = time_graph(decode_plan(noqmm), args.steps, args.warmup)
     tpre = ops / (ms_pre * 1e-3) / 1e12
@@ -741,6 +749,12 @@ def main() -> None:
                      "bound": "mfma", "achieved": round(tpre, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tpre / PEAK_F16_TFLOPS, 4), "traffic": traffic.get("prefill_default_m512")},
     }
+    tq16 = ops / (ms_q16 * 1e-3) / 1e12
+    result["prefill_int16_m512"] = {
+        "workload": "config 4, M=512 K=4096 N=14336 Q4_K: dq_matmul_act(DQ_ACT_Q16) (int16 quantize, "
+                    "k_act16i_from_q16, k_gemm_q4k_q16 on the f16 matrix cores)",
+        "ms_per_call": round(ms_q16, 4), "tops": round(tq16, 1),
+        "pct_peak_f16": round(100 * tq16 / PEAK_F16_TFLOPS, 2)}
     result["decode_default_plan"] = {
         "workload": f"config 3 decode, M=1 K={K} N={N} Q4_K: dq_matmul_plan under KernelPlan's defaults "
                     f"({dq.KERNEL_NAMES[sel_dec.kernel]}, per-32 activations: one quantize launch + the GEMV)",
