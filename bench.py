@@ -757,10 +757,10 @@ def main() -> None:
         "pct_peak_f16": round(100 * tq16 / PEAK_F16_TFLOPS, 2)}
     result["decode_default_plan"] = {
         "workload": f"config 3 decode, M=1 K={K} N={N} Q4_K: dq_matmul_plan under KernelPlan's defaults "
-                    f"({dq.KERNEL_NAMES[sel_dec.kernel]}, per-32 activations: one quantize launch + the GEMV)",
+                    f"({dq.KERNEL_NAMES[sel_dec.kernel]}, per-32 activations quantized inside the GEMV: one launch)",
         "ms_per_call": round(ms_dec, 5),
         "gbs": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 2),
-        "roofline": {"kernel": "dq::k_gemv<Q4_K, per-32, M=1> (ms per call: + quantize)", "bound": "hbm",
+        "roofline": {"kernel": "dq::k_gemv<Q4_K, per-32, M=1, fused quantization>", "bound": "hbm",
                      "achieved": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(dec_bytes / (ms_dec * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
         "without_qmm": {"kernel": dq.KERNEL_NAMES[sel_x86.kernel], "ms_per_call": round(ms_dec_x86, 5),

@@ -489,6 +489,16 @@ int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int6
     DQ_HIP(launch_gemm_p32(w->dev, a32, m, 0, w->dev.n, y, y_stride, bias, s), "gemm launch");
     return DQ_OK;
   }
+  if (fmt == DQ_ACT_PER32 && (w->dev.dtype == DQ_Q4_K || w->dev.dtype == DQ_Q6_K) && m <= 8 &&
+      !use_gemm(w->dev, fmt, m)) {
+    // K-quants x per-32 decode (qmm's int8 gemv): one pass, each wave quantizing its
+    // slice with the standalone quantizer's arithmetic (the codes dq_act_quantize writes)
+    const Workspace ws = split_ws(r, 0);
+    DQ_HIP(launch_gemv_fused(w->dev, x, m > 1 ? x_stride : w->dev.k, m, y, y_stride, bias, s, r.base ? &ws : nullptr,
+                             kActPer32),
+           "gemv launch");
+    return DQ_OK;
+  }
   if (fmt == DQ_ACT_Q16 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, fmt, m)) {
     // Q4_K x int16 prefill: int16 rows, their lo / 256 hi f16 layout, the f16 GEMM
     const size_t rows_bytes = round256((size_t)(m * arb));

@@ -829,13 +829,16 @@ DQ_DEV void wave_lds_sync() {
 }
 
 // Quantize this wave's blocks [b0, b1) of M fp32 rows into the staged LDS layout
-// (the fused decode path), with the standalone quantizers' device functions.
+// (the fused decode path), with the standalone quantizers' device functions. bpu:
+// 32-value activation blocks per weight block (8 for K-quant weights with per-32
+// activations, else 1).
 template <int AF, int M>
-DQ_DEV void quantize_slice(const float* __restrict__ x, int64_t xs, int nblk, int b0, int b1, int r, uint8_t* st) {
+DQ_DEV void quantize_slice(const float* __restrict__ x, int64_t xs, int nblk, int b0, int b1, int bpu, int r,
+                           uint8_t* st) {
   // For each block the fp32 loads of all M rows go out together, then the M
   // quantizations: M loads in flight per round trip instead of one.
   constexpr bool kSb = AF == kActQ8_K;
-  const int64_t kk = (int64_t)nblk * (kSb ? 256 : 32);
+  const int64_t kk = (int64_t)nblk * (kSb ? 256 : 32 * bpu);
   if constexpr (kSb) {
     for (int b = b0; b < b1; ++b) {
       float v[M][4];
@@ -855,7 +858,8 @@ DQ_DEV void quantize_slice(const float* __restrict__ x, int64_t xs, int nblk, in
       }
     }
   } else {
-    for (int bb = b0; bb < b1; bb += 8) {
+    const int e0 = b0 * bpu, e1 = b1 * bpu;  // this slice's 32-value blocks
+    for (int bb = e0; bb < e1; bb += 8) {
       const int blk = bb + (r >> 3);
       float v[M][4];
 #pragma unroll
@@ -865,8 +869,8 @@ DQ_DEV void quantize_slice(const float* __restrict__ x, int64_t xs, int nblk, in
         float d;
         int sum;
         const u32 packed = per32_quant(v[mm], d, sum);
-        if (blk < b1) {
-          uint8_t* o = st + (mm * nblk + blk) * kStage32;
+        if (blk < e1) {
+          uint8_t* o = st + (mm * nblk * bpu + blk) * kStage32;
           *reinterpret_cast<u32*>(o + 16 + 4 * (r & 7)) = packed;
           if ((r & 7) == 0) {
             *reinterpret_cast<float*>(o) = d;
@@ -991,7 +995,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
       ar.commit(arb, nblk, b0, b1, bpu, r, st, st + stage_bytes);
     }
   } else if constexpr (kFuse) {
-    quantize_slice<AF, M>(x, xs, nblk, b0, b1, r, st);
+    quantize_slice<AF, M>(x, xs, nblk, b0, b1, bpu, r, st);
   } else {
     stage_acts<AF, M>(acts, arb, nblk, b0, b1, bpu, r, st);
   }
@@ -1392,8 +1396,12 @@ static hipError_t gemv_pass(const WeightDev& w, int af, const uint8_t* acts, int
                             const Workspace* ws, hipStream_t s) {
   if (x != nullptr) {
     switch (w.dtype) {
-      case kQ4_K: return gemv_waves<kQ4_K, kActQ8_K, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
-      case kQ6_K: return gemv_waves<kQ6_K, kActQ8_K, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      case kQ4_K:
+        if (af == kActPer32) return gemv_waves<kQ4_K, kActPer32, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+        return gemv_waves<kQ4_K, kActQ8_K, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+      case kQ6_K:
+        if (af == kActPer32) return gemv_waves<kQ6_K, kActPer32, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
+        return gemv_waves<kQ6_K, kActQ8_K, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
       case kQ8_0: return gemv_waves<kQ8_0, kActPer32, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
       default: return gemv_waves<kQ4_0, kActPer32, M, true>(w, nullptr, 0, x, xs, n0, n1, y, ys, bias, dbg, ws, s);
     }
@@ -1429,7 +1437,7 @@ static hipError_t gemv_pass(const WeightDev& w, int af, const uint8_t* acts, int
 static hipError_t gemv_rows(const WeightDev& w, int af, const uint8_t* acts, int64_t arb, const float* x, int64_t xs,
                             int64_t m, int64_t n0, int64_t n1, float* y, int64_t ys, const float* bias, int32_t* dbg,
                             const Workspace* ws, hipStream_t s) {
-  const int paf = x != nullptr ? (w.dtype == kQ4_K || w.dtype == kQ6_K ? kActQ8_K : kActPer32) : af;
+  const int paf = x != nullptr && af < 0 ? (w.dtype == kQ4_K || w.dtype == kQ6_K ? kActQ8_K : kActPer32) : af;
   // rows per pass: 8, 4, 2 or 1, the most whose staged activations fit the LDS
   int pmax = 8;
   while (pmax > 1 && gemv_lds_bytes(w.dtype, paf, pmax, 16, w.nblk, false) > kGemvMaxLds) pmax /= 2;
@@ -1506,8 +1514,9 @@ hipError_t launch_gemv(const WeightDev& w, int af, const uint8_t* acts, int64_t 
 }
 
 hipError_t launch_gemv_fused(const WeightDev& w, const float* x, int64_t xs, int64_t m, float* y, int64_t ys,
-                             const float* bias, hipStream_t s, const Workspace* ws) {
-  return gemv_rows(w, -1, nullptr, 0, x, xs, m, 0, w.n, y, ys, bias, nullptr, ws, s);
+                             const float* bias, hipStream_t s, const Workspace* ws, int af) {
+  if (af >= 0 && !(af == kActPer32 && (w.dtype == kQ4_K || w.dtype == kQ6_K))) return hipErrorInvalidValue;
+  return gemv_rows(w, af, nullptr, 0, x, xs, m, 0, w.n, y, ys, bias, nullptr, ws, s);
 }
 
 }  // namespace dq

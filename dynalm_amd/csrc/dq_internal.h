@@ -71,9 +71,11 @@ hipError_t launch_gemv(const WeightDev& w, int af, const uint8_t* acts, int64_t 
                        float* y, int64_t ys, const float* bias, int32_t* dbg, hipStream_t s,
                        const Workspace* ws = nullptr);
 // Decode matmul with the activation quantization fused into the GEMV (fp32 rows x,
-// row stride xs floats; the weight's activation format, dq_act_format_for).
+// row stride xs floats): af < 0, the weight's activation format (dq_act_format_for);
+// af = kActPer32 for Q4_K / Q6_K, per-32 rows (qmm's int8 contract), each wave
+// quantizing its slice with the standalone per-32 quantizer's device function.
 hipError_t launch_gemv_fused(const WeightDev& w, const float* x, int64_t xs, int64_t m, float* y, int64_t ys,
-                             const float* bias, hipStream_t s, const Workspace* ws = nullptr);
+                             const float* bias, hipStream_t s, const Workspace* ws = nullptr, int af = -1);
 // K-ranges per row of the GEMV on this weight under activation format af (1: no
 // split-K), and the bytes of row sums a pass of up to m_pass rows then needs (0 when
 // it does not split). Both depend on the weight and the device only.
