@@ -760,7 +760,7 @@ def main() -> None:
                     f"({dq.KERNEL_NAMES[sel_dec.kernel]}, per-32 activations quantized inside the GEMV: one launch)",
         "ms_per_call": round(ms_dec, 5),
         "gbs": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 2),
-        "roofline": {"kernel": "dq::k_gemv<Q4_K, per-32, M=1, fused quantization>", "bound": "hbm",
+        "roofline": {"kernel": "dq::k_gemv_slab<16, per-32, fused> (Q4_K, M=1, 56-row workgroups)", "bound": "hbm",
                      "achieved": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(dec_bytes / (ms_dec * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
         "without_qmm": {"kernel": dq.KERNEL_NAMES[sel_x86.kernel], "ms_per_call": round(ms_dec_x86, 5),

@@ -1102,14 +1102,17 @@ __global__ __launch_bounds__(W * 64) void k_gemv(const uint8_t* __restrict__ p0,
 // to k_gemv's.
 constexpr int kSlabRows = 56;
 
-template <int NB, bool kFuse>
+template <int NB, int AF, bool kFuse>
 __global__ __launch_bounds__(NB * 64) void k_gemv_slab(const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
                                                        int64_t groups, int64_t n0, int64_t n1,
                                                        const uint8_t* __restrict__ acts, const float* __restrict__ x,
                                                        float* __restrict__ y, const float* __restrict__ bias,
                                                        int32_t* __restrict__ dbg, int64_t dbg_n) {
-  __shared__ __align__(16) uint8_t st[NB * kStageQ8K + kDummyBytes];
-  __shared__ __align__(16) float rec[NB * 64 + NB];  // t-terms [b][row], then da [b]
+  static_assert(AF == kActQ8_K || (AF == kActPer32 && kFuse), "Q8_K rows, or fp32 rows quantized to per-32 here");
+  constexpr bool kSb = AF == kActQ8_K;
+  constexpr int kStage = kSb ? NB * kStageQ8K + kDummyBytes : NB * 8 * kStage32;
+  __shared__ __align__(16) uint8_t st[kStage];
+  __shared__ __align__(16) float rec[NB * 64 + NB];  // t-terms (per-32: sums) [b][row], then da [b]
   const int l = threadIdx.x & 63, b = wave_id();
   const int64_t g0 = n0 / kRowGroup;
   const bool live = l < kSlabRows;
@@ -1136,8 +1139,19 @@ __global__ __launch_bounds__(NB * 64) void k_gemv_slab(const uint8_t* __restrict
   Chunk<kQ4_K, 1> c;
   c.load(rs, bi, bi + 1, bi + 1, r);
   __builtin_amdgcn_sched_barrier(0);
-  uint8_t* ob = st + b * kStageQ8K;
-  if constexpr (kFuse) {
+  if constexpr (!kSb) {
+    // per-32: lanes 8 j .. 8 j + 7 hold the super-block's 32-value block j (values 4 l ..)
+    float d;
+    int sum;
+    const u32 packed = per32_quant(xv, d, sum);
+    uint8_t* ob = st + (8 * b + (l >> 3)) * kStage32;
+    *reinterpret_cast<u32*>(ob + 16 + 4 * (l & 7)) = packed;
+    if ((l & 7) == 0) {
+      *reinterpret_cast<float*>(ob) = d;
+      *reinterpret_cast<int32_t*>(ob + 4) = sum;
+    }
+  } else if constexpr (kFuse) {
+    uint8_t* ob = st + b * kStageQ8K;
     float d;
     int bsum;
     const u32 packed = q8k_quant(xv, d, bsum);
@@ -1160,19 +1174,26 @@ __global__ __launch_bounds__(NB * 64) void k_gemv_slab(const uint8_t* __restrict
   o.nblk = NB;
   o.r = l;
   o.acc[0] = o.cor[0] = 0.0f;
-  compute<kActQ8_K, 1, 1>(c, b, st, o);
+  compute<AF, 1, 1>(c, b, st, o);
+  if (!kSb) rec[b * 64 + l] = o.acc[0];  // the super-block's sum, in sub-block order
   __syncthreads();
   if (b != 0 || !live) return;
-  // k_gemv's chain: acc = fma(da_b, t_b, acc), b in order
-  float t[NB], dv[NB];
-#pragma unroll
-  for (int i = 0; i < NB; ++i) {
-    t[i] = rec[i * 64 + l];
-    dv[i] = rec[NB * 64 + i];
-  }
   float v = 0.0f;
+  if constexpr (kSb) {
+    // k_gemv's chain: acc = fma(da_b, t_b, acc), b in order
+    float t[NB], dv[NB];
 #pragma unroll
-  for (int i = 0; i < NB; ++i) v = fmaf(dv[i], t[i], v);
+    for (int i = 0; i < NB; ++i) {
+      t[i] = rec[i * 64 + l];
+      dv[i] = rec[NB * 64 + i];
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) v = fmaf(dv[i], t[i], v);
+  } else {
+    // k_gemv's per-32 sum over its one-super-block waves, in wave order
+#pragma unroll
+    for (int i = 0; i < NB; ++i) v = v + rec[i * 64 + l];
+  }
   if (n >= n0 && n < n1) y[n] = bias ? v + bias[n] : v;
 }
 
@@ -1334,18 +1355,18 @@ static hipError_t gemv_early(const WeightDev& w, const uint8_t* acts, int64_t ar
   return gemv_launch<WT, AF, M, kFuse, W, 0, kSplit>(w, acts, arb, x, xs, n0, n1, y, ys, bias, dbg, sp, s);
 }
 
-template <bool kFuse>
+template <int AF, bool kFuse>
 static hipError_t gemv_slab(const WeightDev& w, const uint8_t* acts, const float* x, int64_t n0, int64_t n1, float* y,
                             const float* bias, int32_t* dbg, hipStream_t s) {
   const int64_t g0 = n0 / kRowGroup, g1 = (n1 + kRowGroup - 1) / kRowGroup;
   const unsigned grid = (unsigned)(((g1 - g0) * kRowGroup + kSlabRows - 1) / kSlabRows);
   const int64_t groups = w.n_pad / kRowGroup;
   if (w.nblk == 16) {
-    hipLaunchKernelGGL((k_gemv_slab<16, kFuse>), dim3(grid), dim3(16 * 64), 0, s, w.plane[0], w.plane[1], groups, n0,
-                       n1, acts, x, y, bias, dbg, w.n);
+    hipLaunchKernelGGL((k_gemv_slab<16, AF, kFuse>), dim3(grid), dim3(16 * 64), 0, s, w.plane[0], w.plane[1], groups,
+                       n0, n1, acts, x, y, bias, dbg, w.n);
   } else {
-    hipLaunchKernelGGL((k_gemv_slab<8, kFuse>), dim3(grid), dim3(8 * 64), 0, s, w.plane[0], w.plane[1], groups, n0, n1,
-                       acts, x, y, bias, dbg, w.n);
+    hipLaunchKernelGGL((k_gemv_slab<8, AF, kFuse>), dim3(grid), dim3(8 * 64), 0, s, w.plane[0], w.plane[1], groups, n0,
+                       n1, acts, x, y, bias, dbg, w.n);
   }
   return hipGetLastError();
 }
@@ -1359,10 +1380,11 @@ static hipError_t gemv_waves(const WeightDev& w, const uint8_t* acts, int64_t ar
   // row groups, not from [n0, n1): a row's slices, and so its fp32 sum order, do not
   // depend on how the caller partitions the rows (qmm.h:35-36).
   const int64_t groups = w.n_pad / kRowGroup;
-  if constexpr (WT == kQ4_K && AF == kActQ8_K && M == 1) {
+  if constexpr (WT == kQ4_K && M == 1 && (AF == kActQ8_K || (AF == kActPer32 && kFuse))) {
     // fewer row groups than CUs: 56-row workgroups spread the row over more CUs
-    if ((w.nblk == 8 || w.nblk == 16) && groups * kRowGroup <= (int64_t)kSlabRows * w.cus) {
-      return gemv_slab<kFuse>(w, acts, x, n0, n1, y, bias, dbg, s);
+    if ((w.nblk == 8 || w.nblk == 16) && groups * kRowGroup <= (int64_t)kSlabRows * w.cus &&
+        (AF == kActQ8_K || gemv_splits(w, AF) == 1)) {
+      return gemv_slab<AF, kFuse>(w, acts, x, n0, n1, y, bias, dbg, s);
     }
   }
   const int splits = gemv_splits(w, AF);

@@ -3,9 +3,10 @@
 rows, and so the default plan's decode): each wave quantizes its slice of the fp32
 rows with the standalone per-32 quantizer's device function, so the codes, and then
 every output bit, equal dq_act_quantize followed by dq_gemv on the same rows. Cases:
-1 to 8 rows, super-block counts of 1, 5 and 16, a long Q6_K row that the GEMV splits
-over K (K = 14336), and rows x_stride > k floats apart; plus the oracle's per-32
-order within the north-star tolerance.
+1 to 8 rows, super-block counts of 1, 5, 8 and 16 (one Q4_K row of 8 or 16 runs on
+56-row workgroups, k_gemv_slab), config 3's full gate shape, a long Q6_K row that the
+GEMV splits over K (K = 14336), and rows x_stride > k floats apart; plus the oracle's
+per-32 order within the north-star tolerance.
 
 Reference style: dynacore/tests/test_qmm.cpp:178-282 (tier equality).
 """
@@ -29,7 +30,7 @@ def host(t) -> np.ndarray:
 
 
 @pytest.mark.parametrize("t", [O.Q4_K, O.Q6_K], ids=lambda t: O.TYPE_NAMES[t])
-@pytest.mark.parametrize("m,k,n", [(1, 4096, 1000), (3, 1280, 300), (8, 256, 200), (5, 4096, 130)])
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 1000), (1, 2048, 130), (3, 1280, 300), (8, 256, 200), (5, 4096, 130)])
 def test_fused_per32_equals_quantize_then_gemv(cuda, t, m, k, n):
     import dqtorch as T
 
@@ -62,4 +63,24 @@ def test_fused_per32_long_q6k_rows(cuda):
     fused = host(T.matmul_act(w, O.ACT_PER32, xd))
     two = host(T.gemv(w, O.ACT_PER32, T.quantize(O.ACT_PER32, xd)))
     assert np.array_equal(fused.view(np.uint32), two.view(np.uint32))
+    w.free()
+
+
+def test_fused_per32_config3_shape(cuda):
+    """Config 3's gate shape (Q4_K K=4096 N=14336) at one row: the default plan's decode
+    (256 workgroups of 56 rows) equals the two-launch route on every row."""
+    import dqtorch as T
+
+    k, n = 4096, 14336
+    w_rows = gguf_weights(O.Q4_K, n, k, 8950, outlier_frac=0.01)
+    x = activations(1, k, 8951, outliers=False)
+    w = dq.Weight.upload(O.Q4_K, w_rows, k)
+    xd = torch.from_numpy(x).cuda()
+    fused = host(T.matmul_act(w, O.ACT_PER32, xd))
+    two = host(T.gemv(w, O.ACT_PER32, T.quantize(O.ACT_PER32, xd)))
+    assert np.array_equal(fused.view(np.uint32), two.view(np.uint32))
+    rows = np.random.default_rng(8952).choice(n, 128, replace=False)
+    want = O.matmul(O.Q4_K, O.ACT_PER32, w_rows[rows], O.quantize_act(O.ACT_PER32, x), k)
+    ok, worst = close(fused[:, rows], want)
+    assert ok, f"worst error ratio {worst:.3g}"
     w.free()
