@@ -362,14 +362,22 @@ def test_generic_dots_golden_bit_exact(gold, t):
 @pytest.mark.parametrize("t", (O.Q4_K, O.Q6_K), ids=lambda t: O.TYPE_NAMES[t])
 def test_q8K_and_sx_dots_vs_reference_avx2(gold, t):
     """Q8_K (canonical order) vs the reference super-block kernel on the same codes,
-    and sub-scaled vs the reference sx kernel: fp32 reorderings only."""
+    and sub-scaled vs the reference sx kernel: fp32 reorderings only, so every output
+    is held to a per-element bound on its own sum of |terms|: 1e-6 of it, a tenth of
+    the reference's (test_int_kernels.cpp:131-147; the two orders differ by at most
+    2e-8 of it on these vectors, while one dropped or doubled term moves an output by
+    ~1/512 of it)."""
     name = O.TYPE_NAMES[t]
     w = gold[f"w_{name}"]
-    yq = O.matmul(t, O.ACT_Q8_K, w, O.quantize_act(O.ACT_Q8_K, gold["act_x"]), 512)
-    mag = np.abs(gold[f"sbdot_{name}"]).max()
-    assert np.max(np.abs(yq - gold[f"sbdot_{name}"])) <= 1e-5 * mag
+    wf = np.abs(O.dequantize(t, w, 512).astype(np.float64))
+    aq = O.quantize_act(O.ACT_Q8_K, gold["act_x"])
+    yq = O.matmul(t, O.ACT_Q8_K, w, aq, 512)
+    mag = np.abs(O.dequantize_act(O.ACT_Q8_K, aq, 512).astype(np.float64)) @ wf.T
+    assert np.all(np.isfinite(mag))
+    assert np.all(np.abs(yq - gold[f"sbdot_{name}"]) <= 1e-6 * mag)
     ys = O.matmul(t, O.ACT_SX, w, gold["act_sx"], 512)
-    assert np.max(np.abs(ys - gold[f"sxdot_{name}"])) <= 1e-5 * np.abs(gold[f"sxdot_{name}"]).max()
+    mag_s = np.abs(O.dequantize_act(O.ACT_SX, gold["act_sx"], 512).astype(np.float64)) @ wf.T
+    assert np.all(np.abs(ys - gold[f"sxdot_{name}"]) <= 1e-6 * mag_s)
 
 
 @pytest.mark.parametrize("t", (O.Q8_0, O.Q4_K, O.Q6_K), ids=lambda t: O.TYPE_NAMES[t])
