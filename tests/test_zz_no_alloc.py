@@ -41,6 +41,7 @@ CASES = [
     ("q6k-skinny", O.Q6_K, 1536, 1536, 40, 16),       # quantize + skinny passes, then the fused skinny launch
     ("q4_0-b32gemm", O.Q4_0, 2048, 4096, 64, 2),      # per-32 quantize + block GEMM, then the fused GEMV
     ("q6k-down-gemm", O.Q6_K, 4096, 14336, 200, 17),  # Q6_K large GEMM at K = 14336
+    ("q6k-down-split", O.Q6_K, 1536, 8960, 16, 7),    # quantize + split skinny (t-terms in the array) + chains
 ]
 
 

@@ -4,7 +4,8 @@ A fresh child process captures dq_matmul_noalloc into a torch.cuda.graph before 
 other call of it, so the capture holds the first call on the device: the one-time
 lookup of the static array's device address and the launches' attribute calls happen
 while the stream is capturing. Each route that uses the array (the f16 Q4_K GEMM, the
-per-32 block GEMM, the skinny MFMA passes, the split-K decode GEMV) is captured as its
+per-32 block GEMM, the skinny MFMA passes, the split-K decode GEMV, the split skinny
+launch with its t-terms and chain launch) is captured as its
 first call for that weight and shape; every replay, with eager work on the same
 buffers between replays, equals eager dq_matmul bit for bit."""
 from __future__ import annotations
@@ -31,7 +32,8 @@ from dqtest import activations, gguf_weights
 
 # (name, dtype, n, k, m): one route of dq_matmul that uses the array each
 CASES = [("q4k-f16-gemm", dq.Q4_K, 14336, 4096, 512), ("q4_0-b32-gemm", dq.Q4_0, 2048, 4096, 64),
-         ("q6k-skinny", dq.Q6_K, 1536, 1536, 40), ("q8_0-splitk", dq.Q8_0, 4096, 14336, 3)]
+         ("q6k-skinny", dq.Q6_K, 1536, 1536, 40), ("q8_0-splitk", dq.Q8_0, 4096, 14336, 3),
+         ("q6k-skinny-split", dq.Q6_K, 1536, 8960, 16)]
 for name, t, n, k, m in CASES:
     print("case", name, flush=True)
     w = dq.Weight.upload(t, gguf_weights(t, n, k, 700 + t), k)
@@ -63,5 +65,5 @@ def test_noalloc_graph_capture_first_call(cuda):
                          timeout=300, env=env)
     out = res.stdout + res.stderr
     assert res.returncode == 0, out[-3000:]
-    for name in ("q4k-f16-gemm", "q4_0-b32-gemm", "q6k-skinny", "q8_0-splitk"):
+    for name in ("q4k-f16-gemm", "q4_0-b32-gemm", "q6k-skinny", "q8_0-splitk", "q6k-skinny-split"):
         assert f"ok {name}" in res.stdout, out[-3000:]
