@@ -21,7 +21,7 @@ LIB = os.path.join(LIB_DIR, "libdynaq.so")
 CEIL_LIB = os.path.join(LIB_DIR, "libdqceil.so")
 CEIL_SOURCES = ["dq_ceiling.hip"]
 
-SOURCES = ["dq_kernels.hip", "dq_gemv.hip", "dq_gemm.hip", "dq_gemm_b32.hip", "dq_gemm_f32.hip", "dq_gemm_h16.hip", "dq_gemm_p32.hip", "dq_gemm_q16.hip", "dq_skinny.hip", "dq_api.cpp",
+SOURCES = ["dq_kernels.hip", "dq_gemv.hip", "dq_gemm.hip", "dq_gemm_b32.hip", "dq_gemm_f32.hip", "dq_gemm_h16.hip", "dq_gemm_p32.hip", "dq_gemm_q16.hip", "dq_gemm_q6x.hip", "dq_skinny.hip", "dq_api.cpp",
            "dq_gguf.cpp", "dq_external.cpp", "dq_noalloc.hip",
            "dq_plan.cpp"]
 ARCH = os.environ.get("DYNAQ_ARCH", "gfx950")

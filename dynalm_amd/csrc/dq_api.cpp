@@ -122,6 +122,9 @@ constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 // at K = 4096, N = 14336 (graph replay; GEMM vs passes): 16 rows 76 vs 59 us, 32 rows
 // 77 vs 117, 64 rows 81 vs 229, 128 rows 83 vs 448; 512 rows 176 us on the GEMM.
 constexpr int64_t kQ16GemmMinRows = 20;
+// Rows from which Q6_K x per-32 / int16 runs the f16 GEMM (dq_gemm_q6x.hip) instead of
+// the GEMV passes.
+constexpr int64_t kQ6xGemmMinRows = 16;
 
 // Per-(device, stream) workspaces of the public entry points whose kernels need device
 // memory beyond their arguments (dq_gemm's f16 activation operands). Each stream has
@@ -293,6 +296,10 @@ bool use_gemm(const dq::WeightDev& w, int fmt, int64_t m) {
   if (w.dtype == DQ_Q8_0 || w.dtype == DQ_Q4_0) return m >= 13;
   // Q4_K x per-32: the 128-row f16 GEMM against GEMV passes of 4 rows, which read the
   // weights once per pass (the GEMM takes about as long as 10 passes at N = 14336)
+  // Q6_K x per-32 / int16: the f16 GEMM against GEMV passes of up to 4 (8) rows
+  if (w.dtype == DQ_Q6_K && (fmt == DQ_ACT_PER32 || fmt == DQ_ACT_Q16)) {
+    return m >= kQ6xGemmMinRows && dq::gemm_q6x_ok(w, fmt, m, 0, w.n);
+  }
   if (fmt == DQ_ACT_PER32) return m > 64 && dq::gemm_p32_ok(w, m, 0, w.n);
   // Q4_K x int16: the 64-row f16 GEMM against GEMV passes of 4 rows
   if (fmt == DQ_ACT_Q16) return m >= kQ16GemmMinRows && dq::gemm_q16_ok(w, m, 0, w.n);
@@ -407,6 +414,9 @@ size_t matmul_scratch_bytes(const dq_weight* w, int fmt, int64_t m) {
   if (f == DQ_ACT_Q16 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, f, m)) {
     acts += round256((size_t)act16i_bytes(m, w->dev.k));  // the int16 rows, then their act16i layout
   }
+  if (w->dev.dtype == DQ_Q6_K && (f == DQ_ACT_PER32 || f == DQ_ACT_Q16) && use_gemm(w->dev, f, m)) {
+    acts += round256((size_t)(f == DQ_ACT_Q16 ? act16i_bytes(m, w->dev.k) : act32_bytes(m, w->dev.k)));
+  }
   return acts + gemv_split_bytes(w->dev, f, m < 8 ? m : 8);
 }
 
@@ -497,6 +507,22 @@ int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int6
     DQ_HIP(launch_gemv_fused(w->dev, x, m > 1 ? x_stride : w->dev.k, m, y, y_stride, bias, s, r.base ? &ws : nullptr,
                              kActPer32),
            "gemv launch");
+    return DQ_OK;
+  }
+  if (w->dev.dtype == DQ_Q6_K && (fmt == DQ_ACT_PER32 || fmt == DQ_ACT_Q16) && use_gemm(w->dev, fmt, m)) {
+    // Q6_K x per-32 / int16 prefill: the rows, their f16 operand layout, the f16 GEMM
+    const bool i16 = fmt == DQ_ACT_Q16;
+    const size_t rows_bytes = round256((size_t)(m * arb));
+    const size_t lay = (size_t)(i16 ? act16i_bytes(m, w->dev.k) : act32_bytes(m, w->dev.k));
+    void* buf = nullptr;
+    if (int rc = acts_buffer(w->dev.device, rows_bytes + lay, r, &buf); rc != DQ_OK) return rc;
+    uint8_t* a2 = static_cast<uint8_t*>(buf) + rows_bytes;
+    if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, buf, stream); rc != DQ_OK) return rc;
+    const uint8_t* rows = static_cast<const uint8_t*>(buf);
+    DQ_HIP(i16 ? launch_act16i_from_q16(rows, arb, m, w->dev.k, a2, s) : launch_act32_from_p32(rows, arb, m, w->dev.k, a2, s),
+           "operand conversion launch");
+    DQ_HIP(launch_gemm_q6x(w->dev, fmt, a2, i16 ? act16i_rows(m) : act32_rows(m), m, 0, w->dev.n, y, y_stride, bias, s),
+           "gemm launch");
     return DQ_OK;
   }
   if (fmt == DQ_ACT_Q16 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, fmt, m)) {
@@ -851,6 +877,23 @@ int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
       DQ_HIP(dq::launch_act32_from_p32(static_cast<const uint8_t*>(acts), arb, m, w->dev.k, ws, as_stream(stream)),
              "act32 conversion launch");
       DQ_HIP(dq::launch_gemm_p32(w->dev, ws, m, n0, n1, y, y_stride, bias, as_stream(stream)), "gemm launch");
+      return DQ_OK;
+    });
+  }
+  if (w->dev.dtype == DQ_Q6_K && (fmt == DQ_ACT_PER32 || fmt == DQ_ACT_Q16)) {
+    // Q6_K x per-32 / int16: the codes as f16 operands (one conversion launch), then the f16 GEMM
+    if (!dq::gemm_q6x_ok(w->dev, fmt, m, n0, n1)) return fail(DQ_UNSUPPORTED, "m too large");
+    const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
+    const bool i16 = fmt == DQ_ACT_Q16;
+    const size_t bytes = (size_t)(i16 ? dq::act16i_bytes(m, w->dev.k) : dq::act32_bytes(m, w->dev.k));
+    return with_stream_ws(w->dev.device, stream, bytes, [&](uint8_t* ws) -> int {
+      const uint8_t* a = static_cast<const uint8_t*>(acts);
+      DQ_HIP(i16 ? dq::launch_act16i_from_q16(a, arb, m, w->dev.k, ws, as_stream(stream))
+                 : dq::launch_act32_from_p32(a, arb, m, w->dev.k, ws, as_stream(stream)),
+             "operand conversion launch");
+      DQ_HIP(dq::launch_gemm_q6x(w->dev, fmt, ws, i16 ? dq::act16i_rows(m) : dq::act32_rows(m), m, n0, n1, y, y_stride,
+                                 bias, as_stream(stream)),
+             "gemm launch");
       return DQ_OK;
     });
   }

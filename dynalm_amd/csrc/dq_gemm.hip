@@ -734,8 +734,8 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
 }
 
 bool gemm_supported(int dtype, int af) {
-  return ((dtype == kQ4_K || dtype == kQ6_K) && af == kActQ8_K) ||
-         (dtype == kQ4_K && (af == kActPer32 || af == kActQ16)) || gemm_b32_supported(dtype, af);
+  return ((dtype == kQ4_K || dtype == kQ6_K) && (af == kActQ8_K || af == kActPer32 || af == kActQ16)) ||
+         gemm_b32_supported(dtype, af);
 }
 
 namespace {

@@ -26,9 +26,9 @@ bool allowed(const dq_plan& p, int id) { return (p.matmul_disabled & (1u << id))
 
 bool kquant(int t) { return t == DQ_Q4_K || t == DQ_Q6_K; }
 
-// MatmulCaps::qmm_gemm of this GPU: the weight types whose qmm int8 rows run on a GEMM
-// kernel (dq_gemm_b32.hip, dq_gemm_p32.hip).
-bool qmm_gemm(int t) { return t == DQ_Q8_0 || t == DQ_Q4_0 || t == DQ_Q4_K; }
+// MatmulCaps::qmm_gemm of this GPU: the weight types whose qmm rows run on a GEMM kernel
+// (dq_gemm_b32.hip, dq_gemm_p32.hip, dq_gemm_q16.hip, dq_gemm_q6x.hip): all four.
+bool qmm_gemm(int t) { return t == DQ_Q8_0 || t == DQ_Q4_0 || t == DQ_Q4_K || t == DQ_Q6_K; }
 
 }  // namespace
 

@@ -93,7 +93,8 @@ typedef enum dq_dtype {
  *                 (Q4_0 as qmm's int16 mode runs it, qmm_reference.cpp:68-93; the reference's
  *                 AVX2 int16 kernels cover Q8_0, Q4_K and Q6_K); the GEMV forms each
  *                 32-value (Q6_K: 16-value) integer dot exactly; Q4_K's GEMM (from 20
- *                 rows) splits each code into lo and 256 hi on the f16 matrix cores;
+ *                 rows) and Q6_K's (from 16) split each code into lo and 256 hi on the
+ *                 f16 matrix cores;
  *   DQ_ACT_F32    no quantization: fp32 rows of k floats (4k bytes), dynacore's kF32
  *                 contract (f32_row_dot, the reference-accuracy fallback and x86 prefill
  *                 default, dynacore/src/kernel/matmul_registry.cpp:51-54) with the arithmetic
@@ -210,9 +211,9 @@ DQ_API int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int
 /* dq_gemm runs the prefill GEMMs on the matrix cores: Q4_K and Q6_K weights with
  * DQ_ACT_Q8_K activations (the super-block pair's canonical fp32 order, bit-identical to
  * dq_gemv), Q8_0 / Q4_0 weights with DQ_ACT_PER32 (each output in the reference's
- * generic per-32 block order, kernels_generic.cpp:216-239), and Q4_K weights with
- * DQ_ACT_PER32 or DQ_ACT_Q16 (f16 matrix-core GEMMs that sum in an order of their own:
- * within the fp32 tolerance of a K-term dot product of the reference's); other pairs
+ * generic per-32 block order, kernels_generic.cpp:216-239), and Q4_K and Q6_K weights
+ * with DQ_ACT_PER32 or DQ_ACT_Q16 (f16 matrix-core GEMMs that sum in an order of their
+ * own: within the fp32 tolerance of a K-term dot product of the reference's); other pairs
  * return DQ_UNSUPPORTED; any m.
  * Replaces qmm::Kernels::gemm (dynacore/include/dynacore/cpu/qmm.h:128-129). */
 DQ_API int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0, int64_t n1, float* y,

@@ -79,7 +79,7 @@ int ref_has_avx2(void) { return cpu_info().features.avx2 ? 1 : 0; }
 // backend: int8-accelerated, without interleaved copies, SME or external kernels;
 // kernel table: quantize_act / _sb / _sx / 16; per-32 row dots for Q4_0, Q8_0, Q4_K,
 // Q6_K; super-block and sub-scaled dots for Q4_K, Q6_K; int16 dots for all four;
-// qmm int8 and int16 for all four (k % 32 == 0) with a gemm for Q8_0, Q4_0, Q4_K.
+// qmm int8 and int16 for all four (k % 32 == 0), each with a gemm.
 // Returns the MatmulKernelId and writes the MatmulActFormat to *act.
 int ref_select_matmul(int64_t m, int64_t n, int64_t k, int dtype, int x_dense, int expand_min_rows,
                       int int8_decode_max_rows, int int16_decode_max_rows, int int8_superblock_min_rows,
@@ -112,7 +112,7 @@ int ref_select_matmul(int64_t m, int64_t n, int64_t k, int dtype, int x_dense, i
   c.dot_q8_sx_rows = kq;
   c.dot_q16_rows = true;
   c.qmm_int8 = c.qmm_int16 = k % 32 == 0;
-  c.qmm_gemm = wt == DType::kQ8_0 || wt == DType::kQ4_0 || wt == DType::kQ4_K;
+  c.qmm_gemm = wt == DType::kQ8_0 || wt == DType::kQ4_0 || wt == DType::kQ4_K || wt == DType::kQ6_K;
   const MatmulSelection sel = select_matmul(s, p, c);
   if (act != nullptr) *act = static_cast<int>(sel.act);
   return static_cast<int>(sel.id);

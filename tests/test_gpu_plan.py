@@ -109,8 +109,8 @@ def test_ffn_down_plan_int16(cuda, t):
                          ids=["q4_K-300", "q4_K-40", "q8_0-130", "q6_K-70"])
 def test_engine_qmm_plan(cuda, t, m):
     """The engine's plan on a backend with accelerated qmm (int8 rows unbounded,
-    dynalm/src/runtime/engine.cpp:365-375): qmm's gemm on per-32 rows from 9 rows where
-    the type has one (Q4_K: the f16 GEMM above 64 rows), else its gemv; the same bits as
+    dynalm/src/runtime/engine.cpp:365-375): qmm's gemm on per-32 rows from 9 rows (Q4_K:
+    the f16 GEMM above 64 rows, Q6_K: from 16 rows, GEMV passes below); the same bits as
     the per-32 contract's own path, within tolerance of the oracle."""
     import dqtorch as T
 
@@ -121,7 +121,7 @@ def test_engine_qmm_plan(cuda, t, m):
     eng = dq.plan_defaults()
     eng.int8_decode_max_rows = 1 << 30
     sel = dq.select(m, n, k, t, eng)
-    assert (sel.kernel, sel.act) == (dq.KERNEL_QMM_GEMV if t == O.Q6_K else dq.KERNEL_QMM_GEMM, O.ACT_PER32)
+    assert (sel.kernel, sel.act) == (dq.KERNEL_QMM_GEMM, O.ACT_PER32)
     y = run_plan(w, eng, x)
     assert np.array_equal(y.view(np.uint32), host(T.matmul_act(w, O.ACT_PER32, dev(x))).view(np.uint32))
     ok, worst = close(y, O.matmul(t, O.ACT_PER32, rows, O.quantize_act(O.ACT_PER32, x), k))

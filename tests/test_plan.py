@@ -77,11 +77,14 @@ def test_default_classes_known_answers():
     # the engine's plan on a qmm-accelerated backend (engine.cpp:365-375): qmm at any size
     eng = dq.plan_defaults()
     eng.int8_decode_max_rows = 1 << 30
-    for t in (dq.Q4_K, dq.Q8_0, dq.Q4_0):
+    for t in (dq.Q4_K, dq.Q8_0, dq.Q4_0, dq.Q6_K):
         assert (dq.select(512, 14336, 4096, t, eng).kernel, dq.select(512, 14336, 4096, t, eng).act) == (
             dq.KERNEL_QMM_GEMM, dq.ACT_PER32)
         assert dq.select(8, 14336, 4096, t, eng).kernel == dq.KERNEL_QMM_GEMV
-    assert dq.select(512, 4096, 14336, dq.Q6_K, eng).kernel == dq.KERNEL_QMM_GEMV  # no Q6_K qmm gemm here
+    # and its FFN down plan (transformer.cpp:541-550): int16 rows through qmm at any size
+    eng_down = dq.plan_ffn_down(eng)
+    assert (dq.select(512, 4096, 14336, dq.Q6_K, eng_down).kernel, dq.select(512, 4096, 14336, dq.Q6_K, eng_down).act) == (
+        dq.KERNEL_QMM_GEMM, dq.ACT_Q16)
     down = dq.plan_ffn_down()
     for t in (dq.Q6_K, dq.Q4_K, dq.Q8_0, dq.Q4_0):
         assert (dq.select(8, 4096, 14336, t, down).kernel, dq.select(8, 4096, 14336, t, down).act) == (
