@@ -7,24 +7,33 @@
 //   acc += d da_j sum_u sc_u sum_t (q_t - 32) a_t       (qmm_reference.cpp:68-93 with
 // Fmt<kQ6_K>, qmm_unpack.h; the int16 row kernel, kernels_avx2.cpp:1661-1765), u the two
 // 16-value units of the block, sc_u their int8 scales (quant_formats.cpp:192-216). The
-// effective weight w = sc_u (q - 32) lies in [-4064, 4096]: too wide for f16, so it
-// splits exactly as w = 64 wh + wl, wh = floor(w / 64) in [-64, 64], wl in [0, 63], and
-// both 64 wh and wl are f16 integers. They are the A operand of two v_mfma_f32_32x32x16_f16 per K-step
-// into one accumulator, the activation codes the B operand (per-32: the int8 codes;
-// int16: lo and 256 hi, two more MFMAs): every product is exact, and a block's sum
-// |sum w a| <= 32 * 4096 * 127 < 2^24 is exact (int16: rounded to fp32 where the running
-// sum passes 2^24). Then, as the per-32 GEMM (dq_gemm_p32.hip) does,
+// effective weight w = sc_u (q - 32) lies in [-4064, 4096]: too wide for f16, so the
+// scale splits as sc = fh + fl, fh = 16 (sc >> 4) in [-128, 112], fl = sc & 15, and
+// w = fh (q - 32) + fl (q - 32), two f16 integers (at most 4096 = 16 * 8 * 32 and 480 in
+// magnitude). Each is built, scaled by 2^-24, by one packed fma from q as raw f16 bits
+// (the subnormal q 2^-24): fma(q 2^-24, f, -32 f 2^-24), exact because its result is
+// representable. They are the A operand of two v_mfma_f32_32x32x16_f16 per K-step into
+// one accumulator, the activation codes the B operand (per-32: the int8 codes; int16: lo
+// and 256 hi, two more MFMAs): every product is exact, and a block's sum
+// |sum w a| <= 32 * 4096 * 127 < 2^24 (in units of 2^-24) is exact (int16: rounded to fp32
+// where the running sum passes 2^24). Then, as the per-32 GEMM (dq_gemm_p32.hip) does,
 //   per block:        T = fma(da_j, S_j, T)
-//   per super-block:  acc = fma(d, T, acc)
+//   per super-block:  acc = fma(d 2^24, T, acc)
 // The order is not the reference's: the outputs agree within the fp32 tolerance of a
 // K-term dot product, not bit for bit.
 //
 // Work split. A workgroup owns 64 activation rows x 128 weight rows with 4 waves; wave w
 // owns weight rows 32 w .. 32 w + 31 (lane l builds row l % 32's operands for lane half
 // hh = l / 32 from the Q6_K planes it loads itself) against the two 32-row activation
-// tiles. 256 workgroups at config 3's down shape (M = 512, N = 4096). A super-block's
-// activation operands (32 KB per-32, 64 KB int16) and scales (2 KB) go to LDS one interval
-// ahead by direct-to-LDS loads spread over the K-steps, into a ring of two.
+// tiles. 256 workgroups at config 3's down shape (M = 512, N = 4096): one wave per SIMD,
+// so a wave overlaps its own work. Per block, tile 0's MFMA chain runs beside the fold of
+// tile 1's previous block and half of the next block's operand build, then tile 1's
+// chain beside the fold of tile 0's block and the other half. A super-block's activation
+// operands (32 KB per-32, 64 KB int16) and scales (2 KB) go to LDS one interval ahead by
+// direct-to-LDS loads spread over the blocks, into a ring of two; each weight plane chunk
+// is reloaded for the next super-block right after its last read. Each CU streams ~3.3 MB
+// (per-32) or ~5.2 MB (int16) at M = 512, N = 4096, K = 14336, so the per-CU read rate
+// (~22 KB/us) bounds the kernel near 150 (235) us.
 //
 // Activation layouts: per-32 rows as "act32" (k_act32_from_p32, dq_gemm_p32.hip), int16
 // rows as "act16i" (k_act16i_from_q16, dq_gemm_q16.hip), both with the K order in which
@@ -62,36 +71,19 @@ struct XLds {
 static_assert(XLds<true>::kTotal <= 160 * 1024, "LDS");
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-typedef short s2_t __attribute__((ext_vector_type(2)));
-
-// Two codes q (bytes 0 and 2 of the dword p, or 1 and 3) of one unit with scale sc as the
-// f16 pairs (64 wh, wl) of w = sc (q - 32) = 64 wh + wl.
-DQ_DEV void q6_pair_f16(u32 p, int sc, u32& hi, u32& lo) {
-  const s2_t q = __builtin_bit_cast(s2_t, p);
-  const s2_t k = {(short)sc, (short)sc}, c = {(short)(-32 * sc), (short)(-32 * sc)};
-  const s2_t w = q * k + c;
-  const s2_t wh = (w >> (short)6) + (short)64;  // 0 .. 128
-  const s2_t m63 = {63, 63};
-  const s2_t wl = w & m63;
-  // an integer v < 1024 in the mantissa of 1024's f16 (bits 0x6400 | v) is 1024 + v exactly
-  const h2_t fl = __builtin_bit_cast(h2_t, __builtin_bit_cast(u32, wl) | 0x64006400u) - h2_t{1024.0f16, 1024.0f16};
-  const h2_t fh = (__builtin_bit_cast(h2_t, __builtin_bit_cast(u32, wh) | 0x64006400u) - h2_t{1088.0f16, 1088.0f16}) *
-                  h2_t{64.0f16, 64.0f16};
-  lo = __builtin_bit_cast(u32, fl);
-  hi = __builtin_bit_cast(u32, fh);
-}
 
 }  // namespace
 
 // One workgroup: activation rows [64 tm, + 64) x weight rows [nbase0 + 128 tn, + 128), all
 // super-blocks. Arguments as launch_gemm_q6x.
 template <bool kI16>
-__global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemm_q6k_x(
+__global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_q6k_x(
     const uint8_t* __restrict__ ql_plane, const uint8_t* __restrict__ qh_plane, const uint8_t* __restrict__ sc_plane,
     const uint8_t* __restrict__ d_plane, int nb, int64_t nbase0, int64_t n_pad, int64_t n0, int64_t n1,
     const uint8_t* __restrict__ act, int64_t m_pad, int64_t m, float* __restrict__ y, int64_t ys,
     const float* __restrict__ bias, int tiles_m) {
   using X = XLds<kI16>;
+  constexpr int kP = X::kPlanes;
   extern __shared__ __align__(16) uint8_t lds[];
   const int t = threadIdx.x, lane = t & 63;
   const int li = lane & 31, hh = lane >> 5;
@@ -103,142 +95,209 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(1, 2)
 
   // activation layout: codes (bytes per 32-row tile and super-block: 16 K-steps x planes x
   // 1 KB), then da, (then c, unused here)
-  const int64_t codes_bytes = m_pad * nb * 512 * X::kPlanes, da_bytes = m_pad / 32 * nb * 1024;
+  const int64_t codes_bytes = m_pad * nb * 512 * kP, da_bytes = m_pad / 32 * nb * 1024;
   const auto ra = rsrc(act, (u32)(codes_bytes + da_bytes));
   const auto rl = rsrc(ql_plane, (u32)(n_pad * nb * 128));
   const auto rhq = rsrc(qh_plane, (u32)(n_pad * nb * 64));
   const auto rs = rsrc(sc_plane, (u32)(n_pad * nb * 16));
   const auto rd = rsrc(d_plane, (u32)(n_pad * nb * 2));
 
-  // ---- this wave's loads. Operands of super-block s: blocks jb = 8 wave + i (i < 8, and
-  // 16 per wave with two planes) of the buffer; with piece 0 the activation scales of tile
-  // wave (waves 0, 1). The wave's weight row: group g0 + wave / 2, row 32 (wave & 1) + li.
+  // ---- this wave's loads. Operands of super-block s: blocks jb = 8 P wave + i (i < 8 P)
+  // of the buffer; with piece 0 the activation scales of tile wave (waves 0, 1). The wave's
+  // weight row: group g0 + wave / 2, row 32 (wave & 1) + li.
   const u32 g0 = (u32)(nbase >> 6);
   const u32 G = g0 + (u32)(wave >> 1), r64 = (u32)(32 * (wave & 1) + li);
-  constexpr int kPieces = 8 * X::kPlanes;  // 1 KB pieces per wave and super-block
+  constexpr int kPieces = 8 * kP;  // 1 KB pieces per wave and super-block
   auto issue_piece = [&](int s, int i) {
     uint8_t* P = lds + (s & 1) * X::kBuf;
     const int jb = kPieces * wave + i;  // = (k * 2 + tt) * planes + p
     const int p = kI16 ? (jb & 1) : 0, kt = kI16 ? (jb >> 1) : jb;
     const int64_t T = 2 * (int64_t)tm + (kt & 1);
     const int k = kt >> 1;
-    dma16(ra, P + jb * 1024, (u32)(lane * 16), (u32)((((T * nb + s) * 16 + k) * X::kPlanes + p) * 1024));
+    dma16(ra, P + jb * 1024, (u32)(lane * 16), (u32)((((T * nb + s) * 16 + k) * kP + p) * 1024));
     if (i == 0 && wave < 2) {
       const int64_t Tb = 2 * (int64_t)tm + wave;
       dma16(ra, P + X::kDa + wave * 1024, (u32)(lane * 16), (u32)(codes_bytes + (Tb * nb + s) * 1024));
     }
   };
-  // the weight row's planes of super-block s (past the end: the last one again)
+  // The weight row's planes of super-block s (past the end: the last one again), one
+  // register set: each chunk is reloaded with the next super-block's right after the
+  // operand build that last reads it (ql chunks 0, 1 and qh chunk 0 after block 2's
+  // build, the rest after block 6's); the scales and d of the next super-block go to
+  // sc_n / d_n at the start of a super-block.
   struct W6 {
     v4u ql[4], qh[2], sc;
     u32 d;
   };
-  auto ld_w = [&](int s, W6& w) {
-    const u32 b = (u32)(s < nb ? s : nb - 1);
-    const u32 gb = G * (u32)nb + b;
+  auto wofs = [&](int s) -> u32 { return G * (u32)nb + (u32)(s < nb ? s : nb - 1); };
+  auto ld_ql = [&](int s, int i) { return ld16(rl, ((wofs(s) * 8u + 2u * (u32)i + (u32)hh) * 64u + r64) * 16u); };
+  auto ld_qh = [&](int s, int i) { return ld16(rhq, ((wofs(s) * 4u + 2u * (u32)i + (u32)hh) * 64u + r64) * 16u); };
+  auto ld_sc = [&](int s) { return ld16(rs, (wofs(s) * 64u + r64) * 16u); };
+  auto ld_d = [&](int s) { return ld2(rd, (wofs(s) * 64u + r64) * 2u); };
+  // The A operands of block j (K-steps 2 j + h, h = 0, 1) for this lane's row and unit
+  // u = 2 j + hh: w = sc (q - 32) = a_hi + a_lo with a_hi = fh (q - 32), a_lo = fl (q - 32),
+  // fh = 16 (sc >> 4) in [-128, 112], fl = sc & 15, each scaled by 2^-24 and built by one
+  // exact packed fma from q 2^-24 (q as raw f16 bits): fma(q 2^-24, f, -32 f 2^-24).
+  struct Unit {
+    h2_t fh, ch, fl, cl;
+  };
+  auto unit = [&](const v4u& scv, int j) -> Unit {
+    const int sc = (int)(int8_t)((u32)scv[j >> 1] >> (8 * (2 * (j & 1) + hh)));
+    const _Float16 fh = (_Float16)(short)(sc & -16), fl = (_Float16)(short)(sc & 15);
+    constexpr _Float16 kC = (_Float16)-0x1p-19f;  // -32 * 2^-24
+    Unit u;
+    u.fh = h2_t{fh, fh};
+    u.fl = h2_t{fl, fl};
+    u.ch = u.fh * h2_t{kC, kC};
+    u.cl = u.fl * h2_t{kC, kC};
+    return u;
+  };
+  // K-step 2 j + h's operands (a_hi, a_lo)
+  auto build = [&](const W6& w, const Unit& u, int j, int h, v4u& hi, v4u& lo) {
+    const int n = j >> 2, qd = j & 3;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w.ql[i] = ld16(rl, ((gb * 8u + 2u * (u32)i + (u32)hh) * 64u + r64) * 16u);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) w.qh[i] = ld16(rhq, ((gb * 4u + 2u * (u32)i + (u32)hh) * 64u + r64) * 16u);
-    w.sc = ld16(rs, (gb * 64u + r64) * 16u);
-    w.d = ld2(rd, (gb * 64u + r64) * 2u);
+    for (int e = 0; e < 2; ++e) {
+      u32 x = w.ql[2 * n + (qd & 1)][2 * h + e], yq = w.qh[n][2 * h + e];
+      asm volatile("" : "+v"(x), "+v"(yq));  // keeps this operand build here
+      const u32 q = ((qd < 2 ? x : x >> 4) & 0x0F0F0F0Fu) | (((yq >> (2 * qd)) & 0x03030303u) << 4);
+      const h2_t q02 = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0u, q, 0x0C020C00u));  // values 4 e + 0, + 2
+      const h2_t q13 = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0u, q, 0x0C030C01u));  // values 4 e + 1, + 3
+      hi[2 * e] = __builtin_bit_cast(u32, __builtin_elementwise_fma(q02, u.fh, u.ch));
+      hi[2 * e + 1] = __builtin_bit_cast(u32, __builtin_elementwise_fma(q13, u.fh, u.ch));
+      lo[2 * e] = __builtin_bit_cast(u32, __builtin_elementwise_fma(q02, u.fl, u.cl));
+      lo[2 * e + 1] = __builtin_bit_cast(u32, __builtin_elementwise_fma(q13, u.fl, u.cl));
+    }
   };
 
   v16f_t acc[2], S[2], T[2];
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
     acc[mt] = v16f_t{};
-    S[mt] = v16f_t{};
+    T[mt] = v16f_t{};
   }
-  W6 cur, nxt;
+  W6 w;
+  v4u sc_n;
+  u32 d_n;
+  v4u Ah[2], Al[2], Nh[2], Nl[2];  // this block's and the next block's operands (K-steps 2 j, 2 j + 1)
 
+  // Super-block s, per block j in two phases: tile 0's MFMA chain (both K-steps, every
+  // plane, a_hi then a_lo) beside the fold of tile 1's previous block and half the next
+  // block's operand build; then tile 1's chain beside the fold of tile 0's block j and the
+  // other half. Each accumulator is folded while the other tile's MFMAs run, then
+  // restarted from zero.
   auto run_sb = [&](int s) {
     const bool next = s + 1 < nb;
-    ld_w(s + 1, nxt);
+    sc_n = ld_sc(s + 1);
+    d_n = ld_d(s + 1);
     const uint8_t* P = lds + __builtin_amdgcn_readfirstlane((s & 1) * X::kBuf);
+    auto ld_da = [&](int tt, int j) { return as_f(lds4v(P + X::kDa + ((tt * 8 + j) * 32 + li) * 4)); };
+    auto chain = [&](int tt, int j) {
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) T[tt] = v16f_t{};
-    // the A operands (64 wh, wl) of K-step k = 2 j + h for this lane's row
-    auto build = [&](int k, v4u& ah, v4u& al) {
-      const int j = k >> 1, h = k & 1, n = j >> 2, qd = j & 3;
-      // scale of unit 2 j + hh: byte 2 (j & 1) + hh of dword j / 2
-      const int sc = (int)(int8_t)((u32)cur.sc[j >> 1] >> (8 * (2 * (j & 1) + hh)));
+      for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        u32 x = cur.ql[2 * n + (qd & 1)][2 * h + e], yq = cur.qh[n][2 * h + e];
-        asm volatile("" : "+v"(x), "+v"(yq));  // keeps this K-step's operand build here
-        const u32 q = ((qd < 2 ? x : x >> 4) & 0x0F0F0F0Fu) | (((yq >> (2 * qd)) & 0x03030303u) << 4);
-        u32 h0, l0, h1, l1;
-        q6_pair_f16(__builtin_amdgcn_perm(0u, q, 0x0C020C00u), sc, h0, l0);  // values 4 e + 0, + 2
-        q6_pair_f16(__builtin_amdgcn_perm(0u, q, 0x0C030C01u), sc, h1, l1);  // values 4 e + 1, + 3
-        ah[2 * e] = h0;
-        ah[2 * e + 1] = h1;
-        al[2 * e] = l0;
-        al[2 * e + 1] = l1;
+        for (int p = 0; p < kP; ++p) {
+          const v4u b = lds16(P + (((2 * (2 * j + h) + tt) * kP + p) * 64 + lane) * 16);
+          S[tt] = mfma_h(Ah[h], b, h == 0 && p == 0 ? v16f_t{} : S[tt]);
+          S[tt] = mfma_h(Al[h], b, S[tt]);
+        }
       }
     };
-    auto ld_da = [&](int tt, int j) { return as_f(lds4v(P + X::kDa + ((tt * 8 + j) * 32 + li) * 4)); };
-    float da[2];
-    v4u ah, al;
-    build(0, ah, al);
+    // per phase: the LDS reads, then each MFMA followed by a share of the VALU work
+    auto interleave = [&]() {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * kP + 1, 0);  // DS reads
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      __builtin_amdgcn_s_setprio(2);
-      if ((k & 1) == 0) {
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) da[tt] = ld_da(tt, k >> 1);
+      for (int i = 0; i < 4 * kP; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);           // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 28 / (4 * kP), 0);  // VALU
       }
+    };
+    float da1p = 0.0f;
+    Unit un;
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
+    for (int j = 0; j < 8; ++j) {
+      const int jn = (j + 1) & 7;
+      // phase 0
+      const float da0 = ld_da(0, j), da1 = ld_da(1, j);
+      chain(0, j);
+      if (j > 0) {
 #pragma unroll
-        for (int p = 0; p < X::kPlanes; ++p) {
-          const v4u a = lds16(P + (((2 * k + tt) * X::kPlanes + p) * 64 + lane) * 16);
-          S[tt] = mfma_h(ah, a, (k & 1) == 0 && p == 0 ? v16f_t{} : S[tt]);
-          S[tt] = mfma_h(al, a, S[tt]);
-        }
+        for (int r = 0; r < 16; ++r) T[1][r] = fmaf(da1p, S[1][r], T[1][r]);
+        asm volatile("" : "+v"(T[1]));  // the fold happens here, not where T is next read
       }
-      if (k < 15) build(k + 1, ah, al);
+      un = unit(j < 7 ? w.sc : sc_n, jn);
+      build(w, un, jn, 0, Nh[0], Nl[0]);
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
+      // phase 1
+      chain(1, j);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) T[0][r] = fmaf(da0, S[0][r], T[0][r]);
+      asm volatile("" : "+v"(T[0]));
+      build(w, un, jn, 1, Nh[1], Nl[1]);
+      interleave();
+      // chunks whose last read was this build: the next super-block's
+      if (j == 2) {
+        w.ql[0] = ld_ql(s + 1, 0);
+        w.ql[1] = ld_ql(s + 1, 1);
+        w.qh[0] = ld_qh(s + 1, 0);
+      } else if (j == 6) {
+        w.ql[2] = ld_ql(s + 1, 2);
+        w.ql[3] = ld_ql(s + 1, 3);
+        w.qh[1] = ld_qh(s + 1, 1);
+      }
       if (next) {
-        // the next super-block's pieces, spread over the K-steps
-        if (kPieces == 8 ? (k & 1) == 0 : true) issue_piece(s + 1, kPieces == 8 ? (k >> 1) : k);
+        // the next super-block's pieces, one (two) per block
+#pragma unroll
+        for (int i = 0; i < kP; ++i) issue_piece(s + 1, kP * j + i);
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (k & 1) {
-        // block j = k / 2 done: T += da_j S_j over the two tiles
-        __builtin_amdgcn_s_setprio(0);
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) T[tt][r] = fmaf(da[tt], S[tt][r], T[tt][r]);
-          asm volatile("" : "+v"(T[tt]));  // the block's results exist here, not after later MFMAs
-        }
-        __builtin_amdgcn_sched_barrier(0);
+      for (int h = 0; h < 2; ++h) {
+        Ah[h] = Nh[h];
+        Al[h] = Nl[h];
       }
+      da1p = da1;
     }
-    // acc += d T: d of the lane's 16 result rows 8 (r / 4) + 4 hh + r % 4, which lanes 0-31
-    // hold (one weight row each)
-    const float dself = h2f(cur.d);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) T[1][r] = fmaf(da1p, S[1][r], T[1][r]);
+    // acc += d 2^24 T: d of the lane's 16 result rows 8 (r / 4) + 4 hh + r % 4, which lanes
+    // 0-31 hold (one weight row each); T = 0
+    const float d24 = h2f(w.d) * 16777216.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int src = 8 * (r >> 2) + 4 * hh + (r & 3);
-      const float dr = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * src, __builtin_bit_cast(int, dself)));
+      const float dr = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * src, __builtin_bit_cast(int, d24)));
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) acc[tt][r] = fmaf(dr, T[tt][r], acc[tt][r]);
+      for (int tt = 0; tt < 2; ++tt) {
+        acc[tt][r] = fmaf(dr, T[tt][r], acc[tt][r]);
+        T[tt][r] = 0.0f;
+      }
     }
+    w.sc = sc_n;
+    w.d = d_n;
   };
 
-  // prologue: the first super-block's operands and weights
+  // prologue: the first super-block's operands and weights, block 0's A operands
 #pragma unroll
   for (int i = 0; i < kPieces; ++i) issue_piece(0, i);
-  ld_w(0, cur);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w.ql[i] = ld_ql(0, i);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) w.qh[i] = ld_qh(0, i);
+  w.sc = ld_sc(0);
+  w.d = ld_d(0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  {
+    const Unit u0 = unit(w.sc, 0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) build(w, u0, 0, h, Ah[h], Al[h]);
+  }
   lds_barrier();
 #pragma unroll 1
   for (int s = 0; s < nb; ++s) {
     run_sb(s);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
-    cur = nxt;
   }
 
   // ---- outputs (+ bias): activation row 32 mt + li, weight rows nbase + 32 wave +
