@@ -319,7 +319,8 @@ def prefill_sweep(ms: list[int], weights, gen) -> list[dict]:
 def prefill_other_types(gen) -> list[dict]:
     """dq_matmul at M = 512 for the other weight types of a Q4_K_M / Q8_0 / Q4_0 model:
     Q6_K FFN down (K=14336 N=4096) on the Q6_K GEMM, Q8_0 4096 x 4096 and Q4_0
-    K=4096 N=14336 on the 32-value block GEMM (quantization included, 2 rotated copies)."""
+    K=4096 N=14336 on the 32-value block GEMM (quantization included, 2 rotated copies).
+    For Q6_K also dq_matmul_act on per-32 and int16 rows (k_gemm_q6k_x)."""
     import torch
 
     import dynalm_amd as dq
@@ -346,8 +347,19 @@ def prefill_other_types(gen) -> list[dict]:
         log(f"prefill {name} M={m}")
         ms_call = time_graph(lambda i, st: dq.matmul(ws[i % 2], x, m, k, y, n, None, st), 20, 3)
         tops = 2.0 * m * n * k / (ms_call * 1e-3) / 1e12
-        out.append({"weights": f"{name} K={k} N={n}", "m": m, "ms_per_call": round(ms_call, 4), "tops": round(tops, 1),
-                    "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2)})
+        rec = {"weights": f"{name} K={k} N={n}", "m": m, "ms_per_call": round(ms_call, 4), "tops": round(tops, 1),
+               "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2)}
+        if dtype == dq.Q6_K:
+            # the engine plan's contracts for this matrix (qmm int8 rows; the FFN-down plan's
+            # int16 rows): quantize + operand layout + k_gemm_q6k_x on the f16 matrix cores
+            for key, fmt in (("per32", dq.ACT_PER32), ("int16", dq.ACT_Q16)):
+                log(f"prefill {name} M={m} {key}")
+                ms_f = time_graph(lambda i, st, fmt=fmt: dq.matmul_act(ws[i % 2], fmt, x, m, k, y, n, None, st), 20, 3)
+                tf = 2.0 * m * n * k / (ms_f * 1e-3) / 1e12
+                rec[f"{key}_ms_per_call"] = round(ms_f, 4)
+                rec[f"{key}_tops"] = round(tf, 1)
+                rec[f"{key}_pct_peak_f16"] = round(100 * tf / PEAK_F16_TFLOPS, 2)
+        out.append(rec)
         del ws, x, y
     return out
 
