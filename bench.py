@@ -580,7 +580,7 @@ def main() -> None:
     ms_gemv = time_graph(gemv_only, args.steps, args.warmup)
     bytes_step = Q4K_ROW * N + Q8K_ROW + 4 * N
     value = bytes_step / (ms_step * 1e-3) / 1e9
-    # the step is one kernel (k_gemv_slab<16, fused>: Q4_K x Q8_K, M=1): its launch time is ms_step
+    # the step is one kernel (k_gemv_slab<16, 2, true>: Q4_K x Q8_K, M=1): its launch time is ms_step
     achieved = value
 
     # ---- the gated pair at the step's shape: act(x . Wg^T) * (x . Wu^T), one launch
@@ -714,7 +714,7 @@ def main() -> None:
         "ceilings": ceil,
         "tokens_per_s": round(1e3 / ms_step, 1),
         "roofline": {
-            "kernel": "dq::k_gemv_slab<16, true> (Q4_K x Q8_K, M=1, fused quantization, 56-row workgroups)",
+            "kernel": "dq::k_gemv_slab<16, 2, true> (Q4_K x Q8_K, M=1, fused quantization, 56-row workgroups)",
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": PEAK_HBM_GBS,
@@ -724,7 +724,7 @@ def main() -> None:
             "ms_per_launch": round(ms_step, 5),
         },
         "gemv_prequantized": {
-            "kernel": "dq::k_gemv_slab<16, false> (Q4_K x Q8_K, M=1; activations quantized by a separate launch)",
+            "kernel": "dq::k_gemv_slab<16, 2, false> (Q4_K x Q8_K, M=1; activations quantized by a separate launch)",
             "ms_per_launch": round(ms_gemv, 5),
             "gbs": round(bytes_step / (ms_gemv * 1e-3) / 1e9, 2),
         },
@@ -772,7 +772,7 @@ def main() -> None:
                     f"({dq.KERNEL_NAMES[sel_dec.kernel]}, per-32 activations quantized inside the GEMV: one launch)",
         "ms_per_call": round(ms_dec, 5),
         "gbs": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 2),
-        "roofline": {"kernel": "dq::k_gemv_slab<16, per-32, fused> (Q4_K, M=1, 56-row workgroups)", "bound": "hbm",
+        "roofline": {"kernel": "dq::k_gemv_slab<16, 0, true> (Q4_K x per-32, M=1, fused quantization, 56-row workgroups)", "bound": "hbm",
                      "achieved": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(dec_bytes / (ms_dec * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
         "without_qmm": {"kernel": dq.KERNEL_NAMES[sel_x86.kernel], "ms_per_call": round(ms_dec_x86, 5),
