@@ -415,7 +415,7 @@ size_t matmul_scratch_bytes(const dq_weight* w, int fmt, int64_t m) {
     acts += round256((size_t)act16i_bytes(m, w->dev.k));  // the int16 rows, then their act16i layout
   }
   if (w->dev.dtype == DQ_Q6_K && (f == DQ_ACT_PER32 || f == DQ_ACT_Q16) && use_gemm(w->dev, f, m)) {
-    acts += round256((size_t)(f == DQ_ACT_Q16 ? act16i_bytes(m, w->dev.k) : act32_bytes(m, w->dev.k)));
+    acts += round256((size_t)q6x_act_bytes(f, m, w->dev.k)) + (size_t)q6x_part_bytes(w->dev, m, 0, w->dev.n);
   }
   return acts + gemv_split_bytes(w->dev, f, m < 8 ? m : 8);
 }
@@ -510,18 +510,18 @@ int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int6
     return DQ_OK;
   }
   if (w->dev.dtype == DQ_Q6_K && (fmt == DQ_ACT_PER32 || fmt == DQ_ACT_Q16) && use_gemm(w->dev, fmt, m)) {
-    // Q6_K x per-32 / int16 prefill: the rows, their f16 operand layout, the f16 GEMM
-    const bool i16 = fmt == DQ_ACT_Q16;
+    // Q6_K x per-32 / int16 prefill: the rows, their narrow operand layout, the f16 GEMM
+    // (and its range partials)
     const size_t rows_bytes = round256((size_t)(m * arb));
-    const size_t lay = (size_t)(i16 ? act16i_bytes(m, w->dev.k) : act32_bytes(m, w->dev.k));
+    const size_t lay = round256((size_t)q6x_act_bytes(fmt, m, w->dev.k));
+    const size_t pb = (size_t)q6x_part_bytes(w->dev, m, 0, w->dev.n);
     void* buf = nullptr;
-    if (int rc = acts_buffer(w->dev.device, rows_bytes + lay, r, &buf); rc != DQ_OK) return rc;
+    if (int rc = acts_buffer(w->dev.device, rows_bytes + lay + pb, r, &buf); rc != DQ_OK) return rc;
     uint8_t* a2 = static_cast<uint8_t*>(buf) + rows_bytes;
     if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, buf, stream); rc != DQ_OK) return rc;
-    const uint8_t* rows = static_cast<const uint8_t*>(buf);
-    DQ_HIP(i16 ? launch_act16i_from_q16(rows, arb, m, w->dev.k, a2, s) : launch_act32_from_p32(rows, arb, m, w->dev.k, a2, s),
-           "operand conversion launch");
-    DQ_HIP(launch_gemm_q6x(w->dev, fmt, a2, i16 ? act16i_rows(m) : act32_rows(m), m, 0, w->dev.n, y, y_stride, bias, s),
+    DQ_HIP(launch_q6x_act(fmt, static_cast<const uint8_t*>(buf), arb, m, w->dev.k, a2, s), "operand layout launch");
+    DQ_HIP(launch_gemm_q6x(w->dev, fmt, a2, m, 0, w->dev.n, y, y_stride, bias,
+                           pb > 0 ? reinterpret_cast<float*>(a2 + lay) : nullptr, s),
            "gemm launch");
     return DQ_OK;
   }
@@ -881,18 +881,17 @@ int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
     });
   }
   if (w->dev.dtype == DQ_Q6_K && (fmt == DQ_ACT_PER32 || fmt == DQ_ACT_Q16)) {
-    // Q6_K x per-32 / int16: the codes as f16 operands (one conversion launch), then the f16 GEMM
+    // Q6_K x per-32 / int16: the narrow operand layout (one launch), then the f16 GEMM (and
+    // the sum of its range partials)
     if (!dq::gemm_q6x_ok(w->dev, fmt, m, n0, n1)) return fail(DQ_UNSUPPORTED, "m too large");
     const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
-    const bool i16 = fmt == DQ_ACT_Q16;
-    const size_t bytes = (size_t)(i16 ? dq::act16i_bytes(m, w->dev.k) : dq::act32_bytes(m, w->dev.k));
-    return with_stream_ws(w->dev.device, stream, bytes, [&](uint8_t* ws) -> int {
-      const uint8_t* a = static_cast<const uint8_t*>(acts);
-      DQ_HIP(i16 ? dq::launch_act16i_from_q16(a, arb, m, w->dev.k, ws, as_stream(stream))
-                 : dq::launch_act32_from_p32(a, arb, m, w->dev.k, ws, as_stream(stream)),
-             "operand conversion launch");
-      DQ_HIP(dq::launch_gemm_q6x(w->dev, fmt, ws, i16 ? dq::act16i_rows(m) : dq::act32_rows(m), m, n0, n1, y, y_stride,
-                                 bias, as_stream(stream)),
+    const size_t lay = round256((size_t)dq::q6x_act_bytes(fmt, m, w->dev.k));
+    const size_t pb = (size_t)dq::q6x_part_bytes(w->dev, m, n0, n1);
+    return with_stream_ws(w->dev.device, stream, lay + pb, [&](uint8_t* ws) -> int {
+      DQ_HIP(dq::launch_q6x_act(fmt, static_cast<const uint8_t*>(acts), arb, m, w->dev.k, ws, as_stream(stream)),
+             "operand layout launch");
+      DQ_HIP(dq::launch_gemm_q6x(w->dev, fmt, ws, m, n0, n1, y, y_stride, bias,
+                                 pb > 0 ? reinterpret_cast<float*>(ws + lay) : nullptr, as_stream(stream)),
              "gemm launch");
       return DQ_OK;
     });

@@ -14,35 +14,49 @@
 // (the subnormal q 2^-24): fma(q 2^-24, f, -32 f 2^-24), exact because its result is
 // representable. They are the A operand of two v_mfma_f32_32x32x16_f16 per K-step into
 // one accumulator, the activation codes the B operand (per-32: the int8 codes; int16: lo
-// and 256 hi, two more MFMAs): every product is exact, and a block's sum
-// |sum w a| <= 32 * 4096 * 127 < 2^24 (in units of 2^-24) is exact (int16: rounded to fp32
-// where the running sum passes 2^24). Then, as the per-32 GEMM (dq_gemm_p32.hip) does,
+// and 256 hi, each scaled by 2^-24, two more MFMAs): every product is exact, and a
+// block's sum |sum w a| <= 32 * 4096 * 127 < 2^24 (in units of 2^-24) is exact (int16:
+// rounded to fp32 where the running sum passes 2^24 units of 2^-48). Then, as the per-32
+// GEMM (dq_gemm_p32.hip) does,
 //   per block:        T = fma(da_j, S_j, T)
-//   per super-block:  acc = fma(d 2^24, T, acc)
+//   per super-block:  acc = fma(d 2^24 (int16: d 2^48), T, acc)
 // The order is not the reference's: the outputs agree within the fp32 tolerance of a
 // K-term dot product, not bit for bit.
 //
-// Work split. A workgroup owns 64 activation rows x 128 weight rows with 4 waves; wave w
-// owns weight rows 32 w .. 32 w + 31 (lane l builds row l % 32's operands for lane half
-// hh = l / 32 from the Q6_K planes it loads itself) against the two 32-row activation
-// tiles. 256 workgroups at config 3's down shape (M = 512, N = 4096): one wave per SIMD,
-// so a wave overlaps its own work. Per block, tile 0's MFMA chain runs beside the fold of
-// tile 1's previous block and half of the next block's operand build, then tile 1's
-// chain beside the fold of tile 0's block and the other half. A super-block's activation
-// operands (32 KB per-32, 64 KB int16) and scales (2 KB) go to LDS one interval ahead by
-// direct-to-LDS loads spread over the blocks, into a ring of two; each weight plane chunk
-// is reloaded for the next super-block right after its last read. Each CU streams ~3.3 MB
-// (per-32) or ~5.2 MB (int16) at M = 512, N = 4096, K = 14336, so the per-CU read rate
-// (~22 KB/us) bounds the kernel near 150 (235) us.
+// Work split. A workgroup owns 64 activation rows x 128 weight rows with 4 waves, and a
+// range of super-blocks; wave w owns weight rows 32 w .. 32 w + 31 (lane l builds row
+// l % 32's operands for lane half hh = l / 32 from the Q6_K planes it loads itself)
+// against the two 32-row activation tiles. Where the tiles alone leave CUs idle (small m,
+// few weight rows) the super-blocks split into up to 16 ranges, one workgroup each, whose
+// partial outputs a second launch adds in range order (deterministic). 256 workgroups at
+// config 3's down shape (M = 512, N = 4096): one wave per SIMD, so a wave overlaps its own
+// work. Per block, tile 0's MFMA chain runs beside the fold of tile 1's previous block and
+// half of the next block's operand build, then tile 1's chain beside the fold of tile 0's
+// block and the other half. A super-block's activation codes (16 KB per-32, 32 KB int16)
+// and scales (2 KB) go to LDS one interval ahead by direct-to-LDS loads spread over the
+// blocks, into a ring of two; each weight plane chunk is reloaded for the next
+// super-block right after its last read. The codes stay narrow in LDS and become f16 B
+// operands in registers, because each CU's reads (the tile's weights and activation rows)
+// bound the kernel at this shape: ~20 KB/us per CU.
 //
-// Activation layouts: per-32 rows as "act32" (k_act32_from_p32, dq_gemm_p32.hip), int16
-// rows as "act16i" (k_act16i_from_q16, dq_gemm_q16.hip), both with the K order in which
-// K-step k = 2 j + h of lane half hh holds values 32 j + 16 hh + 8 h + {0, 2, 1, 3, 4, 6,
-// 5, 7}; the weight operand is built in that order. Values 32 j + 16 hh + 8 h + t of a
-// super-block are, in its half n = j / 4 and quarter qd = j % 4, ql byte n 64 + 32 (qd & 1)
-// + 16 hh + 8 h + t (the low nibble for qd < 2, else the high one: ql chunk 4 n + 2 (qd & 1)
-// + hh, dwords 2 h, 2 h + 1) with qh bits 2 qd, 2 qd + 1 of qh byte n 32 + 16 hh + 8 h + t
-// (qh chunk 2 n + hh), scale sc of unit 2 j + hh.
+// Activation layouts (written from the quantized rows by k_q6x_act), for M_pad = m rounded
+// up to 64 rows (zero rows past m), T = M_pad / 32 row tiles and nb super-blocks; lane l is
+// row 32 T + l % 32, half hh = l / 32, and K-step k = 2 j + h of a lane half takes values
+// 32 j + 16 hh + 8 h + {0, 2, 1, 3, 4, 6, 5, 7} of the super-block (the weight operand's
+// order: packed 16-bit lanes take bytes (0, 2) and (1, 3) of a dword):
+//   per-32 ("act8")  codes [T][nb][j (8)][lane (64)][16 B]: bytes 8 h + i = code + 128 of
+//                    K-step 2 j + h's value i (f16 in registers: 0x6400 | byte = 1024 + byte,
+//                    minus 1152)
+//   int16 ("act16b") codes [T][nb][j (8)][h (2)][lane (64)][8 x u16]: v + 32768 of value i;
+//                    the B operands are lo = v & 255 as raw f16 bits (the subnormal
+//                    lo 2^-24) and 256 hi 2^-24 = hi 2^-16 through 0x2400 | (hi + 128)
+//                    (= 2^-6 + (hi + 128) 2^-16) minus 2^-6 + 128 2^-16; both exact
+//   da               [T][nb][j (8)][32 rows] floats, after the codes
+// Values 32 j + 16 hh + 8 h + t of a super-block are, in its half n = j / 4 and quarter
+// qd = j % 4, ql byte n 64 + 32 (qd & 1) + 16 hh + 8 h + t (the low nibble for qd < 2,
+// else the high one: ql chunk 4 n + 2 (qd & 1) + hh, dwords 2 h, 2 h + 1) with qh bits
+// 2 qd, 2 qd + 1 of qh byte n 32 + 16 hh + 8 h + t (qh chunk 2 n + hh), scale sc of unit
+// 2 j + hh.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -57,13 +71,14 @@ namespace {
 
 constexpr int kXM = 64, kXN = 128;  // activation rows x weight rows per workgroup
 constexpr int kXThreads = 256;      // 4 waves, one per SIMD
+constexpr int kXMaxSplit = 16;      // super-block ranges per tile at most
 
-// Super-block buffer: activation operands [k (16)][t (2)][p (planes)][lane (64)][16 B],
-// then the activation scales [t (2)][j (8)][row (32)].
+// Super-block buffer: activation codes [j (8)][h (int16: 2)][t (2)][lane (64)][16 B], then
+// the activation scales [t (2)][j (8)][row (32)].
 template <bool kI16>
 struct XLds {
-  static constexpr int kPlanes = kI16 ? 2 : 1;
-  static constexpr int kCodes = 16 * 2 * kPlanes * 1024;
+  static constexpr int kH = kI16 ? 2 : 1;  // 1 KB pieces per block and tile
+  static constexpr int kCodes = 8 * kH * 2 * 1024;
   static constexpr int kDa = kCodes;
   static constexpr int kBuf = kDa + 2048;
   static constexpr int kTotal = 2 * kBuf;
@@ -72,49 +87,110 @@ static_assert(XLds<true>::kTotal <= 160 * 1024, "LDS");
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
+constexpr int kPerm[8] = {0, 2, 1, 3, 4, 6, 5, 7};  // the K-step's value order
+
+int64_t q6x_rows(int64_t m) { return (m + kXM - 1) / kXM * kXM; }
+
 }  // namespace
 
-// One workgroup: activation rows [64 tm, + 64) x weight rows [nbase0 + 128 tn, + 128), all
-// super-blocks. Arguments as launch_gemm_q6x.
+// ---------------------------------------------------------------- layout writer
+
+// Per-32 rows (40 B per 32 values: float d, int32 code sum, int8 codes[32]) -> act8, or
+// ActBlockQ16 rows (72 B: float d, int32 sum, int16 codes[32]) -> act16b. Workgroup
+// (s, T): one 32-row tile's super-block s; rows past m are zeros (codes 0 stored biased).
+template <bool kI16>
+__global__ __launch_bounds__(256) void k_q6x_act(const uint8_t* __restrict__ acts, int64_t arb, int64_t m, int nb,
+                                                 int64_t m_pad, uint8_t* __restrict__ out) {
+  constexpr int kH = kI16 ? 2 : 1, kBlk = kI16 ? 72 : 40;
+  const int t = threadIdx.x;
+  const int s = blockIdx.x;
+  const int64_t T = blockIdx.y;
+  const int64_t codes_bytes = m_pad * nb * 256 * kH;
+#pragma unroll
+  for (int e = 0; e < 2 * kH; ++e) {
+    // unit u = ((j, h), lane) of the (T, s) block: 16 bytes
+    const int u = t + 256 * e, l = u & 63, hh = l >> 5;
+    const int j = kI16 ? (u >> 7) : (u >> 6), h0 = kI16 ? ((u >> 6) & 1) : 0;
+    const int64_t row = 32 * T + (l & 31);
+    u32 o[4];
+    if (row < m) {
+      const uint8_t* b = acts + row * arb + (int64_t)(8 * s + j) * kBlk + 8;
+      if (kI16) {
+        const int16_t* q = reinterpret_cast<const int16_t*>(b) + 16 * hh + 8 * h0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          o[i] = (u32)(uint16_t)(q[kPerm[2 * i]] + 32768) | ((u32)(uint16_t)(q[kPerm[2 * i + 1]] + 32768) << 16);
+        }
+      } else {
+        const int8_t* q = reinterpret_cast<const int8_t*>(b) + 16 * hh;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int h = i >> 1, i0 = 4 * (i & 1);
+          u32 w = 0;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) w |= (u32)(uint8_t)(q[8 * h + kPerm[i0 + c]] + 128) << (8 * c);
+          o[i] = w;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = kI16 ? 0x80008000u : 0x80808080u;
+    }
+    *reinterpret_cast<v4u*>(out + ((((T * nb + s) * 8 + j) * kH + h0) * 64 + l) * 16) = v4u{o[0], o[1], o[2], o[3]};
+  }
+  {
+    // da: thread t = 32 j + r
+    const int j = t >> 5;
+    const int64_t row = 32 * T + (t & 31);
+    const float d = row < m ? *reinterpret_cast<const float*>(acts + row * arb + (int64_t)(8 * s + j) * kBlk) : 0.0f;
+    *reinterpret_cast<float*>(out + codes_bytes + (T * nb + s) * 1024 + t * 4) = d;
+  }
+}
+
+// ---------------------------------------------------------------- the GEMM
+
+// One workgroup: activation rows [64 tm, + 64) x weight rows [nbase0 + 128 tn, + 128),
+// super-blocks of range sp of nsplit. Arguments as launch_gemm_q6x; part: the ranges'
+// partial outputs [nsplit][m][W] (nsplit > 1), W = 128 tiles_n.
 template <bool kI16>
 __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_q6k_x(
     const uint8_t* __restrict__ ql_plane, const uint8_t* __restrict__ qh_plane, const uint8_t* __restrict__ sc_plane,
     const uint8_t* __restrict__ d_plane, int nb, int64_t nbase0, int64_t n_pad, int64_t n0, int64_t n1,
     const uint8_t* __restrict__ act, int64_t m_pad, int64_t m, float* __restrict__ y, int64_t ys,
-    const float* __restrict__ bias, int tiles_m) {
+    const float* __restrict__ bias, int tiles_m, int tiles_n, int nsplit, float* __restrict__ part) {
   using X = XLds<kI16>;
-  constexpr int kP = X::kPlanes;
+  constexpr int kH = X::kH;
   extern __shared__ __align__(16) uint8_t lds[];
   const int t = threadIdx.x, lane = t & 63;
   const int li = lane & 31, hh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int L = blockIdx.x;
-  const int tn = __builtin_amdgcn_readfirstlane(L / tiles_m), tm = __builtin_amdgcn_readfirstlane(L - (L / tiles_m) * tiles_m);
+  const int tiles = tiles_m * tiles_n;
+  const int sp = __builtin_amdgcn_readfirstlane(L / tiles), Lt = L - sp * tiles;
+  const int tn = __builtin_amdgcn_readfirstlane(Lt / tiles_m), tm = __builtin_amdgcn_readfirstlane(Lt - (Lt / tiles_m) * tiles_m);
   const int64_t nbase = nbase0 + (int64_t)kXN * tn;
   const int64_t mbase = (int64_t)tm * kXM;
+  const int sb0 = __builtin_amdgcn_readfirstlane(sp * nb / nsplit), sb1 = __builtin_amdgcn_readfirstlane((sp + 1) * nb / nsplit);
 
-  // activation layout: codes (bytes per 32-row tile and super-block: 16 K-steps x planes x
-  // 1 KB), then da, (then c, unused here)
-  const int64_t codes_bytes = m_pad * nb * 512 * kP, da_bytes = m_pad / 32 * nb * 1024;
+  const int64_t codes_bytes = m_pad * nb * 256 * kH, da_bytes = m_pad / 32 * nb * 1024;
   const auto ra = rsrc(act, (u32)(codes_bytes + da_bytes));
   const auto rl = rsrc(ql_plane, (u32)(n_pad * nb * 128));
   const auto rhq = rsrc(qh_plane, (u32)(n_pad * nb * 64));
   const auto rs = rsrc(sc_plane, (u32)(n_pad * nb * 16));
   const auto rd = rsrc(d_plane, (u32)(n_pad * nb * 2));
 
-  // ---- this wave's loads. Operands of super-block s: blocks jb = 8 P wave + i (i < 8 P)
-  // of the buffer; with piece 0 the activation scales of tile wave (waves 0, 1). The wave's
-  // weight row: group g0 + wave / 2, row 32 (wave & 1) + li.
+  // ---- this wave's loads. Codes of super-block s: pieces jb = 4 kH wave + i (i < 4 kH)
+  // of the buffer, jb = (j kH + h) 2 + tt; with piece 0 the activation scales of tile wave
+  // (waves 0, 1). The wave's weight row: group g0 + wave / 2, row 32 (wave & 1) + li.
   const u32 g0 = (u32)(nbase >> 6);
   const u32 G = g0 + (u32)(wave >> 1), r64 = (u32)(32 * (wave & 1) + li);
-  constexpr int kPieces = 8 * kP;  // 1 KB pieces per wave and super-block
+  constexpr int kPieces = 4 * kH;  // 1 KB pieces per wave and super-block
   auto issue_piece = [&](int s, int i) {
     uint8_t* P = lds + (s & 1) * X::kBuf;
-    const int jb = kPieces * wave + i;  // = (k * 2 + tt) * planes + p
-    const int p = kI16 ? (jb & 1) : 0, kt = kI16 ? (jb >> 1) : jb;
-    const int64_t T = 2 * (int64_t)tm + (kt & 1);
-    const int k = kt >> 1;
-    dma16(ra, P + jb * 1024, (u32)(lane * 16), (u32)((((T * nb + s) * 16 + k) * kP + p) * 1024));
+    const int jb = kPieces * wave + i;
+    const int tt = jb & 1, jh = jb >> 1;  // jh = j kH + h
+    const int64_t T = 2 * (int64_t)tm + tt;
+    dma16(ra, P + jb * 1024, (u32)(lane * 16), (u32)(((T * nb + s) * 8 * kH + jh) * 1024));
     if (i == 0 && wave < 2) {
       const int64_t Tb = 2 * (int64_t)tm + wave;
       dma16(ra, P + X::kDa + wave * 1024, (u32)(lane * 16), (u32)(codes_bytes + (Tb * nb + s) * 1024));
@@ -168,6 +244,19 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
       lo[2 * e + 1] = __builtin_bit_cast(u32, __builtin_elementwise_fma(q13, u.fl, u.cl));
     }
   };
+  // B operands from the narrow codes. per-32: a dword of biased codes (bytes: values
+  // (0, 2), (1, 3) of a pair of K-step slots) -> two f16 pairs 1024 + byte - 1152.
+  auto b8 = [](u32 x, u32 sel) -> u32 {
+    const h2_t v = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, x, sel));
+    return __builtin_bit_cast(u32, v - h2_t{(_Float16)1152.0f, (_Float16)1152.0f});
+  };
+  // int16: a dword of two biased codes -> (lo_a, lo_b) 2^-24 and (hi_a, hi_b) 2^-16
+  auto b16lo = [](u32 x) -> u32 { return __builtin_amdgcn_perm(0u, x, 0x0C020C00u); };
+  auto b16hi = [](u32 x) -> u32 {
+    constexpr _Float16 kOff = (_Float16)(0x1p-6f + 0x1p-9f);  // 2^-6 + 128 2^-16
+    const h2_t v = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x24242424u, x, 0x04030401u));
+    return __builtin_bit_cast(u32, v - h2_t{kOff, kOff});
+  };
 
   v16f_t acc[2], S[2], T[2];
 #pragma unroll
@@ -186,29 +275,32 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   // other half. Each accumulator is folded while the other tile's MFMAs run, then
   // restarted from zero.
   auto run_sb = [&](int s) {
-    const bool next = s + 1 < nb;
+    const bool next = s + 1 < sb1;
     sc_n = ld_sc(s + 1);
     d_n = ld_d(s + 1);
     const uint8_t* P = lds + __builtin_amdgcn_readfirstlane((s & 1) * X::kBuf);
     auto ld_da = [&](int tt, int j) { return as_f(lds4v(P + X::kDa + ((tt * 8 + j) * 32 + li) * 4)); };
     auto chain = [&](int tt, int j) {
+      if (kI16) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < 2; ++h) {
+          const v4u x = lds16(P + ((((j * 2 + h) * 2) + tt) * 64 + lane) * 16);
+          const v4u blo = {b16lo(x[0]), b16lo(x[1]), b16lo(x[2]), b16lo(x[3])};
+          const v4u bhi = {b16hi(x[0]), b16hi(x[1]), b16hi(x[2]), b16hi(x[3])};
+          S[tt] = mfma_h(Ah[h], blo, h == 0 ? v16f_t{} : S[tt]);
+          S[tt] = mfma_h(Al[h], blo, S[tt]);
+          S[tt] = mfma_h(Ah[h], bhi, S[tt]);
+          S[tt] = mfma_h(Al[h], bhi, S[tt]);
+        }
+      } else {
+        const v4u x = lds16(P + ((j * 2 + tt) * 64 + lane) * 16);
 #pragma unroll
-        for (int p = 0; p < kP; ++p) {
-          const v4u b = lds16(P + (((2 * (2 * j + h) + tt) * kP + p) * 64 + lane) * 16);
-          S[tt] = mfma_h(Ah[h], b, h == 0 && p == 0 ? v16f_t{} : S[tt]);
+        for (int h = 0; h < 2; ++h) {
+          const v4u b = {b8(x[2 * h], 0x04010400u), b8(x[2 * h], 0x04030402u), b8(x[2 * h + 1], 0x04010400u),
+                         b8(x[2 * h + 1], 0x04030402u)};
+          S[tt] = mfma_h(Ah[h], b, h == 0 ? v16f_t{} : S[tt]);
           S[tt] = mfma_h(Al[h], b, S[tt]);
         }
-      }
-    };
-    // per phase: the LDS reads, then each MFMA followed by a share of the VALU work
-    auto interleave = [&]() {
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * kP + 1, 0);  // DS reads
-#pragma unroll
-      for (int i = 0; i < 4 * kP; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);           // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 28 / (4 * kP), 0);  // VALU
       }
     };
     float da1p = 0.0f;
@@ -226,7 +318,6 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
       }
       un = unit(j < 7 ? w.sc : sc_n, jn);
       build(w, un, jn, 0, Nh[0], Nl[0]);
-      interleave();
       __builtin_amdgcn_sched_barrier(0);
       // phase 1
       chain(1, j);
@@ -234,7 +325,6 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
       for (int r = 0; r < 16; ++r) T[0][r] = fmaf(da0, S[0][r], T[0][r]);
       asm volatile("" : "+v"(T[0]));
       build(w, un, jn, 1, Nh[1], Nl[1]);
-      interleave();
       // chunks whose last read was this build: the next super-block's
       if (j == 2) {
         w.ql[0] = ld_ql(s + 1, 0);
@@ -246,9 +336,12 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         w.qh[1] = ld_qh(s + 1, 1);
       }
       if (next) {
-        // the next super-block's pieces, one (two) per block
-#pragma unroll
-        for (int i = 0; i < kP; ++i) issue_piece(s + 1, kP * j + i);
+        // the next super-block's pieces: per-32 one per two blocks, int16 one per block
+        if (kI16) {
+          issue_piece(s + 1, j);
+        } else if ((j & 1) == 0) {
+          issue_piece(s + 1, j >> 1);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -260,13 +353,13 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) T[1][r] = fmaf(da1p, S[1][r], T[1][r]);
-    // acc += d 2^24 T: d of the lane's 16 result rows 8 (r / 4) + 4 hh + r % 4, which lanes
-    // 0-31 hold (one weight row each); T = 0
-    const float d24 = h2f(w.d) * 16777216.0f;
+    // acc += d 2^24 T (int16: d 2^48 T): d of the lane's 16 result rows 8 (r / 4) + 4 hh +
+    // r % 4, which lanes 0-31 hold (one weight row each); T = 0
+    const float dsc = h2f(w.d) * (kI16 ? 0x1p48f : 0x1p24f);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int src = 8 * (r >> 2) + 4 * hh + (r & 3);
-      const float dr = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * src, __builtin_bit_cast(int, d24)));
+      const float dr = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * src, __builtin_bit_cast(int, dsc)));
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         acc[tt][r] = fmaf(dr, T[tt][r], acc[tt][r]);
@@ -277,15 +370,15 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     w.d = d_n;
   };
 
-  // prologue: the first super-block's operands and weights, block 0's A operands
+  // prologue: the first super-block's codes and weights, block 0's A operands
 #pragma unroll
-  for (int i = 0; i < kPieces; ++i) issue_piece(0, i);
+  for (int i = 0; i < kPieces; ++i) issue_piece(sb0, i);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) w.ql[i] = ld_ql(0, i);
+  for (int i = 0; i < 4; ++i) w.ql[i] = ld_ql(sb0, i);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) w.qh[i] = ld_qh(0, i);
-  w.sc = ld_sc(0);
-  w.d = ld_d(0);
+  for (int i = 0; i < 2; ++i) w.qh[i] = ld_qh(sb0, i);
+  w.sc = ld_sc(sb0);
+  w.d = ld_d(sb0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   {
     const Unit u0 = unit(w.sc, 0);
@@ -294,15 +387,16 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   }
   lds_barrier();
 #pragma unroll 1
-  for (int s = 0; s < nb; ++s) {
+  for (int s = sb0; s < sb1; ++s) {
     run_sb(s);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
   }
 
-  // ---- outputs (+ bias): activation row 32 mt + li, weight rows nbase + 32 wave +
-  // 8 (r / 4) + 4 hh + r % 4
+  // ---- outputs: activation row 32 mt + li, weight rows nbase + 32 wave + 8 (r / 4) + 4 hh
+  // + r % 4; with one range y (+ bias) in [n0, n1), else the range's partial tile
   const int64_t mrows = m - mbase < kXM ? m - mbase : kXM;
+  const int64_t W = (int64_t)kXN * tiles_n;
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
     const int row = 32 * mt + li;
@@ -311,6 +405,11 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int64_t nq = nbase + 32 * wave + 8 * q + 4 * hh;
+      if (nsplit > 1) {
+        float* pr = part + ((int64_t)sp * m + mbase + row) * W + (nq - nbase0);
+        *reinterpret_cast<float4*>(pr) = float4{acc[mt][4 * q], acc[mt][4 * q + 1], acc[mt][4 * q + 2], acc[mt][4 * q + 3]};
+        continue;
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int64_t n = nq + e;
@@ -323,41 +422,106 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   }
 }
 
+// y[r, n] = sum over the ranges, in range order, of part[range][r][n - nbase0] (+ bias[n]),
+// n in [n0, n1): one thread per output, rows in the grid's y dimension.
+__global__ __launch_bounds__(256) void k_q6x_sum(const float* __restrict__ part, int nsplit, int64_t m, int64_t W,
+                                                 int64_t nbase0, int64_t n0, int64_t n1, float* __restrict__ y,
+                                                 int64_t ys, const float* __restrict__ bias) {
+  const int64_t n = n0 + (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t r = blockIdx.y;
+  if (n >= n1) return;
+  const float* p = part + r * W + (n - nbase0);
+  float v = p[0];
+  for (int i = 1; i < nsplit; ++i) v += p[(int64_t)i * m * W];
+  y[r * ys + n] = bias ? v + bias[n] : v;
+}
+
 // ---------------------------------------------------------------- host
+
+namespace {
+
+struct Q6xGrid {
+  int64_t nbase0, tiles_n, tiles_m;
+  int nsplit;
+};
+
+Q6xGrid q6x_grid(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {
+  Q6xGrid g;
+  g.nbase0 = n0 / kRowGroup * kRowGroup;
+  g.tiles_n = (n1 - g.nbase0 + kXN - 1) / kXN;
+  g.tiles_m = (m + kXM - 1) / kXM;
+  const int64_t tiles = g.tiles_n * g.tiles_m, cus = w.cus > 0 ? w.cus : 256;
+  int64_t sp = tiles >= cus ? 1 : (cus + tiles - 1) / tiles;
+  sp = sp < w.nblk / 2 ? sp : w.nblk / 2;
+  sp = sp < kXMaxSplit ? sp : kXMaxSplit;
+  g.nsplit = (int)(sp > 1 ? sp : 1);
+  return g;
+}
+
+}  // namespace
+
+int64_t q6x_act_bytes(int af, int64_t m, int64_t k) {
+  const int64_t mp = q6x_rows(m), nb = k / 256;
+  return mp * nb * 256 * (af == kActQ16 ? 2 : 1) + mp / 32 * nb * 1024;
+}
+
+int64_t q6x_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {
+  const Q6xGrid g = q6x_grid(w, m, n0, n1);
+  return g.nsplit > 1 ? (int64_t)g.nsplit * m * kXN * g.tiles_n * 4 : 0;
+}
 
 bool gemm_q6x_ok(const WeightDev& w, int af, int64_t m, int64_t n0, int64_t n1) {
   if (w.dtype != kQ6_K || (af != kActPer32 && af != kActQ16) || m <= 0 || n1 <= n0 || w.nblk <= 0) return false;
-  // 32-bit buffer offsets: the ql plane plus one tile's rows past its end, and the layout
+  // 32-bit buffer offsets: the ql plane plus one tile's rows past its end, and the layout;
+  // the layout writer's grid has one row of workgroups per 32 padded rows, the sum's one
+  // per row
   if ((w.n_pad + 2 * kRowGroup) * w.nblk * 128 >= (1ll << 32)) return false;
-  // the layout writers' grids have one row of workgroups per 32 padded rows
-  const bool i16 = af == kActQ16;
-  const int64_t bytes = i16 ? act16i_bytes(m, w.k) : act32_bytes(m, w.k);
-  const int64_t rows = i16 ? act16i_rows(m) : act32_rows(m);
-  if (bytes >= (1ll << 32) || rows / 32 > 65535) return false;
-  // one workgroup per (64 activation rows, 128 weight rows)
-  return (rows / kXM) * ((n1 - n0 / kRowGroup * kRowGroup + kXN - 1) / kXN) < (1ll << 31);
+  if (q6x_act_bytes(af, m, w.k) >= (1ll << 32) || q6x_rows(m) / 32 > 65535) return false;
+  const Q6xGrid g = q6x_grid(w, m, n0, n1);
+  if (g.nsplit > 1 && m > 65535) return false;
+  return g.tiles_m * g.tiles_n * g.nsplit < (1ll << 31);
 }
 
-hipError_t launch_gemm_q6x(const WeightDev& w, int af, const uint8_t* act, int64_t m_pad, int64_t m, int64_t n0,
-                           int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s) {
-  if (!gemm_q6x_ok(w, af, m, n0, n1) || m_pad % kXM != 0 || m_pad < m) return hipErrorInvalidValue;
-  const int64_t nbase0 = n0 / kRowGroup * kRowGroup;
-  const int64_t tiles_n = (n1 - nbase0 + kXN - 1) / kXN;
-  const int64_t tiles_m = (m + kXM - 1) / kXM;
+hipError_t launch_q6x_act(int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t k, uint8_t* out,
+                          hipStream_t s) {
+  const int64_t mp = q6x_rows(m);
+  if (mp / 32 > 65535 || k % 256 != 0 || (af != kActPer32 && af != kActQ16)) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(k / 256), (unsigned)(mp / 32));
+  if (af == kActQ16) {
+    hipLaunchKernelGGL(k_q6x_act<true>, grid, dim3(256), 0, s, acts, arb, m, (int)(k / 256), mp, out);
+  } else {
+    hipLaunchKernelGGL(k_q6x_act<false>, grid, dim3(256), 0, s, acts, arb, m, (int)(k / 256), mp, out);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_q6x(const WeightDev& w, int af, const uint8_t* act, int64_t m, int64_t n0, int64_t n1, float* y,
+                           int64_t ys, const float* bias, float* part, hipStream_t s) {
+  if (!gemm_q6x_ok(w, af, m, n0, n1)) return hipErrorInvalidValue;
+  const Q6xGrid g = q6x_grid(w, m, n0, n1);
+  if (g.nsplit > 1 && part == nullptr) return hipErrorInvalidValue;
+  const int64_t mp = q6x_rows(m);
   const bool i16 = af == kActQ16;
   const void* fn = i16 ? reinterpret_cast<const void*>(&k_gemm_q6k_x<true>)
                        : reinterpret_cast<const void*>(&k_gemm_q6k_x<false>);
   const int lds = i16 ? XLds<true>::kTotal : XLds<false>::kTotal;
   const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e != hipSuccess) return e;
+  const dim3 grid((unsigned)(g.tiles_n * g.tiles_m * g.nsplit));
   if (i16) {
-    hipLaunchKernelGGL(k_gemm_q6k_x<true>, dim3((unsigned)(tiles_n * tiles_m)), dim3(kXThreads), lds, s, w.plane[0],
-                       w.plane[1], w.plane[2], w.plane[3], (int)w.nblk, nbase0, w.n_pad, n0, n1, act, m_pad, m, y, ys,
-                       bias, (int)tiles_m);
+    hipLaunchKernelGGL(k_gemm_q6k_x<true>, grid, dim3(kXThreads), lds, s, w.plane[0], w.plane[1], w.plane[2],
+                       w.plane[3], (int)w.nblk, g.nbase0, w.n_pad, n0, n1, act, mp, m, y, ys, bias, (int)g.tiles_m,
+                       (int)g.tiles_n, g.nsplit, part);
   } else {
-    hipLaunchKernelGGL(k_gemm_q6k_x<false>, dim3((unsigned)(tiles_n * tiles_m)), dim3(kXThreads), lds, s, w.plane[0],
-                       w.plane[1], w.plane[2], w.plane[3], (int)w.nblk, nbase0, w.n_pad, n0, n1, act, m_pad, m, y, ys,
-                       bias, (int)tiles_m);
+    hipLaunchKernelGGL(k_gemm_q6k_x<false>, grid, dim3(kXThreads), lds, s, w.plane[0], w.plane[1], w.plane[2],
+                       w.plane[3], (int)w.nblk, g.nbase0, w.n_pad, n0, n1, act, mp, m, y, ys, bias, (int)g.tiles_m,
+                       (int)g.tiles_n, g.nsplit, part);
+  }
+  if (g.nsplit > 1) {
+    const hipError_t e2 = hipGetLastError();
+    if (e2 != hipSuccess) return e2;
+    hipLaunchKernelGGL(k_q6x_sum, dim3((unsigned)((n1 - n0 + 255) / 256), (unsigned)m), dim3(256), 0, s, part,
+                       g.nsplit, m, (int64_t)kXN * g.tiles_n, g.nbase0, n0, n1, y, ys, bias);
   }
   return hipGetLastError();
 }

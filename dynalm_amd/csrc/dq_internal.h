@@ -119,14 +119,18 @@ hipError_t launch_act16i_from_q16(const uint8_t* acts, int64_t arb, int64_t m, i
 hipError_t launch_gemm_q16(const WeightDev& w, const uint8_t* act, int64_t m, int64_t n0, int64_t n1, float* y,
                            int64_t ys, const float* bias, hipStream_t s);
 // The Q6_K GEMM on the f16 matrix cores (dq_gemm_q6x.hip) for per-32 rows (af =
-// kActPer32, the act32 layout) and int16 rows (kActQ16, the act16i layout): 64 x 128 tiles,
-// w = sc (q - 32) split exactly into f16 operands 64 wh and wl. m_pad: the rows of the layout
-// (act32_rows / act16i_rows of m). gemm_q6x_ok: Q6_K, one of those formats, 32-bit offsets.
-int64_t act32_rows(int64_t m);
-int64_t act16i_rows(int64_t m);
+// kActPer32) and int16 rows (kActQ16): launch_q6x_act writes the rows' narrow operand
+// layout (q6x_act_bytes), launch_gemm_q6x runs 64 x 128 tiles over it. Where the tiles
+// leave CUs idle, each tile's super-blocks split into ranges whose partial outputs go to
+// part (q6x_part_bytes; 0: no split, part may be null) and a second launch adds them in
+// range order. gemm_q6x_ok: Q6_K, one of those formats, 32-bit offsets.
+int64_t q6x_act_bytes(int af, int64_t m, int64_t k);
+int64_t q6x_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
 bool gemm_q6x_ok(const WeightDev& w, int af, int64_t m, int64_t n0, int64_t n1);
-hipError_t launch_gemm_q6x(const WeightDev& w, int af, const uint8_t* act, int64_t m_pad, int64_t m, int64_t n0,
-                           int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s);
+hipError_t launch_q6x_act(int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t k, uint8_t* out,
+                          hipStream_t s);
+hipError_t launch_gemm_q6x(const WeightDev& w, int af, const uint8_t* act, int64_t m, int64_t n0, int64_t n1, float* y,
+                           int64_t ys, const float* bias, float* part, hipStream_t s);
 // The expand-class fp32 GEMM (dq_gemm_f32.hip): weight tiles expanded to fp32 in LDS
 // and contracted with the fp32 rows x (stride xs floats) on the matrix cores; any of
 // the four weight types. Below kF32GemmMinRows rows the fp32 GEMV passes are faster.

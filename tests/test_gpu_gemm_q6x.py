@@ -3,17 +3,19 @@ contracts: per-32 rows (the int8 contract, qmm_reference.cpp:68-93 with Fmt<kQ6_
 int16 rows (ActBlockQ16, kernels_avx2.cpp:1661-1765), through dq_gemm on the block rows,
 dq_matmul_act on fp32 rows (which takes it from 16 rows) and dq_qmm_gemm.
 
-The weight w = sc (q - 32) is split exactly into two f16 operands (64 wh and wl), so the
-per-block integers are exact (per-32; int16: rounded to fp32 where a running sum passes
-2^24) and the fp32 terms are summed in an order of the kernel's own. It is held to the
+The weight w = sc (q - 32) is split exactly into two f16 operands (fh (q - 32) and
+fl (q - 32), sc = fh + fl), so the per-block integers are exact (per-32; int16: rounded to
+fp32 where a running sum passes 2^24) and the fp32 terms are summed in an order of the
+kernel's own. It is held to the
 reference's bound against the exact product, |y - y_exact| <= 1e-5 * sum |w_i x_i|
 (dynacore/tests/test_int_kernels.cpp:131-147), and against the oracle's order to the
 north-star tolerance (per-32: 1e-4 relative, 1e-5 absolute) or to the int16 GEMV's bar
 (int16: 2e-6 * sum |w_i x_i|; its terms reach 2^36 and cancel, so a bar relative to
 the output does not fit).
 
-Cases: 1, 5 and 16 super-blocks, partial 64-row activation tiles, a 128-row weight tile
-past the last row group (n = 1088), a row range cutting the first and last tiles, bias,
+Cases: 1, 5, 16 and 32 super-blocks, partial 64-row activation tiles, super-block ranges
+(split K, 2 to 16 ranges) and none, a 128-row weight tile past the last row group
+(n = 1088), a row range cutting the first and last tiles, bias,
 the extreme weights w = 4096 (sc = -128, q = 0) and w = -3968 with codes of +-127
 (+-32767), the reference's edge blocks, and both writers' routes, which must agree bit
 for bit.
@@ -113,9 +115,11 @@ def _check(fmt: int, m: int, k: int, n: int, n0: int, n1: int, seed: int, extrem
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("m,k", [(5, 256), (16, 256), (67, 1280), (130, 4096)])
+@pytest.mark.parametrize("m,k", [(5, 256), (16, 256), (67, 1280), (130, 4096), (20, 8192)])
 def test_q6x_gemm_superblock_counts(cuda, fmt, m, k):
-    """1, 5 and 16 super-blocks; every m ends on a partial 64-row activation tile."""
+    """1, 5, 16 and 32 super-blocks; every m ends on a partial 64-row activation tile. With
+    8 weight tiles the super-blocks split into ranges (2 at K=1280, 8 at K=4096, 16 at
+    K=8192) whose partials a second launch adds."""
     _check(fmt, m, k, 1024, 0, 1024, 9600 + m + 7 * fmt)
 
 
