@@ -122,9 +122,10 @@ constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 // at K = 4096, N = 14336 (graph replay; GEMM vs passes): 16 rows 76 vs 59 us, 32 rows
 // 77 vs 117, 64 rows 81 vs 229, 128 rows 83 vs 448; 512 rows 176 us on the GEMM.
 constexpr int64_t kQ16GemmMinRows = 20;
-// Rows from which Q6_K x per-32 / int16 runs the f16 GEMM (dq_gemm_q6x.hip) instead of
-// the GEMV passes.
-constexpr int64_t kQ6xGemmMinRows = 16;
+// Rows from which Q6_K x per-32 / int16 runs the f16 GEMM (dq_gemm_q6x.hip, split K where
+// its tiles leave CUs idle) instead of the GEMV passes (measured, K = 4096 / 14336: level
+// at 4 rows, 1.5x faster at 6).
+constexpr int64_t kQ6xGemmMinRows = 5;
 
 // Per-(device, stream) workspaces of the public entry points whose kernels need device
 // memory beyond their arguments (dq_gemm's f16 activation operands). Each stream has

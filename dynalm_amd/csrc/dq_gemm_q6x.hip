@@ -185,8 +185,8 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const u32 g0 = (u32)(nbase >> 6);
   const u32 G = g0 + (u32)(wave >> 1), r64 = (u32)(32 * (wave & 1) + li);
   constexpr int kPieces = 4 * kH;  // 1 KB pieces per wave and super-block
-  auto issue_piece = [&](int s, int i) {
-    uint8_t* P = lds + (s & 1) * X::kBuf;
+  auto issue_piece = [&](int s, int buf, int i) {
+    uint8_t* P = lds + buf * X::kBuf;
     const int jb = kPieces * wave + i;
     const int tt = jb & 1, jh = jb >> 1;  // jh = j kH + h
     const int64_t T = 2 * (int64_t)tm + tt;
@@ -267,65 +267,116 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   W6 w;
   v4u sc_n;
   u32 d_n;
-  v4u Ah[2], Al[2], Nh[2], Nl[2];  // this block's and the next block's operands (K-steps 2 j, 2 j + 1)
+  v4u Ah[2][2], Al[2][2];  // [block parity][K-step h]: block j's operands, then block j + 1's
 
-  // Super-block s, per block j in two phases: tile 0's MFMA chain (both K-steps, every
-  // plane, a_hi then a_lo) beside the fold of tile 1's previous block and half the next
-  // block's operand build; then tile 1's chain beside the fold of tile 0's block j and the
-  // other half. Each accumulator is folded while the other tile's MFMAs run, then
-  // restarted from zero.
+  // Super-block s, per block j in two phases, each in a fixed issue order: tile tt's MFMA
+  // chain (K-steps 2 j, 2 j + 1; a_hi, a_lo) with a share of independent VALU work between
+  // consecutive MFMAs (B conversions, the other tile's fold, the next block's operand
+  // build), so that each MFMA's predecessor has finished when it issues and the matrix core
+  // runs beside the VALU. Phase 0: tile 0 beside the fold of tile 1's previous block and
+  // the next block's K-step 0 operands; phase 1: tile 1 beside the fold of tile 0's block j
+  // and the next block's K-step 1 operands.
+#define SB() __builtin_amdgcn_sched_barrier(0)
   auto run_sb = [&](int s) {
     const bool next = s + 1 < sb1;
     sc_n = ld_sc(s + 1);
     d_n = ld_d(s + 1);
     const uint8_t* P = lds + __builtin_amdgcn_readfirstlane((s & 1) * X::kBuf);
     auto ld_da = [&](int tt, int j) { return as_f(lds4v(P + X::kDa + ((tt * 8 + j) * 32 + li) * 4)); };
-    auto chain = [&](int tt, int j) {
-      if (kI16) {
+    // the codes of block j, tile tt (int16: K-step h); int16 reads both K-steps
+    auto ld_x = [&](int j, int tt, int h) { return lds16(P + ((((j * kH + h) * 2) + tt) * 64 + lane) * 16); };
+    auto fold = [&](int tt, float da, int r0) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const v4u x = lds16(P + ((((j * 2 + h) * 2) + tt) * 64 + lane) * 16);
-          const v4u blo = {b16lo(x[0]), b16lo(x[1]), b16lo(x[2]), b16lo(x[3])};
-          const v4u bhi = {b16hi(x[0]), b16hi(x[1]), b16hi(x[2]), b16hi(x[3])};
-          S[tt] = mfma_h(Ah[h], blo, h == 0 ? v16f_t{} : S[tt]);
-          S[tt] = mfma_h(Al[h], blo, S[tt]);
-          S[tt] = mfma_h(Ah[h], bhi, S[tt]);
-          S[tt] = mfma_h(Al[h], bhi, S[tt]);
-        }
-      } else {
-        const v4u x = lds16(P + ((j * 2 + tt) * 64 + lane) * 16);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const v4u b = {b8(x[2 * h], 0x04010400u), b8(x[2 * h], 0x04030402u), b8(x[2 * h + 1], 0x04010400u),
-                         b8(x[2 * h + 1], 0x04030402u)};
-          S[tt] = mfma_h(Ah[h], b, h == 0 ? v16f_t{} : S[tt]);
-          S[tt] = mfma_h(Al[h], b, S[tt]);
-        }
-      }
+      for (int r = r0; r < r0 + 8; ++r) T[tt][r] = fmaf(da, S[tt][r], T[tt][r]);
     };
     float da1p = 0.0f;
-    Unit un;
+    v4u xa = ld_x(0, 0, 0), xb = kI16 ? ld_x(0, 0, 1) : xa;  // this phase's codes
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int jn = (j + 1) & 7;
-      // phase 0
-      const float da0 = ld_da(0, j), da1 = ld_da(1, j);
-      chain(0, j);
-      if (j > 0) {
+      const int jn = (j + 1) & 7, c = j & 1, cn = c ^ 1;
+      const Unit un = unit(j < 7 ? w.sc : sc_n, jn);
+      float da[2];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) T[1][r] = fmaf(da1p, S[1][r], T[1][r]);
-        asm volatile("" : "+v"(T[1]));  // the fold happens here, not where T is next read
+      for (int tt = 0; tt < 2; ++tt) {
+        if (tt == 0) {
+          da[0] = ld_da(0, j);
+          da[1] = ld_da(1, j);
+        }
+        // prefetch the next phase's codes: tile 1 of block j, or tile 0 of block j + 1
+        v4u ya, yb;
+        if (tt == 0) {
+          ya = ld_x(j, 1, 0);
+          yb = kI16 ? ld_x(j, 1, 1) : ya;
+        } else if (j < 7) {
+          ya = ld_x(j + 1, 0, 0);
+          yb = kI16 ? ld_x(j + 1, 0, 1) : ya;
+        }
+        const int ot = tt ^ 1;  // the tile folded in this phase
+        const bool do_fold = tt == 1 || j > 0;
+        const float fda = tt == 0 ? da1p : da[0];
+        if (kI16) {
+          // 8 MFMAs: (h, plane) = (0, lo) (0, hi) (1, lo) (1, hi), a_hi then a_lo each
+          v4u bl0 = {b16lo(xa[0]), b16lo(xa[1]), b16lo(xa[2]), b16lo(xa[3])};
+          SB();
+          S[tt] = mfma_h(Ah[c][0], bl0, v16f_t{});
+          SB();
+          v4u bh0 = {b16hi(xa[0]), b16hi(xa[1]), b16hi(xa[2]), b16hi(xa[3])};
+          SB();
+          S[tt] = mfma_h(Al[c][0], bl0, S[tt]);
+          SB();
+          v4u bl1 = {b16lo(xb[0]), b16lo(xb[1]), b16lo(xb[2]), b16lo(xb[3])};
+          if (do_fold) fold(ot, fda, 0);
+          SB();
+          S[tt] = mfma_h(Ah[c][0], bh0, S[tt]);
+          SB();
+          v4u bh1 = {b16hi(xb[0]), b16hi(xb[1]), b16hi(xb[2]), b16hi(xb[3])};
+          SB();
+          S[tt] = mfma_h(Al[c][0], bh0, S[tt]);
+          SB();
+          if (do_fold) {
+            fold(ot, fda, 8);
+            asm volatile("" : "+v"(T[ot]));  // the fold happens here, not where T is next read
+          }
+          SB();
+          S[tt] = mfma_h(Ah[c][1], bl1, S[tt]);
+          SB();
+          build(w, un, jn, tt, Ah[cn][tt], Al[cn][tt]);
+          SB();
+          S[tt] = mfma_h(Al[c][1], bl1, S[tt]);
+          SB();
+          S[tt] = mfma_h(Ah[c][1], bh1, S[tt]);
+          SB();
+          S[tt] = mfma_h(Al[c][1], bh1, S[tt]);
+          SB();
+        } else {
+          v4u b0 = {b8(xa[0], 0x04010400u), b8(xa[0], 0x04030402u), b8(xa[1], 0x04010400u), b8(xa[1], 0x04030402u)};
+          SB();
+          S[tt] = mfma_h(Ah[c][0], b0, v16f_t{});
+          SB();
+          v4u b1 = {b8(xa[2], 0x04010400u), b8(xa[2], 0x04030402u), b8(xa[3], 0x04010400u), b8(xa[3], 0x04030402u)};
+          SB();
+          S[tt] = mfma_h(Al[c][0], b0, S[tt]);
+          SB();
+          if (do_fold) fold(ot, fda, 0);
+          SB();
+          S[tt] = mfma_h(Ah[c][1], b1, S[tt]);
+          SB();
+          if (do_fold) {
+            fold(ot, fda, 8);
+            asm volatile("" : "+v"(T[ot]));
+          }
+          SB();
+          S[tt] = mfma_h(Al[c][1], b1, S[tt]);
+          SB();
+          build(w, un, jn, tt, Ah[cn][tt], Al[cn][tt]);
+          SB();
+        }
+        if (tt == 0 || j < 7) {
+          xa = ya;
+          xb = yb;
+        }
       }
-      un = unit(j < 7 ? w.sc : sc_n, jn);
-      build(w, un, jn, 0, Nh[0], Nl[0]);
-      __builtin_amdgcn_sched_barrier(0);
-      // phase 1
-      chain(1, j);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) T[0][r] = fmaf(da0, S[0][r], T[0][r]);
-      asm volatile("" : "+v"(T[0]));
-      build(w, un, jn, 1, Nh[1], Nl[1]);
-      // chunks whose last read was this build: the next super-block's
+      // chunks whose last read was this block's build: the next super-block's
       if (j == 2) {
         w.ql[0] = ld_ql(s + 1, 0);
         w.ql[1] = ld_ql(s + 1, 1);
@@ -335,21 +386,18 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         w.ql[3] = ld_ql(s + 1, 3);
         w.qh[1] = ld_qh(s + 1, 1);
       }
-      if (next) {
-        // the next super-block's pieces: per-32 one per two blocks, int16 one per block
+      // the next super-block's pieces into the other buffer (past the range: this one's
+      // again, unread): per-32 one per two blocks, int16 one per block
+      {
+        const int sn = next ? s + 1 : s;
         if (kI16) {
-          issue_piece(s + 1, j);
+          issue_piece(sn, (s + 1) & 1, j);
         } else if ((j & 1) == 0) {
-          issue_piece(s + 1, j >> 1);
+          issue_piece(sn, (s + 1) & 1, j >> 1);
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        Ah[h] = Nh[h];
-        Al[h] = Nl[h];
-      }
-      da1p = da1;
+      SB();
+      da1p = da[1];
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) T[1][r] = fmaf(da1p, S[1][r], T[1][r]);
@@ -369,10 +417,11 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     w.sc = sc_n;
     w.d = d_n;
   };
+#undef SB
 
   // prologue: the first super-block's codes and weights, block 0's A operands
 #pragma unroll
-  for (int i = 0; i < kPieces; ++i) issue_piece(sb0, i);
+  for (int i = 0; i < kPieces; ++i) issue_piece(sb0, sb0 & 1, i);
 #pragma unroll
   for (int i = 0; i < 4; ++i) w.ql[i] = ld_ql(sb0, i);
 #pragma unroll
@@ -383,7 +432,7 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   {
     const Unit u0 = unit(w.sc, 0);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) build(w, u0, 0, h, Ah[h], Al[h]);
+    for (int h = 0; h < 2; ++h) build(w, u0, 0, h, Ah[0][h], Al[0][h]);
   }
   lds_barrier();
 #pragma unroll 1
