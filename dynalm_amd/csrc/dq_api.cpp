@@ -117,11 +117,17 @@ int scratch_get(int device, size_t need, void** out) { return scratch_get(g_scra
 
 constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
-// Rows from which Q4_K x int16 runs the f16 GEMM (dq_gemm_q16.hip) instead of the
-// int16 GEMV's passes of up to 4 rows, each of which reads the weight once. Measured
-// at K = 4096, N = 14336 (graph replay; GEMM vs passes): 16 rows 76 vs 59 us, 32 rows
-// 77 vs 117, 64 rows 81 vs 229, 128 rows 83 vs 448; 512 rows 176 us on the GEMM.
-constexpr int64_t kQ16GemmMinRows = 20;
+// Rows from which Q4_K x int16 runs the f16 GEMM (dq_gemm_q16.hip, split K where its
+// tiles leave CUs idle) instead of the int16 GEMV's passes of up to 4 rows, each of which
+// reads the weight once. Measured (graph replay, dq_gemm vs dq_gemv on the same rows),
+// K = 4096, N = 14336: 6 rows 30.0 vs 30.2 us, 16 rows 30.9 vs 57.2, 64 rows 36.6 vs
+// 223; N = 4096 (K = 4096 / 14336): 6 rows 19.7 / 35.1 vs 25.5 / 40.3.
+constexpr int64_t kQ16GemmMinRows = 6;
+// Rows from which Q4_K x per-32 runs the f16 GEMM (dq_gemm_p32.hip, split K) instead of
+// the per-32 GEMV's passes (fused quantization up to 8 rows): K = 4096, N = 14336: 12
+// rows 35.6 vs 30.8 us, 16 rows 35.4 vs 36.5, 64 rows 39.6 vs 136; N = 4096 (K = 4096
+// / 14336): 12 rows 21.9 / 39.9 vs 27.1 / 54.7.
+constexpr int64_t kP32GemmMinRows = 12;
 // Rows from which Q6_K x per-32 / int16 runs the f16 GEMM (dq_gemm_q6x.hip, split K where
 // its tiles leave CUs idle) instead of the GEMV passes (measured, K = 4096 / 14336: level
 // at 4 rows, 1.5x faster at 6).
@@ -301,7 +307,7 @@ bool use_gemm(const dq::WeightDev& w, int fmt, int64_t m) {
   if (w.dtype == DQ_Q6_K && (fmt == DQ_ACT_PER32 || fmt == DQ_ACT_Q16)) {
     return m >= kQ6xGemmMinRows && dq::gemm_q6x_ok(w, fmt, m, 0, w.n);
   }
-  if (fmt == DQ_ACT_PER32) return m > 64 && dq::gemm_p32_ok(w, m, 0, w.n);
+  if (fmt == DQ_ACT_PER32) return m >= kP32GemmMinRows && dq::gemm_p32_ok(w, m, 0, w.n);
   // Q4_K x int16: the 64-row f16 GEMM against GEMV passes of 4 rows
   if (fmt == DQ_ACT_Q16) return m >= kQ16GemmMinRows && dq::gemm_q16_ok(w, m, 0, w.n);
   if (w.dtype == DQ_Q6_K) {
@@ -410,10 +416,12 @@ size_t matmul_scratch_bytes(const dq_weight* w, int fmt, int64_t m) {
   size_t acts = round256((size_t)(m * dq_act_row_bytes(f, w->dev.k)));
   if (f == DQ_ACT_Q8_K && gemm_h16_pays(w->dev, m, 0, w->dev.n)) acts = round256((size_t)act16_bytes(m, w->dev.k));
   if (f == DQ_ACT_PER32 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, f, m)) {
-    acts += round256((size_t)act32_bytes(m, w->dev.k));  // the per-32 rows, then their act32 layout
+    // the per-32 rows, then their act32 layout and the range partials
+    acts += round256((size_t)act32_bytes(m, w->dev.k)) + (size_t)p32_part_bytes(w->dev, m, 0, w->dev.n);
   }
   if (f == DQ_ACT_Q16 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, f, m)) {
-    acts += round256((size_t)act16i_bytes(m, w->dev.k));  // the int16 rows, then their act16i layout
+    // the int16 rows, then their act16i layout and the range partials
+    acts += round256((size_t)act16i_bytes(m, w->dev.k)) + (size_t)q16_part_bytes(w->dev, m, 0, w->dev.n);
   }
   if (w->dev.dtype == DQ_Q6_K && (f == DQ_ACT_PER32 || f == DQ_ACT_Q16) && use_gemm(w->dev, f, m)) {
     acts += round256((size_t)q6x_act_bytes(f, m, w->dev.k)) + (size_t)q6x_part_bytes(w->dev, m, 0, w->dev.n);
@@ -490,14 +498,15 @@ int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int6
     // Q4_K x per-32 prefill: per-32 rows, their f16 operand layout, the f16 GEMM (all
     // in the region when one is given)
     const size_t rows_bytes = round256((size_t)(m * arb));
+    const size_t lay = round256((size_t)act32_bytes(m, w->dev.k)), pb = (size_t)p32_part_bytes(w->dev, m, 0, w->dev.n);
     void* buf = nullptr;
-    if (int rc = acts_buffer(w->dev.device, rows_bytes + (size_t)act32_bytes(m, w->dev.k), r, &buf); rc != DQ_OK) {
-      return rc;
-    }
+    if (int rc = acts_buffer(w->dev.device, rows_bytes + lay + pb, r, &buf); rc != DQ_OK) return rc;
     uint8_t* a32 = static_cast<uint8_t*>(buf) + rows_bytes;
     if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, buf, stream); rc != DQ_OK) return rc;
     DQ_HIP(launch_act32_from_p32(static_cast<const uint8_t*>(buf), arb, m, w->dev.k, a32, s), "act32 conversion launch");
-    DQ_HIP(launch_gemm_p32(w->dev, a32, m, 0, w->dev.n, y, y_stride, bias, s), "gemm launch");
+    DQ_HIP(launch_gemm_p32(w->dev, a32, m, 0, w->dev.n, y, y_stride, bias,
+                           pb > 0 ? reinterpret_cast<float*>(a32 + lay) : nullptr, s),
+           "gemm launch");
     return DQ_OK;
   }
   if (fmt == DQ_ACT_PER32 && (w->dev.dtype == DQ_Q4_K || w->dev.dtype == DQ_Q6_K) && m <= 8 &&
@@ -529,15 +538,16 @@ int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int6
   if (fmt == DQ_ACT_Q16 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, fmt, m)) {
     // Q4_K x int16 prefill: int16 rows, their lo / 256 hi f16 layout, the f16 GEMM
     const size_t rows_bytes = round256((size_t)(m * arb));
+    const size_t lay = round256((size_t)act16i_bytes(m, w->dev.k)), pb = (size_t)q16_part_bytes(w->dev, m, 0, w->dev.n);
     void* buf = nullptr;
-    if (int rc = acts_buffer(w->dev.device, rows_bytes + (size_t)act16i_bytes(m, w->dev.k), r, &buf); rc != DQ_OK) {
-      return rc;
-    }
+    if (int rc = acts_buffer(w->dev.device, rows_bytes + lay + pb, r, &buf); rc != DQ_OK) return rc;
     uint8_t* a16 = static_cast<uint8_t*>(buf) + rows_bytes;
     if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, buf, stream); rc != DQ_OK) return rc;
     DQ_HIP(launch_act16i_from_q16(static_cast<const uint8_t*>(buf), arb, m, w->dev.k, a16, s),
            "act16i conversion launch");
-    DQ_HIP(launch_gemm_q16(w->dev, a16, m, 0, w->dev.n, y, y_stride, bias, s), "gemm launch");
+    DQ_HIP(launch_gemm_q16(w->dev, a16, m, 0, w->dev.n, y, y_stride, bias,
+                           pb > 0 ? reinterpret_cast<float*>(a16 + lay) : nullptr, s),
+           "gemm launch");
     return DQ_OK;
   }
   void* acts = nullptr;
@@ -874,10 +884,13 @@ int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
     // Q4_K x per-32: the codes as f16 operands (one conversion launch), then the f16 GEMM
     if (!dq::gemm_p32_ok(w->dev, m, n0, n1)) return fail(DQ_UNSUPPORTED, "m too large");
     const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
-    return with_stream_ws(w->dev.device, stream, (size_t)dq::act32_bytes(m, w->dev.k), [&](uint8_t* ws) -> int {
+    const size_t lay = round256((size_t)dq::act32_bytes(m, w->dev.k)), pb = (size_t)dq::p32_part_bytes(w->dev, m, n0, n1);
+    return with_stream_ws(w->dev.device, stream, lay + pb, [&](uint8_t* ws) -> int {
       DQ_HIP(dq::launch_act32_from_p32(static_cast<const uint8_t*>(acts), arb, m, w->dev.k, ws, as_stream(stream)),
              "act32 conversion launch");
-      DQ_HIP(dq::launch_gemm_p32(w->dev, ws, m, n0, n1, y, y_stride, bias, as_stream(stream)), "gemm launch");
+      DQ_HIP(dq::launch_gemm_p32(w->dev, ws, m, n0, n1, y, y_stride, bias,
+                                 pb > 0 ? reinterpret_cast<float*>(ws + lay) : nullptr, as_stream(stream)),
+             "gemm launch");
       return DQ_OK;
     });
   }
@@ -901,10 +914,13 @@ int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
     // Q4_K x int16: lo / 256 hi as f16 operands (one conversion launch), then the f16 GEMM
     if (!dq::gemm_q16_ok(w->dev, m, n0, n1)) return fail(DQ_UNSUPPORTED, "m too large");
     const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
-    return with_stream_ws(w->dev.device, stream, (size_t)dq::act16i_bytes(m, w->dev.k), [&](uint8_t* ws) -> int {
+    const size_t lay = round256((size_t)dq::act16i_bytes(m, w->dev.k)), pb = (size_t)dq::q16_part_bytes(w->dev, m, n0, n1);
+    return with_stream_ws(w->dev.device, stream, lay + pb, [&](uint8_t* ws) -> int {
       DQ_HIP(dq::launch_act16i_from_q16(static_cast<const uint8_t*>(acts), arb, m, w->dev.k, ws, as_stream(stream)),
              "act16i conversion launch");
-      DQ_HIP(dq::launch_gemm_q16(w->dev, ws, m, n0, n1, y, y_stride, bias, as_stream(stream)), "gemm launch");
+      DQ_HIP(dq::launch_gemm_q16(w->dev, ws, m, n0, n1, y, y_stride, bias,
+                                 pb > 0 ? reinterpret_cast<float*>(ws + lay) : nullptr, as_stream(stream)),
+             "gemm launch");
       return DQ_OK;
     });
   }

@@ -125,7 +125,8 @@ __global__ __launch_bounds__(256) void k_act16i_from_q16(const uint8_t* __restri
 __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_q4k_q16(
     const uint8_t* __restrict__ qs_plane, const uint8_t* __restrict__ hdr_plane, int nb, int64_t nbase0, int64_t n_pad,
     int64_t n0, int64_t n1, const uint8_t* __restrict__ act, int64_t m_pad, int64_t m, float* __restrict__ y,
-    int64_t ys, const float* __restrict__ bias, int tiles_m, int xcd_map) {
+    int64_t ys, const float* __restrict__ bias, int tiles_m, int xcd_map, int tiles_n, int nsplit,
+    float* __restrict__ part) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int t = threadIdx.x, lane = t & 63;
   const int li = lane & 31, hh = lane >> 5;
@@ -133,7 +134,11 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
   // Workgroups with the same weight rows on one XCD (workgroups are dealt to the 8
   // XCDs round-robin), so the activation tiles of a weight tile share its L2.
-  const int L = blockIdx.x;
+  // Range sp of nsplit: super-blocks [sb0, sb1) (partial outputs to part when split).
+  const int tiles = tiles_m * tiles_n;
+  const int sp = __builtin_amdgcn_readfirstlane((int)blockIdx.x / tiles);
+  const int L = (int)blockIdx.x - sp * tiles;
+  const int sb0 = __builtin_amdgcn_readfirstlane(sp * nb / nsplit), sb1 = __builtin_amdgcn_readfirstlane((sp + 1) * nb / nsplit);
   int tn, tm;
   if (xcd_map) {
     tn = 8 * (L / (8 * tiles_m)) + (L & 7);
@@ -196,7 +201,7 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   // fold into T; the next super-block's loads spread over the K-steps, and one of the
   // mins products per sub-block; at the end T into acc.
   auto run_sb = [&](int s) {
-    const bool next = s + 1 < nb;
+    const bool next = s + 1 < sb1;
     hdr_n = ld_hdr(s + 1);
     const uint8_t* P = lds + __builtin_amdgcn_readfirstlane((s & 1) * kQBuf);
     // this lane's weight row (get_scale_min_k4, quant_formats.h:62-70): sc_j as (sc, sc)
@@ -283,14 +288,14 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
   // prologue: the first super-block's operands and weights
 #pragma unroll
-  for (int i = 0; i < 8; ++i) issue_piece(0, i);
-  hdr = ld_hdr(0);
+  for (int i = 0; i < 8; ++i) issue_piece(sb0, i);
+  hdr = ld_hdr(sb0);
 #pragma unroll
-  for (int g = 0; g < 4; ++g) nib[g] = ld_nib(0, g);
+  for (int g = 0; g < 4; ++g) nib[g] = ld_nib(sb0, g);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   lds_barrier();
 #pragma unroll 1
-  for (int s = 0; s < nb; ++s) {
+  for (int s = sb0; s < sb1; ++s) {
     run_sb(s);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
@@ -308,6 +313,11 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int64_t nq = nbase + 32 * wave + 8 * q + 4 * hh;
+      if (nsplit > 1) {
+        float* pr = part + ((int64_t)sp * m + mbase + row) * ((int64_t)kQN * tiles_n) + (nq - nbase0);
+        *reinterpret_cast<float4*>(pr) = float4{acc[mt][4 * q], acc[mt][4 * q + 1], acc[mt][4 * q + 2], acc[mt][4 * q + 3]};
+        continue;
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int64_t n = nq + e;
@@ -347,19 +357,33 @@ hipError_t launch_act16i_from_q16(const uint8_t* acts, int64_t arb, int64_t m, i
   return hipGetLastError();
 }
 
+int64_t q16_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {
+  const int64_t nbase0 = n0 / kRowGroup * kRowGroup;
+  const int64_t tiles_n = (n1 - nbase0 + kQN - 1) / kQN, tiles_m = (m + kQM - 1) / kQM;
+  const int sp = split_ranges(tiles_n * tiles_m, w.cus > 0 ? w.cus : 256, w.nblk);
+  return sp > 1 ? (int64_t)sp * m * kQN * tiles_n * 4 : 0;
+}
+
 hipError_t launch_gemm_q16(const WeightDev& w, const uint8_t* act, int64_t m, int64_t n0, int64_t n1, float* y,
-                           int64_t ys, const float* bias, hipStream_t s) {
+                           int64_t ys, const float* bias, float* part, hipStream_t s) {
   if (!gemm_q16_ok(w, m, n0, n1)) return hipErrorInvalidValue;
   const int64_t nbase0 = n0 / kRowGroup * kRowGroup;
   const int64_t tiles_n = (n1 - nbase0 + kQN - 1) / kQN;
   const int64_t tiles_m = (m + kQM - 1) / kQM;
+  const int nsplit = split_ranges(tiles_n * tiles_m, w.cus > 0 ? w.cus : 256, w.nblk);
+  if (nsplit > 1 && (part == nullptr || m > 65535)) return hipErrorInvalidValue;
   const int xcd_map = tiles_n % 8 == 0 ? 1 : 0;
   const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_q4k_q16),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kQLds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_gemm_q4k_q16, dim3((unsigned)(tiles_n * tiles_m)), dim3(kQThreads), kQLds, s, w.plane[0],
+  hipLaunchKernelGGL(k_gemm_q4k_q16, dim3((unsigned)(tiles_n * tiles_m * nsplit)), dim3(kQThreads), kQLds, s, w.plane[0],
                      w.plane[1], (int)w.nblk, nbase0, w.n_pad, n0, n1, act, act16i_rows(m), m, y, ys, bias,
-                     (int)tiles_m, xcd_map);
+                     (int)tiles_m, xcd_map, (int)tiles_n, nsplit, part);
+  if (nsplit > 1) {
+    const hipError_t e2 = hipGetLastError();
+    if (e2 != hipSuccess) return e2;
+    return launch_split_sum(part, nsplit, m, kQN * tiles_n, nbase0, n0, n1, y, ys, bias, s);
+  }
   return hipGetLastError();
 }
 

@@ -71,7 +71,6 @@ namespace {
 
 constexpr int kXM = 64, kXN = 128;  // activation rows x weight rows per workgroup
 constexpr int kXThreads = 256;      // 4 waves, one per SIMD
-constexpr int kXMaxSplit = 16;      // super-block ranges per tile at most
 
 // Super-block buffer: activation codes [j (8)][h (int16: 2)][t (2)][lane (64)][16 B], then
 // the activation scales [t (2)][j (8)][row (32)].
@@ -473,7 +472,7 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
 // y[r, n] = sum over the ranges, in range order, of part[range][r][n - nbase0] (+ bias[n]),
 // n in [n0, n1): one thread per output, rows in the grid's y dimension.
-__global__ __launch_bounds__(256) void k_q6x_sum(const float* __restrict__ part, int nsplit, int64_t m, int64_t W,
+__global__ __launch_bounds__(256) void k_split_sum(const float* __restrict__ part, int nsplit, int64_t m, int64_t W,
                                                  int64_t nbase0, int64_t n0, int64_t n1, float* __restrict__ y,
                                                  int64_t ys, const float* __restrict__ bias) {
   const int64_t n = n0 + (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -499,11 +498,7 @@ Q6xGrid q6x_grid(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {
   g.nbase0 = n0 / kRowGroup * kRowGroup;
   g.tiles_n = (n1 - g.nbase0 + kXN - 1) / kXN;
   g.tiles_m = (m + kXM - 1) / kXM;
-  const int64_t tiles = g.tiles_n * g.tiles_m, cus = w.cus > 0 ? w.cus : 256;
-  int64_t sp = tiles >= cus ? 1 : (cus + tiles - 1) / tiles;
-  sp = sp < w.nblk / 2 ? sp : w.nblk / 2;
-  sp = sp < kXMaxSplit ? sp : kXMaxSplit;
-  g.nsplit = (int)(sp > 1 ? sp : 1);
+  g.nsplit = split_ranges(g.tiles_n * g.tiles_m, w.cus > 0 ? w.cus : 256, w.nblk);
   return g;
 }
 
@@ -569,9 +564,16 @@ hipError_t launch_gemm_q6x(const WeightDev& w, int af, const uint8_t* act, int64
   if (g.nsplit > 1) {
     const hipError_t e2 = hipGetLastError();
     if (e2 != hipSuccess) return e2;
-    hipLaunchKernelGGL(k_q6x_sum, dim3((unsigned)((n1 - n0 + 255) / 256), (unsigned)m), dim3(256), 0, s, part,
-                       g.nsplit, m, (int64_t)kXN * g.tiles_n, g.nbase0, n0, n1, y, ys, bias);
+    return launch_split_sum(part, g.nsplit, m, (int64_t)kXN * g.tiles_n, g.nbase0, n0, n1, y, ys, bias, s);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_split_sum(const float* part, int nsplit, int64_t m, int64_t W, int64_t nbase0, int64_t n0,
+                            int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s) {
+  if (m <= 0 || m > 65535 || n1 <= n0 || nsplit < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_split_sum, dim3((unsigned)((n1 - n0 + 255) / 256), (unsigned)m), dim3(256), 0, s, part, nsplit,
+                     m, W, nbase0, n0, n1, y, ys, bias);
   return hipGetLastError();
 }
 

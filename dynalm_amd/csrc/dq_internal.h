@@ -99,6 +99,22 @@ hipError_t launch_act16_from_q8k(const uint8_t* acts, int64_t arb, int64_t m, in
 hipError_t launch_act16_quant(const float* x, int64_t x_stride, int64_t m, int64_t k, uint8_t* out, hipStream_t s);
 hipError_t launch_gemm_h16(const WeightDev& w, const uint8_t* act16, int64_t m, int64_t n0, int64_t n1, float* y,
                            int64_t ys, const float* bias, hipStream_t s);
+
+// Split K for the tolerance-parity GEMMs (per-32 and int16 rows, dq_gemm_p32.hip,
+// dq_gemm_q16.hip, dq_gemm_q6x.hip): where a launch's tiles leave CUs idle, each tile's
+// super-blocks split into ranges (split_ranges: as many as fit one round of one workgroup
+// per CU, at least 2 super-blocks each, at most 16); every range writes its partial tile to
+// part[range][m][W] and launch_split_sum adds the ranges in order (+ bias) into y's
+// [n0, n1), so the bits do not depend on timing.
+inline int split_ranges(int64_t tiles, int cus, int64_t nblk) {
+  if (tiles <= 0 || tiles >= cus) return 1;
+  int64_t sp = cus / tiles;
+  sp = sp < nblk / 2 ? sp : nblk / 2;
+  sp = sp < 16 ? sp : 16;
+  return sp > 1 ? (int)sp : 1;
+}
+hipError_t launch_split_sum(const float* part, int nsplit, int64_t m, int64_t W, int64_t nbase0, int64_t n0,
+                            int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s);
 // The Q4_K x per-32 GEMM on the f16 matrix cores (dq_gemm_p32.hip), qmm's int8 gemm
 // contract: 128 x 256 tiles, codes as f16 in the "act32" layout of act32_bytes(m, k)
 // bytes written from per-32 rows (launch_act32_from_p32). gemm_p32_ok: Q4_K and the
@@ -106,8 +122,9 @@ hipError_t launch_gemm_h16(const WeightDev& w, const uint8_t* act16, int64_t m, 
 int64_t act32_bytes(int64_t m, int64_t k);
 bool gemm_p32_ok(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
 hipError_t launch_act32_from_p32(const uint8_t* acts, int64_t arb, int64_t m, int64_t k, uint8_t* out, hipStream_t s);
+int64_t p32_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
 hipError_t launch_gemm_p32(const WeightDev& w, const uint8_t* act32, int64_t m, int64_t n0, int64_t n1, float* y,
-                           int64_t ys, const float* bias, hipStream_t s);
+                           int64_t ys, const float* bias, float* part, hipStream_t s);
 // The Q4_K x int16 GEMM on the f16 matrix cores (dq_gemm_q16.hip), the int16 contract
 // (ActBlockQ16 rows, qmm's int16 mode): 64 x 256 tiles, codes split into lo and 256 hi
 // as f16 in the "act16i" layout of act16i_bytes(m, k) bytes written from ActBlockQ16
@@ -116,8 +133,9 @@ int64_t act16i_bytes(int64_t m, int64_t k);
 bool gemm_q16_ok(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
 hipError_t launch_act16i_from_q16(const uint8_t* acts, int64_t arb, int64_t m, int64_t k, uint8_t* out,
                                   hipStream_t s);
+int64_t q16_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
 hipError_t launch_gemm_q16(const WeightDev& w, const uint8_t* act, int64_t m, int64_t n0, int64_t n1, float* y,
-                           int64_t ys, const float* bias, hipStream_t s);
+                           int64_t ys, const float* bias, float* part, hipStream_t s);
 // The Q6_K GEMM on the f16 matrix cores (dq_gemm_q6x.hip) for per-32 rows (af =
 // kActPer32) and int16 rows (kActQ16): launch_q6x_act writes the rows' narrow operand
 // layout (q6x_act_bytes), launch_gemm_q6x runs 64 x 128 tiles over it. Where the tiles

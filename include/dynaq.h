@@ -92,7 +92,7 @@ typedef enum dq_dtype {
  *                  dynacore/cpu/avx2/kernels_avx2.cpp:1631-1652). With every weight type
  *                 (Q4_0 as qmm's int16 mode runs it, qmm_reference.cpp:68-93; the reference's
  *                 AVX2 int16 kernels cover Q8_0, Q4_K and Q6_K); the GEMV forms each
- *                 32-value (Q6_K: 16-value) integer dot exactly; Q4_K's GEMM (from 20
+ *                 32-value (Q6_K: 16-value) integer dot exactly; Q4_K's GEMM (from 6
  *                 rows) and Q6_K's (from 5) split each code into lo and 256 hi on the
  *                 f16 matrix cores;
  *   DQ_ACT_F32    no quantization: fp32 rows of k floats (4k bytes), dynacore's kF32

@@ -1,6 +1,7 @@
 """GPU parity of the Q4_K x per-32 GEMM on the f16 matrix cores (dq_gemm_p32.hip), qmm's
 int8 gemm contract: dq_gemm on DQ_ACT_PER32 rows, dq_matmul_act(DQ_ACT_PER32) and
-dq_qmm_gemm in int8 mode send Q4_K at more than 64 rows to it.
+dq_qmm_gemm in int8 mode send Q4_K from 12 rows to it (split K where its tiles leave
+CUs idle).
 
 Its per-sub-block integers P_j are exact; the fp32 terms are summed in an order of
 its own (two VALU operations per output and sub-block, the mins term on fp32 MFMAs),
@@ -88,6 +89,12 @@ def _check(m: int, k: int, n: int, n0: int, n1: int, seed: int, saturate: bool =
 def test_p32_superblock_counts(cuda, m, k):
     """1, 3 and 5 super-blocks; m = 300, 130 and 520 end on partial activation tiles."""
     _check(m, k, 2048, 0, 2048, 6100 + m)
+
+
+def test_p32_split_ranges(cuda):
+    """20 rows on 8 weight tiles (K = 4096): each tile's 16 super-blocks split into 8
+    ranges whose partials a second launch adds in order; dq_gemm on the per-32 rows."""
+    _check(20, 4096, 2048, 0, 2048, 6150)
 
 
 def test_p32_row_range(cuda):

@@ -2,7 +2,7 @@
 int16 contract (ActBlockQ16 rows: int16 codes, one scale and one code sum per 32
 values; dynacore/cpu/avx2/kernels_avx2.cpp:1631-1729) through dq_gemm on DQ_ACT_Q16
 rows, dq_matmul_act(DQ_ACT_Q16) on fp32 rows and dq_qmm_gemm in int16 mode, which
-take it from 20 rows.
+take it from 6 rows (split K where its tiles leave CUs idle).
 
 The integers sc_j P_j are rounded to fp32 where they pass 2^24 and the fp32 terms are
 summed in an order of the kernel's own, so it is held to the reference's bound against

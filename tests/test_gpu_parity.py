@@ -922,7 +922,8 @@ Q16_AVX2 = [O.Q8_0, O.Q4_K, O.Q6_K]  # the types with a reference AVX2 int16 ker
 def test_gemv_q16_parity(cuda, t, m):
     """int16 GEMV: within the reference's bound of the exact product and of the oracle;
     integer unit partials bit-exact; dq_matmul_act (GPU quantization) gives the same bits
-    as its kernel on the same rows (the GEMV; for Q6_K from 5 rows the f16 GEMM)."""
+    as its kernel on the same rows (the GEMV; for Q6_K from 5 rows and Q4_K from 6 the f16
+    GEMM)."""
     import dqtorch as T
 
     k, n = 1280, 200
@@ -940,7 +941,8 @@ def test_gemv_q16_parity(cuda, t, m):
     want_u, _ = O.partials(t, O.ACT_Q16, rows, a, k)
     assert np.array_equal(host(units), want_u)
     ya = host(T.matmul_act(w, O.ACT_Q16, dev(x)))
-    same = host(T.gemm(w, O.ACT_Q16, dev(a))) if t == O.Q6_K and m >= 5 else y
+    gemm_route = (t == O.Q6_K and m >= 5) or (t == O.Q4_K and m >= 6)  # dq_matmul_act's GEMM thresholds
+    same = host(T.gemm(w, O.ACT_Q16, dev(a))) if gemm_route else y
     assert np.array_equal(ya.view(np.uint32), same.view(np.uint32))
 
 
