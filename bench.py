@@ -293,13 +293,17 @@ def decode_stack(steps: int, stream: int) -> dict:
 def prefill_sweep(ms: list[int], weights, gen) -> list[dict]:
     """Config 4's sweep: dq_matmul on M fp32 rows (Q8_K quantization on the GPU, then
     the kernel dq_matmul dispatches to: the skinny MFMA GEMV up to 16 rows, the MFMA
-    GEMM above), K=4096 N=14336, rotated weights, graph replay."""
+    GEMM above), K=4096 N=14336, rotated weights, graph replay. Beside it the engine's
+    plan (qmm on per-32 rows at any M, dq_matmul_plan): per-32 quantize + the f16 per-32
+    GEMM (split K where its tiles leave CUs idle)."""
     import torch
 
     import dynalm_amd as dq
 
     out = []
     ng = min(4, len(weights))
+    eng = dq.plan_defaults()
+    eng.int8_decode_max_rows = 1 << 30
     for m in ms:
         x = torch.randn((m, K), generator=gen, device="cuda", dtype=torch.float32)
         y = torch.empty((m, N), dtype=torch.float32, device="cuda")
@@ -309,9 +313,11 @@ def prefill_sweep(ms: list[int], weights, gen) -> list[dict]:
         tops = 2.0 * m * N * K / (ms_call * 1e-3) / 1e12
         cus = torch.cuda.get_device_properties(0).multi_processor_count
         f16 = m > 128 and -(-m // 128) * -(-N // 256) * 8 >= 5 * cus  # the f16 GEMM's rule (gemm_h16_pays)
+        ms_eng = time_graph(lambda i, st: dq.matmul_plan(weights[i % ng], eng, x, m, K, y, N, None, st), iters, 3)
         out.append({"m": m, "kernel": "skinny MFMA GEMV" if m <= 16 else "f16 MFMA GEMM" if f16 else "int8 MFMA GEMM",
                     "ms_per_call": round(ms_call, 4), "tops": round(tops, 1),
-                    "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2), "tokens_per_s": round(m / (ms_call * 1e-3), 1)})
+                    "pct_peak_int8": round(100 * tops / PEAK_INT8_TOPS, 2), "tokens_per_s": round(m / (ms_call * 1e-3), 1),
+                    "engine_plan_per32_ms_per_call": round(ms_eng, 4)})
         del x, y
     return out
 
@@ -524,7 +530,7 @@ def main() -> None:
     ap.add_argument("--copies", type=int, default=16, help="rotated weight copies (x 33 MB)")
     ap.add_argument("--gemm-m", type=int, default=512)
     ap.add_argument("--gemm-iters", type=int, default=50)
-    ap.add_argument("--sweep", default="64,128,512,2048",
+    ap.add_argument("--sweep", default="16,64,128,512,2048",
                     help="config 4 prefill sweep: dq_matmul (quantization + the kernel dq_matmul picks) at these M "
                          "('' to skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
