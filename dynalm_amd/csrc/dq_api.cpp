@@ -415,16 +415,16 @@ size_t matmul_scratch_bytes(const dq_weight* w, int fmt, int64_t m) {
   if (f == DQ_ACT_F32) return gemv_split_bytes(w->dev, f, m < 8 ? m : 8);  // the rows are read in place
   size_t acts = round256((size_t)(m * dq_act_row_bytes(f, w->dev.k)));
   if (f == DQ_ACT_Q8_K && gemm_h16_pays(w->dev, m, 0, w->dev.n)) acts = round256((size_t)act16_bytes(m, w->dev.k));
+  // the f16 GEMMs of the per-32 and int16 contracts: their operand layout (quantized
+  // straight from the fp32 rows) and the range partials
   if (f == DQ_ACT_PER32 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, f, m)) {
-    // the per-32 rows, then their act32 layout and the range partials
-    acts += round256((size_t)act32_bytes(m, w->dev.k)) + (size_t)p32_part_bytes(w->dev, m, 0, w->dev.n);
+    acts = round256((size_t)act32_bytes(m, w->dev.k)) + (size_t)p32_part_bytes(w->dev, m, 0, w->dev.n);
   }
   if (f == DQ_ACT_Q16 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, f, m)) {
-    // the int16 rows, then their act16i layout and the range partials
-    acts += round256((size_t)act16i_bytes(m, w->dev.k)) + (size_t)q16_part_bytes(w->dev, m, 0, w->dev.n);
+    acts = round256((size_t)act16i_bytes(m, w->dev.k)) + (size_t)q16_part_bytes(w->dev, m, 0, w->dev.n);
   }
   if (w->dev.dtype == DQ_Q6_K && (f == DQ_ACT_PER32 || f == DQ_ACT_Q16) && use_gemm(w->dev, f, m)) {
-    acts += round256((size_t)q6x_act_bytes(f, m, w->dev.k)) + (size_t)q6x_part_bytes(w->dev, m, 0, w->dev.n);
+    acts = round256((size_t)q6x_act_bytes(f, m, w->dev.k)) + (size_t)q6x_part_bytes(w->dev, m, 0, w->dev.n);
   }
   return acts + gemv_split_bytes(w->dev, f, m < 8 ? m : 8);
 }
@@ -495,15 +495,13 @@ int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int6
     return gemm_h16_from_x(w, x, m, x_stride, y, y_stride, bias, s, r);
   }
   if (fmt == DQ_ACT_PER32 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, fmt, m)) {
-    // Q4_K x per-32 prefill: per-32 rows, their f16 operand layout, the f16 GEMM (all
-    // in the region when one is given)
-    const size_t rows_bytes = round256((size_t)(m * arb));
+    // Q4_K x per-32 prefill: the fp32 rows quantized straight into the f16 operand layout
+    // (the per-32 quantizer's codes), the f16 GEMM (all in the region when one is given)
     const size_t lay = round256((size_t)act32_bytes(m, w->dev.k)), pb = (size_t)p32_part_bytes(w->dev, m, 0, w->dev.n);
     void* buf = nullptr;
-    if (int rc = acts_buffer(w->dev.device, rows_bytes + lay + pb, r, &buf); rc != DQ_OK) return rc;
-    uint8_t* a32 = static_cast<uint8_t*>(buf) + rows_bytes;
-    if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, buf, stream); rc != DQ_OK) return rc;
-    DQ_HIP(launch_act32_from_p32(static_cast<const uint8_t*>(buf), arb, m, w->dev.k, a32, s), "act32 conversion launch");
+    if (int rc = acts_buffer(w->dev.device, lay + pb, r, &buf); rc != DQ_OK) return rc;
+    uint8_t* a32 = static_cast<uint8_t*>(buf);
+    DQ_HIP(launch_act32_quant(x, m > 1 ? x_stride : w->dev.k, m, w->dev.k, a32, s), "act32 quantize launch");
     DQ_HIP(launch_gemm_p32(w->dev, a32, m, 0, w->dev.n, y, y_stride, bias,
                            pb > 0 ? reinterpret_cast<float*>(a32 + lay) : nullptr, s),
            "gemm launch");
@@ -520,31 +518,27 @@ int matmul_act_impl(const dq_weight* w, int fmt, const float* x, int64_t m, int6
     return DQ_OK;
   }
   if (w->dev.dtype == DQ_Q6_K && (fmt == DQ_ACT_PER32 || fmt == DQ_ACT_Q16) && use_gemm(w->dev, fmt, m)) {
-    // Q6_K x per-32 / int16 prefill: the rows, their narrow operand layout, the f16 GEMM
-    // (and its range partials)
-    const size_t rows_bytes = round256((size_t)(m * arb));
+    // Q6_K x per-32 / int16 prefill: the fp32 rows quantized straight into the narrow
+    // operand layout, the f16 GEMM (and its range partials)
     const size_t lay = round256((size_t)q6x_act_bytes(fmt, m, w->dev.k));
     const size_t pb = (size_t)q6x_part_bytes(w->dev, m, 0, w->dev.n);
     void* buf = nullptr;
-    if (int rc = acts_buffer(w->dev.device, rows_bytes + lay + pb, r, &buf); rc != DQ_OK) return rc;
-    uint8_t* a2 = static_cast<uint8_t*>(buf) + rows_bytes;
-    if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, buf, stream); rc != DQ_OK) return rc;
-    DQ_HIP(launch_q6x_act(fmt, static_cast<const uint8_t*>(buf), arb, m, w->dev.k, a2, s), "operand layout launch");
+    if (int rc = acts_buffer(w->dev.device, lay + pb, r, &buf); rc != DQ_OK) return rc;
+    uint8_t* a2 = static_cast<uint8_t*>(buf);
+    DQ_HIP(launch_q6x_quant(fmt, x, m > 1 ? x_stride : w->dev.k, m, w->dev.k, a2, s), "operand layout quantize launch");
     DQ_HIP(launch_gemm_q6x(w->dev, fmt, a2, m, 0, w->dev.n, y, y_stride, bias,
                            pb > 0 ? reinterpret_cast<float*>(a2 + lay) : nullptr, s),
            "gemm launch");
     return DQ_OK;
   }
   if (fmt == DQ_ACT_Q16 && w->dev.dtype == DQ_Q4_K && use_gemm(w->dev, fmt, m)) {
-    // Q4_K x int16 prefill: int16 rows, their lo / 256 hi f16 layout, the f16 GEMM
-    const size_t rows_bytes = round256((size_t)(m * arb));
+    // Q4_K x int16 prefill: the fp32 rows quantized straight into the lo / 256 hi f16
+    // layout (the int16 quantizer's codes), the f16 GEMM
     const size_t lay = round256((size_t)act16i_bytes(m, w->dev.k)), pb = (size_t)q16_part_bytes(w->dev, m, 0, w->dev.n);
     void* buf = nullptr;
-    if (int rc = acts_buffer(w->dev.device, rows_bytes + lay + pb, r, &buf); rc != DQ_OK) return rc;
-    uint8_t* a16 = static_cast<uint8_t*>(buf) + rows_bytes;
-    if (int rc = dq_act_quantize(fmt, x, m, w->dev.k, m > 1 ? x_stride : w->dev.k, buf, stream); rc != DQ_OK) return rc;
-    DQ_HIP(launch_act16i_from_q16(static_cast<const uint8_t*>(buf), arb, m, w->dev.k, a16, s),
-           "act16i conversion launch");
+    if (int rc = acts_buffer(w->dev.device, lay + pb, r, &buf); rc != DQ_OK) return rc;
+    uint8_t* a16 = static_cast<uint8_t*>(buf);
+    DQ_HIP(launch_act16i_quant(x, m > 1 ? x_stride : w->dev.k, m, w->dev.k, a16, s), "act16i quantize launch");
     DQ_HIP(launch_gemm_q16(w->dev, a16, m, 0, w->dev.n, y, y_stride, bias,
                            pb > 0 ? reinterpret_cast<float*>(a16 + lay) : nullptr, s),
            "gemm launch");

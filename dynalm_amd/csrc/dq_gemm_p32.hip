@@ -52,6 +52,7 @@
 #include "dq_f16mma.h"
 #include "dq_internal.h"
 #include "dq_mfma.h"
+#include "dq_quant.h"
 
 namespace dq {
 
@@ -108,6 +109,39 @@ __global__ __launch_bounds__(256) void k_act32_from_p32(const uint8_t* __restric
       c = *reinterpret_cast<const float*>(b) * (float)*reinterpret_cast<const int32_t*>(b + 4);
     }
     *reinterpret_cast<float*>(out + codes_bytes + da_bytes + (T * nb + s) * 1024 + t * 4) = c;
+  }
+}
+
+// fp32 rows -> act32 directly, with the per-32 quantizer's arithmetic (per32_quant, the
+// same device function as the standalone quantizer: the codes, d and code sums are its
+// bytes, so the layout equals k_act32_from_p32's of those rows). One wave per (super-
+// block, padded row); lane l quantizes values 4 l .. 4 l + 3 (block l / 8), and even lane
+// e = 8 j + 4 hh + 2 h writes K-step 2 j + h of lane half hh with lane e + 1's codes.
+__global__ __launch_bounds__(64) void k_act32_quant(const float* __restrict__ x, int64_t x_stride, int64_t m,
+                                                    int64_t k, int64_t m_pad, uint8_t* __restrict__ out) {
+  const int l = threadIdx.x;
+  const int s = blockIdx.x;
+  const int64_t row = blockIdx.y;
+  const int nb = (int)(k / 256);
+  const auto rx = rsrc(x + (row < m ? row * x_stride : 0), row < m ? (u32)(k * 4) : 0u);
+  float v[4];
+  load4f(rx, (u32)(((int64_t)s * 256 + 4 * l) * 4), v);
+  float d;
+  int sum;
+  const u32 packed = per32_quant(v, d, sum);
+  const u32 next = (u32)__builtin_amdgcn_ds_bpermute(4 * ((l + 1) & 63), (int)packed);
+  const int64_t T = row >> 5, r = row & 31;
+  const int64_t codes_bytes = m_pad * nb * 512, da_bytes = m_pad / 32 * nb * 1024;
+  const int j = l >> 3;
+  if ((l & 1) == 0) {
+    const int hh = (l >> 2) & 1, kk = 2 * j + ((l >> 1) & 1);
+    *reinterpret_cast<v4u*>(out + ((T * nb + s) * 16 + kk) * 1024 + (32 * hh + r) * 16) = codes_f16(packed, next);
+  }
+  if ((l & 7) == 0) {
+    float* dab = reinterpret_cast<float*>(out + codes_bytes + (T * nb + s) * 1024);
+    dab[j * 32 + r] = d;
+    float* cb = reinterpret_cast<float*>(out + codes_bytes + da_bytes + (T * nb + s) * 1024);
+    cb[(j >> 1) * 64 + 32 * (j & 1) + r] = d * (float)sum;
   }
 }
 
@@ -354,6 +388,13 @@ int64_t p32_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {
   const int64_t tiles_n = (n1 - nbase0 + kPN - 1) / kPN, tiles_m = (m + kPM - 1) / kPM;
   const int sp = split_ranges(tiles_n * tiles_m, w.cus > 0 ? w.cus : 256, w.nblk);
   return sp > 1 ? (int64_t)sp * m * kPN * tiles_n * 4 : 0;
+}
+
+hipError_t launch_act32_quant(const float* x, int64_t x_stride, int64_t m, int64_t k, uint8_t* out, hipStream_t s) {
+  const int64_t mp = act32_rows(m);
+  if (mp > 65535 || k % 256 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_act32_quant, dim3((unsigned)(k / 256), (unsigned)mp), dim3(64), 0, s, x, x_stride, m, k, mp, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm_p32(const WeightDev& w, const uint8_t* act32, int64_t m, int64_t n0, int64_t n1, float* y,

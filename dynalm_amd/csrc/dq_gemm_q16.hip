@@ -44,6 +44,7 @@
 #include "dq_f16mma.h"
 #include "dq_internal.h"
 #include "dq_mfma.h"
+#include "dq_quant.h"
 
 namespace dq {
 
@@ -115,6 +116,50 @@ __global__ __launch_bounds__(256) void k_act16i_from_q16(const uint8_t* __restri
       c = *reinterpret_cast<const float*>(b) * (float)*reinterpret_cast<const int32_t*>(b + 4);
     }
     *reinterpret_cast<float*>(out + codes_bytes + da_bytes + (T * nb + s) * 1024 + t * 4) = c;
+  }
+}
+
+// fp32 rows -> act16i directly, with the int16 quantizer's arithmetic (q16_quant, the
+// same device function as the standalone quantizer: the layout equals k_act16i_from_q16's
+// of the rows it writes). One wave per (super-block, padded row); lane l quantizes values
+// 4 l .. 4 l + 3, and even lane e = 8 j + 4 hh + 2 h writes both planes of K-step 2 j + h
+// of lane half hh with lane e + 1's codes.
+__global__ __launch_bounds__(64) void k_act16i_quant(const float* __restrict__ x, int64_t x_stride, int64_t m,
+                                                     int64_t k, int64_t m_pad, uint8_t* __restrict__ out) {
+  const int l = threadIdx.x;
+  const int s = blockIdx.x;
+  const int64_t row = blockIdx.y;
+  const int nb = (int)(k / 256);
+  const auto rx = rsrc(x + (row < m ? row * x_stride : 0), row < m ? (u32)(k * 4) : 0u);
+  float v[4];
+  load4f(rx, (u32)(((int64_t)s * 256 + 4 * l) * 4), v);
+  float d;
+  int sum;
+  const v2u c = q16_quant(v, d, sum);
+  const int src = 4 * ((l + 1) & 63);
+  const u32 n0 = (u32)__builtin_amdgcn_ds_bpermute(src, (int)c.x), n1 = (u32)__builtin_amdgcn_ds_bpermute(src, (int)c.y);
+  const int64_t T = row >> 5, r = row & 31;
+  const int64_t codes_bytes = m_pad * nb * 1024, da_bytes = m_pad / 32 * nb * 1024;
+  const int j = l >> 3;
+  if ((l & 1) == 0) {
+    const int hh = (l >> 2) & 1, kk = 2 * j + ((l >> 1) & 1);
+    // values {0, 2, 1, 3} of this lane, {4, 6, 5, 7} of the next: int16 halves of c / n
+    const int a[8] = {(int16_t)(c.x & 0xFFFFu), (int16_t)(c.y & 0xFFFFu), (int16_t)(c.x >> 16), (int16_t)(c.y >> 16),
+                      (int16_t)(n0 & 0xFFFFu),  (int16_t)(n1 & 0xFFFFu),  (int16_t)(n0 >> 16),  (int16_t)(n1 >> 16)};
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      int q[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q[i] = p ? (a[i] >> 8) * 256 : (a[i] & 255);
+      *reinterpret_cast<v4u*>(out + (((T * nb + s) * 16 + kk) * 2 + p) * 1024 + (32 * hh + r) * 16) =
+          v4u{f16x2(q[0], q[1]), f16x2(q[2], q[3]), f16x2(q[4], q[5]), f16x2(q[6], q[7])};
+    }
+  }
+  if ((l & 7) == 0) {
+    float* dab = reinterpret_cast<float*>(out + codes_bytes + (T * nb + s) * 1024);
+    dab[j * 32 + r] = d;
+    float* cb = reinterpret_cast<float*>(out + codes_bytes + da_bytes + (T * nb + s) * 1024);
+    cb[(j >> 1) * 64 + 32 * (j & 1) + r] = d * (float)sum;
   }
 }
 
@@ -362,6 +407,15 @@ int64_t q16_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {
   const int64_t tiles_n = (n1 - nbase0 + kQN - 1) / kQN, tiles_m = (m + kQM - 1) / kQM;
   const int sp = split_ranges(tiles_n * tiles_m, w.cus > 0 ? w.cus : 256, w.nblk);
   return sp > 1 ? (int64_t)sp * m * kQN * tiles_n * 4 : 0;
+}
+
+hipError_t launch_act16i_quant(const float* x, int64_t x_stride, int64_t m, int64_t k, uint8_t* out,
+                               hipStream_t s) {
+  const int64_t mp = act16i_rows(m);
+  if (mp > 65535 || k % 256 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_act16i_quant, dim3((unsigned)(k / 256), (unsigned)mp), dim3(64), 0, s, x, x_stride, m, k, mp,
+                     out);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm_q16(const WeightDev& w, const uint8_t* act, int64_t m, int64_t n0, int64_t n1, float* y,

@@ -64,6 +64,7 @@
 #include "dq_f16mma.h"
 #include "dq_internal.h"
 #include "dq_mfma.h"
+#include "dq_quant.h"
 
 namespace dq {
 
@@ -144,6 +145,55 @@ __global__ __launch_bounds__(256) void k_q6x_act(const uint8_t* __restrict__ act
     const float d = row < m ? *reinterpret_cast<const float*>(acts + row * arb + (int64_t)(8 * s + j) * kBlk) : 0.0f;
     *reinterpret_cast<float*>(out + codes_bytes + (T * nb + s) * 1024 + t * 4) = d;
   }
+}
+
+// fp32 rows -> act8 / act16b directly, with the standalone quantizers' arithmetic
+// (per32_quant / q16_quant: the layout equals k_q6x_act's of the rows they write). One
+// wave per (super-block, padded row); lane l quantizes values 4 l .. 4 l + 3. per-32: lane
+// e = 8 j + 4 hh writes block j's unit of lane half hh from lanes e .. e + 3; int16: even
+// lane e = 8 j + 4 hh + 2 h writes K-step 2 j + h's unit with lane e + 1's codes.
+template <bool kI16>
+__global__ __launch_bounds__(64) void k_q6x_quant(const float* __restrict__ x, int64_t x_stride, int64_t m, int64_t k,
+                                                  int64_t m_pad, uint8_t* __restrict__ out) {
+  constexpr int kH = kI16 ? 2 : 1;
+  const int l = threadIdx.x;
+  const int s = blockIdx.x;
+  const int64_t row = blockIdx.y;
+  const int nb = (int)(k / 256);
+  const auto rx = rsrc(x + (row < m ? row * x_stride : 0), row < m ? (u32)(k * 4) : 0u);
+  float v[4];
+  load4f(rx, (u32)(((int64_t)s * 256 + 4 * l) * 4), v);
+  float d;
+  int sum;
+  const int64_t T = row >> 5, r = row & 31;
+  const int64_t codes_bytes = m_pad * nb * 256 * kH;
+  const int j = l >> 3, hh = (l >> 2) & 1;
+  if (kI16) {
+    const v2u c = q16_quant(v, d, sum);
+    const int src = 4 * ((l + 1) & 63);
+    const u32 n0 = (u32)__builtin_amdgcn_ds_bpermute(src, (int)c.x), n1 = (u32)__builtin_amdgcn_ds_bpermute(src, (int)c.y);
+    if ((l & 1) == 0) {
+      // halves (v0, v2), (v1, v3) of this lane, (v4, v6), (v5, v7) of the next, plus 32768
+      const int h = (l >> 1) & 1;
+      const v4u o = {__builtin_amdgcn_perm(c.y, c.x, 0x05040100u) ^ 0x80008000u,
+                     __builtin_amdgcn_perm(c.y, c.x, 0x07060302u) ^ 0x80008000u,
+                     __builtin_amdgcn_perm(n1, n0, 0x05040100u) ^ 0x80008000u,
+                     __builtin_amdgcn_perm(n1, n0, 0x07060302u) ^ 0x80008000u};
+      *reinterpret_cast<v4u*>(out + ((((T * nb + s) * 8 + j) * 2 + h) * 64 + 32 * hh + r) * 16) = o;
+    }
+  } else {
+    const u32 c = per32_quant(v, d, sum);
+    // bytes {0, 2, 1, 3} of lanes e .. e + 3, plus 128
+    auto ord = [](u32 w) { return __builtin_amdgcn_perm(0u, w, 0x03010200u) ^ 0x80808080u; };
+    const u32 c1 = (u32)__builtin_amdgcn_ds_bpermute(4 * ((l + 1) & 63), (int)c);
+    const u32 c2 = (u32)__builtin_amdgcn_ds_bpermute(4 * ((l + 2) & 63), (int)c);
+    const u32 c3 = (u32)__builtin_amdgcn_ds_bpermute(4 * ((l + 3) & 63), (int)c);
+    if ((l & 3) == 0) {
+      *reinterpret_cast<v4u*>(out + ((((T * nb + s) * 8 + j)) * 64 + 32 * hh + r) * 16) =
+          v4u{ord(c), ord(c1), ord(c2), ord(c3)};
+    }
+  }
+  if ((l & 7) == 0) reinterpret_cast<float*>(out + codes_bytes + (T * nb + s) * 1024)[j * 32 + r] = d;
 }
 
 // ---------------------------------------------------------------- the GEMM
@@ -535,6 +585,19 @@ hipError_t launch_q6x_act(int af, const uint8_t* acts, int64_t arb, int64_t m, i
     hipLaunchKernelGGL(k_q6x_act<true>, grid, dim3(256), 0, s, acts, arb, m, (int)(k / 256), mp, out);
   } else {
     hipLaunchKernelGGL(k_q6x_act<false>, grid, dim3(256), 0, s, acts, arb, m, (int)(k / 256), mp, out);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_q6x_quant(int af, const float* x, int64_t x_stride, int64_t m, int64_t k, uint8_t* out,
+                            hipStream_t s) {
+  const int64_t mp = q6x_rows(m);
+  if (mp > 65535 || k % 256 != 0 || (af != kActPer32 && af != kActQ16)) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(k / 256), (unsigned)mp);
+  if (af == kActQ16) {
+    hipLaunchKernelGGL(k_q6x_quant<true>, grid, dim3(64), 0, s, x, x_stride, m, k, mp, out);
+  } else {
+    hipLaunchKernelGGL(k_q6x_quant<false>, grid, dim3(64), 0, s, x, x_stride, m, k, mp, out);
   }
   return hipGetLastError();
 }

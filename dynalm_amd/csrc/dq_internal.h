@@ -123,6 +123,9 @@ int64_t act32_bytes(int64_t m, int64_t k);
 bool gemm_p32_ok(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
 hipError_t launch_act32_from_p32(const uint8_t* acts, int64_t arb, int64_t m, int64_t k, uint8_t* out, hipStream_t s);
 int64_t p32_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
+// fp32 rows -> act32 with the per-32 quantizer's arithmetic (the layout of
+// launch_act32_from_p32 on the rows dq_act_quantize writes), in one launch
+hipError_t launch_act32_quant(const float* x, int64_t x_stride, int64_t m, int64_t k, uint8_t* out, hipStream_t s);
 hipError_t launch_gemm_p32(const WeightDev& w, const uint8_t* act32, int64_t m, int64_t n0, int64_t n1, float* y,
                            int64_t ys, const float* bias, float* part, hipStream_t s);
 // The Q4_K x int16 GEMM on the f16 matrix cores (dq_gemm_q16.hip), the int16 contract
@@ -134,6 +137,9 @@ bool gemm_q16_ok(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
 hipError_t launch_act16i_from_q16(const uint8_t* acts, int64_t arb, int64_t m, int64_t k, uint8_t* out,
                                   hipStream_t s);
 int64_t q16_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
+// fp32 rows -> act16i with the int16 quantizer's arithmetic, in one launch
+hipError_t launch_act16i_quant(const float* x, int64_t x_stride, int64_t m, int64_t k, uint8_t* out,
+                               hipStream_t s);
 hipError_t launch_gemm_q16(const WeightDev& w, const uint8_t* act, int64_t m, int64_t n0, int64_t n1, float* y,
                            int64_t ys, const float* bias, float* part, hipStream_t s);
 // The Q6_K GEMM on the f16 matrix cores (dq_gemm_q6x.hip) for per-32 rows (af =
@@ -147,6 +153,9 @@ int64_t q6x_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1);
 bool gemm_q6x_ok(const WeightDev& w, int af, int64_t m, int64_t n0, int64_t n1);
 hipError_t launch_q6x_act(int af, const uint8_t* acts, int64_t arb, int64_t m, int64_t k, uint8_t* out,
                           hipStream_t s);
+// fp32 rows -> the same layout with the per-32 / int16 quantizer's arithmetic, in one launch
+hipError_t launch_q6x_quant(int af, const float* x, int64_t x_stride, int64_t m, int64_t k, uint8_t* out,
+                            hipStream_t s);
 hipError_t launch_gemm_q6x(const WeightDev& w, int af, const uint8_t* act, int64_t m, int64_t n0, int64_t n1, float* y,
                            int64_t ys, const float* bias, float* part, hipStream_t s);
 // The expand-class fp32 GEMM (dq_gemm_f32.hip): weight tiles expanded to fp32 in LDS
