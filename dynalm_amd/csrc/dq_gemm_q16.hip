@@ -54,10 +54,15 @@ constexpr int kQM = 64, kQN = 256;  // activation rows x weight rows per workgro
 constexpr int kQThreads = 512;      // 8 waves, two per SIMD
 // Super-block buffer: operands [k (16)][t (2)][p (2)][lane (64)][16 B], then the
 // activation scales [t (2)][j (8)][row (32)] and the mins operands [t (2)][kk (4)][lane (64)].
-constexpr int kQCodes = 65536, kQDa = kQCodes, kQC = kQDa + 2048;
-constexpr int kQBuf = kQC + 2048;
-constexpr int kQLds = 2 * kQBuf;
-static_assert(kQLds <= 160 * 1024, "LDS");
+// With TT 32-row activation tiles per workgroup (TT = 2, or 1 for few rows): operands
+// 32 TT KB, scales and mins operands TT KB each.
+template <int TT>
+struct QLds {
+  static constexpr int kCodes = 32 * TT * 1024, kDa = kCodes, kC = kDa + TT * 1024;
+  static constexpr int kBuf = kC + TT * 1024;
+  static constexpr int kTotal = 2 * kBuf;
+};
+static_assert(QLds<2>::kTotal <= 160 * 1024, "LDS");
 
 DQ_DEV v16f_t mfma_f32_k2(float a, float b, v16f_t c) { return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0); }
 
@@ -167,11 +172,13 @@ __global__ __launch_bounds__(64) void k_act16i_quant(const float* __restrict__ x
 
 // One workgroup: activation rows [64 tm, + 64) x weight rows [nbase0 + 256 tn, + 256),
 // all super-blocks. Arguments as launch_gemm_q16.
+template <int TT>
 __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_q4k_q16(
     const uint8_t* __restrict__ qs_plane, const uint8_t* __restrict__ hdr_plane, int nb, int64_t nbase0, int64_t n_pad,
     int64_t n0, int64_t n1, const uint8_t* __restrict__ act, int64_t m_pad, int64_t m, float* __restrict__ y,
     int64_t ys, const float* __restrict__ bias, int tiles_m, int xcd_map, int tiles_n, int nsplit,
     float* __restrict__ part) {
+  using X = QLds<TT>;
   extern __shared__ __align__(16) uint8_t lds[];
   const int t = threadIdx.x, lane = t & 63;
   const int li = lane & 31, hh = lane >> 5;
@@ -195,7 +202,7 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   tn = __builtin_amdgcn_readfirstlane(tn);
   tm = __builtin_amdgcn_readfirstlane(tm);
   const int64_t nbase = nbase0 + (int64_t)kQN * tn;
-  const int64_t mbase = (int64_t)tm * kQM;
+  const int64_t mbase = (int64_t)tm * 32 * TT;
 
   const int64_t codes_bytes = m_pad * nb * 1024, da_bytes = m_pad / 32 * nb * 1024;
   const auto ra = rsrc(act, (u32)(codes_bytes + 2 * da_bytes));
@@ -213,17 +220,18 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const u32 vh = (G * (u32)nb * 64u + r64) * 16u;                  // + s * 1024
 
   auto issue_piece = [&](int s, int i) {
-    uint8_t* P = lds + (s & 1) * kQBuf;
-    const int jb = 8 * wave + i;
-    const int64_t T = 2 * (int64_t)tm + ((jb >> 1) & 1);
-    dma16(ra, P + jb * 1024, (u32)(lane * 16), (u32)((((T * nb + s) * 16 + (jb >> 2)) * 2 + (jb & 1)) * 1024));
+    uint8_t* P = lds + (s & 1) * X::kBuf;
+    const int jb = 4 * TT * wave + i;  // = (K-step TT + tile) 2 + plane
+    const int kt = jb >> 1;
+    const int64_t T = (int64_t)TT * tm + (kt % TT);
+    dma16(ra, P + jb * 1024, (u32)(lane * 16), (u32)((((T * nb + s) * 16 + kt / TT) * 2 + (jb & 1)) * 1024));
     if (i == 0 && wave < 4) {
       const int tt = wave & 1;
-      const int64_t Tb = 2 * (int64_t)tm + tt;
-      if (wave < 2) {
-        dma16(ra, P + kQDa + tt * 1024, (u32)(lane * 16), (u32)(codes_bytes + (Tb * nb + s) * 1024));
-      } else {
-        dma16(ra, P + kQC + tt * 1024, (u32)(lane * 16), (u32)(codes_bytes + da_bytes + (Tb * nb + s) * 1024));
+      const int64_t Tb = (int64_t)TT * tm + tt;
+      if (wave < TT) {
+        dma16(ra, P + X::kDa + tt * 1024, (u32)(lane * 16), (u32)(codes_bytes + (Tb * nb + s) * 1024));
+      } else if (wave >= 2 && wave < 2 + TT) {
+        dma16(ra, P + X::kC + tt * 1024, (u32)(lane * 16), (u32)(codes_bytes + da_bytes + (Tb * nb + s) * 1024));
       }
     }
   };
@@ -235,9 +243,9 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   auto ld_nib = [&](int s, int g) { return ld16(rq, vq + (u32)((s < nb ? s : nb - 1) * 8 + 2 * g) * 1024u); };
   auto ld_hdr = [&](int s) { return ld16(rh, vh + (u32)(s < nb ? s : nb - 1) * 1024u); };
 
-  v16f_t acc[2], S[2], T[2];
+  v16f_t acc[TT], S[TT], T[TT];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
+  for (int mt = 0; mt < TT; ++mt) {
     acc[mt] = v16f_t{};
     S[mt] = v16f_t{};
   }
@@ -248,7 +256,7 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   auto run_sb = [&](int s) {
     const bool next = s + 1 < sb1;
     hdr_n = ld_hdr(s + 1);
-    const uint8_t* P = lds + __builtin_amdgcn_readfirstlane((s & 1) * kQBuf);
+    const uint8_t* P = lds + __builtin_amdgcn_readfirstlane((s & 1) * X::kBuf);
     // this lane's weight row (get_scale_min_k4, quant_formats.h:62-70): sc_j as (sc, sc)
     // 16-bit pairs, m_j, d and dmin
     const u32 scA = hdr.y & 0x3F3F3F3Fu;
@@ -257,13 +265,13 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     const u32 mB = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
     const float ndm = -h2f(hdr.x >> 16);
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) T[tt] = v16f_t{};
+    for (int tt = 0; tt < TT; ++tt) T[tt] = v16f_t{};
     // mins product kk of tile tt: A = -dmin m_j of this lane's row, B = c of the lane's
     // activation row, K index hh: sub-block 2 kk + hh
     auto mins = [&](int tt, int kk) {
       const int j = 2 * kk + hh;
       const float am = ndm * (float)((j < 4 ? mA : mB) >> (8 * (j & 3)) & 0xFFu);
-      const float cv = as_f(lds4v(P + kQC + ((tt * 4 + kk) * 64 + lane) * 4));
+      const float cv = as_f(lds4v(P + X::kC + ((tt * 4 + kk) * 64 + lane) * 4));
       acc[tt] = mfma_f32_k2(am, cv, acc[tt]);
     };
     // weight operand of K-step k = 2 j + h: sc_j times 8 nibbles of two dwords, in the
@@ -283,35 +291,41 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
                  mul_bytes(x1 & 0x000F000Fu, sp), mul_bytes((x1 >> 8) & 0x000F000Fu, sp)};
     };
     // da_j of this lane's activation row in tile tt
-    auto ld_da = [&](int tt, int j) { return as_f(lds4v(P + kQDa + ((tt * 8 + j) * 32 + li) * 4)); };
-    float da[2];
+    auto ld_da = [&](int tt, int j) { return as_f(lds4v(P + X::kDa + ((tt * 8 + j) * 32 + li) * 4)); };
+    float da[TT];
     v4u w = build(0);
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       __builtin_amdgcn_s_setprio(2);
       if ((k & 1) == 0) {
-        // the sub-block's activation scales, used after its two K-steps; one of the
-        // super-block's 8 mins products: tile j / 4, pair j % 4
+        // the sub-block's activation scales, used after its two K-steps; the super-block's
+        // 4 TT mins products q = tile 4 + pair over the even K-steps (TT = 2: one per even
+        // K-step; 1: one every other)
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) da[tt] = ld_da(tt, k >> 1);
-        mins(k >> 3, (k >> 1) & 3);
+        for (int tt = 0; tt < TT; ++tt) da[tt] = ld_da(tt, k >> 1);
+        if (TT == 2) {
+          mins(k >> 3, (k >> 1) & 3);
+        } else if ((k & 3) == 0) {
+          mins(0, k >> 2);
+        }
       }
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const v4u alo = lds16(P + (((2 * k + tt) * 2) * 64 + lane) * 16);
-        const v4u ahi = lds16(P + (((2 * k + tt) * 2 + 1) * 64 + lane) * 16);
+      for (int tt = 0; tt < TT; ++tt) {
+        const v4u alo = lds16(P + (((TT * k + tt) * 2) * 64 + lane) * 16);
+        const v4u ahi = lds16(P + (((TT * k + tt) * 2 + 1) * 64 + lane) * 16);
         S[tt] = mfma_h(w, alo, (k & 1) == 0 ? v16f_t{} : S[tt]);
         S[tt] = mfma_h(w, ahi, S[tt]);
       }
       if (k < 15) w = build(k + 1);
-      if ((k & 1) == 0 && next) issue_piece(s + 1, k >> 1);
+      // the next super-block's 4 TT pieces of this wave, evenly over the K-steps
+      if (k % (4 / TT) == 0 && next) issue_piece(s + 1, k / (4 / TT));
       if ((k & 3) == 3) nib[k >> 2] = ld_nib(s + 1, k >> 2);
       __builtin_amdgcn_sched_barrier(0);
       if (k & 1) {
-        // sub-block j = k / 2 done: T += da_j sc_j P_j over the two tiles
+        // sub-block j = k / 2 done: T += da_j sc_j P_j over the tiles
         __builtin_amdgcn_s_setprio(0);
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
+        for (int tt = 0; tt < TT; ++tt) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) T[tt][r] = fmaf(da[tt], S[tt][r], T[tt][r]);
           asm volatile("" : "+v"(T[tt]));  // the sub-block's results exist here, not after later MFMAs
@@ -327,13 +341,13 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
       const int src = 8 * (r >> 2) + 4 * hh + (r & 3);
       const float dr = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * src, __builtin_bit_cast(int, d24)));
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) acc[tt][r] = fmaf(dr, T[tt][r], acc[tt][r]);
+      for (int tt = 0; tt < TT; ++tt) acc[tt][r] = fmaf(dr, T[tt][r], acc[tt][r]);
     }
   };
 
   // prologue: the first super-block's operands and weights
 #pragma unroll
-  for (int i = 0; i < 8; ++i) issue_piece(sb0, i);
+  for (int i = 0; i < 4 * TT; ++i) issue_piece(sb0, i);
   hdr = ld_hdr(sb0);
 #pragma unroll
   for (int g = 0; g < 4; ++g) nib[g] = ld_nib(sb0, g);
@@ -349,9 +363,9 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
   // ---- outputs (+ bias): activation row 32 mt + li, weight rows nbase + 32 wave +
   // 8 (r / 4) + 4 hh + r % 4 (four consecutive rows per r / 4)
-  const int64_t mrows = m - mbase < kQM ? m - mbase : kQM;
+  const int64_t mrows = m - mbase < 32 * TT ? m - mbase : 32 * TT;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
+  for (int mt = 0; mt < TT; ++mt) {
     const int row = 32 * mt + li;
     if (row >= mrows) continue;
     float* yr = y + (mbase + row) * ys;
@@ -402,9 +416,16 @@ hipError_t launch_act16i_from_q16(const uint8_t* acts, int64_t arb, int64_t m, i
   return hipGetLastError();
 }
 
+namespace {
+
+// Activation tiles per workgroup by rows: one for few rows, so no MFMA runs on padding.
+int q16_tt(int64_t m) { return m <= 32 ? 1 : 2; }
+
+}  // namespace
+
 int64_t q16_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {
-  const int64_t nbase0 = n0 / kRowGroup * kRowGroup;
-  const int64_t tiles_n = (n1 - nbase0 + kQN - 1) / kQN, tiles_m = (m + kQM - 1) / kQM;
+  const int64_t nbase0 = n0 / kRowGroup * kRowGroup, am = 32 * q16_tt(m);
+  const int64_t tiles_n = (n1 - nbase0 + kQN - 1) / kQN, tiles_m = (m + am - 1) / am;
   const int sp = split_ranges(tiles_n * tiles_m, w.cus > 0 ? w.cus : 256, w.nblk);
   return sp > 1 ? (int64_t)sp * m * kQN * tiles_n * 4 : 0;
 }
@@ -421,18 +442,28 @@ hipError_t launch_act16i_quant(const float* x, int64_t x_stride, int64_t m, int6
 hipError_t launch_gemm_q16(const WeightDev& w, const uint8_t* act, int64_t m, int64_t n0, int64_t n1, float* y,
                            int64_t ys, const float* bias, float* part, hipStream_t s) {
   if (!gemm_q16_ok(w, m, n0, n1)) return hipErrorInvalidValue;
+  const int tt = q16_tt(m);
   const int64_t nbase0 = n0 / kRowGroup * kRowGroup;
   const int64_t tiles_n = (n1 - nbase0 + kQN - 1) / kQN;
-  const int64_t tiles_m = (m + kQM - 1) / kQM;
+  const int64_t tiles_m = (m + 32 * tt - 1) / (32 * tt);
   const int nsplit = split_ranges(tiles_n * tiles_m, w.cus > 0 ? w.cus : 256, w.nblk);
   if (nsplit > 1 && (part == nullptr || m > 65535)) return hipErrorInvalidValue;
   const int xcd_map = tiles_n % 8 == 0 ? 1 : 0;
-  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_q4k_q16),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kQLds);
+  const void* fn = tt == 1 ? reinterpret_cast<const void*>(&k_gemm_q4k_q16<1>)
+                           : reinterpret_cast<const void*>(&k_gemm_q4k_q16<2>);
+  const int lds = tt == 1 ? QLds<1>::kTotal : QLds<2>::kTotal;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_gemm_q4k_q16, dim3((unsigned)(tiles_n * tiles_m * nsplit)), dim3(kQThreads), kQLds, s, w.plane[0],
-                     w.plane[1], (int)w.nblk, nbase0, w.n_pad, n0, n1, act, act16i_rows(m), m, y, ys, bias,
-                     (int)tiles_m, xcd_map, (int)tiles_n, nsplit, part);
+  const dim3 grid((unsigned)(tiles_n * tiles_m * nsplit));
+  if (tt == 1) {
+    hipLaunchKernelGGL(k_gemm_q4k_q16<1>, grid, dim3(kQThreads), lds, s, w.plane[0], w.plane[1], (int)w.nblk, nbase0,
+                       w.n_pad, n0, n1, act, act16i_rows(m), m, y, ys, bias, (int)tiles_m, xcd_map, (int)tiles_n,
+                       nsplit, part);
+  } else {
+    hipLaunchKernelGGL(k_gemm_q4k_q16<2>, grid, dim3(kQThreads), lds, s, w.plane[0], w.plane[1], (int)w.nblk, nbase0,
+                       w.n_pad, n0, n1, act, act16i_rows(m), m, y, ys, bias, (int)tiles_m, xcd_map, (int)tiles_n,
+                       nsplit, part);
+  }
   if (nsplit > 1) {
     const hipError_t e2 = hipGetLastError();
     if (e2 != hipSuccess) return e2;
