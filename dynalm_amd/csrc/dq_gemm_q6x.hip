@@ -520,18 +520,24 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   }
 }
 
-// y[r, n] = sum over the ranges, in range order, of part[range][r][n - nbase0] (+ bias[n]),
-// n in [n0, n1): one thread per output, rows in the grid's y dimension.
-__global__ __launch_bounds__(256) void k_split_sum(const float* __restrict__ part, int nsplit, int64_t m, int64_t W,
+// y[r, n] = sum over the N ranges, in range order, of part[range][r][n - nbase0] (+ bias[n]),
+// n in [n0, n1): one thread per output, rows in the grid's y dimension. N is a template
+// argument so that the N loads issue together before the first add.
+template <int N>
+__global__ __launch_bounds__(256) void k_split_sum(const float* __restrict__ part, int64_t m, int64_t W,
                                                  int64_t nbase0, int64_t n0, int64_t n1, float* __restrict__ y,
                                                  int64_t ys, const float* __restrict__ bias) {
   const int64_t n = n0 + (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t r = blockIdx.y;
   if (n >= n1) return;
   const float* p = part + r * W + (n - nbase0);
-  float v = p[0];
-  for (int i = 1; i < nsplit; ++i) v += p[(int64_t)i * m * W];
-  y[r * ys + n] = bias ? v + bias[n] : v;
+  float v[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = p[(int64_t)i * m * W];
+  float acc = v[0];
+#pragma unroll
+  for (int i = 1; i < N; ++i) acc += v[i];
+  y[r * ys + n] = bias ? acc + bias[n] : acc;
 }
 
 // ---------------------------------------------------------------- host
@@ -632,11 +638,28 @@ hipError_t launch_gemm_q6x(const WeightDev& w, int af, const uint8_t* act, int64
   return hipGetLastError();
 }
 
+namespace {
+
+template <int N>
+void split_sum_n(const float* part, int64_t m, int64_t W, int64_t nbase0, int64_t n0, int64_t n1, float* y,
+                 int64_t ys, const float* bias, hipStream_t s) {
+  hipLaunchKernelGGL(k_split_sum<N>, dim3((unsigned)((n1 - n0 + 255) / 256), (unsigned)m), dim3(256), 0, s, part, m,
+                     W, nbase0, n0, n1, y, ys, bias);
+}
+
+using SplitSumFn = void (*)(const float*, int64_t, int64_t, int64_t, int64_t, int64_t, float*, int64_t,
+                            const float*, hipStream_t);
+constexpr SplitSumFn kSplitSum[17] = {
+    nullptr,           &split_sum_n<1>,   &split_sum_n<2>,   &split_sum_n<3>,  &split_sum_n<4>,  &split_sum_n<5>,
+    &split_sum_n<6>,   &split_sum_n<7>,   &split_sum_n<8>,   &split_sum_n<9>,  &split_sum_n<10>, &split_sum_n<11>,
+    &split_sum_n<12>,  &split_sum_n<13>,  &split_sum_n<14>,  &split_sum_n<15>, &split_sum_n<16>};
+
+}  // namespace
+
 hipError_t launch_split_sum(const float* part, int nsplit, int64_t m, int64_t W, int64_t nbase0, int64_t n0,
                             int64_t n1, float* y, int64_t ys, const float* bias, hipStream_t s) {
-  if (m <= 0 || m > 65535 || n1 <= n0 || nsplit < 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_split_sum, dim3((unsigned)((n1 - n0 + 255) / 256), (unsigned)m), dim3(256), 0, s, part, nsplit,
-                     m, W, nbase0, n0, n1, y, ys, bias);
+  if (m <= 0 || m > 65535 || n1 <= n0 || nsplit < 1 || nsplit > 16) return hipErrorInvalidValue;
+  kSplitSum[nsplit](part, m, W, nbase0, n0, n1, y, ys, bias, s);
   return hipGetLastError();
 }
 
