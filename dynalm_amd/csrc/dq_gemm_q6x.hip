@@ -70,26 +70,33 @@ namespace dq {
 
 namespace {
 
-constexpr int kXM = 64, kXN = 128;  // activation rows x weight rows per workgroup
-constexpr int kXThreads = 256;      // 4 waves, one per SIMD
+constexpr int kXN = 128;        // weight rows per workgroup
+constexpr int kXThreads = 256;  // 4 waves, one per SIMD
 
-// Super-block buffer: activation codes [j (8)][h (int16: 2)][t (2)][lane (64)][16 B], then
-// the activation scales [t (2)][j (8)][row (32)].
-template <bool kI16>
+// Super-block buffer of a workgroup with TT 32-row activation tiles (TT = 2, or 1 for few
+// rows): activation codes [j (8)][h (int16: 2)][t (TT)][lane (64)][16 B], then the
+// activation scales [t (TT)][j (8)][row (32)].
+template <bool kI16, int TT>
 struct XLds {
   static constexpr int kH = kI16 ? 2 : 1;  // 1 KB pieces per block and tile
-  static constexpr int kCodes = 8 * kH * 2 * 1024;
+  static constexpr int kCodes = 8 * kH * TT * 1024;
   static constexpr int kDa = kCodes;
-  static constexpr int kBuf = kDa + 2048;
+  static constexpr int kBuf = kDa + TT * 1024;
   static constexpr int kTotal = 2 * kBuf;
 };
-static_assert(XLds<true>::kTotal <= 160 * 1024, "LDS");
+static_assert(XLds<true, 2>::kTotal <= 160 * 1024, "LDS");
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kPerm[8] = {0, 2, 1, 3, 4, 6, 5, 7};  // the K-step's value order
 
-int64_t q6x_rows(int64_t m) { return (m + kXM - 1) / kXM * kXM; }
+// Activation tiles per workgroup by rows: one for few rows, so no MFMA runs on padding.
+int q6x_tt(int64_t m) { return m <= 32 ? 1 : 2; }
+// Rows of the operand layout: whole workgroup tiles.
+int64_t q6x_rows(int64_t m) {
+  const int64_t am = 32 * q6x_tt(m);
+  return (m + am - 1) / am * am;
+}
 
 }  // namespace
 
@@ -198,16 +205,16 @@ __global__ __launch_bounds__(64) void k_q6x_quant(const float* __restrict__ x, i
 
 // ---------------------------------------------------------------- the GEMM
 
-// One workgroup: activation rows [64 tm, + 64) x weight rows [nbase0 + 128 tn, + 128),
+// One workgroup: activation rows [32 TT tm, + 32 TT) x weight rows [nbase0 + 128 tn, + 128),
 // super-blocks of range sp of nsplit. Arguments as launch_gemm_q6x; part: the ranges'
 // partial outputs [nsplit][m][W] (nsplit > 1), W = 128 tiles_n.
-template <bool kI16>
+template <bool kI16, int TT>
 __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_q6k_x(
     const uint8_t* __restrict__ ql_plane, const uint8_t* __restrict__ qh_plane, const uint8_t* __restrict__ sc_plane,
     const uint8_t* __restrict__ d_plane, int nb, int64_t nbase0, int64_t n_pad, int64_t n0, int64_t n1,
     const uint8_t* __restrict__ act, int64_t m_pad, int64_t m, float* __restrict__ y, int64_t ys,
     const float* __restrict__ bias, int tiles_m, int tiles_n, int nsplit, float* __restrict__ part) {
-  using X = XLds<kI16>;
+  using X = XLds<kI16, TT>;
   constexpr int kH = X::kH;
   extern __shared__ __align__(16) uint8_t lds[];
   const int t = threadIdx.x, lane = t & 63;
@@ -218,7 +225,7 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const int sp = __builtin_amdgcn_readfirstlane(L / tiles), Lt = L - sp * tiles;
   const int tn = __builtin_amdgcn_readfirstlane(Lt / tiles_m), tm = __builtin_amdgcn_readfirstlane(Lt - (Lt / tiles_m) * tiles_m);
   const int64_t nbase = nbase0 + (int64_t)kXN * tn;
-  const int64_t mbase = (int64_t)tm * kXM;
+  const int64_t mbase = (int64_t)tm * 32 * TT;
   const int sb0 = __builtin_amdgcn_readfirstlane(sp * nb / nsplit), sb1 = __builtin_amdgcn_readfirstlane((sp + 1) * nb / nsplit);
 
   const int64_t codes_bytes = m_pad * nb * 256 * kH, da_bytes = m_pad / 32 * nb * 1024;
@@ -228,20 +235,21 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const auto rs = rsrc(sc_plane, (u32)(n_pad * nb * 16));
   const auto rd = rsrc(d_plane, (u32)(n_pad * nb * 2));
 
-  // ---- this wave's loads. Codes of super-block s: pieces jb = 4 kH wave + i (i < 4 kH)
-  // of the buffer, jb = (j kH + h) 2 + tt; with piece 0 the activation scales of tile wave
-  // (waves 0, 1). The wave's weight row: group g0 + wave / 2, row 32 (wave & 1) + li.
+  // ---- this wave's loads. Codes of super-block s: pieces jb = 2 kH TT wave + i
+  // (i < 2 kH TT) of the buffer, jb = (j kH + h) TT + tt; with piece 0 the activation scales
+  // of tile wave (waves < TT). The wave's weight row: group g0 + wave / 2, row
+  // 32 (wave & 1) + li.
   const u32 g0 = (u32)(nbase >> 6);
   const u32 G = g0 + (u32)(wave >> 1), r64 = (u32)(32 * (wave & 1) + li);
-  constexpr int kPieces = 4 * kH;  // 1 KB pieces per wave and super-block
+  constexpr int kPieces = 2 * kH * TT;  // 1 KB pieces per wave and super-block
   auto issue_piece = [&](int s, int buf, int i) {
     uint8_t* P = lds + buf * X::kBuf;
     const int jb = kPieces * wave + i;
-    const int tt = jb & 1, jh = jb >> 1;  // jh = j kH + h
-    const int64_t T = 2 * (int64_t)tm + tt;
+    const int tt = jb % TT, jh = jb / TT;  // jh = j kH + h
+    const int64_t T = (int64_t)TT * tm + tt;
     dma16(ra, P + jb * 1024, (u32)(lane * 16), (u32)(((T * nb + s) * 8 * kH + jh) * 1024));
-    if (i == 0 && wave < 2) {
-      const int64_t Tb = 2 * (int64_t)tm + wave;
+    if (i == 0 && wave < TT) {
+      const int64_t Tb = (int64_t)TT * tm + wave;
       dma16(ra, P + X::kDa + wave * 1024, (u32)(lane * 16), (u32)(codes_bytes + (Tb * nb + s) * 1024));
     }
   };
@@ -307,9 +315,10 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     return __builtin_bit_cast(u32, v - h2_t{kOff, kOff});
   };
 
-  v16f_t acc[2], S[2], T[2];
+  // TT = 2: S[tt] is tile tt's block sum; TT = 1: S[j & 1] is block j's
+  v16f_t acc[TT], S[2], T[TT];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
+  for (int mt = 0; mt < TT; ++mt) {
     acc[mt] = v16f_t{};
     T[mt] = v16f_t{};
   }
@@ -318,13 +327,15 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   u32 d_n;
   v4u Ah[2][2], Al[2][2];  // [block parity][K-step h]: block j's operands, then block j + 1's
 
-  // Super-block s, per block j in two phases, each in a fixed issue order: tile tt's MFMA
-  // chain (K-steps 2 j, 2 j + 1; a_hi, a_lo) with a share of independent VALU work between
-  // consecutive MFMAs (B conversions, the other tile's fold, the next block's operand
-  // build), so that each MFMA's predecessor has finished when it issues and the matrix core
-  // runs beside the VALU. Phase 0: tile 0 beside the fold of tile 1's previous block and
-  // the next block's K-step 0 operands; phase 1: tile 1 beside the fold of tile 0's block j
-  // and the next block's K-step 1 operands.
+  // Super-block s, per block j in two phases (TT = 2), each in a fixed issue order: tile
+  // tt's MFMA chain (K-steps 2 j, 2 j + 1; a_hi, a_lo) with a share of independent VALU work
+  // between consecutive MFMAs (B conversions, the other tile's fold, the next block's
+  // operand build), so that each MFMA's predecessor has finished when it issues and the
+  // matrix core runs beside the VALU. Phase 0: tile 0 beside the fold of tile 1's previous
+  // block and the next block's K-step 0 operands; phase 1: tile 1 beside the fold of tile
+  // 0's block j and the next block's K-step 1 operands. TT = 1: one phase, the tile's chain
+  // into S[j & 1] beside the fold of block j - 1 (S[(j + 1) & 1]) and the next block's
+  // operands.
 #define SB() __builtin_amdgcn_sched_barrier(0)
   auto run_sb = [&](int s) {
     const bool next = s + 1 < sb1;
@@ -333,7 +344,7 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     const uint8_t* P = lds + __builtin_amdgcn_readfirstlane((s & 1) * X::kBuf);
     auto ld_da = [&](int tt, int j) { return as_f(lds4v(P + X::kDa + ((tt * 8 + j) * 32 + li) * 4)); };
     // the codes of block j, tile tt (int16: K-step h); int16 reads both K-steps
-    auto ld_x = [&](int j, int tt, int h) { return lds16(P + ((((j * kH + h) * 2) + tt) * 64 + lane) * 16); };
+    auto ld_x = [&](int j, int tt, int h) { return lds16(P + ((((j * kH + h) * TT) + tt) * 64 + lane) * 16); };
     auto fold = [&](int tt, float da, int r0) {
 #pragma unroll
       for (int r = r0; r < r0 + 8; ++r) T[tt][r] = fmaf(da, S[tt][r], T[tt][r]);
@@ -344,6 +355,83 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     for (int j = 0; j < 8; ++j) {
       const int jn = (j + 1) & 7, c = j & 1, cn = c ^ 1;
       const Unit un = unit(j < 7 ? w.sc : sc_n, jn);
+      if constexpr (TT == 1) {
+        const float daj = ld_da(0, j);
+        // prefetch block j + 1's codes
+        v4u ya = xa, yb = xb;
+        if (j < 7) {
+          ya = ld_x(j + 1, 0, 0);
+          yb = kI16 ? ld_x(j + 1, 0, 1) : ya;
+        }
+        const bool do_fold = j > 0;
+        auto foldp = [&](int r0) {
+#pragma unroll
+          for (int r = r0; r < r0 + 8; ++r) T[0][r] = fmaf(da1p, S[cn][r], T[0][r]);
+        };
+        if (kI16) {
+          v4u bl0 = {b16lo(xa[0]), b16lo(xa[1]), b16lo(xa[2]), b16lo(xa[3])};
+          SB();
+          S[c] = mfma_h(Ah[c][0], bl0, v16f_t{});
+          SB();
+          v4u bh0 = {b16hi(xa[0]), b16hi(xa[1]), b16hi(xa[2]), b16hi(xa[3])};
+          SB();
+          S[c] = mfma_h(Al[c][0], bl0, S[c]);
+          SB();
+          v4u bl1 = {b16lo(xb[0]), b16lo(xb[1]), b16lo(xb[2]), b16lo(xb[3])};
+          if (do_fold) foldp(0);
+          SB();
+          S[c] = mfma_h(Ah[c][0], bh0, S[c]);
+          SB();
+          v4u bh1 = {b16hi(xb[0]), b16hi(xb[1]), b16hi(xb[2]), b16hi(xb[3])};
+          SB();
+          S[c] = mfma_h(Al[c][0], bh0, S[c]);
+          SB();
+          if (do_fold) {
+            foldp(8);
+            asm volatile("" : "+v"(T[0]));  // the fold happens here, not where T is next read
+          }
+          SB();
+          S[c] = mfma_h(Ah[c][1], bl1, S[c]);
+          SB();
+          build(w, un, jn, 0, Ah[cn][0], Al[cn][0]);
+          SB();
+          S[c] = mfma_h(Al[c][1], bl1, S[c]);
+          SB();
+          build(w, un, jn, 1, Ah[cn][1], Al[cn][1]);
+          SB();
+          S[c] = mfma_h(Ah[c][1], bh1, S[c]);
+          SB();
+          S[c] = mfma_h(Al[c][1], bh1, S[c]);
+          SB();
+        } else {
+          v4u b0 = {b8(xa[0], 0x04010400u), b8(xa[0], 0x04030402u), b8(xa[1], 0x04010400u), b8(xa[1], 0x04030402u)};
+          SB();
+          S[c] = mfma_h(Ah[c][0], b0, v16f_t{});
+          SB();
+          v4u b1 = {b8(xa[2], 0x04010400u), b8(xa[2], 0x04030402u), b8(xa[3], 0x04010400u), b8(xa[3], 0x04030402u)};
+          SB();
+          S[c] = mfma_h(Al[c][0], b0, S[c]);
+          SB();
+          if (do_fold) foldp(0);
+          SB();
+          S[c] = mfma_h(Ah[c][1], b1, S[c]);
+          SB();
+          if (do_fold) {
+            foldp(8);
+            asm volatile("" : "+v"(T[0]));
+          }
+          SB();
+          S[c] = mfma_h(Al[c][1], b1, S[c]);
+          SB();
+          build(w, un, jn, 0, Ah[cn][0], Al[cn][0]);
+          build(w, un, jn, 1, Ah[cn][1], Al[cn][1]);
+          SB();
+        }
+        xa = ya;
+        xb = yb;
+        // the scale of the block folded next
+        da1p = daj;
+      } else {
       float da[2];
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
@@ -425,6 +513,8 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
           xb = yb;
         }
       }
+      da1p = da[1];
+      }
       // chunks whose last read was this block's build: the next super-block's
       if (j == 2) {
         w.ql[0] = ld_ql(s + 1, 0);
@@ -436,20 +526,17 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         w.qh[1] = ld_qh(s + 1, 1);
       }
       // the next super-block's pieces into the other buffer (past the range: this one's
-      // again, unread): per-32 one per two blocks, int16 one per block
+      // again, unread), evenly over the blocks
       {
+        constexpr int kEvery = 8 / kPieces;
         const int sn = next ? s + 1 : s;
-        if (kI16) {
-          issue_piece(sn, (s + 1) & 1, j);
-        } else if ((j & 1) == 0) {
-          issue_piece(sn, (s + 1) & 1, j >> 1);
-        }
+        if (j % kEvery == 0) issue_piece(sn, (s + 1) & 1, j / kEvery);
       }
       SB();
-      da1p = da[1];
     }
+    // the last fold: tile 1's block 7 (TT = 2), block 7 (TT = 1)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) T[1][r] = fmaf(da1p, S[1][r], T[1][r]);
+    for (int r = 0; r < 16; ++r) T[TT - 1][r] = fmaf(da1p, S[1][r], T[TT - 1][r]);
     // acc += d 2^24 T (int16: d 2^48 T): d of the lane's 16 result rows 8 (r / 4) + 4 hh +
     // r % 4, which lanes 0-31 hold (one weight row each); T = 0
     const float dsc = h2f(w.d) * (kI16 ? 0x1p48f : 0x1p24f);
@@ -458,7 +545,7 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
       const int src = 8 * (r >> 2) + 4 * hh + (r & 3);
       const float dr = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * src, __builtin_bit_cast(int, dsc)));
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
+      for (int tt = 0; tt < TT; ++tt) {
         acc[tt][r] = fmaf(dr, T[tt][r], acc[tt][r]);
         T[tt][r] = 0.0f;
       }
@@ -493,10 +580,10 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
   // ---- outputs: activation row 32 mt + li, weight rows nbase + 32 wave + 8 (r / 4) + 4 hh
   // + r % 4; with one range y (+ bias) in [n0, n1), else the range's partial tile
-  const int64_t mrows = m - mbase < kXM ? m - mbase : kXM;
+  const int64_t mrows = m - mbase < 32 * TT ? m - mbase : 32 * TT;
   const int64_t W = (int64_t)kXN * tiles_n;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
+  for (int mt = 0; mt < TT; ++mt) {
     const int row = 32 * mt + li;
     if (row >= mrows) continue;
     float* yr = y + (mbase + row) * ys;
@@ -553,8 +640,10 @@ Q6xGrid q6x_grid(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {
   Q6xGrid g;
   g.nbase0 = n0 / kRowGroup * kRowGroup;
   g.tiles_n = (n1 - g.nbase0 + kXN - 1) / kXN;
-  g.tiles_m = (m + kXM - 1) / kXM;
-  g.nsplit = split_ranges(g.tiles_n * g.tiles_m, w.cus > 0 ? w.cus : 256, w.nblk);
+  g.tiles_m = (m + 32 * q6x_tt(m) - 1) / (32 * q6x_tt(m));
+  // two workgroups fit a CU (4 waves, at most 68 KB of LDS): ranges for two per CU, so
+  // that each SIMD holds two waves to hide the other's waits
+  g.nsplit = split_ranges(g.tiles_n * g.tiles_m, 2 * (w.cus > 0 ? w.cus : 256), w.nblk);
   return g;
 }
 
@@ -614,22 +703,25 @@ hipError_t launch_gemm_q6x(const WeightDev& w, int af, const uint8_t* act, int64
   const Q6xGrid g = q6x_grid(w, m, n0, n1);
   if (g.nsplit > 1 && part == nullptr) return hipErrorInvalidValue;
   const int64_t mp = q6x_rows(m);
-  const bool i16 = af == kActQ16;
-  const void* fn = i16 ? reinterpret_cast<const void*>(&k_gemm_q6k_x<true>)
-                       : reinterpret_cast<const void*>(&k_gemm_q6k_x<false>);
-  const int lds = i16 ? XLds<true>::kTotal : XLds<false>::kTotal;
-  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-  if (e != hipSuccess) return e;
   const dim3 grid((unsigned)(g.tiles_n * g.tiles_m * g.nsplit));
-  if (i16) {
-    hipLaunchKernelGGL(k_gemm_q6k_x<true>, grid, dim3(kXThreads), lds, s, w.plane[0], w.plane[1], w.plane[2],
-                       w.plane[3], (int)w.nblk, g.nbase0, w.n_pad, n0, n1, act, mp, m, y, ys, bias, (int)g.tiles_m,
-                       (int)g.tiles_n, g.nsplit, part);
-  } else {
-    hipLaunchKernelGGL(k_gemm_q6k_x<false>, grid, dim3(kXThreads), lds, s, w.plane[0], w.plane[1], w.plane[2],
-                       w.plane[3], (int)w.nblk, g.nbase0, w.n_pad, n0, n1, act, mp, m, y, ys, bias, (int)g.tiles_m,
-                       (int)g.tiles_n, g.nsplit, part);
+  hipError_t e = hipSuccess;
+#define DQ_Q6X_LAUNCH(I16, TTV)                                                                                      \
+  {                                                                                                                  \
+    const int lds = XLds<I16, TTV>::kTotal;                                                                          \
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_q6k_x<I16, TTV>),                                 \
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lds);                                        \
+    if (e != hipSuccess) return e;                                                                                   \
+    hipLaunchKernelGGL((k_gemm_q6k_x<I16, TTV>), grid, dim3(kXThreads), lds, s, w.plane[0], w.plane[1], w.plane[2], \
+                       w.plane[3], (int)w.nblk, g.nbase0, w.n_pad, n0, n1, act, mp, m, y, ys, bias, (int)g.tiles_m,  \
+                       (int)g.tiles_n, g.nsplit, part);                                                              \
   }
+  const bool one = q6x_tt(m) == 1;
+  if (af == kActQ16) {
+    if (one) DQ_Q6X_LAUNCH(true, 1) else DQ_Q6X_LAUNCH(true, 2)
+  } else {
+    if (one) DQ_Q6X_LAUNCH(false, 1) else DQ_Q6X_LAUNCH(false, 2)
+  }
+#undef DQ_Q6X_LAUNCH
   if (g.nsplit > 1) {
     const hipError_t e2 = hipGetLastError();
     if (e2 != hipSuccess) return e2;

@@ -101,14 +101,15 @@ hipError_t launch_gemm_h16(const WeightDev& w, const uint8_t* act16, int64_t m, 
                            int64_t ys, const float* bias, hipStream_t s);
 
 // Split K for the tolerance-parity GEMMs (per-32 and int16 rows, dq_gemm_p32.hip,
-// dq_gemm_q16.hip, dq_gemm_q6x.hip): where a launch's tiles leave CUs idle, each tile's
-// super-blocks split into ranges (split_ranges: as many as fit one round of one workgroup
-// per CU, at least 2 super-blocks each, at most 16); every range writes its partial tile to
+// dq_gemm_q16.hip, dq_gemm_q6x.hip): where a launch's tiles leave workgroup slots idle,
+// each tile's super-blocks split into ranges (split_ranges: as many as fit one round of the
+// slots -- one workgroup per CU, two for the 4-wave Q6_K GEMM -- at least 2 super-blocks
+// each, at most 16); every range writes its partial tile to
 // part[range][m][W] and launch_split_sum adds the ranges in order (+ bias) into y's
 // [n0, n1), so the bits do not depend on timing.
-inline int split_ranges(int64_t tiles, int cus, int64_t nblk) {
-  if (tiles <= 0 || tiles >= cus) return 1;
-  int64_t sp = cus / tiles;
+inline int split_ranges(int64_t tiles, int slots, int64_t nblk) {
+  if (tiles <= 0 || tiles >= slots) return 1;
+  int64_t sp = slots / tiles;
   sp = sp < nblk / 2 ? sp : nblk / 2;
   sp = sp < 16 ? sp : 16;
   return sp > 1 ? (int)sp : 1;

@@ -13,7 +13,8 @@ north-star tolerance (per-32: 1e-4 relative, 1e-5 absolute) or to the int16 GEMV
 (int16: 2e-6 * sum |w_i x_i|; its terms reach 2^36 and cancel, so a bar relative to
 the output does not fit).
 
-Cases: 1, 5, 16 and 32 super-blocks, partial 64-row activation tiles, super-block ranges
+Cases: 1, 5, 16 and 32 super-blocks, workgroups of one 32-row activation tile (up to 32
+rows) and of two, whole and partial, super-block ranges
 (split K, 2 to 16 ranges) and none, a 128-row weight tile past the last row group
 (n = 1088), a row range cutting the first and last tiles, bias,
 the extreme weights w = 4096 (sc = -128, q = 0) and w = -3968 with codes of +-127
@@ -117,10 +118,20 @@ def _check(fmt: int, m: int, k: int, n: int, n0: int, n1: int, seed: int, extrem
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("m,k", [(5, 256), (16, 256), (67, 1280), (130, 4096), (20, 8192)])
 def test_q6x_gemm_superblock_counts(cuda, fmt, m, k):
-    """1, 5, 16 and 32 super-blocks; every m ends on a partial 64-row activation tile. With
+    """1, 5, 16 and 32 super-blocks; every m ends on a partial activation tile (32 rows up
+    to m = 32, else 64). With
     8 weight tiles the super-blocks split into ranges (2 at K=1280, 8 at K=4096, 16 at
     K=8192) whose partials a second launch adds."""
     _check(fmt, m, k, 1024, 0, 1024, 9600 + m + 7 * fmt)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("m", [1, 31, 32, 33])
+def test_q6x_gemm_tile_rows(cuda, fmt, m):
+    """Around the switch from one 32-row activation tile per workgroup (m <= 32) to two:
+    one row, a partial and a whole single tile, and a second tile with one row; 8 weight
+    tiles, each in 8 super-block ranges."""
+    _check(fmt, m, 4096, 1024, 0, 1024, 9650 + m + 7 * fmt)
 
 
 @pytest.mark.parametrize("fmt", FMTS)
@@ -153,8 +164,9 @@ def test_q6x_gemm_stress(cuda, fmt):
 
 @pytest.mark.parametrize("fmt", FMTS)
 def test_q6x_gemm_down_shape(cuda, fmt):
-    """Config 3's FFN down shape (K=14336, N=4096) at M=512: 256 workgroups over 56
-    super-blocks; 192 sampled columns against the exact product and the oracle."""
+    """Config 3's FFN down shape (K=14336, N=4096) at M=512: 256 tiles, each in two ranges
+    of 28 super-blocks (two workgroups per CU); 192 sampled columns against the exact
+    product and the oracle."""
     import dqtorch as T
 
     m, k, n = 512, 14336, 4096
