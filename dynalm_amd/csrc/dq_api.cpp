@@ -117,21 +117,22 @@ int scratch_get(int device, size_t need, void** out) { return scratch_get(g_scra
 
 constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
-// Rows from which Q4_K x int16 runs the f16 GEMM (dq_gemm_q16.hip, split K where its
-// tiles leave CUs idle) instead of the int16 GEMV's passes of up to 4 rows, each of which
-// reads the weight once. Measured (graph replay, dq_gemm vs dq_gemv on the same rows),
-// K = 4096, N = 14336: 6 rows 30.0 vs 30.2 us, 16 rows 30.9 vs 57.2, 64 rows 36.6 vs
-// 223; N = 4096 (K = 4096 / 14336): 6 rows 19.7 / 35.1 vs 25.5 / 40.3.
-constexpr int64_t kQ16GemmMinRows = 6;
-// Rows from which Q4_K x per-32 runs the f16 GEMM (dq_gemm_p32.hip, split K) instead of
-// the per-32 GEMV's passes (fused quantization up to 8 rows): K = 4096, N = 14336: 12
-// rows 35.6 vs 30.8 us, 16 rows 35.4 vs 36.5, 64 rows 39.6 vs 136; N = 4096 (K = 4096
-// / 14336): 12 rows 21.9 / 39.9 vs 27.1 / 54.7.
-constexpr int64_t kP32GemmMinRows = 12;
-// Rows from which Q6_K x per-32 / int16 runs the f16 GEMM (dq_gemm_q6x.hip, split K where
-// its tiles leave CUs idle) instead of the GEMV passes (measured, K = 4096 / 14336: level
-// at 4 rows, 1.5x faster at 6).
-constexpr int64_t kQ6xGemmMinRows = 5;
+// Rows from which dq_matmul_act runs the f16 GEMMs (split K where their tiles leave CUs
+// idle; one 32-row activation tile per workgroup up to 32 rows) instead of the GEMV
+// passes, which read the weight once per pass of up to 4 rows. Measured per call, fp32
+// rows in (graph replay; GEMV route / GEMM route, the latter's quantization fused into
+// the operand layout):
+//  - Q4_K x int16 (dq_gemm_q16.hip): 5 rows 27.8 / 24.3 us at K = 4096, N = 14336,
+//    25.1 / 16.3 at N = 4096, 36.8 / 26.3 at K = 14336, N = 4096; at 4 rows mixed
+//    (20.6 / 24.5, 17.6 / 15.7, 26.0 / 24.9);
+//  - Q4_K x per-32 (dq_gemm_p32.hip): 5 rows 22.5 / 21.2, 18.5 / 13.2, 32.6 / 21.5;
+//    4 rows 15.8 / 21.0, 13.4 / 14.5, 21.2 / 21.7; 10 rows 50.5 / 21.5 at K = 14336;
+//  - Q6_K x per-32 / int16 (dq_gemm_q6x.hip): 3 rows per-32 24.6 / 23.8 at K = 14336,
+//    N = 4096, 16.2 / 12.6 at K = 4096, N = 4096, 15.5 / 11.7 at N = 1024; int16 26.2 /
+//    26.7, 17.2 / 13.9, 16.3 / 12.8; 2 rows 20.9 / 23.8 at K = 14336.
+constexpr int64_t kQ16GemmMinRows = 5;
+constexpr int64_t kP32GemmMinRows = 5;
+constexpr int64_t kQ6xGemmMinRows = 3;
 
 // Per-(device, stream) workspaces of the public entry points whose kernels need device
 // memory beyond their arguments (dq_gemm's f16 activation operands). Each stream has
@@ -301,14 +302,11 @@ int check_out(const dq_weight* w, int64_t m, int64_t n0, int64_t n1, float* y, i
 bool use_gemm(const dq::WeightDev& w, int fmt, int64_t m) {
   if (!dq::gemm_supported(w.dtype, fmt)) return false;
   if (w.dtype == DQ_Q8_0 || w.dtype == DQ_Q4_0) return m >= 13;
-  // Q4_K x per-32: the 128-row f16 GEMM against GEMV passes of 4 rows, which read the
-  // weights once per pass (the GEMM takes about as long as 10 passes at N = 14336)
-  // Q6_K x per-32 / int16: the f16 GEMM against GEMV passes of up to 4 (8) rows
+  // K-quants x per-32 / int16: the f16 GEMMs against GEMV passes of up to 4 rows
   if (w.dtype == DQ_Q6_K && (fmt == DQ_ACT_PER32 || fmt == DQ_ACT_Q16)) {
     return m >= kQ6xGemmMinRows && dq::gemm_q6x_ok(w, fmt, m, 0, w.n);
   }
   if (fmt == DQ_ACT_PER32) return m >= kP32GemmMinRows && dq::gemm_p32_ok(w, m, 0, w.n);
-  // Q4_K x int16: the 64-row f16 GEMM against GEMV passes of 4 rows
   if (fmt == DQ_ACT_Q16) return m >= kQ16GemmMinRows && dq::gemm_q16_ok(w, m, 0, w.n);
   if (w.dtype == DQ_Q6_K) {
     return m > dq::kSkinnyMaxRows ||

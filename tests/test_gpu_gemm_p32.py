@@ -1,6 +1,6 @@
 """GPU parity of the Q4_K x per-32 GEMM on the f16 matrix cores (dq_gemm_p32.hip), qmm's
 int8 gemm contract: dq_gemm on DQ_ACT_PER32 rows, dq_matmul_act(DQ_ACT_PER32) and
-dq_qmm_gemm in int8 mode send Q4_K from 12 rows to it (split K where its tiles leave
+dq_qmm_gemm in int8 mode send Q4_K from 5 rows to it (split K where its tiles leave
 CUs idle).
 
 Its per-sub-block integers P_j are exact; the fp32 terms are summed in an order of
@@ -95,6 +95,14 @@ def test_p32_split_ranges(cuda):
     """20 rows on 8 weight tiles (K = 4096): each tile's 16 super-blocks split into 8
     ranges whose partials a second launch adds in order; dq_gemm on the per-32 rows."""
     _check(20, 4096, 2048, 0, 2048, 6150)
+
+
+@pytest.mark.parametrize("m", [5, 32, 33, 64, 65])
+def test_p32_tile_rows(cuda, m):
+    """Around the switches from one 32-row activation tile per workgroup (m <= 32) to two
+    (m <= 64) and four: dq_matmul_act's first GEMM row count, whole tiles and one row past
+    them; 8 weight tiles, each in 8 super-block ranges."""
+    _check(m, 4096, 2048, 0, 2048, 6160 + m)
 
 
 def test_p32_row_range(cuda):

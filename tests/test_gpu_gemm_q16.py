@@ -2,7 +2,7 @@
 int16 contract (ActBlockQ16 rows: int16 codes, one scale and one code sum per 32
 values; dynacore/cpu/avx2/kernels_avx2.cpp:1631-1729) through dq_gemm on DQ_ACT_Q16
 rows, dq_matmul_act(DQ_ACT_Q16) on fp32 rows and dq_qmm_gemm in int16 mode, which
-take it from 6 rows (split K where its tiles leave CUs idle).
+take it from 5 rows (split K where its tiles leave CUs idle).
 
 The integers sc_j P_j are rounded to fp32 where they pass 2^24 and the fp32 terms are
 summed in an order of the kernel's own, so it is held to the reference's bound against
@@ -91,8 +91,17 @@ def _check(m: int, k: int, n: int, n0: int, n1: int, seed: int, saturate: bool =
 
 @pytest.mark.parametrize("m,k", [(24, 256), (67, 1280), (130, 4096)])
 def test_q16_gemm_superblock_counts(cuda, m, k):
-    """1, 5 and 16 super-blocks; 24, 67 and 130 rows end on partial 64-row tiles."""
+    """1, 5 and 16 super-blocks; 24, 67 and 130 rows end on partial activation tiles
+    (32 rows per workgroup up to 32 rows, else 64)."""
     _check(m, k, 1024, 0, 1024, 9100 + m)
+
+
+@pytest.mark.parametrize("m", [5, 32, 33])
+def test_q16_gemm_tile_rows(cuda, m):
+    """Around the switch from one 32-row activation tile per workgroup (m <= 32) to two:
+    dq_matmul_act's first GEMM row count, a whole single tile, a second tile with one
+    row; 8 weight tiles, each in 8 super-block ranges."""
+    _check(m, 4096, 2048, 0, 2048, 9150 + m)
 
 
 def test_q16_gemm_row_range(cuda):

@@ -1,7 +1,7 @@
 """GPU parity of the Q6_K GEMM on the f16 matrix cores (dq_gemm_q6x.hip) for qmm's two
 contracts: per-32 rows (the int8 contract, qmm_reference.cpp:68-93 with Fmt<kQ6_K>) and
 int16 rows (ActBlockQ16, kernels_avx2.cpp:1661-1765), through dq_gemm on the block rows,
-dq_matmul_act on fp32 rows (which takes it from 5 rows) and dq_qmm_gemm.
+dq_matmul_act on fp32 rows (which takes it from 3 rows) and dq_qmm_gemm.
 
 The weight w = sc (q - 32) is split exactly into two f16 operands (fh (q - 32) and
 fl (q - 32), sc = fh + fl), so the per-block integers are exact (per-32; int16: rounded to
@@ -37,7 +37,7 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 FMTS = [O.ACT_PER32, O.ACT_Q16]
-MIN_ROWS = 5  # dq_matmul_act's GEMM threshold for Q6_K x per-32 / int16
+MIN_ROWS = 3  # dq_matmul_act's GEMM threshold for Q6_K x per-32 / int16
 
 
 def dev(a: np.ndarray):

@@ -922,7 +922,7 @@ Q16_AVX2 = [O.Q8_0, O.Q4_K, O.Q6_K]  # the types with a reference AVX2 int16 ker
 def test_gemv_q16_parity(cuda, t, m):
     """int16 GEMV: within the reference's bound of the exact product and of the oracle;
     integer unit partials bit-exact; dq_matmul_act (GPU quantization) gives the same bits
-    as its kernel on the same rows (the GEMV; for Q6_K from 5 rows and Q4_K from 6 the f16
+    as its kernel on the same rows (the GEMV; for Q6_K from 3 rows and Q4_K from 5 the f16
     GEMM)."""
     import dqtorch as T
 
@@ -941,7 +941,7 @@ def test_gemv_q16_parity(cuda, t, m):
     want_u, _ = O.partials(t, O.ACT_Q16, rows, a, k)
     assert np.array_equal(host(units), want_u)
     ya = host(T.matmul_act(w, O.ACT_Q16, dev(x)))
-    gemm_route = (t == O.Q6_K and m >= 5) or (t == O.Q4_K and m >= 6)  # dq_matmul_act's GEMM thresholds
+    gemm_route = (t == O.Q6_K and m >= 3) or (t == O.Q4_K and m >= 5)  # dq_matmul_act's GEMM thresholds
     same = host(T.gemm(w, O.ACT_Q16, dev(a))) if gemm_route else y
     assert np.array_equal(ya.view(np.uint32), same.view(np.uint32))
 

@@ -110,7 +110,7 @@ def test_ffn_down_plan_int16(cuda, t):
 def test_engine_qmm_plan(cuda, t, m):
     """The engine's plan on a backend with accelerated qmm (int8 rows unbounded,
     dynalm/src/runtime/engine.cpp:365-375): qmm's gemm on per-32 rows from 9 rows (Q4_K:
-    the f16 GEMM above 64 rows, Q6_K: from 5 rows, GEMV passes below); the same bits as
+    the f16 GEMM above 64 rows, Q6_K: from 3 rows, GEMV passes below); the same bits as
     the per-32 contract's own path, within tolerance of the oracle."""
     import dqtorch as T
 
