@@ -34,7 +34,8 @@
 // over the K-steps, into a ring of two; one barrier per super-block.
 //
 // Activation layout ("act32", k_act32_from_p32 from per-32 rows), for M_pad = m
-// rounded up to 128 rows (zero rows past m), T = M_pad / 32 row tiles, nb super-blocks:
+// rounded up to the workgroup's 32 TT rows (zero rows past m), T = M_pad / 32 row
+// tiles, nb super-blocks:
 //   codes  [T][nb][k (16)][lane (64)][8 halves]  lane l: row 32 T + l % 32, half
 //          hh = l / 32; K-step k = 2 j + h holds values 32 j + 16 hh + 8 h + {0, 2, 1,
 //          3, 4, 6, 5, 7} of the super-block (sub-block j only)
@@ -58,7 +59,7 @@ namespace dq {
 
 namespace {
 
-constexpr int kPM = 128, kPN = 256;  // activation rows x weight rows per workgroup
+constexpr int kPN = 256;  // weight rows per workgroup (activation rows: 32 TT)
 constexpr int kPThreads = 512;       // 8 waves, two per SIMD
 // Super-block buffer: operands [k (16)][t (4)][lane (64)][16 B], then the activation
 // scales [t (4)][j (8)][row (32)] and the mins operands [t (4)][kk (4)][lane (64)].
@@ -373,7 +374,18 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
 // ---------------------------------------------------------------- host
 
-int64_t act32_rows(int64_t m) { return (m + kPM - 1) / kPM * kPM; }
+namespace {
+
+// Activation tiles per workgroup by rows: fewer for few rows, so no MFMA runs on padding.
+int p32_tt(int64_t m) { return m <= 32 ? 1 : m <= 64 ? 2 : 4; }
+
+}  // namespace
+
+// Rows of the act32 layout: whole workgroup tiles (32 p32_tt(m) rows).
+int64_t act32_rows(int64_t m) {
+  const int64_t am = 32 * p32_tt(m);
+  return (m + am - 1) / am * am;
+}
 
 int64_t act32_bytes(int64_t m, int64_t k) {
   const int64_t mp = act32_rows(m), nb = k / 256;
@@ -404,13 +416,6 @@ hipError_t launch_act32_quant(const float* x, int64_t x_stride, int64_t m, int64
   hipLaunchKernelGGL(k_act32_quant, dim3((unsigned)(k / 256), (unsigned)mp), dim3(64), 0, s, x, x_stride, m, k, mp, out);
   return hipGetLastError();
 }
-
-namespace {
-
-// Activation tiles per workgroup by rows: fewer for few rows, so no MFMA runs on padding.
-int p32_tt(int64_t m) { return m <= 32 ? 1 : m <= 64 ? 2 : 4; }
-
-}  // namespace
 
 int64_t p32_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {
   const int64_t nbase0 = n0 / kRowGroup * kRowGroup, am = 32 * p32_tt(m);

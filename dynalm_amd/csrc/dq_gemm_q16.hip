@@ -29,7 +29,8 @@
 // two (the 128-row tile of the per-32 GEMM would need twice the LDS).
 //
 // Activation layout ("act16i", k_act16i_from_q16 from ActBlockQ16 rows), for M_pad =
-// m rounded up to 64 rows (zero rows past m), T = M_pad / 32 row tiles, nb super-blocks:
+// m rounded up to the workgroup's 32 TT rows (zero rows past m), T = M_pad / 32 row
+// tiles, nb super-blocks:
 //   codes  [T][nb][k (16)][p (2)][lane (64)][8 halves]  p = 0: lo, p = 1: 256 hi; lane
 //          l: row 32 T + l % 32, half hh = l / 32; K-step k = 2 j + h holds values
 //          32 j + 16 hh + 8 h + {0, 2, 1, 3, 4, 6, 5, 7} of the super-block
@@ -50,7 +51,7 @@ namespace dq {
 
 namespace {
 
-constexpr int kQM = 64, kQN = 256;  // activation rows x weight rows per workgroup
+constexpr int kQN = 256;  // weight rows per workgroup (activation rows: 32 TT)
 constexpr int kQThreads = 512;      // 8 waves, two per SIMD
 // Super-block buffer: operands [k (16)][t (2)][p (2)][lane (64)][16 B], then the
 // activation scales [t (2)][j (8)][row (32)] and the mins operands [t (2)][kk (4)][lane (64)].
@@ -391,7 +392,18 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
 // ---------------------------------------------------------------- host
 
-int64_t act16i_rows(int64_t m) { return (m + kQM - 1) / kQM * kQM; }
+namespace {
+
+// Activation tiles per workgroup by rows: one for few rows, so no MFMA runs on padding.
+int q16_tt(int64_t m) { return m <= 32 ? 1 : 2; }
+
+}  // namespace
+
+// Rows of the act16i layout: whole workgroup tiles (32 q16_tt(m) rows).
+int64_t act16i_rows(int64_t m) {
+  const int64_t am = 32 * q16_tt(m);
+  return (m + am - 1) / am * am;
+}
 
 int64_t act16i_bytes(int64_t m, int64_t k) {
   const int64_t mp = act16i_rows(m), nb = k / 256;
@@ -415,13 +427,6 @@ hipError_t launch_act16i_from_q16(const uint8_t* acts, int64_t arb, int64_t m, i
                      (int)(k / 256), mp, out);
   return hipGetLastError();
 }
-
-namespace {
-
-// Activation tiles per workgroup by rows: one for few rows, so no MFMA runs on padding.
-int q16_tt(int64_t m) { return m <= 32 ? 1 : 2; }
-
-}  // namespace
 
 int64_t q16_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {
   const int64_t nbase0 = n0 / kRowGroup * kRowGroup, am = 32 * q16_tt(m);
