@@ -408,6 +408,36 @@ def pmc_leg(weights, x, acts, y, stream) -> None:
     log("pmc leg done")
 
 
+def pmc_f16_leg(stream) -> None:
+    """Launches for the counter passes of the f16 GEMMs on the per-32 and int16 contracts
+    (dq_matmul_act): the copy kernel first (calibration), then three calls each of Q6_K
+    K=14336 N=4096 (config 3's down projection) per-32 and int16 at M=512 and per-32 at
+    M=16, and Q4_K K=4096 N=14336 int16 at M=512 and per-32 at M=16."""
+    import torch
+
+    import dynalm_amd as dq
+
+    src = torch.ones(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    for name, t, n, k, cases in (
+            ("q6_K", dq.Q6_K, 4096, 14336, ((512, "per32"), (512, "int16"), (16, "per32"))),
+            ("q4_K", dq.Q4_K, 14336, 4096, ((512, "int16"), (16, "per32")))):
+        rows = random_rows(t, n, k, 5)
+        w = dq.Weight.upload(t, rows, k)
+        for m, fname in cases:
+            fmt = dq.ACT_PER32 if fname == "per32" else dq.ACT_Q16
+            log(f"pmc f16 leg: {name} x {fname}, m={m}")
+            x = torch.randn((m, k), device="cuda")
+            y = torch.empty((m, n), device="cuda")
+            for _ in range(3):
+                dq.matmul_act(w, fmt, x, m, k, y, n, None, stream)
+            torch.cuda.synchronize()
+        w.free()
+    log("pmc f16 leg done")
+
+
 def ceilings(steps: int, warmup: int) -> dict:
     """The two ceilings the headline kernels are quoted against, measured here with
     libdqceil.so (dynalm_amd/csrc/dq_ceiling.hip): the decode GEMV's loads alone
@@ -539,6 +569,10 @@ def main() -> None:
     ap.add_argument("--pmc-leg", action="store_true",
                     help="no timing: a 64 MiB copy kernel (counter calibration), then a few launches of each "
                          "measured kernel, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--pmc-f16-leg", action="store_true",
+                    help="no timing: a 64 MiB copy kernel, then three calls each of the per-32 / int16 f16 GEMMs "
+                         "(Q6_K down projection at M=512 and 16, Q4_K at M=512 int16 and M=16 per-32), for "
+                         "rocprofv3 --pmc passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path would shard the weight "
@@ -576,6 +610,9 @@ def main() -> None:
 
     if args.pmc_leg:
         pmc_leg(weights, x, acts, y, stream)
+        return
+    if args.pmc_f16_leg:
+        pmc_f16_leg(stream)
         return
 
     log(f"decode step x{args.steps} (warmup {args.warmup})")

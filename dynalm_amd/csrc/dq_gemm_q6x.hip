@@ -223,7 +223,19 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const int L = blockIdx.x;
   const int tiles = tiles_m * tiles_n;
   const int sp = __builtin_amdgcn_readfirstlane(L / tiles), Lt = L - sp * tiles;
-  const int tn = __builtin_amdgcn_readfirstlane(Lt / tiles_m), tm = __builtin_amdgcn_readfirstlane(Lt - (Lt / tiles_m) * tiles_m);
+  // Workgroups are dealt to the 8 XCDs round-robin: with tiles_n a multiple of 8, the
+  // activation tiles of one weight tile go to one XCD, so they share its L2's copy of the
+  // weight rows.
+  int tn, tm;
+  if (tiles_n % 8 == 0) {
+    tn = 8 * (Lt / (8 * tiles_m)) + (Lt & 7);
+    tm = (Lt >> 3) % tiles_m;
+  } else {
+    tn = Lt / tiles_m;
+    tm = Lt - tn * tiles_m;
+  }
+  tn = __builtin_amdgcn_readfirstlane(tn);
+  tm = __builtin_amdgcn_readfirstlane(tm);
   const int64_t nbase = nbase0 + (int64_t)kXN * tn;
   const int64_t mbase = (int64_t)tm * 32 * TT;
   const int sb0 = __builtin_amdgcn_readfirstlane(sp * nb / nsplit), sb1 = __builtin_amdgcn_readfirstlane((sp + 1) * nb / nsplit);
