@@ -23,30 +23,32 @@
 // The order is not the reference's: the outputs agree within the fp32 tolerance of a
 // K-term dot product, not bit for bit.
 //
-// Work split. A workgroup owns 64 activation rows x 128 weight rows with 4 waves, and a
-// range of super-blocks; wave w owns weight rows 32 w .. 32 w + 31 (lane l builds row
-// l % 32's operands for lane half hh = l / 32 from the Q6_K planes it loads itself)
-// against the two 32-row activation tiles. Where the tiles alone leave CUs idle (small m,
-// few weight rows) the super-blocks split into up to 16 ranges, one workgroup each, whose
-// partial outputs a second launch adds in range order (deterministic). 256 workgroups at
-// config 3's down shape (M = 512, N = 4096): one wave per SIMD, so a wave overlaps its own
-// work. Per block, tile 0's MFMA chain runs beside the fold of tile 1's previous block and
-// half of the next block's operand build, then tile 1's chain beside the fold of tile 0's
-// block and the other half. A super-block's activation codes (16 KB per-32, 32 KB int16)
-// and scales (2 KB) go to LDS one interval ahead by direct-to-LDS loads spread over the
+// Work split. A workgroup owns 32 TT activation rows (TT = 2 tiles of 32, or 1 up to 32
+// rows) x 128 weight rows with 4 waves, and a range of super-blocks; wave w owns weight
+// rows 32 w .. 32 w + 31 (lane l builds row l % 32's operands for lane half hh = l / 32
+// from the Q6_K planes it loads itself) against the activation tiles. Where the tiles
+// leave workgroup slots idle (two per CU) the super-blocks split into up to 16 ranges, one
+// workgroup each, whose partial outputs a second launch adds in range order
+// (deterministic). A wave overlaps its own MFMAs and VALU work: per block, tile 0's MFMA
+// chain runs beside the fold of tile 1's previous block and half of the next block's
+// operand build, then tile 1's chain beside the fold of tile 0's block and the other half
+// (TT = 1: the tile's chain beside the fold of its previous block and the whole build). A
+// super-block's activation codes (16 KB per tile) and scales (1 KB per tile) go to LDS one interval ahead by direct-to-LDS loads spread over the
 // blocks, into a ring of two; each weight plane chunk is reloaded for the next
-// super-block right after its last read. The codes stay narrow in LDS and become f16 B
-// operands in registers, because each CU's reads (the tile's weights and activation rows)
-// bound the kernel at this shape: ~20 KB/us per CU.
+// super-block right after its last read. The per-32 codes are f16 B operands in LDS
+// already (2 B per value: the kernel is bound by VALU issue, and converting narrow codes
+// in registers cost 16 VALU per tile and block); the int16 codes stay 16-bit there and
+// become their two f16 operands in registers (as f16 pairs they would take 4 B per value,
+// twice the LDS, and leave room for one workgroup per CU).
 //
-// Activation layouts (written from the quantized rows by k_q6x_act), for M_pad = m rounded
-// up to 64 rows (zero rows past m), T = M_pad / 32 row tiles and nb super-blocks; lane l is
-// row 32 T + l % 32, half hh = l / 32, and K-step k = 2 j + h of a lane half takes values
-// 32 j + 16 hh + 8 h + {0, 2, 1, 3, 4, 6, 5, 7} of the super-block (the weight operand's
-// order: packed 16-bit lanes take bytes (0, 2) and (1, 3) of a dword):
-//   per-32 ("act8")  codes [T][nb][j (8)][lane (64)][16 B]: bytes 8 h + i = code + 128 of
-//                    K-step 2 j + h's value i (f16 in registers: 0x6400 | byte = 1024 + byte,
-//                    minus 1152)
+// Activation layouts (written from the quantized rows by k_q6x_act / k_q6x_quant), for
+// M_pad = m rounded up to the workgroup's 32 TT rows (zero rows past m), T = M_pad / 32 row
+// tiles and nb super-blocks; lane l is row 32 T + l % 32, half hh = l / 32, and K-step
+// k = 2 j + h of a lane half takes values 32 j + 16 hh + 8 h + {0, 2, 1, 3, 4, 6, 5, 7} of
+// the super-block (the weight operand's order: packed 16-bit lanes take bytes (0, 2) and
+// (1, 3) of a dword):
+//   per-32 ("act8h") codes [T][nb][j (8)][h (2)][lane (64)][8 x f16]: the int8 code of
+//                    value i as f16 (exact)
 //   int16 ("act16b") codes [T][nb][j (8)][h (2)][lane (64)][8 x u16]: v + 32768 of value i;
 //                    the B operands are lo = v & 255 as raw f16 bits (the subnormal
 //                    lo 2^-24) and 256 hi 2^-24 = hi 2^-16 through 0x2400 | (hi + 128)
@@ -78,7 +80,7 @@ constexpr int kXThreads = 256;  // 4 waves, one per SIMD
 // activation scales [t (TT)][j (8)][row (32)].
 template <bool kI16, int TT>
 struct XLds {
-  static constexpr int kH = kI16 ? 2 : 1;  // 1 KB pieces per block and tile
+  static constexpr int kH = 2;  // 1 KB pieces per block and tile (one per K-step)
   static constexpr int kCodes = 8 * kH * TT * 1024;
   static constexpr int kDa = kCodes;
   static constexpr int kBuf = kDa + TT * 1024;
@@ -102,13 +104,13 @@ int64_t q6x_rows(int64_t m) {
 
 // ---------------------------------------------------------------- layout writer
 
-// Per-32 rows (40 B per 32 values: float d, int32 code sum, int8 codes[32]) -> act8, or
+// Per-32 rows (40 B per 32 values: float d, int32 code sum, int8 codes[32]) -> act8h, or
 // ActBlockQ16 rows (72 B: float d, int32 sum, int16 codes[32]) -> act16b. Workgroup
 // (s, T): one 32-row tile's super-block s; rows past m are zeros (codes 0 stored biased).
 template <bool kI16>
 __global__ __launch_bounds__(256) void k_q6x_act(const uint8_t* __restrict__ acts, int64_t arb, int64_t m, int nb,
                                                  int64_t m_pad, uint8_t* __restrict__ out) {
-  constexpr int kH = kI16 ? 2 : 1, kBlk = kI16 ? 72 : 40;
+  constexpr int kH = 2, kBlk = kI16 ? 72 : 40;
   const int t = threadIdx.x;
   const int s = blockIdx.x;
   const int64_t T = blockIdx.y;
@@ -117,7 +119,7 @@ __global__ __launch_bounds__(256) void k_q6x_act(const uint8_t* __restrict__ act
   for (int e = 0; e < 2 * kH; ++e) {
     // unit u = ((j, h), lane) of the (T, s) block: 16 bytes
     const int u = t + 256 * e, l = u & 63, hh = l >> 5;
-    const int j = kI16 ? (u >> 7) : (u >> 6), h0 = kI16 ? ((u >> 6) & 1) : 0;
+    const int j = u >> 7, h0 = (u >> 6) & 1;
     const int64_t row = 32 * T + (l & 31);
     u32 o[4];
     if (row < m) {
@@ -129,19 +131,13 @@ __global__ __launch_bounds__(256) void k_q6x_act(const uint8_t* __restrict__ act
           o[i] = (u32)(uint16_t)(q[kPerm[2 * i]] + 32768) | ((u32)(uint16_t)(q[kPerm[2 * i + 1]] + 32768) << 16);
         }
       } else {
-        const int8_t* q = reinterpret_cast<const int8_t*>(b) + 16 * hh;
+        const int8_t* q = reinterpret_cast<const int8_t*>(b) + 16 * hh + 8 * h0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int h = i >> 1, i0 = 4 * (i & 1);
-          u32 w = 0;
-#pragma unroll
-          for (int c = 0; c < 4; ++c) w |= (u32)(uint8_t)(q[8 * h + kPerm[i0 + c]] + 128) << (8 * c);
-          o[i] = w;
-        }
+        for (int i = 0; i < 4; ++i) o[i] = f16_pair(q[kPerm[2 * i]], q[kPerm[2 * i + 1]]);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = kI16 ? 0x80008000u : 0x80808080u;
+      for (int i = 0; i < 4; ++i) o[i] = kI16 ? 0x80008000u : 0u;
     }
     *reinterpret_cast<v4u*>(out + ((((T * nb + s) * 8 + j) * kH + h0) * 64 + l) * 16) = v4u{o[0], o[1], o[2], o[3]};
   }
@@ -154,15 +150,15 @@ __global__ __launch_bounds__(256) void k_q6x_act(const uint8_t* __restrict__ act
   }
 }
 
-// fp32 rows -> act8 / act16b directly, with the standalone quantizers' arithmetic
+// fp32 rows -> act8h / act16b directly, with the standalone quantizers' arithmetic
 // (per32_quant / q16_quant: the layout equals k_q6x_act's of the rows they write). One
-// wave per (super-block, padded row); lane l quantizes values 4 l .. 4 l + 3. per-32: lane
-// e = 8 j + 4 hh writes block j's unit of lane half hh from lanes e .. e + 3; int16: even
-// lane e = 8 j + 4 hh + 2 h writes K-step 2 j + h's unit with lane e + 1's codes.
+// wave per (super-block, padded row); lane l = 8 j + 4 hh + 2 h + p quantizes values
+// 4 l .. 4 l + 3, the half p of K-step 2 j + h's unit of lane half hh. per-32: each lane
+// writes its half; int16: even lanes write the unit with lane l + 1's codes.
 template <bool kI16>
 __global__ __launch_bounds__(64) void k_q6x_quant(const float* __restrict__ x, int64_t x_stride, int64_t m, int64_t k,
                                                   int64_t m_pad, uint8_t* __restrict__ out) {
-  constexpr int kH = kI16 ? 2 : 1;
+  constexpr int kH = 2;
   const int l = threadIdx.x;
   const int s = blockIdx.x;
   const int64_t row = blockIdx.y;
@@ -190,15 +186,12 @@ __global__ __launch_bounds__(64) void k_q6x_quant(const float* __restrict__ x, i
     }
   } else {
     const u32 c = per32_quant(v, d, sum);
-    // bytes {0, 2, 1, 3} of lanes e .. e + 3, plus 128
-    auto ord = [](u32 w) { return __builtin_amdgcn_perm(0u, w, 0x03010200u) ^ 0x80808080u; };
-    const u32 c1 = (u32)__builtin_amdgcn_ds_bpermute(4 * ((l + 1) & 63), (int)c);
-    const u32 c2 = (u32)__builtin_amdgcn_ds_bpermute(4 * ((l + 2) & 63), (int)c);
-    const u32 c3 = (u32)__builtin_amdgcn_ds_bpermute(4 * ((l + 3) & 63), (int)c);
-    if ((l & 3) == 0) {
-      *reinterpret_cast<v4u*>(out + ((((T * nb + s) * 8 + j)) * 64 + 32 * hh + r) * 16) =
-          v4u{ord(c), ord(c1), ord(c2), ord(c3)};
-    }
+    // this lane's values 4 l .. 4 l + 3 as f16 pairs (0, 2), (1, 3): half p = l & 1 of
+    // K-step h = (l >> 1) & 1's unit
+    const int h = (l >> 1) & 1, p = l & 1;
+    auto code = [&](int i) { return (int)(int8_t)(c >> (8 * i)); };
+    *reinterpret_cast<v2u*>(out + ((((T * nb + s) * 8 + j) * 2 + h) * 64 + 32 * hh + r) * 16 + 8 * p) =
+        v2u{f16_pair(code(0), code(2)), f16_pair(code(1), code(3))};
   }
   if ((l & 7) == 0) reinterpret_cast<float*>(out + codes_bytes + (T * nb + s) * 1024)[j * 32 + r] = d;
 }
@@ -313,12 +306,7 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
       lo[2 * e + 1] = __builtin_bit_cast(u32, __builtin_elementwise_fma(q13, u.fl, u.cl));
     }
   };
-  // B operands from the narrow codes. per-32: a dword of biased codes (bytes: values
-  // (0, 2), (1, 3) of a pair of K-step slots) -> two f16 pairs 1024 + byte - 1152.
-  auto b8 = [](u32 x, u32 sel) -> u32 {
-    const h2_t v = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, x, sel));
-    return __builtin_bit_cast(u32, v - h2_t{(_Float16)1152.0f, (_Float16)1152.0f});
-  };
+  // B operands. per-32: the layout's f16 codes as they are.
   // int16: a dword of two biased codes -> (lo_a, lo_b) 2^-24 and (hi_a, hi_b) 2^-16
   auto b16lo = [](u32 x) -> u32 { return __builtin_amdgcn_perm(0u, x, 0x0C020C00u); };
   auto b16hi = [](u32 x) -> u32 {
@@ -362,7 +350,7 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
       for (int r = r0; r < r0 + 8; ++r) T[tt][r] = fmaf(da, S[tt][r], T[tt][r]);
     };
     float da1p = 0.0f;
-    v4u xa = ld_x(0, 0, 0), xb = kI16 ? ld_x(0, 0, 1) : xa;  // this phase's codes
+    v4u xa = ld_x(0, 0, 0), xb = ld_x(0, 0, 1);  // this phase's codes (K-steps 0, 1)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int jn = (j + 1) & 7, c = j & 1, cn = c ^ 1;
@@ -373,7 +361,7 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         v4u ya = xa, yb = xb;
         if (j < 7) {
           ya = ld_x(j + 1, 0, 0);
-          yb = kI16 ? ld_x(j + 1, 0, 1) : ya;
+          yb = ld_x(j + 1, 0, 1);
         }
         const bool do_fold = j > 0;
         auto foldp = [&](int r0) {
@@ -416,11 +404,9 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
           S[c] = mfma_h(Al[c][1], bh1, S[c]);
           SB();
         } else {
-          v4u b0 = {b8(xa[0], 0x04010400u), b8(xa[0], 0x04030402u), b8(xa[1], 0x04010400u), b8(xa[1], 0x04030402u)};
+          const v4u b0 = xa, b1 = xb;
           SB();
           S[c] = mfma_h(Ah[c][0], b0, v16f_t{});
-          SB();
-          v4u b1 = {b8(xa[2], 0x04010400u), b8(xa[2], 0x04030402u), b8(xa[3], 0x04010400u), b8(xa[3], 0x04030402u)};
           SB();
           S[c] = mfma_h(Al[c][0], b0, S[c]);
           SB();
@@ -455,10 +441,10 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         v4u ya, yb;
         if (tt == 0) {
           ya = ld_x(j, 1, 0);
-          yb = kI16 ? ld_x(j, 1, 1) : ya;
+          yb = ld_x(j, 1, 1);
         } else if (j < 7) {
           ya = ld_x(j + 1, 0, 0);
-          yb = kI16 ? ld_x(j + 1, 0, 1) : ya;
+          yb = ld_x(j + 1, 0, 1);
         }
         const int ot = tt ^ 1;  // the tile folded in this phase
         const bool do_fold = tt == 1 || j > 0;
@@ -498,11 +484,9 @@ __global__ __launch_bounds__(kXThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
           S[tt] = mfma_h(Al[c][1], bh1, S[tt]);
           SB();
         } else {
-          v4u b0 = {b8(xa[0], 0x04010400u), b8(xa[0], 0x04030402u), b8(xa[1], 0x04010400u), b8(xa[1], 0x04030402u)};
+          const v4u b0 = xa, b1 = xb;
           SB();
           S[tt] = mfma_h(Ah[c][0], b0, v16f_t{});
-          SB();
-          v4u b1 = {b8(xa[2], 0x04010400u), b8(xa[2], 0x04030402u), b8(xa[3], 0x04010400u), b8(xa[3], 0x04030402u)};
           SB();
           S[tt] = mfma_h(Al[c][0], b0, S[tt]);
           SB();
@@ -662,8 +646,9 @@ Q6xGrid q6x_grid(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {
 }  // namespace
 
 int64_t q6x_act_bytes(int af, int64_t m, int64_t k) {
+  (void)af;  // per-32 and int16 layouts: 2 B per value
   const int64_t mp = q6x_rows(m), nb = k / 256;
-  return mp * nb * 256 * (af == kActQ16 ? 2 : 1) + mp / 32 * nb * 1024;
+  return mp * nb * 256 * 2 + mp / 32 * nb * 1024;
 }
 
 int64_t q6x_part_bytes(const WeightDev& w, int64_t m, int64_t n0, int64_t n1) {

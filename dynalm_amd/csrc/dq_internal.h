@@ -144,8 +144,9 @@ hipError_t launch_act16i_quant(const float* x, int64_t x_stride, int64_t m, int6
 hipError_t launch_gemm_q16(const WeightDev& w, const uint8_t* act, int64_t m, int64_t n0, int64_t n1, float* y,
                            int64_t ys, const float* bias, float* part, hipStream_t s);
 // The Q6_K GEMM on the f16 matrix cores (dq_gemm_q6x.hip) for per-32 rows (af =
-// kActPer32) and int16 rows (kActQ16): launch_q6x_act writes the rows' narrow operand
-// layout (q6x_act_bytes), launch_gemm_q6x runs 64 x 128 tiles over it. Where the tiles
+// kActPer32) and int16 rows (kActQ16): launch_q6x_act writes the rows' operand layout
+// (q6x_act_bytes: per-32 codes as f16, int16 codes biased to u16), launch_gemm_q6x runs
+// 32- or 64-row x 128-row tiles over it. Where the tiles
 // leave CUs idle, each tile's super-blocks split into ranges whose partial outputs go to
 // part (q6x_part_bytes; 0: no split, part may be null) and a second launch adds them in
 // range order. gemm_q6x_ok: Q6_K, one of those formats, 32-bit offsets.
