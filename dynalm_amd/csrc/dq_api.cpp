@@ -887,8 +887,8 @@ int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
     });
   }
   if (w->dev.dtype == DQ_Q6_K && (fmt == DQ_ACT_PER32 || fmt == DQ_ACT_Q16)) {
-    // Q6_K x per-32 / int16: the narrow operand layout (one launch), then the f16 GEMM (and
-    // the sum of its range partials)
+    // Q6_K x per-32 / int16: the operand layout (one launch), then the f16 GEMM (and the sum
+    // of its range partials)
     if (!dq::gemm_q6x_ok(w->dev, fmt, m, n0, n1)) return fail(DQ_UNSUPPORTED, "m too large");
     const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
     const size_t lay = round256((size_t)dq::q6x_act_bytes(fmt, m, w->dev.k));

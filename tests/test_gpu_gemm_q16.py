@@ -14,7 +14,8 @@ order keeps the products and the mins term as two sums that cancel, each carryin
 ~1e-5 of fp32 rounding at K = 4096 for outputs of order 1, so two correct orders
 differ by more than 1e-5 absolute near zero.
 
-Cases: 1, 5 and 16 super-blocks, partial 64-row activation tiles, a row range cutting
+Cases: 1, 5 and 16 super-blocks, partial and whole 32- and 64-row activation tiles
+(dq_matmul_act's first GEMM row count included), a row range cutting
 the first and last 256-row weight tiles, bias, saturated scales and codes of +-32767,
 the reference's edge blocks, and both writers' routes (dq_gemm on int16 rows,
 dq_matmul_act on fp32 rows), which must agree bit for bit.
