@@ -245,8 +245,11 @@ DQ_API int dq_matmul_noalloc(const dq_weight* w, const float* x, int64_t m, int6
 /* y = x . w^T (+ bias) with the activations quantized to format fmt (the caller's
  * choice of dynacore's activation contract, which KernelPlan makes per matmul:
  * dynacore/include/dynacore/kernel/kernel_plan.h:50-92). One quantize launch into
- * the per-device scratch, then dq_gemv (dq_gemm where it supports the pair at this
- * m, as dq_matmul chooses). Replaces Device::matmul under a chosen contract. */
+ * the per-device scratch, then dq_gemv, or dq_gemm's kernel where it supports the pair
+ * and is faster at this m: for DQ_ACT_PER32 / DQ_ACT_Q16 the f16 GEMMs take Q4_K from 5
+ * rows and Q6_K from 3, their quantization writing the GEMM's operand layout directly;
+ * below that, DQ_ACT_PER32 on Q4_K / Q6_K quantizes inside the GEMV launch (the same
+ * bits as dq_act_quantize + dq_gemv). Replaces Device::matmul under a chosen contract. */
 DQ_API int dq_matmul_act(const dq_weight* w, int fmt, const float* x, int64_t m, int64_t x_stride, float* y,
                          int64_t y_stride, const float* bias, void* stream);
 
