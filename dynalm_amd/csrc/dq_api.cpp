@@ -296,9 +296,22 @@ int check_out(const dq_weight* w, int64_t m, int64_t n0, int64_t n1, float* y, i
 // 18; quantize + GEMM 26.9 / 32.7 at 13, 27.0 / 32.4 at 18; at K = 14336 the two are
 // equal at 13 rows, 81.7 vs 82.8 us); Q6_K x Q8_K above 64 rows, and above
 // 16 where the skinny GEMV's LDS does not hold the row's super-blocks (K = 14336:
-// 110 us against 171-611 us for 17..64 rows) or the weight has 4096 rows or more (the
+// 110 us against 171-611 us for the VALU GEMV's passes at 17..64 rows; but see
+// skinny_passes16) or the weight has 4096 rows or more (the
 // GEMM's grid fills the CUs: 35 vs 45 us at K = 4096, N = 14336; with N = 1536 it
 // loses, 70 vs 23 us).
+// Q6_K x Q8_K rows too long for the 64-row skinny tiles' LDS: the 16-row skinny launch
+// per 16 rows (one read of the weight each) instead of the GEMM, while those passes read
+// the weight fewer than ~4 times over 4096 rows. K = 14336, graph replay, quantization
+// included: N = 4096 at 24 / 48 / 64 rows 37.8 / 59.5 / 79.4 us against 114-116 for the
+// GEMM, whose few tiles leave most CUs idle; N = 8192 at 24 rows 66.6 against 115.9, at 48
+// 112.6 against 115.5; N = 14336 at 24 rows 118.1 against 120.7, at 64 256.3 against 117.4.
+bool skinny_passes16(const dq::WeightDev& w, int fmt, int64_t m) {
+  return w.dtype == DQ_Q6_K && fmt == DQ_ACT_Q8_K && m > DQ_GEMV_MAX_ROWS && m <= dq::kSkinnyMaxRows &&
+         !dq::gemv_mma_lds_ok(w.nblk, m) && dq::gemv_mma_lds_ok(w.nblk, DQ_GEMV_MAX_ROWS) &&
+         (m + DQ_GEMV_MAX_ROWS - 1) / DQ_GEMV_MAX_ROWS * w.n <= 16384;
+}
+
 bool use_gemm(const dq::WeightDev& w, int fmt, int64_t m) {
   if (!dq::gemm_supported(w.dtype, fmt)) return false;
   if (w.dtype == DQ_Q8_0 || w.dtype == DQ_Q4_0) return m >= 13;
@@ -309,6 +322,7 @@ bool use_gemm(const dq::WeightDev& w, int fmt, int64_t m) {
   if (fmt == DQ_ACT_PER32) return m >= kP32GemmMinRows && dq::gemm_p32_ok(w, m, 0, w.n);
   if (fmt == DQ_ACT_Q16) return m >= kQ16GemmMinRows && dq::gemm_q16_ok(w, m, 0, w.n);
   if (w.dtype == DQ_Q6_K) {
+    if (skinny_passes16(w, fmt, m)) return false;
     return m > dq::kSkinnyMaxRows ||
            (m > DQ_GEMV_MAX_ROWS && (!dq::gemv_mma_lds_ok(w.nblk, m) || w.n >= 4096));
   }
@@ -449,6 +463,23 @@ int matmul_impl(const dq_weight* w, const float* x, int64_t m, int64_t x_stride,
     // the kernel when that is cheap, else after one quantize launch)
     std::vector<GemvJob> j{GemvJob{&w->dev, nullptr, 0, x, m > 1 ? x_stride : w->dev.k, m, y, y_stride, bias}};
     return run_skinny(j, w->dev.device, s, r);
+  }
+  if (skinny_passes16(w->dev, fmt, m)) {
+    // long Q6_K rows at 17..64 rows: the skinny route per 16 rows of x (its quantized rows
+    // and split t-terms in the region when one is given; a last single row on the M = 1
+    // route). Every route gives the same bits.
+    for (int64_t r0 = 0; r0 < m; r0 += DQ_GEMV_MAX_ROWS) {
+      const int64_t rows = m - r0 < DQ_GEMV_MAX_ROWS ? m - r0 : DQ_GEMV_MAX_ROWS;
+      const float* xr = x + r0 * x_stride;
+      float* yr = y + r0 * y_stride;
+      if (rows == 1 || !skinny_ok(w, xr, rows, x_stride)) {
+        if (int rc = matmul_impl(w, xr, rows, x_stride, yr, y_stride, bias, s, r); rc != DQ_OK) return rc;
+        continue;
+      }
+      std::vector<GemvJob> j{GemvJob{&w->dev, nullptr, 0, xr, x_stride, rows, yr, y_stride, bias}};
+      if (int rc = run_skinny(j, w->dev.device, s, r); rc != DQ_OK) return rc;
+    }
+    return DQ_OK;
   }
   void* stream = static_cast<void*>(s);
   if (m > 1 && gemv_mma_supported(w->dev.dtype, fmt, 2) && !use_gemm(w->dev, fmt, m)) {
@@ -817,11 +848,14 @@ int dq_gemv(const dq_weight* w, int fmt, const void* acts, int64_t m, int64_t n0
   if (int rc = check_acts(w, fmt, acts, m); rc != DQ_OK) return rc;
   if (int rc = check_out(w, m, n0, n1, y, y_stride); rc != DQ_OK) return rc;
   if (m == 0 || n0 == n1) return DQ_OK;
-  const int64_t pass = fmt == DQ_ACT_SX ? dq::kSkinnySxMaxRows : dq::kSkinnyMaxRows;
+  // passes of up to 64 rows (sub-scaled: 16); 16 where the 64-row tiles' LDS does not hold
+  // the row's super-blocks
+  int64_t pass = fmt == DQ_ACT_SX ? dq::kSkinnySxMaxRows : dq::kSkinnyMaxRows;
+  if (m > DQ_GEMV_MAX_ROWS && !dq::gemv_mma_lds_ok(w->dev.nblk, m < pass ? m : pass)) pass = DQ_GEMV_MAX_ROWS;
   if (m >= 2 && dq::gemv_mma_supported(w->dev.dtype, fmt, 2) && dq::gemv_mma_lds_ok(w->dev.nblk, m < pass ? m : pass) &&
       (fmt != DQ_ACT_SX || dq::skinny_sx_pays(w->dev, m < pass ? m : pass, n0, n1))) {
-    // K-quants x Q8_K / sub-scaled: the skinny MFMA GEMV in passes of up to 64 (16)
-    // rows (a last single row goes to the M = 1 GEMV)
+    // K-quants x Q8_K / sub-scaled: the skinny MFMA GEMV in passes of `pass` rows (a last
+    // single row goes to the M = 1 GEMV)
     const int64_t arb = dq_act_row_bytes(fmt, w->dev.k);
     const uint8_t* a = static_cast<const uint8_t*>(acts);
     for (int64_t r0 = 0; r0 < m; r0 += pass) {

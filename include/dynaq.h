@@ -222,7 +222,9 @@ DQ_API int dq_gemm(const dq_weight* w, int fmt, const void* acts, int64_t m, int
 /* y = x . w^T (+ bias): quantize x with dq_act_format_for(w), then GEMV or GEMM by
  * m (Q4_K: GEMM above DQ_GEMV_MAX_ROWS, or above 48 rows for weights of <= 4096 rows;
  * Q8_0 / Q4_0: GEMM from 13 rows; Q6_K: GEMM
- * above 64 rows, or above 16 for weights of >= 4096 rows or long K). Replaces Device::matmul
+ * above 64 rows, or above 16 for weights of >= 4096 rows or long K, except long rows on
+ * weights of few rows, which run the 16-row skinny GEMV per 16 rows). Every route gives
+ * the same bits. Replaces Device::matmul
  * (dynacore/include/dynacore/device/device.h:161; CpuDevice::matmul,
  * dynacore/cpu/cpu_device.cpp:869-1177). Uses a per-device scratch buffer. */
 DQ_API int dq_matmul(const dq_weight* w, const float* x, int64_t m, int64_t x_stride, float* y, int64_t y_stride,
