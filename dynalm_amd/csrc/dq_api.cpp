@@ -300,16 +300,22 @@ int check_out(const dq_weight* w, int64_t m, int64_t n0, int64_t n1, float* y, i
 // skinny_passes16) or the weight has 4096 rows or more (the
 // GEMM's grid fills the CUs: 35 vs 45 us at K = 4096, N = 14336; with N = 1536 it
 // loses, 70 vs 23 us).
-// Q6_K x Q8_K rows too long for the 64-row skinny tiles' LDS: the 16-row skinny launch
-// per 16 rows (one read of the weight each) instead of the GEMM, while those passes read
-// the weight fewer than ~4 times over 4096 rows. K = 14336, graph replay, quantization
-// included: N = 4096 at 24 / 48 / 64 rows 37.8 / 59.5 / 79.4 us against 114-116 for the
-// GEMM, whose few tiles leave most CUs idle; N = 8192 at 24 rows 66.6 against 115.9, at 48
-// 112.6 against 115.5; N = 14336 at 24 rows 118.1 against 120.7, at 64 256.3 against 117.4.
+// K-quant x Q8_K rows too long for the 64-row skinny tiles' LDS: the 16-row skinny launch
+// per 16 rows (one read of the weight each) instead of the GEMM where that is faster.
+// Graph replay, quantization included, K = 14336:
+//  - Q6_K, while the passes read the weight fewer than ~4 times over 4096 rows: N = 4096 at
+//    24 / 48 / 64 rows 37.8 / 59.5 / 79.4 us against 114-116 for the int8 GEMM, whose few
+//    tiles leave most CUs idle; N = 8192 at 24 rows 66.6 against 115.9, at 48 112.6
+//    against 115.5; N = 14336 at 24 rows 118.1 against 120.7, at 64 256.3 against 117.4;
+//  - Q4_K, two passes on weights of at most 4096 rows: N = 4096 at 24 rows 30.8 against
+//    40.3 us (K = 11008: 26.5 against 31.9), at 48 48.3 against 42.0; N = 8192 at 24 rows
+//    53.9 against 41.7.
 bool skinny_passes16(const dq::WeightDev& w, int fmt, int64_t m) {
-  return w.dtype == DQ_Q6_K && fmt == DQ_ACT_Q8_K && m > DQ_GEMV_MAX_ROWS && m <= dq::kSkinnyMaxRows &&
-         !dq::gemv_mma_lds_ok(w.nblk, m) && dq::gemv_mma_lds_ok(w.nblk, DQ_GEMV_MAX_ROWS) &&
-         (m + DQ_GEMV_MAX_ROWS - 1) / DQ_GEMV_MAX_ROWS * w.n <= 16384;
+  if (fmt != DQ_ACT_Q8_K || m <= DQ_GEMV_MAX_ROWS || m > dq::kSkinnyMaxRows) return false;
+  if (dq::gemv_mma_lds_ok(w.nblk, m) || !dq::gemv_mma_lds_ok(w.nblk, DQ_GEMV_MAX_ROWS)) return false;
+  const int64_t passes = (m + DQ_GEMV_MAX_ROWS - 1) / DQ_GEMV_MAX_ROWS;
+  if (w.dtype == DQ_Q6_K) return passes * w.n <= 16384;
+  return w.dtype == DQ_Q4_K && passes <= 2 && w.n <= 4096;
 }
 
 bool use_gemm(const dq::WeightDev& w, int fmt, int64_t m) {
@@ -327,6 +333,7 @@ bool use_gemm(const dq::WeightDev& w, int fmt, int64_t m) {
            (m > DQ_GEMV_MAX_ROWS && (!dq::gemv_mma_lds_ok(w.nblk, m) || w.n >= 4096));
   }
   if (m > DQ_GEMV_MAX_ROWS && m <= 48 && w.n <= 4096 && dq::gemv_mma_lds_ok(w.nblk, m)) return false;
+  if (skinny_passes16(w, fmt, m)) return false;
   return m > DQ_GEMV_MAX_ROWS;
 }
 
@@ -465,7 +472,7 @@ int matmul_impl(const dq_weight* w, const float* x, int64_t m, int64_t x_stride,
     return run_skinny(j, w->dev.device, s, r);
   }
   if (skinny_passes16(w->dev, fmt, m)) {
-    // long Q6_K rows at 17..64 rows: the skinny route per 16 rows of x (its quantized rows
+    // long K-quant rows at 17..64 rows: the skinny route per 16 rows of x (its quantized rows
     // and split t-terms in the region when one is given; a last single row on the M = 1
     // route). Every route gives the same bits.
     for (int64_t r0 = 0; r0 < m; r0 += DQ_GEMV_MAX_ROWS) {

@@ -249,20 +249,22 @@ def test_matmul_q4k_route_17_to_48_rows(cuda, m, n, k):
     assert np.array_equal(ym[:, cols].view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("m,n,k", [(24, 4096, 14336), (40, 2048, 14336), (64, 1024, 11008), (33, 8192, 14336),
-                                   (17, 4096, 14336)])
-def test_matmul_q6k_long_rows_17_to_64(cuda, m, n, k):
-    """dq_matmul for 17..64 rows of Q6_K whose rows the 64-row skinny tiles' LDS does not
-    hold: the 16-row skinny route per 16 rows (N = 2048: with the split launch's t-terms;
-    a last single row on the M = 1 route) while it reads the weight fewer than ~4 times
-    over 4096 rows, else the GEMM (N = 8192 at 33 rows). Every route computes the
-    canonical order: the bits of quantize + dq_gemm, and sampled columns equal the
+@pytest.mark.parametrize("t,m,n,k", [(O.Q6_K, 24, 4096, 14336), (O.Q6_K, 40, 2048, 14336), (O.Q6_K, 64, 1024, 11008),
+                                     (O.Q6_K, 33, 8192, 14336), (O.Q6_K, 17, 4096, 14336), (O.Q4_K, 24, 4096, 14336),
+                                     (O.Q4_K, 32, 2048, 11008), (O.Q4_K, 40, 4096, 14336)])
+def test_matmul_long_rows_17_to_64(cuda, t, m, n, k):
+    """dq_matmul for 17..64 rows of K-quants whose rows the 64-row skinny tiles' LDS does
+    not hold: the 16-row skinny route per 16 rows (N = 2048: with the split launch's
+    t-terms; a last single row on the M = 1 route) where it beats the GEMM (Q6_K while it
+    reads the weight fewer than ~4 times over 4096 rows, Q4_K for two passes on at most
+    4096 rows), else the GEMM (Q6_K N = 8192 at 33 rows, Q4_K at 40). Every route computes
+    the canonical order: the bits of quantize + dq_gemm, and sampled columns equal the
     oracle."""
     import dqtorch as T
 
-    w_rows = gguf_weights(O.Q6_K, n, k, 90 + m + k, outlier_frac=0.01)
+    w_rows = gguf_weights(t, n, k, 90 + m + k + t, outlier_frac=0.01)
     x = activations(m, k, 91 + m)
-    w = dq.Weight.upload(O.Q6_K, w_rows, k)
+    w = dq.Weight.upload(t, w_rows, k)
     xd = dev(x)
     bias = O.normal(92 + m, n)
     ym = host(T.matmul(w, xd, bias=dev(bias)))
@@ -272,7 +274,7 @@ def test_matmul_q6k_long_rows_17_to_64(cuda, m, n, k):
     yv = host(T.gemv(w, O.ACT_Q8_K, ad, bias=dev(bias)))
     assert np.array_equal(yv.view(np.uint32), yg.view(np.uint32))
     cols = np.unique(np.concatenate([np.random.default_rng(m).choice(n, 48, replace=False), [0, n - 1]]))
-    want = O.matmul(O.Q6_K, O.ACT_Q8_K, w_rows[cols], O.quantize_act(O.ACT_Q8_K, x), k, bias=bias[cols])
+    want = O.matmul(t, O.ACT_Q8_K, w_rows[cols], O.quantize_act(O.ACT_Q8_K, x), k, bias=bias[cols])
     assert np.array_equal(ym[:, cols].view(np.uint32), want.view(np.uint32))
     w.free()
 
