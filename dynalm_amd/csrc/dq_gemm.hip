@@ -442,6 +442,8 @@ struct Big {
   static_assert(kPrep >= 1 && kTiles % kWaves == 0, "each wave unpacks whole tiles");
   static_assert(kBN % 64 == 0 && (8 * kGroups) % kWaves == 0, "staging roles");
   static_assert(kQ6 ? (4 * kGroups) % kWaves == 0 : kBM / 32 == kWaves, "staging roles");
+  static constexpr int kAJ = kBM / (4 * kWaves);  // activation-code instructions per wave (4 rows each)
+  static_assert(kBM % (16 * kWaves) == 0 && kAJ <= 8, "staging roles");
   static_assert(kLds <= 160 * 1024, "LDS");
 };
 
@@ -483,12 +485,13 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
   const auto rd6 = rsrc((kQ6 ? plane3 : qs_plane) + G0 * nb * 128, (u32)(gspan * nb * 128));
 
   // ---- staging roles (direct-to-LDS, per super-block)
-  // activation codes: wave w, instruction j fills rows 4 (8w + j) .. + 3; the
-  // per-lane part of the source offset repeats with period 4 in j
+  // activation codes: wave w, instruction j < kAJ fills rows kBM / kWaves w + 4 j .. + 3;
+  // the per-lane part of the source offset repeats with period 4 in j
+  constexpr int kAJ = C::kAJ, kAW = kBM / C::kWaves;
   u32 aoff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int row = 4 * (8 * wave + j) + (lane >> 4);
+    const int row = kAW * wave + 4 * j + (lane >> 4);
     aoff[j] = (u32)(row * arb + 4 + 16 * ((lane & 15) ^ (row & 15)));
   }
   // bsums: wave w fills rows 32 w .. 32 w + 31
@@ -496,8 +499,8 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
   constexpr int kWI = 8 * C::kGroups / C::kWaves;  // nibble instructions per wave
   auto issue = [&](int b) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      ld_lds16(ra, lds + kA + 4 * (8 * wave + j) * 256, aoff[j & 3], (u32)(b * 292 + (j >> 2) * 16 * arb));
+    for (int j = 0; j < kAJ; ++j) {
+      ld_lds16(ra, lds + kA + (kAW * wave + 4 * j) * 256, aoff[j & 3], (u32)(b * 292 + (j >> 2) * 16 * arb));
     }
     // nibbles: instruction i = kWI w + j stages chunk i / kGroups of 64-row group i % kGroups
 #pragma unroll
@@ -808,6 +811,13 @@ hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t 
     const int64_t wgs = (rows + 127) / 128 * ((m + 255) / 256);
     if (w.dtype == kQ6_K) {
       if (wgs * 8 >= (int64_t)cus * 7) return launch_big<kQ6_K, 4, 2, 4>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+      // 64 x 64 tiles (4 waves, each 64 activation rows x 16 weight rows) while they are one
+      // per CU at most: the 128 x 64 tiles would leave half the CUs idle or more (K = 14336,
+      // N = 4096: 96-98 against 113-121 us at 65..256 rows; at 384 rows, 384 of them took
+      // 140 against 123 us)
+      if ((rows + 63) / 64 * ((m + 63) / 64) <= cus) {
+        return launch_big<kQ6_K, 1, 4, 1>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+      }
       return launch_big<kQ6_K, 2, 2, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s);
     }
     if (wgs * 8 >= (int64_t)cus * 7) return launch_big<kQ4_K, 4, 2, 4>(w, acts, arb, m, n0, n1, y, ys, bias, s);

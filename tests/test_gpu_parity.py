@@ -1282,12 +1282,15 @@ def test_gemm_b32_row_range_and_saturated_codes(cuda):
 # ------------------------------------------------------------- Q6_K GEMM
 
 
-@pytest.mark.parametrize("m,n,k", [(65, 300, 512), (200, 128, 1280), (512, 256, 2048), (300, 14336, 256)])
+@pytest.mark.parametrize("m,n,k", [(65, 300, 512), (200, 128, 1280), (512, 256, 2048), (300, 14336, 256),
+                                   (100, 1100, 768), (448, 4096, 512)])
 def test_gemm_q6k_bit_exact(cuda, m, n, k):
     """Q6_K x Q8_K on the large GEMM kernels: w = sc (q - 32) split exactly into int8
     operands 64 wh + wl, S = 64 sum(wh a) + sum(wl a) per super-block, combined in the
     canonical order u = d (float)S, acc = fma(da, u, acc): bit-identical to the oracle and
-    to the GEMV (edge blocks: saturated and negative scales, d = 0)."""
+    to the GEMV (edge blocks: saturated and negative scales, d = 0). The 64 x 64 tiles
+    where they are one per CU at most (all but the last two cases; n = 1100 ends inside a
+    tile), the 256 x 128 tiles at n = 14336, the 128 x 64 tiles at 448 x 4096."""
     import dqtorch as T
 
     rows = weight_rows(O.Q6_K, n, k, 2200 + m, edge=True)
@@ -1304,8 +1307,9 @@ def test_gemm_q6k_bit_exact(cuda, m, n, k):
 
 def test_gemm_q6k_extreme_codes_and_route(cuda):
     """Saturated operands (codes 0 and 63, scales -128 and 127, activations +-127 and
-    -128-free Q8_K rows) stay exact; dq_matmul sends 40 rows at K = 14336 (whose super-
-    blocks do not fit the skinny kernel's LDS) to the GEMM, and 70 rows at any K."""
+    -128-free Q8_K rows) stay exact; dq_matmul runs 40 rows at K = 14336 (whose super-
+    blocks do not fit the 64-row skinny tiles' LDS) as 16-row skinny passes on this
+    256-row weight, and 70 rows on the GEMM."""
     import dqtorch as T
 
     k, n, m = 512, 192, 80
