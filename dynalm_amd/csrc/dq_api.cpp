@@ -304,9 +304,10 @@ int check_out(const dq_weight* w, int64_t m, int64_t n0, int64_t n1, float* y, i
 // per 16 rows (one read of the weight each) instead of the GEMM where that is faster.
 // Graph replay, quantization included, K = 14336:
 //  - Q6_K, while the passes read the weight fewer than ~4 times over 4096 rows: N = 4096 at
-//    24 / 48 / 64 rows 37.8 / 59.5 / 79.4 us against 114-116 for the int8 GEMM, whose few
-//    tiles leave most CUs idle; N = 8192 at 24 rows 66.6 against 115.9, at 48 112.6
-//    against 115.5; N = 14336 at 24 rows 118.1 against 120.7, at 64 256.3 against 117.4;
+//    24 / 48 / 64 rows 38.8 / 59.2 / 78.9 us against 86-88 for quantize + the int8 GEMM
+//    (64 x 64 tiles, whose few workgroups leave most CUs idle); N = 8192 at 32 rows 74.2
+//    against 86.8, at 48 110.4 against 86.9; N = 14336 at 24 rows 118.1 against 120.7
+//    (128 x 64 tiles);
 //  - Q4_K, two passes on weights of at most 4096 rows: N = 4096 at 24 rows 30.8 against
 //    40.3 us (K = 11008: 26.5 against 31.9), at 48 48.3 against 42.0; N = 8192 at 24 rows
 //    53.9 against 41.7.
