@@ -441,7 +441,7 @@ struct Big {
   static constexpr int kLds = kDA + 2 * kBM * 4;
   static_assert(kPrep >= 1 && kTiles % kWaves == 0, "each wave unpacks whole tiles");
   static_assert(kBN % 64 == 0 && (8 * kGroups) % kWaves == 0, "staging roles");
-  static_assert(kQ6 ? (4 * kGroups) % kWaves == 0 : kBM / 32 == kWaves, "staging roles");
+  static_assert(kQ6 ? (4 * kGroups) % kWaves == 0 : kBM / 32 <= kWaves, "staging roles");
   static constexpr int kAJ = kBM / (4 * kWaves);  // activation-code instructions per wave (4 rows each)
   static_assert(kBM % (16 * kWaves) == 0 && kAJ <= 8, "staging roles");
   static_assert(kLds <= 160 * 1024, "LDS");
@@ -494,7 +494,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     const int row = kAW * wave + 4 * j + (lane >> 4);
     aoff[j] = (u32)(row * arb + 4 + 16 * ((lane & 15) ^ (row & 15)));
   }
-  // bsums: wave w fills rows 32 w .. 32 w + 31
+  // bsums: wave w < kBM / 32 fills rows 32 w .. 32 w + 31
   const u32 bsoff = (u32)((32 * wave + (lane >> 1)) * arb + 260 + 16 * (lane & 1));
   constexpr int kWI = 8 * C::kGroups / C::kWaves;  // nibble instructions per wave
   auto issue = [&](int b) {
@@ -524,7 +524,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
         ld_lds4(rd6, lds + kBS, (u32)((lane >> 5) * nb * 128 + 4 * (lane & 31)), (u32)(b * 128));
       }
     } else {
-      ld_lds16(ra, lds + kBS + 32 * wave * 32, bsoff, (u32)(b * 292));
+      if (wave < kBM / 32) ld_lds16(ra, lds + kBS + 32 * wave * 32, bsoff, (u32)(b * 292));
     }
     constexpr int kDI = kBM / 64;  // activation-scale instructions, on the last waves
     if (wave >= C::kWaves - kDI) {
@@ -813,14 +813,17 @@ hipError_t launch_gemm(const WeightDev& w, int af, const uint8_t* acts, int64_t 
       if (wgs * 8 >= (int64_t)cus * 7) return launch_big<kQ6_K, 4, 2, 4>(w, acts, arb, m, n0, n1, y, ys, bias, s);
       // 64 x 64 tiles (4 waves, each 64 activation rows x 16 weight rows) while they are one
       // per CU at most: the 128 x 64 tiles would leave half the CUs idle or more (K = 14336,
-      // N = 4096: 96-98 against 113-121 us at 65..256 rows; at 384 rows, 384 of them took
-      // 140 against 123 us)
+      // N = 4096: 87-92 against 113-121 us at 65..256 rows; at 384 rows, 384 of them took
+      // 140 against 123 us); Q4_K below likewise
       if ((rows + 63) / 64 * ((m + 63) / 64) <= cus) {
         return launch_big<kQ6_K, 1, 4, 1>(w, acts, arb, m, n0, n1, y, ys, bias, s);
       }
       return launch_big<kQ6_K, 2, 2, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s);
     }
     if (wgs * 8 >= (int64_t)cus * 7) return launch_big<kQ4_K, 4, 2, 4>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+    if ((rows + 63) / 64 * ((m + 63) / 64) <= cus) {
+      return launch_big<kQ4_K, 1, 4, 1>(w, acts, arb, m, n0, n1, y, ys, bias, s);
+    }
     return launch_big<kQ4_K, 2, 2, 2>(w, acts, arb, m, n0, n1, y, ys, bias, s);
   }
   // up to 128 rows: the 4-wave kernel in the shape (waves along the activation rows, weight

@@ -303,12 +303,12 @@ def _q8k_set_group(a: np.ndarray, row: int, k: int, group: int, code: int) -> No
     a[row, o + 260 + 2 * g: o + 262 + 2 * g] = np.array([16 * code], np.int16).view(np.uint8)
 
 
-@pytest.mark.parametrize("m,n0,n1", [(512, 0, 14336), (300, 5, 14300)])
+@pytest.mark.parametrize("m,n0,n1", [(512, 0, 14336), (300, 5, 14300), (200, 0, 4096), (150, 70, 2000)])
 def test_gemm_big_tile(cuda, m, n0, n1):
-    """The 8-wave 256 x 128 GEMM kernel (the grid at N=14336 fills the GPU): every
-    output bit-identical to the skinny / M=1 GEMV path on the same Q8_K rows, sampled
-    rows bit-identical to the oracle; a partial second activation tile (m=300) and a
-    row range that cuts both end tiles."""
+    """The 8-wave 256 x 128 GEMM kernel (the grid at N=14336 fills the GPU) and the
+    4-wave 64 x 64 one (few tiles: N = 4096, 2000): every output bit-identical to the
+    skinny / M=1 GEMV path on the same Q8_K rows, sampled rows bit-identical to the
+    oracle; partial activation tiles and row ranges that cut both end tiles."""
     import dqtorch as T
 
     k, n = 512, 14336
